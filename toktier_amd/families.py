@@ -1,0 +1,95 @@
+"""Family descriptions for the GPU fresh-encode path.
+
+A family fixes everything that changes token ids on this path: the split
+regex (and with it the device ruleset), the digit group width, whether the
+model ignores merges for whole-vocabulary pieces, and whether the
+artifact declares an NFC normalizer.
+
+Reference data this mirrors:
+- ``src/toktier/kernels/tables/kernel_families.v1.json:103-117``
+  (``qwen3_8b``: ruleset cl100k, digits_max 1, contractions; ``llama_3_1_8b``:
+  digits_max 3).
+- Split patterns: ``crates/toktier-gigatoken-core/src/pretokenize/options.rs:118-132``
+  (GPT2, Qwen2, Olmo3/Llama-3 rows).
+- ``NativePrebuiltGpuConfig`` fields ``ruleset``, ``digits_max``,
+  ``contractions``, ``needs_nfc``, ``ignore_merges``
+  (``crates/toktier-routing-core/src/gpu.rs:22-38``).
+
+GPT-2 is not a GPU family in the reference (its r50k split exists only in
+the CPU scanner ``crates/toktier-gigatoken-core/src/pretokenize/fast/r50k.rs``);
+here it gets its own device ruleset, ``r50k``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+__all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K"]
+
+#: Device ruleset ids (the ``ruleset`` field of the engine config).
+RULESET_CL100K = 0
+RULESET_R50K = 1
+
+QWEN2_PATTERN = (
+    r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}"
+    r"| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+)
+LLAMA3_PATTERN = (
+    r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}"
+    r"| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+)
+#: The pattern HF ``ByteLevel(use_regex=True)`` applies (GPT-2).
+GPT2_PATTERN = (
+    r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+"
+    r"|\s+(?!\S)|\s+"
+)
+
+
+@dataclass(frozen=True)
+class Family:
+    name: str
+    ruleset: int           # RULESET_CL100K or RULESET_R50K
+    ruleset_name: str      # "cl100k" / "r50k"
+    pattern: str
+    digits_max: int        # digit group width (cl100k); 0 = unbounded (r50k)
+    contractions_fold: bool  # (?i:...) contractions (cl100k) vs case-sensitive
+    needs_nfc: bool
+    ignore_merges: bool
+    vocab_size: int        # regular (model) vocabulary size of the real artifact
+    hf_repo: str           # where the real artifact lives (not fetched here)
+    real_sha256: str | None  # pinned sha256 of the real tokenizer.json, if any
+
+
+FAMILIES: dict[str, Family] = {
+    "qwen3_8b": Family(
+        name="qwen3_8b", ruleset=RULESET_CL100K, ruleset_name="cl100k",
+        pattern=QWEN2_PATTERN, digits_max=1, contractions_fold=True,
+        needs_nfc=True, ignore_merges=False, vocab_size=151643,
+        hf_repo="Qwen/Qwen3-8B",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (11,422,654 B)
+        real_sha256="aeb13307a71acd8fe81861d94ad54ab689df773318809eed3cbe794b4492dae4",
+    ),
+    "llama_3_1_8b": Family(
+        name="llama_3_1_8b", ruleset=RULESET_CL100K, ruleset_name="cl100k",
+        pattern=LLAMA3_PATTERN, digits_max=3, contractions_fold=True,
+        needs_nfc=False, ignore_merges=True, vocab_size=128000,
+        hf_repo="meta-llama/Llama-3.1-8B",
+        # same manifest (9,085,658 B)
+        real_sha256="76e48799b099d43365bd24ccd8ecc5aedac831718da780552f03b0a6eb4412aa",
+    ),
+    "gpt2": Family(
+        name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",
+        pattern=GPT2_PATTERN, digits_max=0, contractions_fold=False,
+        needs_nfc=False, ignore_merges=False, vocab_size=50257,
+        hf_repo="openai-community/gpt2", real_sha256=None,
+    ),
+}
+
+
+def family(name: str) -> Family:
+    try:
+        return FAMILIES[name]
+    except KeyError:
+        raise KeyError(
+            f"unknown family {name!r}; known: {sorted(FAMILIES)}"
+        ) from None

@@ -1,0 +1,261 @@
+"""Deterministic stand-in tokenizer artifacts for offline work.
+
+The real ``tokenizer.json`` files of Qwen3-8B, Llama-3.1-8B and GPT-2 are
+not reachable from this environment (no network, none on disk). Token-id
+parity is a property of an *artifact* plus the encode algorithm, so the
+path is exercised on stand-ins that carry each family's exact
+normalizer / pre-tokenizer / model configuration and its real vocabulary
+size, trained with Hugging Face ``tokenizers`` (the certified oracle,
+version 0.22.2) on a corpus assembled from text files of this image plus a
+seeded synthetic multilingual part. Any real artifact can be dropped in
+instead (``toktier_amd.load(family, tokenizer_json=path)``).
+
+Shapes follow the real artifacts:
+
+- ``qwen3_8b``: NFC normalizer; ``Split(Qwen2 regex, isolated)`` +
+  ``ByteLevel(use_regex=False)``; BPE with 151,387 merges over a
+  151,643-entry vocabulary; ``ignore_merges`` false.
+- ``llama_3_1_8b``: no normalizer; ``Split(Llama-3 regex)`` + ``ByteLevel``;
+  BPE with ``ignore_merges`` true over a 128,000-entry vocabulary, merges
+  re-derived tiktoken-style (every split of a token into two vocabulary
+  entries, ordered by the merged token's rank), which gives more merges
+  than vocabulary entries and duplicate merged ids, as the real artifact
+  has (``src/toktier/kernels/bpe_tables.py`` module notes).
+- ``gpt2``: ``ByteLevel(use_regex=True)`` pre-tokenizer; 50,000 merges,
+  50,257 entries including ``<|endoftext|>``.
+
+The committed artifacts live in ``toktier_amd/data/artifacts`` (xz
+compressed); this module regenerates them (``python -m toktier_amd.standin``).
+Training is not bit-reproducible across machines, so the committed files
+and their sha256 (``ARTIFACT_SHA256``) are the identity, not this script.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import lzma
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+
+from .families import FAMILIES, family
+
+DATA_DIR = Path(__file__).resolve().parent / "data" / "artifacts"
+
+__all__ = ["artifact_path", "load_artifact_json", "ARTIFACT_SHA256"]
+
+#: sha256 of the *uncompressed* committed stand-in tokenizer.json files.
+ARTIFACT_SHA256: dict[str, str] = {}
+_SHA_FILE = DATA_DIR / "SHA256SUMS.json"
+if _SHA_FILE.exists():
+    ARTIFACT_SHA256.update(json.loads(_SHA_FILE.read_text()))
+
+
+def artifact_path(name: str) -> Path:
+    return DATA_DIR / f"{name}.tokenizer.json.xz"
+
+
+def load_artifact_json(name: str) -> str:
+    """The committed stand-in ``tokenizer.json`` text, sha256-verified."""
+    family(name)
+    raw = lzma.decompress(artifact_path(name).read_bytes())
+    want = ARTIFACT_SHA256.get(name)
+    got = hashlib.sha256(raw).hexdigest()
+    if want is not None and got != want:
+        raise ValueError(
+            f"stand-in artifact {name} sha256 {got} != recorded {want}"
+        )
+    return raw.decode("utf-8")
+
+
+# ---------------------------------------------------------------- corpus
+
+_TEXT_ROOTS = ("/usr/lib/python3.10", "/usr/local/lib/python3.10/dist-packages")
+
+
+def _code_corpus(limit_bytes: int) -> list[str]:
+    files: list[str] = []
+    for root in _TEXT_ROOTS:
+        for dirpath, dirnames, filenames in os.walk(root):
+            dirnames.sort()
+            for f in sorted(filenames):
+                if f.endswith((".py", ".rst", ".md")):
+                    files.append(os.path.join(dirpath, f))
+    out: list[str] = []
+    total = 0
+    for path in files:
+        try:
+            size = os.path.getsize(path)
+            if size > 2_000_000:
+                continue
+            with open(path, encoding="utf-8", errors="ignore") as fh:
+                text = fh.read()
+        except OSError:
+            continue
+        out.append(text)
+        total += len(text)
+        if total >= limit_bytes:
+            break
+    return out
+
+
+_ACCENTED = "àáâãäåæçèéêëìíîïñòóôõöøùúûüýÿÀÁÂÃÄÅÇÈÉÊËÌÍÎÏÑÒÓÔÕÖØÙÚÛÜÝß"
+_SYLL_C = "bcdfghjklmnpqrstvwxz"
+_SYLL_V = "aeiouy"
+
+
+def _latin1_words(rng: np.random.Generator, n: int) -> list[str]:
+    words = []
+    for _ in range(n):
+        k = int(rng.integers(1, 4))
+        w = []
+        for _ in range(k):
+            w.append(_SYLL_C[int(rng.integers(len(_SYLL_C)))])
+            if rng.random() < 0.45:
+                w.append(_ACCENTED[int(rng.integers(len(_ACCENTED)))])
+            else:
+                w.append(_SYLL_V[int(rng.integers(len(_SYLL_V)))])
+        words.append("".join(w))
+    return words
+
+
+def _synthetic_corpus(seed: int, cjk_chars: int, latin1_words: int,
+                      emoji_lines: int) -> list[str]:
+    rng = np.random.default_rng(seed)
+    out: list[str] = []
+    if cjk_chars:
+        han = np.arange(0x4E00, 0xA000)
+        rng.shuffle(han)
+        # Zipf-ish character frequencies; words are 1-4 characters
+        ranks = np.minimum(rng.zipf(1.15, size=cjk_chars), len(han)) - 1
+        chars = [chr(int(han[r])) for r in ranks]
+        words_vocab = ["".join(chars[i:i + int(rng.integers(1, 5))])
+                       for i in range(0, 60000)]
+        wr = np.minimum(rng.zipf(1.1, size=cjk_chars // 2),
+                        len(words_vocab)) - 1
+        line: list[str] = []
+        n = 0
+        for r in wr:
+            w = words_vocab[int(r)]
+            line.append(w)
+            n += len(w)
+            if rng.random() < 0.08:
+                line.append("\uff0c" if rng.random() < 0.7 else "\u3002")
+            if n > 60:
+                out.append("".join(line))
+                line, n = [], 0
+    if latin1_words:
+        lex = _latin1_words(rng, 40000)
+        wr = np.minimum(rng.zipf(1.1, size=latin1_words), len(lex)) - 1
+        for i in range(0, len(wr), 12):
+            out.append(" ".join(lex[int(r)] for r in wr[i:i + 12]))
+    if emoji_lines:
+        base = list(range(0x1F600, 0x1F64F)) + list(range(0x1F300, 0x1F3FF))
+        for _ in range(emoji_lines):
+            k = int(rng.integers(1, 6))
+            seq = []
+            for _ in range(k):
+                e = chr(base[int(rng.integers(len(base)))])
+                if rng.random() < 0.2:
+                    e += "\u200d" + chr(base[int(rng.integers(len(base)))])
+                if rng.random() < 0.2:
+                    e += "\ufe0f"
+                seq.append(e)
+            out.append(" ".join(seq))
+    return out
+
+
+# -------------------------------------------------------------- training
+
+def _train(name: str) -> dict:
+    from tokenizers import (Regex, Tokenizer, decoders, models,
+                            normalizers, pre_tokenizers, trainers)
+
+    fam = family(name)
+    tok = Tokenizer(models.BPE())
+    if fam.needs_nfc:
+        tok.normalizer = normalizers.NFC()
+    if name == "gpt2":
+        tok.pre_tokenizer = pre_tokenizers.ByteLevel(
+            add_prefix_space=False, trim_offsets=True, use_regex=True)
+    else:
+        tok.pre_tokenizer = pre_tokenizers.Sequence([
+            pre_tokenizers.Split(Regex(fam.pattern), behavior="isolated",
+                                 invert=False),
+            pre_tokenizers.ByteLevel(add_prefix_space=False,
+                                     trim_offsets=False, use_regex=False),
+        ])
+    tok.decoder = decoders.ByteLevel()
+    n_regular = fam.vocab_size - (1 if name == "gpt2" else 0)
+    trainer = trainers.BpeTrainer(
+        vocab_size=n_regular,
+        initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
+        show_progress=False,
+    )
+    corpus = _code_corpus(150_000_000 if name != "gpt2" else 60_000_000)
+    if name == "qwen3_8b":
+        corpus += _synthetic_corpus(20261201, 6_000_000, 1_500_000, 40000)
+    elif name == "llama_3_1_8b":
+        corpus += _synthetic_corpus(20261202, 1_500_000, 800_000, 10000)
+    tok.train_from_iterator(corpus, trainer)
+    spec = json.loads(tok.to_str())
+    model = spec["model"]
+    vocab: dict[str, int] = model["vocab"]
+    if len(vocab) != n_regular:
+        raise RuntimeError(
+            f"{name}: corpus too small: vocab {len(vocab)} < {n_regular}")
+    model["ignore_merges"] = bool(fam.ignore_merges)
+    if name == "llama_3_1_8b":
+        model["merges"] = _tiktoken_style_merges(vocab)
+    added = []
+    if name == "gpt2":
+        vocab["<|endoftext|>"] = 50256
+        added = [("<|endoftext|>", 50256)]
+    elif name == "qwen3_8b":
+        added = [("<|endoftext|>", 151643), ("<|im_start|>", 151644),
+                 ("<|im_end|>", 151645)]
+    else:
+        added = [("<|begin_of_text|>", 128000), ("<|end_of_text|>", 128001)]
+    spec["added_tokens"] = [
+        {"id": i, "content": c, "single_word": False, "lstrip": False,
+         "rstrip": False, "normalized": False, "special": True}
+        for c, i in added
+    ]
+    return spec
+
+
+def _tiktoken_style_merges(vocab: dict[str, int]) -> list[list[str]]:
+    """Every split ``t = a + b`` with ``a, b`` in the vocabulary, ordered by
+    the merged token's id, then by ``(id(a), id(b))``."""
+    merges: list[tuple[int, int, int, str, str]] = []
+    for token, rank in vocab.items():
+        if len(token) < 2:
+            continue
+        for k in range(1, len(token)):
+            a, b = token[:k], token[k:]
+            ia, ib = vocab.get(a), vocab.get(b)
+            if ia is not None and ib is not None:
+                merges.append((rank, ia, ib, a, b))
+    merges.sort()
+    return [[a, b] for _, _, _, a, b in merges]
+
+
+def main(argv: list[str]) -> None:
+    names = argv or sorted(FAMILIES)
+    DATA_DIR.mkdir(parents=True, exist_ok=True)
+    sums = dict(ARTIFACT_SHA256)
+    for name in names:
+        spec = _train(name)
+        raw = json.dumps(spec, ensure_ascii=False,
+                         separators=(",", ":")).encode("utf-8")
+        sums[name] = hashlib.sha256(raw).hexdigest()
+        artifact_path(name).write_bytes(lzma.compress(raw, preset=9))
+        print(name, len(raw), sums[name], flush=True)
+    _SHA_FILE.write_text(json.dumps(sums, indent=1, sort_keys=True) + "\n")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
