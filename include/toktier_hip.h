@@ -1,0 +1,149 @@
+/*
+ * toktier_hip.h -- C-ABI of the MI355X (gfx950) fresh-encode engine.
+ *
+ * One engine = one tokenizer family on one GPU: UTF-8 bytes in, byte-level
+ * BPE token ids out, bit-identical to a from-scratch Hugging Face
+ * `tokenizers` encode of the same text (add_special_tokens=False).
+ *
+ * The entry points replace the reference's Rust GPU engine surface:
+ *   tk_engine_preflight  <- NativePrebuiltGpu::preflight
+ *                           (crates/toktier-routing-core/src/gpu.rs:1383-1404,
+ *                            shape rules validate_tables gpu.rs:1642-1679)
+ *   tk_engine_open       <- NativePrebuiltGpu::new / Executor::new
+ *                           (gpu.rs:1406-1442, :248-344)
+ *   tk_engine_encode     <- NativeGpuEngine::encode_ids
+ *                           (runtime.rs:76-82; gpu.rs:1446-1461, :500-600)
+ *   tk_engine_encode_batch <- NativeGpuEngine::encode_batch_ids
+ *                           (gpu.rs:1463-1546, Executor::encode_batch :605-750)
+ *   tk_engine_delivery   <- NativeGpuEngine::delivery (runtime.rs:81)
+ *   tk_engine_close      <- Drop of the engine / CUDA driver RAII
+ *                           (crates/toktier-cuda-driver/src/lib.rs:424-457)
+ *   tk_last_error        <- NativeRuntimeError / CudaError message
+ *                           (runtime.rs:58-72; cuda-driver lib.rs:31-49)
+ * The table arguments are the reference's kernel-input ABI unchanged
+ * (src/toktier/kernels/bpe_tables.py:1-30): pair_keys/pair_vals (u64,
+ * splitmix64 open addressing), byte_id (i32[256]), vocab_keys/vocab_vals/
+ * vocab_blob (FNV-1a-64 whole-piece hash), unsafe_bits (u32 bitmap), class
+ * table (u8[0x110000], P=0 L=1 N=2 S=3). The engine re-packs them into its
+ * own device layout at open.
+ *
+ * Threading: calls on one engine serialize on an internal mutex (the
+ * reference's Mutex<Executor>, gpu.rs:1361, :1457-1460). Errors: every
+ * entry returns a TK_* status; on failure no ids are produced and
+ * tk_last_error() (thread-local) describes the failure.
+ */
+#ifndef TOKTIER_HIP_H
+#define TOKTIER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TK_ABI_VERSION 1u
+
+/* rulesets (the reference names: gpu.rs:40-62; r50k is new) */
+#define TK_RULESET_CL100K 0 /* Qwen2 / Llama-3 split (digits_max 1 or 3) */
+#define TK_RULESET_R50K 1   /* GPT-2 split */
+
+/* status codes */
+#define TK_OK 0
+#define TK_E_INVALID_ARG (-1) /* null pointer, bad config field */
+#define TK_E_SHAPE (-2)       /* table shape rules (gpu.rs:1642-1679) */
+#define TK_E_DEVICE (-3)      /* HIP runtime failure */
+#define TK_E_ARCH (-4)        /* device is not the expected architecture */
+#define TK_E_UTF8 (-5)        /* input is not valid UTF-8 */
+#define TK_E_NEEDS_NFC (-6)   /* NFC quick check failed: normalize, retry */
+#define TK_E_CAPACITY (-7)    /* caller's id buffer too small / input too big */
+#define TK_E_INTERNAL (-8)
+
+/* tk_engine_encode flags */
+#define TK_FLAG_NORMALIZED 1u /* caller already applied the family's NFC */
+
+typedef struct tk_engine tk_engine;
+
+/* NativePrebuiltGpuConfig (gpu.rs:22-38) minus the fatbin digest fields */
+typedef struct tk_config {
+  uint32_t abi_version;        /* TK_ABI_VERSION */
+  int32_t device_ordinal;
+  int32_t ruleset;             /* TK_RULESET_* */
+  int32_t digits_max;          /* cl100k: 1 (Qwen) or 3 (Llama); r50k: 0 */
+  int32_t contractions;        /* must be 1 (both rulesets split them) */
+  int32_t needs_nfc;           /* family declares an NFC normalizer */
+  int32_t ignore_merges;       /* whole-piece vocabulary hit first */
+  uint64_t pair_count;         /* slots in pair_keys (power of two) */
+  uint64_t vocab_count;        /* slots in vocab_keys (power of two) */
+  const char* family;          /* label only */
+  const char* artifact_sha256; /* label only */
+  const char* expected_architecture; /* "gfx950" or NULL for any */
+} tk_config;
+
+/* Device-free validation of the config and table shapes. Sizes are bytes. */
+int tk_engine_preflight(const tk_config* cfg,
+                        const uint8_t* class_table, size_t class_len,
+                        const uint64_t* pair_keys, size_t pair_keys_len,
+                        const uint64_t* pair_vals, size_t pair_vals_len,
+                        const int32_t* byte_id, size_t byte_id_len,
+                        const uint64_t* vocab_keys, size_t vocab_keys_len,
+                        const uint64_t* vocab_vals, size_t vocab_vals_len,
+                        const uint32_t* unsafe_bits, size_t unsafe_len);
+
+/* Opens the device, uploads the tables. nfc_qc (u8[0x110000]) is needed
+ * only when cfg->needs_nfc. */
+int tk_engine_open(const tk_config* cfg,
+                   const uint8_t* class_table, size_t class_len,
+                   const uint64_t* pair_keys, size_t pair_keys_len,
+                   const uint64_t* pair_vals, size_t pair_vals_len,
+                   const int32_t* byte_id, size_t byte_id_len,
+                   const uint64_t* vocab_keys, size_t vocab_keys_len,
+                   const uint64_t* vocab_vals, size_t vocab_vals_len,
+                   const uint8_t* vocab_blob, size_t vocab_blob_len,
+                   const uint32_t* unsafe_bits, size_t unsafe_len,
+                   const uint8_t* nfc_qc, size_t nfc_qc_len,
+                   tk_engine** out);
+
+void tk_engine_close(tk_engine* engine);
+
+/* One request: host UTF-8 in, host ids out. ids_cap >= nbytes always
+ * suffices (a token covers at least one byte). */
+int tk_engine_encode(tk_engine* engine, const uint8_t* text, size_t nbytes,
+                     uint32_t flags, uint32_t* ids, size_t ids_cap,
+                     size_t* n_ids);
+
+/* A batch: documents concatenated in `joined`, document d spans
+ * [doc_offsets[d], doc_offsets[d+1]) bytes. Row d's ids land in
+ * ids[row_offsets[d] .. row_offsets[d+1]); each row equals
+ * tk_engine_encode of that document alone. row_status[d] is TK_OK or the
+ * row's own error (e.g. TK_E_NEEDS_NFC); rows with an error are empty. */
+int tk_engine_encode_batch(tk_engine* engine, const uint8_t* joined,
+                           const uint64_t* doc_offsets, size_t n_docs,
+                           uint32_t flags, uint32_t* ids, size_t ids_cap,
+                           uint64_t* row_offsets, int32_t* row_status);
+
+/* Device-resident form (no host copies): d_text and d_ids are device
+ * pointers on the engine's device; `stream` is a hipStream_t or NULL for
+ * the engine's own stream. Blocks until *n_ids is known. */
+int tk_engine_encode_device(tk_engine* engine, const void* d_text,
+                            size_t nbytes, uint32_t flags, void* d_ids,
+                            size_t ids_cap, size_t* n_ids, void* stream);
+
+const char* tk_engine_delivery(const tk_engine* engine);     /* "prebuilt" */
+const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
+
+/* Per-stage device times (microseconds) of the last encode on this engine,
+ * measured with HIP events on the engine's stream: [0] pretokenize,
+ * [1] short-piece BPE, [2] long-piece BPE, [3] compaction, [4] total.
+ * Returns the number of values written (<= n). Timing is recorded only when
+ * enabled with tk_engine_set_timing(engine, 1). */
+int tk_engine_set_timing(tk_engine* engine, int enabled);
+int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
+
+/* Thread-local description of the last failure on this thread. */
+const char* tk_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TOKTIER_HIP_H */

@@ -1,0 +1,108 @@
+"""ctypes wrapper of the CPU restatement (``liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and the ``cpu_baseline`` leg of ``bench.py`` as the parity checker. The
+product path (``toktier_amd``) never imports this module.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+E_UTF8, E_NOMEM, E_NEEDS_NFC, E_CAP = -1, -2, -3, -4
+
+
+class _Tables(C.Structure):
+    _fields_ = [
+        ("cls", C.c_void_p), ("pair_keys", C.c_void_p),
+        ("pair_vals", C.c_void_p), ("pair_count", C.c_uint64),
+        ("byte_id", C.c_void_p), ("vocab_keys", C.c_void_p),
+        ("vocab_vals", C.c_void_p), ("vocab_count", C.c_uint64),
+        ("vocab_blob", C.c_void_p), ("nfc_qc", C.c_void_p),
+        ("ruleset", C.c_int32), ("digits_max", C.c_int32),
+        ("ignore_merges", C.c_int32), ("needs_nfc", C.c_int32),
+    ]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        L.tko_pretokenize.restype = C.c_int64
+        L.tko_pretokenize.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+        L.tko_bpe.restype = C.c_int64
+        L.tko_bpe.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]
+        L.tko_nfc_qc.restype = C.c_int
+        L.tko_nfc_qc.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.tko_encode.restype = C.c_int64
+        L.tko_encode.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64]
+        L.tko_utf8_decode.restype = C.c_int64
+        L.tko_utf8_decode.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]
+        _lib = L
+    return _lib
+
+
+class Oracle:
+    """Sequential restatement bound to one family's tables."""
+
+    def __init__(self, tables, cls: np.ndarray, nfc_qc: np.ndarray | None,
+                 ruleset: int, digits_max: int, needs_nfc: bool):
+        self._keep = [tables.pair_keys, tables.pair_vals, tables.byte_id,
+                      tables.vocab_keys, tables.vocab_vals,
+                      tables.vocab_blob, cls, nfc_qc]
+        blob = tables.vocab_blob if tables.vocab_blob.size else np.zeros(1, np.uint8)
+        self._keep.append(blob)
+        self._t = _Tables(
+            cls.ctypes.data, tables.pair_keys.ctypes.data,
+            tables.pair_vals.ctypes.data, tables.pair_keys.size,
+            tables.byte_id.ctypes.data, tables.vocab_keys.ctypes.data,
+            tables.vocab_vals.ctypes.data, tables.vocab_keys.size,
+            blob.ctypes.data,
+            nfc_qc.ctypes.data if nfc_qc is not None else None,
+            ruleset, digits_max, int(tables.ignore_merges), int(needs_nfc))
+        self._lib = lib()
+
+    def pretokenize(self, data: bytes) -> list[int]:
+        """Piece start byte offsets, followed by len(data)."""
+        starts = np.zeros(len(data) + 1, dtype=np.int64)
+        n = self._lib.tko_pretokenize(C.byref(self._t), data, len(data),
+                                      starts.ctypes.data)
+        if n < 0:
+            raise ValueError(f"oracle pretokenize failed ({n})")
+        return starts[: n + 1].tolist()
+
+    def bpe(self, piece: bytes) -> list[int]:
+        out = np.zeros(max(1, len(piece)), dtype=np.uint32)
+        n = self._lib.tko_bpe(C.byref(self._t), piece, len(piece), out.ctypes.data)
+        return out[:n].tolist()
+
+    def nfc_qc(self, data: bytes) -> bool:
+        r = self._lib.tko_nfc_qc(C.byref(self._t), data, len(data))
+        if r < 0:
+            raise ValueError("invalid UTF-8")
+        return bool(r)
+
+    def encode_bytes(self, data: bytes) -> np.ndarray | int:
+        """ids as uint32, or a negative status (E_NEEDS_NFC, E_UTF8)."""
+        out = np.zeros(max(1, len(data)), dtype=np.uint32)
+        n = self._lib.tko_encode(C.byref(self._t), data, len(data),
+                                 out.ctypes.data, out.size)
+        if n < 0:
+            return int(n)
+        return out[:n]

@@ -1,0 +1,384 @@
+/*
+ * toktier_oracle.c -- CPU restatement of the GPU fresh-encode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the parity tests,
+ * the smoke entry and the bench's cpu_baseline leg compare the HIP engine
+ * against. Nothing on the product path links, loads or calls it.
+ *
+ * It restates, in plain sequential C:
+ *   - strict UTF-8 decoding (src/toktier/kernels/pretok_kernel.cu:363-407:
+ *     truncated sequences, F8-FF leads, overlong forms, surrogates and
+ *     values above U+10FFFF are invalid);
+ *   - the family split regexes as a left-to-right alternation matcher, one
+ *     alternative at a time in pattern order, with the greedy/backtracking
+ *     outcome of each alternative written out:
+ *       cl100k (Qwen2 / Llama-3):
+ *         (?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,K}
+ *         | ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+
+ *       (crates/toktier-gigatoken-core/src/pretokenize/options.rs:125,:131;
+ *        K = digits_max, kernel_families.v1.json:104-117)
+ *       r50k (GPT-2):
+ *         's|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+
+ *         |\s+(?!\S)|\s+
+ *       (options.rs:118; crates/.../pretokenize/fast/r50k.rs:1-2)
+ *     with \s / \p{L} / \p{N} membership read from the probed class table
+ *     (classes P=0 L=1 N=2 S=3, pretok_kernel.cu:63) and the case folding
+ *     of (?i:...) restricted to A-Z and U+017F (pretok_kernel.cu:153-158);
+ *   - byte-level BPE with the HF `tokenizers` semantics the reference
+ *     certifies against (pretok_kernel.cu:872-881): initial symbols are
+ *     byte ids (bytes without an id are dropped, pretok_kernel.cu:1012-1021),
+ *     then the adjacent pair of lowest merge rank is merged, leftmost
+ *     first, until none is left; a min-heap of (rank, position) with stale
+ *     entries skipped, which is the published HF algorithm
+ *     (tokenizers 0.22.2, models/bpe/word.rs `merge_all`);
+ *   - ignore_merges: a piece that is itself a vocabulary entry is emitted
+ *     as that one token (pretok_kernel.cu:921-943, :1005-1008);
+ *   - table lookups in the boundary format (src/toktier/kernels/
+ *     bpe_tables.py:99-132: splitmix64 slot, linear probing, empty = ~0;
+ *     FNV-1a-64 vocabulary keys with a byte recheck against the blob);
+ *   - the NFC quick check (pretok_kernel.cu:2139-2181 and
+ *     nfc_quick_check.v1.meta.json predicate).
+ */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "toktier_oracle.h"
+
+enum { CP_ = 0, CL_ = 1, CN_ = 2, CS_ = 3 };
+
+/* ------------------------------------------------------------ hashing */
+
+static uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ULL;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+  return x ^ (x >> 31);
+}
+
+/* rank<<32|merged_id, or -1 */
+static int64_t pair_lookup(const tko_tables* t, uint32_t l, uint32_t r) {
+  uint64_t key = ((uint64_t)l << 32) | r;
+  uint64_t mask = t->pair_count - 1;
+  uint64_t i = splitmix64(key) & mask;
+  for (;;) {
+    uint64_t k = t->pair_keys[i];
+    if (k == ~0ULL) return -1;
+    if (k == key) return (int64_t)t->pair_vals[i];
+    i = (i + 1) & mask;
+  }
+}
+
+static int64_t vocab_lookup(const tko_tables* t, const uint8_t* s, int64_t m) {
+  uint64_t h = 0xCBF29CE484222325ULL;
+  for (int64_t j = 0; j < m; ++j) h = (h ^ s[j]) * 0x100000001B3ULL;
+  uint64_t mask = t->vocab_count - 1;
+  uint64_t i = splitmix64(h) & mask;
+  for (;;) {
+    uint64_t k = t->vocab_keys[i];
+    if (k == ~0ULL) return -1;
+    if (k == h) {
+      uint64_t v = t->vocab_vals[i];
+      int64_t len = (int64_t)((v >> 20) & 0x3FF);
+      uint64_t off = v >> 30;
+      if (len == m && memcmp(t->vocab_blob + off, s, (size_t)m) == 0)
+        return (int64_t)(v & 0xFFFFF);
+    }
+    i = (i + 1) & mask;
+  }
+}
+
+/* ------------------------------------------------------------- UTF-8 */
+
+int64_t tko_utf8_decode(const uint8_t* s, int64_t nb, int32_t* cp,
+                        int64_t* bo) {
+  int64_t n = 0, i = 0;
+  while (i < nb) {
+    uint32_t b0 = s[i];
+    int need;
+    uint32_t v;
+    if (b0 < 0x80) { need = 0; v = b0; }
+    else if (b0 < 0xC0) return -1;
+    else if (b0 < 0xE0) { need = 1; v = b0 & 0x1F; }
+    else if (b0 < 0xF0) { need = 2; v = b0 & 0x0F; }
+    else if (b0 < 0xF8) { need = 3; v = b0 & 0x07; }
+    else return -1;
+    for (int k = 1; k <= need; ++k) {
+      if (i + k >= nb) return -1;
+      uint32_t c = s[i + k];
+      if ((c & 0xC0) != 0x80) return -1;
+      v = (v << 6) | (c & 0x3F);
+    }
+    if ((need == 1 && v < 0x80) || (need == 2 && v < 0x800) ||
+        (need == 3 && v < 0x10000) || v > 0x10FFFF ||
+        (v >= 0xD800 && v <= 0xDFFF))
+      return -1;
+    if (cp) cp[n] = (int32_t)v;
+    if (bo) bo[n] = i;
+    ++n;
+    i += need + 1;
+  }
+  return n;
+}
+
+/* -------------------------------------------------------- pretokenize */
+
+static int fold(int32_t c) {
+  if (c >= 'A' && c <= 'Z') return c + 32;
+  if (c == 0x17F) return 's';
+  return c;
+}
+
+static int is_crlf(int32_t c) { return c == '\r' || c == '\n'; }
+
+/* End (exclusive, in chars) of the cl100k match that starts at char i. */
+static int64_t match_cl100k(const int32_t* cp, const uint8_t* cl, int64_t i,
+                            int64_t n, int K, int fold_case) {
+  /* (?i:'s|'t|'re|'ve|'m|'ll|'d) -- first letters are distinct, so the
+     alternatives cannot compete */
+  if (cp[i] == '\'' && i + 1 < n) {
+    int a = fold_case ? fold(cp[i + 1]) : cp[i + 1];
+    if (a == 's' || a == 't' || a == 'm' || a == 'd') return i + 2;
+    if (i + 2 < n) {
+      int b = fold_case ? fold(cp[i + 2]) : cp[i + 2];
+      if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+          (a == 'l' && b == 'l'))
+        return i + 3;
+    }
+  }
+  /* [^\r\n\p{L}\p{N}]?\p{L}+ : the optional prefix first tries to take
+     cp[i]; a letter is not in the prefix class, so then \p{L}+ starts at i */
+  if (cl[i] == CL_) {
+    int64_t j = i + 1;
+    while (j < n && cl[j] == CL_) ++j;
+    return j;
+  }
+  if (cl[i] != CN_ && !is_crlf(cp[i]) && i + 1 < n && cl[i + 1] == CL_) {
+    int64_t j = i + 2;
+    while (j < n && cl[j] == CL_) ++j;
+    return j;
+  }
+  /* \p{N}{1,K} */
+  if (cl[i] == CN_) {
+    int64_t j = i + 1;
+    while (j < n && cl[j] == CN_ && j - i < K) ++j;
+    return j;
+  }
+  /*  ?[^\s\p{L}\p{N}]+[\r\n]* : with the space taken the run must start at
+     i+1; without it cp[i] itself must be P */
+  {
+    int64_t j = -1;
+    if (cp[i] == ' ') {
+      if (i + 1 < n && cl[i + 1] == CP_) j = i + 1;
+    } else if (cl[i] == CP_) {
+      j = i;
+    }
+    if (j >= 0) {
+      while (j < n && cl[j] == CP_) ++j;
+      while (j < n && is_crlf(cp[j])) ++j;
+      return j;
+    }
+  }
+  /* the rest are whitespace alternatives: cp[i] is \s here */
+  {
+    int64_t e = i;
+    while (e < n && cl[e] == CS_) ++e;
+    /* \s*[\r\n]+ : \s* backs off until [\r\n]+ can start, i.e. the match
+       ends right after the last CR/LF of the run */
+    for (int64_t k = e - 1; k >= i; --k)
+      if (is_crlf(cp[k])) return k + 1;
+    /* \s+(?!\S) : the whole run at end of text, else one char shorter */
+    if (e == n) return e;
+    if (e - 1 > i) return e - 1;
+    /* \s+ */
+    return e;
+  }
+}
+
+/* End of the r50k (GPT-2) match that starts at char i. */
+static int64_t match_r50k(const int32_t* cp, const uint8_t* cl, int64_t i,
+                          int64_t n) {
+  if (cp[i] == '\'' && i + 1 < n) {
+    int a = cp[i + 1];
+    if (a == 's' || a == 't' || a == 'm' || a == 'd') return i + 2;
+    if (i + 2 < n) {
+      int b = cp[i + 2];
+      if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+          (a == 'l' && b == 'l'))
+        return i + 3;
+    }
+  }
+  /* ' ?\p{L}+', ' ?\p{N}+', ' ?[^\s\p{L}\p{N}]+' in that order */
+  for (int want = CL_;; want = (want == CL_ ? CN_ : CP_)) {
+    int64_t j = -1;
+    if (cp[i] == ' ') {
+      if (i + 1 < n && cl[i + 1] == want) j = i + 1;
+    } else if (cl[i] == want) {
+      j = i;
+    }
+    if (j >= 0) {
+      while (j < n && cl[j] == want) ++j;
+      return j;
+    }
+    if (want == CP_) break;
+  }
+  {
+    int64_t e = i;
+    while (e < n && cl[e] == CS_) ++e;
+    if (e == n) return e;          /* \s+(?!\S) at end of text */
+    if (e - 1 > i) return e - 1;   /* backed off by one */
+    return e;                      /* \s+ */
+  }
+}
+
+int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
+                        int64_t* starts) {
+  int32_t* cp = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nb + 1));
+  int64_t* bo = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nb + 1));
+  uint8_t* cl = (uint8_t*)malloc((size_t)(nb + 1));
+  if (!cp || !bo || !cl) { free(cp); free(bo); free(cl); return -2; }
+  int64_t n = tko_utf8_decode(s, nb, cp, bo);
+  if (n < 0) { free(cp); free(bo); free(cl); return -1; }
+  for (int64_t i = 0; i < n; ++i) cl[i] = t->cls[cp[i]];
+  int64_t p = 0, i = 0;
+  while (i < n) {
+    starts[p++] = bo[i];
+    int64_t e = t->ruleset == TKO_RULESET_R50K
+                    ? match_r50k(cp, cl, i, n)
+                    : match_cl100k(cp, cl, i, n, t->digits_max, 1);
+    i = e;
+  }
+  starts[p] = nb;
+  free(cp); free(bo); free(cl);
+  return p;
+}
+
+/* ---------------------------------------------------------------- BPE */
+
+typedef struct { uint32_t rank; int32_t pos; } hent;
+
+static int hless(hent a, hent b) {
+  return a.rank < b.rank || (a.rank == b.rank && a.pos < b.pos);
+}
+
+static void hpush(hent* h, int64_t* n, hent e) {
+  int64_t i = (*n)++;
+  h[i] = e;
+  while (i > 0) {
+    int64_t p = (i - 1) / 2;
+    if (!hless(h[i], h[p])) break;
+    hent tmp = h[i]; h[i] = h[p]; h[p] = tmp;
+    i = p;
+  }
+}
+
+static hent hpop(hent* h, int64_t* n) {
+  hent top = h[0];
+  h[0] = h[--(*n)];
+  int64_t i = 0;
+  for (;;) {
+    int64_t l = 2 * i + 1, r = l + 1, m = i;
+    if (l < *n && hless(h[l], h[m])) m = l;
+    if (r < *n && hless(h[r], h[m])) m = r;
+    if (m == i) break;
+    hent tmp = h[i]; h[i] = h[m]; h[m] = tmp;
+    i = m;
+  }
+  return top;
+}
+
+int64_t tko_bpe(const tko_tables* t, const uint8_t* s, int64_t m,
+                uint32_t* out) {
+  if (m <= 0) return 0;
+  if (t->ignore_merges) {
+    int64_t hit = vocab_lookup(t, s, m);
+    if (hit >= 0) { out[0] = (uint32_t)hit; return 1; }
+  }
+  int32_t* id = (int32_t*)malloc(sizeof(int32_t) * (size_t)m);
+  int32_t* nx = (int32_t*)malloc(sizeof(int32_t) * (size_t)m);
+  int32_t* pv = (int32_t*)malloc(sizeof(int32_t) * (size_t)m);
+  hent* heap = (hent*)malloc(sizeof(hent) * (size_t)(3 * m + 4));
+  if (!id || !nx || !pv || !heap) {
+    free(id); free(nx); free(pv); free(heap);
+    return -2;
+  }
+  int32_t k = 0;
+  for (int64_t j = 0; j < m; ++j) {
+    int32_t v = t->byte_id[s[j]];
+    if (v >= 0) id[k++] = v;  /* bytes without an id are dropped */
+  }
+  for (int32_t j = 0; j < k; ++j) { nx[j] = j + 1 < k ? j + 1 : -1; pv[j] = j - 1; }
+  int64_t hn = 0;
+  for (int32_t j = 0; j + 1 < k; ++j) {
+    int64_t v = pair_lookup(t, (uint32_t)id[j], (uint32_t)id[j + 1]);
+    if (v >= 0) hpush(heap, &hn, (hent){(uint32_t)(v >> 32), j});
+  }
+  while (hn > 0) {
+    hent e = hpop(heap, &hn);
+    int32_t j = e.pos;
+    if (id[j] < 0 || nx[j] < 0) continue;          /* dead or last */
+    int32_t r = nx[j];
+    int64_t v = pair_lookup(t, (uint32_t)id[j], (uint32_t)id[r]);
+    if (v < 0 || (uint32_t)(v >> 32) != e.rank) continue;   /* stale */
+    id[j] = (int32_t)(v & 0xFFFFFFFF);
+    id[r] = -1;
+    nx[j] = nx[r];
+    if (nx[j] >= 0) pv[nx[j]] = j;
+    if (pv[j] >= 0) {
+      int64_t w = pair_lookup(t, (uint32_t)id[pv[j]], (uint32_t)id[j]);
+      if (w >= 0) hpush(heap, &hn, (hent){(uint32_t)(w >> 32), pv[j]});
+    }
+    if (nx[j] >= 0) {
+      int64_t w = pair_lookup(t, (uint32_t)id[j], (uint32_t)id[nx[j]]);
+      if (w >= 0) hpush(heap, &hn, (hent){(uint32_t)(w >> 32), j});
+    }
+  }
+  int64_t c = 0;
+  for (int32_t j = (k > 0 ? 0 : -1); j >= 0; j = nx[j]) out[c++] = (uint32_t)id[j];
+  free(id); free(nx); free(pv); free(heap);
+  return c;
+}
+
+/* ---------------------------------------------------------------- NFC */
+
+int tko_nfc_qc(const tko_tables* t, const uint8_t* s, int64_t nb) {
+  int32_t* cp = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nb + 1));
+  if (!cp) return -2;
+  int64_t n = tko_utf8_decode(s, nb, cp, NULL);
+  if (n < 0) { free(cp); return -1; }
+  int ok = 1;
+  uint8_t prev = 0;
+  for (int64_t i = 0; i < n && ok; ++i) {
+    uint8_t v = t->nfc_qc[cp[i]];
+    if (v == 255 || (i > 0 && prev > v && v != 0)) ok = 0;
+    prev = v;
+  }
+  free(cp);
+  return ok;
+}
+
+/* ------------------------------------------------------------- encode */
+
+int64_t tko_encode(const tko_tables* t, const uint8_t* s, int64_t nb,
+                   uint32_t* out, int64_t cap) {
+  if (nb == 0) return 0;
+  if (t->needs_nfc && t->nfc_qc) {
+    int q = tko_nfc_qc(t, s, nb);
+    if (q < 0) return q == -1 ? TKO_E_UTF8 : TKO_E_NOMEM;
+    if (q == 0) return TKO_E_NEEDS_NFC;
+  }
+  int64_t* starts = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nb + 1));
+  if (!starts) return TKO_E_NOMEM;
+  int64_t p = tko_pretokenize(t, s, nb, starts);
+  if (p < 0) { free(starts); return p == -1 ? TKO_E_UTF8 : TKO_E_NOMEM; }
+  int64_t total = 0;
+  for (int64_t k = 0; k < p; ++k) {
+    int64_t a = starts[k], b = starts[k + 1];
+    if (total + (b - a) > cap) { free(starts); return TKO_E_CAP; }
+    int64_t c = tko_bpe(t, s + a, b - a, out + total);
+    if (c < 0) { free(starts); return TKO_E_NOMEM; }
+    total += c;
+  }
+  free(starts);
+  return total;
+}

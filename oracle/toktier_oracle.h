@@ -1,0 +1,39 @@
+/* toktier_oracle.h -- CPU restatement of the fresh-encode path.
+ * TEST INFRASTRUCTURE ONLY (parity checker); see toktier_oracle.c. */
+#ifndef TOKTIER_ORACLE_H
+#define TOKTIER_ORACLE_H
+#include <stdint.h>
+
+#define TKO_RULESET_CL100K 0
+#define TKO_RULESET_R50K 1
+
+#define TKO_E_UTF8 (-1)
+#define TKO_E_NOMEM (-2)
+#define TKO_E_NEEDS_NFC (-3)
+#define TKO_E_CAP (-4)
+
+typedef struct tko_tables {
+  const uint8_t* cls;          /* 0x110000 class bytes (P/L/N/S) */
+  const uint64_t* pair_keys;
+  const uint64_t* pair_vals;
+  uint64_t pair_count;         /* power of two */
+  const int32_t* byte_id;      /* [256] */
+  const uint64_t* vocab_keys;
+  const uint64_t* vocab_vals;
+  uint64_t vocab_count;        /* power of two */
+  const uint8_t* vocab_blob;
+  const uint8_t* nfc_qc;       /* 0x110000 or NULL */
+  int32_t ruleset;
+  int32_t digits_max;
+  int32_t ignore_merges;
+  int32_t needs_nfc;
+} tko_tables;
+
+int64_t tko_utf8_decode(const uint8_t* s, int64_t nb, int32_t* cp, int64_t* bo);
+int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
+                        int64_t* starts);
+int64_t tko_bpe(const tko_tables* t, const uint8_t* s, int64_t m, uint32_t* out);
+int tko_nfc_qc(const tko_tables* t, const uint8_t* s, int64_t nb);
+int64_t tko_encode(const tko_tables* t, const uint8_t* s, int64_t nb,
+                   uint32_t* out, int64_t cap);
+#endif

@@ -1,0 +1,83 @@
+"""Build ``libtoktier_hip.so`` for gfx950 with hipcc (in-tree).
+
+The library holds the device code object (gfx950) and the C-ABI host
+engine. A manifest beside it records the sha256 of the library, the
+offload architecture, the hipcc version and the exported ``tk_*`` symbols
+(the role of the reference's ``tools/build_fatbin.py`` manifest).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "_lib"
+LIB = LIBDIR / "libtoktier_hip.so"
+MANIFEST = LIBDIR / "manifest.json"
+ARCH = "gfx950"
+
+SOURCES = ["tk_device.hip", "tk_engine.cpp"]
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Wall", "-Wno-unused-function",
+    # packed FP32 instructions stay off on this pool (no float code here)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.sep not in cand or Path(cand).exists()):
+            return cand
+    return "hipcc"
+
+
+def exported_symbols(lib: Path) -> list[str]:
+    nm = "/opt/rocm/llvm/bin/llvm-nm"
+    if not Path(nm).exists():
+        nm = "nm"
+    out = subprocess.run([nm, "-D", "--defined-only", str(lib)],
+                         capture_output=True, text=True, check=True).stdout
+    return sorted({line.split()[-1] for line in out.splitlines()
+                   if line.split() and line.split()[-1].startswith("tk_")})
+
+
+def build(verbose: bool = False) -> Path:
+    LIBDIR.mkdir(exist_ok=True)
+    tmp = LIB.with_suffix(f".so.tmp{os.getpid()}")
+    cmd = [_hipcc(), *HIPCC_FLAGS, "-o", str(tmp),
+           *[str(CSRC / s) for s in SOURCES]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc build of libtoktier_hip.so failed")
+    os.replace(tmp, LIB)
+    ver = subprocess.run([_hipcc(), "--version"], capture_output=True,
+                         text=True).stdout.strip().splitlines()
+    digest = hashlib.sha256(b"toktier-hip-lib\0" + LIB.read_bytes()).hexdigest()
+    MANIFEST.write_text(json.dumps({
+        "library": LIB.name,
+        "sha256_domain": "toktier-hip-lib",
+        "sha256": digest,
+        "architecture": ARCH,
+        "hipcc": ver[:2],
+        "flags": HIPCC_FLAGS,
+        "sources": {s: hashlib.sha256((CSRC / s).read_bytes()).hexdigest()
+                    for s in SOURCES},
+        "symbols": exported_symbols(LIB),
+    }, indent=1) + "\n")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    print(LIB)

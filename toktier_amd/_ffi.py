@@ -1,0 +1,204 @@
+"""ctypes binding of ``libtoktier_hip.so`` (the C-ABI in
+``include/toktier_hip.h``).
+
+Loading fails loudly: there is no CPU fallback behind this module.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from ._build import LIB
+
+TK_ABI_VERSION = 1
+TK_OK = 0
+TK_E_INVALID_ARG = -1
+TK_E_SHAPE = -2
+TK_E_DEVICE = -3
+TK_E_ARCH = -4
+TK_E_UTF8 = -5
+TK_E_NEEDS_NFC = -6
+TK_E_CAPACITY = -7
+TK_E_INTERNAL = -8
+TK_FLAG_NORMALIZED = 1
+
+STATUS_NAMES = {
+    TK_OK: "TK_OK", TK_E_INVALID_ARG: "TK_E_INVALID_ARG",
+    TK_E_SHAPE: "TK_E_SHAPE", TK_E_DEVICE: "TK_E_DEVICE",
+    TK_E_ARCH: "TK_E_ARCH", TK_E_UTF8: "TK_E_UTF8",
+    TK_E_NEEDS_NFC: "TK_E_NEEDS_NFC", TK_E_CAPACITY: "TK_E_CAPACITY",
+    TK_E_INTERNAL: "TK_E_INTERNAL",
+}
+
+#: every entry point include/toktier_hip.h declares
+SYMBOLS = (
+    "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
+    "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
+    "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
+    "tk_engine_last_timing", "tk_last_error",
+)
+
+
+class TkConfig(C.Structure):
+    _fields_ = [
+        ("abi_version", C.c_uint32), ("device_ordinal", C.c_int32),
+        ("ruleset", C.c_int32), ("digits_max", C.c_int32),
+        ("contractions", C.c_int32), ("needs_nfc", C.c_int32),
+        ("ignore_merges", C.c_int32), ("pair_count", C.c_uint64),
+        ("vocab_count", C.c_uint64), ("family", C.c_char_p),
+        ("artifact_sha256", C.c_char_p),
+        ("expected_architecture", C.c_char_p),
+    ]
+
+
+class EngineError(RuntimeError):
+    """A failed engine call: ``status`` is the TK_* code."""
+
+    def __init__(self, status: int, call: str, detail: str):
+        self.status = status
+        self.call = call
+        self.detail = detail
+        super().__init__(f"{call}: {STATUS_NAMES.get(status, status)}: {detail}")
+
+
+_lib: C.CDLL | None = None
+
+
+def lib(path: Path | None = None) -> C.CDLL:
+    """Load the engine library (``RuntimeError`` if it was never built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} is missing: build it with toktier_amd._build.build() "
+            "(hipcc --offload-arch=gfx950); there is no CPU fallback")
+    L = C.CDLL(str(p))
+    vp, sz = C.c_void_p, C.c_size_t
+    L.tk_last_error.restype = C.c_char_p
+    L.tk_last_error.argtypes = []
+    L.tk_engine_preflight.restype = C.c_int
+    L.tk_engine_preflight.argtypes = [C.POINTER(TkConfig)] + [vp, sz] * 7
+    L.tk_engine_open.restype = C.c_int
+    L.tk_engine_open.argtypes = ([C.POINTER(TkConfig)] + [vp, sz] * 9
+                                 + [C.POINTER(vp)])
+    L.tk_engine_close.restype = None
+    L.tk_engine_close.argtypes = [vp]
+    L.tk_engine_encode.restype = C.c_int
+    L.tk_engine_encode.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
+                                   C.POINTER(sz)]
+    L.tk_engine_encode_batch.restype = C.c_int
+    L.tk_engine_encode_batch.argtypes = [vp, vp, vp, sz, C.c_uint32, vp, sz,
+                                         vp, vp]
+    L.tk_engine_encode_device.restype = C.c_int
+    L.tk_engine_encode_device.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
+                                          C.POINTER(sz), vp]
+    L.tk_engine_delivery.restype = C.c_char_p
+    L.tk_engine_delivery.argtypes = [vp]
+    L.tk_engine_architecture.restype = C.c_char_p
+    L.tk_engine_architecture.argtypes = [vp]
+    L.tk_engine_set_timing.restype = C.c_int
+    L.tk_engine_set_timing.argtypes = [vp, C.c_int]
+    L.tk_engine_last_timing.restype = C.c_int
+    L.tk_engine_last_timing.argtypes = [vp, C.POINTER(C.c_double), C.c_int]
+    if path is None:
+        _lib = L
+    return L
+
+
+def check(status: int, call: str) -> None:
+    if status != TK_OK:
+        detail = (lib().tk_last_error() or b"").decode("utf-8", "replace")
+        raise EngineError(status, call, detail)
+
+
+def _ptr(a: np.ndarray | None) -> tuple[int | None, int]:
+    if a is None:
+        return None, 0
+    a = np.ascontiguousarray(a)
+    return a.ctypes.data, a.nbytes
+
+
+class Engine:
+    """One opened engine (a family's tables resident on one GPU)."""
+
+    def __init__(self, cfg: TkConfig, class_table, tables, nfc_qc):
+        self._L = lib()
+        self._keep = (cfg, class_table, tables, nfc_qc)
+        args = []
+        blob = tables.vocab_blob if tables.vocab_blob.size else np.zeros(1, np.uint8)
+        unsafe = tables.unsafe_bits if tables.unsafe_bits.size else np.zeros(0, np.uint32)
+        self._keep = self._keep + (blob, unsafe)
+        for arr in (class_table, tables.pair_keys, tables.pair_vals,
+                    tables.byte_id, tables.vocab_keys, tables.vocab_vals,
+                    blob, unsafe, nfc_qc):
+            args.extend(_ptr(arr))
+        handle = C.c_void_p()
+        check(self._L.tk_engine_open(C.byref(cfg), *args, C.byref(handle)),
+              "tk_engine_open")
+        self._h = handle
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.tk_engine_close(self._h)
+            self._h = None
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter teardown
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def delivery(self) -> str:
+        return self._L.tk_engine_delivery(self._h).decode()
+
+    @property
+    def architecture(self) -> str:
+        return self._L.tk_engine_architecture(self._h).decode()
+
+    def encode(self, data: bytes, flags: int = 0) -> np.ndarray:
+        out = np.empty(max(1, len(data)), dtype=np.uint32)
+        n = C.c_size_t()
+        st = self._L.tk_engine_encode(self._h, data, len(data), flags,
+                                      out.ctypes.data, out.size, C.byref(n))
+        check(st, "tk_engine_encode")
+        return out[: n.value]
+
+    def encode_batch(self, docs: list[bytes], flags: int = 0
+                     ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        offs = np.zeros(len(docs) + 1, dtype=np.uint64)
+        if docs:
+            offs[1:] = np.cumsum([len(d) for d in docs], dtype=np.uint64)
+        joined = b"".join(docs)
+        ids = np.empty(max(1, len(joined)), dtype=np.uint32)
+        rows = np.zeros(len(docs) + 1, dtype=np.uint64)
+        status = np.zeros(max(1, len(docs)), dtype=np.int32)
+        st = self._L.tk_engine_encode_batch(
+            self._h, joined, offs.ctypes.data, len(docs), flags,
+            ids.ctypes.data, ids.size, rows.ctypes.data, status.ctypes.data)
+        check(st, "tk_engine_encode_batch")
+        return ids, rows, status[: len(docs)]
+
+    def encode_device(self, d_text: int, nbytes: int, d_ids: int,
+                      ids_cap: int, flags: int = 0, stream: int | None = None
+                      ) -> int:
+        n = C.c_size_t()
+        st = self._L.tk_engine_encode_device(self._h, d_text, nbytes, flags,
+                                             d_ids, ids_cap, C.byref(n),
+                                             stream)
+        check(st, "tk_engine_encode_device")
+        return n.value
+
+    def set_timing(self, on: bool) -> None:
+        check(self._L.tk_engine_set_timing(self._h, int(on)),
+              "tk_engine_set_timing")
+
+    def last_timing(self) -> list[float]:
+        buf = (C.c_double * 5)()
+        k = self._L.tk_engine_last_timing(self._h, buf, 5)
+        return list(buf[:k])

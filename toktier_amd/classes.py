@@ -1,0 +1,56 @@
+"""Per-codepoint tables shipped with the package.
+
+Both tables are probed from the certified engine by
+``toktier_amd.tables_gen`` and verified here against the sha256 of the
+reference's own tables (``src/toktier/kernels/tables/kernel_families.v1.json:11``
+for ``cl100k_v3``, ``:65`` for ``nfc_qc_v1``; digest of the ``.npy``
+serialisation of the 0x110000-entry ``uint8`` array). A table that does not
+hash to its pin is refused.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import io
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+TABLE_DIR = Path(__file__).resolve().parent / "data" / "tables"
+PLANE = 0x110000
+
+CLASS_TABLE_SHA256 = "aab53c6705260d07f65d9762aecba729b18e11cb9710a4aea54157475cbfdf97"
+NFC_QC_SHA256 = "1a7d121e9092cdf577d992452393d25116b2577ab74dd5a067e6ca00a535d311"
+
+__all__ = ["class_table", "nfc_qc_table", "npy_sha256", "PLANE"]
+
+
+def npy_sha256(arr: np.ndarray) -> str:
+    buf = io.BytesIO()
+    np.save(buf, arr)
+    return hashlib.sha256(buf.getvalue()).hexdigest()
+
+
+def _load(name: str, key: str, sha: str) -> np.ndarray:
+    with np.load(TABLE_DIR / name, allow_pickle=False) as z:
+        arr = np.ascontiguousarray(z[key], dtype=np.uint8)
+    if arr.shape != (PLANE,):
+        raise ValueError(f"{name}: bad shape {arr.shape}")
+    got = npy_sha256(arr)
+    if got != sha:
+        raise ValueError(f"{name}: sha256 {got} != pinned {sha}")
+    arr.setflags(write=False)
+    return arr
+
+
+@lru_cache(maxsize=None)
+def class_table() -> np.ndarray:
+    """Classes P=0, L=1, N=2, S=3 for every codepoint."""
+    return _load("classes.npz", "cl100k", CLASS_TABLE_SHA256)
+
+
+@lru_cache(maxsize=None)
+def nfc_qc_table() -> np.ndarray:
+    """NFC quick-check values: 0 safe starter, 1..K class rank, 255 unsafe."""
+    return _load("nfc_qc.npz", "nfc_qc", NFC_QC_SHA256)

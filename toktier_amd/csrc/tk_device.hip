@@ -1,0 +1,687 @@
+// tk_device.hip -- gfx950 kernels of the fresh-encode path.
+//
+// Stages (one stream, no host round trip in between):
+//   1. k_pretok       per byte: UTF-8 validation, class lookup, NFC quick
+//                     check, and the family split rules as a per-character
+//                     piece-start predicate -> one start bit per byte.
+//   2. k_bpe_small    one wave64 per 64-byte window, lane = byte: every piece
+//                     that lies inside the window is merged in place (lowest
+//                     rank pair, leftmost first) with segmented wave
+//                     reductions; run twice, on the aligned grid and on the
+//                     grid shifted by 32 bytes, so every piece of <= 32
+//                     bytes is handled here. Pieces that fit neither grid
+//                     are queued for stage 3.
+//   3. k_bpe_long     one thread per queued piece: heap-ordered exact merge
+//                     over global scratch.
+//   4. k_count / k_scan / k_compact: device-wide compaction of the per-byte
+//                     token slots into the contiguous id buffer.
+// Token j of a piece is stored at the byte where that token starts, so the
+// id order is the byte order and stage 4 needs no per-piece counts.
+//
+// Split semantics follow the family regexes alternative by alternative
+// (Qwen2 / Llama-3: crates/toktier-gigatoken-core/src/pretokenize/
+// options.rs:125,:131; GPT-2: options.rs:118), restated per character in
+// the way src/toktier/kernels/pretok_kernel.cu:8-27 describes for the
+// cl100k rules; the r50k predicate is this project's own derivation.
+// BPE semantics: HF tokenizers 0.22.2 (lowest rank first, leftmost on
+// ties; pretok_kernel.cu:872-881); table formats: bpe_tables.py:99-132.
+#include "tk_device.h"
+
+namespace tk {
+
+constexpr uint8_t CP_ = 0, CL_ = 1, CN_ = 2, CS_ = 3;
+
+// ------------------------------------------------------------ helpers
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ULL;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+  return x ^ (x >> 31);
+}
+
+// rank<<32 | merged id, or ~0 when the pair has no merge rule
+__device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
+                                                uint32_t l, uint32_t r) {
+  const uint64_t key = ((uint64_t)l << 32) | r;
+  uint64_t i = splitmix64(key) & t.pair_mask;
+  for (;;) {
+    const ulonglong2 s = t.pairs[i];
+    if (s.x == key) return s.y;
+    if (s.x == ~0ULL) return ~0ULL;
+    i = (i + 1) & t.pair_mask;
+  }
+}
+
+// whole-piece vocabulary id (ignore_merges) or -1
+__device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
+                                int64_t m) {
+  uint64_t h = 0xCBF29CE484222325ULL;
+  for (int64_t j = 0; j < m; ++j) h = (h ^ s[j]) * 0x100000001B3ULL;
+  uint64_t i = splitmix64(h) & t.vocab_mask;
+  for (;;) {
+    const ulonglong2 e = t.vocab[i];
+    if (e.x == ~0ULL) return -1;
+    if (e.x == h) {
+      const int64_t len = (int64_t)((e.y >> 20) & 0x3FF);
+      const uint64_t off = e.y >> 30;
+      if (len == m) {
+        bool eq = true;
+        for (int64_t j = 0; j < m && eq; ++j) eq = t.blob[off + j] == s[j];
+        if (eq) return (int32_t)(e.y & 0xFFFFF);
+      }
+    }
+    i = (i + 1) & t.vocab_mask;
+  }
+}
+
+__device__ __forceinline__ bool is_cont(uint8_t b) { return (b & 0xC0) == 0x80; }
+__device__ __forceinline__ bool crlf(int32_t c) { return c == 10 || c == 13; }
+__device__ __forceinline__ int fold(int32_t c) {
+  if (c >= 'A' && c <= 'Z') return c + 32;
+  if (c == 0x17F) return 's';
+  return c;
+}
+
+struct PCtx {
+  const uint8_t* t;
+  int64_t nb;
+  const uint64_t* dm;
+  const uint8_t* cls;
+};
+
+__device__ __forceinline__ bool is_ds(const PCtx& c, int64_t i) {
+  if (i == 0) return true;
+  return c.dm && ((c.dm[i >> 6] >> (i & 63)) & 1);
+}
+
+// Decode the character that starts at byte i (i < nb, not a continuation
+// byte). *ok is false for any invalid form; the value is then U+FFFD.
+__device__ int32_t decode_full(const PCtx& c, int64_t i, bool* ok) {
+  const uint32_t b0 = c.t[i];
+  int need;
+  uint32_t v;
+  if (b0 < 0x80) { *ok = true; return (int32_t)b0; }
+  if (b0 < 0xC0) { *ok = false; return 0xFFFD; }
+  if (b0 < 0xE0) { need = 1; v = b0 & 0x1F; }
+  else if (b0 < 0xF0) { need = 2; v = b0 & 0x0F; }
+  else if (b0 < 0xF8) { need = 3; v = b0 & 0x07; }
+  else { *ok = false; return 0xFFFD; }
+  for (int k = 1; k <= need; ++k) {
+    if (i + k >= c.nb) { *ok = false; return 0xFFFD; }
+    const uint32_t x = c.t[i + k];
+    if ((x & 0xC0) != 0x80) { *ok = false; return 0xFFFD; }
+    v = (v << 6) | (x & 0x3F);
+  }
+  if ((need == 1 && v < 0x80) || (need == 2 && v < 0x800) ||
+      (need == 3 && v < 0x10000) || v > 0x10FFFF ||
+      (v >= 0xD800 && v <= 0xDFFF)) {
+    *ok = false;
+    return 0xFFFD;
+  }
+  *ok = true;
+  return (int32_t)v;
+}
+
+__device__ __forceinline__ int32_t decode_cp(const PCtx& c, int64_t i) {
+  bool ok;
+  return decode_full(c, i, &ok);
+}
+
+struct Ch {
+  int64_t pos;
+  int32_t cp;
+  uint8_t cl;
+};
+
+__device__ __forceinline__ Ch char_at(const PCtx& c, int64_t p) {
+  const int32_t cp = decode_cp(c, p);
+  return Ch{p, cp, c.cls[cp]};
+}
+
+// start of the character before the one at p; -1 if p starts a document
+__device__ __forceinline__ int64_t prev_pos(const PCtx& c, int64_t p) {
+  if (is_ds(c, p)) return -1;
+  int64_t q = p - 1;
+  int k = 0;
+  while (q > 0 && k < 3 && is_cont(c.t[q])) { --q; ++k; }
+  return q;
+}
+
+// start of the character after the one at p; -1 at text / document end
+__device__ __forceinline__ int64_t next_pos(const PCtx& c, int64_t p) {
+  int64_t q = p + 1;
+  int k = 0;
+  while (q < c.nb && k < 3 && is_cont(c.t[q])) { ++q; ++k; }
+  if (q >= c.nb || is_ds(c, q)) return -1;
+  return q;
+}
+
+// Is the apostrophe (or other P char) at q the start of a regex match?
+// It is unless it continues a P run or follows a U+0020 that the
+// " ?[^\s\p{L}\p{N}]+" alternative takes with it.
+__device__ __forceinline__ bool p_arrives(const PCtx& c, int64_t q) {
+  const int64_t r = prev_pos(c, q);
+  if (r < 0) return true;
+  const Ch x = char_at(c, r);
+  return x.cl != CP_ && x.cp != ' ';
+}
+
+// ---- cl100k (Qwen2 / Llama-3) piece-start predicate for a character
+// that does not start a document.
+__device__ bool start_cl100k(const PCtx& c, const Ch& ci, int dmax) {
+  const Ch p1 = char_at(c, prev_pos(c, ci.pos));
+  if (ci.cl == CN_) {
+    // \p{N}{1,K}: digit runs split into groups of K from the run start
+    if (dmax <= 1) return true;
+    int64_t n = 0;
+    for (int64_t q = ci.pos;;) {
+      const int64_t r = prev_pos(c, q);
+      if (r < 0 || char_at(c, r).cl != CN_) break;
+      ++n;
+      q = r;
+    }
+    return n % dmax == 0;
+  }
+  if (ci.cl == CL_) {
+    if (p1.cl != CL_) {
+      // run head: taken by the preceding char as the optional prefix of
+      // [^\r\n\p{L}\p{N}]?\p{L}+ (non-CR/LF whitespace, or a single P
+      // char that starts its own match -- the contraction alternative
+      // consumes the letter just as well)
+      if (p1.cl == CS_) return crlf(p1.cp);
+      if (p1.cl == CP_) return !p_arrives(c, p1.pos);
+      return true;
+    }
+    // inside a letter run: only a contraction match can end here
+    const int64_t q2 = prev_pos(c, p1.pos);
+    if (q2 < 0) return false;
+    const Ch p2 = char_at(c, q2);
+    if (p2.cp == '\'') {
+      const int f1 = fold(p1.cp);
+      return (f1 == 's' || f1 == 't' || f1 == 'm' || f1 == 'd') &&
+             p_arrives(c, q2);
+    }
+    if (p2.cl != CL_) return false;
+    const int64_t q3 = prev_pos(c, q2);
+    if (q3 < 0) return false;
+    if (char_at(c, q3).cp != '\'') return false;
+    const int f1 = fold(p2.cp), f2 = fold(p1.cp);
+    return ((f1 == 'r' && f2 == 'e') || (f1 == 'v' && f2 == 'e') ||
+            (f1 == 'l' && f2 == 'l')) &&
+           p_arrives(c, q3);
+  }
+  if (ci.cl == CP_) return p1.cl != CP_ && p1.cp != ' ';
+  // whitespace
+  const bool cr_i = crlf(ci.cp);
+  if (p1.cl != CS_) return !(p1.cl == CP_ && cr_i);  // [\r\n]* absorption
+  const bool cr_1 = crlf(p1.cp);
+  if (cr_1 && !cr_i) {
+    // right after the last CR/LF of the run (end of \s*[\r\n]+) ...
+    bool more = false;
+    for (int64_t q = next_pos(c, ci.pos); q >= 0; q = next_pos(c, q)) {
+      const Ch x = char_at(c, q);
+      if (x.cl != CS_) break;
+      if (crlf(x.cp)) { more = true; break; }
+    }
+    if (!more) return true;
+    // ... or the first char the P match's [\r\n]* left over
+    for (int64_t q = p1.pos;;) {
+      const int64_t r = prev_pos(c, q);
+      if (r < 0) return false;
+      const Ch x = char_at(c, r);
+      if (x.cl != CS_) return x.cl == CP_;
+      if (!crlf(x.cp)) return false;
+      q = r;
+    }
+  }
+  if (!cr_1 && !cr_i) {
+    // \s+(?!\S) backs off one char before a non-space (not at text end)
+    const int64_t q = next_pos(c, ci.pos);
+    return q >= 0 && char_at(c, q).cl != CS_;
+  }
+  return false;
+}
+
+// ---- r50k (GPT-2) piece-start predicate.
+__device__ bool start_r50k(const PCtx& c, const Ch& ci) {
+  const Ch p1 = char_at(c, prev_pos(c, ci.pos));
+  if (ci.cl == CS_) {
+    if (p1.cl != CS_) return true;
+    const int64_t q = next_pos(c, ci.pos);
+    return q >= 0 && char_at(c, q).cl != CS_;
+  }
+  if (ci.cl == CN_ || ci.cl == CP_) {
+    if (p1.cl == ci.cl) return false;
+    return p1.cp != ' ';
+  }
+  if (p1.cl != CL_) {
+    if (p1.cp == ' ') return false;
+    if (p1.cp == '\'' && p_arrives(c, p1.pos)) {
+      const int a = ci.cp;
+      if (a == 's' || a == 't' || a == 'm' || a == 'd') return false;
+      const int64_t qn = next_pos(c, ci.pos);
+      if (qn >= 0) {
+        const int b = char_at(c, qn).cp;
+        if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+            (a == 'l' && b == 'l'))
+          return false;
+      }
+    }
+    return true;
+  }
+  const int64_t q2 = prev_pos(c, p1.pos);
+  if (q2 < 0) return false;
+  const Ch p2 = char_at(c, q2);
+  if (p2.cp == '\'') {
+    const int a = p1.cp;
+    return (a == 's' || a == 't' || a == 'm' || a == 'd') && p_arrives(c, q2);
+  }
+  if (p2.cl != CL_) return false;
+  const int64_t q3 = prev_pos(c, q2);
+  if (q3 < 0 || char_at(c, q3).cp != '\'') return false;
+  const int a = p2.cp, b = p1.cp;
+  return ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+          (a == 'l' && b == 'l')) &&
+         p_arrives(c, q3);
+}
+
+// ------------------------------------------------------ 1. pretokenize
+
+__global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
+                                                       int64_t cover) {
+  const int64_t g = (int64_t)blockIdx.x * PRETOK_TPB + threadIdx.x;
+  const int64_t base = g * PRETOK_BYTES_PER_THREAD;
+  if (base >= cover) return;
+  const PCtx c{w.text, w.nb, w.docmask, t.cls};
+  uint32_t bits = 0, st = 0;
+  for (int k = 0; k < PRETOK_BYTES_PER_THREAD; ++k) {
+    const int64_t i = base + k;
+    if (i >= w.nb) { bits |= 1u << k; continue; }  // sentinel starts
+    const uint8_t b = w.text[i];
+    if (is_cont(b)) {
+      // a continuation byte must be claimed by a lead at most 3 back
+      int64_t q = i - 1;
+      int back = 1;
+      while (q >= 0 && back <= 3 && is_cont(w.text[q])) { --q; ++back; }
+      bool ok = false;
+      if (q >= 0 && back <= 3) {
+        const uint8_t l = w.text[q];
+        const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2
+                       : l >= 0xC0 ? 1 : 0;
+        ok = need >= back;
+      }
+      if (!ok) st |= ST_UTF8;
+      continue;
+    }
+    bool ok;
+    const int32_t cp = decode_full(c, i, &ok);
+    if (!ok) st |= ST_UTF8;
+    const Ch ci{i, cp, t.cls[cp]};
+    const bool ds = is_ds(c, i);
+    bool s = ds;
+    if (!ds) s = t.ruleset == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
+    if (s) bits |= 1u << k;
+    if (w.check_nfc) {
+      const uint8_t v = t.nfc[cp];
+      if (v == 255) {
+        st |= ST_NFC;
+      } else if (v != 0 && !ds) {
+        const uint8_t pv = t.nfc[decode_cp(c, prev_pos(c, i))];
+        if (pv > v) st |= ST_NFC;
+      }
+    }
+  }
+  reinterpret_cast<uint16_t*>(w.starts)[g] = (uint16_t)bits;
+  if (st) atomicOr(w.status, st);
+}
+
+hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64;
+  const int64_t cover = (nwin + 2) * 64;  // words 0..nwin+1
+  const int64_t threads = cover / PRETOK_BYTES_PER_THREAD;
+  const int64_t blocks = (threads + PRETOK_TPB - 1) / PRETOK_TPB;
+  hipLaunchKernelGGL(k_pretok, dim3((uint32_t)blocks), dim3(PRETOK_TPB), 0, s,
+                     t, w, cover);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------ 2. short-piece BPE
+
+__device__ __forceinline__ uint64_t mask_le(int lane) {
+  return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
+}
+
+__global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
+                                                   int phase, int64_t nwin) {
+  const int lane = threadIdx.x & 63;
+  const int64_t win = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (win >= nwin) return;  // whole wave
+  const int64_t base = phase == 0 ? win * 64 : win * 64 - 32;
+  uint64_t S;
+  bool E;
+  if (phase == 0) {
+    S = w.starts[win];
+    E = w.starts[win + 1] & 1;
+  } else {
+    const uint64_t lo = win > 0 ? w.starts[win - 1] : ~0ULL;
+    S = (lo >> 32) | (w.starts[win] << 32);
+    E = (w.starts[win] >> 32) & 1;
+  }
+  const int64_t pos = base + lane;
+  const bool valid = pos >= 0 && pos < w.nb;
+  const uint64_t le = S & mask_le(lane);
+  const int ps = le ? 63 - __builtin_clzll(le) : -1;
+  const uint64_t gt = S & ~mask_le(lane);
+  const int pe = gt ? __builtin_ctzll(gt) : 64;
+  const bool contained = ps >= 0 && (pe < 64 || E);
+  bool elig = valid && contained;
+  if (phase == 1 && elig) {
+    const int64_t a = base + ps, b = base + pe;
+    if ((a >> 6) == ((b - 1) >> 6)) elig = false;  // aligned grid has it
+  }
+  if (phase == 0 && valid && ps == lane && !contained) {
+    // this piece runs past the window: find its end, queue it if neither
+    // grid holds it whole
+    // (bit 0 of the next word is clear here: E is false; the sentinel
+    // bits at and after nb end the search inside the nwin+2 words)
+    int64_t wd = win + 1;
+    uint64_t word = w.starts[wd];
+    while (word == 0) word = w.starts[++wd];
+    const int64_t b = wd * 64 + __builtin_ctzll(word);
+    const int64_t a = pos;
+    if (b - a > 64 || ((a + 32) >> 6) != ((b - 1 + 32) >> 6)) {
+      const uint32_t k = atomicAdd(w.longcount, 1u);
+      if (k < w.long_cap) {
+        w.longlist[2 * k] = (uint32_t)a;
+        w.longlist[2 * k + 1] = (uint32_t)b;
+      } else {
+        atomicOr(w.status, ST_LONGOVF);
+      }
+    }
+  }
+
+  const uint32_t byte = valid ? w.text[pos] : 0u;
+  const int32_t bid = elig ? t.byte_id[byte] : -1;
+  uint64_t live = __ballot(bid >= 0);
+  uint32_t sym = (uint32_t)bid;
+  int isb = 1;
+  const int src_ps = ps >= 0 ? ps : lane;
+
+  if (t.ignore_merges) {
+    const bool lead = elig && lane == ps;
+    int32_t hit = -1;
+    if (lead) hit = vocab_lookup(t, w.text + pos, pe - ps);
+    const uint64_t hm = __ballot(hit >= 0);
+    const int32_t hid = __shfl(hit, src_ps);
+    const bool phit = elig && ((hm >> src_ps) & 1);
+    if (phit && lane == ps) { sym = (uint32_t)hid; isb = 0; }
+    live &= ~__ballot(phit && lane != ps);
+  }
+
+  uint32_t rk = RANK_INF, mid = 0;
+  bool dirty = true;
+  for (;;) {
+    const bool me = (live >> lane) & 1;
+    const uint64_t after = live & ~mask_le(lane);
+    const int nx = after ? __builtin_ctzll(after) : 64;
+    const int src = nx < 64 ? nx : lane;
+    const uint32_t nsym = __shfl(sym, src);
+    const int nisb = __shfl(isb, src);
+    const uint32_t nbyte = __shfl(byte, src);
+    if (dirty) {
+      rk = RANK_INF;
+      if (elig && me && nx < pe) {
+        const uint64_t v = (isb && nisb) ? t.bytepair[(byte << 8) | nbyte]
+                                         : pair_lookup(t, sym, nsym);
+        if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+      }
+      dirty = false;
+    }
+    const uint32_t key = rk != RANK_INF ? ((rk << 6) | (uint32_t)lane) : RANK_INF;
+    uint32_t m = key;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t o = __shfl_down(m, d);
+      if (lane + d < pe) m = min(m, o);
+    }
+    const uint32_t pm = __shfl(m, src_ps);
+    const bool act = elig && pm != RANK_INF;
+    if (!__any(act)) break;
+    const bool win_ = act && key == pm;
+    const uint64_t wm = __ballot(win_);
+    const uint64_t before = live & ((1ULL << lane) - 1);
+    const int pv = before ? 63 - __builtin_clzll(before) : -1;
+    const bool dies = me && pv >= 0 && ((wm >> pv) & 1);
+    if (win_) { sym = mid; isb = 0; }
+    live &= ~__ballot(dies);
+    const uint64_t after2 = live & ~mask_le(lane);
+    const int nx2 = after2 ? __builtin_ctzll(after2) : 64;
+    dirty = win_ || (((live >> lane) & 1) && nx2 < 64 && ((wm >> nx2) & 1));
+  }
+  if (elig) w.tok[pos] = ((live >> lane) & 1) ? sym : INVALID_ID;
+}
+
+hipError_t launch_bpe_small(const DevTables& t, const DevWork& w, int phase,
+                            hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64 + (phase == 1 ? 1 : 0);
+  const int64_t blocks = (nwin + 3) / 4;
+  hipLaunchKernelGGL(k_bpe_small, dim3((uint32_t)blocks), dim3(256), 0, s, t,
+                     w, phase, nwin);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------- 3. long-piece BPE
+
+__device__ __forceinline__ void heap_push(uint64_t* h, uint32_t& n, uint64_t e) {
+  uint32_t i = n++;
+  h[i] = e;
+  while (i > 0) {
+    const uint32_t p = (i - 1) >> 1;
+    if (h[p] <= h[i]) break;
+    const uint64_t x = h[p]; h[p] = h[i]; h[i] = x;
+    i = p;
+  }
+}
+
+__device__ __forceinline__ uint64_t heap_pop(uint64_t* h, uint32_t& n) {
+  const uint64_t top = h[0];
+  h[0] = h[--n];
+  uint32_t i = 0;
+  for (;;) {
+    const uint32_t l = 2 * i + 1, r = l + 1;
+    uint32_t m = i;
+    if (l < n && h[l] < h[m]) m = l;
+    if (r < n && h[r] < h[m]) m = r;
+    if (m == i) break;
+    const uint64_t x = h[m]; h[m] = h[i]; h[i] = x;
+    i = m;
+  }
+  return top;
+}
+
+__device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
+                           uint32_t b) {
+  uint32_t* tok = w.tok;
+  if (t.ignore_merges) {
+    const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
+    if (hit >= 0) {
+      tok[a] = (uint32_t)hit;
+      for (uint32_t p = a + 1; p < b; ++p) tok[p] = INVALID_ID;
+      return;
+    }
+  }
+  int32_t* nx = w.nx;
+  int32_t* pv = w.pv;
+  uint64_t* h = w.heap + 3ull * a;
+  uint32_t hn = 0;
+  int32_t prev = -1;
+  for (uint32_t p = a; p < b; ++p) {
+    const int32_t id = t.byte_id[w.text[p]];
+    if (id < 0) { tok[p] = INVALID_ID; continue; }
+    tok[p] = (uint32_t)id;
+    pv[p] = prev;
+    if (prev >= 0) nx[prev] = (int32_t)p;
+    prev = (int32_t)p;
+  }
+  if (prev >= 0) nx[prev] = -1;
+  for (uint32_t p = a; p < b; ++p) {
+    if (tok[p] == INVALID_ID || nx[p] < 0) continue;
+    const uint64_t v = t.bytepair[((uint32_t)w.text[p] << 8) | w.text[nx[p]]];
+    if (v != ~0ULL) heap_push(h, hn, (v & 0xFFFFFFFF00000000ULL) | p);
+  }
+  while (hn > 0) {
+    const uint64_t e = heap_pop(h, hn);
+    const uint32_t p = (uint32_t)e;
+    const uint32_t r = (uint32_t)(e >> 32);
+    if (tok[p] == INVALID_ID || nx[p] < 0) continue;
+    const int32_t q = nx[p];
+    const uint64_t v = pair_lookup(t, tok[p], tok[q]);
+    if (v == ~0ULL || (uint32_t)(v >> 32) != r) continue;  // stale entry
+    tok[p] = (uint32_t)v;
+    tok[q] = INVALID_ID;
+    nx[p] = nx[q];
+    if (nx[p] >= 0) pv[nx[p]] = (int32_t)p;
+    if (pv[p] >= 0) {
+      const uint64_t u = pair_lookup(t, tok[pv[p]], tok[p]);
+      if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | (uint32_t)pv[p]);
+    }
+    if (nx[p] >= 0) {
+      const uint64_t u = pair_lookup(t, tok[p], tok[nx[p]]);
+      if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | p);
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void k_bpe_long(DevTables t, DevWork w) {
+  uint32_t n = *w.longcount;
+  if (n > w.long_cap) n = w.long_cap;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride)
+    bpe_serial(t, w, w.longlist[2 * k], w.longlist[2 * k + 1]);
+}
+
+hipError_t launch_bpe_long(const DevTables& t, const DevWork& w,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(k_bpe_long, dim3(1024), dim3(64), 0, s, t, w);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------ 4. compaction
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(v, d);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// exclusive scan of one value per thread over a 256-thread block
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
+  __shared__ uint32_t wsum[4];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t inc = wave_incl_scan(v, lane);
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
+  for (int k = 0; k < 4; ++k) {
+    if (k < wv) off += wsum[k];
+    tot += wsum[k];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+__global__ __launch_bounds__(COMPACT_TPB) void k_count(DevWork w, int64_t nblk) {
+  const int64_t blk = blockIdx.x;
+  const int64_t p0 = blk * COMPACT_BLOCK + (int64_t)threadIdx.x * COMPACT_PER_THREAD;
+  uint32_t c = 0;
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = p0 + k;
+    if (p < w.nb && w.tok[p] != INVALID_ID) ++c;
+  }
+  uint32_t tot;
+  block_excl_scan(c, &tot);
+  if (threadIdx.x == 0) w.blkcount[blk] = tot;
+}
+
+__global__ __launch_bounds__(1024) void k_scan(DevWork w, int64_t nblk) {
+  __shared__ uint32_t part[1024];
+  const int64_t per = (nblk + 1023) / 1024;
+  const int64_t lo = threadIdx.x * per;
+  uint32_t s = 0;
+  for (int64_t k = lo; k < lo + per && k < nblk; ++k) s += w.blkcount[k];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (int k = 0; k < 1024; ++k) { const uint32_t x = part[k]; part[k] = acc; acc += x; }
+    w.blkprefix[nblk] = acc;
+    w.status[1] = acc;
+  }
+  __syncthreads();
+  uint32_t acc = part[threadIdx.x];
+  for (int64_t k = lo; k < lo + per && k < nblk; ++k) {
+    w.blkprefix[k] = acc;
+    acc += w.blkcount[k];
+  }
+}
+
+__global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w) {
+  const int64_t blk = blockIdx.x;
+  const int64_t p0 = blk * COMPACT_BLOCK + (int64_t)threadIdx.x * COMPACT_PER_THREAD;
+  uint32_t c = 0;
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = p0 + k;
+    if (p < w.nb && w.tok[p] != INVALID_ID) ++c;
+  }
+  uint32_t tot;
+  uint32_t off = block_excl_scan(c, &tot) + w.blkprefix[blk];
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = p0 + k;
+    if (p < w.nb) {
+      const uint32_t v = w.tok[p];
+      if (v != INVALID_ID) w.out[off++] = v;
+    }
+  }
+}
+
+hipError_t launch_compact(const DevWork& w, hipStream_t s) {
+  const int64_t nblk = (w.nb + COMPACT_BLOCK - 1) / COMPACT_BLOCK;
+  if (nblk > 0) {
+    hipLaunchKernelGGL(k_count, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0, s, w, nblk);
+  }
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, w, nblk);
+  if (nblk > 0) {
+    hipLaunchKernelGGL(k_compact, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0, s, w);
+  }
+  return hipGetLastError();
+}
+
+// row d starts at the number of tokens whose first byte lies before
+// doc_offsets[d]
+__global__ void k_doc_offsets(DevWork w, const uint64_t* doc_offsets,
+                              uint32_t n, uint64_t* rows) {
+  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d > n) return;
+  int64_t p = (int64_t)doc_offsets[d];
+  if (p > w.nb) p = w.nb;
+  const int64_t blk = p / COMPACT_BLOCK;
+  uint64_t c = w.blkprefix[blk];
+  for (int64_t q = blk * COMPACT_BLOCK; q < p; ++q) c += w.tok[q] != INVALID_ID;
+  rows[d] = c;
+}
+
+hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
+                              uint32_t n_docs, uint64_t* row_offsets,
+                              hipStream_t s) {
+  const uint32_t n = n_docs + 1;
+  hipLaunchKernelGGL(k_doc_offsets, dim3((n + 63) / 64), dim3(64), 0, s, w,
+                     doc_offsets, n_docs, row_offsets);
+  return hipGetLastError();
+}
+
+}  // namespace tk

@@ -1,0 +1,562 @@
+// tk_engine.cpp -- host side of the gfx950 fresh-encode engine and its
+// C-ABI (include/toktier_hip.h).
+//
+// Mirrors the reference executor (crates/toktier-routing-core/src/gpu.rs):
+// table validation (validate_tables :1642-1679), device open with an
+// architecture check (Executor::new :248-344), a capacity-sized workspace
+// reused across calls (ensure_workspace :370-381), one stream, the encode
+// sequence H2D -> stages -> count read -> ids read (encode_in_workspace
+// :570-600), and the batched channel with forced starts at document heads
+// (Executor::encode_batch :605-750). Unlike the reference host, the NFC
+// decision is taken on the device (quick check fused into the pretokenize
+// stage); only a failing text goes back to the caller for exact
+// normalization (TK_E_NEEDS_NFC).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/toktier_hip.h"
+#include "tk_device.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(call)                                                      \
+  do {                                                                     \
+    hipError_t e_ = (call);                                                \
+    if (e_ != hipSuccess)                                                  \
+      return fail(TK_E_DEVICE, "%s failed: %s (%s)", #call,                \
+                  hipGetErrorName(e_), hipGetErrorString(e_));             \
+  } while (0)
+
+constexpr size_t PLANE = 0x110000;
+
+bool pow2(uint64_t x) { return x && !(x & (x - 1)); }
+
+template <class T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  ~DevBuf() { reset(); }
+  void reset() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  hipError_t alloc(size_t count) {
+    reset();
+    void* q = nullptr;
+    hipError_t e = hipMalloc(&q, count ? count * sizeof(T) : 1);
+    if (e == hipSuccess) { p = static_cast<T*>(q); n = count; }
+    return e;
+  }
+};
+
+// 64-bit splitmix, the pair-table slot function (bpe_tables.py:107-111)
+uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ULL;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+  return x ^ (x >> 31);
+}
+
+uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
+                          uint64_t count, uint32_t l, uint32_t r) {
+  const uint64_t key = ((uint64_t)l << 32) | r, mask = count - 1;
+  uint64_t i = splitmix64(key) & mask;
+  for (uint64_t probes = 0; probes < count; ++probes) {
+    if (keys[i] == key) return vals[i];
+    if (keys[i] == ~0ULL) return ~0ULL;
+    i = (i + 1) & mask;
+  }
+  return ~0ULL;
+}
+
+}  // namespace
+
+struct tk_engine {
+  std::mutex mu;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string family, sha, arch;
+  tk_config cfg{};
+  // tables
+  DevBuf<uint8_t> cls, nfc, blob;
+  DevBuf<ulonglong2> pairs, vocab;
+  DevBuf<uint64_t> bytepair;
+  DevBuf<int32_t> byte_id;
+  std::vector<uint8_t> host_nfc;
+  tk::DevTables t{};
+  // workspace
+  size_t cap = 0;
+  DevBuf<uint8_t> text;
+  DevBuf<uint64_t> starts, docmask, heap, docoffs, rows;
+  DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
+  DevBuf<int32_t> nx, pv;
+  size_t docs_cap = 0;
+  // timing
+  bool timing = false;
+  hipEvent_t ev[6] = {};
+  double last_us[5] = {};
+};
+
+namespace {
+
+int validate(const tk_config* cfg, size_t class_len, size_t pk_len,
+             size_t pv_len, size_t byte_id_len, size_t vk_len, size_t vv_len,
+             size_t unsafe_len) {
+  if (!cfg) return fail(TK_E_INVALID_ARG, "config is null");
+  if (cfg->abi_version != TK_ABI_VERSION)
+    return fail(TK_E_INVALID_ARG, "abi_version %u != %u", cfg->abi_version,
+                TK_ABI_VERSION);
+  if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K)
+    return fail(TK_E_INVALID_ARG, "unsupported ruleset %d", cfg->ruleset);
+  if (cfg->ruleset == TK_RULESET_CL100K &&
+      (cfg->digits_max < 1 || cfg->digits_max > 64))
+    return fail(TK_E_INVALID_ARG, "digits_max %d out of range", cfg->digits_max);
+  if (!cfg->contractions)
+    return fail(TK_E_INVALID_ARG, "rulesets without contractions are not supported");
+  // shape rules of the reference executor (gpu.rs:1642-1679)
+  if (class_len < PLANE)
+    return fail(TK_E_SHAPE, "class table does not cover U+10FFFF");
+  if (!pow2(cfg->pair_count) || pk_len != 8 * cfg->pair_count || pv_len != pk_len)
+    return fail(TK_E_SHAPE, "pair tables have an invalid shape");
+  if (!pow2(cfg->vocab_count) || vk_len != 8 * cfg->vocab_count || vv_len != vk_len)
+    return fail(TK_E_SHAPE, "vocabulary tables have an invalid shape");
+  if (byte_id_len != 256 * 4 || unsafe_len % 4 != 0)
+    return fail(TK_E_SHAPE, "byte-id or unsafe-rank table has an invalid shape");
+  return TK_OK;
+}
+
+int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
+  size_t need = 1u << 16;
+  while (need < nb) need <<= 1;
+  if (need > (size_t)1 << 30) return fail(TK_E_CAPACITY, "input of %zu bytes exceeds 1 GiB", nb);
+  if (need > e->cap) {
+    const size_t words = need / 64 + 8;
+    const size_t nblk = need / tk::COMPACT_BLOCK + 2;
+    const size_t long_cap = need / 32 + 64;
+    HIP_TRY(e->text.alloc(need + 64));
+    HIP_TRY(e->starts.alloc(words));
+    HIP_TRY(e->docmask.alloc(words));
+    HIP_TRY(e->tok.alloc(need + 64));
+    HIP_TRY(e->nx.alloc(need));
+    HIP_TRY(e->pv.alloc(need));
+    HIP_TRY(e->heap.alloc(3 * need));
+    HIP_TRY(e->longlist.alloc(2 * long_cap));
+    HIP_TRY(e->ctrl.alloc(16));
+    HIP_TRY(e->blkcount.alloc(nblk));
+    HIP_TRY(e->blkprefix.alloc(nblk));
+    HIP_TRY(e->out.alloc(need));
+    e->cap = need;
+  }
+  if (n_docs + 1 > e->docs_cap) {
+    HIP_TRY(e->docoffs.alloc(n_docs + 1));
+    HIP_TRY(e->rows.alloc(n_docs + 1));
+    e->docs_cap = n_docs + 1;
+  }
+  return TK_OK;
+}
+
+// Runs every stage for nb bytes already at d_text. Leaves ids in e->out and
+// [status, total] in e->ctrl.
+int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
+                 const uint64_t* d_docmask, bool check_nfc, hipStream_t s) {
+  tk::DevWork w{};
+  w.text = d_text;
+  w.nb = (int64_t)nb;
+  w.docmask = d_docmask;
+  w.check_nfc = check_nfc ? 1 : 0;
+  w.starts = e->starts.p;
+  w.tok = e->tok.p;
+  w.nx = e->nx.p;
+  w.pv = e->pv.p;
+  w.heap = e->heap.p;
+  w.longlist = e->longlist.p;
+  w.longcount = e->ctrl.p + 2;
+  w.long_cap = (uint32_t)(e->longlist.n / 2);
+  w.status = e->ctrl.p;
+  w.blkcount = e->blkcount.p;
+  w.blkprefix = e->blkprefix.p;
+  w.out = e->out.p;
+  HIP_TRY(hipMemsetAsync(e->ctrl.p, 0, 16 * sizeof(uint32_t), s));
+  if (e->timing) HIP_TRY(hipEventRecord(e->ev[0], s));
+  HIP_TRY(tk::launch_pretok(e->t, w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(e->ev[1], s));
+  HIP_TRY(tk::launch_bpe_small(e->t, w, 0, s));
+  HIP_TRY(tk::launch_bpe_small(e->t, w, 1, s));
+  if (e->timing) HIP_TRY(hipEventRecord(e->ev[2], s));
+  HIP_TRY(tk::launch_bpe_long(e->t, w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(e->ev[3], s));
+  HIP_TRY(tk::launch_compact(w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(e->ev[4], s));
+  return TK_OK;
+}
+
+int read_ctrl(tk_engine* e, hipStream_t s, uint32_t* status, uint32_t* total) {
+  uint32_t h[4];
+  HIP_TRY(hipMemcpyAsync(h, e->ctrl.p, sizeof h, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (e->timing) {
+    float ms;
+    for (int k = 0; k < 4; ++k) {
+      HIP_TRY(hipEventElapsedTime(&ms, e->ev[k], e->ev[k + 1]));
+      e->last_us[k] = ms * 1e3;
+    }
+    HIP_TRY(hipEventElapsedTime(&ms, e->ev[0], e->ev[4]));
+    e->last_us[4] = ms * 1e3;
+  }
+  *status = h[0];
+  *total = h[1];
+  if (h[0] & tk::ST_LONGOVF)
+    return fail(TK_E_INTERNAL, "long-piece queue overflow");
+  return TK_OK;
+}
+
+// host-side checks used only on a batch whose device status flagged a
+// failure, to find the failing rows
+bool host_utf8_ok(const uint8_t* s, size_t n) {
+  size_t i = 0;
+  while (i < n) {
+    uint32_t b0 = s[i], v;
+    int need;
+    if (b0 < 0x80) { ++i; continue; }
+    if (b0 < 0xC0) return false;
+    if (b0 < 0xE0) { need = 1; v = b0 & 0x1F; }
+    else if (b0 < 0xF0) { need = 2; v = b0 & 0x0F; }
+    else if (b0 < 0xF8) { need = 3; v = b0 & 7; }
+    else return false;
+    for (int k = 1; k <= need; ++k) {
+      if (i + k >= n || (s[i + k] & 0xC0) != 0x80) return false;
+      v = (v << 6) | (s[i + k] & 0x3F);
+    }
+    if ((need == 1 && v < 0x80) || (need == 2 && v < 0x800) ||
+        (need == 3 && v < 0x10000) || v > 0x10FFFF || (v >= 0xD800 && v <= 0xDFFF))
+      return false;
+    i += need + 1;
+  }
+  return true;
+}
+
+bool host_nfc_ok(const std::vector<uint8_t>& qc, const uint8_t* s, size_t n) {
+  size_t i = 0;
+  uint8_t prev = 0;
+  bool first = true;
+  while (i < n) {
+    uint32_t b0 = s[i], v;
+    int need = b0 < 0x80 ? 0 : b0 < 0xE0 ? 1 : b0 < 0xF0 ? 2 : 3;
+    v = need == 0 ? b0 : need == 1 ? (b0 & 0x1F) : need == 2 ? (b0 & 0x0F) : (b0 & 7);
+    for (int k = 1; k <= need && i + k < n; ++k) v = (v << 6) | (s[i + k] & 0x3F);
+    if (v >= PLANE) return false;
+    const uint8_t q = qc[v];
+    if (q == 255 || (!first && q != 0 && prev > q)) return false;
+    prev = q;
+    first = false;
+    i += need + 1;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tk_last_error(void) { return g_err.c_str(); }
+
+int tk_engine_preflight(const tk_config* cfg, const uint8_t* class_table,
+                        size_t class_len, const uint64_t* pair_keys,
+                        size_t pair_keys_len, const uint64_t* pair_vals,
+                        size_t pair_vals_len, const int32_t* byte_id,
+                        size_t byte_id_len, const uint64_t* vocab_keys,
+                        size_t vocab_keys_len, const uint64_t* vocab_vals,
+                        size_t vocab_vals_len, const uint32_t* unsafe_bits,
+                        size_t unsafe_len) {
+  if (!class_table || !pair_keys || !pair_vals || !byte_id || !vocab_keys ||
+      !vocab_vals)
+    return fail(TK_E_INVALID_ARG, "a table pointer is null");
+  (void)unsafe_bits;
+  return validate(cfg, class_len, pair_keys_len, pair_vals_len, byte_id_len,
+                  vocab_keys_len, vocab_vals_len, unsafe_len);
+}
+
+int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
+                   size_t class_len, const uint64_t* pair_keys,
+                   size_t pair_keys_len, const uint64_t* pair_vals,
+                   size_t pair_vals_len, const int32_t* byte_id,
+                   size_t byte_id_len, const uint64_t* vocab_keys,
+                   size_t vocab_keys_len, const uint64_t* vocab_vals,
+                   size_t vocab_vals_len, const uint8_t* vocab_blob,
+                   size_t vocab_blob_len, const uint32_t* unsafe_bits,
+                   size_t unsafe_len, const uint8_t* nfc_qc,
+                   size_t nfc_qc_len, tk_engine** out) {
+  if (!out) return fail(TK_E_INVALID_ARG, "out is null");
+  *out = nullptr;
+  int rc = tk_engine_preflight(cfg, class_table, class_len, pair_keys,
+                               pair_keys_len, pair_vals, pair_vals_len, byte_id,
+                               byte_id_len, vocab_keys, vocab_keys_len,
+                               vocab_vals, vocab_vals_len, unsafe_bits,
+                               unsafe_len);
+  if (rc != TK_OK) return rc;
+  if (cfg->needs_nfc && (!nfc_qc || nfc_qc_len < PLANE))
+    return fail(TK_E_SHAPE, "needs_nfc requires the NFC quick-check table");
+  if (cfg->ignore_merges && !vocab_blob && vocab_blob_len)
+    return fail(TK_E_INVALID_ARG, "vocabulary blob is null");
+  const uint64_t n_pairs = cfg->pair_count;
+  // ranks are packed rank<<6|lane in 32 bits on the device
+  for (uint64_t i = 0; i < n_pairs; ++i)
+    if (pair_keys[i] != ~0ULL && (pair_vals[i] >> 32) >= tk::MAX_MERGES)
+      return fail(TK_E_SHAPE, "merge rank exceeds 2^25");
+
+  int ndev = 0;
+  HIP_TRY(hipGetDeviceCount(&ndev));
+  if (cfg->device_ordinal < 0 || cfg->device_ordinal >= ndev)
+    return fail(TK_E_DEVICE, "device ordinal %d not present (%d devices)",
+                cfg->device_ordinal, ndev);
+  HIP_TRY(hipSetDevice(cfg->device_ordinal));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, cfg->device_ordinal));
+  std::string arch = prop.gcnArchName;
+  const size_t colon = arch.find(':');
+  if (colon != std::string::npos) arch = arch.substr(0, colon);
+  if (cfg->expected_architecture && *cfg->expected_architecture &&
+      arch != cfg->expected_architecture)
+    return fail(TK_E_ARCH, "device architecture %s != expected %s",
+                arch.c_str(), cfg->expected_architecture);
+
+  tk_engine* e = new tk_engine();
+  e->device = cfg->device_ordinal;
+  e->cfg = *cfg;
+  e->family = cfg->family ? cfg->family : "";
+  e->sha = cfg->artifact_sha256 ? cfg->artifact_sha256 : "";
+  e->cfg.family = e->family.c_str();
+  e->cfg.artifact_sha256 = e->sha.c_str();
+  e->cfg.expected_architecture = nullptr;
+  e->arch = arch;
+  auto bail = [&](int code) {
+    tk_engine_close(e);
+    return code;
+  };
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
+  for (auto& ev : e->ev)
+    if (hipEventCreate(&ev) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipEventCreate failed"));
+
+  // interleave key/value so one 16-byte load reads a whole slot
+  std::vector<ulonglong2> pairs(n_pairs);
+  for (uint64_t i = 0; i < n_pairs; ++i) pairs[i] = {pair_keys[i], pair_vals[i]};
+  std::vector<ulonglong2> vocab(cfg->vocab_count);
+  for (uint64_t i = 0; i < cfg->vocab_count; ++i) vocab[i] = {vocab_keys[i], vocab_vals[i]};
+  // direct table for the first merge level: both symbols still raw bytes
+  std::vector<uint64_t> bp(65536, ~0ULL);
+  for (int a = 0; a < 256; ++a)
+    for (int b = 0; b < 256; ++b)
+      if (byte_id[a] >= 0 && byte_id[b] >= 0)
+        bp[(a << 8) | b] = host_pair_lookup(pair_keys, pair_vals, n_pairs,
+                                            (uint32_t)byte_id[a], (uint32_t)byte_id[b]);
+
+  auto up = [&](auto& buf, const void* src, size_t count) -> int {
+    if (buf.alloc(count) != hipSuccess)
+      return fail(TK_E_DEVICE, "hipMalloc of a %zu-entry table failed", count);
+    if (count && hipMemcpy(buf.p, src, count * sizeof(*buf.p), hipMemcpyHostToDevice) != hipSuccess)
+      return fail(TK_E_DEVICE, "table upload failed");
+    return TK_OK;
+  };
+  if ((rc = up(e->cls, class_table, PLANE)) != TK_OK) return bail(rc);
+  if ((rc = up(e->pairs, pairs.data(), pairs.size())) != TK_OK) return bail(rc);
+  if ((rc = up(e->vocab, vocab.data(), vocab.size())) != TK_OK) return bail(rc);
+  if ((rc = up(e->bytepair, bp.data(), bp.size())) != TK_OK) return bail(rc);
+  if ((rc = up(e->byte_id, byte_id, 256)) != TK_OK) return bail(rc);
+  const uint8_t zero = 0;
+  if ((rc = up(e->blob, vocab_blob_len ? vocab_blob : &zero,
+               vocab_blob_len ? vocab_blob_len : 1)) != TK_OK)
+    return bail(rc);
+  if (cfg->needs_nfc) {
+    if ((rc = up(e->nfc, nfc_qc, PLANE)) != TK_OK) return bail(rc);
+    e->host_nfc.assign(nfc_qc, nfc_qc + PLANE);
+  }
+  e->t.cls = e->cls.p;
+  e->t.nfc = cfg->needs_nfc ? e->nfc.p : nullptr;
+  e->t.pairs = e->pairs.p;
+  e->t.pair_mask = n_pairs - 1;
+  e->t.bytepair = e->bytepair.p;
+  e->t.byte_id = e->byte_id.p;
+  e->t.vocab = e->vocab.p;
+  e->t.vocab_mask = cfg->vocab_count - 1;
+  e->t.blob = e->blob.p;
+  e->t.ruleset = cfg->ruleset;
+  e->t.dmax = cfg->ruleset == TK_RULESET_CL100K ? cfg->digits_max : 0;
+  e->t.ignore_merges = cfg->ignore_merges ? 1 : 0;
+  e->t.needs_nfc = cfg->needs_nfc ? 1 : 0;
+  if (hipDeviceSynchronize() != hipSuccess)
+    return bail(fail(TK_E_DEVICE, "device synchronize after upload failed"));
+  *out = e;
+  return TK_OK;
+}
+
+void tk_engine_close(tk_engine* e) {
+  if (!e) return;
+  (void)hipSetDevice(e->device);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  for (auto& ev : e->ev)
+    if (ev) (void)hipEventDestroy(ev);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+int tk_engine_set_timing(tk_engine* e, int enabled) {
+  if (!e) return fail(TK_E_INVALID_ARG, "engine is null");
+  std::lock_guard<std::mutex> lk(e->mu);
+  e->timing = enabled != 0;
+  return TK_OK;
+}
+
+int tk_engine_last_timing(const tk_engine* e, double* us, int n) {
+  if (!e || !us) return fail(TK_E_INVALID_ARG, "null argument");
+  int k = 0;
+  for (; k < n && k < 5; ++k) us[k] = e->last_us[k];
+  return k;
+}
+
+const char* tk_engine_delivery(const tk_engine* e) { return e ? "prebuilt" : ""; }
+const char* tk_engine_architecture(const tk_engine* e) { return e ? e->arch.c_str() : ""; }
+
+int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
+                            uint32_t flags, void* d_ids, size_t ids_cap,
+                            size_t* n_ids, void* stream) {
+  if (!e || !n_ids || (nbytes && (!d_text || !d_ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  *n_ids = 0;
+  if (nbytes == 0) return TK_OK;
+  HIP_TRY(hipSetDevice(e->device));
+  int rc = ensure_workspace(e, nbytes, 0);
+  if (rc != TK_OK) return rc;
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
+  const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
+  rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr, check, s);
+  if (rc != TK_OK) return rc;
+  uint32_t st, total;
+  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
+  if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
+  if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  HIP_TRY(hipMemcpyAsync(d_ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToDevice, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  *n_ids = total;
+  return TK_OK;
+}
+
+int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
+                     uint32_t flags, uint32_t* ids, size_t ids_cap,
+                     size_t* n_ids) {
+  if (!e || !n_ids || (nbytes && (!text || !ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  *n_ids = 0;
+  if (nbytes == 0) return TK_OK;
+  HIP_TRY(hipSetDevice(e->device));
+  int rc = ensure_workspace(e, nbytes, 0);
+  if (rc != TK_OK) return rc;
+  hipStream_t s = e->stream;
+  HIP_TRY(hipMemcpyAsync(e->text.p, text, nbytes, hipMemcpyHostToDevice, s));
+  const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
+  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s);
+  if (rc != TK_OK) return rc;
+  uint32_t st, total;
+  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
+  if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
+  if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  HIP_TRY(hipMemcpyAsync(ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  *n_ids = total;
+  return TK_OK;
+}
+
+int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
+                           const uint64_t* doc_offsets, size_t n_docs,
+                           uint32_t flags, uint32_t* ids, size_t ids_cap,
+                           uint64_t* row_offsets, int32_t* row_status) {
+  if (!e || !doc_offsets || !row_offsets || !row_status)
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  const size_t nb = n_docs ? doc_offsets[n_docs] : 0;
+  for (size_t d = 0; d < n_docs; ++d) {
+    if (doc_offsets[d] > doc_offsets[d + 1])
+      return fail(TK_E_INVALID_ARG, "doc_offsets must be non-decreasing");
+    row_status[d] = TK_OK;
+  }
+  if (doc_offsets[0] != 0) return fail(TK_E_INVALID_ARG, "doc_offsets[0] must be 0");
+  for (size_t d = 0; d <= n_docs; ++d) row_offsets[d] = 0;
+  if (nb == 0) return TK_OK;
+  if (!joined || !ids) return fail(TK_E_INVALID_ARG, "null argument");
+  HIP_TRY(hipSetDevice(e->device));
+  int rc = ensure_workspace(e, nb, n_docs);
+  if (rc != TK_OK) return rc;
+  hipStream_t s = e->stream;
+  // forced piece starts at every document head (gpu.rs:644-652)
+  std::vector<uint64_t> mask(nb / 64 + 2, 0);
+  for (size_t d = 0; d < n_docs; ++d) {
+    const uint64_t p = doc_offsets[d];
+    if (p < nb) mask[p >> 6] |= 1ULL << (p & 63);
+  }
+  HIP_TRY(hipMemcpyAsync(e->text.p, joined, nb, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(e->docmask.p, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
+  const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
+  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s);
+  if (rc != TK_OK) return rc;
+  tk::DevWork w{};
+  w.nb = (int64_t)nb;
+  w.tok = e->tok.p;
+  w.blkprefix = e->blkprefix.p;
+  HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
+  uint32_t st, total;
+  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
+    // find the rows that failed; their ids are dropped, the others stand
+    std::vector<uint32_t> keep;
+    keep.reserve(total);
+    std::vector<uint64_t> rows(row_offsets, row_offsets + n_docs + 1);
+    uint64_t acc = 0;
+    for (size_t d = 0; d < n_docs; ++d) {
+      const uint8_t* doc = joined + doc_offsets[d];
+      const size_t len = doc_offsets[d + 1] - doc_offsets[d];
+      int rs = TK_OK;
+      if ((st & tk::ST_UTF8) && !host_utf8_ok(doc, len)) rs = TK_E_UTF8;
+      else if ((st & tk::ST_NFC) && check && !host_nfc_ok(e->host_nfc, doc, len))
+        rs = TK_E_NEEDS_NFC;
+      row_status[d] = rs;
+      row_offsets[d] = acc;
+      if (rs == TK_OK)
+        for (uint64_t k = rows[d]; k < rows[d + 1]; ++k) keep.push_back(ids[k]);
+      acc = keep.size();
+    }
+    row_offsets[n_docs] = acc;
+    std::memcpy(ids, keep.data(), keep.size() * 4);
+  }
+  return TK_OK;
+}
+
+}  // extern "C"
