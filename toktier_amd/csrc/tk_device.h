@@ -61,7 +61,9 @@ constexpr int COMPACT_PER_THREAD = 16;
 constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
 
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s);
-hipError_t launch_bpe_small(const DevTables& t, const DevWork& w, int phase,
+hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
+                            hipStream_t s);
+hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
                             hipStream_t s);
 hipError_t launch_bpe_long(const DevTables& t, const DevWork& w,
                            hipStream_t s);

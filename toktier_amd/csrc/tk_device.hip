@@ -352,63 +352,25 @@ __device__ __forceinline__ uint64_t mask_le(int lane) {
   return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
 }
 
-__global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
-                                                   int phase, int64_t nwin) {
-  const int lane = threadIdx.x & 63;
-  const int64_t win = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (win >= nwin) return;  // whole wave
-  const int64_t base = phase == 0 ? win * 64 : win * 64 - 32;
-  uint64_t S;
-  bool E;
-  if (phase == 0) {
-    S = w.starts[win];
-    E = w.starts[win + 1] & 1;
-  } else {
-    const uint64_t lo = win > 0 ? w.starts[win - 1] : ~0ULL;
-    S = (lo >> 32) | (w.starts[win] << 32);
-    E = (w.starts[win] >> 32) & 1;
-  }
+// Byte-level BPE of every eligible piece held by one wave, lane = byte at
+// base + lane. ps/pe: the lane's piece as lanes [ps, pe) of this wave.
+// Each round every piece merges its lowest-ranked pair (leftmost on equal
+// rank: key = rank<<6 | lane) -- the HF order -- until no pair has a rule.
+// Token ids land at the byte where each token starts; the piece's other
+// bytes get INVALID_ID.
+__device__ void wave_bpe(const DevTables& t, const DevWork& w, int64_t base,
+                         int lane, bool elig, int ps, int pe) {
   const int64_t pos = base + lane;
-  const bool valid = pos >= 0 && pos < w.nb;
-  const uint64_t le = S & mask_le(lane);
-  const int ps = le ? 63 - __builtin_clzll(le) : -1;
-  const uint64_t gt = S & ~mask_le(lane);
-  const int pe = gt ? __builtin_ctzll(gt) : 64;
-  const bool contained = ps >= 0 && (pe < 64 || E);
-  bool elig = valid && contained;
-  if (phase == 1 && elig) {
-    const int64_t a = base + ps, b = base + pe;
-    if ((a >> 6) == ((b - 1) >> 6)) elig = false;  // aligned grid has it
-  }
-  if (phase == 0 && valid && ps == lane && !contained) {
-    // this piece runs past the window: find its end, queue it if neither
-    // grid holds it whole
-    // (bit 0 of the next word is clear here: E is false; the sentinel
-    // bits at and after nb end the search inside the nwin+2 words)
-    int64_t wd = win + 1;
-    uint64_t word = w.starts[wd];
-    while (word == 0) word = w.starts[++wd];
-    const int64_t b = wd * 64 + __builtin_ctzll(word);
-    const int64_t a = pos;
-    if (b - a > 64 || ((a + 32) >> 6) != ((b - 1 + 32) >> 6)) {
-      const uint32_t k = atomicAdd(w.longcount, 1u);
-      if (k < w.long_cap) {
-        w.longlist[2 * k] = (uint32_t)a;
-        w.longlist[2 * k + 1] = (uint32_t)b;
-      } else {
-        atomicOr(w.status, ST_LONGOVF);
-      }
-    }
-  }
-
-  const uint32_t byte = valid ? w.text[pos] : 0u;
+  const uint32_t byte = elig ? w.text[pos] : 0u;
   const int32_t bid = elig ? t.byte_id[byte] : -1;
   uint64_t live = __ballot(bid >= 0);
   uint32_t sym = (uint32_t)bid;
   int isb = 1;
   const int src_ps = ps >= 0 ? ps : lane;
+  if (!__any(elig)) return;
 
   if (t.ignore_merges) {
+    // whole-piece vocabulary hit first (pretok_kernel.cu:921-943 role)
     const bool lead = elig && lane == ps;
     int32_t hit = -1;
     if (lead) hit = vocab_lookup(t, w.text + pos, pe - ps);
@@ -462,12 +424,90 @@ __global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
   if (elig) w.tok[pos] = ((live >> lane) & 1) ? sym : INVALID_ID;
 }
 
-hipError_t launch_bpe_small(const DevTables& t, const DevWork& w, int phase,
+// One wave per 64-byte window. First the aligned window [64v, 64v+64):
+// every piece inside it; then the shifted window [64v-32, 64v+32): the
+// pieces that straddle an aligned boundary but fit it. A piece of <= 32
+// bytes always fits one of the two. Anything else is queued.
+__global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
+                                                   int64_t nwin) {
+  const int lane = threadIdx.x & 63;
+  const int64_t win = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (win > nwin) return;  // whole wave; win == nwin: last shifted window
+  for (int phase = (win == nwin ? 1 : 0); phase < 2; ++phase) {
+    const int64_t base = phase == 0 ? win * 64 : win * 64 - 32;
+    uint64_t S;
+    bool E;
+    if (phase == 0) {
+      S = w.starts[win];
+      E = w.starts[win + 1] & 1;
+    } else {
+      const uint64_t lo = win > 0 ? w.starts[win - 1] : ~0ULL;
+      S = (lo >> 32) | (w.starts[win] << 32);
+      E = (w.starts[win] >> 32) & 1;
+    }
+    const int64_t pos = base + lane;
+    const bool valid = pos >= 0 && pos < w.nb;
+    const uint64_t le = S & mask_le(lane);
+    const int ps = le ? 63 - __builtin_clzll(le) : -1;
+    const uint64_t gt = S & ~mask_le(lane);
+    const int pe = gt ? __builtin_ctzll(gt) : 64;
+    const bool contained = ps >= 0 && (pe < 64 || E);
+    bool elig = valid && contained;
+    if (phase == 1 && elig) {
+      const int64_t a = base + ps, b = base + pe;
+      if ((a >> 6) == ((b - 1) >> 6)) elig = false;  // aligned grid had it
+    }
+    if (phase == 0 && valid && ps == lane && !contained) {
+      // the piece runs past the window: find its end (bit 0 of the next
+      // word is clear since E is false; the sentinel bits at and after nb
+      // end the search inside the nwin+2 words) and queue it if neither
+      // grid holds it whole
+      int64_t wd = win + 1;
+      uint64_t word = w.starts[wd];
+      while (word == 0) word = w.starts[++wd];
+      const int64_t b = wd * 64 + __builtin_ctzll(word);
+      const int64_t a = pos;
+      if (b - a > 64 || ((a + 32) >> 6) != ((b - 1 + 32) >> 6)) {
+        const uint32_t k = atomicAdd(w.longcount, 1u);
+        if (k < w.long_cap) {
+          w.longlist[2 * k] = (uint32_t)a;
+          w.longlist[2 * k + 1] = (uint32_t)b;
+        } else {
+          atomicOr(w.status, ST_LONGOVF);
+        }
+      }
+    }
+    wave_bpe(t, w, base, lane, elig, ps, pe);
+  }
+}
+
+hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
                             hipStream_t s) {
-  const int64_t nwin = (w.nb + 63) / 64 + (phase == 1 ? 1 : 0);
-  const int64_t blocks = (nwin + 3) / 4;
+  const int64_t nwin = (w.nb + 63) / 64;
+  const int64_t blocks = (nwin + 1 + 3) / 4;
   hipLaunchKernelGGL(k_bpe_small, dim3((uint32_t)blocks), dim3(256), 0, s, t,
-                     w, phase, nwin);
+                     w, nwin);
+  return hipGetLastError();
+}
+
+// Queued pieces of at most 64 bytes (those that straddle both grids): one
+// wave per piece, lane = byte offset.
+__global__ __launch_bounds__(256) void k_bpe_queue(DevTables t, DevWork w) {
+  const int lane = threadIdx.x & 63;
+  uint32_t n = *w.longcount;
+  if (n > w.long_cap) n = w.long_cap;
+  const uint32_t waves = gridDim.x * 4;
+  for (uint32_t k = blockIdx.x * 4 + (threadIdx.x >> 6); k < n; k += waves) {
+    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    const int len = (int)(b - a);
+    if (len > 64) continue;  // wave-uniform
+    wave_bpe(t, w, (int64_t)a, lane, lane < len, 0, len);
+  }
+}
+
+hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_bpe_queue, dim3(512), dim3(256), 0, s, t, w);
   return hipGetLastError();
 }
 
@@ -557,8 +597,10 @@ __global__ __launch_bounds__(64) void k_bpe_long(DevTables t, DevWork w) {
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride)
-    bpe_serial(t, w, w.longlist[2 * k], w.longlist[2 * k + 1]);
+  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
+    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    if (b - a > 64) bpe_serial(t, w, a, b);
+  }
 }
 
 hipError_t launch_bpe_long(const DevTables& t, const DevWork& w,

@@ -199,9 +199,9 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   if (e->timing) HIP_TRY(hipEventRecord(e->ev[0], s));
   HIP_TRY(tk::launch_pretok(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(e->ev[1], s));
-  HIP_TRY(tk::launch_bpe_small(e->t, w, 0, s));
-  HIP_TRY(tk::launch_bpe_small(e->t, w, 1, s));
+  HIP_TRY(tk::launch_bpe_small(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(e->ev[2], s));
+  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
   HIP_TRY(tk::launch_bpe_long(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(e->ev[3], s));
   HIP_TRY(tk::launch_compact(w, s));
