@@ -80,3 +80,42 @@ def test_batch_rows_equal_single():
     rows = t.encode_batch(docs)
     for d, r in zip(docs, rows):
         assert list(r.array) == k.hf_ids(d)
+
+
+def _long_texts(name):
+    from toktier_amd import workloads
+    k = kit(name)
+    rng = np.random.default_rng(11)
+    base = workloads.config2(k.json, n_chars=40_000)
+    letters = "".join(ch for ch in base if ch.isalpha())
+    texts = [
+        "a" * 300, "ab" * 200, "=" * 500, "-" * 129 + "x", " " * 200 + "x",
+        "\n" * 150, "\r\n" * 100 + " y", "1" * 300, "中" * 100, "é" * 90,
+        "\U0001f600" * 70, " " + "q" * 65, "'s" + "t" * 80,
+        letters[:5000], letters[5000:5130], " " + letters[6000:9000],
+    ]
+    for _ in range(30):
+        n = int(rng.integers(65, 1500))
+        a = int(rng.integers(0, len(letters) - n))
+        texts.append(letters[a:a + n])
+    return texts
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_long_pieces(name):
+    k, t = kit(name), tok(name)
+    for s in _long_texts(name):
+        got = list(t.encode(s).array)
+        assert got == k.hf_ids(s), (name, s[:80], len(s))
+
+
+def test_cjk_and_pathological_runs():
+    from toktier_amd import workloads
+    name = "qwen3_8b"
+    k, t = kit(name), tok(name)
+    text = workloads.config5(k.json, n_chars=400_000, n_runs=4, run_chars=30_000)
+    data = text.encode()
+    got = t.encode(text).array
+    want = k.oracle.encode_bytes(data)
+    assert not isinstance(want, int)
+    assert np.array_equal(got, want)

@@ -31,6 +31,8 @@ struct DevTables {
   int32_t dmax;                // digit group width (cl100k)
   int32_t ignore_merges;
   int32_t needs_nfc;
+  int32_t cert;                // long pieces may be cut and certified:
+                               // rank-ordered table, every byte has an id
 };
 
 // Per-request device buffers (sized by capacity).
@@ -48,11 +50,26 @@ struct DevWork {
   uint32_t* longlist;    // (start, end) pairs
   uint32_t* longcount;   // [1]
   uint32_t long_cap;     // capacity of longlist in pairs
-  uint32_t* status;      // [1]
+  uint32_t* status;      // ctrl[0]; ctrl[1] = total ids
   uint32_t* blkcount;    // per compaction block
   uint32_t* blkprefix;   // exclusive prefix, [nblk + 1]
   uint32_t* out;         // compacted ids
+  // long-piece segmentation (one bit / slot per byte)
+  uint64_t* inlong;      // bytes of pieces over 64 bytes
+  uint64_t* cuts;        // candidate segment starts inside long pieces
+  uint64_t* failm;       // cuts whose certificate failed this pass
+  uint64_t* hfirst;      // first-token merge events, at the segment start
+  uint64_t* hlast;       // last-token merge events, at the segment start
+  uint32_t* hmeta;       // event counts (first | last << 16)
+  uint32_t* seglist;     // segments that fit no grid window
+  uint32_t* segcount;    // ctrl[3]
+  uint32_t seg_cap;
+  uint32_t* nfail;       // ctrl[4]
 };
+
+// ctrl word layout (device -> host)
+constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
+              CTRL_FAIL = 4, CTRL_WORDS = 16;
 
 constexpr int PRETOK_BYTES_PER_THREAD = 16;
 constexpr int PRETOK_TPB = 256;
@@ -65,8 +82,15 @@ hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
                             hipStream_t s);
 hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
                             hipStream_t s);
-hipError_t launch_bpe_long(const DevTables& t, const DevWork& w,
-                           hipStream_t s);
+hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
+                            hipStream_t s);
+hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
+                               hipStream_t s);
+hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
+                                hipStream_t s);
+hipError_t launch_certify(const DevTables& t, const DevWork& w,
+                          hipStream_t s);
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
 hipError_t launch_compact(const DevWork& w, hipStream_t s);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,

@@ -5,14 +5,18 @@
 //                     check, and the family split rules as a per-character
 //                     piece-start predicate -> one start bit per byte.
 //   2. k_bpe_small    one wave64 per 64-byte window, lane = byte: every piece
-//                     that lies inside the window is merged in place (lowest
+//                     inside the aligned window, then every piece inside the
+//                     window shifted by 32 bytes, is merged in place (lowest
 //                     rank pair, leftmost first) with segmented wave
-//                     reductions; run twice, on the aligned grid and on the
-//                     grid shifted by 32 bytes, so every piece of <= 32
-//                     bytes is handled here. Pieces that fit neither grid
-//                     are queued for stage 3.
-//   3. k_bpe_long     one thread per queued piece: heap-ordered exact merge
-//                     over global scratch.
+//                     reductions. Any piece of <= 32 bytes fits one of the
+//                     two; the others are queued.
+//      k_bpe_list     queued pieces of <= 64 bytes, one wave each.
+//   3. long pieces    (> 64 bytes) are cut into short segments at likely
+//                     token boundaries (k_long_windows), merged segment by
+//                     segment with boundary-token histories
+//                     (k_long_segments), and every cut is certified
+//                     (k_certify); failed cuts are removed and the affected
+//                     segments redone until every cut holds.
 //   4. k_count / k_scan / k_compact: device-wide compaction of the per-byte
 //                     token slots into the contiguous id buffer.
 // Token j of a piece is stored at the byte where that token starts, so the
@@ -352,24 +356,37 @@ __device__ __forceinline__ uint64_t mask_le(int lane) {
   return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
 }
 
-// Byte-level BPE of every eligible piece held by one wave, lane = byte at
-// base + lane. ps/pe: the lane's piece as lanes [ps, pe) of this wave.
-// Each round every piece merges its lowest-ranked pair (leftmost on equal
-// rank: key = rank<<6 | lane) -- the HF order -- until no pair has a rule.
-// Token ids land at the byte where each token starts; the piece's other
-// bytes get INVALID_ID.
-__device__ void wave_bpe(const DevTables& t, const DevWork& w, int64_t base,
-                         int lane, bool elig, int ps, int pe) {
+__device__ __forceinline__ uint64_t lanes_in(int lo, int hi) {  // [lo, hi)
+  const uint64_t up = hi >= 64 ? ~0ULL : ((1ULL << hi) - 1);
+  return up & ~((1ULL << lo) - 1);
+}
+
+// Byte-level BPE of every eligible segment held by one wave, lane = byte
+// at base + lane; ps/pe: the lane's segment as lanes [ps, pe). Each round
+// every segment merges its lowest-ranked pair (leftmost on equal rank:
+// key = rank<<6 | lane) -- the HF order -- until no pair has a rule.
+//   vocab_first: a whole piece that is a vocabulary entry is that one
+//     token (ignore_merges families; pieces only, never sub-segments).
+//   hist: record the merge events that change the segment's first token
+//     (hfirst[seg_start + k]) and its last token (hlast[seg_start + k]) as
+//     rank<<32|new_id, with the counts in hmeta[seg_start].
+//   write: store the ids (token id at its first byte, INVALID_ID at the
+//     other bytes of the segment) into tok.
+// Returns the final mask of lanes that start a token.
+__device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
+                             int64_t base, int lane, bool elig, int ps,
+                             int pe, bool vocab_first, bool hist,
+                             bool write) {
   const int64_t pos = base + lane;
   const uint32_t byte = elig ? w.text[pos] : 0u;
   const int32_t bid = elig ? t.byte_id[byte] : -1;
   uint64_t live = __ballot(bid >= 0);
+  if (!__any(elig)) return 0;
   uint32_t sym = (uint32_t)bid;
   int isb = 1;
   const int src_ps = ps >= 0 ? ps : lane;
-  if (!__any(elig)) return;
 
-  if (t.ignore_merges) {
+  if (vocab_first && t.ignore_merges) {
     // whole-piece vocabulary hit first (pretok_kernel.cu:921-943 role)
     const bool lead = elig && lane == ps;
     int32_t hit = -1;
@@ -382,6 +399,7 @@ __device__ void wave_bpe(const DevTables& t, const DevWork& w, int64_t base,
   }
 
   uint32_t rk = RANK_INF, mid = 0;
+  uint32_t nfirst = 0, nlast = 0;  // event counts, kept by lane ps
   bool dirty = true;
   for (;;) {
     const bool me = (live >> lane) & 1;
@@ -411,6 +429,23 @@ __device__ void wave_bpe(const DevTables& t, const DevWork& w, int64_t base,
     const bool act = elig && pm != RANK_INF;
     if (!__any(act)) break;
     const bool win_ = act && key == pm;
+    if (hist) {
+      const uint32_t nf = __shfl(nfirst, src_ps);
+      const uint32_t nl = __shfl(nlast, src_ps);
+      bool lastev = false;
+      if (win_) {
+        // the merged pair's right symbol is the segment's last symbol
+        lastev = nx + 1 >= pe || ((live & lanes_in(nx + 1, pe)) == 0);
+        const uint64_t ev = ((uint64_t)rk << 32) | mid;
+        if (lane == ps) w.hfirst[base + ps + nf] = ev;
+        if (lastev) w.hlast[base + ps + nl] = ev;
+      }
+      const uint64_t lm = __ballot(lastev);
+      if (elig && lane == ps) {
+        if (win_) ++nfirst;
+        if (lm & lanes_in(ps, pe)) ++nlast;
+      }
+    }
     const uint64_t wm = __ballot(win_);
     const uint64_t before = live & ((1ULL << lane) - 1);
     const int pv = before ? 63 - __builtin_clzll(before) : -1;
@@ -421,30 +456,70 @@ __device__ void wave_bpe(const DevTables& t, const DevWork& w, int64_t base,
     const int nx2 = after2 ? __builtin_ctzll(after2) : 64;
     dirty = win_ || (((live >> lane) & 1) && nx2 < 64 && ((wm >> nx2) & 1));
   }
-  if (elig) w.tok[pos] = ((live >> lane) & 1) ? sym : INVALID_ID;
+  if (hist && elig && lane == ps) w.hmeta[base + ps] = nfirst | (nlast << 16);
+  if (write && elig) w.tok[pos] = ((live >> lane) & 1) ? sym : INVALID_ID;
+  return live;
 }
 
-// One wave per 64-byte window. First the aligned window [64v, 64v+64):
-// every piece inside it; then the shifted window [64v-32, 64v+32): the
-// pieces that straddle an aligned boundary but fit it. A piece of <= 32
-// bytes always fits one of the two. Anything else is queued.
+// Find the end of the segment that starts at `a` and runs past the word
+// boundary at 64*wd (bit 0 of word wd is known clear). seg(word) gives the
+// boundary bits; the sentinel start bits at and after nb end the search.
+template <class SegBits>
+__device__ __forceinline__ int64_t seg_end_after(int64_t wd, SegBits seg) {
+  uint64_t word = seg(wd);
+  while (word == 0) word = seg(++wd);
+  return wd * 64 + __builtin_ctzll(word);
+}
+
+__device__ __forceinline__ bool fits_a_grid(int64_t a, int64_t b) {
+  return b - a <= 64 &&
+         (((a >> 6) == ((b - 1) >> 6)) || (((a + 32) >> 6) == ((b - 1 + 32) >> 6)));
+}
+
+__device__ __forceinline__ void push_pair(uint32_t* list, uint32_t* count,
+                                          uint32_t cap, uint32_t* status,
+                                          int64_t a, int64_t b) {
+  const uint32_t k = atomicAdd(count, 1u);
+  if (k < cap) {
+    list[2 * k] = (uint32_t)a;
+    list[2 * k + 1] = (uint32_t)b;
+  } else {
+    atomicOr(status, ST_LONGOVF);
+  }
+}
+
+// Window geometry shared by the grid kernels: phase 0 is the aligned
+// window [64v, 64v+64), phase 1 the shifted window [64v-32, 64v+32).
+// Given a function word -> boundary bits, returns the window's boundary
+// mask S and whether a boundary sits at the window end (E).
+template <class SegBits>
+__device__ __forceinline__ void window_bits(int64_t v, int phase, SegBits seg,
+                                            uint64_t* S, bool* E) {
+  if (phase == 0) {
+    *S = seg(v);
+    *E = seg(v + 1) & 1;
+  } else {
+    const uint64_t lo = v > 0 ? seg(v - 1) : ~0ULL;
+    const uint64_t hi = seg(v);
+    *S = (lo >> 32) | (hi << 32);
+    *E = (hi >> 32) & 1;
+  }
+}
+
+// One wave per 64-byte window: first the aligned window, then the shifted
+// one. A piece of <= 32 bytes always fits one of the two; the rest are
+// queued (longlist) by the lane that starts them.
 __global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
                                                    int64_t nwin) {
   const int lane = threadIdx.x & 63;
-  const int64_t win = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (win > nwin) return;  // whole wave; win == nwin: last shifted window
-  for (int phase = (win == nwin ? 1 : 0); phase < 2; ++phase) {
-    const int64_t base = phase == 0 ? win * 64 : win * 64 - 32;
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v > nwin) return;  // whole wave; v == nwin: last shifted window
+  auto seg = [&](int64_t wd) { return w.starts[wd]; };
+  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
+    const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
     uint64_t S;
     bool E;
-    if (phase == 0) {
-      S = w.starts[win];
-      E = w.starts[win + 1] & 1;
-    } else {
-      const uint64_t lo = win > 0 ? w.starts[win - 1] : ~0ULL;
-      S = (lo >> 32) | (w.starts[win] << 32);
-      E = (w.starts[win] >> 32) & 1;
-    }
+    window_bits(v, phase, seg, &S, &E);
     const int64_t pos = base + lane;
     const bool valid = pos >= 0 && pos < w.nb;
     const uint64_t le = S & mask_le(lane);
@@ -453,31 +528,14 @@ __global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
     const int pe = gt ? __builtin_ctzll(gt) : 64;
     const bool contained = ps >= 0 && (pe < 64 || E);
     bool elig = valid && contained;
-    if (phase == 1 && elig) {
-      const int64_t a = base + ps, b = base + pe;
-      if ((a >> 6) == ((b - 1) >> 6)) elig = false;  // aligned grid had it
-    }
+    if (phase == 1 && elig && ((base + ps) >> 6) == ((base + pe - 1) >> 6))
+      elig = false;  // the aligned grid had it
     if (phase == 0 && valid && ps == lane && !contained) {
-      // the piece runs past the window: find its end (bit 0 of the next
-      // word is clear since E is false; the sentinel bits at and after nb
-      // end the search inside the nwin+2 words) and queue it if neither
-      // grid holds it whole
-      int64_t wd = win + 1;
-      uint64_t word = w.starts[wd];
-      while (word == 0) word = w.starts[++wd];
-      const int64_t b = wd * 64 + __builtin_ctzll(word);
-      const int64_t a = pos;
-      if (b - a > 64 || ((a + 32) >> 6) != ((b - 1 + 32) >> 6)) {
-        const uint32_t k = atomicAdd(w.longcount, 1u);
-        if (k < w.long_cap) {
-          w.longlist[2 * k] = (uint32_t)a;
-          w.longlist[2 * k + 1] = (uint32_t)b;
-        } else {
-          atomicOr(w.status, ST_LONGOVF);
-        }
-      }
+      const int64_t b = seg_end_after(v + 1, seg);
+      if (!fits_a_grid(pos, b))
+        push_pair(w.longlist, w.longcount, w.long_cap, w.status, pos, b);
     }
-    wave_bpe(t, w, base, lane, elig, ps, pe);
+    wave_bpe(t, w, base, lane, elig, ps, pe, true, false, true);
   }
 }
 
@@ -490,28 +548,47 @@ hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
   return hipGetLastError();
 }
 
-// Queued pieces of at most 64 bytes (those that straddle both grids): one
-// wave per piece, lane = byte offset.
-__global__ __launch_bounds__(256) void k_bpe_queue(DevTables t, DevWork w) {
+// Entries of at most 64 bytes from a (start, end) list: one wave each,
+// lane = byte offset. Longer entries are left to the other stages.
+__global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
+                                                  const uint32_t* list,
+                                                  const uint32_t* count,
+                                                  uint32_t cap, int hist) {
   const int lane = threadIdx.x & 63;
-  uint32_t n = *w.longcount;
-  if (n > w.long_cap) n = w.long_cap;
+  uint32_t n = *count;
+  if (n > cap) n = cap;
   const uint32_t waves = gridDim.x * 4;
   for (uint32_t k = blockIdx.x * 4 + (threadIdx.x >> 6); k < n; k += waves) {
-    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
     if (len > 64) continue;  // wave-uniform
-    wave_bpe(t, w, (int64_t)a, lane, lane < len, 0, len);
+    wave_bpe(t, w, (int64_t)a, lane, lane < len, 0, len, !hist, hist != 0, true);
   }
 }
 
 hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
                             hipStream_t s) {
-  hipLaunchKernelGGL(k_bpe_queue, dim3(512), dim3(256), 0, s, t, w);
+  hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
+                     (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
+                     w.long_cap, 0);
   return hipGetLastError();
 }
 
 // ------------------------------------------------- 3. long-piece BPE
+//
+// A piece longer than 64 bytes is cut into short segments at positions that
+// are token boundaries in the BPE of a 64-byte window centred on them; the
+// segments are merged independently (wave per window, recording how each
+// segment's first and last token evolve); then every cut is certified:
+// with a merge table in which every rule that consumes a token ranks above
+// every rule that makes it, the whole-piece process is the rank-ordered
+// interleaving of the segment processes as long as no pair across a cut is
+// ever merged, and whether it is can be decided from the two boundary
+// histories alone (the pair across the cut at each moment, against the
+// ranks at which its two tokens are next consumed). A failed cut is
+// removed and the joined segment redone, until every remaining cut holds;
+// the worst case is the whole piece as one segment. Tables with a rule
+// out of that order, or bytes without an id, take the serial path.
 
 __device__ __forceinline__ void heap_push(uint64_t* h, uint32_t& n, uint64_t e) {
   uint32_t i = n++;
@@ -540,10 +617,13 @@ __device__ __forceinline__ uint64_t heap_pop(uint64_t* h, uint32_t& n) {
   return top;
 }
 
+// Exact merge of [a, b) by one thread (heap of rank<<32|position, stale
+// entries skipped -- the HF algorithm), with the same history recording as
+// wave_bpe when `hist`.
 __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
-                           uint32_t b) {
+                           uint32_t b, bool vocab_first, bool hist) {
   uint32_t* tok = w.tok;
-  if (t.ignore_merges) {
+  if (vocab_first && t.ignore_merges) {
     const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
     if (hit >= 0) {
       tok[a] = (uint32_t)hit;
@@ -554,7 +634,7 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
   int32_t* nx = w.nx;
   int32_t* pv = w.pv;
   uint64_t* h = w.heap + 3ull * a;
-  uint32_t hn = 0;
+  uint32_t hn = 0, nfirst = 0, nlast = 0;
   int32_t prev = -1;
   for (uint32_t p = a; p < b; ++p) {
     const int32_t id = t.byte_id[w.text[p]];
@@ -578,6 +658,10 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
     const int32_t q = nx[p];
     const uint64_t v = pair_lookup(t, tok[p], tok[q]);
     if (v == ~0ULL || (uint32_t)(v >> 32) != r) continue;  // stale entry
+    if (hist) {
+      if (p == a) w.hfirst[a + nfirst++] = v;
+      if (nx[q] < 0) w.hlast[a + nlast++] = v;
+    }
     tok[p] = (uint32_t)v;
     tok[q] = INVALID_ID;
     nx[p] = nx[q];
@@ -591,21 +675,224 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
       if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | p);
     }
   }
+  if (hist) w.hmeta[a] = nfirst | (nlast << 16);
 }
 
-__global__ __launch_bounds__(64) void k_bpe_long(DevTables t, DevWork w) {
+// Queued pieces over 64 bytes: a whole-vocabulary hit (ignore_merges), the
+// serial path when certification is off, else mark their bytes in inlong.
+__global__ __launch_bounds__(64) void k_long_prep(DevTables t, DevWork w) {
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
-    if (b - a > 64) bpe_serial(t, w, a, b);
+    if (b - a <= 64) continue;
+    if (t.ignore_merges) {
+      const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
+      if (hit >= 0) {
+        w.tok[a] = (uint32_t)hit;
+        for (uint32_t p = a + 1; p < b; ++p) w.tok[p] = INVALID_ID;
+        continue;
+      }
+    }
+    if (!t.cert) {
+      bpe_serial(t, w, a, b, false, false);
+      continue;
+    }
+    const uint32_t wa = a >> 6, wb = (b - 1) >> 6;
+    for (uint32_t wd = wa; wd <= wb; ++wd) {
+      const uint32_t lo = wd == wa ? (a & 63) : 0;
+      const uint32_t hi = wd == wb ? ((b - 1) & 63) + 1 : 64;
+      const uint64_t m = lanes_in((int)lo, (int)hi);
+      if (m == ~0ULL) w.inlong[wd] = m;  // a whole word of one piece
+      else atomicOr(reinterpret_cast<unsigned long long*>(&w.inlong[wd]), m);
+    }
   }
 }
 
-hipError_t launch_bpe_long(const DevTables& t, const DevWork& w,
-                           hipStream_t s) {
-  hipLaunchKernelGGL(k_bpe_long, dim3(1024), dim3(64), 0, s, t, w);
+__device__ __forceinline__ uint64_t inlong_window(const DevWork& w, int64_t v,
+                                                  int phase) {
+  if (phase == 0) return w.inlong[v];
+  const uint64_t lo = v > 0 ? w.inlong[v - 1] : 0;
+  return (lo >> 32) | (w.inlong[v] << 32);
+}
+
+// Cut selection: BPE of the long-piece bytes of every window, window edges
+// taken as cuts; the token starts in the window's central 32 bytes become
+// candidate cuts. Aligned window v owns bits 16..47 of word v, shifted
+// window v owns bits 48..63 of word v-1 and 0..15 of word v.
+__global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
+                                                      int64_t nwin) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v > nwin) return;
+  auto seg = [&](int64_t wd) { return w.starts[wd]; };
+  uint16_t* cut16 = reinterpret_cast<uint16_t*>(w.cuts);
+  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
+    const uint64_t L = inlong_window(w, v, phase);
+    if (L == 0) continue;  // wave-uniform
+    const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
+    uint64_t S;
+    bool E;
+    window_bits(v, phase, seg, &S, &E);
+    S |= 1;  // the window start cuts whatever runs into it
+    const uint64_t le = S & mask_le(lane);
+    const int ps = 63 - __builtin_clzll(le);
+    const uint64_t gt = S & ~mask_le(lane);
+    const int pe = gt ? __builtin_ctzll(gt) : 64;
+    const bool elig = (L >> lane) & 1;
+    const uint64_t live = wave_bpe(t, w, base, lane, elig, ps, pe, false,
+                                   false, false);
+    if (lane == 0) {
+      if (phase == 0) {
+        cut16[4 * v + 1] = (uint16_t)(live >> 16);
+        cut16[4 * v + 2] = (uint16_t)(live >> 32);
+      } else {
+        if (v > 0) cut16[4 * (v - 1) + 3] = (uint16_t)(live >> 16);
+        cut16[4 * v] = (uint16_t)(live >> 32);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint64_t seg_word(const DevWork& w, int64_t wd) {
+  return w.starts[wd] | (w.cuts[wd] & w.inlong[wd]);
+}
+
+// Segment pass over the long-piece bytes (grid windows as in k_bpe_small,
+// with histories). Segments that fit no grid window go to seglist.
+__global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
+                                                       int64_t nwin) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v > nwin) return;
+  auto seg = [&](int64_t wd) { return seg_word(w, wd); };
+  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
+    const uint64_t L = inlong_window(w, v, phase);
+    if (L == 0) continue;
+    const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
+    uint64_t S;
+    bool E;
+    window_bits(v, phase, seg, &S, &E);
+    const int64_t pos = base + lane;
+    const bool inl = (L >> lane) & 1;
+    const uint64_t le = S & mask_le(lane);
+    const int ps = le ? 63 - __builtin_clzll(le) : -1;
+    const uint64_t gt = S & ~mask_le(lane);
+    const int pe = gt ? __builtin_ctzll(gt) : 64;
+    const bool contained = ps >= 0 && (pe < 64 || E);
+    bool elig = inl && contained;
+    if (phase == 1 && elig && ((base + ps) >> 6) == ((base + pe - 1) >> 6))
+      elig = false;
+    if (phase == 0 && inl && ps == lane && !contained) {
+      const int64_t b = seg_end_after(v + 1, seg);
+      if (!fits_a_grid(pos, b))
+        push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
+    }
+    wave_bpe(t, w, base, lane, elig, ps, pe, false, true, true);
+  }
+}
+
+// seglist entries over 64 bytes: serial merge with histories.
+__global__ __launch_bounds__(64) void k_seg_serial(DevTables t, DevWork w) {
+  uint32_t n = *w.segcount;
+  if (n > w.seg_cap) n = w.seg_cap;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
+    const uint32_t a = w.seglist[2 * k], b = w.seglist[2 * k + 1];
+    if (b - a > 64) bpe_serial(t, w, a, b, false, true);
+  }
+}
+
+// Certify every cut: thread per bitmask word. A failing cut is recorded in
+// failm (applied before the next segment pass) and counted.
+__global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
+                                                 int64_t nwords) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= nwords) return;
+  uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
+  while (cuts) {
+    const int bit = __builtin_ctzll(cuts);
+    cuts &= cuts - 1;
+    const int64_t c = v * 64 + bit;
+    // start of the segment that ends at c
+    int64_t wd = v;
+    uint64_t word = seg_word(w, wd) & ((1ULL << bit) - 1);
+    while (word == 0) word = seg_word(w, --wd);
+    const int64_t a = wd * 64 + (63 - __builtin_clzll(word));
+    const uint32_t ma = w.hmeta[a], mb = w.hmeta[c];
+    const uint32_t na = ma >> 16, nbv = mb & 0xFFFF;
+    const uint64_t* ea = w.hlast + a;
+    const uint64_t* eb = w.hfirst + c;
+    uint32_t L = (uint32_t)t.byte_id[w.text[c - 1]];
+    uint32_t R = (uint32_t)t.byte_id[w.text[c]];
+    uint32_t i = 0, j = 0;
+    bool ok = true;
+    for (;;) {
+      const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
+      const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
+      const uint64_t x = pair_lookup(t, L, R);
+      const uint32_t rho = x != ~0ULL ? (uint32_t)(x >> 32) : RANK_INF;
+      if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
+      if (ra == RANK_INF && rb == RANK_INF) break;
+      if (ra <= rb) { L = (uint32_t)ea[i]; ++i; }
+      if (rb <= ra) { R = (uint32_t)eb[j]; ++j; }
+    }
+    if (!ok) {
+      atomicOr(reinterpret_cast<unsigned long long*>(&w.failm[v]), 1ULL << bit);
+      atomicAdd(w.nfail, 1u);
+    }
+  }
+}
+
+__global__ void k_apply_fail(DevWork w, int64_t nwords) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= nwords) return;
+  const uint64_t f = w.failm[v];
+  if (f) {
+    w.cuts[v] &= ~f;
+    w.failm[v] = 0;
+  }
+}
+
+hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(64), 0, s, t, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
+                               hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_long_windows, dim3((uint32_t)((nwin + 4) / 4)),
+                     dim3(256), 0, s, t, w, nwin);
+  return hipGetLastError();
+}
+
+hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
+                                hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_long_segments, dim3((uint32_t)((nwin + 4) / 4)),
+                     dim3(256), 0, s, t, w, nwin);
+  hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
+                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
+                     w.seg_cap, 1);
+  hipLaunchKernelGGL(k_seg_serial, dim3(256), dim3(64), 0, s, t, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_certify(const DevTables& t, const DevWork& w,
+                          hipStream_t s) {
+  const int64_t nwords = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_certify, dim3((uint32_t)((nwords + 255) / 256)),
+                     dim3(256), 0, s, t, w, nwords);
+  return hipGetLastError();
+}
+
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
+  const int64_t nwords = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_apply_fail, dim3((uint32_t)((nwords + 255) / 256)),
+                     dim3(256), 0, s, w, nwords);
   return hipGetLastError();
 }
 

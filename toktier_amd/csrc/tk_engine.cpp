@@ -109,11 +109,14 @@ struct tk_engine {
   DevBuf<uint64_t> starts, docmask, heap, docoffs, rows;
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
   DevBuf<int32_t> nx, pv;
+  DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast;
+  DevBuf<uint32_t> hmeta, seglist;
   size_t docs_cap = 0;
   // timing
   bool timing = false;
-  hipEvent_t ev[6] = {};
+  hipEvent_t ev[8] = {};
   double last_us[5] = {};
+  size_t last_passes = 0;
 };
 
 namespace {
@@ -160,7 +163,14 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->pv.alloc(need));
     HIP_TRY(e->heap.alloc(3 * need));
     HIP_TRY(e->longlist.alloc(2 * long_cap));
-    HIP_TRY(e->ctrl.alloc(16));
+    HIP_TRY(e->ctrl.alloc(tk::CTRL_WORDS));
+    HIP_TRY(e->inlong.alloc(words));
+    HIP_TRY(e->cuts.alloc(words));
+    HIP_TRY(e->failm.alloc(words));
+    HIP_TRY(e->hfirst.alloc(need));
+    HIP_TRY(e->hlast.alloc(need));
+    HIP_TRY(e->hmeta.alloc(need));
+    HIP_TRY(e->seglist.alloc(2 * (need / 2 + 64)));
     HIP_TRY(e->blkcount.alloc(nblk));
     HIP_TRY(e->blkprefix.alloc(nblk));
     HIP_TRY(e->out.alloc(need));
@@ -174,10 +184,8 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
   return TK_OK;
 }
 
-// Runs every stage for nb bytes already at d_text. Leaves ids in e->out and
-// [status, total] in e->ctrl.
-int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
-                 const uint64_t* d_docmask, bool check_nfc, hipStream_t s) {
+tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
+                      const uint64_t* d_docmask, bool check_nfc) {
   tk::DevWork w{};
   w.text = d_text;
   w.nb = (int64_t)nb;
@@ -189,43 +197,103 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.pv = e->pv.p;
   w.heap = e->heap.p;
   w.longlist = e->longlist.p;
-  w.longcount = e->ctrl.p + 2;
+  w.longcount = e->ctrl.p + tk::CTRL_LONG;
   w.long_cap = (uint32_t)(e->longlist.n / 2);
-  w.status = e->ctrl.p;
+  w.status = e->ctrl.p + tk::CTRL_STATUS;
   w.blkcount = e->blkcount.p;
   w.blkprefix = e->blkprefix.p;
   w.out = e->out.p;
-  HIP_TRY(hipMemsetAsync(e->ctrl.p, 0, 16 * sizeof(uint32_t), s));
-  if (e->timing) HIP_TRY(hipEventRecord(e->ev[0], s));
-  HIP_TRY(tk::launch_pretok(e->t, w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(e->ev[1], s));
-  HIP_TRY(tk::launch_bpe_small(e->t, w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(e->ev[2], s));
-  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
-  HIP_TRY(tk::launch_bpe_long(e->t, w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(e->ev[3], s));
-  HIP_TRY(tk::launch_compact(w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(e->ev[4], s));
+  w.inlong = e->inlong.p;
+  w.cuts = e->cuts.p;
+  w.failm = e->failm.p;
+  w.hfirst = e->hfirst.p;
+  w.hlast = e->hlast.p;
+  w.hmeta = e->hmeta.p;
+  w.seglist = e->seglist.p;
+  w.segcount = e->ctrl.p + tk::CTRL_SEG;
+  w.seg_cap = (uint32_t)(e->seglist.n / 2);
+  w.nfail = e->ctrl.p + tk::CTRL_FAIL;
+  return w;
+}
+
+int read_ctrl_words(tk_engine* e, hipStream_t s, uint32_t* h) {
+  HIP_TRY(hipMemcpyAsync(h, e->ctrl.p, 8 * sizeof(uint32_t),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
+    return fail(TK_E_INTERNAL, "piece queue overflow");
   return TK_OK;
 }
 
-int read_ctrl(tk_engine* e, hipStream_t s, uint32_t* status, uint32_t* total) {
-  uint32_t h[4];
-  HIP_TRY(hipMemcpyAsync(h, e->ctrl.p, sizeof h, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
-  if (e->timing) {
-    float ms;
-    for (int k = 0; k < 4; ++k) {
-      HIP_TRY(hipEventElapsedTime(&ms, e->ev[k], e->ev[k + 1]));
-      e->last_us[k] = ms * 1e3;
-    }
-    HIP_TRY(hipEventElapsedTime(&ms, e->ev[0], e->ev[4]));
-    e->last_us[4] = ms * 1e3;
+float elapsed_us(hipEvent_t a, hipEvent_t b) {
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return 0.f;
+  return ms * 1e3f;
+}
+
+// Runs every stage for nb bytes already at d_text and waits for the result:
+// ids in e->out, status and total count returned. Long pieces whose cuts
+// fail certification are redone here (host-driven passes, each removing
+// the failed cuts) until every cut holds.
+int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
+                 const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
+                 uint32_t* status, uint32_t* total) {
+  const tk::DevWork w = make_work(e, d_text, nb, d_docmask, check_nfc);
+  const size_t words = nb / 64 + 4;
+  hipEvent_t* ev = e->ev;
+  HIP_TRY(hipMemsetAsync(e->ctrl.p, 0, tk::CTRL_WORDS * sizeof(uint32_t), s));
+  HIP_TRY(hipMemsetAsync(e->inlong.p, 0, words * 8, s));
+  HIP_TRY(hipMemsetAsync(e->failm.p, 0, words * 8, s));
+  if (e->timing) HIP_TRY(hipEventRecord(ev[0], s));
+  HIP_TRY(tk::launch_pretok(e->t, w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(ev[1], s));
+  HIP_TRY(tk::launch_bpe_small(e->t, w, s));
+  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(ev[2], s));
+  HIP_TRY(tk::launch_long_prep(e->t, w, s));
+  if (e->t.cert) {
+    HIP_TRY(tk::launch_long_windows(e->t, w, s));
+    HIP_TRY(tk::launch_long_segments(e->t, w, s));
+    HIP_TRY(tk::launch_certify(e->t, w, s));
   }
-  *status = h[0];
-  *total = h[1];
-  if (h[0] & tk::ST_LONGOVF)
-    return fail(TK_E_INTERNAL, "long-piece queue overflow");
+  if (e->timing) HIP_TRY(hipEventRecord(ev[3], s));
+  HIP_TRY(tk::launch_compact(w, s));
+  if (e->timing) HIP_TRY(hipEventRecord(ev[4], s));
+  uint32_t h[8];
+  int rc = read_ctrl_words(e, s, h);
+  if (rc != TK_OK) return rc;
+  if (e->timing) {
+    for (int k = 0; k < 4; ++k) e->last_us[k] = elapsed_us(ev[k], ev[k + 1]);
+    e->last_us[4] = elapsed_us(ev[0], ev[4]);
+  }
+  if (h[tk::CTRL_FAIL] != 0) {
+    // every pass removes at least one cut, so this ends (at worst with each
+    // long piece as one segment); the bound only guards against a defect
+    size_t passes = 0;
+    if (e->timing) HIP_TRY(hipEventRecord(ev[5], s));
+    while (h[tk::CTRL_FAIL] != 0) {
+      if (++passes > nb + 1) return fail(TK_E_INTERNAL, "certification did not converge");
+      HIP_TRY(hipMemsetAsync(e->ctrl.p + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
+      HIP_TRY(tk::launch_apply_fail(w, s));
+      HIP_TRY(tk::launch_long_segments(e->t, w, s));
+      HIP_TRY(tk::launch_certify(e->t, w, s));
+      if ((rc = read_ctrl_words(e, s, h)) != TK_OK) return rc;
+    }
+    if (e->timing) HIP_TRY(hipEventRecord(ev[6], s));
+    HIP_TRY(tk::launch_compact(w, s));
+    if (e->timing) HIP_TRY(hipEventRecord(ev[7], s));
+    if ((rc = read_ctrl_words(e, s, h)) != TK_OK) return rc;
+    if (e->timing) {
+      e->last_us[2] += elapsed_us(ev[5], ev[6]);
+      e->last_us[3] = elapsed_us(ev[6], ev[7]);
+      e->last_us[4] = elapsed_us(ev[0], ev[7]);
+    }
+    e->last_passes = passes;
+  } else {
+    e->last_passes = 0;
+  }
+  *status = h[tk::CTRL_STATUS];
+  *total = h[tk::CTRL_TOTAL];
   return TK_OK;
 }
 
@@ -404,6 +472,13 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.dmax = cfg->ruleset == TK_RULESET_CL100K ? cfg->digits_max : 0;
   e->t.ignore_merges = cfg->ignore_merges ? 1 : 0;
   e->t.needs_nfc = cfg->needs_nfc ? 1 : 0;
+  // Long pieces are cut and certified only when every merge rule that
+  // consumes a token ranks above every rule that produces it (no bit set
+  // in unsafe_bits) and every byte has an initial id.
+  bool cert = true;
+  for (size_t i = 0; i < unsafe_len / 4; ++i) cert = cert && unsafe_bits[i] == 0;
+  for (int b = 0; b < 256; ++b) cert = cert && byte_id[b] >= 0;
+  e->t.cert = cert ? 1 : 0;
   if (hipDeviceSynchronize() != hipSuccess)
     return bail(fail(TK_E_DEVICE, "device synchronize after upload failed"));
   *out = e;
@@ -450,10 +525,10 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   if (rc != TK_OK) return rc;
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
-  rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr, check, s);
-  if (rc != TK_OK) return rc;
   uint32_t st, total;
-  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr,
+                    check, s, &st, &total);
+  if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
@@ -477,10 +552,9 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   hipStream_t s = e->stream;
   HIP_TRY(hipMemcpyAsync(e->text.p, text, nbytes, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
-  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s);
-  if (rc != TK_OK) return rc;
   uint32_t st, total;
-  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, &st, &total);
+  if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
@@ -521,15 +595,11 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   HIP_TRY(hipMemcpyAsync(e->docmask.p, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
-  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s);
-  if (rc != TK_OK) return rc;
-  tk::DevWork w{};
-  w.nb = (int64_t)nb;
-  w.tok = e->tok.p;
-  w.blkprefix = e->blkprefix.p;
-  HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   uint32_t st, total;
-  if ((rc = read_ctrl(e, s, &st, &total)) != TK_OK) return rc;
+  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, &st, &total);
+  if (rc != TK_OK) return rc;
+  const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check);
+  HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToHost, s));
