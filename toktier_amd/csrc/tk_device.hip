@@ -418,7 +418,10 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
       }
       dirty = false;
     }
-    const uint32_t key = rk != RANK_INF ? ((rk << 6) | (uint32_t)lane) : RANK_INF;
+    // a lane whose symbol was merged away keeps its old pair rank in rk;
+    // only live lanes compete
+    const uint32_t key = (me && rk != RANK_INF) ? ((rk << 6) | (uint32_t)lane)
+                                                : RANK_INF;
     uint32_t m = key;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
