@@ -33,6 +33,8 @@ struct DevTables {
   int32_t needs_nfc;
   int32_t cert;                // long pieces may be cut and certified:
                                // rank-ordered table, every byte has an id
+  const uint32_t* unsafe;      // unsafe-rank bitmap or nullptr
+  uint32_t unsafe_words;
 };
 
 // Per-request device buffers (sized by capacity).
@@ -65,6 +67,8 @@ struct DevWork {
   uint32_t* segcount;    // ctrl[3]
   uint32_t seg_cap;
   uint32_t* nfail;       // ctrl[4]
+  uint64_t* dirty_cur;   // repair pass: words (64 bytes) to redo, 1 bit each
+  uint64_t* dirty_next;  // words marked by the current certify pass
 };
 
 // ctrl word layout (device -> host)
@@ -87,8 +91,8 @@ hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
-                                hipStream_t s);
-hipError_t launch_certify(const DevTables& t, const DevWork& w,
+                                int all, hipStream_t s);
+hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s);
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
 hipError_t launch_compact(const DevWork& w, hipStream_t s);

@@ -681,15 +681,249 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
   if (hist) w.hmeta[a] = nfirst | (nlast << 16);
 }
 
-// Queued pieces over 64 bytes: a whole-vocabulary hit (ignore_merges), the
-// serial path when certification is off, else mark their bytes in inlong.
+// ---- wide pieces: one wave per piece / segment of 65..WIDE_MAX bytes,
+// state in LDS (slot s = 64*row + lane). Each round merges every leftmost
+// non-overlapping occurrence of the lowest-ranked pair at once, which is the
+// one-at-a-time order when that rank's result is consumed only by higher
+// ranks; a rank flagged in unsafe_bits merges its leftmost occurrence
+// alone (src/toktier/kernels/bpe_tables.py:435-501 guard,
+// pretok_kernel.cu:1174-1186).
+constexpr int WIDE_MAX = 512;
+constexpr int WIDE_ROWS = WIDE_MAX / 64;
+constexpr uint32_t SYM_RAW = 0x80000000u;  // symbol is still its raw byte
+
+struct WideLds {
+  uint32_t sym[WIDE_MAX];
+  uint32_t rk[WIDE_MAX];
+  uint32_t mid[WIDE_MAX];
+  int16_t nx[WIDE_MAX];
+  int16_t pv[WIDE_MAX];
+};
+
+__device__ __forceinline__ void lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+}
+
+__device__ __forceinline__ bool rank_unsafe(const DevTables& t, uint32_t r) {
+  return t.unsafe && ((r >> 5) < t.unsafe_words) &&
+         ((t.unsafe[r >> 5] >> (r & 31)) & 1);
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) v = min(v, (uint32_t)__shfl_xor(v, d));
+  return v;
+}
+
+// pair value for the symbols at slots s and n of a piece starting at a
+__device__ __forceinline__ uint64_t wide_pair(const DevTables& t,
+                                              const DevWork& w, uint32_t a,
+                                              const WideLds& L, int s, int n) {
+  const uint32_t x = L.sym[s], y = L.sym[n];
+  if ((x & y) & SYM_RAW)
+    return t.bytepair[((uint32_t)w.text[a + s] << 8) | w.text[a + n]];
+  return pair_lookup(t, x & ~SYM_RAW, y & ~SYM_RAW);
+}
+
+__device__ void wave_bpe_wide(const DevTables& t, const DevWork& w,
+                              uint32_t a, int len, bool vocab_first,
+                              bool hist, WideLds& L) {
+  const int lane = threadIdx.x & 63;
+  const int rows = (len + 63) >> 6;
+  if (vocab_first && t.ignore_merges) {
+    int32_t hit = -1;
+    if (lane == 0) hit = vocab_lookup(t, w.text + a, len);
+    hit = __shfl(hit, 0);
+    if (hit >= 0) {
+      for (int r = 0; r < rows; ++r) {
+        const int s = r * 64 + lane;
+        if (s < len) w.tok[a + s] = s == 0 ? (uint32_t)hit : INVALID_ID;
+      }
+      return;
+    }
+  }
+  uint64_t live[WIDE_ROWS];
+#pragma unroll
+  for (int r = 0; r < WIDE_ROWS; ++r) {
+    const int s = r * 64 + lane;
+    int32_t id = -1;
+    if (r < rows && s < len) id = t.byte_id[w.text[a + s]];
+    if (r < rows) L.sym[s] = id >= 0 ? (SYM_RAW | (uint32_t)id) : 0u;
+    live[r] = __ballot(id >= 0);
+  }
+  // neighbour links over the live slots
+#pragma unroll
+  for (int r = 0; r < WIDE_ROWS; ++r) {
+    if (r >= rows) break;
+    const int s = r * 64 + lane;
+    int n = -1, p = -1;
+    uint64_t m = live[r] & ~mask_le(lane);
+    if (m) n = r * 64 + __builtin_ctzll(m);
+    for (int q = r + 1; n < 0 && q < rows; ++q)
+      if (live[q]) n = q * 64 + __builtin_ctzll(live[q]);
+    m = live[r] & ((1ULL << lane) - 1);
+    if (m) p = r * 64 + 63 - __builtin_clzll(m);
+    for (int q = r - 1; p < 0 && q >= 0; --q)
+      if (live[q]) p = q * 64 + 63 - __builtin_clzll(live[q]);
+    L.nx[s] = (int16_t)n;
+    L.pv[s] = (int16_t)p;
+  }
+  lds_fence();
+#pragma unroll
+  for (int r = 0; r < WIDE_ROWS; ++r) {
+    if (r >= rows) break;
+    const int s = r * 64 + lane;
+    uint32_t k = RANK_INF, m = 0;
+    const int n = L.nx[s];
+    if (((live[r] >> lane) & 1) && n >= 0) {
+      const uint64_t v = wide_pair(t, w, a, L, s, n);
+      if (v != ~0ULL) { k = (uint32_t)(v >> 32); m = (uint32_t)v; }
+    }
+    L.rk[s] = k;
+    L.mid[s] = m;
+  }
+  uint32_t nfirst = 0, nlast = 0;
+  for (;;) {
+    lds_fence();
+    uint32_t best = RANK_INF;
+#pragma unroll
+    for (int r = 0; r < WIDE_ROWS; ++r) {
+      if (r >= rows) break;
+      const int s = r * 64 + lane;
+      const uint32_t k = L.rk[s];
+      if (((live[r] >> lane) & 1) && k != RANK_INF) best = min(best, (k << 9) | (uint32_t)s);
+    }
+    best = wave_min_u32(best);
+    if (best == RANK_INF) break;
+    const uint32_t R = best >> 9;
+    const int s0 = (int)(best & 511);
+    uint64_t sel[WIDE_ROWS];
+    if (rank_unsafe(t, R)) {
+#pragma unroll
+      for (int r = 0; r < WIDE_ROWS; ++r) sel[r] = (r == (s0 >> 6)) ? (1ULL << (s0 & 63)) : 0;
+    } else {
+      // leftmost non-overlapping occurrences, left to right
+      int blocked = -1;
+#pragma unroll
+      for (int r = 0; r < WIDE_ROWS; ++r) {
+        sel[r] = 0;
+        if (r >= rows) continue;
+        const int s = r * 64 + lane;
+        uint64_t occ = __ballot(((live[r] >> lane) & 1) && L.rk[s] == R);
+        while (occ) {
+          const int b = __builtin_ctzll(occ);
+          occ &= occ - 1;
+          const int q = r * 64 + b;
+          if (q != blocked) {
+            sel[r] |= 1ULL << b;
+            blocked = L.nx[q];
+          }
+        }
+      }
+    }
+    if (hist) {
+      // first live slot and last live slot of the piece
+      int f = -1, l = -1;
+      for (int r = 0; r < rows; ++r)
+        if (live[r]) { f = r * 64 + __builtin_ctzll(live[r]); break; }
+      for (int r = rows - 1; r >= 0; --r)
+        if (live[r]) { l = r * 64 + 63 - __builtin_clzll(live[r]); break; }
+      const int pl = L.pv[l];
+      if ((sel[f >> 6] >> (f & 63)) & 1) {
+        if (lane == 0) w.hfirst[a + nfirst] = ((uint64_t)R << 32) | L.mid[f];
+        ++nfirst;
+      }
+      if (pl >= 0 && ((sel[pl >> 6] >> (pl & 63)) & 1)) {
+        if (lane == 0) w.hlast[a + nlast] = ((uint64_t)R << 32) | L.mid[pl];
+        ++nlast;
+      }
+    }
+    // a slot dies when its left neighbour is a selected left symbol
+    uint64_t dead[WIDE_ROWS];
+#pragma unroll
+    for (int r = 0; r < WIDE_ROWS; ++r) {
+      bool dies = false;
+      if (r < rows) {
+        const int s = r * 64 + lane;
+        const int p = L.pv[s];
+        dies = ((live[r] >> lane) & 1) && p >= 0 && ((sel[p >> 6] >> (p & 63)) & 1);
+      }
+      dead[r] = __ballot(dies);
+    }
+    lds_fence();
+#pragma unroll
+    for (int r = 0; r < WIDE_ROWS; ++r) {
+      if (r >= rows) break;
+      const int s = r * 64 + lane;
+      if ((sel[r] >> lane) & 1) {
+        const int rn = L.nx[s];
+        const int nn = L.nx[rn];
+        L.sym[s] = L.mid[s];
+        L.nx[s] = (int16_t)nn;
+        if (nn >= 0) L.pv[nn] = (int16_t)s;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < WIDE_ROWS; ++r) live[r] &= ~dead[r];
+    lds_fence();
+    // pairs that changed: the selected slots and the slots right before them
+#pragma unroll
+    for (int r = 0; r < WIDE_ROWS; ++r) {
+      if (r >= rows) break;
+      const int s = r * 64 + lane;
+      if (!((live[r] >> lane) & 1)) continue;
+      const int n = L.nx[s];
+      const bool dirty = ((sel[r] >> lane) & 1) ||
+                         (n >= 0 && ((sel[n >> 6] >> (n & 63)) & 1));
+      if (!dirty) continue;
+      uint32_t k = RANK_INF, m = 0;
+      if (n >= 0) {
+        const uint64_t v = wide_pair(t, w, a, L, s, n);
+        if (v != ~0ULL) { k = (uint32_t)(v >> 32); m = (uint32_t)v; }
+      }
+      L.rk[s] = k;
+      L.mid[s] = m;
+    }
+  }
+  lds_fence();
+#pragma unroll
+  for (int r = 0; r < WIDE_ROWS; ++r) {
+    if (r >= rows) break;
+    const int s = r * 64 + lane;
+    if (s < len)
+      w.tok[a + s] = ((live[r] >> lane) & 1) ? (L.sym[s] & ~SYM_RAW) : INVALID_ID;
+  }
+  if (hist && lane == 0) w.hmeta[a] = nfirst | (nlast << 16);
+}
+
+// Entries of 65..WIDE_MAX bytes from a (start, end) list, one wave each.
+__global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
+                                                  const uint32_t* list,
+                                                  const uint32_t* count,
+                                                  uint32_t cap, int hist) {
+  __shared__ WideLds lds[4];
+  uint32_t n = *count;
+  if (n > cap) n = cap;
+  const int wv = threadIdx.x >> 6;
+  const uint32_t waves = gridDim.x * 4;
+  for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
+    const uint32_t a = list[2 * k], b = list[2 * k + 1];
+    const int len = (int)(b - a);
+    if (len <= 64 || len > WIDE_MAX) continue;  // wave-uniform
+    wave_bpe_wide(t, w, a, len, !hist, hist != 0, lds[wv]);
+  }
+}
+
+// Queued pieces over WIDE_MAX bytes: a whole-vocabulary hit
+// (ignore_merges), the serial path when certification is off, else mark
+// their bytes in inlong for the cut / segment / certify stages.
 __global__ __launch_bounds__(64) void k_long_prep(DevTables t, DevWork w) {
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
-    if (b - a <= 64) continue;
+    if (b - a <= (uint32_t)WIDE_MAX) continue;
     if (t.ignore_merges) {
       const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
       if (hit >= 0) {
@@ -762,15 +996,23 @@ __device__ __forceinline__ uint64_t seg_word(const DevWork& w, int64_t wd) {
   return w.starts[wd] | (w.cuts[wd] & w.inlong[wd]);
 }
 
+__device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
+  return wd >= 0 && ((d[wd >> 6] >> (wd & 63)) & 1);
+}
+
 // Segment pass over the long-piece bytes (grid windows as in k_bpe_small,
-// with histories). Segments that fit no grid window go to seglist.
+// with histories). Segments that fit no grid window go to seglist. With
+// all == 0 (a repair pass) only windows touching a dirty word are redone.
 __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
-                                                       int64_t nwin) {
+                                                       int64_t nwin, int all) {
   const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (v > nwin) return;
   auto seg = [&](int64_t wd) { return seg_word(w, wd); };
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
+    if (!all && !word_dirty(w.dirty_cur, v) &&
+        !(phase == 1 && word_dirty(w.dirty_cur, v - 1)))
+      continue;
     const uint64_t L = inlong_window(w, v, phase);
     if (L == 0) continue;
     const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
@@ -796,23 +1038,25 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
   }
 }
 
-// seglist entries over 64 bytes: serial merge with histories.
+// seglist entries over WIDE_MAX bytes: serial merge with histories.
 __global__ __launch_bounds__(64) void k_seg_serial(DevTables t, DevWork w) {
   uint32_t n = *w.segcount;
   if (n > w.seg_cap) n = w.seg_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
     const uint32_t a = w.seglist[2 * k], b = w.seglist[2 * k + 1];
-    if (b - a > 64) bpe_serial(t, w, a, b, false, true);
+    if (b - a > (uint32_t)WIDE_MAX) bpe_serial(t, w, a, b, false, true);
   }
 }
 
-// Certify every cut: thread per bitmask word. A failing cut is recorded in
-// failm (applied before the next segment pass) and counted.
+// Certify every cut (thread per bitmask word; in a repair pass only the
+// dirty words). A failing cut is recorded in failm and counted, and the
+// words of the two segments it joins are marked dirty for the next pass.
 __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
-                                                 int64_t nwords) {
+                                                 int64_t nwords, int all) {
   const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (v >= nwords) return;
+  if (!all && !word_dirty(w.dirty_cur, v)) return;
   uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
   while (cuts) {
     const int bit = __builtin_ctzll(cuts);
@@ -844,10 +1088,20 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
     if (!ok) {
       atomicOr(reinterpret_cast<unsigned long long*>(&w.failm[v]), 1ULL << bit);
       atomicAdd(w.nfail, 1u);
+      // end of the segment that starts at c
+      int64_t we = v;
+      uint64_t up = seg_word(w, we) & ~mask_le(bit);
+      while (up == 0) up = seg_word(w, ++we);
+      const int64_t e = we * 64 + __builtin_ctzll(up);
+      for (int64_t q = a >> 6; q <= (e >> 6); ++q)
+        atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
+                 1ULL << (q & 63));
     }
   }
 }
 
+// Between passes: drop the failed cuts, and make the words marked by the
+// last certify pass the dirty set of the next one.
 __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (v >= nwords) return;
@@ -856,11 +1110,19 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
     w.cuts[v] &= ~f;
     w.failm[v] = 0;
   }
+  if (v < (nwords + 63) / 64 + 1) {
+    w.dirty_cur[v] = w.dirty_next[v];
+    w.dirty_next[v] = 0;
+  }
 }
 
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
                             hipStream_t s) {
   hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(64), 0, s, t, w);
+  // pieces of 65..WIDE_MAX bytes are merged whole, one wave each
+  hipLaunchKernelGGL(k_bpe_wide, dim3(2048), dim3(256), 0, s, t, w,
+                     (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
+                     w.long_cap, 0);
   return hipGetLastError();
 }
 
@@ -873,22 +1135,25 @@ hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
 }
 
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
-                                hipStream_t s) {
+                                int all, hipStream_t s) {
   const int64_t nwin = (w.nb + 63) / 64;
   hipLaunchKernelGGL(k_long_segments, dim3((uint32_t)((nwin + 4) / 4)),
-                     dim3(256), 0, s, t, w, nwin);
+                     dim3(256), 0, s, t, w, nwin, all);
   hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
+                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
+                     w.seg_cap, 1);
+  hipLaunchKernelGGL(k_bpe_wide, dim3(512), dim3(256), 0, s, t, w,
                      (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
                      w.seg_cap, 1);
   hipLaunchKernelGGL(k_seg_serial, dim3(256), dim3(64), 0, s, t, w);
   return hipGetLastError();
 }
 
-hipError_t launch_certify(const DevTables& t, const DevWork& w,
+hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s) {
   const int64_t nwords = (w.nb + 63) / 64;
   hipLaunchKernelGGL(k_certify, dim3((uint32_t)((nwords + 255) / 256)),
-                     dim3(256), 0, s, t, w, nwords);
+                     dim3(256), 0, s, t, w, nwords, all);
   return hipGetLastError();
 }
 

@@ -109,8 +109,8 @@ struct tk_engine {
   DevBuf<uint64_t> starts, docmask, heap, docoffs, rows;
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
   DevBuf<int32_t> nx, pv;
-  DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast;
-  DevBuf<uint32_t> hmeta, seglist;
+  DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
+  DevBuf<uint32_t> hmeta, seglist, unsafe;
   size_t docs_cap = 0;
   // timing
   bool timing = false;
@@ -171,6 +171,8 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->hlast.alloc(need));
     HIP_TRY(e->hmeta.alloc(need));
     HIP_TRY(e->seglist.alloc(2 * (need / 2 + 64)));
+    HIP_TRY(e->dirty_cur.alloc(words / 64 + 2));
+    HIP_TRY(e->dirty_next.alloc(words / 64 + 2));
     HIP_TRY(e->blkcount.alloc(nblk));
     HIP_TRY(e->blkprefix.alloc(nblk));
     HIP_TRY(e->out.alloc(need));
@@ -213,6 +215,8 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.segcount = e->ctrl.p + tk::CTRL_SEG;
   w.seg_cap = (uint32_t)(e->seglist.n / 2);
   w.nfail = e->ctrl.p + tk::CTRL_FAIL;
+  w.dirty_cur = e->dirty_cur.p;
+  w.dirty_next = e->dirty_next.p;
   return w;
 }
 
@@ -244,6 +248,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   HIP_TRY(hipMemsetAsync(e->ctrl.p, 0, tk::CTRL_WORDS * sizeof(uint32_t), s));
   HIP_TRY(hipMemsetAsync(e->inlong.p, 0, words * 8, s));
   HIP_TRY(hipMemsetAsync(e->failm.p, 0, words * 8, s));
+  HIP_TRY(hipMemsetAsync(e->dirty_next.p, 0, (words / 64 + 2) * 8, s));
   if (e->timing) HIP_TRY(hipEventRecord(ev[0], s));
   HIP_TRY(tk::launch_pretok(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(ev[1], s));
@@ -253,8 +258,8 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   HIP_TRY(tk::launch_long_prep(e->t, w, s));
   if (e->t.cert) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s));
-    HIP_TRY(tk::launch_long_segments(e->t, w, s));
-    HIP_TRY(tk::launch_certify(e->t, w, s));
+    HIP_TRY(tk::launch_long_segments(e->t, w, 1, s));
+    HIP_TRY(tk::launch_certify(e->t, w, 1, s));
   }
   if (e->timing) HIP_TRY(hipEventRecord(ev[3], s));
   HIP_TRY(tk::launch_compact(w, s));
@@ -275,8 +280,8 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
       if (++passes > nb + 1) return fail(TK_E_INTERNAL, "certification did not converge");
       HIP_TRY(hipMemsetAsync(e->ctrl.p + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
       HIP_TRY(tk::launch_apply_fail(w, s));
-      HIP_TRY(tk::launch_long_segments(e->t, w, s));
-      HIP_TRY(tk::launch_certify(e->t, w, s));
+      HIP_TRY(tk::launch_long_segments(e->t, w, 0, s));
+      HIP_TRY(tk::launch_certify(e->t, w, 0, s));
       if ((rc = read_ctrl_words(e, s, h)) != TK_OK) return rc;
     }
     if (e->timing) HIP_TRY(hipEventRecord(ev[6], s));
@@ -479,6 +484,13 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   for (size_t i = 0; i < unsafe_len / 4; ++i) cert = cert && unsafe_bits[i] == 0;
   for (int b = 0; b < 256; ++b) cert = cert && byte_id[b] >= 0;
   e->t.cert = cert ? 1 : 0;
+  e->t.unsafe = nullptr;
+  e->t.unsafe_words = 0;
+  if (!cert && unsafe_len >= 4) {
+    if ((rc = up(e->unsafe, unsafe_bits, unsafe_len / 4)) != TK_OK) return bail(rc);
+    e->t.unsafe = e->unsafe.p;
+    e->t.unsafe_words = (uint32_t)(unsafe_len / 4);
+  }
   if (hipDeviceSynchronize() != hipSuccess)
     return bail(fail(TK_E_DEVICE, "device synchronize after upload failed"));
   *out = e;
