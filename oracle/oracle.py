@@ -98,10 +98,17 @@ class Oracle:
             raise ValueError("invalid UTF-8")
         return bool(r)
 
-    def encode_bytes(self, data: bytes) -> np.ndarray | int:
-        """ids as uint32, or a negative status (E_NEEDS_NFC, E_UTF8)."""
+    def encode_bytes(self, data: bytes, normalized: bool = False
+                     ) -> np.ndarray | int:
+        """ids as uint32, or a negative status (E_NEEDS_NFC, E_UTF8).
+        ``normalized``: the text already went through the family's NFC, so
+        the quick check is skipped (the engine's TK_FLAG_NORMALIZED)."""
         out = np.zeros(max(1, len(data)), dtype=np.uint32)
-        n = self._lib.tko_encode(C.byref(self._t), data, len(data),
+        t = self._t
+        if normalized and t.needs_nfc:
+            t = _Tables.from_buffer_copy(self._t)
+            t.needs_nfc = 0
+        n = self._lib.tko_encode(C.byref(t), data, len(data),
                                  out.ctypes.data, out.size)
         if n < 0:
             return int(n)

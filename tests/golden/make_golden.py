@@ -1,0 +1,72 @@
+"""Writes golden_ids.json: inputs and the ids HF ``tokenizers`` 0.22.2 (the
+certified engine the reference pins against, ``README.md:7-10``) gives for
+them on the committed stand-in artifacts, ``add_special_tokens=False``.
+
+Run from the repository root: ``python tests/golden/make_golden.py``.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT))
+
+from tokenizers import Tokenizer, __version__ as tk_version  # noqa: E402
+
+from toktier_amd import standin, workloads  # noqa: E402
+
+SAMPLES = [
+    "", "a", " ", "  ", "\n", "\r\n", "hello world", "Hello, World!",
+    "it's 'S they'RE we'VE I'M you'LL he'D don't", "x'sy  'll",
+    "12345 1234567 3.14159 0x1F", "  leading and trailing  ",
+    "tabs\tand\tnew\nlines\r\n\r\n  \n", "naïve café résumé Ångström",
+    "中文字符测试，这是一个句子。", "😀👍🏽 👨‍👩‍👧 ❤️", "!!!???...---",
+    "a  b   c    d", "\t\tword", " !x", "'s", "''s", "!'s", "ſ'ſ", "'ſ",
+    "foo\r\n\r\n\tbar", "x \r\n y", "end with spaces   ", " nbsp ",
+    "a" * 100, "=" * 80, " " * 70 + "x", "1" * 40, "'" + "s" * 70,
+    "The quick brown fox jumps over the lazy dog. 0123456789!",
+    "def f(x):\n    return x**2  # comment\n",
+    "é composed? Å", "　ideographic space line sep",
+]
+
+
+def fuzz(rng: np.random.Generator, n: int) -> list[str]:
+    alpha = ["a", "A", "'", "s", "S", "ſ", "1", "2", " ", "\t", "\r",
+             "\n", "!", "é", "中", " ", "t", "l", "e", "r", "v", "d",
+             "m", "L", "E", "D", "\U0001f600", "-", ".", "́"]
+    return ["".join(alpha[int(i)] for i in rng.integers(0, len(alpha), int(k)))
+            for k in rng.integers(1, 40, size=n)]
+
+
+def main() -> None:
+    out = {"tokenizers_version": tk_version, "families": {}}
+    for name in ("qwen3_8b", "llama_3_1_8b", "gpt2"):
+        js = standin.load_artifact_json(name)
+        tok = Tokenizer.from_str(js)
+        rng = np.random.default_rng(99)
+        texts = list(SAMPLES) + fuzz(rng, 120)
+        snippet = workloads.config2(js, n_chars=6000)
+        texts += [snippet[i:i + 500] for i in range(0, 6000, 1000)]
+        code = workloads.config4(js, n_chars=3000)
+        texts += [code[i:i + 600] for i in range(0, 3000, 600)]
+        cjk = workloads.config5(js, n_chars=4000, n_runs=1, run_chars=500)
+        texts += [cjk[i:i + 800] for i in range(0, 4000, 800)]
+        cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}
+                 for t in texts]
+        out["families"][name] = {
+            "artifact_sha256": standin.ARTIFACT_SHA256[name],
+            "cases": cases,
+        }
+    path = Path(__file__).resolve().parent / "golden_ids.json"
+    path.write_text(json.dumps(out, ensure_ascii=False, indent=0) + "\n",
+                    encoding="utf-8")
+    print(path, sum(len(f["cases"]) for f in out["families"].values()), "cases")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,104 @@
+"""CPU: the C-ABI library loads, exports every entry point that
+include/toktier_hip.h declares, and validates its inputs without a GPU
+(preflight mirrors validate_tables, gpu.rs:1642-1679)."""
+
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import kit
+from toktier_amd import _ffi, classes
+from toktier_amd._build import LIB
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "toktier_hip.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(tk_[a-z_]+)\s*\(", text))
+
+
+def test_header_declares_the_binding_surface():
+    assert declared_symbols() == set(_ffi.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIB.exists(), "run __graft_entry__.build() first"
+    lib = C.CDLL(str(LIB))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def _cfg(k, **over):
+    t = k.tables
+    f = k.family
+    cfg = _ffi.TkConfig(
+        abi_version=_ffi.TK_ABI_VERSION, device_ordinal=0, ruleset=f.ruleset,
+        digits_max=f.digits_max, contractions=1, needs_nfc=int(f.needs_nfc),
+        ignore_merges=int(t.ignore_merges), pair_count=t.pair_count,
+        vocab_count=t.vocab_count, family=f.name.encode(),
+        artifact_sha256=b"x", expected_architecture=b"gfx950")
+    for key, val in over.items():
+        setattr(cfg, key, val)
+    return cfg
+
+
+def _preflight(cfg, k, **arrays):
+    t = k.tables
+    a = dict(cls=classes.class_table(), pk=t.pair_keys, pv=t.pair_vals,
+             bid=t.byte_id, vk=t.vocab_keys, vv=t.vocab_vals,
+             ub=t.unsafe_bits if t.unsafe_bits.size else np.zeros(0, np.uint32))
+    a.update(arrays)
+    args = []
+    for key in ("cls", "pk", "pv", "bid", "vk", "vv", "ub"):
+        arr = np.ascontiguousarray(a[key])
+        args += [arr.ctypes.data if arr.size else None, arr.nbytes]
+    return _ffi.lib().tk_engine_preflight(C.byref(cfg), *args)
+
+
+@pytest.mark.parametrize("name", ["qwen3_8b", "gpt2"])
+def test_preflight_accepts_valid_tables(name):
+    k = kit(name)
+    assert _preflight(_cfg(k), k) == _ffi.TK_OK
+
+
+def test_preflight_rejects_bad_shapes_and_config():
+    k = kit("gpt2")
+    L = _ffi.lib()
+    assert _preflight(_cfg(k, abi_version=99), k) == _ffi.TK_E_INVALID_ARG
+    assert b"abi_version" in L.tk_last_error()
+    assert _preflight(_cfg(k, ruleset=7), k) == _ffi.TK_E_INVALID_ARG
+    assert _preflight(_cfg(k, ruleset=0, digits_max=0), k) == _ffi.TK_E_INVALID_ARG
+    assert _preflight(_cfg(k, contractions=0), k) == _ffi.TK_E_INVALID_ARG
+    assert _preflight(_cfg(k), k, cls=classes.class_table()[:1000]) == _ffi.TK_E_SHAPE
+    assert b"U+10FFFF" in L.tk_last_error()
+    assert _preflight(_cfg(k, pair_count=k.tables.pair_count - 1), k) == _ffi.TK_E_SHAPE
+    assert _preflight(_cfg(k), k, pv=k.tables.pair_vals[:-1]) == _ffi.TK_E_SHAPE
+    assert _preflight(_cfg(k), k, bid=k.tables.byte_id[:255]) == _ffi.TK_E_SHAPE
+    assert _preflight(_cfg(k), k, ub=np.zeros(3, np.uint8)) == _ffi.TK_E_SHAPE
+
+
+def test_open_without_a_device_fails_cleanly():
+    try:
+        import torch
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is visible")
+    except ImportError:
+        pass
+    k = kit("gpt2")
+    with pytest.raises(_ffi.EngineError) as err:
+        _ffi.Engine(_cfg(k), classes.class_table(), k.tables, None)
+    assert err.value.status == _ffi.TK_E_DEVICE
+
+
+def test_null_arguments_are_refused():
+    L = _ffi.lib()
+    n = C.c_size_t()
+    assert L.tk_engine_encode(None, b"abc", 3, 0, None, 0, C.byref(n)) == _ffi.TK_E_INVALID_ARG
+    assert L.tk_engine_set_timing(None, 1) == _ffi.TK_E_INVALID_ARG
+    assert L.tk_engine_delivery(None) == b""

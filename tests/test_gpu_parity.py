@@ -119,3 +119,75 @@ def test_cjk_and_pathological_runs():
     want = k.oracle.encode_bytes(data)
     assert not isinstance(want, int)
     assert np.array_equal(got, want)
+
+
+def test_golden_vectors_through_the_c_abi():
+    import json
+    from pathlib import Path
+    g = json.loads((Path(__file__).resolve().parent / "golden" /
+                    "golden_ids.json").read_text(encoding="utf-8"))
+    for name in FAMILY_NAMES:
+        t = tok(name)
+        for case in g["families"][name]["cases"]:
+            assert list(t.encode(case["text"]).array) == case["ids"], (name, case["text"])
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4, 5])
+def test_full_size_configs_match_oracle(cfg):
+    from toktier_amd import workloads
+    name, gen = workloads.CONFIGS[cfg]
+    k, t = kit(name), tok(name)
+    data = gen(k.json).encode()
+    got = t.encode_bytes(data)
+    want = k.oracle.encode_bytes(data)
+    assert not isinstance(want, int)
+    assert np.array_equal(got, want)
+    if cfg == 1:
+        assert list(got) == k.hf_ids(data.decode())
+
+
+def test_full_size_batch_config3_rows():
+    from toktier_amd import workloads
+    k, t = kit("gpt2"), tok("gpt2")
+    docs = workloads.config3(k.json)
+    rows = t.encode_batch(docs)
+    assert len(rows) == len(docs)
+    for d, r in zip(docs, rows):
+        want = k.oracle.encode_bytes(d.encode())
+        assert np.array_equal(r.array, want)
+
+
+def test_nfc_fallback_matches_hf():
+    k, t = kit("qwen3_8b"), tok("qwen3_8b")
+    texts = ["café au lait", "Å and Å", "ẹ́",
+             "plain ascii", "ẛ̣ 각"]
+    for s in texts:
+        assert list(t.encode(s).array) == k.hf_ids(s), s
+    rows = t.encode_batch(texts)
+    for s, r in zip(texts, rows):
+        assert list(r.array) == k.hf_ids(s), s
+
+
+def test_invalid_utf8_is_an_error():
+    from toktier_amd import _ffi
+    t = tok("gpt2")
+    for bad in (b"\xff", b"ok\xc3", b"\xc0\x80", b"\xed\xa0\x80 x", b"\x80"):
+        with pytest.raises(_ffi.EngineError) as err:
+            t.engine.encode(bad)
+        assert err.value.status == _ffi.TK_E_UTF8
+
+
+def test_device_resident_entry_and_determinism():
+    import torch
+    from toktier_amd import workloads
+    k, t = kit("qwen3_8b"), tok("qwen3_8b")
+    data = workloads.config5(k.json, n_chars=200_000, n_runs=2,
+                             run_chars=10_000).encode()
+    d_text = torch.frombuffer(bytearray(data), dtype=torch.uint8).to("cuda:0")
+    d_ids = torch.empty(len(data), dtype=torch.int32, device="cuda:0")
+    want = k.oracle.encode_bytes(data)
+    for _ in range(3):
+        n = t.engine.encode_device(d_text.data_ptr(), len(data),
+                                   d_ids.data_ptr(), len(data))
+        got = d_ids[:n].cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want)

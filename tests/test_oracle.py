@@ -1,0 +1,244 @@
+"""CPU: pin the oracle (oracle/toktier_oracle.c) before trusting it.
+
+Each check is chosen so that a plausible restatement mistake fails it:
+- table digests equal the reference's pinned sha256 values;
+- published constants of the hash functions (FNV-1a offset basis,
+  SplitMix64's first output) and the reference's own table fixtures
+  (duplicate refusal, load factor, the non-monotone guard example);
+- the split rules against the certified engine's pre-tokenizer offsets by
+  brute force over every short string of an alphabet that reaches every
+  branch of the rules, and over seeded fuzz;
+- full encodes against the committed golden vectors (HF tokenizers 0.22.2
+  on the stand-in artifacts) and against HF directly on larger texts;
+- planted mistakes (a wrong digit group width, the wrong rule set) must
+  make the comparison fail.
+"""
+
+from __future__ import annotations
+
+import itertools
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import FAMILY_NAMES, kit
+from toktier_amd import bpe_tables, classes
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "golden_ids.json"
+
+
+def _golden():
+    return json.loads(GOLDEN.read_text(encoding="utf-8"))
+
+
+# ------------------------------------------------------------- tables
+
+def test_class_table_matches_reference_digest():
+    tab = classes.class_table()  # raises unless the pinned digest matches
+    assert classes.npy_sha256(tab) == classes.CLASS_TABLE_SHA256
+    assert np.bincount(tab, minlength=4).tolist() == [971148, 141028, 1911, 25]
+    assert tab[ord("a")] == 1 and tab[ord("7")] == 2 and tab[ord(" ")] == 3
+    assert tab[ord("!")] == 0 and tab[0x4E2D] == 1 and tab[0xA0] == 3
+
+
+def test_nfc_table_matches_reference_digest():
+    qc = classes.nfc_qc_table()
+    assert classes.npy_sha256(qc) == classes.NFC_QC_SHA256
+    assert qc[ord("a")] == 0 and qc[0xE9] == 0      # precomposed e-acute
+    assert qc[0x301] == 255                          # composes with a base
+    assert qc[0x212B] == 255                         # singleton (Angstrom)
+
+
+def test_fnv1a64_published_constants():
+    assert bpe_tables.fnv1a64(b"") == 0xCBF29CE484222325
+    assert bpe_tables.fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert bpe_tables.fnv1a64(b"foobar") == 0x85944171F73967E8
+
+
+def test_splitmix64_published_first_output():
+    # SplitMix64 seeded with 0 yields 0xE220A8397B1DCDAF first
+    assert bpe_tables.splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+def test_hash_table_shape_and_determinism():
+    keys = list(range(1000))
+    vals = [k * 7 for k in keys]
+    k1, v1 = bpe_tables.build_hash(keys, vals)
+    k2, v2 = bpe_tables.build_hash(keys, vals)
+    assert (k1 == k2).all() and (v1 == v2).all()
+    assert k1.size >= 3 * len(keys) and k1.size & (k1.size - 1) == 0
+    # every key is found by the probe the kernels use
+    mask = k1.size - 1
+    for key, val in zip(keys, vals):
+        i = bpe_tables.splitmix64(key) & mask
+        while int(k1[i]) != key:
+            assert int(k1[i]) != 0xFFFFFFFFFFFFFFFF
+            i = (i + 1) & mask
+        assert int(v1[i]) == val
+
+
+def test_hash_table_refuses_duplicates():
+    with pytest.raises(ValueError, match="duplicate"):
+        bpe_tables.build_hash([5, 5], [1, 2])
+
+
+def test_unsafe_rank_fixtures():
+    # reference fixtures (tests/gpu/test_bpe_tables.py:231-267)
+    assert bpe_tables.unsafe_ranks([["a", "b"], ["ab", "c"]]) == []
+    assert bpe_tables.unsafe_ranks([["xy", "z"], ["x", "y"]]) == [1]
+    assert bpe_tables.unsafe_ranks(["xy z", "x y"]) == [1]
+
+
+def test_byte_level_alphabet():
+    b2u = bpe_tables.bytes_to_unicode()
+    assert len(b2u) == 256 and len(set(b2u.values())) == 256
+    assert b2u[ord("A")] == "A" and b2u[0x20] == "Ġ" and b2u[0x0A] == "Ċ"
+    raw = bytes([0x00, 0x41, 0xC3, 0xA9, 0xFF])
+    assert bpe_tables.token_to_raw("".join(b2u[b] for b in raw)) == raw
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_exported_tables_follow_the_artifact(name):
+    k = kit(name)
+    spec = json.loads(k.json)["model"]
+    t = k.tables
+    assert t.n_merges == len(spec["merges"])
+    assert t.pair_count >= 3 * t.n_merges
+    assert (t.byte_id >= 0).all()
+    assert bool(t.ignore_merges) == k.family.ignore_merges
+
+
+# ------------------------------------------------------- split rules
+
+BRUTE_ALPHABET = ["a", "'", "s", "S", "ſ", "1", " ", "\t", "\r", "\n",
+                  "!", "é", "中", " ", "r", "e"]
+
+
+def _hf_split_starts(kit_, text: str) -> list[int]:
+    pre = kit_.hf.pre_tokenizer
+    offs = [o for _, o in pre.pre_tokenize_str(text)]
+    starts = sorted({len(text[:a].encode("utf-8")) for a, _ in offs})
+    return starts + [len(text.encode("utf-8"))]
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_split_rules_brute_force(name):
+    """Every string of length <= 3 over the alphabet, plus every length-4
+    string over a core subset, splits like the certified engine."""
+    k = kit(name)
+    core = ["a", "'", "s", " ", "\r", "\n", "!", "1", "r"]
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 4)
+         for p in itertools.product(BRUTE_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(core, repeat=4)),
+    )
+    bad = []
+    for s in cases:
+        if k.oracle.pretokenize(s.encode("utf-8")) != _hf_split_starts(k, s):
+            bad.append(s)
+    assert not bad, bad[:10]
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_split_rules_fuzz(name):
+    k = kit(name)
+    rng = np.random.default_rng(5)
+    alpha = BRUTE_ALPHABET + ["d", "m", "t", "l", "v", "L", "E", "T", "2",
+                              "\U0001f600", "-", ".", "　", " "]
+    for _ in range(3000):
+        s = "".join(alpha[int(i)] for i in rng.integers(0, len(alpha), int(rng.integers(1, 30))))
+        assert k.oracle.pretokenize(s.encode("utf-8")) == _hf_split_starts(k, s), s
+
+
+# ------------------------------------------------------------ encodes
+
+def _expected(k, text: str, ids: list[int]):
+    """Oracle result for text; an NFC family's failing quick check is
+    answered by encoding the engine-normalized text, as the facade does."""
+    got = k.oracle.encode_bytes(text.encode("utf-8"))
+    if isinstance(got, int) and k.family.needs_nfc:
+        from tokenizers import normalizers
+        norm = normalizers.NFC().normalize_str(text)
+        got = k.oracle.encode_bytes(norm.encode("utf-8"), normalized=True)
+    return got
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_oracle_matches_golden_vectors(name):
+    g = _golden()["families"][name]
+    k = kit(name)
+    from toktier_amd import standin
+    assert g["artifact_sha256"] == standin.ARTIFACT_SHA256[name]
+    for case in g["cases"]:
+        got = _expected(k, case["text"], case["ids"])
+        assert not isinstance(got, int), (case["text"], got)
+        assert got.tolist() == case["ids"], case["text"]
+
+
+@pytest.mark.parametrize("name", FAMILY_NAMES)
+def test_oracle_matches_hf_on_mixed_text(name):
+    from toktier_amd import workloads
+    k = kit(name)
+    gen = {"qwen3_8b": workloads.config2, "gpt2": workloads.config2,
+           "llama_3_1_8b": workloads.config4}[name]
+    text = gen(k.json, n_chars=200_000)
+    assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
+
+
+def test_oracle_matches_hf_on_cjk_and_long_runs():
+    from toktier_amd import workloads
+    k = kit("qwen3_8b")
+    text = workloads.config5(k.json, n_chars=120_000, n_runs=2, run_chars=8000)
+    assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
+
+
+def test_nfc_quick_check_is_sound():
+    """A passing string is left unchanged by the engine's NFC."""
+    from tokenizers import normalizers
+    k = kit("qwen3_8b")
+    nfc = normalizers.NFC()
+    qc = classes.nfc_qc_table()
+    rng = np.random.default_rng(3)
+    pool = np.nonzero(qc != 255)[0]
+    pool = pool[(pool < 0xD800) | (pool > 0xDFFF)]
+    for _ in range(400):
+        s = "".join(chr(int(c)) for c in rng.choice(pool, size=12))
+        if k.oracle.nfc_qc(s.encode()):
+            assert nfc.normalize_str(s) == s
+    assert not k.oracle.nfc_qc("é".encode())        # composes
+    assert not k.oracle.nfc_qc("ậ"[::-1].encode())
+    assert k.oracle.nfc_qc("café 中文 \U0001f600".encode())
+
+
+# --------------------------------------------------- planted mistakes
+
+def test_planted_wrong_digit_width_is_caught():
+    from oracle.oracle import Oracle
+    k = kit("qwen3_8b")
+    f = k.family
+    wrong = Oracle(k.tables, classes.class_table(), classes.nfc_qc_table(),
+                   f.ruleset, 3, f.needs_nfc)
+    text = "year 2024 and 1234567 units"
+    # the stand-in Qwen vocabulary has no multi-digit tokens, so the ids
+    # cannot tell the groups apart; the split offsets can
+    assert wrong.pretokenize(text.encode()) != _hf_split_starts(k, text)
+    assert k.oracle.pretokenize(text.encode()) == _hf_split_starts(k, text)
+
+
+def test_planted_wrong_ruleset_is_caught():
+    from oracle.oracle import Oracle
+    k = kit("gpt2")
+    f = k.family
+    wrong = Oracle(k.tables, classes.class_table(), None, 0, 1, False)
+    text = "we're 12 'S  \n\n x!y"
+    assert wrong.encode_bytes(text.encode()).tolist() != k.hf_ids(text)
+    assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
+
+
+def test_invalid_utf8_is_refused():
+    k = kit("gpt2")
+    for bad in (b"\xff", b"a\xc3", b"\xc0\x80", b"\xed\xa0\x80", b"\x80abc",
+                b"\xf4\x90\x80\x80"):
+        assert k.oracle.encode_bytes(bad) == -1, bad

@@ -222,13 +222,22 @@ def config5(tokenizer_json: str, n_chars: int = CHARS_4M, sample: int = 0,
         return "".join(out)[:n]
 
     body = n_chars - n_runs * run_chars
+    n_cjk_runs = n_runs // 2
+    # character budgets of the body after the runs' own share: 50% CJK,
+    # 10% emoji, 40% Latin over the whole request
+    want = {"cjk": 0.5 * n_chars - n_cjk_runs * run_chars,
+            "emoji": 0.1 * n_chars,
+            "latin": 0.4 * n_chars - (n_runs - n_cjk_runs) * run_chars}
+    have = {"cjk": 0.0, "emoji": 0.0, "latin": 0.0}
     parts: list[str] = []
     total = 0
     while total < body:
-        r = rng.random()
-        if r < 0.5:
+        # the category furthest below its budget, with a little noise
+        kind = max(want, key=lambda c: (want[c] - have[c]) / max(want[c], 1.0)
+                   + 0.05 * rng.random())
+        if kind == "cjk":
             s = cjk_run(int(rng.integers(4, 60))) + ("\uff0c" if rng.random() < 0.6 else "\u3002")
-        elif r < 0.6:
+        elif kind == "emoji":
             k = int(rng.integers(1, 4))
             em = []
             for _ in range(k):
@@ -241,6 +250,7 @@ def config5(tokenizer_json: str, n_chars: int = CHARS_4M, sample: int = 0,
             s = "".join(em) + " "
         else:
             s = latin.word() + (" " if rng.random() < 0.9 else "\n")
+        have[kind] += len(s)
         parts.append(s)
         total += len(s)
     text = "".join(parts)[:body]
