@@ -159,8 +159,9 @@ def test_full_size_batch_config3_rows():
 
 def test_nfc_fallback_matches_hf():
     k, t = kit("qwen3_8b"), tok("qwen3_8b")
-    texts = ["café au lait", "Å and Å", "ẹ́",
-             "plain ascii", "ẛ̣ 각"]
+    texts = ["cafe\u0301 au lait", "A\u030a and \u212b", "e\u0301\u0323",
+             "plain ascii", "\u1e9b\u0323 \uac00\u11a8",
+             "x" * 70 + "e\u0301" * 40]
     for s in texts:
         assert list(t.encode(s).array) == k.hf_ids(s), s
     rows = t.encode_batch(texts)
