@@ -58,7 +58,21 @@ def main() -> int:
                     help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true",
                     help="skip the per-step oracle parity check")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 10 plain device-to-device copies of MIB "
+                         "MiB (the reference kernel for scaling the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 10}))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on exactly one GPU; "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -141,7 +155,7 @@ def main() -> int:
     n_tok = float(np.mean([a.size for a in ids_dev]))
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
     st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["k_pretok", "k_bpe_small", "k_bpe_queue+k_bpe_long", "k_count+k_scan+k_compact"]
+    names = ["k_pretok", "k_bpe_small", "queued+long pieces (k_bpe_list, k_bpe_wide, k_long_*, k_certify)", "compaction (k_count, k_scan, k_compact)"]
     avg = st[:, :4].mean(axis=0)
     dom = int(np.argmax(avg))
     b_alg = n_bytes + 4.0 * n_tok

@@ -253,8 +253,8 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   HIP_TRY(tk::launch_pretok(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(ev[1], s));
   HIP_TRY(tk::launch_bpe_small(e->t, w, s));
-  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
   if (e->timing) HIP_TRY(hipEventRecord(ev[2], s));
+  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
   HIP_TRY(tk::launch_long_prep(e->t, w, s));
   if (e->t.cert) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s));
