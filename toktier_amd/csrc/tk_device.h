@@ -16,6 +16,18 @@ constexpr uint32_t ST_UTF8 = 1u;     // invalid UTF-8 seen
 constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
 
+// Compact pair table: bijection of the 36-bit pair key (left<<18 | right),
+// shared by the host builder and the device probe.
+constexpr uint64_t MASK36 = (1ULL << 36) - 1;
+constexpr uint32_t CTAB_MAX_DISP = 16;
+__host__ __device__ __forceinline__ uint64_t perm36(uint64_t x) {
+  x = (x * 0x9E3779B97F4A7C15ULL) & MASK36;  // odd multiplier: bijective
+  x ^= x >> 18;                              // xorshift: bijective
+  x = (x * 0xBF58476D1CE4E5B9ULL) & MASK36;
+  x ^= x >> 17;
+  return x;
+}
+
 // Device copies of the family tables, in the engine's own layout.
 struct DevTables {
   const uint8_t* cls;          // [0x110000] P/L/N/S
@@ -35,6 +47,9 @@ struct DevTables {
                                // rank-ordered table, every byte has an id
   const uint32_t* unsafe;      // unsafe-rank bitmap or nullptr
   uint32_t unsafe_words;
+  const uint64_t* ctab;        // compact pair table or nullptr
+  uint64_t cmask;              // buckets - 1
+  uint32_t cbits;              // log2(buckets)
 };
 
 // Per-request device buffers (sized by capacity).

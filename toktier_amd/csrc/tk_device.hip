@@ -44,9 +44,34 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   return x ^ (x >> 31);
 }
 
-// rank<<32 | merged id, or ~0 when the pair has no merge rule
+// rank<<32 | merged id, or ~0 when the pair has no merge rule.
+// The compact table (when the engine built one): 64-byte buckets of eight
+// u64 slots, slot = tag<<41 | displacement<<37 | rank<<18 | id, found by a
+// bijection of the 36-bit key (left<<18 | right); the bucket index is the
+// low bits of the permuted key and the tag the rest, so a slot identifies
+// its key exactly. Small enough to stay in one XCD's L2.
 __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
                                                 uint32_t l, uint32_t r) {
+  if (t.ctab) {
+    if ((l | r) >= (1u << 18)) return ~0ULL;  // every rule's ids fit 18 bits
+    const uint64_t x = perm36(((uint64_t)l << 18) | r);
+    const uint64_t home = x & t.cmask;
+    const uint64_t tag = x >> t.cbits;
+    for (uint32_t d = 0; d < CTAB_MAX_DISP; ++d) {
+      const ulonglong2* b =
+          reinterpret_cast<const ulonglong2*>(t.ctab + (((home + d) & t.cmask) << 3));
+      const ulonglong2 s0 = b[0], s1 = b[1], s2 = b[2], s3 = b[3];
+      const uint64_t sl[8] = {s0.x, s0.y, s1.x, s1.y, s2.x, s2.y, s3.x, s3.y};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint64_t s = sl[k];
+        if (s == ~0ULL) return ~0ULL;
+        if ((s >> 41) == tag && ((s >> 37) & 15) == d)
+          return (((s >> 18) & 0x7FFFF) << 32) | (s & 0x3FFFF);
+      }
+    }
+    return ~0ULL;
+  }
   const uint64_t key = ((uint64_t)l << 32) | r;
   uint64_t i = splitmix64(key) & t.pair_mask;
   for (;;) {

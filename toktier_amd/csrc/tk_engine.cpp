@@ -15,6 +15,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -88,6 +89,52 @@ uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
   return ~0ULL;
 }
 
+// Compact pair table (see pair_lookup in tk_device.hip): 64-byte buckets of
+// eight slots at a load of at most 3/4. Returns false when the artifact
+// does not fit the packing (ids >= 2^18, ranks >= 2^19 - 1); the engine then
+// probes the interleaved boundary table instead.
+bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
+                         uint64_t count, std::vector<uint64_t>& out,
+                         uint32_t& bits) {
+  std::vector<std::pair<uint64_t, uint64_t>> ent;  // (key36, rank<<18|id)
+  for (uint64_t i = 0; i < count; ++i) {
+    if (keys[i] == ~0ULL) continue;
+    const uint64_t l = keys[i] >> 32, r = keys[i] & 0xFFFFFFFFULL;
+    const uint64_t rank = vals[i] >> 32, id = vals[i] & 0xFFFFFFFFULL;
+    if (l >= (1u << 18) || r >= (1u << 18) || id >= (1u << 18) ||
+        rank >= (1u << 19) - 1)
+      return false;
+    ent.push_back({(l << 18) | r, (rank << 18) | id});
+  }
+  std::sort(ent.begin(), ent.end(), [](const auto& a, const auto& b) {
+    return a.second < b.second;
+  });
+  bits = 13;
+  while ((8ULL << bits) * 3 < ent.size() * 4) ++bits;
+  for (; bits <= 22; ++bits) {
+    const uint64_t nbk = 1ULL << bits, mask = nbk - 1;
+    out.assign(nbk * 8, ~0ULL);
+    bool ok = true;
+    for (const auto& e : ent) {
+      const uint64_t x = tk::perm36(e.first);
+      const uint64_t home = x & mask, tag = x >> bits;
+      bool placed = false;
+      for (uint64_t d = 0; d < tk::CTAB_MAX_DISP && !placed; ++d) {
+        uint64_t* b = &out[((home + d) & mask) * 8];
+        for (int k = 0; k < 8; ++k)
+          if (b[k] == ~0ULL) {
+            b[k] = (tag << 41) | (d << 37) | e.second;
+            placed = true;
+            break;
+          }
+      }
+      if (!placed) { ok = false; break; }
+    }
+    if (ok) return true;
+  }
+  return false;
+}
+
 }  // namespace
 
 struct tk_engine {
@@ -99,7 +146,7 @@ struct tk_engine {
   // tables
   DevBuf<uint8_t> cls, nfc, blob;
   DevBuf<ulonglong2> pairs, vocab;
-  DevBuf<uint64_t> bytepair;
+  DevBuf<uint64_t> bytepair, ctab;
   DevBuf<int32_t> byte_id;
   std::vector<uint8_t> host_nfc;
   tk::DevTables t{};
@@ -484,6 +531,17 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   for (size_t i = 0; i < unsafe_len / 4; ++i) cert = cert && unsafe_bits[i] == 0;
   for (int b = 0; b < 256; ++b) cert = cert && byte_id[b] >= 0;
   e->t.cert = cert ? 1 : 0;
+  e->t.ctab = nullptr;
+  {
+    std::vector<uint64_t> ct;
+    uint32_t bits = 0;
+    if (build_compact_pairs(pair_keys, pair_vals, n_pairs, ct, bits)) {
+      if ((rc = up(e->ctab, ct.data(), ct.size())) != TK_OK) return bail(rc);
+      e->t.ctab = e->ctab.p;
+      e->t.cmask = (1ULL << bits) - 1;
+      e->t.cbits = bits;
+    }
+  }
   e->t.unsafe = nullptr;
   e->t.unsafe_words = 0;
   if (!cert && unsafe_len >= 4) {
