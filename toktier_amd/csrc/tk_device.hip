@@ -45,11 +45,12 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
 }
 
 // rank<<32 | merged id, or ~0 when the pair has no merge rule.
-// The compact table (when the engine built one): 64-byte buckets of eight
+// The compact table (when the engine built one): 16-byte buckets of two
 // u64 slots, slot = tag<<41 | displacement<<37 | rank<<18 | id, found by a
 // bijection of the 36-bit key (left<<18 | right); the bucket index is the
 // low bits of the permuted key and the tag the rest, so a slot identifies
-// its key exactly. Small enough to stay in one XCD's L2.
+// its key exactly. One 16-byte load per bucket, as the boundary table,
+// in a table a quarter of its size (it stays in one XCD's L2).
 __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
                                                 uint32_t l, uint32_t r) {
   if (t.ctab) {
@@ -57,18 +58,15 @@ __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
     const uint64_t x = perm36(((uint64_t)l << 18) | r);
     const uint64_t home = x & t.cmask;
     const uint64_t tag = x >> t.cbits;
-    for (uint32_t d = 0; d < CTAB_MAX_DISP; ++d) {
-      const ulonglong2* b =
-          reinterpret_cast<const ulonglong2*>(t.ctab + (((home + d) & t.cmask) << 3));
-      const ulonglong2 s0 = b[0], s1 = b[1], s2 = b[2], s3 = b[3];
-      const uint64_t sl[8] = {s0.x, s0.y, s1.x, s1.y, s2.x, s2.y, s3.x, s3.y};
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint64_t s = sl[k];
-        if (s == ~0ULL) return ~0ULL;
-        if ((s >> 41) == tag && ((s >> 37) & 15) == d)
-          return (((s >> 18) & 0x7FFFF) << 32) | (s & 0x3FFFF);
-      }
+    const ulonglong2* tab = reinterpret_cast<const ulonglong2*>(t.ctab);
+    for (uint64_t d = 0; d < CTAB_MAX_DISP; ++d) {
+      const ulonglong2 b = tab[(home + d) & t.cmask];
+      const uint64_t want = (tag << 41) | (d << 37);
+      // (an empty slot is all ones; test it first so it can never match)
+      if (b.x == ~0ULL) return ~0ULL;
+      if ((b.x & ~0x1FFFFFFFFFULL) == want) return (((b.x >> 18) & 0x7FFFF) << 32) | (b.x & 0x3FFFF);
+      if (b.y == ~0ULL) return ~0ULL;
+      if ((b.y & ~0x1FFFFFFFFFULL) == want) return (((b.y >> 18) & 0x7FFFF) << 32) | (b.y & 0x3FFFF);
     }
     return ~0ULL;
   }
@@ -398,10 +396,10 @@ __device__ __forceinline__ uint64_t lanes_in(int lo, int hi) {  // [lo, hi)
 //   write: store the ids (token id at its first byte, INVALID_ID at the
 //     other bytes of the segment) into tok.
 // Returns the final mask of lanes that start a token.
+template <bool vocab_first, bool hist, bool write>
 __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
                              int64_t base, int lane, bool elig, int ps,
-                             int pe, bool vocab_first, bool hist,
-                             bool write) {
+                             int pe) {
   const int64_t pos = base + lane;
   const uint32_t byte = elig ? w.text[pos] : 0u;
   const int32_t bid = elig ? t.byte_id[byte] : -1;
@@ -563,7 +561,7 @@ __global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
       if (!fits_a_grid(pos, b))
         push_pair(w.longlist, w.longcount, w.long_cap, w.status, pos, b);
     }
-    wave_bpe(t, w, base, lane, elig, ps, pe, true, false, true);
+    wave_bpe<true, false, true>(t, w, base, lane, elig, ps, pe);
   }
 }
 
@@ -590,7 +588,8 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
     if (len > 64) continue;  // wave-uniform
-    wave_bpe(t, w, (int64_t)a, lane, lane < len, 0, len, !hist, hist != 0, true);
+    if (hist) wave_bpe<false, true, true>(t, w, (int64_t)a, lane, lane < len, 0, len);
+    else wave_bpe<true, false, true>(t, w, (int64_t)a, lane, lane < len, 0, len);
   }
 }
 
@@ -1003,8 +1002,8 @@ __global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
     const uint64_t gt = S & ~mask_le(lane);
     const int pe = gt ? __builtin_ctzll(gt) : 64;
     const bool elig = (L >> lane) & 1;
-    const uint64_t live = wave_bpe(t, w, base, lane, elig, ps, pe, false,
-                                   false, false);
+    const uint64_t live =
+        wave_bpe<false, false, false>(t, w, base, lane, elig, ps, pe);
     if (lane == 0) {
       if (phase == 0) {
         cut16[4 * v + 1] = (uint16_t)(live >> 16);
@@ -1059,7 +1058,7 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
       if (!fits_a_grid(pos, b))
         push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
     }
-    wave_bpe(t, w, base, lane, elig, ps, pe, false, true, true);
+    wave_bpe<false, true, true>(t, w, base, lane, elig, ps, pe);
   }
 }
 
@@ -1217,17 +1216,19 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total)
   return off + inc - v;
 }
 
+// Token slots are read lane-interleaved (consecutive lanes, consecutive
+// bytes) so every load and every output store of a wave is contiguous.
 __global__ __launch_bounds__(COMPACT_TPB) void k_count(DevWork w, int64_t nblk) {
-  const int64_t blk = blockIdx.x;
-  const int64_t p0 = blk * COMPACT_BLOCK + (int64_t)threadIdx.x * COMPACT_PER_THREAD;
+  const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
   uint32_t c = 0;
+#pragma unroll
   for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
-    const int64_t p = p0 + k;
+    const int64_t p = base + (int64_t)k * COMPACT_TPB;
     if (p < w.nb && w.tok[p] != INVALID_ID) ++c;
   }
   uint32_t tot;
   block_excl_scan(c, &tot);
-  if (threadIdx.x == 0) w.blkcount[blk] = tot;
+  if (threadIdx.x == 0) w.blkcount[blockIdx.x] = tot;
 }
 
 __global__ __launch_bounds__(1024) void k_scan(DevWork w, int64_t nblk) {
@@ -1253,21 +1254,27 @@ __global__ __launch_bounds__(1024) void k_scan(DevWork w, int64_t nblk) {
 }
 
 __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w) {
-  const int64_t blk = blockIdx.x;
-  const int64_t p0 = blk * COMPACT_BLOCK + (int64_t)threadIdx.x * COMPACT_PER_THREAD;
-  uint32_t c = 0;
+  __shared__ uint32_t wsum[COMPACT_TPB / 64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
+  uint32_t run = w.blkprefix[blockIdx.x];
   for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
-    const int64_t p = p0 + k;
-    if (p < w.nb && w.tok[p] != INVALID_ID) ++c;
-  }
-  uint32_t tot;
-  uint32_t off = block_excl_scan(c, &tot) + w.blkprefix[blk];
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
-    const int64_t p = p0 + k;
-    if (p < w.nb) {
-      const uint32_t v = w.tok[p];
-      if (v != INVALID_ID) w.out[off++] = v;
+    const int64_t p = base + (int64_t)k * COMPACT_TPB;
+    const uint32_t v = p < w.nb ? w.tok[p] : INVALID_ID;
+    const bool keep = v != INVALID_ID;
+    const uint64_t m = __ballot(keep);
+    if (lane == 0) wsum[wv] = (uint32_t)__popcll(m);
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (int q = 0; q < COMPACT_TPB / 64; ++q) {
+      if (q < wv) before += wsum[q];
+      total += wsum[q];
     }
+    if (keep)
+      w.out[run + before + (uint32_t)__popcll(m & ((1ULL << lane) - 1))] = v;
+    run += total;
+    __syncthreads();
   }
 }
 

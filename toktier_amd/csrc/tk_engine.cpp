@@ -89,8 +89,8 @@ uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
   return ~0ULL;
 }
 
-// Compact pair table (see pair_lookup in tk_device.hip): 64-byte buckets of
-// eight slots at a load of at most 3/4. Returns false when the artifact
+// Compact pair table (see pair_lookup in tk_device.hip): 16-byte buckets of
+// two slots at a load of at most 0.6. Returns false when the artifact
 // does not fit the packing (ids >= 2^18, ranks >= 2^19 - 1); the engine then
 // probes the interleaved boundary table instead.
 bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
@@ -110,18 +110,18 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
     return a.second < b.second;
   });
   bits = 13;
-  while ((8ULL << bits) * 3 < ent.size() * 4) ++bits;
+  while ((2ULL << bits) * 6 < ent.size() * 10) ++bits;
   for (; bits <= 22; ++bits) {
     const uint64_t nbk = 1ULL << bits, mask = nbk - 1;
-    out.assign(nbk * 8, ~0ULL);
+    out.assign(nbk * 2, ~0ULL);
     bool ok = true;
     for (const auto& e : ent) {
       const uint64_t x = tk::perm36(e.first);
       const uint64_t home = x & mask, tag = x >> bits;
       bool placed = false;
       for (uint64_t d = 0; d < tk::CTAB_MAX_DISP && !placed; ++d) {
-        uint64_t* b = &out[((home + d) & mask) * 8];
-        for (int k = 0; k < 8; ++k)
+        uint64_t* b = &out[((home + d) & mask) * 2];
+        for (int k = 0; k < 2; ++k)
           if (b[k] == ~0ULL) {
             b[k] = (tag << 41) | (d << 37) | e.second;
             placed = true;
