@@ -90,7 +90,6 @@ struct DevWork {
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_WORDS = 16;
 
-constexpr int PRETOK_BYTES_PER_THREAD = 16;
 constexpr int PRETOK_TPB = 256;
 constexpr int COMPACT_TPB = 256;
 constexpr int COMPACT_PER_THREAD = 16;

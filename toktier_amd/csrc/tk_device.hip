@@ -110,22 +110,11 @@ __device__ __forceinline__ int fold(int32_t c) {
   return c;
 }
 
-struct PCtx {
-  const uint8_t* t;
-  int64_t nb;
-  const uint64_t* dm;
-  const uint8_t* cls;
-};
-
-__device__ __forceinline__ bool is_ds(const PCtx& c, int64_t i) {
-  if (i == 0) return true;
-  return c.dm && ((c.dm[i >> 6] >> (i & 63)) & 1);
-}
-
-// Decode the character that starts at byte i (i < nb, not a continuation
-// byte). *ok is false for any invalid form; the value is then U+FFFD.
-__device__ int32_t decode_full(const PCtx& c, int64_t i, bool* ok) {
-  const uint32_t b0 = c.t[i];
+// Decode the character whose first bytes are b0..b3, `avail` of them inside
+// the text. *ok is false for any invalid form; the value is then U+FFFD.
+__device__ __forceinline__ int32_t decode4(uint32_t b0, uint32_t b1,
+                                           uint32_t b2, uint32_t b3,
+                                           int64_t avail, bool* ok) {
   int need;
   uint32_t v;
   if (b0 < 0x80) { *ok = true; return (int32_t)b0; }
@@ -135,9 +124,8 @@ __device__ int32_t decode_full(const PCtx& c, int64_t i, bool* ok) {
   else if (b0 < 0xF8) { need = 3; v = b0 & 0x07; }
   else { *ok = false; return 0xFFFD; }
   for (int k = 1; k <= need; ++k) {
-    if (i + k >= c.nb) { *ok = false; return 0xFFFD; }
-    const uint32_t x = c.t[i + k];
-    if ((x & 0xC0) != 0x80) { *ok = false; return 0xFFFD; }
+    const uint32_t x = k == 1 ? b1 : k == 2 ? b2 : b3;
+    if (k >= avail || (x & 0xC0) != 0x80) { *ok = false; return 0xFFFD; }
     v = (v << 6) | (x & 0x3F);
   }
   if ((need == 1 && v < 0x80) || (need == 2 && v < 0x800) ||
@@ -150,61 +138,131 @@ __device__ int32_t decode_full(const PCtx& c, int64_t i, bool* ok) {
   return (int32_t)v;
 }
 
-__device__ __forceinline__ int32_t decode_cp(const PCtx& c, int64_t i) {
-  bool ok;
-  return decode_full(c, i, &ok);
-}
-
 struct Ch {
   int64_t pos;
   int32_t cp;
   uint8_t cl;
 };
 
-__device__ __forceinline__ Ch char_at(const PCtx& c, int64_t p) {
-  const int32_t cp = decode_cp(c, p);
-  return Ch{p, cp, c.cls[cp]};
-}
+// Positions are byte offsets into the request; a character is named by the
+// byte where it starts. A context answers four questions for the split
+// predicates: does a document start at i, where does the previous / next
+// character start, which character (code point, class) is at p.
+// GCtx reads the request in HBM.
+struct GCtx {
+  const uint8_t* t;
+  int64_t nb;
+  const uint64_t* dm;  // document-start bits or nullptr
+  const uint8_t* cls;
 
-// start of the character before the one at p; -1 if p starts a document
-__device__ __forceinline__ int64_t prev_pos(const PCtx& c, int64_t p) {
-  if (is_ds(c, p)) return -1;
-  int64_t q = p - 1;
-  int k = 0;
-  while (q > 0 && k < 3 && is_cont(c.t[q])) { --q; ++k; }
-  return q;
-}
+  __device__ __forceinline__ bool ds(int64_t i) const {
+    if (i == 0) return true;
+    return dm && ((dm[i >> 6] >> (i & 63)) & 1);
+  }
+  __device__ __forceinline__ int32_t cp_at(int64_t i, bool* ok) const {
+    const int64_t a = nb - i;
+    return decode4(t[i], a > 1 ? t[i + 1] : 0, a > 2 ? t[i + 2] : 0,
+                   a > 3 ? t[i + 3] : 0, a, ok);
+  }
+  __device__ __forceinline__ Ch at(int64_t p) const {
+    bool ok;
+    const int32_t cp = cp_at(p, &ok);
+    return Ch{p, cp, cls[cp]};
+  }
+  // start of the character before the one at p; -1 if p starts a document
+  __device__ __forceinline__ int64_t prev(int64_t p) const {
+    if (ds(p)) return -1;
+    int64_t q = p - 1;
+    int k = 0;
+    while (q > 0 && k < 3 && is_cont(t[q])) { --q; ++k; }
+    return q;
+  }
+  // start of the character after the one at p; -1 at text / document end
+  __device__ __forceinline__ int64_t next(int64_t p) const {
+    int64_t q = p + 1;
+    int k = 0;
+    while (q < nb && k < 3 && is_cont(t[q])) { ++q; ++k; }
+    if (q >= nb || ds(q)) return -1;
+    return q;
+  }
+};
 
-// start of the character after the one at p; -1 at text / document end
-__device__ __forceinline__ int64_t next_pos(const PCtx& c, int64_t p) {
-  int64_t q = p + 1;
-  int k = 0;
-  while (q < c.nb && k < 3 && is_cont(c.t[q])) { ++q; ++k; }
-  if (q >= c.nb || is_ds(c, q)) return -1;
-  return q;
-}
+// Pretokenize tiles: a block stages PT_TILE bytes plus PT_PAD bytes each
+// side in LDS and decodes one entry per byte position for the tile plus
+// PT_HALO positions each side:
+//   bits  0..20 code point (decode at that byte; U+FFFD if invalid there)
+//   bits 21..22 class
+//   bits 23..24 back: prev(p) = p - 1 - back(p - 1)
+//   bits 25..26 fwd:  next(p) = p + 1 + fwd(p) (before the end checks)
+//   bit  27     the decode at p is valid UTF-8
+constexpr int PT_TILE = 4096;
+constexpr int PT_HALO = 64;
+constexpr int PT_SPAN = PT_TILE + 2 * PT_HALO;
+constexpr int PT_PAD = 80;  // >= PT_HALO + 4, a multiple of 16
+constexpr int PT_BYTES = PT_TILE + 2 * PT_PAD;
+constexpr int PT_DMW = PT_TILE / 64 + 6;  // doc-mask words from tile word - 3
+
+// LCtx answers from a block's LDS tile and falls back to GCtx for
+// positions outside it (long digit / whitespace runs, rare).
+struct LCtx {
+  GCtx g;
+  const uint32_t* se;  // entries of positions [lo, lo + PT_SPAN)
+  int64_t lo;
+  const uint64_t* sdm;  // doc-mask words [wlo, wlo + PT_DMW)
+  int64_t wlo;
+
+  __device__ __forceinline__ bool in(int64_t p) const {
+    return (uint64_t)(p - lo) < (uint64_t)PT_SPAN;
+  }
+  __device__ __forceinline__ bool ds(int64_t i) const {
+    if (i == 0) return true;
+    if (!g.dm) return false;
+    const int64_t k = (i >> 6) - wlo;
+    if ((uint64_t)k < (uint64_t)PT_DMW) return (sdm[k] >> (i & 63)) & 1;
+    return g.ds(i);
+  }
+  __device__ __forceinline__ Ch at(int64_t p) const {
+    if (!in(p)) return g.at(p);
+    const uint32_t e = se[p - lo];
+    return Ch{p, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+  }
+  __device__ __forceinline__ int64_t prev(int64_t p) const {
+    if (ds(p)) return -1;
+    const int64_t q = p - 1;
+    if (!in(q)) return g.prev(p);
+    return q - ((se[q - lo] >> 23) & 3);
+  }
+  __device__ __forceinline__ int64_t next(int64_t p) const {
+    if (!in(p)) return g.next(p);
+    const int64_t q = p + 1 + ((se[p - lo] >> 25) & 3);
+    if (q >= g.nb || ds(q)) return -1;
+    return q;
+  }
+};
 
 // Is the apostrophe (or other P char) at q the start of a regex match?
 // It is unless it continues a P run or follows a U+0020 that the
 // " ?[^\s\p{L}\p{N}]+" alternative takes with it.
-__device__ __forceinline__ bool p_arrives(const PCtx& c, int64_t q) {
-  const int64_t r = prev_pos(c, q);
+template <class C>
+__device__ __forceinline__ bool p_arrives(const C& c, int64_t q) {
+  const int64_t r = c.prev(q);
   if (r < 0) return true;
-  const Ch x = char_at(c, r);
+  const Ch x = c.at(r);
   return x.cl != CP_ && x.cp != ' ';
 }
 
 // ---- cl100k (Qwen2 / Llama-3) piece-start predicate for a character
 // that does not start a document.
-__device__ bool start_cl100k(const PCtx& c, const Ch& ci, int dmax) {
-  const Ch p1 = char_at(c, prev_pos(c, ci.pos));
+template <class C>
+__device__ bool start_cl100k(const C& c, const Ch& ci, int dmax) {
+  const Ch p1 = c.at(c.prev(ci.pos));
   if (ci.cl == CN_) {
     // \p{N}{1,K}: digit runs split into groups of K from the run start
     if (dmax <= 1) return true;
     int64_t n = 0;
     for (int64_t q = ci.pos;;) {
-      const int64_t r = prev_pos(c, q);
-      if (r < 0 || char_at(c, r).cl != CN_) break;
+      const int64_t r = c.prev(q);
+      if (r < 0 || c.at(r).cl != CN_) break;
       ++n;
       q = r;
     }
@@ -221,18 +279,18 @@ __device__ bool start_cl100k(const PCtx& c, const Ch& ci, int dmax) {
       return true;
     }
     // inside a letter run: only a contraction match can end here
-    const int64_t q2 = prev_pos(c, p1.pos);
+    const int64_t q2 = c.prev(p1.pos);
     if (q2 < 0) return false;
-    const Ch p2 = char_at(c, q2);
+    const Ch p2 = c.at(q2);
     if (p2.cp == '\'') {
       const int f1 = fold(p1.cp);
       return (f1 == 's' || f1 == 't' || f1 == 'm' || f1 == 'd') &&
              p_arrives(c, q2);
     }
     if (p2.cl != CL_) return false;
-    const int64_t q3 = prev_pos(c, q2);
+    const int64_t q3 = c.prev(q2);
     if (q3 < 0) return false;
-    if (char_at(c, q3).cp != '\'') return false;
+    if (c.at(q3).cp != '\'') return false;
     const int f1 = fold(p2.cp), f2 = fold(p1.cp);
     return ((f1 == 'r' && f2 == 'e') || (f1 == 'v' && f2 == 'e') ||
             (f1 == 'l' && f2 == 'l')) &&
@@ -246,17 +304,17 @@ __device__ bool start_cl100k(const PCtx& c, const Ch& ci, int dmax) {
   if (cr_1 && !cr_i) {
     // right after the last CR/LF of the run (end of \s*[\r\n]+) ...
     bool more = false;
-    for (int64_t q = next_pos(c, ci.pos); q >= 0; q = next_pos(c, q)) {
-      const Ch x = char_at(c, q);
+    for (int64_t q = c.next(ci.pos); q >= 0; q = c.next(q)) {
+      const Ch x = c.at(q);
       if (x.cl != CS_) break;
       if (crlf(x.cp)) { more = true; break; }
     }
     if (!more) return true;
     // ... or the first char the P match's [\r\n]* left over
     for (int64_t q = p1.pos;;) {
-      const int64_t r = prev_pos(c, q);
+      const int64_t r = c.prev(q);
       if (r < 0) return false;
-      const Ch x = char_at(c, r);
+      const Ch x = c.at(r);
       if (x.cl != CS_) return x.cl == CP_;
       if (!crlf(x.cp)) return false;
       q = r;
@@ -264,19 +322,20 @@ __device__ bool start_cl100k(const PCtx& c, const Ch& ci, int dmax) {
   }
   if (!cr_1 && !cr_i) {
     // \s+(?!\S) backs off one char before a non-space (not at text end)
-    const int64_t q = next_pos(c, ci.pos);
-    return q >= 0 && char_at(c, q).cl != CS_;
+    const int64_t q = c.next(ci.pos);
+    return q >= 0 && c.at(q).cl != CS_;
   }
   return false;
 }
 
 // ---- r50k (GPT-2) piece-start predicate.
-__device__ bool start_r50k(const PCtx& c, const Ch& ci) {
-  const Ch p1 = char_at(c, prev_pos(c, ci.pos));
+template <class C>
+__device__ bool start_r50k(const C& c, const Ch& ci) {
+  const Ch p1 = c.at(c.prev(ci.pos));
   if (ci.cl == CS_) {
     if (p1.cl != CS_) return true;
-    const int64_t q = next_pos(c, ci.pos);
-    return q >= 0 && char_at(c, q).cl != CS_;
+    const int64_t q = c.next(ci.pos);
+    return q >= 0 && c.at(q).cl != CS_;
   }
   if (ci.cl == CN_ || ci.cl == CP_) {
     if (p1.cl == ci.cl) return false;
@@ -287,9 +346,9 @@ __device__ bool start_r50k(const PCtx& c, const Ch& ci) {
     if (p1.cp == '\'' && p_arrives(c, p1.pos)) {
       const int a = ci.cp;
       if (a == 's' || a == 't' || a == 'm' || a == 'd') return false;
-      const int64_t qn = next_pos(c, ci.pos);
+      const int64_t qn = c.next(ci.pos);
       if (qn >= 0) {
-        const int b = char_at(c, qn).cp;
+        const int b = c.at(qn).cp;
         if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
             (a == 'l' && b == 'l'))
           return false;
@@ -297,16 +356,16 @@ __device__ bool start_r50k(const PCtx& c, const Ch& ci) {
     }
     return true;
   }
-  const int64_t q2 = prev_pos(c, p1.pos);
+  const int64_t q2 = c.prev(p1.pos);
   if (q2 < 0) return false;
-  const Ch p2 = char_at(c, q2);
+  const Ch p2 = c.at(q2);
   if (p2.cp == '\'') {
     const int a = p1.cp;
     return (a == 's' || a == 't' || a == 'm' || a == 'd') && p_arrives(c, q2);
   }
   if (p2.cl != CL_) return false;
-  const int64_t q3 = prev_pos(c, q2);
-  if (q3 < 0 || char_at(c, q3).cp != '\'') return false;
+  const int64_t q3 = c.prev(q2);
+  if (q3 < 0 || c.at(q3).cp != '\'') return false;
   const int a = p2.cp, b = p1.cp;
   return ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
           (a == 'l' && b == 'l')) &&
@@ -315,61 +374,114 @@ __device__ bool start_r50k(const PCtx& c, const Ch& ci) {
 
 // ------------------------------------------------------ 1. pretokenize
 
+// One block per PT_TILE bytes (64 start words). Stage the bytes, decode
+// every position of the tile and its halo into LDS entries, then each wave
+// takes one 64-byte word at a time, lane = byte, and ballots the start bits
+// into the word.
 __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
-                                                       int64_t cover) {
-  const int64_t g = (int64_t)blockIdx.x * PRETOK_TPB + threadIdx.x;
-  const int64_t base = g * PRETOK_BYTES_PER_THREAD;
-  if (base >= cover) return;
-  const PCtx c{w.text, w.nb, w.docmask, t.cls};
-  uint32_t bits = 0, st = 0;
-  for (int k = 0; k < PRETOK_BYTES_PER_THREAD; ++k) {
-    const int64_t i = base + k;
-    if (i >= w.nb) { bits |= 1u << k; continue; }  // sentinel starts
-    const uint8_t b = w.text[i];
-    if (is_cont(b)) {
-      // a continuation byte must be claimed by a lead at most 3 back
-      int64_t q = i - 1;
-      int back = 1;
-      while (q >= 0 && back <= 3 && is_cont(w.text[q])) { --q; ++back; }
-      bool ok = false;
-      if (q >= 0 && back <= 3) {
-        const uint8_t l = w.text[q];
-        const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2
-                       : l >= 0xC0 ? 1 : 0;
-        ok = need >= back;
+                                                       int64_t nwords) {
+  __shared__ __align__(16) uint8_t sb[PT_BYTES];
+  __shared__ uint32_t se[PT_SPAN];
+  __shared__ uint64_t sdm[PT_DMW];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * PT_TILE;
+  const int64_t nb = w.nb;
+  const bool al = ((uintptr_t)w.text & 15) == 0;
+  for (int j = tid; j < PT_BYTES / 16; j += PRETOK_TPB) {
+    const int64_t p = base - PT_PAD + 16 * j;
+    uint4 v;
+    if (al && p >= 0 && p + 16 <= nb) {
+      v = *reinterpret_cast<const uint4*>(w.text + p);
+    } else {
+      uint32_t x[4] = {0, 0, 0, 0};
+      for (int k = 0; k < 16; ++k) {
+        const int64_t q = p + k;
+        if (q >= 0 && q < nb) x[k >> 2] |= (uint32_t)w.text[q] << (8 * (k & 3));
       }
-      if (!ok) st |= ST_UTF8;
-      continue;
+      v = make_uint4(x[0], x[1], x[2], x[3]);
     }
-    bool ok;
-    const int32_t cp = decode_full(c, i, &ok);
-    if (!ok) st |= ST_UTF8;
-    const Ch ci{i, cp, t.cls[cp]};
-    const bool ds = is_ds(c, i);
-    bool s = ds;
-    if (!ds) s = t.ruleset == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
-    if (s) bits |= 1u << k;
-    if (w.check_nfc) {
-      const uint8_t v = t.nfc[cp];
-      if (v == 255) {
-        st |= ST_NFC;
-      } else if (v != 0 && !ds) {
-        const uint8_t pv = t.nfc[decode_cp(c, prev_pos(c, i))];
-        if (pv > v) st |= ST_NFC;
-      }
+    *reinterpret_cast<uint4*>(sb + 16 * j) = v;
+  }
+  const int64_t wlo = (base >> 6) - 3;
+  if (w.docmask) {
+    const int64_t nmw = nb / 64 + 2;  // words the caller's mask holds
+    for (int j = tid; j < PT_DMW; j += PRETOK_TPB) {
+      const int64_t wd = wlo + j;
+      sdm[j] = (wd >= 0 && wd < nmw) ? w.docmask[wd] : 0;
     }
   }
-  reinterpret_cast<uint16_t*>(w.starts)[g] = (uint16_t)bits;
+  __syncthreads();
+  const int64_t lo = base - PT_HALO;
+  for (int j = tid; j < PT_SPAN; j += PRETOK_TPB) {
+    const int64_t p = lo + j;
+    const int sj = j + (PT_PAD - PT_HALO);  // byte p in sb
+    uint32_t e = 0;
+    if (p >= 0 && p < nb) {
+      int back = 0, fwd = 0;
+      for (int64_t q = p; q > 0 && back < 3 && is_cont(sb[sj - back]); --q) ++back;
+      while (p + 1 + fwd < nb && fwd < 3 && is_cont(sb[sj + 1 + fwd])) ++fwd;
+      bool ok;
+      const int32_t cp = decode4(sb[sj], sb[sj + 1], sb[sj + 2], sb[sj + 3],
+                                 nb - p, &ok);
+      e = (uint32_t)cp | ((uint32_t)t.cls[cp] << 21) | ((uint32_t)back << 23) |
+          ((uint32_t)fwd << 25) | (ok ? 1u << 27 : 0u);
+    }
+    se[j] = e;
+  }
+  __syncthreads();
+  const LCtx c{GCtx{w.text, nb, w.docmask, t.cls}, se, lo, sdm, wlo};
+  const int lane = tid & 63, wv = tid >> 6;
+  uint32_t st = 0;
+  for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
+    const int64_t wd = (base >> 6) + k;
+    if (wd >= nwords) break;
+    const int64_t i = base + 64 * k + lane;
+    const int sj = 64 * k + lane + PT_PAD;
+    bool s = true;  // sentinel starts past the text
+    if (i < nb) {
+      const uint8_t b = sb[sj];
+      if (is_cont(b)) {
+        // a continuation byte must be claimed by a lead at most 3 back
+        int back = 1;
+        while (i - back >= 0 && back <= 3 && is_cont(sb[sj - back])) ++back;
+        bool ok = false;
+        if (i - back >= 0 && back <= 3) {
+          const uint8_t l = sb[sj - back];
+          const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2
+                         : l >= 0xC0 ? 1 : 0;
+          ok = need >= back;
+        }
+        if (!ok) st |= ST_UTF8;
+        s = false;
+      } else {
+        const uint32_t e = se[i - lo];
+        if (!((e >> 27) & 1)) st |= ST_UTF8;
+        const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+        const bool ds = c.ds(i);
+        s = ds || (t.ruleset == 1 ? start_r50k(c, ci)
+                                  : start_cl100k(c, ci, t.dmax));
+        if (w.check_nfc) {
+          const uint8_t v = t.nfc[ci.cp];
+          if (v == 255) {
+            st |= ST_NFC;
+          } else if (v != 0 && !ds) {
+            if (t.nfc[c.at(c.prev(i)).cp] > v) st |= ST_NFC;
+          }
+        }
+      }
+    }
+    const uint64_t m = __ballot(s);
+    if (lane == 0) w.starts[wd] = m;
+  }
   if (st) atomicOr(w.status, st);
 }
 
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s) {
   const int64_t nwin = (w.nb + 63) / 64;
-  const int64_t cover = (nwin + 2) * 64;  // words 0..nwin+1
-  const int64_t threads = cover / PRETOK_BYTES_PER_THREAD;
-  const int64_t blocks = (threads + PRETOK_TPB - 1) / PRETOK_TPB;
+  const int64_t nwords = nwin + 2;  // words 0..nwin+1
+  const int64_t blocks = (nwords * 64 + PT_TILE - 1) / PT_TILE;
   hipLaunchKernelGGL(k_pretok, dim3((uint32_t)blocks), dim3(PRETOK_TPB), 0, s,
-                     t, w, cover);
+                     t, w, nwords);
   return hipGetLastError();
 }
 
@@ -383,6 +495,17 @@ __device__ __forceinline__ uint64_t lanes_in(int lo, int hi) {  // [lo, hi)
   const uint64_t up = hi >= 64 ? ~0ULL : ((1ULL << hi) - 1);
   return up & ~((1ULL << lo) - 1);
 }
+
+// lane i receives lane i + d of its row of 16; lanes whose source lies past
+// the row end receive RANK_INF
+template <int d>
+__device__ __forceinline__ uint32_t dpp_shl(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)RANK_INF, (int)v, 0x100 + d,
+                                               0xF, 0xF, false);
+}
+
+constexpr uint32_t SYM_ID = 0xFFFFF;      // token id bits of a packed symbol
+constexpr uint32_t SYM_BYTE = 1u << 28;   // the symbol is still one raw byte
 
 // Byte-level BPE of every eligible segment held by one wave, lane = byte
 // at base + lane; ps/pe: the lane's segment as lanes [ps, pe). Each round
@@ -405,8 +528,10 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
   const int32_t bid = elig ? t.byte_id[byte] : -1;
   uint64_t live = __ballot(bid >= 0);
   if (!__any(elig)) return 0;
-  uint32_t sym = (uint32_t)bid;
-  int isb = 1;
+  // The lane's symbol in one word for a single cross-lane read: token id
+  // (ids fit 20 bits in every table), the raw byte, and SYM_BYTE while the
+  // symbol is still that one byte.
+  uint32_t sym = (uint32_t)bid | (byte << 20) | SYM_BYTE;
   const int src_ps = ps >= 0 ? ps : lane;
 
   if (vocab_first && t.ignore_merges) {
@@ -417,9 +542,30 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     const uint64_t hm = __ballot(hit >= 0);
     const int32_t hid = __shfl(hit, src_ps);
     const bool phit = elig && ((hm >> src_ps) & 1);
-    if (phit && lane == ps) { sym = (uint32_t)hid; isb = 0; }
+    if (phit && lane == ps) sym = (uint32_t)hid;
     live &= ~__ballot(phit && lane != ps);
   }
+
+  // Segment geometry, fixed for the call. starts/ends: first and last lane
+  // of every segment. blkN: all ones unless lane + N is in the lane's own
+  // segment and row of 16 (OR-ed into what the DPP step reads, so the
+  // shifts run on the full wave and never read a masked-off lane); rowN:
+  // the lane sits before lane N and its segment runs past it.
+  const uint64_t starts = __ballot(lane == ps);
+  const uint64_t ends = __ballot(ps >= 0 && lane == pe - 1);
+  const uint64_t cut = starts | (ends << 1);
+  const uint64_t in1 = ~((cut >> 1) | (1ULL << 63));  // no cut in (i, i+1]
+  const uint64_t in2 = in1 & (in1 >> 1);
+  const uint64_t in4 = in2 & (in2 >> 2);
+  const uint64_t in8 = in4 & (in4 >> 4);
+  const int col = lane & 15;
+  const uint32_t blk1 = (col + 1 < 16 && ((in1 >> lane) & 1)) ? 0u : ~0u;
+  const uint32_t blk2 = (col + 2 < 16 && ((in2 >> lane) & 1)) ? 0u : ~0u;
+  const uint32_t blk4 = (col + 4 < 16 && ((in4 >> lane) & 1)) ? 0u : ~0u;
+  const uint32_t blk8 = (col + 8 < 16 && ((in8 >> lane) & 1)) ? 0u : ~0u;
+  const bool row16 = lane < 16 && pe > 16;
+  const bool row32 = lane < 32 && pe > 32;
+  const bool row48 = lane < 48 && pe > 48;
 
   uint32_t rk = RANK_INF, mid = 0;
   uint32_t nfirst = 0, nlast = 0;  // event counts, kept by lane ps
@@ -428,15 +574,14 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     const bool me = (live >> lane) & 1;
     const uint64_t after = live & ~mask_le(lane);
     const int nx = after ? __builtin_ctzll(after) : 64;
-    const int src = nx < 64 ? nx : lane;
-    const uint32_t nsym = __shfl(sym, src);
-    const int nisb = __shfl(isb, src);
-    const uint32_t nbyte = __shfl(byte, src);
+    const uint32_t nsym = __shfl(sym, nx < 64 ? nx : lane);
     if (dirty) {
       rk = RANK_INF;
       if (elig && me && nx < pe) {
-        const uint64_t v = (isb && nisb) ? t.bytepair[(byte << 8) | nbyte]
-                                         : pair_lookup(t, sym, nsym);
+        const uint64_t v =
+            (sym & nsym & SYM_BYTE)
+                ? t.bytepair[((sym >> 12) & 0xFF00) | ((nsym >> 20) & 0xFF)]
+                : pair_lookup(t, sym & SYM_ID, nsym & SYM_ID);
         if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
       }
       dirty = false;
@@ -445,16 +590,29 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     // only live lanes compete
     const uint32_t key = (me && rk != RANK_INF) ? ((rk << 6) | (uint32_t)lane)
                                                 : RANK_INF;
+    // segmented suffix minimum: inside each row of 16 lanes by DPP row
+    // shifts (lane i reads lane i + d), then the later rows' minima
     uint32_t m = key;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t o = __shfl_down(m, d);
-      if (lane + d < pe) m = min(m, o);
-    }
-    const uint32_t pm = __shfl(m, src_ps);
-    const bool act = elig && pm != RANK_INF;
-    if (!__any(act)) break;
-    const bool win_ = act && key == pm;
+    m = min(m, dpp_shl<1>(m) | blk1);
+    m = min(m, dpp_shl<2>(m) | blk2);
+    m = min(m, dpp_shl<4>(m) | blk4);
+    m = min(m, dpp_shl<8>(m) | blk8);
+    const uint32_t m16 = __builtin_amdgcn_readlane(m, 16);
+    const uint32_t m32 = __builtin_amdgcn_readlane(m, 32);
+    const uint32_t m48 = __builtin_amdgcn_readlane(m, 48);
+    m = min(m, row16 ? m16 : RANK_INF);
+    m = min(m, row32 ? m32 : RANK_INF);
+    m = min(m, row48 ? m48 : RANK_INF);
+    // A lane whose key is the minimum of its suffix is a record; each
+    // segment's winner (its lowest key) is its first record. A carry
+    // started at each segment's first lane runs over the lanes that are
+    // neither records nor the segment's last lane and stops on the first
+    // that is.
+    const uint64_t rec = __ballot(key != RANK_INF && m == key);
+    if (rec == 0) break;
+    const uint64_t stop = rec | ends;
+    const uint64_t wm = ((~stop + starts) & stop) & rec;
+    const bool win_ = (wm >> lane) & 1;
     if (hist) {
       const uint32_t nf = __shfl(nfirst, src_ps);
       const uint32_t nl = __shfl(nlast, src_ps);
@@ -472,18 +630,19 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
         if (lm & lanes_in(ps, pe)) ++nlast;
       }
     }
-    const uint64_t wm = __ballot(win_);
-    const uint64_t before = live & ((1ULL << lane) - 1);
-    const int pv = before ? 63 - __builtin_clzll(before) : -1;
-    const bool dies = me && pv >= 0 && ((wm >> pv) & 1);
-    if (win_) { sym = mid; isb = 0; }
-    live &= ~__ballot(dies);
-    const uint64_t after2 = live & ~mask_le(lane);
-    const int nx2 = after2 ? __builtin_ctzll(after2) : 64;
-    dirty = win_ || (((live >> lane) & 1) && nx2 < 64 && ((wm >> nx2) & 1));
+    // Each winner absorbs the next live lane: a carry from the lane above
+    // the winner runs over the dead lanes and lands on it. The same on the
+    // bit-reversed masks finds the live lane before each winner, whose
+    // right neighbour changed.
+    const uint64_t gone = (~live + (wm << 1)) & live;
+    if (win_) sym = mid;
+    live &= ~gone;
+    const uint64_t lr = __brevll(live);
+    const uint64_t prevw = __brevll((~lr + (__brevll(wm) << 1)) & lr);
+    dirty = ((wm | prevw) >> lane) & 1;
   }
   if (hist && elig && lane == ps) w.hmeta[base + ps] = nfirst | (nlast << 16);
-  if (write && elig) w.tok[pos] = ((live >> lane) & 1) ? sym : INVALID_ID;
+  if (write && elig) w.tok[pos] = ((live >> lane) & 1) ? (sym & SYM_ID) : INVALID_ID;
   return live;
 }
 

@@ -438,10 +438,20 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (cfg->ignore_merges && !vocab_blob && vocab_blob_len)
     return fail(TK_E_INVALID_ARG, "vocabulary blob is null");
   const uint64_t n_pairs = cfg->pair_count;
-  // ranks are packed rank<<6|lane in 32 bits on the device
-  for (uint64_t i = 0; i < n_pairs; ++i)
-    if (pair_keys[i] != ~0ULL && (pair_vals[i] >> 32) >= tk::MAX_MERGES)
+  // ranks are packed rank<<6|lane in 32 bits on the device, token ids in
+  // 20 bits (the vocabulary value format already limits them to that)
+  for (uint64_t i = 0; i < n_pairs; ++i) {
+    if (pair_keys[i] == ~0ULL) continue;
+    if ((pair_vals[i] >> 32) >= tk::MAX_MERGES)
       return fail(TK_E_SHAPE, "merge rank exceeds 2^25");
+    if ((pair_vals[i] & 0xFFFFFFFFULL) >= (1u << 20) ||
+        (pair_keys[i] >> 32) >= (1u << 20) ||
+        (pair_keys[i] & 0xFFFFFFFFULL) >= (1u << 20))
+      return fail(TK_E_SHAPE, "merge token id exceeds 2^20");
+  }
+  for (int b = 0; b < 256; ++b)
+    if (byte_id[b] >= (1 << 20))
+      return fail(TK_E_SHAPE, "byte token id exceeds 2^20");
 
   int ndev = 0;
   HIP_TRY(hipGetDeviceCount(&ndev));
