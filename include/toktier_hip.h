@@ -124,7 +124,9 @@ int tk_engine_encode_batch(tk_engine* engine, const uint8_t* joined,
 
 /* Device-resident form (no host copies): d_text and d_ids are device
  * pointers on the engine's device; `stream` is a hipStream_t or NULL for
- * the engine's own stream. Blocks until *n_ids is known. */
+ * the engine's own stream. Blocks until *n_ids is known. The ids are
+ * compacted straight into d_ids; after a failure (*n_ids == 0) its first
+ * ids_cap entries hold no defined values. */
 int tk_engine_encode_device(tk_engine* engine, const void* d_text,
                             size_t nbytes, uint32_t flags, void* d_ids,
                             size_t ids_cap, size_t* n_ids, void* stream);

@@ -15,6 +15,7 @@ constexpr uint32_t MAX_MERGES = 1u << 25;
 constexpr uint32_t ST_UTF8 = 1u;     // invalid UTF-8 seen
 constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
+constexpr uint32_t ST_CAPACITY = 8u;  // more ids than the output holds
 
 // Compact pair table: bijection of the 36-bit pair key (left<<18 | right),
 // shared by the host builder and the device probe.
@@ -71,6 +72,7 @@ struct DevWork {
   uint32_t* blkcount;    // per compaction block
   uint32_t* blkprefix;   // exclusive prefix, [nblk + 1]
   uint32_t* out;         // compacted ids
+  uint32_t out_cap;      // capacity of out in ids
   // long-piece segmentation (one bit / slot per byte)
   uint64_t* inlong;      // bytes of pieces over 64 bytes
   uint64_t* cuts;        // candidate segment starts inside long pieces
@@ -84,6 +86,10 @@ struct DevWork {
   uint32_t* nfail;       // ctrl[4]
   uint64_t* dirty_cur;   // repair pass: words (64 bytes) to redo, 1 bit each
   uint64_t* dirty_next;  // words marked by the current certify pass
+  // per-call clearing done by k_pretok for the stages after it
+  uint32_t* ctrl_next;   // the other control slot (used by the next call)
+  int64_t clear_words;   // inlong / failm words
+  int64_t clear_dwords;  // dirty_next words
 };
 
 // ctrl word layout (device -> host)
@@ -95,21 +101,27 @@ constexpr int COMPACT_TPB = 256;
 constexpr int COMPACT_PER_THREAD = 16;
 constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
 
-hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s);
+// start / stop: optional timing events taken from the start of the stage's
+// first dispatch / the end of its last one
+hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
+                         hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
-                            hipStream_t s);
+                            hipStream_t s, hipEvent_t start = nullptr,
+                            hipEvent_t stop = nullptr);
 hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
                             hipStream_t s);
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s);
+                            hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
                                 int all, hipStream_t s);
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
-                          hipStream_t s);
+                          hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
-hipError_t launch_compact(const DevWork& w, hipStream_t s);
+hipError_t launch_compact(const DevWork& w, hipStream_t s,
+                          hipEvent_t start = nullptr,
+                          hipEvent_t stop = nullptr);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);

@@ -31,6 +31,8 @@
 // ties; pretok_kernel.cu:872-881); table formats: bpe_tables.py:99-132.
 #include "tk_device.h"
 
+#include <hip/hip_ext.h>
+
 namespace tk {
 
 constexpr uint8_t CP_ = 0, CL_ = 1, CN_ = 2, CS_ = 3;
@@ -402,6 +404,22 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     }
     *reinterpret_cast<uint4*>(sb + 16 * j) = v;
   }
+  // Clear what the later stages of this call accumulate into: the block's
+  // 64 words of the long-piece masks, its word of repair bits, and (block
+  // 0) the control slot of the next call; the last block takes the tails.
+  {
+    const int64_t wd0 = (base >> 6), dw0 = blockIdx.x;
+    const bool last = blockIdx.x == gridDim.x - 1;
+    for (int64_t j = wd0 + tid; j < w.clear_words && (j < wd0 + 64 || last);
+         j += PRETOK_TPB) {
+      w.inlong[j] = 0;
+      w.failm[j] = 0;
+    }
+    for (int64_t j = dw0 + tid; j < w.clear_dwords && (j == dw0 || last);
+         j += PRETOK_TPB)
+      w.dirty_next[j] = 0;
+    if (blockIdx.x == 0 && tid < CTRL_WORDS) w.ctrl_next[tid] = 0;
+  }
   const int64_t wlo = (base >> 6) - 3;
   if (w.docmask) {
     const int64_t nmw = nb / 64 + 2;  // words the caller's mask holds
@@ -476,12 +494,24 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   if (st) atomicOr(w.status, st);
 }
 
-hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s) {
+// Launch, optionally with timing events taken from the dispatch itself
+// (hipExtLaunchKernel): no marker packets between the stages.
+template <typename... KArgs, typename... Args>
+void launch_ev(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+               hipEvent_t start, hipEvent_t stop, Args... args) {
+  if (start || stop)
+    hipExtLaunchKernelGGL(k, grid, block, 0, s, start, stop, 0, args...);
+  else
+    hipLaunchKernelGGL(k, grid, block, 0, s, args...);
+}
+
+hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
+                         hipEvent_t start, hipEvent_t stop) {
   const int64_t nwin = (w.nb + 63) / 64;
   const int64_t nwords = nwin + 2;  // words 0..nwin+1
   const int64_t blocks = (nwords * 64 + PT_TILE - 1) / PT_TILE;
-  hipLaunchKernelGGL(k_pretok, dim3((uint32_t)blocks), dim3(PRETOK_TPB), 0, s,
-                     t, w, nwords);
+  launch_ev(k_pretok, dim3((uint32_t)blocks), dim3(PRETOK_TPB), s, start, stop,
+            t, w, nwords);
   return hipGetLastError();
 }
 
@@ -725,11 +755,11 @@ __global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
 }
 
 hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
-                            hipStream_t s) {
+                            hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   const int64_t nwin = (w.nb + 63) / 64;
   const int64_t blocks = (nwin + 1 + 3) / 4;
-  hipLaunchKernelGGL(k_bpe_small, dim3((uint32_t)blocks), dim3(256), 0, s, t,
-                     w, nwin);
+  launch_ev(k_bpe_small, dim3((uint32_t)blocks), dim3(256), s, start, stop,
+            t, w, nwin);
   return hipGetLastError();
 }
 
@@ -1300,12 +1330,12 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
 }
 
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s) {
+                            hipStream_t s, hipEvent_t stop) {
   hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(64), 0, s, t, w);
   // pieces of 65..WIDE_MAX bytes are merged whole, one wave each
-  hipLaunchKernelGGL(k_bpe_wide, dim3(2048), dim3(256), 0, s, t, w,
-                     (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
-                     w.long_cap, 0);
+  launch_ev(k_bpe_wide, dim3(2048), dim3(256), s, nullptr, stop, t, w,
+            (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
+            w.long_cap, 0);
   return hipGetLastError();
 }
 
@@ -1333,10 +1363,10 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 }
 
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
-                          hipStream_t s) {
+                          hipStream_t s, hipEvent_t stop) {
   const int64_t nwords = (w.nb + 63) / 64;
-  hipLaunchKernelGGL(k_certify, dim3((uint32_t)((nwords + 255) / 256)),
-                     dim3(256), 0, s, t, w, nwords, all);
+  launch_ev(k_certify, dim3((uint32_t)((nwords + 255) / 256)), dim3(256), s,
+            nullptr, stop, t, w, nwords, all);
   return hipGetLastError();
 }
 
@@ -1390,30 +1420,40 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_count(DevWork w, int64_t nblk) 
   if (threadIdx.x == 0) w.blkcount[blockIdx.x] = tot;
 }
 
-__global__ __launch_bounds__(1024) void k_scan(DevWork w, int64_t nblk) {
-  __shared__ uint32_t part[1024];
-  const int64_t per = (nblk + 1023) / 1024;
+// exclusive prefix of the block counts: each of 1024 threads sums a
+// contiguous run of counts, the block scans the run totals, then each
+// thread writes its run's prefixes
+constexpr int SCAN_TPB = 1024;
+__global__ __launch_bounds__(SCAN_TPB) void k_scan(DevWork w, int64_t nblk) {
+  __shared__ uint32_t wsum[SCAN_TPB / 64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t per = (nblk + SCAN_TPB - 1) / SCAN_TPB;
   const int64_t lo = threadIdx.x * per;
   uint32_t s = 0;
   for (int64_t k = lo; k < lo + per && k < nblk; ++k) s += w.blkcount[k];
-  part[threadIdx.x] = s;
+  const uint32_t inc = wave_incl_scan(s, lane);
+  if (lane == 63) wsum[wv] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (int k = 0; k < 1024; ++k) { const uint32_t x = part[k]; part[k] = acc; acc += x; }
-    w.blkprefix[nblk] = acc;
-    w.status[1] = acc;
+  uint32_t acc = inc - s, tot = 0;
+  for (int q = 0; q < SCAN_TPB / 64; ++q) {
+    if (q < wv) acc += wsum[q];
+    tot += wsum[q];
   }
-  __syncthreads();
-  uint32_t acc = part[threadIdx.x];
+  if (threadIdx.x == 0) {
+    w.blkprefix[nblk] = tot;
+    w.status[1] = tot;
+    if (tot > w.out_cap) atomicOr(w.status, ST_CAPACITY);
+  }
   for (int64_t k = lo; k < lo + per && k < nblk; ++k) {
     w.blkprefix[k] = acc;
     acc += w.blkcount[k];
   }
 }
 
-__global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w) {
+__global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w,
+                                                         int64_t nblk) {
   __shared__ uint32_t wsum[COMPACT_TPB / 64];
+  if (w.blkprefix[nblk] > w.out_cap) return;  // whole grid: reported by k_scan
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
   uint32_t run = w.blkprefix[blockIdx.x];
@@ -1437,14 +1477,18 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w) {
   }
 }
 
-hipError_t launch_compact(const DevWork& w, hipStream_t s) {
+hipError_t launch_compact(const DevWork& w, hipStream_t s, hipEvent_t start,
+                          hipEvent_t stop) {
   const int64_t nblk = (w.nb + COMPACT_BLOCK - 1) / COMPACT_BLOCK;
   if (nblk > 0) {
-    hipLaunchKernelGGL(k_count, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0, s, w, nblk);
+    launch_ev(k_count, dim3((uint32_t)nblk), dim3(COMPACT_TPB), s, start,
+              nullptr, w, nblk);
   }
-  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, w, nblk);
+  launch_ev(k_scan, dim3(1), dim3(SCAN_TPB), s, nblk > 0 ? nullptr : start,
+            nblk > 0 ? nullptr : stop, w, nblk);
   if (nblk > 0) {
-    hipLaunchKernelGGL(k_compact, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0, s, w);
+    launch_ev(k_compact, dim3((uint32_t)nblk), dim3(COMPACT_TPB), s, nullptr,
+              stop, w, nblk);
   }
   return hipGetLastError();
 }

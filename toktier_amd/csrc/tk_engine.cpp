@@ -159,6 +159,8 @@ struct tk_engine {
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
   DevBuf<uint32_t> hmeta, seglist, unsafe;
   size_t docs_cap = 0;
+  uint32_t slot = 0;  // control slot of the next call
+  uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
   // timing
   bool timing = false;
   hipEvent_t ev[8] = {};
@@ -210,7 +212,10 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->pv.alloc(need));
     HIP_TRY(e->heap.alloc(3 * need));
     HIP_TRY(e->longlist.alloc(2 * long_cap));
-    HIP_TRY(e->ctrl.alloc(tk::CTRL_WORDS));
+    // two control slots: each call's k_pretok clears the slot of the next
+    HIP_TRY(e->ctrl.alloc(2 * tk::CTRL_WORDS));
+    HIP_TRY(hipMemset(e->ctrl.p, 0, 2 * tk::CTRL_WORDS * sizeof(uint32_t)));
+    e->slot = 0;
     HIP_TRY(e->inlong.alloc(words));
     HIP_TRY(e->cuts.alloc(words));
     HIP_TRY(e->failm.alloc(words));
@@ -234,7 +239,9 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
 }
 
 tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
-                      const uint64_t* d_docmask, bool check_nfc) {
+                      const uint64_t* d_docmask, bool check_nfc,
+                      uint32_t* out, size_t out_cap) {
+  uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   tk::DevWork w{};
   w.text = d_text;
   w.nb = (int64_t)nb;
@@ -246,12 +253,13 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.pv = e->pv.p;
   w.heap = e->heap.p;
   w.longlist = e->longlist.p;
-  w.longcount = e->ctrl.p + tk::CTRL_LONG;
+  w.longcount = ctrl + tk::CTRL_LONG;
   w.long_cap = (uint32_t)(e->longlist.n / 2);
-  w.status = e->ctrl.p + tk::CTRL_STATUS;
+  w.status = ctrl + tk::CTRL_STATUS;
   w.blkcount = e->blkcount.p;
   w.blkprefix = e->blkprefix.p;
-  w.out = e->out.p;
+  w.out = out;
+  w.out_cap = (uint32_t)std::min<size_t>(out_cap, 0xFFFFFFFFu);
   w.inlong = e->inlong.p;
   w.cuts = e->cuts.p;
   w.failm = e->failm.p;
@@ -259,16 +267,19 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.hlast = e->hlast.p;
   w.hmeta = e->hmeta.p;
   w.seglist = e->seglist.p;
-  w.segcount = e->ctrl.p + tk::CTRL_SEG;
+  w.segcount = ctrl + tk::CTRL_SEG;
   w.seg_cap = (uint32_t)(e->seglist.n / 2);
-  w.nfail = e->ctrl.p + tk::CTRL_FAIL;
+  w.nfail = ctrl + tk::CTRL_FAIL;
   w.dirty_cur = e->dirty_cur.p;
   w.dirty_next = e->dirty_next.p;
+  w.ctrl_next = e->ctrl.p + (e->slot ^ 1) * tk::CTRL_WORDS;
+  w.clear_words = (int64_t)(nb / 64 + 4);
+  w.clear_dwords = w.clear_words / 64 + 2;
   return w;
 }
 
-int read_ctrl_words(tk_engine* e, hipStream_t s, uint32_t* h) {
-  HIP_TRY(hipMemcpyAsync(h, e->ctrl.p, 8 * sizeof(uint32_t),
+int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
+  HIP_TRY(hipMemcpyAsync(h, ctrl, 8 * sizeof(uint32_t),
                          hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
@@ -283,36 +294,38 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 }
 
 // Runs every stage for nb bytes already at d_text and waits for the result:
-// ids in e->out, status and total count returned. Long pieces whose cuts
-// fail certification are redone here (host-driven passes, each removing
-// the failed cuts) until every cut holds.
+// ids in out (when they fit out_cap; else ST_CAPACITY), status and total
+// count returned. Long pieces whose cuts fail certification are redone here
+// (host-driven passes, each removing the failed cuts) until every cut holds.
+// Nothing is cleared from the host: k_pretok clears the per-call masks and
+// the control slot of the next call, so the stages run back to back.
 int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
                  const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
-                 uint32_t* status, uint32_t* total) {
-  const tk::DevWork w = make_work(e, d_text, nb, d_docmask, check_nfc);
-  const size_t words = nb / 64 + 4;
+                 uint32_t* out, size_t out_cap, uint32_t* status,
+                 uint32_t* total) {
+  const tk::DevWork w =
+      make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap);
+  uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
-  HIP_TRY(hipMemsetAsync(e->ctrl.p, 0, tk::CTRL_WORDS * sizeof(uint32_t), s));
-  HIP_TRY(hipMemsetAsync(e->inlong.p, 0, words * 8, s));
-  HIP_TRY(hipMemsetAsync(e->failm.p, 0, words * 8, s));
-  HIP_TRY(hipMemsetAsync(e->dirty_next.p, 0, (words / 64 + 2) * 8, s));
-  if (e->timing) HIP_TRY(hipEventRecord(ev[0], s));
-  HIP_TRY(tk::launch_pretok(e->t, w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(ev[1], s));
-  HIP_TRY(tk::launch_bpe_small(e->t, w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(ev[2], s));
+  // Stage boundaries, timestamps taken by the dispatches themselves:
+  // ev[0] start of k_pretok, ev[1..4] the end of the last dispatch of each
+  // stage. (Each timed dispatch delays the next one by a few microseconds,
+  // so the events sit on as few dispatches as the breakdown allows.)
+  hipEvent_t* tv = e->timing ? ev : nullptr;
+  auto at = [&](int k) { return tv ? tv[k] : nullptr; };
+  HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
+  e->slot ^= 1;  // this call's k_pretok clears the other slot
+  HIP_TRY(tk::launch_bpe_small(e->t, w, s, nullptr, at(2)));
   HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
-  HIP_TRY(tk::launch_long_prep(e->t, w, s));
+  HIP_TRY(tk::launch_long_prep(e->t, w, s, e->t.cert ? nullptr : at(3)));
   if (e->t.cert) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s));
     HIP_TRY(tk::launch_long_segments(e->t, w, 1, s));
-    HIP_TRY(tk::launch_certify(e->t, w, 1, s));
+    HIP_TRY(tk::launch_certify(e->t, w, 1, s, at(3)));
   }
-  if (e->timing) HIP_TRY(hipEventRecord(ev[3], s));
-  HIP_TRY(tk::launch_compact(w, s));
-  if (e->timing) HIP_TRY(hipEventRecord(ev[4], s));
-  uint32_t h[8];
-  int rc = read_ctrl_words(e, s, h);
+  HIP_TRY(tk::launch_compact(w, s, nullptr, at(4)));
+  uint32_t* h = e->host_ctrl;
+  int rc = read_ctrl_words(ctrl, s, h);
   if (rc != TK_OK) return rc;
   if (e->timing) {
     for (int k = 0; k < 4; ++k) e->last_us[k] = elapsed_us(ev[k], ev[k + 1]);
@@ -325,16 +338,16 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
     if (e->timing) HIP_TRY(hipEventRecord(ev[5], s));
     while (h[tk::CTRL_FAIL] != 0) {
       if (++passes > nb + 1) return fail(TK_E_INTERNAL, "certification did not converge");
-      HIP_TRY(hipMemsetAsync(e->ctrl.p + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
+      HIP_TRY(hipMemsetAsync(ctrl + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
       HIP_TRY(tk::launch_apply_fail(w, s));
       HIP_TRY(tk::launch_long_segments(e->t, w, 0, s));
       HIP_TRY(tk::launch_certify(e->t, w, 0, s));
-      if ((rc = read_ctrl_words(e, s, h)) != TK_OK) return rc;
+      if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     }
     if (e->timing) HIP_TRY(hipEventRecord(ev[6], s));
     HIP_TRY(tk::launch_compact(w, s));
     if (e->timing) HIP_TRY(hipEventRecord(ev[7], s));
-    if ((rc = read_ctrl_words(e, s, h)) != TK_OK) return rc;
+    if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     if (e->timing) {
       e->last_us[2] += elapsed_us(ev[5], ev[6]);
       e->last_us[3] = elapsed_us(ev[6], ev[7]);
@@ -485,8 +498,12 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
   for (auto& ev : e->ev)
-    if (hipEventCreate(&ev) != hipSuccess)
-      return bail(fail(TK_E_DEVICE, "hipEventCreate failed"));
+    // timing-only events: no system-scope fence between the stages
+    if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
+  if (hipHostMalloc(reinterpret_cast<void**>(&e->host_ctrl),
+                    tk::CTRL_WORDS * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+    return bail(fail(TK_E_DEVICE, "hipHostMalloc failed"));
 
   // interleave key/value so one 16-byte load reads a whole slot
   std::vector<ulonglong2> pairs(n_pairs);
@@ -572,6 +589,7 @@ void tk_engine_close(tk_engine* e) {
   for (auto& ev : e->ev)
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream) (void)hipStreamDestroy(e->stream);
+  if (e->host_ctrl) (void)hipHostFree(e->host_ctrl);
   delete e;
 }
 
@@ -606,14 +624,15 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
+  // the compaction writes straight into the caller's buffer
   rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr,
-                    check, s, &st, &total);
+                    check, s, static_cast<uint32_t*>(d_ids), ids_cap, &st,
+                    &total);
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
-  if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
-  HIP_TRY(hipMemcpyAsync(d_ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToDevice, s));
-  HIP_TRY(hipStreamSynchronize(s));
+  if ((st & tk::ST_CAPACITY) || total > ids_cap)
+    return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   *n_ids = total;
   return TK_OK;
 }
@@ -633,7 +652,8 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   HIP_TRY(hipMemcpyAsync(e->text.p, text, nbytes, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
-  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, &st, &total);
+  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, e->out.p,
+                    e->out.n, &st, &total);
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -676,9 +696,11 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
-  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, &st, &total);
+  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, e->out.p,
+                    e->out.n, &st, &total);
   if (rc != TK_OK) return rc;
-  const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check);
+  const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check,
+                                  e->out.p, e->out.n);
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
