@@ -17,16 +17,24 @@ constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
 constexpr uint32_t ST_CAPACITY = 8u;  // more ids than the output holds
 
-// Compact pair table: bijection of the 36-bit pair key (left<<18 | right),
-// shared by the host builder and the device probe.
-constexpr uint64_t MASK36 = (1ULL << 36) - 1;
-constexpr uint32_t CTAB_MAX_DISP = 16;
-__host__ __device__ __forceinline__ uint64_t perm36(uint64_t x) {
-  x = (x * 0x9E3779B97F4A7C15ULL) & MASK36;  // odd multiplier: bijective
-  x ^= x >> 18;                              // xorshift: bijective
-  x = (x * 0xBF58476D1CE4E5B9ULL) & MASK36;
-  x ^= x >> 17;
-  return x;
+// Compact pair table: a bijection of the 36-bit pair key (left, right <
+// 2^18), shared by the host builder and the device probe. Two Feistel
+// rounds on the 18-bit halves; the round function is a 24-bit multiply
+// (full rate on the vector ALU) folded onto itself.
+// Slot = tag<<42 | displacement<<37 | rank<<18 | id; the bucket index is
+// the low bits of the permuted key and the tag the rest, so a slot names
+// its key exactly.
+constexpr uint32_t CTAB_MAX_DISP = 32;
+constexpr uint32_t CTAB_MIN_BITS = 14;  // tags fit 22 bits
+constexpr uint64_t CTAB_LOW = (1ULL << 37) - 1;  // rank and id bits
+__host__ __device__ __forceinline__ uint32_t pair_round(uint32_t x, uint32_t c) {
+  const uint32_t p = (x & 0x3FFFFu) * c;
+  return (p ^ (p >> 16)) & 0x3FFFFu;
+}
+__host__ __device__ __forceinline__ uint64_t pair_perm(uint32_t l, uint32_t r) {
+  const uint32_t a = l ^ pair_round(r, 0x9E3779u);
+  const uint32_t b = r ^ pair_round(a, 0x85EBCBu);
+  return ((uint64_t)(a & 0x3FFFFu) << 18) | (b & 0x3FFFFu);
 }
 
 // Device copies of the family tables, in the engine's own layout.
@@ -86,6 +94,11 @@ struct DevWork {
   uint32_t* nfail;       // ctrl[4]
   uint64_t* dirty_cur;   // repair pass: words (64 bytes) to redo, 1 bit each
   uint64_t* dirty_next;  // words marked by the current certify pass
+  // packed short-piece BPE
+  uint32_t* plist;       // piece starts by length class
+  uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
+  uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
+  uint32_t* pnext;       // next work unit (ctrl)
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
   int64_t clear_words;   // inlong / failm words
@@ -94,9 +107,34 @@ struct DevWork {
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
-              CTRL_FAIL = 4, CTRL_WORDS = 16;
+              CTRL_FAIL = 4, CTRL_PCOUNT = 16, CTRL_PNEXT = 29,
+              CTRL_WORDS = 32;
+// length classes of the packed short-piece BPE (counts at CTRL_PCOUNT)
+constexpr int PACK_CLASSES = 13;
+constexpr int PACK_BLOCKS = 2048;
+// slots (lanes per piece) of the length classes, and the shortest piece of
+// each class: class c holds pieces of pack_lmin(c)..pack_slot(c) bytes
+__host__ __device__ constexpr int pack_slot(int c) {
+  return c <= 6 ? c + 2 : c == 7 ? 10 : c == 8 ? 12 : c == 9 ? 16
+       : c == 10 ? 21 : c == 11 ? 32 : 64;
+}
+__host__ __device__ constexpr int pack_lmin(int c) {
+  return c <= 7 ? c + 2 : pack_slot(c - 1) + 1;
+}
+// start of class c's list; each class has room for every piece of its
+// shortest length that nb bytes can hold (c == PACK_CLASSES: total length)
+__host__ __device__ inline int64_t pack_off(int64_t nb, int c) {
+  int64_t o = 0;
+  for (int k = 0; k < c; ++k) o += nb / pack_lmin(k) + 1;
+  return o;
+}
 
 constexpr int PRETOK_TPB = 256;
+constexpr int PT_TILE = 4096;  // bytes per k_pretok block (64 start words)
+// k_pretok blocks: the start words 0..nwin+1 (nwin = ceil(nb / 64))
+__host__ __device__ inline int64_t pretok_tiles(int64_t nb) {
+  return (((nb + 63) / 64 + 2) * 64 + PT_TILE - 1) / PT_TILE;
+}
 constexpr int COMPACT_TPB = 256;
 constexpr int COMPACT_PER_THREAD = 16;
 constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
@@ -105,11 +143,8 @@ constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
 // first dispatch / the end of its last one
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
-hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
-                            hipStream_t s, hipEvent_t start = nullptr,
-                            hipEvent_t stop = nullptr);
-hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
-                            hipStream_t s);
+hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop = nullptr);
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
                             hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,

@@ -4,13 +4,13 @@
 //   1. k_pretok       per byte: UTF-8 validation, class lookup, NFC quick
 //                     check, and the family split rules as a per-character
 //                     piece-start predicate -> one start bit per byte.
-//   2. k_bpe_small    one wave64 per 64-byte window, lane = byte: every piece
-//                     inside the aligned window, then every piece inside the
-//                     window shifted by 32 bytes, is merged in place (lowest
-//                     rank pair, leftmost first) with segmented wave
-//                     reductions. Any piece of <= 32 bytes fits one of the
-//                     two; the others are queued.
-//      k_bpe_list     queued pieces of <= 64 bytes, one wave each.
+//      (k_pretok also sizes the pieces that start in its tile: pieces of
+//                     1-2 bytes are finished there, longer than 64 queued
+//                     for stage 3, the rest counted by length class.)
+//   2. k_pack_scan / k_pack_scatter list the pieces of 2..64 bytes by
+//                     length class; k_bpe_pack merges them (lowest rank
+//                     pair, leftmost first) with segmented wave reductions,
+//                     lane = byte, 64 / slot pieces of one class per wave.
 //   3. long pieces    (> 64 bytes) are cut into short segments at likely
 //                     token boundaries (k_long_windows), merged segment by
 //                     segment with boundary-token histories
@@ -48,27 +48,28 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
 
 // rank<<32 | merged id, or ~0 when the pair has no merge rule.
 // The compact table (when the engine built one): 16-byte buckets of two
-// u64 slots, slot = tag<<41 | displacement<<37 | rank<<18 | id, found by a
-// bijection of the 36-bit key (left<<18 | right); the bucket index is the
-// low bits of the permuted key and the tag the rest, so a slot identifies
-// its key exactly. One 16-byte load per bucket, as the boundary table,
-// in a table a quarter of its size (it stays in one XCD's L2).
+// u64 slots (tk_device.h), probed linearly from the home bucket; the first
+// probe settles almost every lookup. Else the interleaved boundary table.
 __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
                                                 uint32_t l, uint32_t r) {
   if (t.ctab) {
     if ((l | r) >= (1u << 18)) return ~0ULL;  // every rule's ids fit 18 bits
-    const uint64_t x = perm36(((uint64_t)l << 18) | r);
-    const uint64_t home = x & t.cmask;
+    const uint64_t x = pair_perm(l, r);
     const uint64_t tag = x >> t.cbits;
     const ulonglong2* tab = reinterpret_cast<const ulonglong2*>(t.ctab);
+    uint64_t i = x & t.cmask;
     for (uint64_t d = 0; d < CTAB_MAX_DISP; ++d) {
-      const ulonglong2 b = tab[(home + d) & t.cmask];
-      const uint64_t want = (tag << 41) | (d << 37);
-      // (an empty slot is all ones; test it first so it can never match)
-      if (b.x == ~0ULL) return ~0ULL;
-      if ((b.x & ~0x1FFFFFFFFFULL) == want) return (((b.x >> 18) & 0x7FFFF) << 32) | (b.x & 0x3FFFF);
-      if (b.y == ~0ULL) return ~0ULL;
-      if ((b.y & ~0x1FFFFFFFFFULL) == want) return (((b.y >> 18) & 0x7FFFF) << 32) | (b.y & 0x3FFFF);
+      const ulonglong2 b = tab[i];
+      const uint64_t want = (tag << 42) | (d << 37);
+      // an empty slot is all ones: it must never count as a match
+      const bool mx = b.x != ~0ULL && (b.x & ~CTAB_LOW) == want;
+      const bool my = b.y != ~0ULL && (b.y & ~CTAB_LOW) == want;
+      if (mx || my) {
+        const uint64_t s = mx ? b.x : b.y;
+        return (((s >> 18) & 0x7FFFF) << 32) | (s & 0x3FFFF);
+      }
+      if (b.x == ~0ULL || b.y == ~0ULL) return ~0ULL;
+      i = (i + 1) & t.cmask;
     }
     return ~0ULL;
   }
@@ -102,6 +103,61 @@ __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
     }
     i = (i + 1) & t.vocab_mask;
   }
+}
+
+__device__ __forceinline__ uint64_t mask_le(int lane) {
+  return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
+}
+
+__device__ __forceinline__ uint64_t lanes_in(int lo, int hi) {  // [lo, hi)
+  const uint64_t up = hi >= 64 ? ~0ULL : ((1ULL << hi) - 1);
+  return up & ~((1ULL << lo) - 1);
+}
+
+__device__ __forceinline__ void push_pair(uint32_t* list, uint32_t* count,
+                                          uint32_t cap, uint32_t* status,
+                                          int64_t a, int64_t b) {
+  const uint32_t k = atomicAdd(count, 1u);
+  if (k < cap) {
+    list[2 * k] = (uint32_t)a;
+    list[2 * k + 1] = (uint32_t)b;
+  } else {
+    atomicOr(status, ST_LONGOVF);
+  }
+}
+
+// ---- piece classes (stage 2)
+// A piece is finished without BPE when it is one byte, or two bytes and no
+// whole-piece vocabulary rule applies; pieces of 2..64 bytes are merged in
+// packed waves by length class; longer ones take the long-piece stages.
+constexpr int PIECE_NONE = -1, PIECE_ONE = -2, PIECE_TWO = -3, PIECE_LONG = -4;
+
+__device__ __forceinline__ int pack_class(int L) {  // 2 <= L <= 64
+  return (L > 2) + (L > 3) + (L > 4) + (L > 5) + (L > 6) + (L > 7) + (L > 8) +
+         (L > 10) + (L > 12) + (L > 16) + (L > 21) + (L > 32);
+}
+
+// Kind of the piece that starts at bit `lane` of a start word (given the
+// word after it): PIECE_NONE if no piece starts there.
+__device__ __forceinline__ int piece_kind(uint64_t word, uint64_t next,
+                                          int lane, bool two_direct) {
+  if (!((word >> lane) & 1)) return PIECE_NONE;
+  const uint64_t gt = word & ~mask_le(lane);
+  const int L = gt ? __builtin_ctzll(gt) - lane
+              : next ? 64 - lane + __builtin_ctzll(next) : 65;
+  if (L == 1) return PIECE_ONE;
+  if (L == 2 && two_direct) return PIECE_TWO;
+  if (L <= 64) return pack_class(L);
+  return PIECE_LONG;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(v, d);
+    if (lane >= d) v += o;
+  }
+  return v;
 }
 
 __device__ __forceinline__ bool is_cont(uint8_t b) { return (b & 0xC0) == 0x80; }
@@ -197,7 +253,6 @@ struct GCtx {
 //   bits 23..24 back: prev(p) = p - 1 - back(p - 1)
 //   bits 25..26 fwd:  next(p) = p + 1 + fwd(p) (before the end checks)
 //   bit  27     the decode at p is valid UTF-8
-constexpr int PT_TILE = 4096;
 constexpr int PT_HALO = 64;
 constexpr int PT_SPAN = PT_TILE + 2 * PT_HALO;
 constexpr int PT_PAD = 80;  // >= PT_HALO + 4, a multiple of 16
@@ -385,7 +440,10 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   __shared__ __align__(16) uint8_t sb[PT_BYTES];
   __shared__ uint32_t se[PT_SPAN];
   __shared__ uint64_t sdm[PT_DMW];
+  __shared__ uint64_t sw[PT_TILE / 64 + 1];  // the tile's start words + next
+  __shared__ uint32_t lcnt[PACK_CLASSES];
   const int tid = threadIdx.x;
+  if (tid < PACK_CLASSES) lcnt[tid] = 0;
   const int64_t base = (int64_t)blockIdx.x * PT_TILE;
   const int64_t nb = w.nb;
   const bool al = ((uintptr_t)w.text & 15) == 0;
@@ -450,9 +508,14 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   const LCtx c{GCtx{w.text, nb, w.docmask, t.cls}, se, lo, sdm, wlo};
   const int lane = tid & 63, wv = tid >> 6;
   uint32_t st = 0;
-  for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
+  // the tile's words, and the first word after it (the next block writes
+  // that one; it is recomputed here to size the pieces near the tile end)
+  for (int k = wv; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
     const int64_t wd = (base >> 6) + k;
-    if (wd >= nwords) break;
+    if (wd >= nwords) {  // past the sentinel words: all starts
+      if (lane == 0) sw[k] = ~0ULL;
+      continue;
+    }
     const int64_t i = base + 64 * k + lane;
     const int sj = 64 * k + lane + PT_PAD;
     bool s = true;  // sentinel starts past the text
@@ -489,9 +552,40 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
       }
     }
     const uint64_t m = __ballot(s);
-    if (lane == 0) w.starts[wd] = m;
+    if (lane == 0) {
+      sw[k] = m;
+      if (k < PT_TILE / 64) w.starts[wd] = m;
+    }
   }
   if (st) atomicOr(w.status, st);
+  __syncthreads();
+  // Stage-2 bookkeeping for the pieces that start in this tile: finish the
+  // one- and two-byte ones, queue the long ones, count the rest by class
+  // (the counts are scanned by k_pack_scan).
+  const bool two = !t.ignore_merges;
+  for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
+    const int64_t a = base + 64 * k + lane;
+    if (a >= nb) break;  // (positions only grow along the loop)
+    const int kind = piece_kind(sw[k], sw[k + 1], lane, two);
+    if (kind >= 0) {
+      atomicAdd(&lcnt[kind], 1u);
+    } else if (kind == PIECE_ONE) {
+      const int32_t id = t.byte_id[sb[64 * k + lane + PT_PAD]];
+      w.tok[a] = id >= 0 ? (uint32_t)id : INVALID_ID;
+    } else if (kind == PIECE_TWO) {
+      const uint32_t b0 = sb[64 * k + lane + PT_PAD];
+      const uint32_t b1 = sb[64 * k + lane + PT_PAD + 1];
+      const int32_t i0 = t.byte_id[b0], i1 = t.byte_id[b1];
+      const uint64_t mg = (i0 >= 0 && i1 >= 0) ? t.bytepair[(b0 << 8) | b1] : ~0ULL;
+      w.tok[a] = mg != ~0ULL ? (uint32_t)mg : i0 >= 0 ? (uint32_t)i0 : INVALID_ID;
+      w.tok[a + 1] = (mg == ~0ULL && i1 >= 0) ? (uint32_t)i1 : INVALID_ID;
+    } else if (kind == PIECE_LONG) {
+      // the end is filled in by k_long_prep once every start word is known
+      push_pair(w.longlist, w.longcount, w.long_cap, w.status, a, 0);
+    }
+  }
+  __syncthreads();
+  if (tid < PACK_CLASSES) w.pblk[(int64_t)tid * gridDim.x + blockIdx.x] = lcnt[tid];
 }
 
 // Launch, optionally with timing events taken from the dispatch itself
@@ -507,24 +601,14 @@ void launch_ev(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
 
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start, hipEvent_t stop) {
-  const int64_t nwin = (w.nb + 63) / 64;
-  const int64_t nwords = nwin + 2;  // words 0..nwin+1
-  const int64_t blocks = (nwords * 64 + PT_TILE - 1) / PT_TILE;
-  launch_ev(k_pretok, dim3((uint32_t)blocks), dim3(PRETOK_TPB), s, start, stop,
-            t, w, nwords);
+  const int64_t nwords = (w.nb + 63) / 64 + 2;  // words 0..nwin+1
+  launch_ev(k_pretok, dim3((uint32_t)pretok_tiles(w.nb)), dim3(PRETOK_TPB), s,
+            start, stop, t, w, nwords);
   return hipGetLastError();
 }
 
 // ------------------------------------------------ 2. short-piece BPE
 
-__device__ __forceinline__ uint64_t mask_le(int lane) {
-  return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
-}
-
-__device__ __forceinline__ uint64_t lanes_in(int lo, int hi) {  // [lo, hi)
-  const uint64_t up = hi >= 64 ? ~0ULL : ((1ULL << hi) - 1);
-  return up & ~((1ULL << lo) - 1);
-}
 
 // lane i receives lane i + d of its row of 16; lanes whose source lies past
 // the row end receive RANK_INF
@@ -537,8 +621,10 @@ __device__ __forceinline__ uint32_t dpp_shl(uint32_t v) {
 constexpr uint32_t SYM_ID = 0xFFFFF;      // token id bits of a packed symbol
 constexpr uint32_t SYM_BYTE = 1u << 28;   // the symbol is still one raw byte
 
-// Byte-level BPE of every eligible segment held by one wave, lane = byte
-// at base + lane; ps/pe: the lane's segment as lanes [ps, pe). Each round
+// Byte-level BPE of every eligible segment held by one wave; lane holds
+// the byte at pos, a segment's bytes sit on consecutive lanes; ps/pe: the
+// lane's segment as lanes [ps, pe) (a grid window has pos = base + lane;
+// histories are indexed from base + ps, so hist needs that layout). Each round
 // every segment merges its lowest-ranked pair (leftmost on equal rank:
 // key = rank<<6 | lane) -- the HF order -- until no pair has a rule.
 //   vocab_first: a whole piece that is a vocabulary entry is that one
@@ -551,9 +637,8 @@ constexpr uint32_t SYM_BYTE = 1u << 28;   // the symbol is still one raw byte
 // Returns the final mask of lanes that start a token.
 template <bool vocab_first, bool hist, bool write>
 __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
-                             int64_t base, int lane, bool elig, int ps,
-                             int pe) {
-  const int64_t pos = base + lane;
+                             int64_t base, int64_t pos, int lane, bool elig,
+                             int ps, int pe) {
   const uint32_t byte = elig ? w.text[pos] : 0u;
   const int32_t bid = elig ? t.byte_id[byte] : -1;
   uint64_t live = __ballot(bid >= 0);
@@ -691,18 +776,6 @@ __device__ __forceinline__ bool fits_a_grid(int64_t a, int64_t b) {
          (((a >> 6) == ((b - 1) >> 6)) || (((a + 32) >> 6) == ((b - 1 + 32) >> 6)));
 }
 
-__device__ __forceinline__ void push_pair(uint32_t* list, uint32_t* count,
-                                          uint32_t cap, uint32_t* status,
-                                          int64_t a, int64_t b) {
-  const uint32_t k = atomicAdd(count, 1u);
-  if (k < cap) {
-    list[2 * k] = (uint32_t)a;
-    list[2 * k + 1] = (uint32_t)b;
-  } else {
-    atomicOr(status, ST_LONGOVF);
-  }
-}
-
 // Window geometry shared by the grid kernels: phase 0 is the aligned
 // window [64v, 64v+64), phase 1 the shifted window [64v-32, 64v+32).
 // Given a function word -> boundary bits, returns the window's boundary
@@ -721,45 +794,100 @@ __device__ __forceinline__ void window_bits(int64_t v, int phase, SegBits seg,
   }
 }
 
-// One wave per 64-byte window: first the aligned window, then the shifted
-// one. A piece of <= 32 bytes always fits one of the two; the rest are
-// queued (longlist) by the lane that starts them.
-__global__ __launch_bounds__(256) void k_bpe_small(DevTables t, DevWork w,
-                                                   int64_t nwin) {
-  const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (v > nwin) return;  // whole wave; v == nwin: last shifted window
-  auto seg = [&](int64_t wd) { return w.starts[wd]; };
-  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
-    const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
-    uint64_t S;
-    bool E;
-    window_bits(v, phase, seg, &S, &E);
-    const int64_t pos = base + lane;
-    const bool valid = pos >= 0 && pos < w.nb;
-    const uint64_t le = S & mask_le(lane);
-    const int ps = le ? 63 - __builtin_clzll(le) : -1;
-    const uint64_t gt = S & ~mask_le(lane);
-    const int pe = gt ? __builtin_ctzll(gt) : 64;
-    const bool contained = ps >= 0 && (pe < 64 || E);
-    bool elig = valid && contained;
-    if (phase == 1 && elig && ((base + ps) >> 6) == ((base + pe - 1) >> 6))
-      elig = false;  // the aligned grid had it
-    if (phase == 0 && valid && ps == lane && !contained) {
-      const int64_t b = seg_end_after(v + 1, seg);
-      if (!fits_a_grid(pos, b))
-        push_pair(w.longlist, w.longcount, w.long_cap, w.status, pos, b);
-    }
-    wave_bpe<true, false, true>(t, w, base, lane, elig, ps, pe);
+// ---- pieces of up to 64 bytes, packed by length
+//
+// k_pretok counted the pieces of each tile by length class (pieces of
+// pack_lmin(c)..pack_slot(c) bytes); k_pack_scan turns the counts into
+// per-tile offsets, k_pack_scatter lists the piece starts by class, and
+// k_bpe_pack merges them with one wave per work unit: 64 / slot pieces of
+// one class on slot lanes each. The rounds a wave runs then follow its own
+// pieces' lengths rather than the longest piece of a stretch of text.
+
+// end of the piece that starts at a (the next start bit; sentinel bits at
+// and past nb end the search)
+__device__ __forceinline__ int64_t piece_end(const DevWork& w, int64_t a) {
+  const int64_t wd = a >> 6;
+  const uint64_t gt = w.starts[wd] & ~mask_le((int)(a & 63));
+  if (gt) return wd * 64 + __builtin_ctzll(gt);
+  return seg_end_after(wd + 1, [&](int64_t x) { return w.starts[x]; });
+}
+
+// exclusive prefix of each class's per-tile counts (one wave per class)
+__global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6;
+  if (c >= PACK_CLASSES) return;  // whole wave
+  uint32_t* cnt = w.pblk + (int64_t)c * ntile;
+  uint32_t run = 0;
+  for (int64_t j0 = 0; j0 < ntile; j0 += 64) {
+    const int64_t j = j0 + lane;
+    const uint32_t v = j < ntile ? cnt[j] : 0u;
+    const uint32_t inc = wave_incl_scan(v, lane);
+    if (j < ntile) cnt[j] = run + inc - v;
+    run += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+  }
+  if (lane == 0) w.pcount[c] = run;
+}
+
+// list every packed piece of a tile at its class offset (the order inside
+// a tile's share does not matter: each piece is merged on its own)
+__global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
+                                                             DevWork w) {
+  __shared__ uint32_t lcnt[PACK_CLASSES];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t base = (int64_t)blockIdx.x * PT_TILE;
+  if (tid < PACK_CLASSES)
+    lcnt[tid] = (uint32_t)pack_off(w.nb, tid) +
+                w.pblk[(int64_t)tid * gridDim.x + blockIdx.x];
+  __syncthreads();
+  const bool two = !t.ignore_merges;
+  for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
+    const int64_t a = base + 64 * k + lane;
+    if (a >= w.nb) break;
+    const int64_t wd = a >> 6;
+    const int kind = piece_kind(w.starts[wd], w.starts[wd + 1], lane, two);
+    if (kind >= 0) w.plist[atomicAdd(&lcnt[kind], 1u)] = (uint32_t)a;
   }
 }
 
-hipError_t launch_bpe_small(const DevTables& t, const DevWork& w,
-                            hipStream_t s, hipEvent_t start, hipEvent_t stop) {
-  const int64_t nwin = (w.nb + 63) / 64;
-  const int64_t blocks = (nwin + 1 + 3) / 4;
-  launch_ev(k_bpe_small, dim3((uint32_t)blocks), dim3(256), s, start, stop,
-            t, w, nwin);
+// Work units in order, the longest class first; wave g takes units
+// g, g + G, g + 2G, ... (G waves in the grid), so every wave gets a share of
+// each class.
+__global__ __launch_bounds__(256) void k_bpe_pack(DevTables t, DevWork w) {
+  const int lane = threadIdx.x & 63;
+  uint32_t units[PACK_CLASSES];
+  uint32_t total = 0;
+  for (int c = PACK_CLASSES - 1; c >= 0; --c) {
+    const uint32_t k = 64 / pack_slot(c);
+    units[c] = (w.pcount[c] + k - 1) / k;
+    total += units[c];
+  }
+  const uint32_t G = gridDim.x * (blockDim.x / 64);
+  for (uint32_t u0 = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+       u0 < total; u0 += G) {
+    uint32_t u = u0;
+    int c = PACK_CLASSES - 1;
+    while (u >= units[c]) u -= units[c--];
+    const int sl = pack_slot(c), k = 64 / sl;
+    const int slot = lane / sl, off = lane - slot * sl;
+    const uint32_t idx = u * k + slot;
+    int64_t a = 0, L = 0;
+    if (slot < k && idx < w.pcount[c]) {
+      a = w.plist[pack_off(w.nb, c) + idx];
+      L = piece_end(w, a) - a;
+    }
+    const bool elig = off < L;
+    const int ps = elig ? slot * sl : lane, pe = elig ? slot * sl + (int)L : lane + 1;
+    wave_bpe<true, false, true>(t, w, 0, a + off, lane, elig, ps, pe);
+  }
+}
+
+hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop) {
+  const int64_t ntile = pretok_tiles(w.nb);
+  hipLaunchKernelGGL(k_pack_scan, dim3(1), dim3(1024), 0, s, w, ntile);
+  hipLaunchKernelGGL(k_pack_scatter, dim3((uint32_t)ntile), dim3(PRETOK_TPB), 0,
+                     s, t, w);
+  launch_ev(k_bpe_pack, dim3(PACK_BLOCKS), dim3(256), s, nullptr, stop, t, w);
   return hipGetLastError();
 }
 
@@ -777,17 +905,9 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
     if (len > 64) continue;  // wave-uniform
-    if (hist) wave_bpe<false, true, true>(t, w, (int64_t)a, lane, lane < len, 0, len);
-    else wave_bpe<true, false, true>(t, w, (int64_t)a, lane, lane < len, 0, len);
+    if (hist) wave_bpe<false, true, true>(t, w, (int64_t)a, (int64_t)a + lane, lane, lane < len, 0, len);
+    else wave_bpe<true, false, true>(t, w, (int64_t)a, (int64_t)a + lane, lane, lane < len, 0, len);
   }
-}
-
-hipError_t launch_bpe_queue(const DevTables& t, const DevWork& w,
-                            hipStream_t s) {
-  hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
-                     (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
-                     w.long_cap, 0);
-  return hipGetLastError();
 }
 
 // ------------------------------------------------- 3. long-piece BPE
@@ -1135,7 +1255,10 @@ __global__ __launch_bounds__(64) void k_long_prep(DevTables t, DevWork w) {
   if (n > w.long_cap) n = w.long_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
   for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
-    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    // k_pretok queued the start only; the end is the next start bit
+    const uint32_t a = w.longlist[2 * k];
+    const uint32_t b = (uint32_t)piece_end(w, a);
+    w.longlist[2 * k + 1] = b;
     if (b - a <= (uint32_t)WIDE_MAX) continue;
     if (t.ignore_merges) {
       const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
@@ -1192,7 +1315,7 @@ __global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
     const int pe = gt ? __builtin_ctzll(gt) : 64;
     const bool elig = (L >> lane) & 1;
     const uint64_t live =
-        wave_bpe<false, false, false>(t, w, base, lane, elig, ps, pe);
+        wave_bpe<false, false, false>(t, w, base, base + lane, lane, elig, ps, pe);
     if (lane == 0) {
       if (phase == 0) {
         cut16[4 * v + 1] = (uint16_t)(live >> 16);
@@ -1213,8 +1336,9 @@ __device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
   return wd >= 0 && ((d[wd >> 6] >> (wd & 63)) & 1);
 }
 
-// Segment pass over the long-piece bytes (grid windows as in k_bpe_small,
-// with histories). Segments that fit no grid window go to seglist. With
+// Segment pass over the long-piece bytes (64-byte grid windows, aligned and
+// shifted by 32, with histories). Segments that fit no grid window go to
+// seglist. With
 // all == 0 (a repair pass) only windows touching a dirty word are redone.
 __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
                                                        int64_t nwin, int all) {
@@ -1247,7 +1371,7 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
       if (!fits_a_grid(pos, b))
         push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
     }
-    wave_bpe<false, true, true>(t, w, base, lane, elig, ps, pe);
+    wave_bpe<false, true, true>(t, w, base, base + lane, lane, elig, ps, pe);
   }
 }
 
@@ -1378,15 +1502,6 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 }
 
 // ------------------------------------------------------ 4. compaction
-
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(v, d);
-    if (lane >= d) v += o;
-  }
-  return v;
-}
 
 // exclusive scan of one value per thread over a 256-thread block
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {

@@ -90,9 +90,11 @@ uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
 }
 
 // Compact pair table (see pair_lookup in tk_device.hip): 16-byte buckets of
-// two slots at a load of at most 0.6. Returns false when the artifact
-// does not fit the packing (ids >= 2^18, ranks >= 2^19 - 1); the engine then
-// probes the interleaved boundary table instead.
+// two slots at a load of at most 0.3 (at most 0.15 if the displacement
+// limit needs a larger table). Entries go in by rank, so the frequent low-rank rules sit in their
+// home bucket. Returns false when the artifact does not fit the packing
+// (ids >= 2^18, ranks >= 2^19 - 1); the engine then probes the interleaved
+// boundary table instead.
 bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
                          uint64_t count, std::vector<uint64_t>& out,
                          uint32_t& bits) {
@@ -109,21 +111,24 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
   std::sort(ent.begin(), ent.end(), [](const auto& a, const auto& b) {
     return a.second < b.second;
   });
-  bits = 13;
-  while ((2ULL << bits) * 6 < ent.size() * 10) ++bits;
+  // load <= 0.3: a lookup of a pair without a rule (about half of all
+  // lookups) then ends in its home bucket
+  bits = tk::CTAB_MIN_BITS;
+  while ((2ULL << bits) * 3 < ent.size() * 10) ++bits;
   for (; bits <= 22; ++bits) {
     const uint64_t nbk = 1ULL << bits, mask = nbk - 1;
     out.assign(nbk * 2, ~0ULL);
     bool ok = true;
     for (const auto& e : ent) {
-      const uint64_t x = tk::perm36(e.first);
+      const uint64_t x = tk::pair_perm((uint32_t)(e.first >> 18),
+                                       (uint32_t)(e.first & 0x3FFFF));
       const uint64_t home = x & mask, tag = x >> bits;
       bool placed = false;
       for (uint64_t d = 0; d < tk::CTAB_MAX_DISP && !placed; ++d) {
         uint64_t* b = &out[((home + d) & mask) * 2];
         for (int k = 0; k < 2; ++k)
           if (b[k] == ~0ULL) {
-            b[k] = (tag << 41) | (d << 37) | e.second;
+            b[k] = (tag << 42) | (d << 37) | e.second;
             placed = true;
             break;
           }
@@ -157,7 +162,7 @@ struct tk_engine {
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
   DevBuf<int32_t> nx, pv;
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
-  DevBuf<uint32_t> hmeta, seglist, unsafe;
+  DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk;
   size_t docs_cap = 0;
   uint32_t slot = 0;  // control slot of the next call
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
@@ -228,6 +233,8 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->blkcount.alloc(nblk));
     HIP_TRY(e->blkprefix.alloc(nblk));
     HIP_TRY(e->out.alloc(need));
+    HIP_TRY(e->plist.alloc((size_t)tk::pack_off((int64_t)need, tk::PACK_CLASSES)));
+    HIP_TRY(e->pblk.alloc((size_t)tk::PACK_CLASSES * tk::pretok_tiles((int64_t)need)));
     e->cap = need;
   }
   if (n_docs + 1 > e->docs_cap) {
@@ -272,6 +279,10 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.nfail = ctrl + tk::CTRL_FAIL;
   w.dirty_cur = e->dirty_cur.p;
   w.dirty_next = e->dirty_next.p;
+  w.plist = e->plist.p;
+  w.pblk = e->pblk.p;
+  w.pcount = ctrl + tk::CTRL_PCOUNT;
+  w.pnext = ctrl + tk::CTRL_PNEXT;
   w.ctrl_next = e->ctrl.p + (e->slot ^ 1) * tk::CTRL_WORDS;
   w.clear_words = (int64_t)(nb / 64 + 4);
   w.clear_dwords = w.clear_words / 64 + 2;
@@ -315,8 +326,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   auto at = [&](int k) { return tv ? tv[k] : nullptr; };
   HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
-  HIP_TRY(tk::launch_bpe_small(e->t, w, s, nullptr, at(2)));
-  HIP_TRY(tk::launch_bpe_queue(e->t, w, s));
+  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));
   HIP_TRY(tk::launch_long_prep(e->t, w, s, e->t.cert ? nullptr : at(3)));
   if (e->t.cert) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s));
