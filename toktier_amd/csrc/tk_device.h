@@ -98,7 +98,9 @@ struct DevWork {
   uint32_t* plist;       // piece starts by length class
   uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
   uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
-  uint32_t* pnext;       // next work unit (ctrl)
+  uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
+  uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
+  uint32_t seq;          // call number written to gate[GATE_SEQ]
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
   int64_t clear_words;   // inlong / failm words
@@ -107,8 +109,10 @@ struct DevWork {
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
-              CTRL_FAIL = 4, CTRL_PCOUNT = 16, CTRL_PNEXT = 29,
-              CTRL_WORDS = 32;
+              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_WORDS = 32;
+// gate words in host memory, written by k_pack_scan: the host learns early
+// whether the cut / certify stages have any work
+constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_WORDS = 4;
 // length classes of the packed short-piece BPE (counts at CTRL_PCOUNT)
 constexpr int PACK_CLASSES = 13;
 constexpr int PACK_BLOCKS = 2048;
@@ -146,7 +150,9 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop = nullptr);
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s, hipEvent_t stop = nullptr);
+                            hipStream_t s);
+hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop = nullptr);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,

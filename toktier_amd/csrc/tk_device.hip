@@ -812,20 +812,50 @@ __device__ __forceinline__ int64_t piece_end(const DevWork& w, int64_t a) {
   return seg_end_after(wd + 1, [&](int64_t x) { return w.starts[x]; });
 }
 
-// exclusive prefix of each class's per-tile counts (one wave per class)
+// exclusive prefix of each class's per-tile counts: the counts are staged
+// in LDS (coalesced loads, all in flight at once), one wave scans a class
+constexpr int PACK_SCAN_LDS = 12288;  // counts held in LDS per chunk
 __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
+  __shared__ uint32_t cnt[PACK_SCAN_LDS];
+  __shared__ uint32_t carry[PACK_CLASSES];
   const int lane = threadIdx.x & 63, c = threadIdx.x >> 6;
-  if (c >= PACK_CLASSES) return;  // whole wave
-  uint32_t* cnt = w.pblk + (int64_t)c * ntile;
-  uint32_t run = 0;
-  for (int64_t j0 = 0; j0 < ntile; j0 += 64) {
-    const int64_t j = j0 + lane;
-    const uint32_t v = j < ntile ? cnt[j] : 0u;
-    const uint32_t inc = wave_incl_scan(v, lane);
-    if (j < ntile) cnt[j] = run + inc - v;
-    run += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+  if (threadIdx.x < PACK_CLASSES) carry[threadIdx.x] = 0;
+  // chunks of tiles so that PACK_CLASSES rows fit the LDS
+  const int64_t chunk = PACK_SCAN_LDS / PACK_CLASSES;
+  for (int64_t t0 = 0; t0 < ntile; t0 += chunk) {
+    const int64_t n = ntile - t0 < chunk ? ntile - t0 : chunk;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < PACK_CLASSES * n; i += 1024) {
+      const int64_t cc = i / n, j = i - cc * n;
+      cnt[i] = w.pblk[cc * ntile + t0 + j];
+    }
+    __syncthreads();
+    if (c < PACK_CLASSES) {
+      uint32_t run = carry[c];
+      for (int64_t j0 = 0; j0 < n; j0 += 64) {
+        const int64_t j = j0 + lane;
+        const uint32_t v = j < n ? cnt[c * n + j] : 0u;
+        const uint32_t inc = wave_incl_scan(v, lane);
+        if (j < n) cnt[c * n + j] = run + inc - v;
+        run += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+      }
+      if (lane == 0) carry[c] = run;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < PACK_CLASSES * n; i += 1024) {
+      const int64_t cc = i / n, j = i - cc * n;
+      w.pblk[cc * ntile + t0 + j] = cnt[i];
+    }
   }
-  if (lane == 0) w.pcount[c] = run;
+  __syncthreads();
+  if (threadIdx.x < PACK_CLASSES) w.pcount[threadIdx.x] = carry[threadIdx.x];
+  if (threadIdx.x == 0 && w.gate) {
+    // k_long_prep (the previous kernel) has counted the pieces over WIDE_MAX
+    w.gate[GATE_BIG] = *w.nbig;
+    __threadfence_system();
+    w.gate[GATE_SEQ] = w.seq;
+    __threadfence_system();
+  }
 }
 
 // list every packed piece of a tile at its class offset (the order inside
@@ -1250,37 +1280,60 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
 // Queued pieces over WIDE_MAX bytes: a whole-vocabulary hit
 // (ignore_merges), the serial path when certification is off, else mark
 // their bytes in inlong for the cut / segment / certify stages.
-__global__ __launch_bounds__(64) void k_long_prep(DevTables t, DevWork w) {
+__global__ __launch_bounds__(256) void k_long_prep(DevTables t, DevWork w) {
+  __shared__ uint32_t nbig;
+  if (threadIdx.x == 0) nbig = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
-    // k_pretok queued the start only; the end is the next start bit
-    const uint32_t a = w.longlist[2 * k];
-    const uint32_t b = (uint32_t)piece_end(w, a);
-    w.longlist[2 * k + 1] = b;
-    if (b - a <= (uint32_t)WIDE_MAX) continue;
-    if (t.ignore_merges) {
-      const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
-      if (hit >= 0) {
-        w.tok[a] = (uint32_t)hit;
-        for (uint32_t p = a + 1; p < b; ++p) w.tok[p] = INVALID_ID;
+  const uint32_t waves = gridDim.x * (blockDim.x / 64);
+  // 64 entries per wave and step: lane j resolves entry k0 + j, then the
+  // wave handles the entries over WIDE_MAX bytes one by one
+  for (uint32_t k0 = (blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 64;
+       k0 < n; k0 += waves * 64) {
+    const uint32_t k = k0 + lane;
+    uint32_t a = 0, b = 0;
+    if (k < n) {
+      // k_pretok queued the start only; the end is the next start bit
+      a = w.longlist[2 * k];
+      b = (uint32_t)piece_end(w, a);
+      w.longlist[2 * k + 1] = b;
+    }
+    uint64_t big = __ballot(k < n && b - a > (uint32_t)WIDE_MAX);
+    if (lane == 0 && big) atomicAdd(&nbig, (uint32_t)__popcll(big));
+    while (big) {  // wave-uniform
+      const int j = __builtin_ctzll(big);
+      big &= big - 1;
+      const uint32_t pa = __shfl(a, j), pb = __shfl(b, j);
+      if (t.ignore_merges) {
+        int32_t hit = -1;
+        if (lane == 0) hit = vocab_lookup(t, w.text + pa, (int64_t)(pb - pa));
+        hit = __shfl(hit, 0);
+        if (hit >= 0) {
+          for (uint32_t p = pa + lane; p < pb; p += 64)
+            w.tok[p] = p == pa ? (uint32_t)hit : INVALID_ID;
+          continue;
+        }
+      }
+      if (!t.cert) {
+        if (lane == 0) bpe_serial(t, w, pa, pb, false, false);
         continue;
       }
-    }
-    if (!t.cert) {
-      bpe_serial(t, w, a, b, false, false);
-      continue;
-    }
-    const uint32_t wa = a >> 6, wb = (b - 1) >> 6;
-    for (uint32_t wd = wa; wd <= wb; ++wd) {
-      const uint32_t lo = wd == wa ? (a & 63) : 0;
-      const uint32_t hi = wd == wb ? ((b - 1) & 63) + 1 : 64;
-      const uint64_t m = lanes_in((int)lo, (int)hi);
-      if (m == ~0ULL) w.inlong[wd] = m;  // a whole word of one piece
-      else atomicOr(reinterpret_cast<unsigned long long*>(&w.inlong[wd]), m);
+      // mark the piece's bytes: whole words directly, the two edge words
+      // (shared with neighbouring pieces) with an atomic OR
+      const uint32_t wa = pa >> 6, wb = (pb - 1) >> 6;
+      for (uint32_t wd = wa + lane; wd <= wb; wd += 64) {
+        const uint32_t lo = wd == wa ? (pa & 63) : 0;
+        const uint32_t hi = wd == wb ? ((pb - 1) & 63) + 1 : 64;
+        const uint64_t m = lanes_in((int)lo, (int)hi);
+        if (m == ~0ULL) w.inlong[wd] = m;
+        else atomicOr(reinterpret_cast<unsigned long long*>(&w.inlong[wd]), m);
+      }
     }
   }
+  __syncthreads();
+  if (threadIdx.x == 0 && nbig) atomicAdd(w.nbig, nbig);
 }
 
 __device__ __forceinline__ uint64_t inlong_window(const DevWork& w, int64_t v,
@@ -1454,8 +1507,13 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
 }
 
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s, hipEvent_t stop) {
-  hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(64), 0, s, t, w);
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(256), 0, s, t, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop) {
   // pieces of 65..WIDE_MAX bytes are merged whole, one wave each
   launch_ev(k_bpe_wide, dim3(2048), dim3(256), s, nullptr, stop, t, w,
             (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,

@@ -16,6 +16,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -166,6 +168,10 @@ struct tk_engine {
   size_t docs_cap = 0;
   uint32_t slot = 0;  // control slot of the next call
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
+  // gate words: host memory the device writes mid-pipeline
+  volatile uint32_t* gate = nullptr;
+  uint32_t* gate_dev = nullptr;
+  uint32_t seq = 0;
   // timing
   bool timing = false;
   hipEvent_t ev[8] = {};
@@ -282,7 +288,9 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.plist = e->plist.p;
   w.pblk = e->pblk.p;
   w.pcount = ctrl + tk::CTRL_PCOUNT;
-  w.pnext = ctrl + tk::CTRL_PNEXT;
+  w.nbig = ctrl + tk::CTRL_BIG;
+  w.gate = e->gate_dev;
+  w.seq = e->seq;
   w.ctrl_next = e->ctrl.p + (e->slot ^ 1) * tk::CTRL_WORDS;
   w.clear_words = (int64_t)(nb / 64 + 4);
   w.clear_dwords = w.clear_words / 64 + 2;
@@ -296,6 +304,25 @@ int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
   return TK_OK;
+}
+
+// Wait until k_pack_scan of call `seq` has written the gate words (a
+// spin on host memory). A device fault would stop the writer, so after a
+// generous bound the stream is synchronized to surface its error.
+int wait_gate(tk_engine* e, uint32_t seq, hipStream_t s) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint64_t spin = 0;; ++spin) {
+    if (e->gate[tk::GATE_SEQ] == seq) {
+      std::atomic_thread_fence(std::memory_order_acquire);
+      return TK_OK;
+    }
+    if ((spin & 1023) == 1023 &&
+        std::chrono::steady_clock::now() - t0 > std::chrono::seconds(10)) {
+      HIP_TRY(hipStreamSynchronize(s));
+      if (e->gate[tk::GATE_SEQ] == seq) return TK_OK;
+      return fail(TK_E_INTERNAL, "gate words were not written");
+    }
+  }
 }
 
 float elapsed_us(hipEvent_t a, hipEvent_t b) {
@@ -314,6 +341,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
                  const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
                  uint32_t* out, size_t out_cap, uint32_t* status,
                  uint32_t* total) {
+  ++e->seq;
   const tk::DevWork w =
       make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap);
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
@@ -326,9 +354,19 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   auto at = [&](int k) { return tv ? tv[k] : nullptr; };
   HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
-  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));
-  HIP_TRY(tk::launch_long_prep(e->t, w, s, e->t.cert ? nullptr : at(3)));
+  HIP_TRY(tk::launch_long_prep(e->t, w, s));
+  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));  // k_pack_scan writes the gate
+  // The cut / certify stages run only when a piece over WIDE_MAX bytes
+  // exists: the device tells through the gate words while the packed
+  // merge is still running, so the decision costs no device time.
+  uint32_t big = 0;
   if (e->t.cert) {
+    int grc = wait_gate(e, w.seq, s);
+    if (grc != TK_OK) return grc;
+    big = e->gate[tk::GATE_BIG];
+  }
+  HIP_TRY(tk::launch_bpe_wide(e->t, w, s, big ? nullptr : at(3)));
+  if (big) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s));
     HIP_TRY(tk::launch_long_segments(e->t, w, 1, s));
     HIP_TRY(tk::launch_certify(e->t, w, 1, s, at(3)));
@@ -514,6 +552,18 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipHostMalloc(reinterpret_cast<void**>(&e->host_ctrl),
                     tk::CTRL_WORDS * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipHostMalloc failed"));
+  {
+    void* g = nullptr;
+    if (hipHostMalloc(&g, tk::GATE_WORDS * sizeof(uint32_t),
+                      hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipHostMalloc (gate) failed"));
+    std::memset(g, 0, tk::GATE_WORDS * sizeof(uint32_t));
+    e->gate = static_cast<volatile uint32_t*>(g);
+    void* gd = nullptr;
+    if (hipHostGetDevicePointer(&gd, g, 0) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipHostGetDevicePointer failed"));
+    e->gate_dev = static_cast<uint32_t*>(gd);
+  }
 
   // interleave key/value so one 16-byte load reads a whole slot
   std::vector<ulonglong2> pairs(n_pairs);
@@ -600,6 +650,7 @@ void tk_engine_close(tk_engine* e) {
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->host_ctrl) (void)hipHostFree(e->host_ctrl);
+  if (e->gate) (void)hipHostFree(const_cast<uint32_t*>(e->gate));
   delete e;
 }
 
