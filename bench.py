@@ -155,7 +155,7 @@ def main() -> int:
     n_tok = float(np.mean([a.size for a in ids_dev]))
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
     st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["k_pretok", "short pieces (k_pieces, k_bpe_pack)", "long pieces (k_long_prep, k_bpe_wide, k_long_*, k_certify)", "compaction (k_count, k_scan, k_compact)"]
+    names = ["k_pretok", "short pieces (k_long_prep, k_pack_scan, k_pack_scatter, k_bpe_pack)", "long pieces past the short ones (k_bpe_wide, k_long_*, k_certify; side stream)", "compaction (k_count, k_scan, k_compact)"]
     avg = st[:, :4].mean(axis=0)
     dom = int(np.argmax(avg))
     b_alg = n_bytes + 4.0 * n_tok

@@ -175,6 +175,9 @@ struct tk_engine {
   // timing
   bool timing = false;
   hipEvent_t ev[8] = {};
+  // side stream for the long-piece stages, and its fork / join events
+  hipStream_t stream2 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   double last_us[5] = {};
   size_t last_passes = 0;
 };
@@ -348,13 +351,15 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   hipEvent_t* ev = e->ev;
   // Stage boundaries, timestamps taken by the dispatches themselves:
   // ev[0] start of k_pretok, ev[1..4] the end of the last dispatch of each
-  // stage. (Each timed dispatch delays the next one by a few microseconds,
-  // so the events sit on as few dispatches as the breakdown allows.)
+  // stage; the long-piece stage (ev[3]) runs on the side stream alongside
+  // the packed merge. (Each timed dispatch delays the next one by a few
+  // microseconds, so the events sit on as few dispatches as they can.)
   hipEvent_t* tv = e->timing ? ev : nullptr;
   auto at = [&](int k) { return tv ? tv[k] : nullptr; };
   HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_long_prep(e->t, w, s));
+  HIP_TRY(hipEventRecord(e->ev_fork, s));  // long pieces resolved
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));  // k_pack_scan writes the gate
   // The cut / certify stages run only when a piece over WIDE_MAX bytes
   // exists: the device tells through the gate words while the packed
@@ -365,19 +370,31 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
     if (grc != TK_OK) return grc;
     big = e->gate[tk::GATE_BIG];
   }
-  HIP_TRY(tk::launch_bpe_wide(e->t, w, s, big ? nullptr : at(3)));
+  // the long-piece stages need only k_pretok and k_long_prep: they run on
+  // the side stream while the packed merge runs
+  hipStream_t s2 = e->stream2;
+  HIP_TRY(hipStreamWaitEvent(s2, e->ev_fork, 0));
+  HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, big ? nullptr : at(3)));
   if (big) {
-    HIP_TRY(tk::launch_long_windows(e->t, w, s));
-    HIP_TRY(tk::launch_long_segments(e->t, w, 1, s));
-    HIP_TRY(tk::launch_certify(e->t, w, 1, s, at(3)));
+    HIP_TRY(tk::launch_long_windows(e->t, w, s2));
+    HIP_TRY(tk::launch_long_segments(e->t, w, 1, s2));
+    HIP_TRY(tk::launch_certify(e->t, w, 1, s2, at(3)));
   }
+  HIP_TRY(hipEventRecord(e->ev_join, s2));
+  HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
   HIP_TRY(tk::launch_compact(w, s, nullptr, at(4)));
   uint32_t* h = e->host_ctrl;
   int rc = read_ctrl_words(ctrl, s, h);
   if (rc != TK_OK) return rc;
   if (e->timing) {
-    for (int k = 0; k < 4; ++k) e->last_us[k] = elapsed_us(ev[k], ev[k + 1]);
-    e->last_us[4] = elapsed_us(ev[0], ev[4]);
+    // [2]: how far the long-piece stages ran past the packed merge
+    const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
+    const double t3 = elapsed_us(ev[0], ev[3]), t4 = elapsed_us(ev[0], ev[4]);
+    e->last_us[0] = t1;
+    e->last_us[1] = t2 - t1;
+    e->last_us[2] = t3 > t2 ? t3 - t2 : 0.0;
+    e->last_us[3] = t4 - (t3 > t2 ? t3 : t2);
+    e->last_us[4] = t4;
   }
   if (h[tk::CTRL_FAIL] != 0) {
     // every pass removes at least one cut, so this ends (at worst with each
@@ -543,8 +560,12 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
     tk_engine_close(e);
     return code;
   };
-  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&e->stream2, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
+  if (hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming) != hipSuccess)
+    return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
     if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
@@ -648,7 +669,11 @@ void tk_engine_close(tk_engine* e) {
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   for (auto& ev : e->ev)
     if (ev) (void)hipEventDestroy(ev);
+  if (e->stream2) (void)hipStreamSynchronize(e->stream2);
+  if (e->ev_fork) (void)hipEventDestroy(e->ev_fork);
+  if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->stream) (void)hipStreamDestroy(e->stream);
+  if (e->stream2) (void)hipStreamDestroy(e->stream2);
   if (e->host_ctrl) (void)hipHostFree(e->host_ctrl);
   if (e->gate) (void)hipHostFree(const_cast<uint32_t*>(e->gate));
   delete e;
