@@ -18,7 +18,10 @@ Also on the JSON line:
 - ``roofline``: the dominant kernel stage's achieved bandwidth, taken as
   the per-request algorithmic bytes (UTF-8 bytes read once + 4 bytes per
   id written once) over that stage's average duration from HIP events on
-  the engine's stream, against the 8 TB/s HBM peak.
+  the engine's stream, against the 8 TB/s HBM peak. ``traffic`` is the
+  kernel's measured HBM bytes per launch from the committed rocprofv3
+  counter summary (profiles/c<config>_traffic.json) when it was taken on the
+  library build being run, else null.
 - ``cpu_baseline``: the C restatement (oracle) timed on this host's cores
   on a bounded sample of the same workload, one thread.
 
@@ -46,6 +49,22 @@ TARGET_MS = 3.88
 
 def pct(xs, q):
     return float(np.percentile(np.asarray(xs), q))
+
+
+def measured_traffic(config: int, kernel: str):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled by
+    a plain copy's reading) from the committed rocprofv3 summary, when that
+    summary was taken on this very library build; else None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", f"c{config}_traffic.json")) as f:
+            d = json.load(f)
+        with open(os.path.join(ROOT, "toktier_amd", "_lib", "manifest.json")) as f:
+            m = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if d.get("library_sha256") != m.get("sha256") or d.get("kernel") != kernel:
+        return None
+    return int(d["fetch_bytes"] + d["write_bytes"])
 
 
 def main() -> int:
@@ -155,7 +174,7 @@ def main() -> int:
     n_tok = float(np.mean([a.size for a in ids_dev]))
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
     st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["k_pretok", "short pieces (k_long_prep, k_pack_scan, k_pack_scatter, k_bpe_pack)", "long pieces past the short ones (k_bpe_wide, k_long_*, k_certify; side stream)", "compaction (k_count, k_scan, k_compact)"]
+    names = ["pretokenize + piece lists (k_pretok, k_long_prep, k_pack_scan, k_pack_scatter)", "k_bpe_pack", "long pieces past k_bpe_pack (k_bpe_wide, k_long_*, k_certify; side stream)", "compaction (k_count, k_scan, k_compact)"]
     avg = st[:, :4].mean(axis=0)
     dom = int(np.argmax(avg))
     b_alg = n_bytes + 4.0 * n_tok
@@ -220,7 +239,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": None,
+            "traffic": measured_traffic(args.config, names[dom]),
             "alg_bytes_per_launch": int(b_alg),
             "path_achieved": round(b_alg / (ms_per_step * 1e-3) / 1e9, 3),
         },

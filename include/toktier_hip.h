@@ -135,10 +135,9 @@ const char* tk_engine_delivery(const tk_engine* engine);     /* "prebuilt" */
 const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
 
 /* Per-stage device times (microseconds) of the last encode on this engine,
- * from HIP events on the engine's streams: [0] pretokenize (and piece
- * sizing), [1] long-piece preparation and short-piece BPE, [2] the time the
- * long-piece BPE (run beside the short-piece BPE) went past it,
- * [3] compaction, [4] total.
+ * from HIP events on the engine's streams: [0] pretokenize and piece
+ * listing, [1] short-piece BPE, [2] the time the long-piece BPE (run beside
+ * the short-piece BPE) went past it, [3] compaction, [4] total.
  * Returns the number of values written (<= n). Timing is recorded only when
  * enabled with tk_engine_set_timing(engine, 1). */
 int tk_engine_set_timing(tk_engine* engine, int enabled);

@@ -17,16 +17,19 @@ constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
 constexpr uint32_t ST_CAPACITY = 8u;  // more ids than the output holds
 
-// Compact pair table: a bijection of the 36-bit pair key (left, right <
-// 2^18), shared by the host builder and the device probe. Two Feistel
-// rounds on the 18-bit halves; the round function is a 24-bit multiply
-// (full rate on the vector ALU) folded onto itself.
-// Slot = tag<<42 | displacement<<37 | rank<<18 | id; the bucket index is
-// the low bits of the permuted key and the tag the rest, so a slot names
-// its key exactly.
-constexpr uint32_t CTAB_MAX_DISP = 32;
-constexpr uint32_t CTAB_MIN_BITS = 14;  // tags fit 22 bits
-constexpr uint64_t CTAB_LOW = (1ULL << 37) - 1;  // rank and id bits
+// Compact pair table: 16-byte buckets of two u64 slots, two candidate
+// buckets per pair (cuckoo placement), so a lookup is two independent
+// 16-byte loads and no probe chain; at a load of about 0.6 the table is a
+// quarter of the boundary table's size and stays in an XCD's L2.
+// The pair key (left, right < 2^18) goes through a bijection of 36 bits
+// (two Feistel rounds on the 18-bit halves; the round function is a 24-bit
+// multiply, full rate on the vector ALU, folded onto itself). Its low
+// `bits` bits are the first bucket, the rest the tag; the second bucket is
+// the first XOR a hash of the tag. Slot = tag<<38 | second<<37 | rank<<18
+// | id, so (bucket, slot) names its key exactly; an empty slot is all ones,
+// which no tag reaches.
+constexpr uint32_t CTAB_MIN_BITS = 12;
+constexpr uint32_t CTAB_MAX_BITS = 22;
 __host__ __device__ __forceinline__ uint32_t pair_round(uint32_t x, uint32_t c) {
   const uint32_t p = (x & 0x3FFFFu) * c;
   return (p ^ (p >> 16)) & 0x3FFFFu;
@@ -35,6 +38,12 @@ __host__ __device__ __forceinline__ uint64_t pair_perm(uint32_t l, uint32_t r) {
   const uint32_t a = l ^ pair_round(r, 0x9E3779u);
   const uint32_t b = r ^ pair_round(a, 0x85EBCBu);
   return ((uint64_t)(a & 0x3FFFFu) << 18) | (b & 0x3FFFFu);
+}
+// second bucket of a key with first bucket b1 and tag (< 2^24)
+__host__ __device__ __forceinline__ uint32_t pair_alt(uint32_t b1, uint32_t tag,
+                                                      uint32_t bits) {
+  const uint32_t h = (tag & 0xFFFFFFu) * 0xC2B2AFu;  // a 24-bit multiply
+  return (b1 ^ (h >> (32 - bits))) & ((1u << bits) - 1);
 }
 
 // Device copies of the family tables, in the engine's own layout.
@@ -147,6 +156,8 @@ constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
 // first dispatch / the end of its last one
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
+                             hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop = nullptr);
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,

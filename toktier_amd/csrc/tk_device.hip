@@ -46,32 +46,25 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   return x ^ (x >> 31);
 }
 
-// rank<<32 | merged id, or ~0 when the pair has no merge rule.
-// The compact table (when the engine built one): 16-byte buckets of two
-// u64 slots (tk_device.h), probed linearly from the home bucket; the first
-// probe settles almost every lookup. Else the interleaved boundary table.
+// rank<<32 | merged id, or ~0 when the pair has no merge rule: the
+// compact two-choice table when the engine built one (tk_device.h), else
+// the interleaved boundary table.
 __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
                                                 uint32_t l, uint32_t r) {
   if (t.ctab) {
     if ((l | r) >= (1u << 18)) return ~0ULL;  // every rule's ids fit 18 bits
     const uint64_t x = pair_perm(l, r);
-    const uint64_t tag = x >> t.cbits;
+    const uint32_t b1 = (uint32_t)(x & t.cmask);
+    const uint32_t tag = (uint32_t)(x >> t.cbits);
+    const uint32_t b2 = pair_alt(b1, tag, t.cbits);
     const ulonglong2* tab = reinterpret_cast<const ulonglong2*>(t.ctab);
-    uint64_t i = x & t.cmask;
-    for (uint64_t d = 0; d < CTAB_MAX_DISP; ++d) {
-      const ulonglong2 b = tab[i];
-      const uint64_t want = (tag << 42) | (d << 37);
-      // an empty slot is all ones: it must never count as a match
-      const bool mx = b.x != ~0ULL && (b.x & ~CTAB_LOW) == want;
-      const bool my = b.y != ~0ULL && (b.y & ~CTAB_LOW) == want;
-      if (mx || my) {
-        const uint64_t s = mx ? b.x : b.y;
-        return (((s >> 18) & 0x7FFFF) << 32) | (s & 0x3FFFF);
-      }
-      if (b.x == ~0ULL || b.y == ~0ULL) return ~0ULL;
-      i = (i + 1) & t.cmask;
-    }
-    return ~0ULL;
+    const ulonglong2 u = tab[b1], v = tab[b2];  // independent loads
+    const uint64_t w0 = (uint64_t)tag << 1, w1 = w0 | 1;
+    const uint64_t s = (u.x >> 37) == w0 ? u.x : (u.y >> 37) == w0 ? u.y
+                     : (v.x >> 37) == w1 ? v.x : (v.y >> 37) == w1 ? v.y
+                     : ~0ULL;
+    if (s == ~0ULL) return ~0ULL;
+    return (((s >> 18) & 0x7FFFF) << 32) | (s & 0x3FFFF);
   }
   const uint64_t key = ((uint64_t)l << 32) | r;
   uint64_t i = splitmix64(key) & t.pair_mask;
@@ -825,10 +818,9 @@ __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
   for (int64_t t0 = 0; t0 < ntile; t0 += chunk) {
     const int64_t n = ntile - t0 < chunk ? ntile - t0 : chunk;
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < PACK_CLASSES * n; i += 1024) {
-      const int64_t cc = i / n, j = i - cc * n;
-      cnt[i] = w.pblk[cc * ntile + t0 + j];
-    }
+    for (int cc = 0; cc < PACK_CLASSES; ++cc)
+      for (int64_t j = threadIdx.x; j < n; j += 1024)
+        cnt[cc * n + j] = w.pblk[cc * ntile + t0 + j];
     __syncthreads();
     if (c < PACK_CLASSES) {
       uint32_t run = carry[c];
@@ -842,10 +834,9 @@ __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
       if (lane == 0) carry[c] = run;
     }
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < PACK_CLASSES * n; i += 1024) {
-      const int64_t cc = i / n, j = i - cc * n;
-      w.pblk[cc * ntile + t0 + j] = cnt[i];
-    }
+    for (int cc = 0; cc < PACK_CLASSES; ++cc)
+      for (int64_t j = threadIdx.x; j < n; j += 1024)
+        w.pblk[cc * ntile + t0 + j] = cnt[cc * n + j];
   }
   __syncthreads();
   if (threadIdx.x < PACK_CLASSES) w.pcount[threadIdx.x] = carry[threadIdx.x];
@@ -911,12 +902,17 @@ __global__ __launch_bounds__(256) void k_bpe_pack(DevTables t, DevWork w) {
   }
 }
 
-hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop) {
+hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
+                             hipStream_t s, hipEvent_t stop) {
   const int64_t ntile = pretok_tiles(w.nb);
   hipLaunchKernelGGL(k_pack_scan, dim3(1), dim3(1024), 0, s, w, ntile);
-  hipLaunchKernelGGL(k_pack_scatter, dim3((uint32_t)ntile), dim3(PRETOK_TPB), 0,
-                     s, t, w);
+  launch_ev(k_pack_scatter, dim3((uint32_t)ntile), dim3(PRETOK_TPB), s,
+            nullptr, stop, t, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop) {
   launch_ev(k_bpe_pack, dim3(PACK_BLOCKS), dim3(256), s, nullptr, stop, t, w);
   return hipGetLastError();
 }

@@ -91,12 +91,13 @@ uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
   return ~0ULL;
 }
 
-// Compact pair table (see pair_lookup in tk_device.hip): 16-byte buckets of
-// two slots at a load of at most 0.3 (at most 0.15 if the displacement
-// limit needs a larger table). Entries go in by rank, so the frequent low-rank rules sit in their
-// home bucket. Returns false when the artifact does not fit the packing
-// (ids >= 2^18, ranks >= 2^19 - 1); the engine then probes the interleaved
-// boundary table instead.
+// Compact pair table (tk_device.h): two candidate buckets of two slots per
+// pair, filled by cuckoo placement (an entry that finds both buckets full
+// displaces one of the residents to that resident's other bucket, and so
+// on), at a load of at most 0.6; a table one size larger is tried when a
+// placement walk runs too long. Returns false when the artifact does not fit
+// the packing (ids >= 2^18, ranks >= 2^19 - 1); the engine then probes the
+// interleaved boundary table instead.
 bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
                          uint64_t count, std::vector<uint64_t>& out,
                          uint32_t& bits) {
@@ -110,30 +111,48 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
       return false;
     ent.push_back({(l << 18) | r, (rank << 18) | id});
   }
-  std::sort(ent.begin(), ent.end(), [](const auto& a, const auto& b) {
-    return a.second < b.second;
-  });
-  // load <= 0.3: a lookup of a pair without a rule (about half of all
-  // lookups) then ends in its home bucket
   bits = tk::CTAB_MIN_BITS;
-  while ((2ULL << bits) * 3 < ent.size() * 10) ++bits;
-  for (; bits <= 22; ++bits) {
-    const uint64_t nbk = 1ULL << bits, mask = nbk - 1;
+  while ((2ULL << bits) * 6 < ent.size() * 10) ++bits;
+  for (; bits <= tk::CTAB_MAX_BITS; ++bits) {
+    const uint64_t nbk = 1ULL << bits;
     out.assign(nbk * 2, ~0ULL);
+    uint64_t rng = 0x2545F4914F6CDD1DULL;
     bool ok = true;
     for (const auto& e : ent) {
       const uint64_t x = tk::pair_perm((uint32_t)(e.first >> 18),
                                        (uint32_t)(e.first & 0x3FFFF));
-      const uint64_t home = x & mask, tag = x >> bits;
+      // the entry being placed: tag, first bucket, rank<<18 | id, and the
+      // bucket to try first
+      uint32_t tag = (uint32_t)(x >> bits);
+      uint32_t b1 = (uint32_t)(x & (nbk - 1));
+      uint64_t low = e.second;
+      uint32_t at = b1;
       bool placed = false;
-      for (uint64_t d = 0; d < tk::CTAB_MAX_DISP && !placed; ++d) {
-        uint64_t* b = &out[((home + d) & mask) * 2];
-        for (int k = 0; k < 2; ++k)
-          if (b[k] == ~0ULL) {
-            b[k] = (tag << 42) | (d << 37) | e.second;
-            placed = true;
-            break;
+      for (int kick = 0; kick < 512 && !placed; ++kick) {
+        const uint32_t alt = tk::pair_alt(b1, tag, bits);
+        const uint32_t other = at == b1 ? alt : b1;
+        for (const uint32_t bk : {at, other}) {
+          for (int k = 0; k < 2 && !placed; ++k) {
+            uint64_t& slot = out[(uint64_t)bk * 2 + k];
+            if (slot == ~0ULL) {
+              slot = ((uint64_t)tag << 38) | ((uint64_t)(bk != b1) << 37) | low;
+              placed = true;
+            }
           }
+          if (placed) break;
+        }
+        if (placed) break;
+        // both full: take a resident's place in `at`; the resident moves on
+        // to its other bucket (pair_alt is an involution for a fixed tag)
+        rng ^= rng << 13; rng ^= rng >> 7; rng ^= rng << 17;
+        uint64_t& victim = out[(uint64_t)at * 2 + (rng & 1)];
+        const uint64_t v = victim;
+        victim = ((uint64_t)tag << 38) | ((uint64_t)(at != b1) << 37) | low;
+        tag = (uint32_t)(v >> 38);
+        const bool vsecond = (v >> 37) & 1;
+        b1 = vsecond ? tk::pair_alt(at, tag, bits) : at;
+        low = v & ((1ULL << 37) - 1);
+        at = vsecond ? b1 : tk::pair_alt(b1, tag, bits);
       }
       if (!placed) { ok = false; break; }
     }
@@ -350,17 +369,19 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
   // Stage boundaries, timestamps taken by the dispatches themselves:
-  // ev[0] start of k_pretok, ev[1..4] the end of the last dispatch of each
-  // stage; the long-piece stage (ev[3]) runs on the side stream alongside
-  // the packed merge. (Each timed dispatch delays the next one by a few
+  // ev[0] start of k_pretok; ev[1] end of the piece listing (k_long_prep,
+  // k_pack_scan, k_pack_scatter); ev[2] end of k_bpe_pack; ev[3] end of the
+  // long-piece stages (side stream, alongside k_bpe_pack); ev[4] end of the
+  // compaction. (Each timed dispatch delays the next one by a few
   // microseconds, so the events sit on as few dispatches as they can.)
   hipEvent_t* tv = e->timing ? ev : nullptr;
   auto at = [&](int k) { return tv ? tv[k] : nullptr; };
-  HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
+  HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_long_prep(e->t, w, s));
   HIP_TRY(hipEventRecord(e->ev_fork, s));  // long pieces resolved
-  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));  // k_pack_scan writes the gate
+  HIP_TRY(tk::launch_pack_lists(e->t, w, s, at(1)));  // k_pack_scan writes the gate
+  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));
   // The cut / certify stages run only when a piece over WIDE_MAX bytes
   // exists: the device tells through the gate words while the packed
   // merge is still running, so the decision costs no device time.
