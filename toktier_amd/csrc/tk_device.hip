@@ -422,12 +422,93 @@ __device__ bool start_r50k(const C& c, const Ch& ci) {
          p_arrives(c, q3);
 }
 
+// ---- the same predicates from a fixed context, without branches on
+// loads: the character (c0), the four before it (c1..c4, nearest first;
+// hN false where the text or document ends) and the one after it (cn, hn).
+// Returns 1 (starts a piece), 0, or, when the answer needs more of the
+// run around the character: FAST_DIGITS (the digits before it decide,
+// group width over 1) or FAST_CRLF (whitespace right after a CR/LF: the
+// rest of the whitespace run decides).
+constexpr int FAST_DIGITS = -2, FAST_CRLF = -3;
+struct Ctx5 {
+  uint32_t c0, c1, c2, c3, c4, cn;  // entries (code point | class << 21)
+  bool h2, h3, h4, hn;              // c1 always exists
+};
+__device__ __forceinline__ int ecl(uint32_t e) { return (e >> 21) & 3; }
+__device__ __forceinline__ int ecp(uint32_t e) { return (int)(e & 0x1FFFFF); }
+// p_arrives of the character whose predecessor is e (present: h)
+__device__ __forceinline__ bool arrives_after(uint32_t e, bool h) {
+  return !h || (ecl(e) != CP_ && ecp(e) != ' ');
+}
+__device__ __forceinline__ bool is_stmd(int f) {
+  return f == 's' || f == 't' || f == 'm' || f == 'd';
+}
+__device__ __forceinline__ bool is_re_ve_ll(int a, int b) {
+  return (a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+         (a == 'l' && b == 'l');
+}
+
+__device__ __forceinline__ int fast_cl100k(const Ctx5& x, int dmax) {
+  const int k0 = ecl(x.c0), k1 = ecl(x.c1);
+  const int k2 = x.h2 ? ecl(x.c2) : -1, k3 = x.h3 ? ecl(x.c3) : -1;
+  if (k0 == CN_) {
+    if (dmax <= 1) return 1;
+    // digits before this one: 0, 1 or 2 decide; 3 or more need the run
+    if (k1 != CN_) return 1;
+    if (k2 != CN_) return 1 % dmax == 0;
+    if (k3 != CN_) return 2 % dmax == 0;
+    return FAST_DIGITS;
+  }
+  const int p1 = ecp(x.c1);
+  if (k0 == CL_) {
+    if (k1 != CL_) {
+      if (k1 == CS_) return crlf(p1);
+      if (k1 == CP_) return !arrives_after(x.c2, x.h2);
+      return 1;
+    }
+    const int p2 = x.h2 ? ecp(x.c2) : -1;
+    if (p2 == '\'') return is_stmd(fold(p1)) && arrives_after(x.c3, x.h3);
+    if (k2 != CL_) return 0;
+    const int p3 = x.h3 ? ecp(x.c3) : -1;
+    return p3 == '\'' && is_re_ve_ll(fold(p2), fold(p1)) &&
+           arrives_after(x.c4, x.h4);
+  }
+  if (k0 == CP_) return k1 != CP_ && p1 != ' ';
+  const bool cr_i = crlf(ecp(x.c0));
+  if (k1 != CS_) return !(k1 == CP_ && cr_i);
+  const bool cr_1 = crlf(p1);
+  if (cr_1 && !cr_i) return FAST_CRLF;
+  if (!cr_1 && !cr_i) return x.hn && ecl(x.cn) != CS_;
+  return 0;
+}
+
+__device__ __forceinline__ int fast_r50k(const Ctx5& x) {
+  const int k0 = ecl(x.c0), k1 = ecl(x.c1), p0 = ecp(x.c0), p1 = ecp(x.c1);
+  if (k0 == CS_) return k1 != CS_ || (x.hn && ecl(x.cn) != CS_);
+  if (k0 == CN_ || k0 == CP_) return k1 != k0 && p1 != ' ';
+  if (k1 != CL_) {
+    if (p1 == ' ') return 0;
+    if (p1 == '\'' && arrives_after(x.c2, x.h2)) {
+      if (is_stmd(p0)) return 0;
+      if (x.hn && is_re_ve_ll(p0, ecp(x.cn))) return 0;
+    }
+    return 1;
+  }
+  const int p2 = x.h2 ? ecp(x.c2) : -1;
+  if (p2 == '\'') return is_stmd(p1) && arrives_after(x.c3, x.h3);
+  if (!x.h2 || ecl(x.c2) != CL_) return 0;
+  const int p3 = x.h3 ? ecp(x.c3) : -1;
+  return p3 == '\'' && is_re_ve_ll(p2, p1) && arrives_after(x.c4, x.h4);
+}
+
 // ------------------------------------------------------ 1. pretokenize
 
 // One block per PT_TILE bytes (64 start words). Stage the bytes, decode
 // every position of the tile and its halo into LDS entries, then each wave
 // takes one 64-byte word at a time, lane = byte, and ballots the start bits
-// into the word.
+// into the word. Positions inside the block are 32-bit offsets from lo (the
+// first entry); RS is the ruleset, DM whether document starts are marked.
+template <int RS, bool DM>
 __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
                                                        int64_t nwords) {
   __shared__ __align__(16) uint8_t sb[PT_BYTES];
@@ -435,8 +516,19 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   __shared__ uint64_t sdm[PT_DMW];
   __shared__ uint64_t sw[PT_TILE / 64 + 1];  // the tile's start words + next
   __shared__ uint32_t lcnt[PACK_CLASSES];
+  // pieces over 64 bytes that start in the tile (at most PT_TILE / 65)
+  __shared__ uint32_t llong[PT_TILE / 64], nlong, longbase;
+  // the first 256 code points' class and NFC values, and the byte ids:
+  // LDS copies for the common case (one entry per thread)
+  static_assert(PRETOK_TPB == 256, "one table entry per thread");
+  __shared__ uint8_t lcls[256], lnfc[256];
+  __shared__ int32_t lbid[256];
   const int tid = threadIdx.x;
   if (tid < PACK_CLASSES) lcnt[tid] = 0;
+  if (tid == 0) nlong = 0;
+  lcls[tid] = t.cls[tid];
+  lnfc[tid] = w.check_nfc ? t.nfc[tid] : 0;
+  lbid[tid] = t.byte_id[tid];
   const int64_t base = (int64_t)blockIdx.x * PT_TILE;
   const int64_t nb = w.nb;
   const bool al = ((uintptr_t)w.text & 15) == 0;
@@ -472,7 +564,7 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     if (blockIdx.x == 0 && tid < CTRL_WORDS) w.ctrl_next[tid] = 0;
   }
   const int64_t wlo = (base >> 6) - 3;
-  if (w.docmask) {
+  if (DM) {
     const int64_t nmw = nb / 64 + 2;  // words the caller's mask holds
     for (int j = tid; j < PT_DMW; j += PRETOK_TPB) {
       const int64_t wd = wlo + j;
@@ -481,24 +573,49 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   }
   __syncthreads();
   const int64_t lo = base - PT_HALO;
+  // entries within the text: local offsets [jlo, jhi)
+  const int jlo = lo < 0 ? (int)(-lo) : 0;
+  const int jhi = nb - lo < PT_SPAN ? (int)(nb - lo) : PT_SPAN;
   for (int j = tid; j < PT_SPAN; j += PRETOK_TPB) {
-    const int64_t p = lo + j;
-    const int sj = j + (PT_PAD - PT_HALO);  // byte p in sb
+    const int sj = j + (PT_PAD - PT_HALO);  // its byte in sb
     uint32_t e = 0;
-    if (p >= 0 && p < nb) {
-      int back = 0, fwd = 0;
-      for (int64_t q = p; q > 0 && back < 3 && is_cont(sb[sj - back]); --q) ++back;
-      while (p + 1 + fwd < nb && fwd < 3 && is_cont(sb[sj + 1 + fwd])) ++fwd;
-      bool ok;
-      const int32_t cp = decode4(sb[sj], sb[sj + 1], sb[sj + 2], sb[sj + 3],
-                                 nb - p, &ok);
-      e = (uint32_t)cp | ((uint32_t)t.cls[cp] << 21) | ((uint32_t)back << 23) |
-          ((uint32_t)fwd << 25) | (ok ? 1u << 27 : 0u);
+    if (j >= jlo && j < jhi) {
+      const int pg = lo + j < 3 ? (int)(lo + j) : 3;  // min(position, 3)
+      const uint32_t b0 = sb[sj], b1 = sb[sj + 1], b2 = sb[sj + 2], b3 = sb[sj + 3];
+      const bool c0 = is_cont(b0), c1 = is_cont(b1), c2 = is_cont(b2), c3 = is_cont(b3);
+      const bool m1 = is_cont(sb[sj - 1]), m2 = is_cont(sb[sj - 2]);
+      // steps back to a lead over at most three continuation bytes (never
+      // below position 0); continuation bytes after this one (bytes past
+      // the text are staged as 0)
+      const int back = (pg > 0 && c0) ? ((pg > 1 && m1) ? ((pg > 2 && m2) ? 3 : 2) : 1) : 0;
+      const int fwd = c1 ? (c2 ? (c3 ? 3 : 2) : 1) : 0;
+      // UTF-8 decode, valid forms only (U+FFFD otherwise)
+      const int n = b0 < 0x80 ? 0 : b0 < 0xC0 ? 4 : b0 < 0xE0 ? 1 : b0 < 0xF0 ? 2 : b0 < 0xF8 ? 3 : 4;
+      const int64_t avail = nb - (lo + j);
+      const uint32_t v = n == 0 ? b0
+                       : n == 1 ? ((b0 & 0x1F) << 6) | (b1 & 0x3F)
+                       : n == 2 ? ((b0 & 0x0F) << 12) | ((b1 & 0x3F) << 6) | (b2 & 0x3F)
+                       : ((b0 & 0x07) << 18) | ((b1 & 0x3F) << 12) | ((b2 & 0x3F) << 6) | (b3 & 0x3F);
+      const bool bad = n == 4 || n >= avail || (n >= 1 && !c1) ||
+                       (n >= 2 && !c2) || (n >= 3 && !c3) ||
+                       (n == 1 && v < 0x80) || (n == 2 && v < 0x800) ||
+                       (n == 3 && v < 0x10000) || v > 0x10FFFF ||
+                       (v >= 0xD800 && v <= 0xDFFF);
+      const uint32_t cp = bad ? 0xFFFDu : v;
+      const uint32_t cl = cp < 256 ? lcls[cp] : t.cls[cp];
+      e = cp | (cl << 21) | ((uint32_t)back << 23) | ((uint32_t)fwd << 25) |
+          (bad ? 0u : 1u << 27);
     }
     se[j] = e;
   }
   __syncthreads();
-  const LCtx c{GCtx{w.text, nb, w.docmask, t.cls}, se, lo, sdm, wlo};
+  const LCtx c{GCtx{w.text, nb, DM ? w.docmask : nullptr, t.cls}, se, lo, sdm, wlo};
+  // document start at local offset L: position 0, or a marked doc head
+  const int Lz = lo <= 0 ? (int)(-lo) : -1;
+  auto ds = [&](int L) { return DM ? c.ds(lo + L) : L == Lz; };
+  auto prv = [&](int L) {  // local offset of the character before L
+    return L - 1 - (int)((se[L - 1] >> 23) & 3);
+  };
   const int lane = tid & 63, wv = tid >> 6;
   uint32_t st = 0;
   // the tile's words, and the first word after it (the next block writes
@@ -510,10 +627,18 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
       continue;
     }
     const int64_t i = base + 64 * k + lane;
+    const int Li = PT_HALO + 64 * k + lane;  // i - lo
     const int sj = 64 * k + lane + PT_PAD;
+    // ASCII byte kinds across the word (bytes past the text are 0): the
+    // run-level cases below read them instead of walking the run
+    const uint32_t bb = sb[sj];
+    const uint64_t mWS = __ballot(bb == ' ' || bb == '\t' || bb == 0x0B || bb == 0x0C);
+    const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
+    const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
+    const uint64_t mHI = __ballot(bb >= 0x80);
     bool s = true;  // sentinel starts past the text
     if (i < nb) {
-      const uint8_t b = sb[sj];
+      const uint8_t b = (uint8_t)bb;
       if (is_cont(b)) {
         // a continuation byte must be claimed by a lead at most 3 back
         int back = 1;
@@ -528,18 +653,112 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
         if (!ok) st |= ST_UTF8;
         s = false;
       } else {
-        const uint32_t e = se[i - lo];
+        const uint32_t e = se[Li];
         if (!((e >> 27) & 1)) st |= ST_UTF8;
-        const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
-        const bool ds = c.ds(i);
-        s = ds || (t.ruleset == 1 ? start_r50k(c, ci)
-                                  : start_cl100k(c, ci, t.dmax));
+        const bool d0 = ds(Li);
+        uint32_t e1 = 0;
+        if (d0) {
+          s = true;
+        } else {
+          // the fixed context: every offset used lies in the LDS span (tile
+          // positions are at least PT_HALO from either end, and the four
+          // characters back cover at most 16 bytes); the one after is
+          // checked
+          Ctx5 x;
+          x.c0 = e;
+          const int L1 = prv(Li);
+          x.c1 = e1 = se[L1];
+          x.h2 = !ds(L1);
+          const int L2 = x.h2 ? prv(L1) : L1;
+          x.c2 = se[L2];
+          x.h3 = x.h2 && !ds(L2);
+          const int L3 = x.h3 ? prv(L2) : L2;
+          x.c3 = se[L3];
+          x.h4 = x.h3 && !ds(L3);
+          const int L4 = x.h4 ? prv(L3) : L3;
+          x.c4 = se[L4];
+          const int Ln = Li + 1 + (int)((e >> 25) & 3);
+          const bool nin = Ln < PT_SPAN;
+          x.hn = lo + Ln < nb && !ds(Ln);
+          x.cn = nin ? se[Ln] : 0u;
+          int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
+          const uint64_t below = (1ULL << lane) - 1;
+          if (r == FAST_DIGITS && !DM) {
+            // the ASCII digits before i, when the word shows where they begin
+            const uint64_t nd_ = ~mDG & below;
+            if (nd_ && !((mHI >> (63 - __builtin_clzll(nd_))) & 1))
+              r = (lane - 1 - (63 - __builtin_clzll(nd_))) % t.dmax == 0;
+          } else if (r == FAST_CRLF && !DM && bb < 0x80) {
+            // another CR/LF ahead in the run: it shows in the word before
+            // the first byte that is neither (unless that byte is not ASCII)
+            const uint64_t above = ~mask_le(lane);
+            const uint64_t stop = ~(mWS | mCR) & above;
+            const int f = stop ? __builtin_ctzll(stop) : 64;
+            const int g = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
+            if (g < f) {
+              // then the char before the CR/LF run that precedes i
+              const uint64_t nc = ~mCR & below;
+              if (nc) {
+                const int h = 63 - __builtin_clzll(nc);
+                if ((mWS >> h) & 1) r = 0;
+                else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
+              }
+            } else if (f < 64 && !((mHI >> f) & 1)) {
+              r = 1;
+            }
+          }
+          if (r == FAST_DIGITS) {
+            // \p{N}{1,K}: count the digits before i inside the span
+            int L = L3, nd = 3;
+            r = -1;
+            for (;;) {
+              if (ds(L)) { r = nd % t.dmax == 0; break; }
+              if (L - 1 < 0) break;  // past the span: general path
+              const int Lr = prv(L);
+              if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
+              ++nd;
+              L = Lr;
+            }
+          } else if (r == FAST_CRLF) {
+            // end of \s*[\r\n]+ unless another CR/LF follows in the run;
+            // then the first char the P match's [\r\n]* left over
+            r = -1;
+            bool more = false, known = false;
+            for (int L = Ln;;) {
+              if (lo + L >= nb || ds(L)) { known = true; break; }
+              if (L >= PT_SPAN) break;
+              const uint32_t eq = se[L];
+              if (ecl(eq) != CS_) { known = true; break; }
+              if (crlf(ecp(eq))) { more = known = true; break; }
+              L += 1 + (int)((eq >> 25) & 3);
+            }
+            if (known && !more) r = 1;
+            if (known && more) {
+              for (int L = L1;;) {
+                if (ds(L)) { r = 0; break; }
+                if (L - 1 < 0) break;
+                const int Lr = prv(L);
+                const uint32_t ex = se[Lr];
+                if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
+                if (!crlf(ecp(ex))) { r = 0; break; }
+                L = Lr;
+              }
+            }
+          }
+          if (r < 0) {
+            const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+            r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
+          }
+          s = r != 0;
+        }
         if (w.check_nfc) {
-          const uint8_t v = t.nfc[ci.cp];
+          const uint32_t cp = e & 0x1FFFFF;
+          const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
           if (v == 255) {
             st |= ST_NFC;
-          } else if (v != 0 && !ds) {
-            if (t.nfc[c.at(c.prev(i)).cp] > v) st |= ST_NFC;
+          } else if (v != 0 && !d0) {
+            const uint32_t pc = e1 & 0x1FFFFF;
+            if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
           }
         }
       }
@@ -563,22 +782,36 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     if (kind >= 0) {
       atomicAdd(&lcnt[kind], 1u);
     } else if (kind == PIECE_ONE) {
-      const int32_t id = t.byte_id[sb[64 * k + lane + PT_PAD]];
+      const int32_t id = lbid[sb[64 * k + lane + PT_PAD]];
       w.tok[a] = id >= 0 ? (uint32_t)id : INVALID_ID;
     } else if (kind == PIECE_TWO) {
       const uint32_t b0 = sb[64 * k + lane + PT_PAD];
       const uint32_t b1 = sb[64 * k + lane + PT_PAD + 1];
-      const int32_t i0 = t.byte_id[b0], i1 = t.byte_id[b1];
+      const int32_t i0 = lbid[b0], i1 = lbid[b1];
       const uint64_t mg = (i0 >= 0 && i1 >= 0) ? t.bytepair[(b0 << 8) | b1] : ~0ULL;
       w.tok[a] = mg != ~0ULL ? (uint32_t)mg : i0 >= 0 ? (uint32_t)i0 : INVALID_ID;
       w.tok[a + 1] = (mg == ~0ULL && i1 >= 0) ? (uint32_t)i1 : INVALID_ID;
     } else if (kind == PIECE_LONG) {
-      // the end is filled in by k_long_prep once every start word is known
-      push_pair(w.longlist, w.longcount, w.long_cap, w.status, a, 0);
+      llong[atomicAdd(&nlong, 1u)] = (uint32_t)a;
     }
   }
   __syncthreads();
   if (tid < PACK_CLASSES) w.pblk[(int64_t)tid * gridDim.x + blockIdx.x] = lcnt[tid];
+  // queue the long pieces with one counter update per tile; their ends are
+  // filled in by k_long_prep once every start word is known
+  if (nlong) {
+    if (tid == 0) longbase = atomicAdd(w.longcount, nlong);
+    __syncthreads();
+    for (uint32_t j = tid; j < nlong; j += PRETOK_TPB) {
+      const uint32_t k = longbase + j;
+      if (k < w.long_cap) {
+        w.longlist[2 * k] = llong[j];
+        w.longlist[2 * k + 1] = 0;
+      } else {
+        atomicOr(w.status, ST_LONGOVF);
+      }
+    }
+  }
 }
 
 // Launch, optionally with timing events taken from the dispatch itself
@@ -595,8 +828,15 @@ void launch_ev(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start, hipEvent_t stop) {
   const int64_t nwords = (w.nb + 63) / 64 + 2;  // words 0..nwin+1
-  launch_ev(k_pretok, dim3((uint32_t)pretok_tiles(w.nb)), dim3(PRETOK_TPB), s,
-            start, stop, t, w, nwords);
+  const dim3 g((uint32_t)pretok_tiles(w.nb)), b(PRETOK_TPB);
+  const bool dm = w.docmask != nullptr;
+  if (t.ruleset == 1) {
+    if (dm) launch_ev(k_pretok<1, true>, g, b, s, start, stop, t, w, nwords);
+    else launch_ev(k_pretok<1, false>, g, b, s, start, stop, t, w, nwords);
+  } else {
+    if (dm) launch_ev(k_pretok<0, true>, g, b, s, start, stop, t, w, nwords);
+    else launch_ev(k_pretok<0, false>, g, b, s, start, stop, t, w, nwords);
+  }
   return hipGetLastError();
 }
 
