@@ -119,9 +119,12 @@ struct DevWork {
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_WORDS = 32;
-// gate words in host memory, written by k_pack_scan: the host learns early
-// whether the cut / certify stages have any work
-constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_WORDS = 4;
+// gate words in host memory: k_pack_scan writes GATE_SEQ / GATE_BIG (the
+// host learns early whether the cut / certify stages have any work), k_scan
+// writes the request's outcome (status, id count, failed cuts) and then
+// GATE_DONE, so no copy is needed to read it
+constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
+              GATE_FAIL = 4, GATE_DONE = 5, GATE_WORDS = 8;
 // length classes of the packed short-piece BPE (counts at CTRL_PCOUNT)
 constexpr int PACK_CLASSES = 13;
 constexpr int PACK_BLOCKS = 2048;

@@ -1852,6 +1852,15 @@ __global__ __launch_bounds__(SCAN_TPB) void k_scan(DevWork w, int64_t nblk) {
     w.blkprefix[nblk] = tot;
     w.status[1] = tot;
     if (tot > w.out_cap) atomicOr(w.status, ST_CAPACITY);
+    if (w.gate) {
+      // every stage that sets status bits or failed cuts has finished
+      w.gate[GATE_STATUS] = atomicOr(w.status, 0u);
+      w.gate[GATE_TOTAL] = tot;
+      w.gate[GATE_FAIL] = *w.nfail;
+      __threadfence_system();
+      w.gate[GATE_DONE] = w.seq;
+      __threadfence_system();
+    }
   }
   for (int64_t k = lo; k < lo + per && k < nblk; ++k) {
     w.blkprefix[k] = acc;

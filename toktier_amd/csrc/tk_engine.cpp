@@ -404,9 +404,17 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   HIP_TRY(hipEventRecord(e->ev_join, s2));
   HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
   HIP_TRY(tk::launch_compact(w, s, nullptr, at(4)));
+  // k_scan has left the outcome in the gate words: no read-back copy
+  HIP_TRY(hipStreamSynchronize(s));
   uint32_t* h = e->host_ctrl;
-  int rc = read_ctrl_words(ctrl, s, h);
-  if (rc != TK_OK) return rc;
+  if (e->gate[tk::GATE_DONE] != w.seq)
+    return fail(TK_E_INTERNAL, "outcome words were not written");
+  h[tk::CTRL_STATUS] = e->gate[tk::GATE_STATUS];
+  h[tk::CTRL_TOTAL] = e->gate[tk::GATE_TOTAL];
+  h[tk::CTRL_FAIL] = e->gate[tk::GATE_FAIL];
+  if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
+    return fail(TK_E_INTERNAL, "piece queue overflow");
+  int rc = TK_OK;
   if (e->timing) {
     // [2]: how far the long-piece stages ran past the packed merge
     const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
