@@ -1113,7 +1113,8 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
 // Work units in order, the longest class first; wave g takes units
 // g, g + G, g + 2G, ... (G waves in the grid), so every wave gets a share of
 // each class.
-__global__ __launch_bounds__(256) void k_bpe_pack(DevTables t, DevWork w) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void k_bpe_pack(DevTables t, DevWork w) {
   const int lane = threadIdx.x & 63;
   uint32_t units[PACK_CLASSES];
   uint32_t total = 0;
