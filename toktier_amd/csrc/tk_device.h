@@ -8,8 +8,8 @@ namespace tk {
 
 constexpr uint32_t INVALID_ID = 0xFFFFFFFFu;
 constexpr uint32_t RANK_INF = 0xFFFFFFFFu;
-// ranks are packed as rank<<6|lane into 32 bits inside a wave
-constexpr uint32_t MAX_MERGES = 1u << 25;
+// pair keys inside a wave are (63 - segment start)<<26 | rank<<6 | lane
+constexpr uint32_t MAX_MERGES = (1u << 20) - 1;  // ranks < 2^20 - 1
 
 // status word bits (device -> host)
 constexpr uint32_t ST_UTF8 = 1u;     // invalid UTF-8 seen
@@ -70,6 +70,9 @@ struct DevTables {
   uint32_t cbits;              // log2(buckets)
 };
 
+// length classes of the packed short-piece BPE (see pack_slot)
+constexpr int PACK_CLASSES = 13;
+
 // Per-request device buffers (sized by capacity).
 struct DevWork {
   const uint8_t* text;   // nb bytes (+ padding readable)
@@ -105,6 +108,7 @@ struct DevWork {
   uint64_t* dirty_next;  // words marked by the current certify pass
   // packed short-piece BPE
   uint32_t* plist;       // piece starts by length class
+  uint32_t poff[PACK_CLASSES];  // start of each class's list (pack_off)
   uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
   uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
@@ -125,14 +129,21 @@ constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
 // GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
               GATE_FAIL = 4, GATE_DONE = 5, GATE_WORDS = 8;
-// length classes of the packed short-piece BPE (counts at CTRL_PCOUNT)
-constexpr int PACK_CLASSES = 13;
+// packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
 constexpr int PACK_BLOCKS = 2048;
 // slots (lanes per piece) of the length classes, and the shortest piece of
 // each class: class c holds pieces of pack_lmin(c)..pack_slot(c) bytes
 __host__ __device__ constexpr int pack_slot(int c) {
   return c <= 6 ? c + 2 : c == 7 ? 10 : c == 8 ? 12 : c == 9 ? 16
        : c == 10 ? 21 : c == 11 ? 32 : 64;
+}
+// pieces per work unit, and a multiplier m with (lane * m) >> 12 == lane /
+// pack_slot(c) for every lane < 64
+__host__ __device__ constexpr int pack_per_unit(int c) {
+  return 64 / pack_slot(c);
+}
+__host__ __device__ constexpr int pack_magic(int c) {
+  return (4096 + pack_slot(c) - 1) / pack_slot(c);
 }
 __host__ __device__ constexpr int pack_lmin(int c) {
   return c <= 7 ? c + 2 : pack_slot(c - 1) + 1;

@@ -843,12 +843,19 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
 // ------------------------------------------------ 2. short-piece BPE
 
 
-// lane i receives lane i + d of its row of 16; lanes whose source lies past
-// the row end receive RANK_INF
-template <int d>
-__device__ __forceinline__ uint32_t dpp_shl(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)RANK_INF, (int)v, 0x100 + d,
-                                               0xF, 0xF, false);
+// One step of a segmented prefix minimum over the wave: every lane takes the
+// minimum with the lane the DPP control names (row_shr:d reads lane - d in
+// its row of 16; row_bcast:15 / :31 read lane 15 / 31 into the later rows
+// row_mask selects); lanes without a source keep their value.
+template <int ctrl, int row_mask>
+__device__ __forceinline__ uint32_t dpp_min(uint32_t m) {
+  return min(m, (uint32_t)__builtin_amdgcn_update_dpp((int)RANK_INF, (int)m, ctrl,
+                                                      row_mask, 0xF, false));
+}
+
+// the calling lane's bit of a wave-uniform mask, as a lane predicate
+__device__ __forceinline__ bool lane_bit(uint64_t mask) {
+  return __builtin_amdgcn_inverse_ballot_w64(mask);
 }
 
 constexpr uint32_t SYM_ID = 0xFFFFF;      // token id bits of a packed symbol
@@ -858,8 +865,8 @@ constexpr uint32_t SYM_BYTE = 1u << 28;   // the symbol is still one raw byte
 // the byte at pos, a segment's bytes sit on consecutive lanes; ps/pe: the
 // lane's segment as lanes [ps, pe) (a grid window has pos = base + lane;
 // histories are indexed from base + ps, so hist needs that layout). Each round
-// every segment merges its lowest-ranked pair (leftmost on equal rank:
-// key = rank<<6 | lane) -- the HF order -- until no pair has a rule.
+// every segment merges its lowest-ranked pair (leftmost on equal rank) -- the
+// HF order -- until no pair has a rule.
 //   vocab_first: a whole piece that is a vocabulary entry is that one
 //     token (ignore_merges families; pieces only, never sub-segments).
 //   hist: record the merge events that change the segment's first token
@@ -894,73 +901,57 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     live &= ~__ballot(phit && lane != ps);
   }
 
-  // Segment geometry, fixed for the call. starts/ends: first and last lane
-  // of every segment. blkN: all ones unless lane + N is in the lane's own
-  // segment and row of 16 (OR-ed into what the DPP step reads, so the
-  // shifts run on the full wave and never read a masked-off lane); rowN:
-  // the lane sits before lane N and its segment runs past it.
-  const uint64_t starts = __ballot(lane == ps);
+  // Segment geometry, fixed for the call: the first and last lane of every
+  // segment, bit-reversed for the carry chains below. A pair's key is
+  // (63 - segment start) << 26 | rank << 6 | lane (ranks < 2^20 - 1): keys
+  // of earlier segments are larger, so a wave-wide prefix minimum is each
+  // segment's own, and a segment's lowest key -- lowest rank, leftmost on
+  // ties -- is the last lane whose key equals its prefix minimum.
+  const uint64_t rstarts = __brevll(__ballot(lane == ps));
   const uint64_t ends = __ballot(ps >= 0 && lane == pe - 1);
-  const uint64_t cut = starts | (ends << 1);
-  const uint64_t in1 = ~((cut >> 1) | (1ULL << 63));  // no cut in (i, i+1]
-  const uint64_t in2 = in1 & (in1 >> 1);
-  const uint64_t in4 = in2 & (in2 >> 2);
-  const uint64_t in8 = in4 & (in4 >> 4);
-  const int col = lane & 15;
-  const uint32_t blk1 = (col + 1 < 16 && ((in1 >> lane) & 1)) ? 0u : ~0u;
-  const uint32_t blk2 = (col + 2 < 16 && ((in2 >> lane) & 1)) ? 0u : ~0u;
-  const uint32_t blk4 = (col + 4 < 16 && ((in4 >> lane) & 1)) ? 0u : ~0u;
-  const uint32_t blk8 = (col + 8 < 16 && ((in8 >> lane) & 1)) ? 0u : ~0u;
-  const bool row16 = lane < 16 && pe > 16;
-  const bool row32 = lane < 32 && pe > 32;
-  const bool row48 = lane < 48 && pe > 48;
+  const uint64_t rends = __brevll(ends);
+  const uint32_t seg_lane = ((uint32_t)(63 - src_ps) << 26) | (uint32_t)lane;
+  const uint64_t above = ~mask_le(lane);
 
   uint32_t rk = RANK_INF, mid = 0;
   uint32_t nfirst = 0, nlast = 0;  // event counts, kept by lane ps
-  bool dirty = true;
+  uint64_t dirty = ~0ULL;          // lanes whose pair changed
   for (;;) {
-    const bool me = (live >> lane) & 1;
-    const uint64_t after = live & ~mask_le(lane);
+    const uint64_t after = live & above;
     const int nx = after ? __builtin_ctzll(after) : 64;
-    const uint32_t nsym = __shfl(sym, nx < 64 ? nx : lane);
-    if (dirty) {
+    // (nx = 64 reads lane 0; that value is never used)
+    const uint32_t nsym = (uint32_t)__builtin_amdgcn_ds_bpermute(nx << 2, (int)sym);
+    if (lane_bit(dirty)) {
       rk = RANK_INF;
-      if (elig && me && nx < pe) {
+      if (lane_bit(live) && nx < pe) {
         const uint64_t v =
             (sym & nsym & SYM_BYTE)
                 ? t.bytepair[((sym >> 12) & 0xFF00) | ((nsym >> 20) & 0xFF)]
                 : pair_lookup(t, sym & SYM_ID, nsym & SYM_ID);
         if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
       }
-      dirty = false;
     }
     // a lane whose symbol was merged away keeps its old pair rank in rk;
     // only live lanes compete
-    const uint32_t key = (me && rk != RANK_INF) ? ((rk << 6) | (uint32_t)lane)
-                                                : RANK_INF;
-    // segmented suffix minimum: inside each row of 16 lanes by DPP row
-    // shifts (lane i reads lane i + d), then the later rows' minima
+    const bool valid = lane_bit(live) && rk != RANK_INF;
+    const uint32_t key = valid ? (seg_lane | (rk << 6)) : RANK_INF;
     uint32_t m = key;
-    m = min(m, dpp_shl<1>(m) | blk1);
-    m = min(m, dpp_shl<2>(m) | blk2);
-    m = min(m, dpp_shl<4>(m) | blk4);
-    m = min(m, dpp_shl<8>(m) | blk8);
-    const uint32_t m16 = __builtin_amdgcn_readlane(m, 16);
-    const uint32_t m32 = __builtin_amdgcn_readlane(m, 32);
-    const uint32_t m48 = __builtin_amdgcn_readlane(m, 48);
-    m = min(m, row16 ? m16 : RANK_INF);
-    m = min(m, row32 ? m32 : RANK_INF);
-    m = min(m, row48 ? m48 : RANK_INF);
-    // A lane whose key is the minimum of its suffix is a record; each
-    // segment's winner (its lowest key) is its first record. A carry
-    // started at each segment's first lane runs over the lanes that are
-    // neither records nor the segment's last lane and stops on the first
-    // that is.
-    const uint64_t rec = __ballot(key != RANK_INF && m == key);
+    m = dpp_min<0x111, 0xF>(m);  // row_shr:1
+    m = dpp_min<0x112, 0xF>(m);  // row_shr:2
+    m = dpp_min<0x114, 0xF>(m);  // row_shr:4
+    m = dpp_min<0x118, 0xF>(m);  // row_shr:8
+    m = dpp_min<0x142, 0xA>(m);  // row_bcast:15 into rows 1 and 3
+    m = dpp_min<0x143, 0xC>(m);  // row_bcast:31 into rows 2 and 3
+    const uint64_t rec = __ballot(valid && m == key);
     if (rec == 0) break;
-    const uint64_t stop = rec | ends;
-    const uint64_t wm = ((~stop + starts) & stop) & rec;
-    const bool win_ = (wm >> lane) & 1;
+    // Each segment's winner is its last record: on the bit-reversed masks a
+    // carry started at each segment's last lane runs over the lanes that
+    // are neither records nor the segment's first lane and stops on the
+    // first that is.
+    const uint64_t rrec = __brevll(rec);
+    const uint64_t stop = rrec | rstarts;
+    const uint64_t wm = __brevll(((~stop + rends) & stop) & rrec);
+    const bool win_ = lane_bit(wm);
     if (hist) {
       const uint32_t nf = __shfl(nfirst, src_ps);
       const uint32_t nl = __shfl(nlast, src_ps);
@@ -987,10 +978,10 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     live &= ~gone;
     const uint64_t lr = __brevll(live);
     const uint64_t prevw = __brevll((~lr + (__brevll(wm) << 1)) & lr);
-    dirty = ((wm | prevw) >> lane) & 1;
+    dirty = wm | prevw;
   }
   if (hist && elig && lane == ps) w.hmeta[base + ps] = nfirst | (nlast << 16);
-  if (write && elig) w.tok[pos] = ((live >> lane) & 1) ? (sym & SYM_ID) : INVALID_ID;
+  if (write && elig) w.tok[pos] = lane_bit(live) ? (sym & SYM_ID) : INVALID_ID;
   return live;
 }
 
@@ -1097,8 +1088,7 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t base = (int64_t)blockIdx.x * PT_TILE;
   if (tid < PACK_CLASSES)
-    lcnt[tid] = (uint32_t)pack_off(w.nb, tid) +
-                w.pblk[(int64_t)tid * gridDim.x + blockIdx.x];
+    lcnt[tid] = w.poff[tid] + w.pblk[(int64_t)tid * gridDim.x + blockIdx.x];
   __syncthreads();
   const bool two = !t.ignore_merges;
   for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
@@ -1118,9 +1108,9 @@ void k_bpe_pack(DevTables t, DevWork w) {
   const int lane = threadIdx.x & 63;
   uint32_t units[PACK_CLASSES];
   uint32_t total = 0;
+#pragma unroll
   for (int c = PACK_CLASSES - 1; c >= 0; --c) {
-    const uint32_t k = 64 / pack_slot(c);
-    units[c] = (w.pcount[c] + k - 1) / k;
+    units[c] = (w.pcount[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
     total += units[c];
   }
   const uint32_t G = gridDim.x * (blockDim.x / 64);
@@ -1129,12 +1119,12 @@ void k_bpe_pack(DevTables t, DevWork w) {
     uint32_t u = u0;
     int c = PACK_CLASSES - 1;
     while (u >= units[c]) u -= units[c--];
-    const int sl = pack_slot(c), k = 64 / sl;
-    const int slot = lane / sl, off = lane - slot * sl;
+    const int sl = pack_slot(c), k = pack_per_unit(c);
+    const int slot = (lane * pack_magic(c)) >> 12, off = lane - slot * sl;
     const uint32_t idx = u * k + slot;
     int64_t a = 0, L = 0;
     if (slot < k && idx < w.pcount[c]) {
-      a = w.plist[pack_off(w.nb, c) + idx];
+      a = w.plist[w.poff[c] + idx];
       L = piece_end(w, a) - a;
     }
     const bool elig = off < L;

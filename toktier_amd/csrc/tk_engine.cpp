@@ -308,6 +308,8 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.dirty_cur = e->dirty_cur.p;
   w.dirty_next = e->dirty_next.p;
   w.plist = e->plist.p;
+  for (int c = 0; c < tk::PACK_CLASSES; ++c)
+    w.poff[c] = (uint32_t)tk::pack_off((int64_t)nb, c);  // < 2^32 for nb <= 1 GiB
   w.pblk = e->pblk.p;
   w.pcount = ctrl + tk::CTRL_PCOUNT;
   w.nbig = ctrl + tk::CTRL_BIG;
@@ -545,12 +547,13 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (cfg->ignore_merges && !vocab_blob && vocab_blob_len)
     return fail(TK_E_INVALID_ARG, "vocabulary blob is null");
   const uint64_t n_pairs = cfg->pair_count;
-  // ranks are packed rank<<6|lane in 32 bits on the device, token ids in
-  // 20 bits (the vocabulary value format already limits them to that)
+  // ranks are packed segment<<26|rank<<6|lane in 32 bits on the device
+  // (a rank list whose products are 20-bit ids stays far below that), token
+  // ids in 20 bits (the vocabulary value format already limits them to that)
   for (uint64_t i = 0; i < n_pairs; ++i) {
     if (pair_keys[i] == ~0ULL) continue;
     if ((pair_vals[i] >> 32) >= tk::MAX_MERGES)
-      return fail(TK_E_SHAPE, "merge rank exceeds 2^25");
+      return fail(TK_E_SHAPE, "merge rank exceeds 2^20 - 2");
     if ((pair_vals[i] & 0xFFFFFFFFULL) >= (1u << 20) ||
         (pair_keys[i] >> 32) >= (1u << 20) ||
         (pair_keys[i] & 0xFFFFFFFFULL) >= (1u << 20))
