@@ -111,6 +111,8 @@ struct DevWork {
   uint32_t poff[PACK_CLASSES];  // start of each class's list (pack_off)
   uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
   uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
+  uint32_t* uend;        // [PACK_CLASSES] end of each class's work units in
+                         // k_bpe_pack's order, longest class first (ctrl)
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
@@ -122,7 +124,8 @@ struct DevWork {
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
-              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_WORDS = 32;
+              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_UEND = 32,
+              CTRL_WORDS = 64;
 // gate words in host memory: k_pack_scan writes GATE_SEQ / GATE_BIG (the
 // host learns early whether the cut / certify stages have any work), k_scan
 // writes the request's outcome (status, id count, failed cuts) and then

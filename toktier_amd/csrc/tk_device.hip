@@ -98,6 +98,11 @@ __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
   }
 }
 
+// the wave's index in its block, as a wave-uniform (scalar) value
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ uint64_t mask_le(int lane) {
   return lane == 63 ? ~0ULL : ((2ULL << lane) - 1);
 }
@@ -616,7 +621,7 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   auto prv = [&](int L) {  // local offset of the character before L
     return L - 1 - (int)((se[L - 1] >> 23) & 3);
   };
-  const int lane = tid & 63, wv = tid >> 6;
+  const int lane = tid & 63, wv = wave_id();
   uint32_t st = 0;
   // the tile's words, and the first word after it (the next block writes
   // that one; it is recomputed here to size the pieces near the tile end)
@@ -1042,7 +1047,7 @@ constexpr int PACK_SCAN_LDS = 12288;  // counts held in LDS per chunk
 __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
   __shared__ uint32_t cnt[PACK_SCAN_LDS];
   __shared__ uint32_t carry[PACK_CLASSES];
-  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, c = wave_id();
   if (threadIdx.x < PACK_CLASSES) carry[threadIdx.x] = 0;
   // chunks of tiles so that PACK_CLASSES rows fit the LDS
   const int64_t chunk = PACK_SCAN_LDS / PACK_CLASSES;
@@ -1071,6 +1076,14 @@ __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
   }
   __syncthreads();
   if (threadIdx.x < PACK_CLASSES) w.pcount[threadIdx.x] = carry[threadIdx.x];
+  if (threadIdx.x == 64) {
+    uint32_t run = 0;
+#pragma unroll
+    for (int c = PACK_CLASSES - 1; c >= 0; --c) {
+      run += (carry[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
+      w.uend[c] = run;
+    }
+  }
   if (threadIdx.x == 0 && w.gate) {
     // k_long_prep (the previous kernel) has counted the pieces over WIDE_MAX
     w.gate[GATE_BIG] = *w.nbig;
@@ -1085,7 +1098,7 @@ __global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
 __global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
                                                              DevWork w) {
   __shared__ uint32_t lcnt[PACK_CLASSES];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
   const int64_t base = (int64_t)blockIdx.x * PT_TILE;
   if (tid < PACK_CLASSES)
     lcnt[tid] = w.poff[tid] + w.pblk[(int64_t)tid * gridDim.x + blockIdx.x];
@@ -1100,30 +1113,43 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
   }
 }
 
-// Work units in order, the longest class first; wave g takes units
-// g, g + G, g + 2G, ... (G waves in the grid), so every wave gets a share of
-// each class.
+constexpr uint32_t pack_geo(int c) {
+  return (uint32_t)pack_slot(c) | (uint32_t)pack_per_unit(c) << 8 |
+         (uint32_t)pack_magic(c) << 16;
+}
+__constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
+    pack_geo(0), pack_geo(1), pack_geo(2), pack_geo(3), pack_geo(4),
+    pack_geo(5), pack_geo(6), pack_geo(7), pack_geo(8), pack_geo(9),
+    pack_geo(10), pack_geo(11), pack_geo(12)};
+static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
+
+// Work units in order, the longest class first (class c owns units
+// [uend[c + 1], uend[c])); wave g takes units g, g + G, g + 2G, ... (G waves
+// in the grid), so every wave gets a share of each class.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   const int lane = threadIdx.x & 63;
-  uint32_t units[PACK_CLASSES];
-  uint32_t total = 0;
-#pragma unroll
-  for (int c = PACK_CLASSES - 1; c >= 0; --c) {
-    units[c] = (w.pcount[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
-    total += units[c];
-  }
-  const uint32_t G = gridDim.x * (blockDim.x / 64);
-  for (uint32_t u0 = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
-       u0 < total; u0 += G) {
-    uint32_t u = u0;
-    int c = PACK_CLASSES - 1;
-    while (u >= units[c]) u -= units[c--];
-    const int sl = pack_slot(c), k = pack_per_unit(c);
-    const int slot = (lane * pack_magic(c)) >> 12, off = lane - slot * sl;
-    const uint32_t idx = u * k + slot;
+  // lane q < PACK_CLASSES holds class q's unit end, piece count and slot
+  // geometry (slot | pieces per unit << 8 | pack_magic << 16); lane
+  // PACK_CLASSES holds a zero unit end
+  const bool cl = lane < PACK_CLASSES;
+  const uint32_t ue_l = cl ? w.uend[lane] : 0u;
+  const uint32_t pc_l = cl ? w.pcount[lane] : 0u;
+  const uint32_t geo_l = cl ? PACK_GEO[lane] : 0u;
+  const uint32_t total = __builtin_amdgcn_readfirstlane(ue_l);
+  const uint32_t G = gridDim.x * 4;
+  for (uint32_t u0 = blockIdx.x * 4 + wave_id(); u0 < total; u0 += G) {
+    // the unit's class: the last class whose unit end lies past u0
+    const uint64_t inq = __ballot(cl && u0 < ue_l);
+    const int c = 63 - __builtin_clzll(inq);
+    const uint32_t geo = __builtin_amdgcn_readlane(geo_l, c);
+    const uint32_t ubeg = __builtin_amdgcn_readlane(ue_l, c + 1);
+    const uint32_t cnt = __builtin_amdgcn_readlane(pc_l, c);
+    const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = geo >> 16;
+    const int slot = (lane * mg) >> 12, off = lane - slot * sl;
+    const uint32_t idx = (u0 - ubeg) * k + slot;
     int64_t a = 0, L = 0;
-    if (slot < k && idx < w.pcount[c]) {
+    if (slot < k && idx < cnt) {
       a = w.plist[w.poff[c] + idx];
       L = piece_end(w, a) - a;
     }
@@ -1158,7 +1184,7 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
   uint32_t n = *count;
   if (n > cap) n = cap;
   const uint32_t waves = gridDim.x * 4;
-  for (uint32_t k = blockIdx.x * 4 + (threadIdx.x >> 6); k < n; k += waves) {
+  for (uint32_t k = blockIdx.x * 4 + wave_id(); k < n; k += waves) {
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
     if (len > 64) continue;  // wave-uniform
@@ -1494,7 +1520,7 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
   __shared__ WideLds lds[4];
   uint32_t n = *count;
   if (n > cap) n = cap;
-  const int wv = threadIdx.x >> 6;
+  const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
@@ -1517,7 +1543,7 @@ __global__ __launch_bounds__(256) void k_long_prep(DevTables t, DevWork w) {
   const uint32_t waves = gridDim.x * (blockDim.x / 64);
   // 64 entries per wave and step: lane j resolves entry k0 + j, then the
   // wave handles the entries over WIDE_MAX bytes one by one
-  for (uint32_t k0 = (blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 64;
+  for (uint32_t k0 = (blockIdx.x * (blockDim.x / 64) + wave_id()) * 64;
        k0 < n; k0 += waves * 64) {
     const uint32_t k = k0 + lane;
     uint32_t a = 0, b = 0;
@@ -1577,7 +1603,7 @@ __device__ __forceinline__ uint64_t inlong_window(const DevWork& w, int64_t v,
 __global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
                                                       int64_t nwin) {
   const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v > nwin) return;
   auto seg = [&](int64_t wd) { return w.starts[wd]; };
   uint16_t* cut16 = reinterpret_cast<uint16_t*>(w.cuts);
@@ -1623,7 +1649,7 @@ __device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
 __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
                                                        int64_t nwin, int all) {
   const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v > nwin) return;
   auto seg = [&](int64_t wd) { return seg_word(w, wd); };
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
@@ -1791,7 +1817,7 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 // exclusive scan of one value per thread over a 256-thread block
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   __shared__ uint32_t wsum[4];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = wave_id();
   const uint32_t inc = wave_incl_scan(v, lane);
   if (lane == 63) wsum[wv] = inc;
   __syncthreads();
@@ -1826,7 +1852,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_count(DevWork w, int64_t nblk) 
 constexpr int SCAN_TPB = 1024;
 __global__ __launch_bounds__(SCAN_TPB) void k_scan(DevWork w, int64_t nblk) {
   __shared__ uint32_t wsum[SCAN_TPB / 64];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = wave_id();
   const int64_t per = (nblk + SCAN_TPB - 1) / SCAN_TPB;
   const int64_t lo = threadIdx.x * per;
   uint32_t s = 0;
@@ -1863,7 +1889,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w,
                                                          int64_t nblk) {
   __shared__ uint32_t wsum[COMPACT_TPB / 64];
   if (w.blkprefix[nblk] > w.out_cap) return;  // whole grid: reported by k_scan
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = wave_id();
   const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
   uint32_t run = w.blkprefix[blockIdx.x];
   for (int k = 0; k < COMPACT_PER_THREAD; ++k) {

@@ -312,6 +312,7 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
     w.poff[c] = (uint32_t)tk::pack_off((int64_t)nb, c);  // < 2^32 for nb <= 1 GiB
   w.pblk = e->pblk.p;
   w.pcount = ctrl + tk::CTRL_PCOUNT;
+  w.uend = ctrl + tk::CTRL_UEND;
   w.nbig = ctrl + tk::CTRL_BIG;
   w.gate = e->gate_dev;
   w.seq = e->seq;
