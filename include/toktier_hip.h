@@ -134,13 +134,14 @@ int tk_engine_encode_device(tk_engine* engine, const void* d_text,
 const char* tk_engine_delivery(const tk_engine* engine);     /* "prebuilt" */
 const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
 
-/* Per-stage device times (microseconds) of the last encode on this engine,
- * from HIP events on the engine's streams: [0] pretokenize and piece
- * listing, [1] short-piece BPE, [2] the time the long-piece BPE (run beside
- * the short-piece BPE) went past it, [3] compaction, [4] total.
- * Returns the number of values written (<= n). Timing is recorded only when
- * enabled with tk_engine_set_timing(engine, 1). */
-int tk_engine_set_timing(tk_engine* engine, int enabled);
+/* Device times (microseconds) of the last encode on this engine, from HIP
+ * events taken by the dispatches themselves. Mode 1 (every stage): [0]
+ * pretokenize and piece listing, [1] short-piece BPE, [2] the time the
+ * long-piece BPE (run beside the short-piece BPE) went past it, [3]
+ * compaction, [4] total. Mode 2 (least disturbance): [1] the short-piece
+ * BPE kernel's own duration, the others 0. Mode 0 (default): nothing is
+ * recorded. Returns the number of values written (<= n). */
+int tk_engine_set_timing(tk_engine* engine, int mode);
 int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
 
 /* Thread-local description of the last failure on this thread. */

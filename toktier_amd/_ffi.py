@@ -194,8 +194,9 @@ class Engine:
         check(st, "tk_engine_encode_device")
         return n.value
 
-    def set_timing(self, on: bool) -> None:
-        check(self._L.tk_engine_set_timing(self._h, int(on)),
+    def set_timing(self, mode: int) -> None:
+        """0 off, 1 (or True) every stage, 2 the packed merge kernel only."""
+        check(self._L.tk_engine_set_timing(self._h, int(mode)),
               "tk_engine_set_timing")
 
     def last_timing(self) -> list[float]:

@@ -176,7 +176,7 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
 hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
                              hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop = nullptr);
+                           hipEvent_t start, hipEvent_t stop);
 hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
                             hipStream_t s);
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,

@@ -76,6 +76,36 @@ __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
   }
 }
 
+// The compact table's lookup in 32-bit arithmetic (the same key bijection,
+// buckets and slot layout as pair_lookup): true, with the merge's rank and
+// id, when the pair has a rule. Both candidate buckets are loaded before
+// either is inspected (one memory round trip). l, r < 2^18: the engine
+// builds the table only when every byte id and every rule id is below 2^18.
+__device__ __forceinline__ bool ctab_find(const DevTables& t, uint32_t l,
+                                          uint32_t r, uint32_t* rank,
+                                          uint32_t* id) {
+  const uint32_t a = (l ^ pair_round(r, 0x9E3779u)) & 0x3FFFFu;
+  const uint32_t b = (r ^ pair_round(a, 0x85EBCBu)) & 0x3FFFFu;
+  // the 36-bit key a << 18 | b as hi:lo
+  const uint32_t lo = (a << 18) | b, hi = a >> 14;
+  const uint32_t b1 = lo & (uint32_t)t.cmask;
+  const uint32_t tag = __builtin_amdgcn_alignbit(hi, lo, t.cbits);
+  const uint32_t b2 = pair_alt(b1, tag, t.cbits);
+  const uint4* tab = reinterpret_cast<const uint4*>(t.ctab);
+  const uint4 u = tab[b1], v = tab[b2];
+  // a slot's high word >> 5 is tag << 1 | (second bucket)
+  const uint32_t w0 = tag << 1, w1 = w0 | 1u;
+  // (masks rather than selects: the slot words are picked with no branch,
+  // so the compiler keeps the two 16-byte loads whole)
+  const uint32_t k0 = (u.y >> 5) == w0 ? ~0u : 0u, k1 = (u.w >> 5) == w0 ? ~0u : 0u;
+  const uint32_t k2 = (v.y >> 5) == w1 ? ~0u : 0u, k3 = (v.w >> 5) == w1 ? ~0u : 0u;
+  const uint32_t slo = (u.x & k0) | (u.z & k1) | (v.x & k2) | (v.z & k3);
+  const uint32_t shi = (u.y & k0) | (u.w & k1) | (v.y & k2) | (v.w & k3);
+  *rank = __builtin_amdgcn_alignbit(shi, slo, 18) & 0x7FFFFu;
+  *id = slo & 0x3FFFFu;
+  return (k0 | k1 | k2 | k3) != 0u;
+}
+
 // whole-piece vocabulary id (ignore_merges) or -1
 __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
                                 int64_t m) {
@@ -929,11 +959,20 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     if (lane_bit(dirty)) {
       rk = RANK_INF;
       if (lane_bit(live) && nx < pe) {
-        const uint64_t v =
-            (sym & nsym & SYM_BYTE)
-                ? t.bytepair[((sym >> 12) & 0xFF00) | ((nsym >> 20) & 0xFF)]
-                : pair_lookup(t, sym & SYM_ID, nsym & SYM_ID);
-        if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+        if (sym & nsym & SYM_BYTE) {
+          const uint64_t v =
+              t.bytepair[((sym >> 12) & 0xFF00) | ((nsym >> 20) & 0xFF)];
+          if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+        } else if (t.ctab) {
+          uint32_t r_, m_;
+          if (ctab_find(t, sym & SYM_ID, nsym & SYM_ID, &r_, &m_)) {
+            rk = r_;
+            mid = m_;
+          }
+        } else {
+          const uint64_t v = pair_lookup(t, sym & SYM_ID, nsym & SYM_ID);
+          if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+        }
       }
     }
     // a lane whose symbol was merged away keeps its old pair rank in rk;
@@ -947,7 +986,7 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     m = dpp_min<0x118, 0xF>(m);  // row_shr:8
     m = dpp_min<0x142, 0xA>(m);  // row_bcast:15 into rows 1 and 3
     m = dpp_min<0x143, 0xC>(m);  // row_bcast:31 into rows 2 and 3
-    const uint64_t rec = __ballot(valid && m == key);
+    const uint64_t rec = __builtin_amdgcn_ballot_w64(valid && m == key);
     if (rec == 0) break;
     // Each segment's winner is its last record: on the bit-reversed masks a
     // carry started at each segment's last lane runs over the lanes that
@@ -1169,8 +1208,8 @@ hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
 }
 
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop) {
-  launch_ev(k_bpe_pack, dim3(PACK_BLOCKS), dim3(256), s, nullptr, stop, t, w);
+                           hipEvent_t start, hipEvent_t stop) {
+  launch_ev(k_bpe_pack, dim3(PACK_BLOCKS), dim3(256), s, start, stop, t, w);
   return hipGetLastError();
 }
 

@@ -192,7 +192,7 @@ struct tk_engine {
   uint32_t* gate_dev = nullptr;
   uint32_t seq = 0;
   // timing
-  bool timing = false;
+  int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
   hipEvent_t ev[8] = {};
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
@@ -371,20 +371,29 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
       make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap);
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
-  // Stage boundaries, timestamps taken by the dispatches themselves:
+  // Timing mode 1, stage boundaries taken by the dispatches themselves:
   // ev[0] start of k_pretok; ev[1] end of the piece listing (k_long_prep,
   // k_pack_scan, k_pack_scatter); ev[2] end of k_bpe_pack; ev[3] end of the
-  // long-piece stages (side stream, alongside k_bpe_pack); ev[4] end of the
-  // compaction. (Each timed dispatch delays the next one by a few
-  // microseconds, so the events sit on as few dispatches as they can.)
-  hipEvent_t* tv = e->timing ? ev : nullptr;
-  auto at = [&](int k) { return tv ? tv[k] : nullptr; };
+  // long-piece stages on the side stream; ev[4] end
+  // of the compaction. Mode 2: ev[1] / ev[2] are the start / end of
+  // k_bpe_pack's own dispatch only. (Each timed dispatch delays the next
+  // one by a few microseconds, so the events sit on as few dispatches as
+  // they can.)
+  const bool stages = e->timing == 1, packonly = e->timing == 2;
+  auto at = [&](int k) { return stages ? ev[k] : nullptr; };
   HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_long_prep(e->t, w, s));
+  // The long-piece stages need only k_pretok and k_long_prep: they run on
+  // the side stream, k_bpe_wide (latency-bound, few waves) from here on,
+  // beside the piece listing and the packed merge.
+  hipStream_t s2 = e->stream2;
   HIP_TRY(hipEventRecord(e->ev_fork, s));  // long pieces resolved
+  HIP_TRY(hipStreamWaitEvent(s2, e->ev_fork, 0));
+  HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr));
   HIP_TRY(tk::launch_pack_lists(e->t, w, s, at(1)));  // k_pack_scan writes the gate
-  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, at(2)));
+  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
+                              stages || packonly ? ev[2] : nullptr));
   // The cut / certify stages run only when a piece over WIDE_MAX bytes
   // exists: the device tells through the gate words while the packed
   // merge is still running, so the decision costs no device time.
@@ -394,15 +403,12 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
     if (grc != TK_OK) return grc;
     big = e->gate[tk::GATE_BIG];
   }
-  // the long-piece stages need only k_pretok and k_long_prep: they run on
-  // the side stream while the packed merge runs
-  hipStream_t s2 = e->stream2;
-  HIP_TRY(hipStreamWaitEvent(s2, e->ev_fork, 0));
-  HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, big ? nullptr : at(3)));
   if (big) {
     HIP_TRY(tk::launch_long_windows(e->t, w, s2));
     HIP_TRY(tk::launch_long_segments(e->t, w, 1, s2));
     HIP_TRY(tk::launch_certify(e->t, w, 1, s2, at(3)));
+  } else if (stages) {
+    HIP_TRY(hipEventRecord(ev[3], s2));
   }
   HIP_TRY(hipEventRecord(e->ev_join, s2));
   HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
@@ -418,21 +424,25 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
   int rc = TK_OK;
-  if (e->timing) {
+  if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
     const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
-    const double t3 = elapsed_us(ev[0], ev[3]), t4 = elapsed_us(ev[0], ev[4]);
+    const double t3 = elapsed_us(ev[0], ev[3]);
+    const double t4 = elapsed_us(ev[0], ev[4]);
     e->last_us[0] = t1;
     e->last_us[1] = t2 - t1;
     e->last_us[2] = t3 > t2 ? t3 - t2 : 0.0;
     e->last_us[3] = t4 - (t3 > t2 ? t3 : t2);
     e->last_us[4] = t4;
+  } else if (packonly) {
+    for (double& x : e->last_us) x = 0.0;
+    e->last_us[1] = elapsed_us(ev[1], ev[2]);
   }
   if (h[tk::CTRL_FAIL] != 0) {
     // every pass removes at least one cut, so this ends (at worst with each
     // long piece as one segment); the bound only guards against a defect
     size_t passes = 0;
-    if (e->timing) HIP_TRY(hipEventRecord(ev[5], s));
+    if (stages) HIP_TRY(hipEventRecord(ev[5], s));
     while (h[tk::CTRL_FAIL] != 0) {
       if (++passes > nb + 1) return fail(TK_E_INTERNAL, "certification did not converge");
       HIP_TRY(hipMemsetAsync(ctrl + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
@@ -441,11 +451,11 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
       HIP_TRY(tk::launch_certify(e->t, w, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     }
-    if (e->timing) HIP_TRY(hipEventRecord(ev[6], s));
+    if (stages) HIP_TRY(hipEventRecord(ev[6], s));
     HIP_TRY(tk::launch_compact(w, s));
-    if (e->timing) HIP_TRY(hipEventRecord(ev[7], s));
+    if (stages) HIP_TRY(hipEventRecord(ev[7], s));
     if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
-    if (e->timing) {
+    if (stages) {
       e->last_us[2] += elapsed_us(ev[5], ev[6]);
       e->last_us[3] = elapsed_us(ev[6], ev[7]);
       e->last_us[4] = elapsed_us(ev[0], ev[7]);
@@ -596,8 +606,11 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&e->stream2, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
-  if (hipEventCreateWithFlags(&e->ev_fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming) != hipSuccess)
+  // fork / join between the engine's two streams on one device: no
+  // system-scope fence
+  const unsigned fj = hipEventDisableTiming | hipEventDisableSystemFence;
+  if (hipEventCreateWithFlags(&e->ev_fork, fj) != hipSuccess ||
+      hipEventCreateWithFlags(&e->ev_join, fj) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
@@ -674,9 +687,13 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.cert = cert ? 1 : 0;
   e->t.ctab = nullptr;
   {
+    // with the compact table every symbol the packed merge looks up (a
+    // byte's id or a rule's product) is below 2^18
+    bool small_ids = true;
+    for (int b = 0; b < 256; ++b) small_ids = small_ids && byte_id[b] < (1 << 18);
     std::vector<uint64_t> ct;
     uint32_t bits = 0;
-    if (build_compact_pairs(pair_keys, pair_vals, n_pairs, ct, bits)) {
+    if (small_ids && build_compact_pairs(pair_keys, pair_vals, n_pairs, ct, bits)) {
       if ((rc = up(e->ctab, ct.data(), ct.size())) != TK_OK) return bail(rc);
       e->t.ctab = e->ctab.p;
       e->t.cmask = (1ULL << bits) - 1;
@@ -714,8 +731,10 @@ void tk_engine_close(tk_engine* e) {
 
 int tk_engine_set_timing(tk_engine* e, int enabled) {
   if (!e) return fail(TK_E_INVALID_ARG, "engine is null");
+  if (enabled < 0 || enabled > 2)
+    return fail(TK_E_INVALID_ARG, "timing mode %d is not 0, 1 or 2", enabled);
   std::lock_guard<std::mutex> lk(e->mu);
-  e->timing = enabled != 0;
+  e->timing = enabled;
   return TK_OK;
 }
 
