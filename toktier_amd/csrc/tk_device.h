@@ -108,6 +108,7 @@ struct DevWork {
   uint64_t* dirty_next;  // words marked by the current certify pass
   // packed short-piece BPE
   uint32_t* plist;       // piece starts by length class
+  uint32_t* plocal;      // [tiles][PT_LOCAL_SLOTS] the same, tile by tile
   uint32_t poff[PACK_CLASSES];  // start of each class's list (pack_off)
   uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
   uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
@@ -126,12 +127,13 @@ struct DevWork {
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_UEND = 32,
               CTRL_WORDS = 64;
-// gate words in host memory: k_pack_scan writes GATE_SEQ / GATE_BIG (the
-// host learns early whether the cut / certify stages have any work), k_scan
+// gate words in host memory: k_pack_copy writes GATE_NLONG / GATE_BIG and
+// then GATE_SEQ (the host learns, while the packed merge runs, whether the
+// long-piece stages have any work), k_scan
 // writes the request's outcome (status, id count, failed cuts) and then
 // GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
-              GATE_FAIL = 4, GATE_DONE = 5, GATE_WORDS = 8;
+              GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_WORDS = 8;
 // packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
 constexpr int PACK_BLOCKS = 2048;
 // slots (lanes per piece) of the length classes, and the shortest piece of
@@ -165,6 +167,16 @@ constexpr int PT_TILE = 4096;  // bytes per k_pretok block (64 start words)
 __host__ __device__ inline int64_t pretok_tiles(int64_t nb) {
   return (((nb + 63) / 64 + 2) * 64 + PT_TILE - 1) / PT_TILE;
 }
+// k_pretok lists each tile's packed pieces by class in a region of its own
+// (plocal): class c may hold every piece of pack_lmin(c) or more bytes that
+// starts in the tile
+__host__ __device__ constexpr int pack_local_cap(int c) {
+  return PT_TILE / pack_lmin(c) + 1;
+}
+__host__ __device__ constexpr int pack_local_off(int c) {
+  return c == 0 ? 0 : pack_local_off(c - 1) + pack_local_cap(c - 1);
+}
+constexpr int PT_LOCAL_SLOTS = pack_local_off(PACK_CLASSES);
 constexpr int COMPACT_TPB = 256;
 constexpr int COMPACT_PER_THREAD = 16;
 constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
@@ -173,14 +185,15 @@ constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
 // first dispatch / the end of its last one
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
-hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
-                             hipStream_t s, hipEvent_t stop = nullptr);
+// k_lists (per-class offsets of the tiles' piece lists, and the long
+// pieces' ends) and k_pack_copy (one list per class; the gate words)
+hipError_t launch_lists(const DevTables& t, const DevWork& w, hipStream_t s);
+hipError_t launch_pack_copy(const DevWork& w, hipStream_t s,
+                            hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop);
-hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s);
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop = nullptr);
+                           hipEvent_t stop, uint32_t nlong);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,

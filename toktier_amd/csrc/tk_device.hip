@@ -160,6 +160,14 @@ __device__ __forceinline__ void push_pair(uint32_t* list, uint32_t* count,
 // packed waves by length class; longer ones take the long-piece stages.
 constexpr int PIECE_NONE = -1, PIECE_ONE = -2, PIECE_TWO = -3, PIECE_LONG = -4;
 
+__constant__ uint32_t PACK_LOCAL_OFF[PACK_CLASSES] = {
+    pack_local_off(0), pack_local_off(1), pack_local_off(2),
+    pack_local_off(3), pack_local_off(4), pack_local_off(5),
+    pack_local_off(6), pack_local_off(7), pack_local_off(8),
+    pack_local_off(9), pack_local_off(10), pack_local_off(11),
+    pack_local_off(12)};
+static_assert(PACK_CLASSES == 13, "PACK_LOCAL_OFF lists every class");
+
 __device__ __forceinline__ int pack_class(int L) {  // 2 <= L <= 64
   return (L > 2) + (L > 3) + (L > 4) + (L > 5) + (L > 6) + (L > 7) + (L > 8) +
          (L > 10) + (L > 12) + (L > 16) + (L > 21) + (L > 32);
@@ -536,6 +544,23 @@ __device__ __forceinline__ int fast_r50k(const Ctx5& x) {
   return p3 == '\'' && is_re_ve_ll(p2, p1) && arrives_after(x.c4, x.h4);
 }
 
+// exclusive scan of one value per thread over a 256-thread block
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
+  __shared__ uint32_t wsum[4];
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  const uint32_t inc = wave_incl_scan(v, lane);
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
+  for (int k = 0; k < 4; ++k) {
+    if (k < wv) off += wsum[k];
+    tot += wsum[k];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
 // ------------------------------------------------------ 1. pretokenize
 
 // One block per PT_TILE bytes (64 start words). Stage the bytes, decode
@@ -558,8 +583,12 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   static_assert(PRETOK_TPB == 256, "one table entry per thread");
   __shared__ uint8_t lcls[256], lnfc[256];
   __shared__ int32_t lbid[256];
+  __shared__ uint32_t loff[PACK_CLASSES];  // class regions of plocal
   const int tid = threadIdx.x;
-  if (tid < PACK_CLASSES) lcnt[tid] = 0;
+  if (tid < PACK_CLASSES) {
+    lcnt[tid] = 0;
+    loff[tid] = PACK_LOCAL_OFF[tid];
+  }
   if (tid == 0) nlong = 0;
   lcls[tid] = t.cls[tid];
   lnfc[tid] = w.check_nfc ? t.nfc[tid] : 0;
@@ -807,15 +836,16 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
   if (st) atomicOr(w.status, st);
   __syncthreads();
   // Stage-2 bookkeeping for the pieces that start in this tile: finish the
-  // one- and two-byte ones, queue the long ones, count the rest by class
-  // (the counts are scanned by k_pack_scan).
+  // one- and two-byte ones, queue the long ones, list the rest by class in
+  // the tile's region of plocal (the counts are scanned by k_lists).
   const bool two = !t.ignore_merges;
   for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
     const int64_t a = base + 64 * k + lane;
     if (a >= nb) break;  // (positions only grow along the loop)
     const int kind = piece_kind(sw[k], sw[k + 1], lane, two);
     if (kind >= 0) {
-      atomicAdd(&lcnt[kind], 1u);
+      const uint32_t j = atomicAdd(&lcnt[kind], 1u);
+      w.plocal[(int64_t)blockIdx.x * PT_LOCAL_SLOTS + loff[kind] + j] = (uint32_t)a;
     } else if (kind == PIECE_ONE) {
       const int32_t id = lbid[sb[64 * k + lane + PT_PAD]];
       w.tok[a] = id >= 0 ? (uint32_t)id : INVALID_ID;
@@ -1080,78 +1110,6 @@ __device__ __forceinline__ int64_t piece_end(const DevWork& w, int64_t a) {
   return seg_end_after(wd + 1, [&](int64_t x) { return w.starts[x]; });
 }
 
-// exclusive prefix of each class's per-tile counts: the counts are staged
-// in LDS (coalesced loads, all in flight at once), one wave scans a class
-constexpr int PACK_SCAN_LDS = 12288;  // counts held in LDS per chunk
-__global__ __launch_bounds__(1024) void k_pack_scan(DevWork w, int64_t ntile) {
-  __shared__ uint32_t cnt[PACK_SCAN_LDS];
-  __shared__ uint32_t carry[PACK_CLASSES];
-  const int lane = threadIdx.x & 63, c = wave_id();
-  if (threadIdx.x < PACK_CLASSES) carry[threadIdx.x] = 0;
-  // chunks of tiles so that PACK_CLASSES rows fit the LDS
-  const int64_t chunk = PACK_SCAN_LDS / PACK_CLASSES;
-  for (int64_t t0 = 0; t0 < ntile; t0 += chunk) {
-    const int64_t n = ntile - t0 < chunk ? ntile - t0 : chunk;
-    __syncthreads();
-    for (int cc = 0; cc < PACK_CLASSES; ++cc)
-      for (int64_t j = threadIdx.x; j < n; j += 1024)
-        cnt[cc * n + j] = w.pblk[cc * ntile + t0 + j];
-    __syncthreads();
-    if (c < PACK_CLASSES) {
-      uint32_t run = carry[c];
-      for (int64_t j0 = 0; j0 < n; j0 += 64) {
-        const int64_t j = j0 + lane;
-        const uint32_t v = j < n ? cnt[c * n + j] : 0u;
-        const uint32_t inc = wave_incl_scan(v, lane);
-        if (j < n) cnt[c * n + j] = run + inc - v;
-        run += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
-      }
-      if (lane == 0) carry[c] = run;
-    }
-    __syncthreads();
-    for (int cc = 0; cc < PACK_CLASSES; ++cc)
-      for (int64_t j = threadIdx.x; j < n; j += 1024)
-        w.pblk[cc * ntile + t0 + j] = cnt[cc * n + j];
-  }
-  __syncthreads();
-  if (threadIdx.x < PACK_CLASSES) w.pcount[threadIdx.x] = carry[threadIdx.x];
-  if (threadIdx.x == 64) {
-    uint32_t run = 0;
-#pragma unroll
-    for (int c = PACK_CLASSES - 1; c >= 0; --c) {
-      run += (carry[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
-      w.uend[c] = run;
-    }
-  }
-  if (threadIdx.x == 0 && w.gate) {
-    // k_long_prep (the previous kernel) has counted the pieces over WIDE_MAX
-    w.gate[GATE_BIG] = *w.nbig;
-    __threadfence_system();
-    w.gate[GATE_SEQ] = w.seq;
-    __threadfence_system();
-  }
-}
-
-// list every packed piece of a tile at its class offset (the order inside
-// a tile's share does not matter: each piece is merged on its own)
-__global__ __launch_bounds__(PRETOK_TPB) void k_pack_scatter(DevTables t,
-                                                             DevWork w) {
-  __shared__ uint32_t lcnt[PACK_CLASSES];
-  const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
-  const int64_t base = (int64_t)blockIdx.x * PT_TILE;
-  if (tid < PACK_CLASSES)
-    lcnt[tid] = w.poff[tid] + w.pblk[(int64_t)tid * gridDim.x + blockIdx.x];
-  __syncthreads();
-  const bool two = !t.ignore_merges;
-  for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
-    const int64_t a = base + 64 * k + lane;
-    if (a >= w.nb) break;
-    const int64_t wd = a >> 6;
-    const int kind = piece_kind(w.starts[wd], w.starts[wd + 1], lane, two);
-    if (kind >= 0) w.plist[atomicAdd(&lcnt[kind], 1u)] = (uint32_t)a;
-  }
-}
-
 constexpr uint32_t pack_geo(int c) {
   return (uint32_t)pack_slot(c) | (uint32_t)pack_per_unit(c) << 8 |
          (uint32_t)pack_magic(c) << 16;
@@ -1196,15 +1154,6 @@ void k_bpe_pack(DevTables t, DevWork w) {
     const int ps = elig ? slot * sl : lane, pe = elig ? slot * sl + (int)L : lane + 1;
     wave_bpe<true, false, true>(t, w, 0, a + off, lane, elig, ps, pe);
   }
-}
-
-hipError_t launch_pack_lists(const DevTables& t, const DevWork& w,
-                             hipStream_t s, hipEvent_t stop) {
-  const int64_t ntile = pretok_tiles(w.nb);
-  hipLaunchKernelGGL(k_pack_scan, dim3(1), dim3(1024), 0, s, w, ntile);
-  launch_ev(k_pack_scatter, dim3((uint32_t)ntile), dim3(PRETOK_TPB), s,
-            nullptr, stop, t, w);
-  return hipGetLastError();
 }
 
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
@@ -1551,6 +1500,177 @@ __device__ void wave_bpe_wide(const DevTables& t, const DevWork& w,
   if (hist && lane == 0) w.hmeta[a] = nfirst | (nlast << 16);
 }
 
+// Wave-wide minimum (the prefix minimum's last lane), as a scalar.
+__device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
+  v = dpp_min<0x111, 0xF>(v);
+  v = dpp_min<0x112, 0xF>(v);
+  v = dpp_min<0x114, 0xF>(v);
+  v = dpp_min<0x118, 0xF>(v);
+  v = dpp_min<0x142, 0xA>(v);
+  v = dpp_min<0x143, 0xC>(v);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// One piece of 65..64R bytes merged by one wave with its state in registers:
+// position p = 64r + lane sits in row r (symbol, pair rank and product per
+// row and lane; live masks per row). Same order as wave_bpe_wide: each round
+// takes the lowest-ranked pair, and a safe rank merges all its leftmost
+// non-overlapping occurrences at once, an unsafe one its leftmost alone.
+// Per round: one wave minimum, the selection on the scalar unit, and pair
+// lookups for the positions whose pair changed (the winners and the live
+// positions before them).
+template <int R>
+__device__ void wave_bpe_rows(const DevTables& t, const DevWork& w, uint32_t a,
+                              int len, bool vocab_first) {
+  const int lane = threadIdx.x & 63;
+  if (vocab_first && t.ignore_merges) {
+    int32_t hit = -1;
+    if (lane == 0) hit = vocab_lookup(t, w.text + a, len);
+    hit = __shfl(hit, 0);
+    if (hit >= 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int p = 64 * r + lane;
+        if (p < len) w.tok[a + p] = p == 0 ? (uint32_t)hit : INVALID_ID;
+      }
+      return;
+    }
+  }
+  uint32_t sym[R], rk[R], mid[R];
+  uint64_t live[R], dirty[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int p = 64 * r + lane;
+    const uint32_t byte = p < len ? w.text[a + p] : 0u;
+    const int32_t bid = p < len ? t.byte_id[byte] : -1;
+    sym[r] = (uint32_t)bid | (byte << 20) | SYM_BYTE;
+    live[r] = __ballot(bid >= 0);
+    dirty[r] = live[r];
+    rk[r] = RANK_INF;
+    mid[r] = 0;
+  }
+  const uint64_t above = ~mask_le(lane);
+  // next / previous live position of position q (scalar), -1 when none
+  auto next_live = [&](int q) {
+    int res = -1;
+#pragma unroll
+    for (int r = R - 1; r >= 0; --r) {
+      uint64_t m = live[r];
+      if (r == (q >> 6)) m &= ~mask_le(q & 63);
+      else if (r < (q >> 6)) m = 0;
+      if (m) res = 64 * r + __builtin_ctzll(m);
+    }
+    return res;
+  };
+  auto prev_live = [&](int q) {
+    int res = -1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint64_t m = live[r];
+      if (r == (q >> 6)) m &= (1ULL << (q & 63)) - 1;
+      else if (r > (q >> 6)) m = 0;
+      if (m) res = 64 * r + 63 - __builtin_clzll(m);
+    }
+    return res;
+  };
+  for (;;) {
+    // the first live position after each row
+    int nf[R];
+    {
+      int f = -1;
+#pragma unroll
+      for (int r = R - 1; r >= 0; --r) {
+        nf[r] = f;
+        if (live[r]) f = 64 * r + __builtin_ctzll(live[r]);
+      }
+    }
+    // pair ranks at the dirty positions
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (!dirty[r]) continue;  // wave-uniform
+      const uint64_t after = live[r] & above;
+      const int nl = after ? __builtin_ctzll(after) : 64;
+      uint32_t ns = (uint32_t)__builtin_amdgcn_ds_bpermute(nl << 2, (int)sym[r]);
+      bool has = nl < 64;
+      if (nf[r] >= 0) {  // wave-uniform: the later rows' first live symbol
+        uint32_t fs = 0;
+#pragma unroll
+        for (int q = r + 1; q < R; ++q)
+          if ((nf[r] >> 6) == q) fs = __builtin_amdgcn_readlane(sym[q], nf[r] & 63);
+        if (!has) ns = fs;
+        has = true;
+      }
+      if (lane_bit(dirty[r])) {
+        rk[r] = RANK_INF;
+        if (has) {
+          if (sym[r] & ns & SYM_BYTE) {
+            const uint64_t v =
+                t.bytepair[((sym[r] >> 12) & 0xFF00) | ((ns >> 20) & 0xFF)];
+            if (v != ~0ULL) { rk[r] = (uint32_t)(v >> 32); mid[r] = (uint32_t)v; }
+          } else if (t.ctab) {
+            uint32_t r_, m_;
+            if (ctab_find(t, sym[r] & SYM_ID, ns & SYM_ID, &r_, &m_)) {
+              rk[r] = r_;
+              mid[r] = m_;
+            }
+          } else {
+            const uint64_t v = pair_lookup(t, sym[r] & SYM_ID, ns & SYM_ID);
+            if (v != ~0ULL) { rk[r] = (uint32_t)(v >> 32); mid[r] = (uint32_t)v; }
+          }
+        }
+      }
+    }
+    uint32_t m = RANK_INF;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane_bit(live[r]) && rk[r] != RANK_INF)
+        m = min(m, (rk[r] << 9) | (uint32_t)(64 * r + lane));
+    const uint32_t best = wave_min_dpp(m);
+    if (best == RANK_INF) break;
+    const uint32_t rank = best >> 9;
+    // the merges of this round, as bits r of the lane holding position
+    // 64r + lane: winners, the positions they absorb, the positions whose
+    // pair changes
+    uint32_t wbit = 0, gbit = 0, dbit = 0;
+    auto set = [&](uint32_t& bits, int q) {
+      if (q >= 0 && lane == (q & 63)) bits |= 1u << (q >> 6);
+    };
+    auto take = [&](int q) {
+      const int g = next_live(q);
+      set(wbit, q);
+      set(gbit, g);
+      set(dbit, q);
+      set(dbit, prev_live(q));
+      return g;
+    };
+    if (rank_unsafe(t, rank)) {
+      take((int)(best & 511));
+    } else {
+      int blocked = -1;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        uint64_t o = __builtin_amdgcn_ballot_w64(lane_bit(live[r]) && rk[r] == rank);
+        while (o) {  // wave-uniform, positions in order
+          const int q = 64 * r + __builtin_ctzll(o);
+          o &= o - 1;
+          if (q != blocked) blocked = take(q);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if ((wbit >> r) & 1) sym[r] = mid[r];
+      live[r] &= ~__builtin_amdgcn_ballot_w64((gbit >> r) & 1);
+      dirty[r] = __builtin_amdgcn_ballot_w64((dbit >> r) & 1) & live[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int p = 64 * r + lane;
+    if (p < len) w.tok[a + p] = lane_bit(live[r]) ? (sym[r] & SYM_ID) : INVALID_ID;
+  }
+}
+
 // Entries of 65..WIDE_MAX bytes from a (start, end) list, one wave each.
 __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
                                                   const uint32_t* list,
@@ -1561,29 +1681,55 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
   if (n > cap) n = cap;
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
+  // These waves are few and latency-bound (one merge round after another)
+  // while k_bpe_pack fills the same SIMDs: they get issue priority.
+  if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
-    if (len <= 64 || len > WIDE_MAX) continue;  // wave-uniform
+    // (pieces of up to 256 bytes without histories: k_bpe_rows)
+    if (len <= (hist ? 64 : 256) || len > WIDE_MAX) continue;  // wave-uniform
     wave_bpe_wide(t, w, a, len, !hist, hist != 0, lds[wv]);
+  }
+}
+
+// Long-list entries of 65..256 bytes (no histories), one wave each, state in
+// registers.
+__global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
+  uint32_t n = *w.longcount;
+  if (n > w.long_cap) n = w.long_cap;
+  const int wv = wave_id();
+  const uint32_t waves = gridDim.x * 4;
+  // few, latency-bound waves beside k_bpe_pack on the same SIMDs
+  if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
+  for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
+    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    const int len = (int)(b - a);
+    if (len <= 64 || len > 256) continue;  // wave-uniform
+    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true);
+    else wave_bpe_rows<4>(t, w, a, len, true);
   }
 }
 
 // Queued pieces over WIDE_MAX bytes: a whole-vocabulary hit
 // (ignore_merges), the serial path when certification is off, else mark
 // their bytes in inlong for the cut / segment / certify stages.
-__global__ __launch_bounds__(256) void k_long_prep(DevTables t, DevWork w) {
+// Long pieces (blocks blk of nblk, 256 threads each): the ends of the queued
+// starts, and the pieces over WIDE_MAX bytes -- a whole-vocabulary hit, the
+// serial merge when certification is off, else their bytes marked in
+// inlong and counted in nbig.
+__device__ void long_prep(const DevTables& t, const DevWork& w, uint32_t blk,
+                          uint32_t nblk) {
   __shared__ uint32_t nbig;
   if (threadIdx.x == 0) nbig = 0;
   __syncthreads();
   const int lane = threadIdx.x & 63;
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
-  const uint32_t waves = gridDim.x * (blockDim.x / 64);
+  const uint32_t waves = nblk * 4;
   // 64 entries per wave and step: lane j resolves entry k0 + j, then the
   // wave handles the entries over WIDE_MAX bytes one by one
-  for (uint32_t k0 = (blockIdx.x * (blockDim.x / 64) + wave_id()) * 64;
-       k0 < n; k0 += waves * 64) {
+  for (uint32_t k0 = (blk * 4 + wave_id()) * 64; k0 < n; k0 += waves * 64) {
     const uint32_t k = k0 + lane;
     uint32_t a = 0, b = 0;
     if (k < n) {
@@ -1626,6 +1772,84 @@ __global__ __launch_bounds__(256) void k_long_prep(DevTables t, DevWork w) {
   }
   __syncthreads();
   if (threadIdx.x == 0 && nbig) atomicAdd(w.nbig, nbig);
+}
+
+// The piece lists, one launch after k_pretok: block c < PACK_CLASSES turns
+// class c's per-tile counts into per-tile offsets (exclusive prefix over the
+// tiles, in place) and its total; the other blocks run long_prep.
+constexpr int LONG_PREP_BLOCKS = 256;
+__global__ __launch_bounds__(256) void k_lists(DevTables t, DevWork w,
+                                               int64_t ntile) {
+  if (blockIdx.x < PACK_CLASSES) {
+    const int c = blockIdx.x;
+    uint32_t* row = w.pblk + (int64_t)c * ntile;
+    const int64_t per = (ntile + 255) / 256;
+    const int64_t lo = threadIdx.x * per, hi = lo + per < ntile ? lo + per : ntile;
+    uint32_t sum = 0;
+    for (int64_t j = lo; j < hi; ++j) sum += row[j];
+    uint32_t tot;
+    uint32_t acc = block_excl_scan(sum, &tot);
+    for (int64_t j = lo; j < hi; ++j) {
+      const uint32_t v = row[j];
+      row[j] = acc;
+      acc += v;
+    }
+    if (threadIdx.x == 0) w.pcount[c] = tot;
+    return;
+  }
+  long_prep(t, w, blockIdx.x - PACK_CLASSES, gridDim.x - PACK_CLASSES);
+}
+
+// Gathers the tiles' class lists into one list per class (tile t's pieces of
+// class c at poff[c] + its offset; the order inside a tile's share does not
+// matter: each piece is merged on its own). Block 0 also lays out
+// k_bpe_pack's work units and opens the gate: how many pieces are over 64
+// bytes (k_pretok queued them) and how many over WIDE_MAX (k_lists counted
+// them).
+__global__ __launch_bounds__(256) void k_pack_copy(DevWork w, int64_t ntile) {
+  __shared__ uint32_t cbeg[PACK_CLASSES + 1];  // prefix of the tile's counts
+  __shared__ uint32_t cdst[PACK_CLASSES], csrc[PACK_CLASSES];
+  const int tid = threadIdx.x;
+  const int64_t tl = blockIdx.x;
+  if (tid < PACK_CLASSES) {
+    const uint32_t off = w.pblk[(int64_t)tid * ntile + tl];
+    const uint32_t nxt = tl + 1 < ntile ? w.pblk[(int64_t)tid * ntile + tl + 1]
+                                        : w.pcount[tid];
+    cdst[tid] = w.poff[tid] + off;
+    csrc[tid] = PACK_LOCAL_OFF[tid];
+    cbeg[tid + 1] = nxt - off;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    cbeg[0] = 0;
+    for (int c = 0; c < PACK_CLASSES; ++c) cbeg[c + 1] += cbeg[c];
+  }
+  __syncthreads();
+  const uint32_t n = cbeg[PACK_CLASSES];
+  const uint32_t* src = w.plocal + tl * PT_LOCAL_SLOTS;
+  for (uint32_t j = tid; j < n; j += 256) {
+    int c = 0;
+#pragma unroll
+    for (int q = 1; q < PACK_CLASSES; ++q) c += j >= cbeg[q];
+    const uint32_t k = j - cbeg[c];
+    w.plist[cdst[c] + k] = src[csrc[c] + k];
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    uint32_t run = 0;
+#pragma unroll
+    for (int c = PACK_CLASSES - 1; c >= 0; --c) {
+      run += (w.pcount[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
+      w.uend[c] = run;
+    }
+    if (w.gate) {
+      const uint32_t nl = *w.longcount;
+      w.gate[GATE_NLONG] = nl < w.long_cap ? nl : w.long_cap;
+      w.gate[GATE_BIG] = *w.nbig;
+      __threadfence_system();
+      w.gate[GATE_SEQ] = w.seq;
+      __threadfence_system();
+    }
+  }
 }
 
 __device__ __forceinline__ uint64_t inlong_window(const DevWork& w, int64_t v,
@@ -1798,16 +2022,28 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   }
 }
 
-hipError_t launch_long_prep(const DevTables& t, const DevWork& w,
-                            hipStream_t s) {
-  hipLaunchKernelGGL(k_long_prep, dim3(256), dim3(256), 0, s, t, w);
+hipError_t launch_lists(const DevTables& t, const DevWork& w, hipStream_t s) {
+  const int64_t ntile = pretok_tiles(w.nb);
+  hipLaunchKernelGGL(k_lists, dim3(PACK_CLASSES + LONG_PREP_BLOCKS), dim3(256),
+                     0, s, t, w, ntile);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_copy(const DevWork& w, hipStream_t s, hipEvent_t stop) {
+  const int64_t ntile = pretok_tiles(w.nb);
+  launch_ev(k_pack_copy, dim3((uint32_t)ntile), dim3(256), s, nullptr, stop, w,
+            ntile);
   return hipGetLastError();
 }
 
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop) {
-  // pieces of 65..WIDE_MAX bytes are merged whole, one wave each
-  launch_ev(k_bpe_wide, dim3(2048), dim3(256), s, nullptr, stop, t, w,
+                           hipEvent_t stop, uint32_t nlong) {
+  // pieces of 65..WIDE_MAX bytes are merged whole, one wave each (a wave
+  // per queued long piece, up to 2048 blocks of four): up to 256 bytes in
+  // registers (k_bpe_rows), longer ones with their state in LDS
+  const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
+  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), 0, s, t, w);
+  launch_ev(k_bpe_wide, dim3(blocks), dim3(256), s, nullptr, stop, t, w,
             (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
             w.long_cap, 0);
   return hipGetLastError();
@@ -1852,23 +2088,6 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 }
 
 // ------------------------------------------------------ 4. compaction
-
-// exclusive scan of one value per thread over a 256-thread block
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
-  __shared__ uint32_t wsum[4];
-  const int lane = threadIdx.x & 63, wv = wave_id();
-  const uint32_t inc = wave_incl_scan(v, lane);
-  if (lane == 63) wsum[wv] = inc;
-  __syncthreads();
-  uint32_t off = 0, tot = 0;
-  for (int k = 0; k < 4; ++k) {
-    if (k < wv) off += wsum[k];
-    tot += wsum[k];
-  }
-  __syncthreads();
-  *total = tot;
-  return off + inc - v;
-}
 
 // Token slots are read lane-interleaved (consecutive lanes, consecutive
 // bytes) so every load and every output store of a wave is contiguous.

@@ -183,7 +183,7 @@ struct tk_engine {
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
   DevBuf<int32_t> nx, pv;
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
-  DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk;
+  DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk, plocal;
   size_t docs_cap = 0;
   uint32_t slot = 0;  // control slot of the next call
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
@@ -196,7 +196,7 @@ struct tk_engine {
   hipEvent_t ev[8] = {};
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
-  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  hipEvent_t ev_join = nullptr;  // side stream -> engine stream
   double last_us[5] = {};
   size_t last_passes = 0;
 };
@@ -263,6 +263,7 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->out.alloc(need));
     HIP_TRY(e->plist.alloc((size_t)tk::pack_off((int64_t)need, tk::PACK_CLASSES)));
     HIP_TRY(e->pblk.alloc((size_t)tk::PACK_CLASSES * tk::pretok_tiles((int64_t)need)));
+    HIP_TRY(e->plocal.alloc((size_t)tk::PT_LOCAL_SLOTS * tk::pretok_tiles((int64_t)need)));
     e->cap = need;
   }
   if (n_docs + 1 > e->docs_cap) {
@@ -308,6 +309,7 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.dirty_cur = e->dirty_cur.p;
   w.dirty_next = e->dirty_next.p;
   w.plist = e->plist.p;
+  w.plocal = e->plocal.p;
   for (int c = 0; c < tk::PACK_CLASSES; ++c)
     w.poff[c] = (uint32_t)tk::pack_off((int64_t)nb, c);  // < 2^32 for nb <= 1 GiB
   w.pblk = e->pblk.p;
@@ -331,7 +333,7 @@ int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
   return TK_OK;
 }
 
-// Wait until k_pack_scan of call `seq` has written the gate words (a
+// Wait until k_pack_copy of call `seq` has written the gate words (a
 // spin on host memory). A device fault would stop the writer, so after a
 // generous bound the stream is synchronized to surface its error.
 int wait_gate(tk_engine* e, uint32_t seq, hipStream_t s) {
@@ -372,9 +374,9 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
   // Timing mode 1, stage boundaries taken by the dispatches themselves:
-  // ev[0] start of k_pretok; ev[1] end of the piece listing (k_long_prep,
-  // k_pack_scan, k_pack_scatter); ev[2] end of k_bpe_pack; ev[3] end of the
-  // long-piece stages on the side stream; ev[4] end
+  // ev[0] start of k_pretok; ev[1] end of the piece listing (k_lists,
+  // k_pack_copy); ev[2] end of k_bpe_pack; ev[3] end of the
+  // long-piece stages on the side stream (when there are long pieces); ev[4] end
   // of the compaction. Mode 2: ev[1] / ev[2] are the start / end of
   // k_bpe_pack's own dispatch only. (Each timed dispatch delays the next
   // one by a few microseconds, so the events sit on as few dispatches as
@@ -383,35 +385,32 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
   HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
   e->slot ^= 1;  // this call's k_pretok clears the other slot
-  HIP_TRY(tk::launch_long_prep(e->t, w, s));
-  // The long-piece stages need only k_pretok and k_long_prep: they run on
-  // the side stream, k_bpe_wide (latency-bound, few waves) from here on,
-  // beside the piece listing and the packed merge.
-  hipStream_t s2 = e->stream2;
-  HIP_TRY(hipEventRecord(e->ev_fork, s));  // long pieces resolved
-  HIP_TRY(hipStreamWaitEvent(s2, e->ev_fork, 0));
-  HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr));
-  HIP_TRY(tk::launch_pack_lists(e->t, w, s, at(1)));  // k_pack_scan writes the gate
+  HIP_TRY(tk::launch_lists(e->t, w, s));
+  HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
                               stages || packonly ? ev[2] : nullptr));
-  // The cut / certify stages run only when a piece over WIDE_MAX bytes
-  // exists: the device tells through the gate words while the packed
-  // merge is still running, so the decision costs no device time.
-  uint32_t big = 0;
-  if (e->t.cert) {
-    int grc = wait_gate(e, w.seq, s);
-    if (grc != TK_OK) return grc;
-    big = e->gate[tk::GATE_BIG];
+  // The gate words tell, while the packed merge runs, how many pieces are
+  // over 64 bytes and whether any is over WIDE_MAX. Only then do the
+  // long-piece stages go on the side stream, beside k_bpe_pack: they need
+  // k_lists alone, which ran before k_pack_copy opened the gate, so no
+  // event orders them (and none is needed when there is no long piece).
+  int grc = wait_gate(e, w.seq, s);
+  if (grc != TK_OK) return grc;
+  const uint32_t nlong = e->gate[tk::GATE_NLONG];
+  const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
+  if (nlong > 0) {
+    hipStream_t s2 = e->stream2;
+    HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
+    if (big) {
+      HIP_TRY(tk::launch_long_windows(e->t, w, s2));
+      HIP_TRY(tk::launch_long_segments(e->t, w, 1, s2));
+      HIP_TRY(tk::launch_certify(e->t, w, 1, s2, at(3)));
+    } else if (stages) {
+      HIP_TRY(hipEventRecord(ev[3], s2));
+    }
+    HIP_TRY(hipEventRecord(e->ev_join, s2));
+    HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
   }
-  if (big) {
-    HIP_TRY(tk::launch_long_windows(e->t, w, s2));
-    HIP_TRY(tk::launch_long_segments(e->t, w, 1, s2));
-    HIP_TRY(tk::launch_certify(e->t, w, 1, s2, at(3)));
-  } else if (stages) {
-    HIP_TRY(hipEventRecord(ev[3], s2));
-  }
-  HIP_TRY(hipEventRecord(e->ev_join, s2));
-  HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
   HIP_TRY(tk::launch_compact(w, s, nullptr, at(4)));
   // k_scan has left the outcome in the gate words: no read-back copy
   HIP_TRY(hipStreamSynchronize(s));
@@ -427,7 +426,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
     const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
-    const double t3 = elapsed_us(ev[0], ev[3]);
+    const double t3 = nlong > 0 ? elapsed_us(ev[0], ev[3]) : 0.0;
     const double t4 = elapsed_us(ev[0], ev[4]);
     e->last_us[0] = t1;
     e->last_us[1] = t2 - t1;
@@ -606,11 +605,10 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&e->stream2, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
-  // fork / join between the engine's two streams on one device: no
+  // join of the side stream into the engine stream (one device): no
   // system-scope fence
-  const unsigned fj = hipEventDisableTiming | hipEventDisableSystemFence;
-  if (hipEventCreateWithFlags(&e->ev_fork, fj) != hipSuccess ||
-      hipEventCreateWithFlags(&e->ev_join, fj) != hipSuccess)
+  if (hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming |
+                                               hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
@@ -720,7 +718,6 @@ void tk_engine_close(tk_engine* e) {
   for (auto& ev : e->ev)
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream2) (void)hipStreamSynchronize(e->stream2);
-  if (e->ev_fork) (void)hipEventDestroy(e->ev_fork);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->stream2) (void)hipStreamDestroy(e->stream2);
