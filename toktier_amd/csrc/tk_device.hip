@@ -1521,7 +1521,8 @@ __device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
 // positions before them).
 template <int R>
 __device__ void wave_bpe_rows(const DevTables& t, const DevWork& w, uint32_t a,
-                              int len, bool vocab_first) {
+                              int len, bool vocab_first,
+                              const uint32_t* unsafe_lds) {
   const int lane = threadIdx.x & 63;
   if (vocab_first && t.ignore_merges) {
     int32_t hit = -1;
@@ -1643,7 +1644,11 @@ __device__ void wave_bpe_rows(const DevTables& t, const DevWork& w, uint32_t a,
       set(dbit, prev_live(q));
       return g;
     };
-    if (rank_unsafe(t, rank)) {
+    const bool unsafe =
+        unsafe_lds ? ((rank >> 5) < t.unsafe_words &&
+                      ((unsafe_lds[rank >> 5] >> (rank & 31)) & 1))
+                   : rank_unsafe(t, rank);
+    if (unsafe) {
       take((int)(best & 511));
     } else {
       int blocked = -1;
@@ -1695,7 +1700,17 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
 
 // Long-list entries of 65..256 bytes (no histories), one wave each, state in
 // registers.
+// With an unsafe-rank bitmap of at most ROWS_UNSAFE_LDS words, the launch
+// gives each block a copy of it in LDS (one lookup per merge round).
+constexpr uint32_t ROWS_UNSAFE_LDS = 12288;
 __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
+  extern __shared__ uint32_t unsafe_lds[];
+  const bool lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS;
+  if (lds) {
+    for (uint32_t j = threadIdx.x; j < t.unsafe_words; j += 256)
+      unsafe_lds[j] = t.unsafe[j];
+    __syncthreads();
+  }
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   const int wv = wave_id();
@@ -1706,8 +1721,9 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
     const int len = (int)(b - a);
     if (len <= 64 || len > 256) continue;  // wave-uniform
-    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true);
-    else wave_bpe_rows<4>(t, w, a, len, true);
+    const uint32_t* ul = lds ? unsafe_lds : nullptr;
+    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, ul);
+    else wave_bpe_rows<4>(t, w, a, len, true, ul);
   }
 }
 
@@ -1732,12 +1748,39 @@ __device__ void long_prep(const DevTables& t, const DevWork& w, uint32_t blk,
   for (uint32_t k0 = (blk * 4 + wave_id()) * 64; k0 < n; k0 += waves * 64) {
     const uint32_t k = k0 + lane;
     uint32_t a = 0, b = 0;
+    bool far = false;
     if (k < n) {
-      // k_pretok queued the start only; the end is the next start bit
+      // k_pretok queued the start only; the end is the next start bit,
+      // found here when it lies in the piece's first two words
       a = w.longlist[2 * k];
-      b = (uint32_t)piece_end(w, a);
-      w.longlist[2 * k + 1] = b;
+      const int64_t wd = a >> 6;
+      const uint64_t gt = w.starts[wd] & ~mask_le((int)(a & 63));
+      const uint64_t nx = w.starts[wd + 1];
+      if (gt) b = (uint32_t)(wd * 64 + __builtin_ctzll(gt));
+      else if (nx) b = (uint32_t)((wd + 1) * 64 + __builtin_ctzll(nx));
+      else far = true;
     }
+    // longer pieces: the wave reads 64 words at a time (the words pretok
+    // wrote end at nwords, and the word holding byte nb has a start bit at
+    // or after nb, so the search ends before them)
+    const int64_t nwords = (w.nb + 63) / 64 + 2;
+    for (uint64_t pend = __ballot(far); pend; pend &= pend - 1) {
+      const int j = __builtin_ctzll(pend);
+      const uint32_t pa = __shfl(a, j);
+      uint32_t end = 0;
+      for (int64_t wd = (pa >> 6) + 2;; wd += 64) {
+        const uint64_t word = wd + lane < nwords ? w.starts[wd + lane] : ~0ULL;
+        const uint64_t nz = __ballot(word != 0);
+        if (nz) {
+          const int l = __builtin_ctzll(nz);
+          const uint64_t wl = __shfl(word, l);
+          end = (uint32_t)((wd + l) * 64 + __builtin_ctzll(wl));
+          break;
+        }
+      }
+      if (lane == j) b = end;
+    }
+    if (k < n) w.longlist[2 * k + 1] = b;
     uint64_t big = __ballot(k < n && b - a > (uint32_t)WIDE_MAX);
     if (lane == 0 && big) atomicAdd(&nbig, (uint32_t)__popcll(big));
     while (big) {  // wave-uniform
@@ -2042,7 +2085,9 @@ hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
   // per queued long piece, up to 2048 blocks of four): up to 256 bytes in
   // registers (k_bpe_rows), longer ones with their state in LDS
   const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
-  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), 0, s, t, w);
+  const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
+                         ? (size_t)t.unsafe_words * 4 : 0;
+  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, t, w);
   launch_ev(k_bpe_wide, dim3(blocks), dim3(256), s, nullptr, stop, t, w,
             (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
             w.long_cap, 0);
