@@ -16,6 +16,7 @@ constexpr uint32_t ST_UTF8 = 1u;     // invalid UTF-8 seen
 constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
 constexpr uint32_t ST_CAPACITY = 8u;  // more ids than the output holds
+constexpr uint32_t ST_STALL = 16u;    // compaction look-back timed out (internal)
 
 // Compact pair table: 16-byte buckets of two u64 slots, two candidate
 // buckets per pair (cuckoo placement), so a lookup is two independent
@@ -91,6 +92,7 @@ struct DevWork {
   uint32_t* status;      // ctrl[0]; ctrl[1] = total ids
   uint32_t* blkcount;    // per compaction block
   uint32_t* blkprefix;   // exclusive prefix, [nblk + 1]
+  uint64_t* cstat;       // [nblk] compaction status words (look-back)
   uint32_t* out;         // compacted ids
   uint32_t out_cap;      // capacity of out in ids
   // long-piece segmentation (one bit / slot per byte)
@@ -129,7 +131,7 @@ constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_WORDS = 64;
 // gate words in host memory: k_pack_copy writes GATE_NLONG / GATE_BIG and
 // then GATE_SEQ (the host learns, while the packed merge runs, whether the
-// long-piece stages have any work), k_scan
+// long-piece stages have any work), k_compact's last block
 // writes the request's outcome (status, id count, failed cuts) and then
 // GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
@@ -201,9 +203,8 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
-hipError_t launch_compact(const DevWork& w, hipStream_t s,
-                          hipEvent_t start = nullptr,
-                          hipEvent_t stop = nullptr);
+hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
+                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);

@@ -1,24 +1,27 @@
 // tk_device.hip -- gfx950 kernels of the fresh-encode path.
 //
-// Stages (one stream, no host round trip in between):
+// Stages (one stream; the long-piece stages on a second one, beside stage 2):
 //   1. k_pretok       per byte: UTF-8 validation, class lookup, NFC quick
 //                     check, and the family split rules as a per-character
 //                     piece-start predicate -> one start bit per byte.
 //      (k_pretok also sizes the pieces that start in its tile: pieces of
 //                     1-2 bytes are finished there, longer than 64 queued
-//                     for stage 3, the rest counted by length class.)
-//   2. k_pack_scan / k_pack_scatter list the pieces of 2..64 bytes by
-//                     length class; k_bpe_pack merges them (lowest rank
+//                     for stage 3, the rest listed by length class in the
+//                     tile's own region.)
+//   2. k_lists / k_pack_copy gather the pieces of 2..64 bytes into one list
+//                     per length class; k_bpe_pack merges them (lowest rank
 //                     pair, leftmost first) with segmented wave reductions,
 //                     lane = byte, 64 / slot pieces of one class per wave.
-//   3. long pieces    (> 64 bytes) are cut into short segments at likely
-//                     token boundaries (k_long_windows), merged segment by
-//                     segment with boundary-token histories
-//                     (k_long_segments), and every cut is certified
-//                     (k_certify); failed cuts are removed and the affected
-//                     segments redone until every cut holds.
-//   4. k_count / k_scan / k_compact: device-wide compaction of the per-byte
-//                     token slots into the contiguous id buffer.
+//   3. long pieces    (> 64 bytes): up to 256 bytes merged whole, one wave
+//                     each, state in registers (k_bpe_rows), up to 512 in
+//                     LDS (k_bpe_wide); longer ones are cut into short
+//                     segments at likely token boundaries (k_long_windows),
+//                     merged segment by segment with boundary-token
+//                     histories (k_long_segments), and every cut is
+//                     certified (k_certify); failed cuts are removed and the
+//                     affected segments redone until every cut holds.
+//   4. k_compact      device-wide compaction of the per-byte token slots
+//                     into the contiguous id buffer, one pass (look-back).
 // Token j of a piece is stored at the byte where that token starts, so the
 // id order is the byte order and stage 4 needs no per-piece counts.
 //
@@ -1095,8 +1098,8 @@ __device__ __forceinline__ void window_bits(int64_t v, int phase, SegBits seg,
 // ---- pieces of up to 64 bytes, packed by length
 //
 // k_pretok counted the pieces of each tile by length class (pieces of
-// pack_lmin(c)..pack_slot(c) bytes); k_pack_scan turns the counts into
-// per-tile offsets, k_pack_scatter lists the piece starts by class, and
+// pack_lmin(c)..pack_slot(c) bytes); k_lists turns the counts into
+// per-tile offsets, k_pack_copy gathers the tiles' lists by class, and
 // k_bpe_pack merges them with one wave per work unit: 64 / slot pieces of
 // one class on slot lanes each. The rounds a wave runs then follow its own
 // pieces' lengths rather than the longest piece of a stretch of text.
@@ -2134,100 +2137,117 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 
 // ------------------------------------------------------ 4. compaction
 
-// Token slots are read lane-interleaved (consecutive lanes, consecutive
-// bytes) so every load and every output store of a wave is contiguous.
-__global__ __launch_bounds__(COMPACT_TPB) void k_count(DevWork w, int64_t nblk) {
-  const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
-  uint32_t c = 0;
-#pragma unroll
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
-    const int64_t p = base + (int64_t)k * COMPACT_TPB;
-    if (p < w.nb && w.tok[p] != INVALID_ID) ++c;
-  }
-  uint32_t tot;
-  block_excl_scan(c, &tot);
-  if (threadIdx.x == 0) w.blkcount[blockIdx.x] = tot;
+// One pass over the token slots: every block counts the ids in its
+// COMPACT_BLOCK slots (COMPACT_PER_THREAD consecutive slots per thread),
+// publishes the count, takes its offset from its predecessors' words
+// (decoupled look-back: the nearest predecessor that has published a running
+// total, plus the counts in between, 64 predecessors per step), publishes
+// its running total and writes its ids. A status word is tag << 32 |
+// CST_TOTAL (a running total, else a count) | value: words left by other
+// launches carry other tags and read as not yet published. A block waits
+// only for blocks dispatched before it, which publish their counts without
+// waiting, and every wait is bounded.
+constexpr uint32_t CST_TOTAL = 1u << 31;
+constexpr int COMPACT_SPIN = 1 << 20;
+
+__device__ __forceinline__ void cst_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t cst_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// exclusive prefix of the block counts: each of 1024 threads sums a
-// contiguous run of counts, the block scans the run totals, then each
-// thread writes its run's prefixes
-constexpr int SCAN_TPB = 1024;
-__global__ __launch_bounds__(SCAN_TPB) void k_scan(DevWork w, int64_t nblk) {
-  __shared__ uint32_t wsum[SCAN_TPB / 64];
-  const int lane = threadIdx.x & 63, wv = wave_id();
-  const int64_t per = (nblk + SCAN_TPB - 1) / SCAN_TPB;
-  const int64_t lo = threadIdx.x * per;
-  uint32_t s = 0;
-  for (int64_t k = lo; k < lo + per && k < nblk; ++k) s += w.blkcount[k];
-  const uint32_t inc = wave_incl_scan(s, lane);
-  if (lane == 63) wsum[wv] = inc;
-  __syncthreads();
-  uint32_t acc = inc - s, tot = 0;
-  for (int q = 0; q < SCAN_TPB / 64; ++q) {
-    if (q < wv) acc += wsum[q];
-    tot += wsum[q];
+__global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk,
+                                                         uint32_t tag) {
+  __shared__ uint32_t sbase;
+  const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
+  const int64_t b = blockIdx.x;
+  const int64_t p0 = b * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
+  uint32_t v[COMPACT_PER_THREAD];
+  if (p0 + COMPACT_PER_THREAD <= w.nb) {
+    const uint4* src = reinterpret_cast<const uint4*>(w.tok + p0);
+#pragma unroll
+    for (int q = 0; q < COMPACT_PER_THREAD / 4; ++q) {
+      const uint4 x = src[q];
+      v[4 * q] = x.x;
+      v[4 * q + 1] = x.y;
+      v[4 * q + 2] = x.z;
+      v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < COMPACT_PER_THREAD; ++k)
+      v[k] = p0 + k < w.nb ? w.tok[p0 + k] : INVALID_ID;
   }
-  if (threadIdx.x == 0) {
-    w.blkprefix[nblk] = tot;
-    w.status[1] = tot;
-    if (tot > w.out_cap) atomicOr(w.status, ST_CAPACITY);
+  uint32_t c = 0;
+#pragma unroll
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) c += v[k] != INVALID_ID;
+  uint32_t tot;
+  const uint32_t off = block_excl_scan(c, &tot);
+  if (wv == 0) {
+    const uint64_t hi = (uint64_t)tag << 32;
+    uint32_t base = 0;
+    bool ok = true;
+    if (b == 0) {
+      if (lane == 0) cst_store(&w.cstat[0], hi | CST_TOTAL | tot);
+    } else {
+      if (lane == 0) cst_store(&w.cstat[b], hi | tot);
+      for (int64_t j = b - 1;; j -= 64) {
+        const int64_t q = j - lane;
+        uint64_t st = hi | CST_TOTAL;  // before block 0: a total of zero
+        if (q >= 0) {
+          st = cst_load(&w.cstat[q]);
+          for (int spin = 0; (st >> 32) != tag && spin < COMPACT_SPIN; ++spin)
+            st = cst_load(&w.cstat[q]);
+          if ((st >> 32) != tag) {
+            ok = false;
+            st = hi | CST_TOTAL;
+          }
+        }
+        const uint64_t tm = __ballot(((uint32_t)st & CST_TOTAL) != 0);
+        const int l = tm ? __builtin_ctzll(tm) : 64;
+        const uint32_t val = lane <= l ? ((uint32_t)st & ~CST_TOTAL) : 0u;
+        base += (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(val, lane), 63);
+        if (tm) break;  // wave-uniform
+      }
+      if (lane == 0) cst_store(&w.cstat[b], hi | CST_TOTAL | (base + tot));
+    }
+    if (lane == 0) {
+      sbase = base;
+      w.blkprefix[b] = base;
+      if (!ok) atomicOr(w.status, ST_STALL);
+    }
+  }
+  __syncthreads();
+  uint32_t o = sbase + off;
+#pragma unroll
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k)
+    if (v[k] != INVALID_ID) {
+      if (o < w.out_cap) w.out[o] = v[k];
+      ++o;
+    }
+  if (b == nblk - 1 && tid == 0) {
+    const uint32_t total = sbase + tot;
+    w.blkprefix[nblk] = total;
+    w.status[1] = total;
+    if (total > w.out_cap) atomicOr(w.status, ST_CAPACITY);
     if (w.gate) {
-      // every stage that sets status bits or failed cuts has finished
+      // every earlier stage that sets status bits or failed cuts has ended
       w.gate[GATE_STATUS] = atomicOr(w.status, 0u);
-      w.gate[GATE_TOTAL] = tot;
+      w.gate[GATE_TOTAL] = total;
       w.gate[GATE_FAIL] = *w.nfail;
       __threadfence_system();
       w.gate[GATE_DONE] = w.seq;
       __threadfence_system();
     }
   }
-  for (int64_t k = lo; k < lo + per && k < nblk; ++k) {
-    w.blkprefix[k] = acc;
-    acc += w.blkcount[k];
-  }
 }
 
-__global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w,
-                                                         int64_t nblk) {
-  __shared__ uint32_t wsum[COMPACT_TPB / 64];
-  if (w.blkprefix[nblk] > w.out_cap) return;  // whole grid: reported by k_scan
-  const int lane = threadIdx.x & 63, wv = wave_id();
-  const int64_t base = (int64_t)blockIdx.x * COMPACT_BLOCK + threadIdx.x;
-  uint32_t run = w.blkprefix[blockIdx.x];
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
-    const int64_t p = base + (int64_t)k * COMPACT_TPB;
-    const uint32_t v = p < w.nb ? w.tok[p] : INVALID_ID;
-    const bool keep = v != INVALID_ID;
-    const uint64_t m = __ballot(keep);
-    if (lane == 0) wsum[wv] = (uint32_t)__popcll(m);
-    __syncthreads();
-    uint32_t before = 0, total = 0;
-#pragma unroll
-    for (int q = 0; q < COMPACT_TPB / 64; ++q) {
-      if (q < wv) before += wsum[q];
-      total += wsum[q];
-    }
-    if (keep)
-      w.out[run + before + (uint32_t)__popcll(m & ((1ULL << lane) - 1))] = v;
-    run += total;
-    __syncthreads();
-  }
-}
-
-hipError_t launch_compact(const DevWork& w, hipStream_t s, hipEvent_t start,
-                          hipEvent_t stop) {
+hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
+                          hipEvent_t start, hipEvent_t stop) {
   const int64_t nblk = (w.nb + COMPACT_BLOCK - 1) / COMPACT_BLOCK;
-  if (nblk > 0) {
-    launch_ev(k_count, dim3((uint32_t)nblk), dim3(COMPACT_TPB), s, start,
-              nullptr, w, nblk);
-  }
-  launch_ev(k_scan, dim3(1), dim3(SCAN_TPB), s, nblk > 0 ? nullptr : start,
-            nblk > 0 ? nullptr : stop, w, nblk);
-  if (nblk > 0) {
-    launch_ev(k_compact, dim3((uint32_t)nblk), dim3(COMPACT_TPB), s, nullptr,
-              stop, w, nblk);
-  }
+  launch_ev(k_compact, dim3((uint32_t)(nblk > 0 ? nblk : 1)), dim3(COMPACT_TPB), s,
+            start, stop, w, nblk > 0 ? nblk : 1, tag);
   return hipGetLastError();
 }
 

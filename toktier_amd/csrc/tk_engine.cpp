@@ -179,7 +179,7 @@ struct tk_engine {
   // workspace
   size_t cap = 0;
   DevBuf<uint8_t> text;
-  DevBuf<uint64_t> starts, docmask, heap, docoffs, rows;
+  DevBuf<uint64_t> starts, docmask, heap, docoffs, rows, cstat;
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
   DevBuf<int32_t> nx, pv;
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
@@ -191,6 +191,7 @@ struct tk_engine {
   volatile uint32_t* gate = nullptr;
   uint32_t* gate_dev = nullptr;
   uint32_t seq = 0;
+  uint32_t ctag = 0;  // compaction launches (status-word tags)
   // timing
   int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
   hipEvent_t ev[8] = {};
@@ -260,6 +261,9 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->dirty_next.alloc(words / 64 + 2));
     HIP_TRY(e->blkcount.alloc(nblk));
     HIP_TRY(e->blkprefix.alloc(nblk));
+    // compaction status words: tags start at 1, so zeroed words never match
+    HIP_TRY(e->cstat.alloc(nblk));
+    HIP_TRY(hipMemset(e->cstat.p, 0, nblk * sizeof(uint64_t)));
     HIP_TRY(e->out.alloc(need));
     HIP_TRY(e->plist.alloc((size_t)tk::pack_off((int64_t)need, tk::PACK_CLASSES)));
     HIP_TRY(e->pblk.alloc((size_t)tk::PACK_CLASSES * tk::pretok_tiles((int64_t)need)));
@@ -294,6 +298,7 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.status = ctrl + tk::CTRL_STATUS;
   w.blkcount = e->blkcount.p;
   w.blkprefix = e->blkprefix.p;
+  w.cstat = e->cstat.p;
   w.out = out;
   w.out_cap = (uint32_t)std::min<size_t>(out_cap, 0xFFFFFFFFu);
   w.inlong = e->inlong.p;
@@ -330,6 +335,8 @@ int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
   HIP_TRY(hipStreamSynchronize(s));
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
+  if (h[tk::CTRL_STATUS] & tk::ST_STALL)
+    return fail(TK_E_INTERNAL, "compaction look-back timed out");
   return TK_OK;
 }
 
@@ -411,7 +418,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
     HIP_TRY(hipEventRecord(e->ev_join, s2));
     HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
   }
-  HIP_TRY(tk::launch_compact(w, s, nullptr, at(4)));
+  HIP_TRY(tk::launch_compact(w, s, ++e->ctag, nullptr, at(4)));
   // k_scan has left the outcome in the gate words: no read-back copy
   HIP_TRY(hipStreamSynchronize(s));
   uint32_t* h = e->host_ctrl;
@@ -422,6 +429,8 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   h[tk::CTRL_FAIL] = e->gate[tk::GATE_FAIL];
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
+  if (h[tk::CTRL_STATUS] & tk::ST_STALL)
+    return fail(TK_E_INTERNAL, "compaction look-back timed out");
   int rc = TK_OK;
   if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
@@ -451,7 +460,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     }
     if (stages) HIP_TRY(hipEventRecord(ev[6], s));
-    HIP_TRY(tk::launch_compact(w, s));
+    HIP_TRY(tk::launch_compact(w, s, ++e->ctag));
     if (stages) HIP_TRY(hipEventRecord(ev[7], s));
     if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     if (stages) {
