@@ -23,7 +23,7 @@ constexpr uint32_t ST_STALL = 16u;    // compaction look-back timed out (interna
 // 16-byte loads and no probe chain; at a load of about 0.6 the table is a
 // quarter of the boundary table's size and stays in an XCD's L2.
 // The pair key (left, right < 2^18) goes through a bijection of 36 bits
-// (two Feistel rounds on the 18-bit halves; the round function is a 24-bit
+// (one Feistel round: left << 18 | right ^ f(left), where f is a 24-bit
 // multiply, full rate on the vector ALU, folded onto itself). Its low
 // `bits` bits are the first bucket, the rest the tag; the second bucket is
 // the first XOR a hash of the tag. Slot = tag<<38 | second<<37 | rank<<18
@@ -36,9 +36,8 @@ __host__ __device__ __forceinline__ uint32_t pair_round(uint32_t x, uint32_t c) 
   return (p ^ (p >> 16)) & 0x3FFFFu;
 }
 __host__ __device__ __forceinline__ uint64_t pair_perm(uint32_t l, uint32_t r) {
-  const uint32_t a = l ^ pair_round(r, 0x9E3779u);
-  const uint32_t b = r ^ pair_round(a, 0x85EBCBu);
-  return ((uint64_t)(a & 0x3FFFFu) << 18) | (b & 0x3FFFFu);
+  const uint32_t b = r ^ pair_round(l, 0x9E3779u);
+  return ((uint64_t)(l & 0x3FFFFu) << 18) | (b & 0x3FFFFu);
 }
 // second bucket of a key with first bucket b1 and tag (< 2^24)
 __host__ __device__ __forceinline__ uint32_t pair_alt(uint32_t b1, uint32_t tag,

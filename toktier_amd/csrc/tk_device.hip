@@ -87,8 +87,8 @@ __device__ __forceinline__ uint64_t pair_lookup(const DevTables& t,
 __device__ __forceinline__ bool ctab_find(const DevTables& t, uint32_t l,
                                           uint32_t r, uint32_t* rank,
                                           uint32_t* id) {
-  const uint32_t a = (l ^ pair_round(r, 0x9E3779u)) & 0x3FFFFu;
-  const uint32_t b = (r ^ pair_round(a, 0x85EBCBu)) & 0x3FFFFu;
+  const uint32_t a = l;
+  const uint32_t b = (r ^ pair_round(l, 0x9E3779u)) & 0x3FFFFu;
   // the 36-bit key a << 18 | b as hi:lo
   const uint32_t lo = (a << 18) | b, hi = a >> 14;
   const uint32_t b1 = lo & (uint32_t)t.cmask;
@@ -981,7 +981,9 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
   const uint32_t seg_lane = ((uint32_t)(63 - src_ps) << 26) | (uint32_t)lane;
   const uint64_t above = ~mask_le(lane);
 
-  uint32_t rk = RANK_INF, mid = 0;
+  // the lane's pair key (seg_lane | rank << 6) and product; RANK_INF when
+  // the lane has no pair with a rule or is no longer live
+  uint32_t kx = RANK_INF, mid = 0;
   uint32_t nfirst = 0, nlast = 0;  // event counts, kept by lane ps
   uint64_t dirty = ~0ULL;          // lanes whose pair changed
   for (;;) {
@@ -990,28 +992,25 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     // (nx = 64 reads lane 0; that value is never used)
     const uint32_t nsym = (uint32_t)__builtin_amdgcn_ds_bpermute(nx << 2, (int)sym);
     if (lane_bit(dirty)) {
-      rk = RANK_INF;
+      kx = RANK_INF;
       if (lane_bit(live) && nx < pe) {
         if (sym & nsym & SYM_BYTE) {
           const uint64_t v =
               t.bytepair[((sym >> 12) & 0xFF00) | ((nsym >> 20) & 0xFF)];
-          if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+          if (v != ~0ULL) { kx = seg_lane | ((uint32_t)(v >> 32) << 6); mid = (uint32_t)v; }
         } else if (t.ctab) {
           uint32_t r_, m_;
           if (ctab_find(t, sym & SYM_ID, nsym & SYM_ID, &r_, &m_)) {
-            rk = r_;
+            kx = seg_lane | (r_ << 6);
             mid = m_;
           }
         } else {
           const uint64_t v = pair_lookup(t, sym & SYM_ID, nsym & SYM_ID);
-          if (v != ~0ULL) { rk = (uint32_t)(v >> 32); mid = (uint32_t)v; }
+          if (v != ~0ULL) { kx = seg_lane | ((uint32_t)(v >> 32) << 6); mid = (uint32_t)v; }
         }
       }
     }
-    // a lane whose symbol was merged away keeps its old pair rank in rk;
-    // only live lanes compete
-    const bool valid = lane_bit(live) && rk != RANK_INF;
-    const uint32_t key = valid ? (seg_lane | (rk << 6)) : RANK_INF;
+    const uint32_t key = kx;
     uint32_t m = key;
     m = dpp_min<0x111, 0xF>(m);  // row_shr:1
     m = dpp_min<0x112, 0xF>(m);  // row_shr:2
@@ -1019,7 +1018,8 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     m = dpp_min<0x118, 0xF>(m);  // row_shr:8
     m = dpp_min<0x142, 0xA>(m);  // row_bcast:15 into rows 1 and 3
     m = dpp_min<0x143, 0xC>(m);  // row_bcast:31 into rows 2 and 3
-    const uint64_t rec = __builtin_amdgcn_ballot_w64(valid && m == key);
+    const uint64_t rec = __builtin_amdgcn_ballot_w64(m == key) &
+                         ~__builtin_amdgcn_ballot_w64(key == RANK_INF);
     if (rec == 0) break;
     // Each segment's winner is its last record: on the bit-reversed masks a
     // carry started at each segment's last lane runs over the lanes that
@@ -1036,7 +1036,7 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
       if (win_) {
         // the merged pair's right symbol is the segment's last symbol
         lastev = nx + 1 >= pe || ((live & lanes_in(nx + 1, pe)) == 0);
-        const uint64_t ev = ((uint64_t)rk << 32) | mid;
+        const uint64_t ev = ((uint64_t)((kx >> 6) & 0xFFFFFu) << 32) | mid;
         if (lane == ps) w.hfirst[base + ps + nf] = ev;
         if (lastev) w.hlast[base + ps + nl] = ev;
       }
@@ -1052,6 +1052,7 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     // right neighbour changed.
     const uint64_t gone = (~live + (wm << 1)) & live;
     if (win_) sym = mid;
+    if (lane_bit(gone)) kx = RANK_INF;
     live &= ~gone;
     const uint64_t lr = __brevll(live);
     const uint64_t prevw = __brevll((~lr + (__brevll(wm) << 1)) & lr);
@@ -2138,17 +2139,18 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 // ------------------------------------------------------ 4. compaction
 
 // One pass over the token slots: every block counts the ids in its
-// COMPACT_BLOCK slots (COMPACT_PER_THREAD consecutive slots per thread),
-// publishes the count, takes its offset from its predecessors' words
-// (decoupled look-back: the nearest predecessor that has published a running
-// total, plus the counts in between, 64 predecessors per step), publishes
-// its running total and writes its ids. A status word is tag << 32 |
-// CST_TOTAL (a running total, else a count) | value: words left by other
-// launches carry other tags and read as not yet published. A block waits
-// only for blocks dispatched before it, which publish their counts without
-// waiting, and every wait is bounded.
+// COMPACT_BLOCK slots (COMPACT_PER_THREAD consecutive slots per thread) and
+// stages them in LDS, publishes the count, takes its offset from its
+// predecessors' words (decoupled look-back: the nearest predecessor that has
+// published a running total, plus the counts in between, 1024 predecessors
+// per step), publishes its running total and stores its ids contiguously.
+// A status word is tag << 32 | CST_TOTAL (a running total, else a count) |
+// value: words left by other launches carry other tags and read as not yet
+// published. A block waits only for blocks dispatched before it, which
+// publish their counts without waiting, and every wait is bounded.
 constexpr uint32_t CST_TOTAL = 1u << 31;
 constexpr int COMPACT_SPIN = 1 << 20;
+constexpr int COMPACT_LOOK = 16;
 
 __device__ __forceinline__ void cst_store(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2160,6 +2162,7 @@ __device__ __forceinline__ uint64_t cst_load(const uint64_t* p) {
 __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk,
                                                          uint32_t tag) {
   __shared__ uint32_t sbase;
+  __shared__ uint32_t sout[COMPACT_BLOCK];  // the block's ids, in order
   const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
   const int64_t b = blockIdx.x;
   const int64_t p0 = b * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
@@ -2183,7 +2186,10 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
 #pragma unroll
   for (int k = 0; k < COMPACT_PER_THREAD; ++k) c += v[k] != INVALID_ID;
   uint32_t tot;
-  const uint32_t off = block_excl_scan(c, &tot);
+  uint32_t off = block_excl_scan(c, &tot);
+#pragma unroll
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k)
+    if (v[k] != INVALID_ID) sout[off++] = v[k];
   if (wv == 0) {
     const uint64_t hi = (uint64_t)tag << 32;
     uint32_t base = 0;
@@ -2192,23 +2198,36 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
       if (lane == 0) cst_store(&w.cstat[0], hi | CST_TOTAL | tot);
     } else {
       if (lane == 0) cst_store(&w.cstat[b], hi | tot);
-      for (int64_t j = b - 1;; j -= 64) {
-        const int64_t q = j - lane;
-        uint64_t st = hi | CST_TOTAL;  // before block 0: a total of zero
-        if (q >= 0) {
-          st = cst_load(&w.cstat[q]);
-          for (int spin = 0; (st >> 32) != tag && spin < COMPACT_SPIN; ++spin)
-            st = cst_load(&w.cstat[q]);
-          if ((st >> 32) != tag) {
+      // COMPACT_LOOK * 64 predecessors per step, nearest first: lane l of
+      // part k reads block j - 64k - l
+      for (int64_t j = b - 1;; j -= 64 * COMPACT_LOOK) {
+        uint64_t st[COMPACT_LOOK];
+#pragma unroll
+        for (int k = 0; k < COMPACT_LOOK; ++k) {
+          const int64_t q = j - 64 * k - lane;
+          st[k] = q >= 0 ? cst_load(&w.cstat[q]) : (hi | CST_TOTAL);
+        }
+#pragma unroll
+        for (int k = 0; k < COMPACT_LOOK; ++k) {
+          const int64_t q = j - 64 * k - lane;
+          for (int spin = 0; q >= 0 && (st[k] >> 32) != tag && spin < COMPACT_SPIN; ++spin)
+            st[k] = cst_load(&w.cstat[q]);
+          if ((st[k] >> 32) != tag) {  // only after the bounded wait
             ok = false;
-            st = hi | CST_TOTAL;
+            st[k] = hi | CST_TOTAL;
           }
         }
-        const uint64_t tm = __ballot(((uint32_t)st & CST_TOTAL) != 0);
-        const int l = tm ? __builtin_ctzll(tm) : 64;
-        const uint32_t val = lane <= l ? ((uint32_t)st & ~CST_TOTAL) : 0u;
-        base += (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(val, lane), 63);
-        if (tm) break;  // wave-uniform
+        bool done = false;
+#pragma unroll
+        for (int k = 0; k < COMPACT_LOOK; ++k) {
+          if (done) break;  // wave-uniform
+          const uint64_t tm = __ballot(((uint32_t)st[k] & CST_TOTAL) != 0);
+          const int l = tm ? __builtin_ctzll(tm) : 64;
+          const uint32_t val = lane <= l ? ((uint32_t)st[k] & ~CST_TOTAL) : 0u;
+          base += (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan(val, lane), 63);
+          done = tm != 0;
+        }
+        if (done) break;
       }
       if (lane == 0) cst_store(&w.cstat[b], hi | CST_TOTAL | (base + tot));
     }
@@ -2219,15 +2238,12 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
     }
   }
   __syncthreads();
-  uint32_t o = sbase + off;
-#pragma unroll
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k)
-    if (v[k] != INVALID_ID) {
-      if (o < w.out_cap) w.out[o] = v[k];
-      ++o;
-    }
+  // contiguous stores of the staged ids
+  const uint32_t base = sbase;
+  for (uint32_t j = tid; j < tot; j += COMPACT_TPB)
+    if (base + j < w.out_cap) w.out[base + j] = sout[j];
   if (b == nblk - 1 && tid == 0) {
-    const uint32_t total = sbase + tot;
+    const uint32_t total = base + tot;
     w.blkprefix[nblk] = total;
     w.status[1] = total;
     if (total > w.out_cap) atomicOr(w.status, ST_CAPACITY);
