@@ -670,8 +670,19 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
                        (v >= 0xD800 && v <= 0xDFFF);
       const uint32_t cp = bad ? 0xFFFDu : v;
       const uint32_t cl = cp < 256 ? lcls[cp] : t.cls[cp];
+      // a continuation byte is valid when the first byte back that is not
+      // one (at most three back, not before position 0) is a lead that
+      // announces at least that many continuation bytes
+      bool ok = !bad;
+      if (c0) {
+        const bool m3 = is_cont(sb[sj - 3]);
+        const int d = !m1 ? 1 : !m2 ? 2 : !m3 ? 3 : 4;
+        const uint32_t l = sb[sj - (d < 4 ? d : 3)];
+        const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2 : l >= 0xC0 ? 1 : 0;
+        ok = d <= pg && need >= d;
+      }
       e = cp | (cl << 21) | ((uint32_t)back << 23) | ((uint32_t)fwd << 25) |
-          (bad ? 0u : 1u << 27);
+          (ok ? 1u << 27 : 0u);
     }
     se[j] = e;
   }
@@ -706,22 +717,13 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     bool s = true;  // sentinel starts past the text
     if (i < nb) {
       const uint8_t b = (uint8_t)bb;
+      // the entry's valid bit: a lead that decodes, or a continuation byte
+      // that a lead claims
+      const uint32_t e = se[Li];
+      if (!((e >> 27) & 1)) st |= ST_UTF8;
       if (is_cont(b)) {
-        // a continuation byte must be claimed by a lead at most 3 back
-        int back = 1;
-        while (i - back >= 0 && back <= 3 && is_cont(sb[sj - back])) ++back;
-        bool ok = false;
-        if (i - back >= 0 && back <= 3) {
-          const uint8_t l = sb[sj - back];
-          const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2
-                         : l >= 0xC0 ? 1 : 0;
-          ok = need >= back;
-        }
-        if (!ok) st |= ST_UTF8;
         s = false;
       } else {
-        const uint32_t e = se[Li];
-        if (!((e >> 27) & 1)) st |= ST_UTF8;
         const bool d0 = ds(Li);
         uint32_t e1 = 0;
         if (d0) {
