@@ -63,6 +63,7 @@ struct DevTables {
   int32_t needs_nfc;
   int32_t cert;                // long pieces may be cut and certified:
                                // rank-ordered table, every byte has an id
+  int32_t all_bytes;           // every byte has an id (no dropped bytes)
   const uint32_t* unsafe;      // unsafe-rank bitmap or nullptr
   uint32_t unsafe_words;
   const uint64_t* ctab;        // compact pair table or nullptr
@@ -143,10 +144,18 @@ __host__ __device__ constexpr int pack_slot(int c) {
   return c <= 6 ? c + 2 : c == 7 ? 10 : c == 8 ? 12 : c == 9 ? 16
        : c == 10 ? 21 : c == 11 ? 32 : 64;
 }
+// Classes of up to PACK_LANE_MAX bytes are merged one piece per lane (64
+// pieces per work unit, each merged serially by its lane); longer ones one
+// piece per slot of pack_slot(c) lanes (64 / slot pieces per unit, merged by
+// the lanes together).
+constexpr int PACK_LANE_MAX = 16;
+__host__ __device__ constexpr bool pack_lane(int c) {
+  return pack_slot(c) <= PACK_LANE_MAX;
+}
 // pieces per work unit, and a multiplier m with (lane * m) >> 12 == lane /
 // pack_slot(c) for every lane < 64
 __host__ __device__ constexpr int pack_per_unit(int c) {
-  return 64 / pack_slot(c);
+  return pack_lane(c) ? 64 : 64 / pack_slot(c);
 }
 __host__ __device__ constexpr int pack_magic(int c) {
   return (4096 + pack_slot(c) - 1) / pack_slot(c);

@@ -1116,9 +1116,96 @@ __device__ __forceinline__ int64_t piece_end(const DevWork& w, int64_t a) {
   return seg_end_after(wd + 1, [&](int64_t x) { return w.starts[x]; });
 }
 
+// the pair's rule as (rank, product id): the compact table when the engine
+// built one, else the boundary table
+__device__ __forceinline__ bool pair_find(const DevTables& t, uint32_t l,
+                                          uint32_t r, uint32_t* rank,
+                                          uint32_t* id) {
+  if (t.ctab) return ctab_find(t, l, r, rank, id);
+  const uint64_t v = pair_lookup(t, l, r);
+  *rank = (uint32_t)(v >> 32);
+  *id = (uint32_t)v;
+  return v != ~0ULL;
+}
+
+// One piece of n <= L bytes per lane (n == 0: none), merged serially by its
+// lane in the HF order: the lowest-ranked pair, leftmost on ties, one merge
+// per step. Positions keep their byte offsets: a live mask per lane, the
+// rank of the pair each live position starts in registers (rk[i]), symbols
+// and pair products in LDS at [position][lane] (lsym, lmid: this wave's
+// L x 64 words each). Every byte has an id (the engine's all_bytes flag).
+template <int L>
+__device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
+                         uint32_t* lmid, int64_t a, int n) {
+  const int lane = threadIdx.x & 63;
+  uint32_t rk[L];
+  uint32_t live = n > 0 ? (1u << n) - 1 : 0u;  // n <= 16
+  bool done = n == 0;
+  if (!done && t.ignore_merges) {
+    // whole-piece vocabulary hit first (pretok_kernel.cu:921-943 role)
+    const int32_t hit = vocab_lookup(t, w.text + a, n);
+    if (hit >= 0) {
+      lsym[lane] = (uint32_t)hit;
+      live = 1u;
+      done = true;
+    }
+  }
+  {
+    uint32_t by[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) by[i] = i < n ? w.text[a + i] : 0u;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      rk[i] = RANK_INF;
+      if (!done && i < n) lsym[i * 64 + lane] = (uint32_t)t.byte_id[by[i]];
+      if (!done && i + 1 < n) {
+        const uint64_t v = t.bytepair[(by[i] << 8) | by[i + 1]];
+        if (v != ~0ULL) {
+          rk[i] = (uint32_t)(v >> 32);
+          lmid[i * 64 + lane] = (uint32_t)v;
+        }
+      }
+    }
+  }
+  for (;;) {
+    uint32_t best = RANK_INF;
+    int bi = 0;
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i)
+      if (rk[i] < best) {
+        best = rk[i];
+        bi = i;
+      }
+    if (best == RANK_INF) break;  // this lane's piece is finished
+    // bi absorbs the next live position nb; p and nn: its live neighbours
+    // after the merge
+    const uint32_t mid = lmid[bi * 64 + lane];
+    const int nb = __builtin_ctz(live & ~((2u << bi) - 1u));
+    const uint32_t after = live & ~((2u << nb) - 1u);
+    const uint32_t before = live & ((1u << bi) - 1u);
+    const int nn = after ? __builtin_ctz(after) : -1;
+    const int p = before ? 31 - __builtin_clz(before) : -1;
+    live &= ~(1u << nb);
+    lsym[bi * 64 + lane] = mid;
+    uint32_t rp = RANK_INF, mp = 0, rb = RANK_INF, mb = 0;
+    if (p >= 0 && !pair_find(t, lsym[p * 64 + lane], mid, &rp, &mp)) rp = RANK_INF;
+    if (nn >= 0 && !pair_find(t, mid, lsym[nn * 64 + lane], &rb, &mb)) rb = RANK_INF;
+    if (rp != RANK_INF) lmid[p * 64 + lane] = mp;
+    if (rb != RANK_INF) lmid[bi * 64 + lane] = mb;
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+      rk[i] = i == p ? rp : i == bi ? rb : i == nb ? RANK_INF : rk[i];
+  }
+#pragma unroll
+  for (int i = 0; i < L; ++i)
+    if (i < n)
+      w.tok[a + i] = ((live >> i) & 1) ? (lsym[i * 64 + lane] & SYM_ID) : INVALID_ID;
+}
+
+constexpr uint32_t PACK_GEO_LANE = 1u << 31;  // one piece per lane
 constexpr uint32_t pack_geo(int c) {
   return (uint32_t)pack_slot(c) | (uint32_t)pack_per_unit(c) << 8 |
-         (uint32_t)pack_magic(c) << 16;
+         (uint32_t)pack_magic(c) << 16 | (pack_lane(c) ? PACK_GEO_LANE : 0u);
 }
 __constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
     pack_geo(0), pack_geo(1), pack_geo(2), pack_geo(3), pack_geo(4),
@@ -1128,37 +1215,61 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 
 // Work units in order, the longest class first (class c owns units
 // [uend[c + 1], uend[c])); wave g takes units g, g + G, g + 2G, ... (G waves
-// in the grid), so every wave gets a share of each class.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
+// in the grid), so every wave gets a share of each class. Classes of up to
+// PACK_LANE_MAX bytes: 64 pieces per unit, one per lane (lane_bpe); longer
+// ones: 64 / slot pieces per unit, a slot of lanes each (wave_bpe).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
-  const int lane = threadIdx.x & 63;
-  // lane q < PACK_CLASSES holds class q's unit end, piece count and slot
-  // geometry (slot | pieces per unit << 8 | pack_magic << 16); lane
-  // PACK_CLASSES holds a zero unit end
+  __shared__ uint32_t lds[4][2][PACK_LANE_MAX * 64];
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  // lane q < PACK_CLASSES holds class q's unit end, piece count and
+  // geometry (slot | pieces per unit << 8 | pack_magic << 16 | lane flag);
+  // lane PACK_CLASSES holds a zero unit end
   const bool cl = lane < PACK_CLASSES;
   const uint32_t ue_l = cl ? w.uend[lane] : 0u;
   const uint32_t pc_l = cl ? w.pcount[lane] : 0u;
   const uint32_t geo_l = cl ? PACK_GEO[lane] : 0u;
   const uint32_t total = __builtin_amdgcn_readfirstlane(ue_l);
   const uint32_t G = gridDim.x * 4;
-  for (uint32_t u0 = blockIdx.x * 4 + wave_id(); u0 < total; u0 += G) {
+  for (uint32_t u0 = blockIdx.x * 4 + wv; u0 < total; u0 += G) {
     // the unit's class: the last class whose unit end lies past u0
     const uint64_t inq = __ballot(cl && u0 < ue_l);
     const int c = 63 - __builtin_clzll(inq);
     const uint32_t geo = __builtin_amdgcn_readlane(geo_l, c);
     const uint32_t ubeg = __builtin_amdgcn_readlane(ue_l, c + 1);
     const uint32_t cnt = __builtin_amdgcn_readlane(pc_l, c);
-    const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = geo >> 16;
-    const int slot = (lane * mg) >> 12, off = lane - slot * sl;
-    const uint32_t idx = (u0 - ubeg) * k + slot;
-    int64_t a = 0, L = 0;
-    if (slot < k && idx < cnt) {
-      a = w.plist[w.poff[c] + idx];
-      L = piece_end(w, a) - a;
+    const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
+    const uint32_t first = (u0 - ubeg) * k;  // the unit's first piece
+    if ((geo & PACK_GEO_LANE) && t.all_bytes) {  // wave-uniform
+      const uint32_t idx = first + lane;
+      int64_t a = 0;
+      int n = 0;
+      if (idx < cnt) {
+        a = w.plist[w.poff[c] + idx];
+        n = (int)(piece_end(w, a) - a);
+      }
+      uint32_t* ls = lds[wv][0];
+      uint32_t* lm = lds[wv][1];
+      if (sl <= 4) lane_bpe<4>(t, w, ls, lm, a, n);
+      else if (sl <= 8) lane_bpe<8>(t, w, ls, lm, a, n);
+      else lane_bpe<16>(t, w, ls, lm, a, n);
+      continue;
     }
-    const bool elig = off < L;
-    const int ps = elig ? slot * sl : lane, pe = elig ? slot * sl + (int)L : lane + 1;
-    wave_bpe<true, false, true>(t, w, 0, a + off, lane, elig, ps, pe);
+    // slot-packed: 64 / slot pieces at a time (a lane-class unit without
+    // the lane path takes several passes)
+    const int per = 64 / sl;
+    const int slot = (lane * mg) >> 12, off = lane - slot * sl;
+    for (int j0 = 0; j0 < k; j0 += per) {
+      const uint32_t idx = first + j0 + slot;
+      int64_t a = 0, L = 0;
+      if (slot < per && j0 + slot < k && idx < cnt) {
+        a = w.plist[w.poff[c] + idx];
+        L = piece_end(w, a) - a;
+      }
+      const bool elig = off < L;
+      const int ps = elig ? slot * sl : lane, pe = elig ? slot * sl + (int)L : lane + 1;
+      wave_bpe<true, false, true>(t, w, 0, a + off, lane, elig, ps, pe);
+    }
   }
 }
 

@@ -692,6 +692,9 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   for (size_t i = 0; i < unsafe_len / 4; ++i) cert = cert && unsafe_bits[i] == 0;
   for (int b = 0; b < 256; ++b) cert = cert && byte_id[b] >= 0;
   e->t.cert = cert ? 1 : 0;
+  bool all_bytes = true;
+  for (int b = 0; b < 256; ++b) all_bytes = all_bytes && byte_id[b] >= 0;
+  e->t.all_bytes = all_bytes ? 1 : 0;
   e->t.ctab = nullptr;
   {
     // with the compact table every symbol the packed merge looks up (a
