@@ -1131,14 +1131,14 @@ __device__ __forceinline__ bool pair_find(const DevTables& t, uint32_t l,
 // One piece of n <= L bytes per lane (n == 0: none), merged serially by its
 // lane in the HF order: the lowest-ranked pair, leftmost on ties, one merge
 // per step. Positions keep their byte offsets: a live mask per lane, the
-// rank of the pair each live position starts in registers (rk[i]), symbols
-// and pair products in LDS at [position][lane] (lsym, lmid: this wave's
-// L x 64 words each). Every byte has an id (the engine's all_bytes flag).
+// rank and product of the pair each live position starts in registers (rk,
+// md), the symbols in LDS at [position][lane] (lsym: this wave's L x 64
+// words). Every byte has an id (the engine's all_bytes flag).
 template <int L>
 __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
-                         uint32_t* lmid, int64_t a, int n) {
+                         int64_t a, int n) {
   const int lane = threadIdx.x & 63;
-  uint32_t rk[L];
+  uint32_t rk[L], md[L];
   uint32_t live = n > 0 ? (1u << n) - 1 : 0u;  // n <= 16
   bool done = n == 0;
   if (!done && t.ignore_merges) {
@@ -1157,29 +1157,30 @@ __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       rk[i] = RANK_INF;
+      md[i] = 0;
       if (!done && i < n) lsym[i * 64 + lane] = (uint32_t)t.byte_id[by[i]];
       if (!done && i + 1 < n) {
         const uint64_t v = t.bytepair[(by[i] << 8) | by[i + 1]];
         if (v != ~0ULL) {
           rk[i] = (uint32_t)(v >> 32);
-          lmid[i * 64 + lane] = (uint32_t)v;
+          md[i] = (uint32_t)v;
         }
       }
     }
   }
   for (;;) {
-    uint32_t best = RANK_INF;
+    uint32_t best = RANK_INF, mid = 0;
     int bi = 0;
 #pragma unroll
     for (int i = 0; i < L - 1; ++i)
       if (rk[i] < best) {
         best = rk[i];
+        mid = md[i];
         bi = i;
       }
     if (best == RANK_INF) break;  // this lane's piece is finished
     // bi absorbs the next live position nb; p and nn: its live neighbours
     // after the merge
-    const uint32_t mid = lmid[bi * 64 + lane];
     const int nb = __builtin_ctz(live & ~((2u << bi) - 1u));
     const uint32_t after = live & ~((2u << nb) - 1u);
     const uint32_t before = live & ((1u << bi) - 1u);
@@ -1190,11 +1191,11 @@ __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
     uint32_t rp = RANK_INF, mp = 0, rb = RANK_INF, mb = 0;
     if (p >= 0 && !pair_find(t, lsym[p * 64 + lane], mid, &rp, &mp)) rp = RANK_INF;
     if (nn >= 0 && !pair_find(t, mid, lsym[nn * 64 + lane], &rb, &mb)) rb = RANK_INF;
-    if (rp != RANK_INF) lmid[p * 64 + lane] = mp;
-    if (rb != RANK_INF) lmid[bi * 64 + lane] = mb;
 #pragma unroll
-    for (int i = 0; i < L; ++i)
+    for (int i = 0; i < L; ++i) {
       rk[i] = i == p ? rp : i == bi ? rb : i == nb ? RANK_INF : rk[i];
+      md[i] = i == p ? mp : i == bi ? mb : md[i];
+    }
   }
 #pragma unroll
   for (int i = 0; i < L; ++i)
@@ -1218,9 +1219,9 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 // in the grid), so every wave gets a share of each class. Classes of up to
 // PACK_LANE_MAX bytes: 64 pieces per unit, one per lane (lane_bpe); longer
 // ones: 64 / slot pieces per unit, a slot of lanes each (wave_bpe).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
-  __shared__ uint32_t lds[4][2][PACK_LANE_MAX * 64];
+  __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
   const int lane = threadIdx.x & 63, wv = wave_id();
   // lane q < PACK_CLASSES holds class q's unit end, piece count and
   // geometry (slot | pieces per unit << 8 | pack_magic << 16 | lane flag);
@@ -1248,11 +1249,10 @@ void k_bpe_pack(DevTables t, DevWork w) {
         a = w.plist[w.poff[c] + idx];
         n = (int)(piece_end(w, a) - a);
       }
-      uint32_t* ls = lds[wv][0];
-      uint32_t* lm = lds[wv][1];
-      if (sl <= 4) lane_bpe<4>(t, w, ls, lm, a, n);
-      else if (sl <= 8) lane_bpe<8>(t, w, ls, lm, a, n);
-      else lane_bpe<16>(t, w, ls, lm, a, n);
+      uint32_t* ls = lds[wv];
+      if (sl <= 4) lane_bpe<4>(t, w, ls, a, n);
+      else if (sl <= 8) lane_bpe<8>(t, w, ls, a, n);
+      else lane_bpe<16>(t, w, ls, a, n);
       continue;
     }
     // slot-packed: 64 / slot pieces at a time (a lane-class unit without
