@@ -714,122 +714,119 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
     const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
     const uint64_t mHI = __ballot(bb >= 0x80);
-    bool s = true;  // sentinel starts past the text
-    if (i < nb) {
-      const uint8_t b = (uint8_t)bb;
-      // the entry's valid bit: a lead that decodes, or a continuation byte
-      // that a lead claims
-      const uint32_t e = se[Li];
-      if (!((e >> 27) & 1)) st |= ST_UTF8;
-      if (is_cont(b)) {
-        s = false;
-      } else {
-        const bool d0 = ds(Li);
-        uint32_t e1 = 0;
-        if (d0) {
-          s = true;
-        } else {
-          // the fixed context: every offset used lies in the LDS span (tile
-          // positions are at least PT_HALO from either end, and the four
-          // characters back cover at most 16 bytes); the one after is
-          // checked
-          Ctx5 x;
-          x.c0 = e;
-          const int L1 = prv(Li);
-          x.c1 = e1 = se[L1];
-          x.h2 = !ds(L1);
-          const int L2 = x.h2 ? prv(L1) : L1;
-          x.c2 = se[L2];
-          x.h3 = x.h2 && !ds(L2);
-          const int L3 = x.h3 ? prv(L2) : L2;
-          x.c3 = se[L3];
-          x.h4 = x.h3 && !ds(L3);
-          const int L4 = x.h4 ? prv(L3) : L3;
-          x.c4 = se[L4];
-          const int Ln = Li + 1 + (int)((e >> 25) & 3);
-          const bool nin = Ln < PT_SPAN;
-          x.hn = lo + Ln < nb && !ds(Ln);
-          x.cn = nin ? se[Ln] : 0u;
-          int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
-          const uint64_t below = (1ULL << lane) - 1;
-          if (r == FAST_DIGITS && !DM) {
-            // the ASCII digits before i, when the word shows where they begin
-            const uint64_t nd_ = ~mDG & below;
-            if (nd_ && !((mHI >> (63 - __builtin_clzll(nd_))) & 1))
-              r = (lane - 1 - (63 - __builtin_clzll(nd_))) % t.dmax == 0;
-          } else if (r == FAST_CRLF && !DM && bb < 0x80) {
-            // another CR/LF ahead in the run: it shows in the word before
-            // the first byte that is neither (unless that byte is not ASCII)
-            const uint64_t above = ~mask_le(lane);
-            const uint64_t stop = ~(mWS | mCR) & above;
-            const int f = stop ? __builtin_ctzll(stop) : 64;
-            const int g = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
-            if (g < f) {
-              // then the char before the CR/LF run that precedes i
-              const uint64_t nc = ~mCR & below;
-              if (nc) {
-                const int h = 63 - __builtin_clzll(nc);
-                if ((mWS >> h) & 1) r = 0;
-                else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
-              }
-            } else if (f < 64 && !((mHI >> f) & 1)) {
-              r = 1;
+    // Every lane evaluates the fast predicate from the fixed context (only
+    // selects); the lanes it leaves open (runs to walk, the general path)
+    // are resolved in a section the wave enters only when it has any.
+    const bool in = i < nb;
+    const bool lead = in && !is_cont((uint8_t)bb);
+    // the entry's valid bit: a lead that decodes, or a continuation byte
+    // that a lead claims
+    const uint32_t e = se[Li];
+    if (in && !((e >> 27) & 1)) st |= ST_UTF8;
+    const bool d0 = ds(Li);
+    // the fixed context: every offset used lies in the LDS span (tile
+    // positions are at least PT_HALO from either end, and the four
+    // characters back cover at most 16 bytes); the one after is checked
+    Ctx5 x;
+    x.c0 = e;
+    const int L1 = prv(Li);
+    x.c1 = se[L1];
+    x.h2 = !ds(L1);
+    const int L2 = x.h2 ? prv(L1) : L1;
+    x.c2 = se[L2];
+    x.h3 = x.h2 && !ds(L2);
+    const int L3 = x.h3 ? prv(L2) : L2;
+    x.c3 = se[L3];
+    x.h4 = x.h3 && !ds(L3);
+    const int L4 = x.h4 ? prv(L3) : L3;
+    x.c4 = se[L4];
+    const int Ln = Li + 1 + (int)((e >> 25) & 3);
+    const bool nin = Ln < PT_SPAN;
+    x.hn = lo + Ln < nb && !ds(Ln);
+    x.cn = nin ? se[Ln] : 0u;
+    int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
+    const bool open = lead && !d0 && r < 0;
+    if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
+      if (open) {
+        const uint64_t below = (1ULL << lane) - 1;
+        if (r == FAST_DIGITS && !DM) {
+          // the ASCII digits before i, when the word shows where they begin
+          const uint64_t nd_ = ~mDG & below;
+          if (nd_ && !((mHI >> (63 - __builtin_clzll(nd_))) & 1))
+            r = (lane - 1 - (63 - __builtin_clzll(nd_))) % t.dmax == 0;
+        } else if (r == FAST_CRLF && !DM && bb < 0x80) {
+          // another CR/LF ahead in the run: it shows in the word before
+          // the first byte that is neither (unless that byte is not ASCII)
+          const uint64_t above = ~mask_le(lane);
+          const uint64_t stop = ~(mWS | mCR) & above;
+          const int f = stop ? __builtin_ctzll(stop) : 64;
+          const int g = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
+          if (g < f) {
+            // then the char before the CR/LF run that precedes i
+            const uint64_t nc = ~mCR & below;
+            if (nc) {
+              const int h = 63 - __builtin_clzll(nc);
+              if ((mWS >> h) & 1) r = 0;
+              else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
             }
+          } else if (f < 64 && !((mHI >> f) & 1)) {
+            r = 1;
           }
-          if (r == FAST_DIGITS) {
-            // \p{N}{1,K}: count the digits before i inside the span
-            int L = L3, nd = 3;
-            r = -1;
-            for (;;) {
-              if (ds(L)) { r = nd % t.dmax == 0; break; }
-              if (L - 1 < 0) break;  // past the span: general path
+        }
+        if (r == FAST_DIGITS) {
+          // \p{N}{1,K}: count the digits before i inside the span
+          int L = L3, nd = 3;
+          r = -1;
+          for (;;) {
+            if (ds(L)) { r = nd % t.dmax == 0; break; }
+            if (L - 1 < 0) break;  // past the span: general path
+            const int Lr = prv(L);
+            if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
+            ++nd;
+            L = Lr;
+          }
+        } else if (r == FAST_CRLF) {
+          // end of \s*[\r\n]+ unless another CR/LF follows in the run;
+          // then the first char the P match's [\r\n]* left over
+          r = -1;
+          bool more = false, known = false;
+          for (int L = Ln;;) {
+            if (lo + L >= nb || ds(L)) { known = true; break; }
+            if (L >= PT_SPAN) break;
+            const uint32_t eq = se[L];
+            if (ecl(eq) != CS_) { known = true; break; }
+            if (crlf(ecp(eq))) { more = known = true; break; }
+            L += 1 + (int)((eq >> 25) & 3);
+          }
+          if (known && !more) r = 1;
+          if (known && more) {
+            for (int L = L1;;) {
+              if (ds(L)) { r = 0; break; }
+              if (L - 1 < 0) break;
               const int Lr = prv(L);
-              if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
-              ++nd;
+              const uint32_t ex = se[Lr];
+              if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
+              if (!crlf(ecp(ex))) { r = 0; break; }
               L = Lr;
             }
-          } else if (r == FAST_CRLF) {
-            // end of \s*[\r\n]+ unless another CR/LF follows in the run;
-            // then the first char the P match's [\r\n]* left over
-            r = -1;
-            bool more = false, known = false;
-            for (int L = Ln;;) {
-              if (lo + L >= nb || ds(L)) { known = true; break; }
-              if (L >= PT_SPAN) break;
-              const uint32_t eq = se[L];
-              if (ecl(eq) != CS_) { known = true; break; }
-              if (crlf(ecp(eq))) { more = known = true; break; }
-              L += 1 + (int)((eq >> 25) & 3);
-            }
-            if (known && !more) r = 1;
-            if (known && more) {
-              for (int L = L1;;) {
-                if (ds(L)) { r = 0; break; }
-                if (L - 1 < 0) break;
-                const int Lr = prv(L);
-                const uint32_t ex = se[Lr];
-                if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
-                if (!crlf(ecp(ex))) { r = 0; break; }
-                L = Lr;
-              }
-            }
-          }
-          if (r < 0) {
-            const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
-            r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
-          }
-          s = r != 0;
-        }
-        if (w.check_nfc) {
-          const uint32_t cp = e & 0x1FFFFF;
-          const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
-          if (v == 255) {
-            st |= ST_NFC;
-          } else if (v != 0 && !d0) {
-            const uint32_t pc = e1 & 0x1FFFFF;
-            if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
           }
         }
+        if (r < 0) {
+          const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+          r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
+        }
+      }
+    }
+    // sentinel starts past the text; no start inside a character
+    const bool s = !in || (lead && (d0 || r != 0));
+    if (w.check_nfc && lead) {
+      const uint32_t cp = e & 0x1FFFFF;
+      const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
+      if (v == 255) {
+        st |= ST_NFC;
+      } else if (v != 0 && !d0) {
+        const uint32_t pc = x.c1 & 0x1FFFFF;
+        if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
       }
     }
     const uint64_t m = __ballot(s);
