@@ -566,13 +566,13 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total)
 
 // ------------------------------------------------------ 1. pretokenize
 
-// One block per PT_TILE bytes (64 start words). Stage the bytes, decode
+// One block per PT_TILE bytes (PT_TILE / 64 start words). Stage the bytes, decode
 // every position of the tile and its halo into LDS entries, then each wave
 // takes one 64-byte word at a time, lane = byte, and ballots the start bits
 // into the word. Positions inside the block are 32-bit offsets from lo (the
 // first entry); RS is the ruleset, DM whether document starts are marked.
 template <int RS, bool DM>
-__global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
+__global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pretok(DevTables t, DevWork w,
                                                        int64_t nwords) {
   __shared__ __align__(16) uint8_t sb[PT_BYTES];
   __shared__ uint32_t se[PT_SPAN];
@@ -615,17 +615,21 @@ __global__ __launch_bounds__(PRETOK_TPB) void k_pretok(DevTables t, DevWork w,
     *reinterpret_cast<uint4*>(sb + 16 * j) = v;
   }
   // Clear what the later stages of this call accumulate into: the block's
-  // 64 words of the long-piece masks, its word of repair bits, and (block
-  // 0) the control slot of the next call; the last block takes the tails.
+  // words of the long-piece masks, the words of repair bits whose first
+  // covered word is one of the block's (a repair word covers 64 words), and
+  // (block 0) the control slot of the next call; the last block takes the
+  // tails.
   {
-    const int64_t wd0 = (base >> 6), dw0 = blockIdx.x;
+    constexpr int64_t TW = PT_TILE / 64;
+    const int64_t wd0 = (base >> 6);
+    const int64_t dw0 = (wd0 + 63) / 64, dw1 = (wd0 + TW + 63) / 64;
     const bool last = blockIdx.x == gridDim.x - 1;
-    for (int64_t j = wd0 + tid; j < w.clear_words && (j < wd0 + 64 || last);
+    for (int64_t j = wd0 + tid; j < w.clear_words && (j < wd0 + TW || last);
          j += PRETOK_TPB) {
       w.inlong[j] = 0;
       w.failm[j] = 0;
     }
-    for (int64_t j = dw0 + tid; j < w.clear_dwords && (j == dw0 || last);
+    for (int64_t j = dw0 + tid; j < w.clear_dwords && (j < dw1 || last);
          j += PRETOK_TPB)
       w.dirty_next[j] = 0;
     if (blockIdx.x == 0 && tid < CTRL_WORDS) w.ctrl_next[tid] = 0;
