@@ -59,7 +59,8 @@ def pct(xs, q):
 def measured_traffic(config: int, kernel: str):
     """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, scaled by
     a plain copy's reading) from the committed rocprofv3 summary, when that
-    summary was taken on this very library build; else None."""
+    summary was taken on a library built from these very sources, flags and
+    compiler (the manifest's build key); else None."""
     try:
         with open(os.path.join(ROOT, "profiles", f"c{config}_traffic.json")) as f:
             d = json.load(f)
@@ -67,7 +68,7 @@ def measured_traffic(config: int, kernel: str):
             m = json.load(f)
     except (OSError, ValueError):
         return None
-    if d.get("library_sha256") != m.get("sha256") or d.get("kernel") != kernel:
+    if d.get("build_key") != m.get("build_key") or d.get("kernel") != kernel:
         return None
     return int(d["fetch_bytes"] + d["write_bytes"])
 
@@ -192,7 +193,11 @@ def main() -> int:
     n_tok = float(np.mean([a.size for a in ids_dev]))
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
     st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["pretokenize + piece lists (k_pretok, k_long_prep, k_pack_scan, k_pack_scatter)", "k_bpe_pack", "long pieces past k_bpe_pack (k_bpe_wide, k_long_*, k_certify; side stream)", "compaction (k_count, k_scan, k_compact)"]
+    names = ["pretokenize + piece lists (k_pretok, k_lists, k_pack_copy)",
+             "k_bpe_pack",
+             "long pieces past k_bpe_pack (k_bpe_rows, k_bpe_wide, k_long_*, "
+             "k_certify; side stream)",
+             "compaction (k_compact)"]
     avg = st[:, :4].mean(axis=0)
     pack_avg_us = float(np.mean(pack_us))
     b_alg = n_bytes + 4.0 * n_tok

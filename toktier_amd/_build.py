@@ -49,6 +49,17 @@ def exported_symbols(lib: Path) -> list[str]:
                    if line.split() and line.split()[-1].startswith("tk_")})
 
 
+def build_key(sources: dict, flags: list, hipcc: list) -> str:
+    """Digest of what determines the code object: the sources, the flags
+    and the compiler version. hipcc gives each compile a random unit id,
+    so two builds of the same sources differ in a few bytes of the library
+    and its own sha256 cannot name a build across rebuilds; this key can
+    (the committed counter summaries are matched on it)."""
+    body = json.dumps({"sources": sources, "flags": flags, "hipcc": hipcc,
+                       "arch": ARCH}, sort_keys=True)
+    return hashlib.sha256(b"toktier-hip-build\0" + body.encode()).hexdigest()
+
+
 def build(verbose: bool = False) -> Path:
     LIBDIR.mkdir(exist_ok=True)
     tmp = LIB.with_suffix(f".so.tmp{os.getpid()}")
@@ -64,15 +75,17 @@ def build(verbose: bool = False) -> Path:
     ver = subprocess.run([_hipcc(), "--version"], capture_output=True,
                          text=True).stdout.strip().splitlines()
     digest = hashlib.sha256(b"toktier-hip-lib\0" + LIB.read_bytes()).hexdigest()
+    sources = {s: hashlib.sha256((CSRC / s).read_bytes()).hexdigest()
+               for s in SOURCES}
     MANIFEST.write_text(json.dumps({
         "library": LIB.name,
         "sha256_domain": "toktier-hip-lib",
         "sha256": digest,
+        "build_key": build_key(sources, HIPCC_FLAGS, ver[:2]),
         "architecture": ARCH,
         "hipcc": ver[:2],
         "flags": HIPCC_FLAGS,
-        "sources": {s: hashlib.sha256((CSRC / s).read_bytes()).hexdigest()
-                    for s in SOURCES},
+        "sources": sources,
         "symbols": exported_symbols(LIB),
     }, indent=1) + "\n")
     return LIB
