@@ -79,6 +79,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, choices=[2, 4, 5])
+    ap.add_argument("--chat", action="store_true",
+                    help="lay the config's text out as chat turns in the "
+                         "family's template (added-token literals, split "
+                         "out on the device)")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true",
@@ -109,6 +113,8 @@ def main() -> int:
     from toktier_amd import workloads
 
     fam, gen = workloads.CONFIGS[args.config]
+    if args.chat:
+        gen = lambda js, n_chars: workloads.chat(js, fam, n_chars=n_chars)  # noqa: E731
     tok = toktier_amd.load(fam)
     eng = tok.engine
     n_chars = workloads.CHARS_4M
@@ -184,6 +190,8 @@ def main() -> int:
         f = tok.family
         orc = Oracle(tok.tables, classes.class_table(), classes.nfc_qc_table(),
                      f.ruleset, f.digits_max, f.needs_nfc)
+        orc.set_added([t.content.encode() for t in tok.added_tokens],
+                      [t.id for t in tok.added_tokens])
         for i in range(K):
             want = orc.encode_bytes(reqs[i])
             if isinstance(want, int) or not np.array_equal(want, ids_dev[i]):
@@ -210,6 +218,8 @@ def main() -> int:
         f = tok.family
         orc = Oracle(tok.tables, classes.class_table(), classes.nfc_qc_table(),
                      f.ruleset, f.digits_max, f.needs_nfc)
+        orc.set_added([t.content.encode() for t in tok.added_tokens],
+                      [t.id for t in tok.added_tokens])
         t1 = time.perf_counter()
         done = 0
         chars = 0
@@ -240,8 +250,10 @@ def main() -> int:
         "data": "synthetic: seeded Zipf token-concat generator over the "
                 "stand-in vocabulary of the family",
         "config": {
-            "workload": f"C{args.config}: {fam}, one fresh request of "
-                        f"{n_chars:,} chars, bytes resident in HBM",
+            "workload": f"C{args.config}{' chat' if args.chat else ''}: "
+                        f"{fam}, one fresh request of {n_chars:,} chars"
+                        f"{' in chat turns (added-token literals)' if args.chat else ''}"
+                        ", bytes resident in HBM",
             "family": fam, "chars": n_chars, "bytes": int(n_bytes),
             "tokens": int(n_tok), "requests": K,
         },
@@ -263,7 +275,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": measured_traffic(args.config, "k_bpe_pack"),
+            "traffic": (None if args.chat else
+                        measured_traffic(args.config, "k_bpe_pack")),
             "alg_bytes_per_launch": int(b_alg),
             "path_achieved": round(b_alg / (ms_per_step * 1e-3) / 1e9, 3),
         },

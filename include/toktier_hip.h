@@ -15,6 +15,15 @@
  *                           (runtime.rs:76-82; gpu.rs:1446-1461, :500-600)
  *   tk_engine_encode_batch <- NativeGpuEngine::encode_batch_ids
  *                           (gpu.rs:1463-1546, Executor::encode_batch :605-750)
+ *   tk_engine_set_added  <- AddedTokenFrontend construction and the
+ *                           router's added-token check ahead of the GPU
+ *                           (src/toktier/frontend/added.py:316-375, scan
+ *                           :503-533, assemble :544-555;
+ *                           runtime.rs:527-536, :641-662): the literals are
+ *                           extracted on the device instead of routing
+ *                           the whole input to the CPU reference
+ *   tk_engine_last_literals <- the R_INPUT_ADDED_TOKEN ledger fact
+ *                           (runtime.rs:648-654), as a count
  *   tk_engine_delivery   <- NativeGpuEngine::delivery (runtime.rs:81)
  *   tk_engine_close      <- Drop of the engine / CUDA driver RAII
  *                           (crates/toktier-cuda-driver/src/lib.rs:424-457)
@@ -58,9 +67,20 @@ extern "C" {
 #define TK_E_NEEDS_NFC (-6)   /* NFC quick check failed: normalize, retry */
 #define TK_E_CAPACITY (-7)    /* caller's id buffer too small / input too big */
 #define TK_E_INTERNAL (-8)
+#define TK_E_UNSUPPORTED (-9) /* an added-token table this engine refuses */
 
 /* tk_engine_encode flags */
 #define TK_FLAG_NORMALIZED 1u /* caller already applied the family's NFC */
+#define TK_FLAG_NO_ADDED 2u   /* do not extract added-token literals: the
+                                 caller already split them out (the text is
+                                 one segment between literals) */
+
+/* added-token flags (tokenizer.json "added_tokens" fields) */
+#define TK_ADDED_SPECIAL 1u
+#define TK_ADDED_SINGLE_WORD 2u
+#define TK_ADDED_LSTRIP 4u
+#define TK_ADDED_RSTRIP 8u
+#define TK_ADDED_NORMALIZED 16u
 
 typedef struct tk_engine tk_engine;
 
@@ -130,6 +150,24 @@ int tk_engine_encode_batch(tk_engine* engine, const uint8_t* joined,
 int tk_engine_encode_device(tk_engine* engine, const void* d_text,
                             size_t nbytes, uint32_t flags, void* d_ids,
                             size_t ids_cap, size_t* n_ids, void* stream);
+
+/* Added tokens of the artifact (tokenizer.json "added_tokens", in artifact
+ * order): literal k is contents[offsets[k] .. offsets[k+1]) (UTF-8, 1..255
+ * bytes, all distinct), its id ids[k], its flags flags[k] (TK_ADDED_*).
+ * Every later encode (unless TK_FLAG_NO_ADDED) first splits the text at
+ * the literals the way HF tokenizers 0.22.2 does (leftmost match, the
+ * longest at that position, scanning on after it), emits each literal's
+ * id, and encodes the text between literals segment by segment (each
+ * segment is pretokenized as a document of its own). n == 0 removes the
+ * table. TK_E_UNSUPPORTED: a literal with single_word / lstrip / rstrip,
+ * a normalized literal when the family normalizes (NFC), or normalized and
+ * raw literals that can overlap (HF extracts them in two passes). */
+int tk_engine_set_added(tk_engine* engine, size_t n, const uint8_t* contents,
+                        const uint64_t* offsets, const uint32_t* ids,
+                        const uint8_t* flags);
+
+/* Literals extracted by the last encode on this engine. */
+int tk_engine_last_literals(const tk_engine* engine, uint64_t* n);
 
 const char* tk_engine_delivery(const tk_engine* engine);     /* "prebuilt" */
 const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */

@@ -52,10 +52,18 @@ def lib() -> C.CDLL:
         L.tko_nfc_qc.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         L.tko_encode.restype = C.c_int64
         L.tko_encode.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64]
+        L.tko_encode_added.restype = C.c_int64
+        L.tko_encode_added.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int64, C.c_void_p, C.c_int64]
         L.tko_utf8_decode.restype = C.c_int64
         L.tko_utf8_decode.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]
         _lib = L
     return _lib
+
+
+class _Added(C.Structure):
+    _fields_ = [("blob", C.c_void_p), ("offsets", C.c_void_p),
+                ("ids", C.c_void_p), ("n", C.c_int64)]
 
 
 class Oracle:
@@ -77,6 +85,20 @@ class Oracle:
             nfc_qc.ctypes.data if nfc_qc is not None else None,
             ruleset, digits_max, int(tables.ignore_merges), int(needs_nfc))
         self._lib = lib()
+        self._added = None
+
+    def set_added(self, contents: list[bytes], ids: list[int]) -> None:
+        """Added-token literals split out before encoding (no flags)."""
+        if not contents:
+            self._added = None
+            return
+        blob = np.frombuffer(b"".join(contents), dtype=np.uint8).copy()
+        offs = np.zeros(len(contents) + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum([len(c) for c in contents], dtype=np.uint64)
+        idv = np.asarray(ids, dtype=np.uint32)
+        self._added_keep = (blob, offs, idv)
+        self._added = _Added(blob.ctypes.data, offs.ctypes.data,
+                             idv.ctypes.data, len(contents))
 
     def pretokenize(self, data: bytes) -> list[int]:
         """Piece start byte offsets, followed by len(data)."""
@@ -98,18 +120,26 @@ class Oracle:
             raise ValueError("invalid UTF-8")
         return bool(r)
 
-    def encode_bytes(self, data: bytes, normalized: bool = False
-                     ) -> np.ndarray | int:
+    def encode_bytes(self, data: bytes, normalized: bool = False,
+                     literals: bool = True) -> np.ndarray | int:
         """ids as uint32, or a negative status (E_NEEDS_NFC, E_UTF8).
         ``normalized``: the text already went through the family's NFC, so
-        the quick check is skipped (the engine's TK_FLAG_NORMALIZED)."""
+        the quick check is skipped (the engine's TK_FLAG_NORMALIZED).
+        ``literals``: split out the added-token literals set by
+        ``set_added`` (off: the text is one segment between literals, the
+        engine's TK_FLAG_NO_ADDED)."""
         out = np.zeros(max(1, len(data)), dtype=np.uint32)
         t = self._t
         if normalized and t.needs_nfc:
             t = _Tables.from_buffer_copy(self._t)
             t.needs_nfc = 0
-        n = self._lib.tko_encode(C.byref(t), data, len(data),
-                                 out.ctypes.data, out.size)
+        if self._added is not None and literals:
+            n = self._lib.tko_encode_added(C.byref(t), C.byref(self._added),
+                                           data, len(data), out.ctypes.data,
+                                           out.size)
+        else:
+            n = self._lib.tko_encode(C.byref(t), data, len(data),
+                                     out.ctypes.data, out.size)
         if n < 0:
             return int(n)
         return out[:n]

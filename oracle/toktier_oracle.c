@@ -382,3 +382,52 @@ int64_t tko_encode(const tko_tables* t, const uint8_t* s, int64_t nb,
   free(starts);
   return total;
 }
+
+/* ------------------------------------------------- added-token split */
+
+/* HF tokenizers 0.22.2 splits the text at its added-token literals before
+ * normalization and pretokenization (the added vocabulary's Aho-Corasick
+ * search in leftmost-longest mode; the reference calls the same split,
+ * src/toktier/frontend/added.py:490-533, and joins the parts,
+ * :544-555): scanning left to right, the first position where a literal
+ * matches takes the longest literal matching there, and the scan resumes
+ * after it. Each literal is its own id; the text between two literals is
+ * encoded as a text of its own (its own quick check, pretokenization and
+ * merges). Literals here carry no single_word / lstrip / rstrip flag. */
+int64_t tko_encode_added(const tko_tables* t, const tko_added* a,
+                         const uint8_t* s, int64_t nb, uint32_t* out,
+                         int64_t cap) {
+  uint8_t first[256];
+  memset(first, 0, sizeof first);
+  for (int64_t k = 0; k < a->n; ++k)
+    if (a->offsets[k + 1] > a->offsets[k]) first[a->blob[a->offsets[k]]] = 1;
+  int64_t total = 0, seg = 0, i = 0;
+  while (i <= nb) {
+    int64_t best = -1, blen = 0;
+    if (i < nb && first[s[i]]) {
+      for (int64_t k = 0; k < a->n; ++k) {
+        const int64_t L = (int64_t)(a->offsets[k + 1] - a->offsets[k]);
+        if (L > blen && L <= nb - i &&
+            memcmp(s + i, a->blob + a->offsets[k], (size_t)L) == 0) {
+          best = k;
+          blen = L;
+        }
+      }
+    }
+    if (best >= 0 || i == nb) {
+      if (i > seg) {
+        int64_t c = tko_encode(t, s + seg, i - seg, out + total, cap - total);
+        if (c < 0) return c;
+        total += c;
+      }
+      if (i == nb) break;
+      if (total + 1 > cap) return TKO_E_CAP;
+      out[total++] = a->ids[best];
+      i += blen;
+      seg = i;
+    } else {
+      ++i;
+    }
+  }
+  return total;
+}

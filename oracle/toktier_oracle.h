@@ -36,4 +36,15 @@ int64_t tko_bpe(const tko_tables* t, const uint8_t* s, int64_t m, uint32_t* out)
 int tko_nfc_qc(const tko_tables* t, const uint8_t* s, int64_t nb);
 int64_t tko_encode(const tko_tables* t, const uint8_t* s, int64_t nb,
                    uint32_t* out, int64_t cap);
+
+/* added-token literals: literal k is blob[offsets[k] .. offsets[k+1]) */
+typedef struct tko_added {
+  const uint8_t* blob;
+  const uint64_t* offsets;  /* n + 1 */
+  const uint32_t* ids;
+  int64_t n;
+} tko_added;
+int64_t tko_encode_added(const tko_tables* t, const tko_added* a,
+                         const uint8_t* s, int64_t nb, uint32_t* out,
+                         int64_t cap);
 #endif

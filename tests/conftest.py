@@ -53,6 +53,11 @@ class FamilyKit:
         self.oracle = Oracle(self.tables, classes.class_table(),
                              classes.nfc_qc_table(), self.family.ruleset,
                              self.family.digits_max, self.family.needs_nfc)
+        # the artifact's added-token literals, split out as HF does
+        import toktier_amd
+        self.added = toktier_amd.added_tokens(self.json)
+        self.oracle.set_added([t.content.encode() for t in self.added],
+                              [t.id for t in self.added])
         self._hf = None
 
     @property
@@ -64,6 +69,31 @@ class FamilyKit:
 
     def hf_ids(self, text: str) -> list[int]:
         return self.hf.encode(text, add_special_tokens=False).ids
+
+    def expected(self, text: str):
+        """The oracle's ids for ``text``; when a segment fails the NFC
+        quick check, the text is split at its literals, each segment is
+        normalized by the certified engine's NFC and encoded alone, and the
+        literal ids are spliced back in (what the facade does)."""
+        got = self.oracle.encode_bytes(text.encode("utf-8"))
+        if not (isinstance(got, int) and self.family.needs_nfc):
+            return got
+        import numpy as np
+        from tokenizers import normalizers
+        from toktier_amd import LiteralSplitter
+        nfc = normalizers.NFC()
+        parts = []
+        for seg, lit in LiteralSplitter(self.added).split(text):
+            if lit is not None:
+                parts.append(np.asarray([lit], dtype=np.uint32))
+                continue
+            ids = self.oracle.encode_bytes(
+                nfc.normalize_str(seg).encode("utf-8"), normalized=True,
+                literals=False)
+            if isinstance(ids, int):
+                return ids
+            parts.append(ids)
+        return np.concatenate(parts) if parts else np.zeros(0, np.uint32)
 
 
 _KITS: dict[str, FamilyKit] = {}

@@ -43,6 +43,44 @@ def fuzz(rng: np.random.Generator, n: int) -> list[str]:
             for k in rng.integers(1, 40, size=n)]
 
 
+def literal_cases(name: str) -> list[str]:
+    """Texts holding the family's added-token literals: chat turns,
+    literals back to back, inside words, at the ends, partial and nested
+    look-alikes, and (NFC family) a combining mark right after a literal
+    (it composes with the literal's last byte unless the literal is split
+    out first)."""
+    lits = [c for c, _, _ in standin.family_added_tokens(name)]
+    a, b = lits[0], lits[-1]
+    texts = [
+        a, a + a, a + b + a, "x" + a + "y", " " + a + " ", a + "  \n",
+        "word" + a + "'s", "12" + a + "34", a[:-1], a[1:], "<" + a + ">",
+        a[:-1] + a, "\r\n" + a + "\r\n \n", "  " + a + "\t\t",
+        "".join(lits[:12]), " ".join(lits[-6:]),
+        a + "\u0338 e\u0301 done", "café" + b + "\u0301",
+    ]
+    if name == "qwen3_8b":
+        texts += [
+            "<|im_start|>system\nYou are helpful.<|im_end|>\n"
+            "<|im_start|>user\nWhat's 2+2?<|im_end|>\n"
+            "<|im_start|>assistant\n<think>\nsimple</think>\n\n4<|im_end|>\n",
+            "<tool_call>\n{\"name\": \"f\"}\n</tool_call><tool_response>ok</tool_response>",
+            "<|fim_prefix|>def f(x):<|fim_suffix|>\n<|fim_middle|>",
+            "<|vision_start|><|image_pad|><|image_pad|><|vision_end|>naïve",
+        ]
+    elif name == "llama_3_1_8b":
+        texts += [
+            "<|begin_of_text|><|start_header_id|>system<|end_header_id|>\n\n"
+            "Be brief.<|eot_id|><|start_header_id|>user<|end_header_id|>\n\n"
+            "hi   there<|eot_id|><|start_header_id|>assistant<|end_header_id|>\n\n",
+            "<|reserved_special_token_12|><|reserved_special_token_1|>x",
+            "<|reserved_special_token_2|>47|>", "<|python_tag|>print(1)<|eom_id|>",
+        ]
+    else:
+        texts += ["doc one.<|endoftext|>doc two<|endoftext|><|endoftext|>",
+                  "<|endoftext"]
+    return texts
+
+
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
     for name in ("qwen3_8b", "llama_3_1_8b", "gpt2"):
@@ -56,6 +94,7 @@ def main() -> None:
         texts += [code[i:i + 600] for i in range(0, 3000, 600)]
         cjk = workloads.config5(js, n_chars=4000, n_runs=1, run_chars=500)
         texts += [cjk[i:i + 800] for i in range(0, 4000, 800)]
+        texts += literal_cases(name)
         cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}
                  for t in texts]
         out["families"][name] = {

@@ -9,6 +9,11 @@ bit-identical to a from-scratch HF ``tokenizers`` encode of ``text`` with
 device NFC quick check is normalized exactly with the certified engine's
 NFC normalizer and encoded again on the device, which is what the
 reference host does for every non-ASCII text (``gpu.rs:1446-1461``).
+
+Added tokens (the artifact's ``added_tokens``, e.g. ``<|im_end|>``) are
+split out on the device, the way HF does it before normalization and
+pretokenization; the reference instead routes every input that holds one
+to its CPU engine (``frontend/added.py:503-555``, ``runtime.rs:641-662``).
 """
 
 from __future__ import annotations
@@ -22,7 +27,9 @@ from pathlib import Path
 import numpy as np
 
 from . import bpe_tables, classes, families, standin
-from ._ffi import (TK_ABI_VERSION, TK_E_NEEDS_NFC, TK_FLAG_NORMALIZED,
+from ._ffi import (TK_ABI_VERSION, TK_ADDED_LSTRIP, TK_ADDED_NORMALIZED,
+                   TK_ADDED_RSTRIP, TK_ADDED_SINGLE_WORD, TK_ADDED_SPECIAL,
+                   TK_E_NEEDS_NFC, TK_FLAG_NO_ADDED, TK_FLAG_NORMALIZED,
                    Engine, EngineError, TkConfig)
 
 __all__ = ["load", "Tokenizer", "Encoding", "EngineError", "families"]
@@ -51,6 +58,80 @@ class _Counters:
     last_bytes: int = 0
     last_ids: int = 0
     last_stage_us: list = field(default_factory=list)
+    last_literals: int = 0
+
+
+@dataclass(frozen=True)
+class AddedToken:
+    """One ``added_tokens`` entry of a tokenizer.json."""
+
+    content: str
+    id: int
+    flags: int  # TK_ADDED_* bits
+
+
+def added_tokens(tokenizer_json: str) -> list[AddedToken]:
+    """The artifact's added tokens in artifact order, with their flags and
+    the ids HF tokenizers 0.22.2 gives them when it loads the file: the
+    ``id`` field is not used; a content that is a model vocabulary entry
+    keeps that entry's id, any other takes the vocabulary size, or one
+    more than the largest id given so far when that is not below it; an
+    empty or repeated content is skipped (the first one stands)."""
+    spec = json.loads(tokenizer_json)
+    vocab = (spec.get("model") or {}).get("vocab") or {}
+    size = len(vocab)
+    given: dict[str, int] = {}
+    out = []
+    for t in spec.get("added_tokens") or []:
+        content = str(t["content"])
+        if not content or content in given:
+            continue
+        if content in vocab:
+            tid = int(vocab[content])
+        else:
+            top = max(given.values(), default=None)
+            tid = size if top is None or top < size else top + 1
+        given[content] = tid
+        fl = ((TK_ADDED_SPECIAL if t.get("special") else 0)
+              | (TK_ADDED_SINGLE_WORD if t.get("single_word") else 0)
+              | (TK_ADDED_LSTRIP if t.get("lstrip") else 0)
+              | (TK_ADDED_RSTRIP if t.get("rstrip") else 0)
+              | (TK_ADDED_NORMALIZED if t.get("normalized") else 0))
+        out.append(AddedToken(content, tid, fl))
+    return out
+
+
+class LiteralSplitter:
+    """HF's added-token split on the host, for the texts the device sends
+    back for exact normalization: scanning left to right, the first
+    position where a literal matches takes the longest literal matching
+    there, and the scan goes on after it (the same split the device does;
+    the reference's scan / assemble, ``frontend/added.py:503-555``). A
+    regex alternation tried longest first is exactly that: Python's
+    alternation takes the first alternative that matches at the leftmost
+    position where any does."""
+
+    def __init__(self, tokens: list[AddedToken]):
+        import re
+        self._ids = {t.content: t.id for t in tokens}
+        by_len = sorted(tokens, key=lambda t: -len(t.content))
+        self._pat = (re.compile("|".join(re.escape(t.content) for t in by_len))
+                     if tokens else None)
+
+    def split(self, text: str) -> list[tuple[str, int | None]]:
+        """Ordered ``(segment, None)`` / ``(literal, id)`` spans."""
+        if self._pat is None:
+            return [(text, None)] if text else []
+        out: list[tuple[str, int | None]] = []
+        at = 0
+        for m in self._pat.finditer(text):
+            if m.start() > at:
+                out.append((text[at:m.start()], None))
+            out.append((m.group(), self._ids[m.group()]))
+            at = m.end()
+        if at < len(text):
+            out.append((text[at:], None))
+        return out
 
 
 class Tokenizer:
@@ -83,6 +164,17 @@ class Tokenizer:
         self._lock = threading.Lock()
         self._counters = _Counters()
         self._nfc = None
+        self.added_tokens = added_tokens(tokenizer_json)
+        if self.added_tokens:
+            try:
+                self.engine.set_added(
+                    [t.content.encode("utf-8") for t in self.added_tokens],
+                    [t.id for t in self.added_tokens],
+                    [t.flags for t in self.added_tokens])
+            except EngineError:
+                self.engine.close()
+                raise
+        self._splitter = None
 
     # -- exact normalization for texts that fail the device quick check
     def _normalize(self, text: str) -> str:
@@ -91,21 +183,48 @@ class Tokenizer:
             self._nfc = normalizers.NFC()
         return self._nfc.normalize_str(text)
 
+    # -- texts that fail the device quick check: split at the literals,
+    # normalize each segment exactly, encode the segments as one batch
+    # (literal extraction off: they are the text between literals) and
+    # splice the literal ids back in (frontend/added.py:544-555)
+    def split_literals(self, text: str) -> list[tuple[str, int | None]]:
+        if self._splitter is None:
+            self._splitter = LiteralSplitter(self.added_tokens)
+        return self._splitter.split(text)
+
+    def _encode_normalized(self, text: str) -> np.ndarray:
+        plan = self.split_literals(text)
+        segs = [self._normalize(t).encode("utf-8") for t, i in plan if i is None]
+        ids, rows, status = self.engine.encode_batch(
+            segs, TK_FLAG_NORMALIZED | TK_FLAG_NO_ADDED)
+        parts, k = [], 0
+        for t, i in plan:
+            if i is not None:
+                parts.append(np.asarray([i], dtype=np.uint32))
+                continue
+            if status[k] != 0:
+                raise EngineError(int(status[k]), "tk_engine_encode_batch",
+                                  "segment failed after normalization")
+            parts.append(ids[int(rows[k]):int(rows[k + 1])])
+            k += 1
+        with self._lock:
+            self._counters.renormalized += 1
+        return (np.concatenate(parts) if parts
+                else np.zeros(0, dtype=np.uint32))
+
     def encode_bytes(self, data: bytes) -> np.ndarray:
         try:
             ids = self.engine.encode(data)
         except EngineError as err:
             if err.status != TK_E_NEEDS_NFC:
                 raise
-            data = self._normalize(data.decode("utf-8")).encode("utf-8")
-            ids = self.engine.encode(data, TK_FLAG_NORMALIZED)
-            with self._lock:
-                self._counters.renormalized += 1
+            ids = self._encode_normalized(data.decode("utf-8"))
         with self._lock:
             c = self._counters
             c.executions += 1
             c.last_bytes = len(data)
             c.last_ids = int(ids.size)
+            c.last_literals = self.engine.last_literals()
         return ids
 
     def encode(self, text: str) -> Encoding:
@@ -126,16 +245,8 @@ class Tokenizer:
             else:
                 raise EngineError(int(status[d]), "tk_engine_encode_batch",
                                   f"row {d} failed")
-        if redo:
-            nd = [self._normalize(texts[d]).encode("utf-8") for d in redo]
-            ids2, rows2, status2 = self.engine.encode_batch(nd, TK_FLAG_NORMALIZED)
-            for k, d in enumerate(redo):
-                if status2[k] != 0:
-                    raise EngineError(int(status2[k]), "tk_engine_encode_batch",
-                                      f"row {d} failed after normalization")
-                out[d] = Encoding(ids2[int(rows2[k]):int(rows2[k + 1])].copy())
-            with self._lock:
-                self._counters.renormalized += len(redo)
+        for d in redo:
+            out[d] = Encoding(self._encode_normalized(texts[d]))
         with self._lock:
             self._counters.executions += 1
         return out  # type: ignore[return-value]
@@ -164,7 +275,10 @@ class Tokenizer:
             "execution_counts": {"gpu": c.executions},
             "fallback_counts": {},
             "nfc_renormalized": c.renormalized,
-            "last_execution": {"bytes": c.last_bytes, "ids": c.last_ids},
+            "added_tokens": len(self.added_tokens),
+            "added_token_frontend": "device" if self.added_tokens else None,
+            "last_execution": {"bytes": c.last_bytes, "ids": c.last_ids,
+                               "added_literals": c.last_literals},
         }
 
     def close(self) -> None:

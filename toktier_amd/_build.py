@@ -22,7 +22,7 @@ LIB = LIBDIR / "libtoktier_hip.so"
 MANIFEST = LIBDIR / "manifest.json"
 ARCH = "gfx950"
 
-SOURCES = ["tk_device.hip", "tk_engine.cpp"]
+SOURCES = ["tk_device.hip", "tk_added.hip", "tk_engine.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -23,14 +23,22 @@ TK_E_UTF8 = -5
 TK_E_NEEDS_NFC = -6
 TK_E_CAPACITY = -7
 TK_E_INTERNAL = -8
+TK_E_UNSUPPORTED = -9
 TK_FLAG_NORMALIZED = 1
+TK_FLAG_NO_ADDED = 2
+# added-token flags (tokenizer.json "added_tokens" fields)
+TK_ADDED_SPECIAL = 1
+TK_ADDED_SINGLE_WORD = 2
+TK_ADDED_LSTRIP = 4
+TK_ADDED_RSTRIP = 8
+TK_ADDED_NORMALIZED = 16
 
 STATUS_NAMES = {
     TK_OK: "TK_OK", TK_E_INVALID_ARG: "TK_E_INVALID_ARG",
     TK_E_SHAPE: "TK_E_SHAPE", TK_E_DEVICE: "TK_E_DEVICE",
     TK_E_ARCH: "TK_E_ARCH", TK_E_UTF8: "TK_E_UTF8",
     TK_E_NEEDS_NFC: "TK_E_NEEDS_NFC", TK_E_CAPACITY: "TK_E_CAPACITY",
-    TK_E_INTERNAL: "TK_E_INTERNAL",
+    TK_E_INTERNAL: "TK_E_INTERNAL", TK_E_UNSUPPORTED: "TK_E_UNSUPPORTED",
 }
 
 #: every entry point include/toktier_hip.h declares
@@ -38,7 +46,8 @@ SYMBOLS = (
     "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
     "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
-    "tk_engine_last_timing", "tk_last_error",
+    "tk_engine_last_timing", "tk_engine_set_added",
+    "tk_engine_last_literals", "tk_last_error",
 )
 
 
@@ -105,6 +114,10 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_set_timing.argtypes = [vp, C.c_int]
     L.tk_engine_last_timing.restype = C.c_int
     L.tk_engine_last_timing.argtypes = [vp, C.POINTER(C.c_double), C.c_int]
+    L.tk_engine_set_added.restype = C.c_int
+    L.tk_engine_set_added.argtypes = [vp, sz, vp, vp, vp, vp]
+    L.tk_engine_last_literals.restype = C.c_int
+    L.tk_engine_last_literals.argtypes = [vp, C.POINTER(C.c_uint64)]
     if path is None:
         _lib = L
     return L
@@ -193,6 +206,28 @@ class Engine:
                                              stream)
         check(st, "tk_engine_encode_device")
         return n.value
+
+    def set_added(self, contents: list[bytes], ids: list[int],
+                  flags: list[int]) -> None:
+        """Install the artifact's added tokens (``TK_ADDED_*`` flags); an
+        empty list removes them."""
+        n = len(contents)
+        blob = np.frombuffer(b"".join(contents) or b"\0", dtype=np.uint8).copy()
+        offs = np.zeros(n + 1, dtype=np.uint64)
+        if n:
+            offs[1:] = np.cumsum([len(c) for c in contents], dtype=np.uint64)
+        idv = np.asarray(ids if n else [0], dtype=np.uint32)
+        fl = np.asarray(flags if n else [0], dtype=np.uint8)
+        check(self._L.tk_engine_set_added(self._h, n, blob.ctypes.data,
+                                          offs.ctypes.data, idv.ctypes.data,
+                                          fl.ctypes.data),
+              "tk_engine_set_added")
+
+    def last_literals(self) -> int:
+        n = C.c_uint64()
+        check(self._L.tk_engine_last_literals(self._h, C.byref(n)),
+              "tk_engine_last_literals")
+        return int(n.value)
 
     def set_timing(self, mode: int) -> None:
         """0 off, 1 (or True) every stage, 2 the packed merge kernel only."""

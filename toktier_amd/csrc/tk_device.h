@@ -119,6 +119,14 @@ struct DevWork {
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
+  // added-token literals (nullptr when the call extracts none): a literal
+  // [s, e) marks s in lits and s+1..e-1 in litb, and s and e as document
+  // starts; its bytes form no piece, and its id is written at tok[s]
+  uint64_t* lits;
+  uint64_t* litb;
+  uint64_t* cand;        // literal matches: bit per byte where one starts
+  uint32_t* litm;        // per byte: the longest literal matching there
+  uint32_t* nlit;        // literals extracted (ctrl)
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
   int64_t clear_words;   // inlong / failm words
@@ -127,15 +135,32 @@ struct DevWork {
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
-              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_PCOUNT = 16, CTRL_UEND = 32,
-              CTRL_WORDS = 64;
+              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PCOUNT = 16,
+              CTRL_UEND = 32, CTRL_WORDS = 64;
 // gate words in host memory: k_pack_copy writes GATE_NLONG / GATE_BIG and
 // then GATE_SEQ (the host learns, while the packed merge runs, whether the
 // long-piece stages have any work), k_compact's last block
 // writes the request's outcome (status, id count, failed cuts) and then
 // GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
-              GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_WORDS = 8;
+              GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_NLIT = 7,
+              GATE_WORDS = 8;
+
+// Added-token literals on the device: a trie over their bytes. Node v has
+// edges [first, first + n) of the edge array, sorted by byte, each edge
+// child << 8 | byte; term is the literal that ends at v plus one (0: none).
+// Node 0 is the root. gate: the literals' first bytes (bit b of word b/64).
+struct DevAdded {
+  const uint2* nodes;     // {first edge, n | term << 9}
+  const uint32_t* edges;  // child << 8 | byte
+  const uint32_t* len;    // literal bytes
+  const uint32_t* id;     // literal token id
+  uint64_t gate[4];
+  uint32_t lmax;          // longest literal, bytes (1..255)
+  uint32_t n;             // literals
+};
+constexpr int ADDED_MAX_LEN = 255;
+constexpr int ADDED_BLOCK_BYTES = 4096;  // k_added_find: 16 bytes per thread
 // packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
 constexpr int PACK_BLOCKS = 2048;
 // slots (lanes per piece) of the length classes, and the shortest piece of
@@ -213,6 +238,10 @@ hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
 hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// k_added_find + k_added_select: the literal split of the request (the
+// document-start mask is cleared first unless the caller marked documents)
+hipError_t launch_added(const DevAdded& a, const DevWork& w, bool clear_docmask,
+                        hipStream_t s, hipEvent_t start = nullptr);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);

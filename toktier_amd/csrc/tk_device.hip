@@ -635,14 +635,24 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     if (blockIdx.x == 0 && tid < CTRL_WORDS) w.ctrl_next[tid] = 0;
   }
   const int64_t wlo = (base >> 6) - 3;
+  // dm: the staged mask words hold a document start. A block without one
+  // decides as if documents were not marked (the same answers: the mask
+  // only matters where it has bits, and positions past the staged words go
+  // to the mask in HBM either way).
+  bool dm = false;
   if (DM) {
     const int64_t nmw = nb / 64 + 2;  // words the caller's mask holds
+    int nz = 0;
     for (int j = tid; j < PT_DMW; j += PRETOK_TPB) {
       const int64_t wd = wlo + j;
-      sdm[j] = (wd >= 0 && wd < nmw) ? w.docmask[wd] : 0;
+      const uint64_t v = (wd >= 0 && wd < nmw) ? w.docmask[wd] : 0;
+      sdm[j] = v;
+      nz |= v != 0;
     }
+    dm = __syncthreads_or(nz) != 0;
+  } else {
+    __syncthreads();
   }
-  __syncthreads();
   const int64_t lo = base - PT_HALO;
   // entries within the text: local offsets [jlo, jhi)
   const int jlo = lo < 0 ? (int)(-lo) : 0;
@@ -694,7 +704,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   const LCtx c{GCtx{w.text, nb, DM ? w.docmask : nullptr, t.cls}, se, lo, sdm, wlo};
   // document start at local offset L: position 0, or a marked doc head
   const int Lz = lo <= 0 ? (int)(-lo) : -1;
-  auto ds = [&](int L) { return DM ? c.ds(lo + L) : L == Lz; };
+  auto ds = [&](int L) { return dm ? c.ds(lo + L) : L == Lz; };
   auto prv = [&](int L) {  // local offset of the character before L
     return L - 1 - (int)((se[L - 1] >> 23) & 3);
   };
@@ -753,12 +763,12 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
       if (open) {
         const uint64_t below = (1ULL << lane) - 1;
-        if (r == FAST_DIGITS && !DM) {
+        if (r == FAST_DIGITS && !dm) {
           // the ASCII digits before i, when the word shows where they begin
           const uint64_t nd_ = ~mDG & below;
           if (nd_ && !((mHI >> (63 - __builtin_clzll(nd_))) & 1))
             r = (lane - 1 - (63 - __builtin_clzll(nd_))) % t.dmax == 0;
-        } else if (r == FAST_CRLF && !DM && bb < 0x80) {
+        } else if (r == FAST_CRLF && !dm && bb < 0x80) {
           // another CR/LF ahead in the run: it shows in the word before
           // the first byte that is neither (unless that byte is not ASCII)
           const uint64_t above = ~mask_le(lane);
@@ -833,7 +843,10 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
       }
     }
-    const uint64_t m = __ballot(s);
+    uint64_t m = __ballot(s);
+    // no start inside an added-token literal (its first byte is a document
+    // start already)
+    if (DM && w.litb) m &= ~w.litb[wd];
     if (lane == 0) {
       sw[k] = m;
       if (k < PT_TILE / 64) w.starts[wd] = m;
@@ -848,7 +861,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
     const int64_t a = base + 64 * k + lane;
     if (a >= nb) break;  // (positions only grow along the loop)
-    const int kind = piece_kind(sw[k], sw[k + 1], lane, two);
+    int kind = piece_kind(sw[k], sw[k + 1], lane, two);
+    // a literal's piece is done: its id is in tok already
+    if (DM && w.lits && ((w.lits[(base >> 6) + k] >> lane) & 1)) kind = PIECE_NONE;
     if (kind >= 0) {
       const uint32_t j = atomicAdd(&lcnt[kind], 1u);
       w.plocal[(int64_t)blockIdx.x * PT_LOCAL_SLOTS + loff[kind] + j] = (uint32_t)a;
@@ -2366,6 +2381,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
       w.gate[GATE_STATUS] = atomicOr(w.status, 0u);
       w.gate[GATE_TOTAL] = total;
       w.gate[GATE_FAIL] = *w.nfail;
+      w.gate[GATE_NLIT] = w.nlit ? *w.nlit : 0u;
       __threadfence_system();
       w.gate[GATE_DONE] = w.seq;
       __threadfence_system();

@@ -19,6 +19,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -184,6 +185,12 @@ struct tk_engine {
   DevBuf<int32_t> nx, pv;
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
   DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk, plocal;
+  // added-token literals (tk_engine_set_added) and their per-call masks
+  DevBuf<uint2> lit_nodes;
+  DevBuf<uint32_t> lit_edges, lit_len, lit_id, litm;
+  DevBuf<uint64_t> lits, litb, cand;
+  tk::DevAdded added{};
+  uint64_t last_literals = 0;
   size_t docs_cap = 0;
   uint32_t slot = 0;  // control slot of the next call
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
@@ -270,6 +277,13 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->plocal.alloc((size_t)tk::PT_LOCAL_SLOTS * tk::pretok_tiles((int64_t)need)));
     e->cap = need;
   }
+  if (e->added.n && e->litm.n < e->cap + 64) {
+    const size_t words = e->cap / 64 + 8;
+    HIP_TRY(e->lits.alloc(words));
+    HIP_TRY(e->litb.alloc(words));
+    HIP_TRY(e->cand.alloc(words));
+    HIP_TRY(e->litm.alloc(e->cap + 64));
+  }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
     HIP_TRY(e->rows.alloc(n_docs + 1));
@@ -280,7 +294,7 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
 
 tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
                       const uint64_t* d_docmask, bool check_nfc,
-                      uint32_t* out, size_t out_cap) {
+                      uint32_t* out, size_t out_cap, bool literals) {
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   tk::DevWork w{};
   w.text = d_text;
@@ -324,6 +338,11 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.ctrl_next = e->ctrl.p + (e->slot ^ 1) * tk::CTRL_WORDS;
+  w.nlit = ctrl + tk::CTRL_NLIT;
+  w.lits = literals ? e->lits.p : nullptr;
+  w.litb = literals ? e->litb.p : nullptr;
+  w.cand = literals ? e->cand.p : nullptr;
+  w.litm = literals ? e->litm.p : nullptr;
   w.clear_words = (int64_t)(nb / 64 + 4);
   w.clear_dwords = w.clear_words / 64 + 2;
   return w;
@@ -371,13 +390,19 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 // (host-driven passes, each removing the failed cuts) until every cut holds.
 // Nothing is cleared from the host: k_pretok clears the per-call masks and
 // the control slot of the next call, so the stages run back to back.
+// Added-token literals (literals == true): k_added_find / k_added_select
+// split the request first; the split marks document starts, so k_pretok
+// runs its document-mask instance (on e->docmask, cleared by k_added_find,
+// when the caller marked no documents).
 int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
                  const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
                  uint32_t* out, size_t out_cap, uint32_t* status,
-                 uint32_t* total) {
+                 uint32_t* total, bool literals = false) {
   ++e->seq;
+  const bool own_mask = literals && d_docmask == nullptr;
+  if (own_mask) d_docmask = e->docmask.p;
   const tk::DevWork w =
-      make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap);
+      make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap, literals);
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
   // Timing mode 1, stage boundaries taken by the dispatches themselves:
@@ -390,7 +415,12 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   // they can.)
   const bool stages = e->timing == 1, packonly = e->timing == 2;
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
-  HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
+  if (literals) {
+    HIP_TRY(tk::launch_added(e->added, w, own_mask, s, at(0)));
+    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, nullptr));
+  } else {
+    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
+  }
   e->slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_lists(e->t, w, s));
   HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
@@ -427,6 +457,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   h[tk::CTRL_STATUS] = e->gate[tk::GATE_STATUS];
   h[tk::CTRL_TOTAL] = e->gate[tk::GATE_TOTAL];
   h[tk::CTRL_FAIL] = e->gate[tk::GATE_FAIL];
+  e->last_literals = literals ? e->gate[tk::GATE_NLIT] : 0;
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
   if (h[tk::CTRL_STATUS] & tk::ST_STALL)
@@ -519,6 +550,21 @@ bool host_nfc_ok(const std::vector<uint8_t>& qc, const uint8_t* s, size_t n) {
     i += need + 1;
   }
   return true;
+}
+
+bool literal_mode(const tk_engine* e, uint32_t flags) {
+  return e->added.n > 0 && !(flags & TK_FLAG_NO_ADDED);
+}
+
+bool utf8_ok(const uint8_t* s, size_t n) { return host_utf8_ok(s, n); }
+
+// a proper suffix of x is a prefix of y, or one holds the other
+bool can_overlap(const std::string& x, const std::string& y) {
+  if (x.find(y) != std::string::npos || y.find(x) != std::string::npos)
+    return true;
+  for (size_t k = 1; k < x.size() && k < y.size() + 1; ++k)
+    if (k <= y.size() && x.compare(x.size() - k, k, y, 0, k) == 0) return true;
+  return false;
 }
 
 }  // namespace
@@ -754,6 +800,124 @@ int tk_engine_last_timing(const tk_engine* e, double* us, int n) {
   return k;
 }
 
+int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
+                        const uint64_t* offsets, const uint32_t* ids,
+                        const uint8_t* flags) {
+  if (!e) return fail(TK_E_INVALID_ARG, "engine is null");
+  std::lock_guard<std::mutex> lk(e->mu);
+  if (n > 0 && (!contents || !offsets || !ids || !flags))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  if (n > 65536) return fail(TK_E_UNSUPPORTED, "%zu added tokens (at most 65536)", n);
+  std::vector<std::string> raw, norm;
+  for (size_t k = 0; k < n; ++k) {
+    if (offsets[k + 1] < offsets[k])
+      return fail(TK_E_INVALID_ARG, "offsets must be non-decreasing");
+    const size_t len = offsets[k + 1] - offsets[k];
+    const uint8_t* c = contents + offsets[k];
+    if (len == 0 || len > (size_t)tk::ADDED_MAX_LEN)
+      return fail(TK_E_UNSUPPORTED, "added token %zu has %zu bytes (1..%d)", k,
+                  len, tk::ADDED_MAX_LEN);
+    if (!utf8_ok(c, len))
+      return fail(TK_E_INVALID_ARG, "added token %zu is not valid UTF-8", k);
+    if (ids[k] == tk::INVALID_ID)
+      return fail(TK_E_INVALID_ARG, "added token %zu has id 0xFFFFFFFF", k);
+    if (flags[k] & (TK_ADDED_SINGLE_WORD | TK_ADDED_LSTRIP | TK_ADDED_RSTRIP))
+      return fail(TK_E_UNSUPPORTED,
+                  "added token %zu uses single_word / lstrip / rstrip", k);
+    if ((flags[k] & TK_ADDED_NORMALIZED) && e->t.needs_nfc)
+      return fail(TK_E_UNSUPPORTED,
+                  "added token %zu is normalized=true and the family "
+                  "normalizes: it would be matched on normalized segments", k);
+    (flags[k] & TK_ADDED_NORMALIZED ? norm : raw)
+        .emplace_back(reinterpret_cast<const char*>(c), len);
+  }
+  // HF extracts raw literals first and normalized ones in the segments
+  // left over; with the identity normalizer one leftmost-longest pass gives
+  // the same split exactly when no literal of one kind can overlap one of
+  // the other
+  for (const auto& x : raw)
+    for (const auto& y : norm)
+      if (can_overlap(x, y) || can_overlap(y, x))
+        return fail(TK_E_UNSUPPORTED,
+                    "a raw and a normalized added token can overlap");
+  // trie: node 0 is the root; children kept sorted by byte
+  std::vector<std::map<uint8_t, uint32_t>> kids(1);
+  std::vector<uint32_t> term(1, 0);
+  uint32_t lmax = 0;
+  uint64_t gate[4] = {0, 0, 0, 0};
+  std::vector<uint32_t> len(n), idv(n);
+  for (size_t k = 0; k < n; ++k) {
+    const uint8_t* c = contents + offsets[k];
+    const uint32_t L = (uint32_t)(offsets[k + 1] - offsets[k]);
+    uint32_t v = 0;
+    for (uint32_t j = 0; j < L; ++j) {
+      auto it = kids[v].find(c[j]);
+      if (it == kids[v].end()) {
+        const uint32_t u = (uint32_t)kids.size();
+        kids[v][c[j]] = u;
+        kids.emplace_back();
+        term.push_back(0);
+        v = u;
+      } else {
+        v = it->second;
+      }
+    }
+    if (term[v]) return fail(TK_E_INVALID_ARG, "added token %zu is a duplicate", k);
+    term[v] = (uint32_t)k + 1;
+    len[k] = L;
+    idv[k] = ids[k];
+    lmax = std::max(lmax, L);
+    gate[c[0] >> 6] |= 1ULL << (c[0] & 63);
+  }
+  if (kids.size() >= (1u << 24))
+    return fail(TK_E_UNSUPPORTED, "added-token trie over 2^24 nodes");
+  std::vector<uint2> nodes(kids.size());
+  std::vector<uint32_t> edges;
+  for (size_t v = 0; v < kids.size(); ++v) {
+    nodes[v].x = (uint32_t)edges.size();
+    nodes[v].y = (uint32_t)kids[v].size() | (term[v] << 9);
+    for (const auto& kv : kids[v]) edges.push_back((kv.second << 8) | kv.first);
+  }
+  HIP_TRY(hipSetDevice(e->device));
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  e->added = tk::DevAdded{};
+  if (n == 0) return TK_OK;
+  auto up = [&](auto& buf, const auto& v) -> int {
+    if (buf.alloc(v.size()) != hipSuccess)
+      return fail(TK_E_DEVICE, "hipMalloc of the added-token tables failed");
+    if (hipMemcpy(buf.p, v.data(), v.size() * sizeof(v[0]), hipMemcpyHostToDevice) != hipSuccess)
+      return fail(TK_E_DEVICE, "added-token table upload failed");
+    return TK_OK;
+  };
+  int rc;
+  if ((rc = up(e->lit_nodes, nodes)) != TK_OK) return rc;
+  if ((rc = up(e->lit_edges, edges)) != TK_OK) return rc;
+  if ((rc = up(e->lit_len, len)) != TK_OK) return rc;
+  if ((rc = up(e->lit_id, idv)) != TK_OK) return rc;
+  tk::DevAdded a{};
+  a.nodes = e->lit_nodes.p;
+  a.edges = e->lit_edges.p;
+  a.len = e->lit_len.p;
+  a.id = e->lit_id.p;
+  for (int k = 0; k < 4; ++k) a.gate[k] = gate[k];
+  a.lmax = lmax;
+  a.n = (uint32_t)n;
+  e->added = a;
+  // the per-call masks follow the workspace capacity
+  if (e->cap) {
+    e->litm.reset();
+    rc = ensure_workspace(e, e->cap, 0);
+    if (rc != TK_OK) return rc;
+  }
+  return TK_OK;
+}
+
+int tk_engine_last_literals(const tk_engine* e, uint64_t* n) {
+  if (!e || !n) return fail(TK_E_INVALID_ARG, "null argument");
+  *n = e->last_literals;
+  return TK_OK;
+}
+
 const char* tk_engine_delivery(const tk_engine* e) { return e ? "prebuilt" : ""; }
 const char* tk_engine_architecture(const tk_engine* e) { return e ? e->arch.c_str() : ""; }
 
@@ -774,7 +938,7 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   // the compaction writes straight into the caller's buffer
   rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr,
                     check, s, static_cast<uint32_t*>(d_ids), ids_cap, &st,
-                    &total);
+                    &total, literal_mode(e, flags));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -800,7 +964,7 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, e->out.p,
-                    e->out.n, &st, &total);
+                    e->out.n, &st, &total, literal_mode(e, flags));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -844,10 +1008,10 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, e->out.p,
-                    e->out.n, &st, &total);
+                    e->out.n, &st, &total, literal_mode(e, flags));
   if (rc != TK_OK) return rc;
   const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check,
-                                  e->out.p, e->out.n);
+                                  e->out.p, e->out.n, false);
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));

@@ -25,7 +25,9 @@ Shapes follow the real artifacts:
   50,257 entries including ``<|endoftext|>``.
 
 The committed artifacts live in ``toktier_amd/data/artifacts`` (xz
-compressed); this module regenerates them (``python -m toktier_amd.standin``).
+compressed); this module regenerates them (``python -m toktier_amd.standin``),
+or only rewrites their added-token lists to the real families' ones
+(``python -m toktier_amd.standin --added-only``).
 Training is not bit-reproducible across machines, so the committed files
 and their sha256 (``ARTIFACT_SHA256``) are the identity, not this script.
 """
@@ -210,21 +212,63 @@ def _train(name: str) -> dict:
     model["ignore_merges"] = bool(fam.ignore_merges)
     if name == "llama_3_1_8b":
         model["merges"] = _tiktoken_style_merges(vocab)
-    added = []
     if name == "gpt2":
         vocab["<|endoftext|>"] = 50256
-        added = [("<|endoftext|>", 50256)]
-    elif name == "qwen3_8b":
-        added = [("<|endoftext|>", 151643), ("<|im_start|>", 151644),
-                 ("<|im_end|>", 151645)]
-    else:
-        added = [("<|begin_of_text|>", 128000), ("<|end_of_text|>", 128001)]
-    spec["added_tokens"] = [
-        {"id": i, "content": c, "single_word": False, "lstrip": False,
-         "rstrip": False, "normalized": False, "special": True}
-        for c, i in added
-    ]
+    spec["added_tokens"] = added_token_entries(name)
     return spec
+
+
+def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
+    """(content, id, special) of the family's added tokens, in the real
+    artifacts' order: Qwen3's 26 chat / tool / vision / FIM markers
+    (ids 151643-151668; the tool, FIM and think markers are not special),
+    Llama-3.1's 256 (128000-128255, reserved slots included) and GPT-2's
+    end-of-text marker."""
+    if name == "gpt2":
+        return [("<|endoftext|>", 50256, True)]
+    if name == "qwen3_8b":
+        special = ["endoftext", "im_start", "im_end", "object_ref_start",
+                   "object_ref_end", "box_start", "box_end", "quad_start",
+                   "quad_end", "vision_start", "vision_end", "vision_pad",
+                   "image_pad", "video_pad"]
+        out = [(f"<|{t}|>", 151643 + k, True) for k, t in enumerate(special)]
+        rest = ["<tool_call>", "</tool_call>", "<|fim_prefix|>",
+                "<|fim_middle|>", "<|fim_suffix|>", "<|fim_pad|>",
+                "<|repo_name|>", "<|file_sep|>", "<tool_response>",
+                "</tool_response>", "<think>", "</think>"]
+        out += [(t, 151657 + k, False) for k, t in enumerate(rest)]
+        return out
+    named = {128000: "begin_of_text", 128001: "end_of_text",
+             128002: "reserved_special_token_0",
+             128003: "reserved_special_token_1",
+             128004: "finetune_right_pad_id",
+             128005: "reserved_special_token_2",
+             128006: "start_header_id", 128007: "end_header_id",
+             128008: "eom_id", 128009: "eot_id", 128010: "python_tag"}
+    return [(f"<|{named.get(i, f'reserved_special_token_{i - 128008}')}|>",
+             i, True) for i in range(128000, 128256)]
+
+
+def added_token_entries(name: str) -> list[dict]:
+    return [{"id": i, "content": c, "single_word": False, "lstrip": False,
+             "rstrip": False, "normalized": False, "special": sp}
+            for c, i, sp in family_added_tokens(name)]
+
+
+def patch_added_tokens(names: list[str]) -> None:
+    """Rewrite the committed artifacts' added_tokens list (the merges and
+    vocabulary stay as they are) and their recorded sha256."""
+    sums = dict(ARTIFACT_SHA256)
+    for name in names:
+        spec = json.loads(load_artifact_json(name))
+        spec["added_tokens"] = added_token_entries(name)
+        raw = json.dumps(spec, ensure_ascii=False,
+                         separators=(",", ":")).encode("utf-8")
+        sums[name] = hashlib.sha256(raw).hexdigest()
+        artifact_path(name).write_bytes(lzma.compress(raw, preset=9))
+        ARTIFACT_SHA256[name] = sums[name]
+        print(name, len(raw), sums[name], flush=True)
+    _SHA_FILE.write_text(json.dumps(sums, indent=1, sort_keys=True) + "\n")
 
 
 def _tiktoken_style_merges(vocab: dict[str, int]) -> list[list[str]]:
@@ -244,6 +288,9 @@ def _tiktoken_style_merges(vocab: dict[str, int]) -> list[list[str]]:
 
 
 def main(argv: list[str]) -> None:
+    if argv[:1] == ["--added-only"]:
+        patch_added_tokens(argv[1:] or sorted(FAMILIES))
+        return
     names = argv or sorted(FAMILIES)
     DATA_DIR.mkdir(parents=True, exist_ok=True)
     sums = dict(ARTIFACT_SHA256)

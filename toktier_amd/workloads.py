@@ -266,6 +266,37 @@ def config5(tokenizer_json: str, n_chars: int = CHARS_4M, sample: int = 0,
     return "".join(out)[:n_chars]
 
 
+def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
+         sample: int = 0) -> str:
+    """C2-style text laid out as chat turns in the family's template, so
+    the request carries added-token literals: Qwen3 ``<|im_start|>role``
+    ... ``<|im_end|>`` (assistant turns with a ``<think>`` block), Llama-3
+    header / ``<|eot_id|>`` turns after ``<|begin_of_text|>``, GPT-2
+    documents joined by ``<|endoftext|>``. Turns hold U[200, 3000] chars."""
+    rng = np.random.default_rng(SEED_BASE + 6 + 1000 * sample)
+    body = config2(tokenizer_json, n_chars=n_chars, sample=sample)
+    roles = ["system", "user", "assistant"]
+    out: list[str] = ["<|begin_of_text|>"] if family == "llama_3_1_8b" else []
+    total, at, turn = sum(map(len, out)), 0, 0
+    while total < n_chars and at < len(body):
+        n = int(rng.integers(200, 3001))
+        content = body[at:at + n]
+        at += n
+        role = roles[0] if turn == 0 else roles[1 + (turn - 1) % 2]
+        if family == "qwen3_8b":
+            if role == "assistant" and rng.random() < 0.5:
+                content = "<think>\n" + content[: n // 3] + "\n</think>\n\n" + content[n // 3:]
+            piece = f"<|im_start|>{role}\n{content}<|im_end|>\n"
+        elif family == "llama_3_1_8b":
+            piece = f"<|start_header_id|>{role}<|end_header_id|>\n\n{content}<|eot_id|>"
+        else:
+            piece = content + "<|endoftext|>"
+        out.append(piece)
+        total += len(piece)
+        turn += 1
+    return "".join(out)[:n_chars]
+
+
 CONFIGS = {
     1: ("qwen3_8b", config1),
     2: ("qwen3_8b", config2),
