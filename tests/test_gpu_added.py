@@ -1,4 +1,4 @@
-"""GPU parity of the added-token split (k_added_find / k_added_select ahead
+"""GPU parity of the added-token split (k_added ahead
 of k_pretok) through the C-ABI: the engine against HF tokenizers 0.22.2
 and the oracle, bit for bit."""
 
@@ -189,3 +189,24 @@ def test_unsupported_tables_are_refused():
         assert list(t2.encode(s).array) == \
             hf.encode(s, add_special_tokens=False).ids, s
     t2.close()
+
+
+@pytest.mark.parametrize("name", ["llama_3_1_8b", "qwen3_8b"])
+def test_document_starts_inside_runs(name):
+    """Document starts (batch boundaries and literal edges) inside digit
+    runs (Llama-3 groups digits by three) and CR/LF whitespace runs: the
+    pretokenizer's word-mask shortcuts must end a run at each of them."""
+    k, t = kit(name), tok(name)
+    lit = k.added[-1].content
+    rng = np.random.default_rng(21)
+    pieces = ["1234567", "89", "0", " \r\n", "\r\n", "\r\n x", " \t\r\n\r\n ",
+              "a", "'s", "  ", "\n\n", lit, "x" * 30, "12" * 20]
+    docs = []
+    for _ in range(80):
+        docs.append("".join(pieces[int(i)] for i in
+                            rng.integers(0, len(pieces), int(rng.integers(1, 9)))))
+    rows = t.encode_batch(docs)
+    for d, r in zip(docs, rows):
+        assert list(r.array) == k.hf_ids(d), repr(d)
+    joined = "".join(docs)
+    assert list(t.encode(joined).array) == k.hf_ids(joined)

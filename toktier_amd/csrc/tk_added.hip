@@ -8,22 +8,30 @@
 // segment. The reference does the split on the host and routes every input
 // that holds a literal to its CPU engine (src/toktier/frontend/added.py:
 // 503-533, crates/toktier-routing-core/src/runtime.rs:527-536, :641-662).
-// Here the split runs on the device, in two kernels, and the segments stay
-// on the GPU path as documents of their own:
-//   k_added_find    per byte whose value starts a literal: walk the trie of
-//                   the literals from there and keep the longest match
-//                   (candidate bit + literal index); clear the masks the
-//                   selection fills.
-//   k_added_select  leftmost-longest choice among the candidates. A
-//                   candidate that no earlier candidate reaches is always
-//                   chosen: a thread starts there and walks the candidates
-//                   that follow up to the next such one, choosing each one
-//                   that starts at or after the end of the last choice
-//                   (back-to-back literals are each their own walk). A
-//                   chosen literal [s, e) marks document
-//                   starts at s and e, s in lits, s+1..e-1 in litb, and
-//                   writes its id at tok[s] (INVALID_ID on its other bytes).
-// k_pretok then forms no piece on a literal's bytes.
+// Here the split runs on the device, in one kernel ahead of k_pretok, and
+// the segments stay on the GPU path as documents of their own.
+//
+// Which literals are chosen is a function of the text alone, so every
+// block decides it for its own bytes without waiting for another:
+//   - a candidate is a position where some literal matches; its literal is
+//     the longest one matching there (a walk down the trie of the
+//     literals);
+//   - a candidate that no earlier candidate reaches (every candidate in the
+//     lmax - 1 bytes before it ends at or before it) is certain: it is
+//     chosen whatever was chosen before it;
+//   - any other candidate is decided by going back to the nearest certain
+//     candidate and scanning forward from there, choosing each candidate
+//     that starts at or after the end of the last choice.
+// A block stages its 4096 bytes with AD_BACK bytes before and AD_AHEAD
+// after (and the trie's edge table, when it fits) in LDS, finds the
+// candidates of the
+// staged range, decides every candidate whose literal can reach its bytes,
+// and writes its own 64 mask words whole: document starts at each chosen
+// literal's first byte and just past its end, the first byte in lits, the
+// others in litb; the literal's id goes to tok at its first byte. Chains of
+// overlapping candidates longer than the staged range are followed in HBM
+// (the text does not change), which is slow but only arises in texts built
+// to overlap literals. k_pretok then forms no piece on a literal's bytes.
 #include "tk_device.h"
 
 #include <hip/hip_ext.h>
@@ -32,188 +40,241 @@ namespace tk {
 
 namespace {
 
+constexpr int AD_BACK = 512;    // > 2 * ADDED_MAX_LEN: a reaching literal
+                                // and its certainty window are staged
+constexpr int AD_AHEAD = 256;   // > ADDED_MAX_LEN: a walk from the block's
+                                // last byte stays staged
+constexpr int AD_STAGE = AD_BACK + ADDED_BLOCK_BYTES + AD_AHEAD;
+constexpr int AD_CAND = AD_BACK + ADDED_BLOCK_BYTES;  // candidates staged
+static_assert(AD_STAGE % 16 == 0, "16-byte staging");
+static_assert(2 * ADDED_MAX_LEN < AD_BACK && ADDED_MAX_LEN < AD_AHEAD,
+              "staged margins hold a literal and its certainty window");
+
 __device__ __forceinline__ bool gate_hit(const DevAdded& a, uint32_t b) {
   const uint64_t g = b < 64 ? a.gate[0] : b < 128 ? a.gate[1]
                    : b < 192 ? a.gate[2] : a.gate[3];
   return (g >> (b & 63)) & 1;
 }
 
-__device__ __forceinline__ bool doc_start(const uint64_t* dm, int64_t i) {
-  return dm && ((dm[i >> 6] >> (i & 63)) & 1);
+// the trie edge (node, byte), or ~0 when there is none
+__device__ __forceinline__ uint64_t edge_find(const uint64_t* tab,
+                                              uint32_t size, uint32_t key) {
+  uint32_t i = added_slot(key, size);
+  for (;;) {
+    const uint64_t e = tab[i];
+    if ((uint32_t)(e >> 36) == key) return e;
+    if (e == ~0ULL) return ~0ULL;
+    i = i + 1 == size ? 0 : i + 1;
+  }
 }
 
-// Longest literal that matches at p (its index + 1, 0 for none). The walk
-// stops at the text end and, when documents are marked, at the next
-// document start (a literal never spans two documents).
-__device__ uint32_t longest_at(const DevAdded& a, const uint8_t* text,
-                               int64_t nb, const uint64_t* dm, int64_t p) {
+// The trie walk from p: len << 16 | (literal + 1) for the longest literal
+// that matches there, 0 for none. It stops at the text end and at the next
+// document start (a literal never spans two documents). bytes[q - base] is
+// the byte at q, dmw[(q >> 6) - dm_base] its document-start word (dmw may
+// be null), tab the edge table (LDS or HBM).
+__device__ uint32_t trie_match(const DevAdded& a, const uint8_t* bytes,
+                               int64_t base, int64_t nb, const uint64_t* dmw,
+                               int64_t dm_base, const uint64_t* tab,
+                               int64_t p) {
+  if (!gate_hit(a, bytes[p - base])) return 0;
   uint32_t v = 0, best = 0;
   for (uint32_t j = 0; j < a.lmax; ++j) {
     const int64_t q = p + j;
-    if (q >= nb || (j > 0 && doc_start(dm, q))) break;
-    const uint32_t b = text[q];
-    const uint2 nd = a.nodes[v];
-    uint32_t child = 0;
-    for (uint32_t k = 0; k < (nd.y & 0x1FF); ++k) {
-      const uint32_t ed = a.edges[nd.x + k];
-      if ((ed & 0xFF) == b) { child = ed >> 8; break; }
-      if ((ed & 0xFF) > b) break;  // edges are sorted by byte
-    }
-    if (child == 0) break;  // the root is nobody's child
-    v = child;
-    const uint32_t term = a.nodes[v].y >> 9;
-    if (term) best = term;
+    if (q >= nb) break;
+    if (j > 0 && dmw && ((dmw[(q >> 6) - dm_base] >> (q & 63)) & 1)) break;
+    const uint64_t e = edge_find(tab, a.tab_size, (v << 8) | bytes[q - base]);
+    if (e == ~0ULL) break;
+    v = (uint32_t)(e >> 16) & 0xFFFFF;
+    if (e & 0xFFFF) best = ((j + 1) << 16) | (uint32_t)(e & 0xFFFF);
   }
   return best;
 }
 
-// One block per ADDED_BLOCK_BYTES bytes (64 mask words), 16 bytes per
-// thread; threads 4w..4w+3 hold word w of the block.
-__global__ __launch_bounds__(256) void k_added_find(DevAdded a, DevWork w,
-                                                    uint64_t* docmask,
-                                                    int clear_dm,
-                                                    int64_t nwords) {
-  const int tid = threadIdx.x;
-  const int64_t p0 = (int64_t)blockIdx.x * ADDED_BLOCK_BYTES + 16 * tid;
-  const int64_t nb = w.nb;
-  const uint64_t* dm = clear_dm ? nullptr : docmask;
-  uint8_t b[16];
-  if (p0 + 16 <= nb && ((uintptr_t)(w.text + p0) & 15) == 0) {
-    const uint4 v = *reinterpret_cast<const uint4*>(w.text + p0);
-    const uint32_t x[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int k = 0; k < 16; ++k) b[k] = (uint8_t)(x[k >> 2] >> (8 * (k & 3)));
-  } else {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) b[k] = p0 + k < nb ? w.text[p0 + k] : 0;
-  }
-  uint32_t m16 = 0;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t p = p0 + k;
-    if (p < nb && gate_hit(a, b[k])) {
-      const uint32_t lit = longest_at(a, w.text, nb, dm, p);
-      if (lit) {
-        m16 |= 1u << k;
-        w.litm[p] = lit - 1;
-      }
-    }
-  }
-  // the four 16-bit pieces of each 64-byte word
-  const uint32_t m1 = __shfl_down(m16, 1), m2 = __shfl_down(m16, 2),
-                 m3 = __shfl_down(m16, 3);
-  if ((tid & 3) == 0) {
-    const int64_t wd = p0 >> 6;
-    if (wd < nwords) {
-      w.cand[wd] = (uint64_t)m16 | ((uint64_t)m1 << 16) |
-                   ((uint64_t)m2 << 32) | ((uint64_t)m3 << 48);
-      w.lits[wd] = 0;
-      w.litb[wd] = 0;
-      if (clear_dm) docmask[wd] = 0;
-    }
-  }
-}
+// L: the edge table and the literal lengths are read from the block's LDS
+// copies (one code path per case, so no pointer mixes LDS and HBM: such a
+// pointer makes flat loads, which wait for every memory operation in
+// flight).
+template <bool L>
+struct Block {
+  const DevAdded& a;
+  const uint8_t* text;
+  int64_t nb;
+  const uint64_t* dm;       // document starts (batch) or nullptr
+  const uint16_t* scand;    // staged candidates [s0, s0 + AD_CAND): lit + 1
+  const uint8_t* slen;      // literal lengths (LDS copy when L)
+  int64_t s0;
 
-// A candidate that no earlier candidate can cover is chosen whatever was
-// chosen before it: true when every candidate j in [p - lmax + 1, p) ends
-// (j + its length) at or before p.
-__device__ bool certain(const DevAdded& a, const DevWork& w, int64_t p) {
-  const int64_t lo = p - (int64_t)a.lmax + 1 > 0 ? p - (int64_t)a.lmax + 1 : 0;
-  for (int64_t wd = lo >> 6; wd <= (p >> 6); ++wd) {
-    uint64_t m = w.cand[wd];
-    if (wd == (p >> 6)) m &= (1ULL << (p & 63)) - 1;      // below p
-    if (wd == (lo >> 6)) m &= ~((1ULL << (lo & 63)) - 1);  // from lo
-    while (m) {
-      const int64_t j = wd * 64 + __builtin_ctzll(m);
-      m &= m - 1;
-      if (j + (int64_t)a.len[w.litm[j]] > p) return false;
+  // literal + 1 of the candidate at q, 0 for none
+  __device__ __forceinline__ uint32_t cand(int64_t q) const {
+    if (q < 0) return 0;
+    const int64_t j = q - s0;
+    if ((uint64_t)j < (uint64_t)AD_CAND) return scand[j];
+    return q < nb ? trie_match(a, text, 0, nb, dm, 0, a.tab, q) & 0xFFFF : 0;
+  }
+  __device__ __forceinline__ int64_t len(uint32_t c) const {
+    return L ? slen[c - 1] : a.len[c - 1];
+  }
+  // no candidate in [q - lmax + 1, q) reaches past q
+  __device__ bool certain(int64_t q) const {
+    for (int64_t j = q - 1; j > q - (int64_t)a.lmax && j >= 0; --j) {
+      const uint32_t c = cand(j);
+      if (c && j + len(c) > q) return false;
     }
+    return true;
   }
-  return true;
-}
-
-// first candidate in (p, hi), or -1
-__device__ int64_t next_cand(const uint64_t* cand, int64_t p, int64_t hi,
-                             int64_t nwords) {
-  for (int64_t wd = (p + 1) >> 6; wd < nwords && wd * 64 < hi; ++wd) {
-    uint64_t m = cand[wd];
-    if (wd == ((p + 1) >> 6)) m &= ~((1ULL << ((p + 1) & 63)) - 1);
-    if (m) {
-      const int64_t q = wd * 64 + __builtin_ctzll(m);
-      return q < hi ? q : -1;
-    }
-  }
-  return -1;
-}
-
-__device__ void choose(const DevAdded& a, const DevWork& w, uint64_t* docmask,
-                       int64_t s) {
-  const uint32_t lit = w.litm[s];
-  const int64_t e = s + a.len[lit];
-  atomicOr((unsigned long long*)&docmask[s >> 6], 1ULL << (s & 63));
-  if (e < w.nb)
-    atomicOr((unsigned long long*)&docmask[e >> 6], 1ULL << (e & 63));
-  atomicOr((unsigned long long*)&w.lits[s >> 6], 1ULL << (s & 63));
-  for (int64_t q = s + 1; q < e;) {  // litb: bits s+1 .. e-1, word by word
-    const int64_t wd = q >> 6, hi = (wd + 1) * 64 < e ? (wd + 1) * 64 : e;
-    const int lo_b = (int)(q & 63), n = (int)(hi - q);
-    const uint64_t m = n >= 64 ? ~0ULL : (((1ULL << n) - 1) << lo_b);
-    atomicOr((unsigned long long*)&w.litb[wd], m);
-    q = hi;
-  }
-  w.tok[s] = a.id[lit];
-  for (int64_t q = s + 1; q < e; ++q) w.tok[q] = INVALID_ID;
-  atomicAdd(w.nlit, 1u);
-}
-
-// One thread per mask word. Each certain candidate in the word is chosen,
-// and its thread walks on through the candidates after it, each within
-// lmax - 1 bytes of the one before, up to the next certain one: a candidate
-// there is chosen when it starts at or after the end of the last choice (a
-// literal chosen before the certain candidate cannot reach past it, or the
-// candidate would not be certain). Every walk is finite: candidates only
-// grow along it.
-__global__ __launch_bounds__(256) void k_added_select(DevAdded a, DevWork w,
-                                                      uint64_t* docmask,
-                                                      int64_t nwords) {
-  const int64_t wd = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (wd >= nwords) return;
-  uint64_t m = w.cand[wd];
-  const int64_t L = a.lmax;
-  while (m) {
-    const int64_t p = wd * 64 + __builtin_ctzll(m);
-    m &= m - 1;
-    if (!certain(a, w, p)) continue;
-    choose(a, w, docmask, p);
-    int64_t cover = p + a.len[w.litm[p]], prev = p;
+  // is candidate p chosen?
+  __device__ bool chosen(int64_t p) const {
+    if (certain(p)) return true;
+    // p is reached by an earlier candidate, so each step back finds one
+    // within lmax - 1 bytes, until a certain one
+    int64_t h = p;
     for (;;) {
-      // a candidate lmax or more bytes after the last one is certain
-      const int64_t q = next_cand(w.cand, prev, prev + L, nwords);
-      if (q < 0 || certain(a, w, q)) break;
-      if (q >= cover) {
-        choose(a, w, docmask, q);
-        cover = q + a.len[w.litm[q]];
+      int64_t j = h - 1;
+      while (j >= 0 && !cand(j)) --j;
+      if (j < 0) return true;  // (cannot happen: h is reached by one)
+      h = j;
+      if (certain(h)) break;
+    }
+    int64_t cover = h + len(cand(h));
+    for (int64_t q = h + 1; q < p; ++q) {
+      const uint32_t c = cand(q);
+      if (c && q >= cover) cover = q + len(c);
+    }
+    return p >= cover;
+  }
+};
+
+__device__ __forceinline__ void set_bits(unsigned long long* words, int64_t from,
+                                         int64_t lo, int64_t hi) {
+  // bits [lo, hi) of the block whose first byte is `from` (clipped to it)
+  if (lo < from) lo = from;
+  if (hi > from + ADDED_BLOCK_BYTES) hi = from + ADDED_BLOCK_BYTES;
+  while (lo < hi) {
+    const int k = (int)((lo - from) >> 6);
+    const int64_t end = from + 64 * (k + 1) < hi ? from + 64 * (k + 1) : hi;
+    const int b0 = (int)((lo - from) & 63), n = (int)(end - lo);
+    atomicOr(&words[k], n >= 64 ? ~0ULL : (((1ULL << n) - 1) << b0));
+    lo = end;
+  }
+}
+
+template <bool L>
+__global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
+                                               const uint64_t* host_dm,
+                                               uint64_t* docmask,
+                                               int64_t nwords) {
+  __shared__ __align__(16) uint8_t sx[AD_STAGE];
+  __shared__ uint64_t stab[ADDED_TAB_LDS];
+  __shared__ uint16_t scand[AD_CAND];
+  __shared__ uint8_t slen_l[ADDED_LEN_LDS];
+  __shared__ unsigned long long sdm[64], slits[64], slitb[64];
+  __shared__ uint64_t shdm[AD_STAGE / 64];  // caller's document starts
+  __shared__ uint32_t scount;
+  const int tid = threadIdx.x;
+  const int64_t B = (int64_t)blockIdx.x * ADDED_BLOCK_BYTES;
+  const int64_t s0 = B - AD_BACK, nb = w.nb;
+  int hit = 0;
+  for (int j = tid; j < AD_STAGE / 16; j += 256) {
+    const int64_t p = s0 + 16 * j;
+    uint4 v;
+    if (p >= 0 && p + 16 <= nb && ((uintptr_t)(w.text + p) & 15) == 0) {
+      v = *reinterpret_cast<const uint4*>(w.text + p);
+    } else {
+      uint32_t x[4] = {0, 0, 0, 0};
+      for (int k = 0; k < 16; ++k) {
+        const int64_t q = p + k;
+        if (q >= 0 && q < nb) x[k >> 2] |= (uint32_t)w.text[q] << (8 * (k & 3));
       }
-      prev = q;
+      v = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+    *reinterpret_cast<uint4*>(sx + 16 * j) = v;
+    // a first byte of some literal in the candidate range
+    if (16 * j < AD_CAND) {
+      const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+      for (int k = 0; k < 16; ++k) {
+        const int64_t q = p + k;
+        hit |= (int)gate_hit(a, (x[k >> 2] >> (8 * (k & 3))) & 0xFF) &
+               (q >= 0 && q < nb);
+      }
     }
   }
+  if (tid < 64) sdm[tid] = slits[tid] = slitb[tid] = 0;
+  if (tid == 0) scount = 0;
+  const int64_t w0 = s0 >> 6;  // s0 is a multiple of 64
+  if (host_dm && tid < AD_STAGE / 64) {
+    const int64_t wd = w0 + tid;
+    shdm[tid] = (wd >= 0 && wd < nwords) ? host_dm[wd] : 0;
+  }
+  const bool any = __syncthreads_or(hit) != 0;
+  if (any) {
+    if (L) {
+      for (uint32_t k = tid; k < a.tab_size; k += 256) stab[k] = a.tab[k];
+      for (uint32_t k = tid; k < a.n; k += 256) slen_l[k] = a.len[k];
+    }
+    __syncthreads();
+    for (int j = tid; j < AD_CAND; j += 256) {
+      const int64_t p = s0 + j;
+      uint16_t c = 0;
+      if (p >= 0 && p < nb) {
+        if (host_dm)
+          c = (uint16_t)trie_match(a, sx, s0, nb, shdm, w0, L ? stab : a.tab, p);
+        else
+          c = (uint16_t)trie_match(a, sx, s0, nb, nullptr, 0, L ? stab : a.tab, p);
+      }
+      scand[j] = c;
+    }
+    __syncthreads();
+    const Block<L> blk{a, w.text, nb, host_dm, scand, slen_l, s0};
+    // every candidate whose literal, or the document start just past it,
+    // falls on the block's bytes
+    uint32_t mine = 0;
+    for (int j = AD_BACK - ADDED_MAX_LEN + tid; j < AD_CAND; j += 256) {
+      const uint32_t c = scand[j];
+      if (!c) continue;
+      const int64_t s = s0 + j, e = s + blk.len(c);
+      if (e < B || !blk.chosen(s)) continue;
+      set_bits(sdm, B, s, s + 1);
+      if (e < nb) set_bits(sdm, B, e, e + 1);
+      set_bits(slits, B, s, s + 1);
+      set_bits(slitb, B, s + 1, e);
+      if (s >= B) {
+        w.tok[s] = a.id[c - 1];
+        for (int64_t q = s + 1; q < e; ++q) w.tok[q] = INVALID_ID;
+        ++mine;
+      }
+    }
+    if (mine) atomicAdd(&scount, mine);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int64_t wd = (B >> 6) + tid;
+    if (wd < nwords) {
+      docmask[wd] = (host_dm ? host_dm[wd] : 0ULL) | sdm[tid];
+      w.lits[wd] = slits[tid];
+      w.litb[wd] = slitb[tid];
+    }
+  }
+  if (tid == 0 && scount) atomicAdd(w.nlit, scount);
 }
 
 }  // namespace
 
-hipError_t launch_added(const DevAdded& a, const DevWork& w, bool clear_docmask,
-                        hipStream_t s, hipEvent_t start) {
-  const int64_t nwords = (w.nb + 63) / 64 + 2;  // the words k_pretok reads
+hipError_t launch_added(const DevAdded& a, const DevWork& w,
+                        const uint64_t* host_dm, hipStream_t s,
+                        hipEvent_t start) {
+  // the words k_pretok reads; the caller's mask holds nb / 64 + 2 of them
+  const int64_t nwords = (w.nb + 63) / 64 + 2;
   uint64_t* dm = const_cast<uint64_t*>(w.docmask);
-  const uint32_t gf = (uint32_t)((nwords * 64 + ADDED_BLOCK_BYTES - 1) / ADDED_BLOCK_BYTES);
+  const uint32_t g = (uint32_t)((nwords * 64 + ADDED_BLOCK_BYTES - 1) / ADDED_BLOCK_BYTES);
+  const bool lds = a.tab_size <= (uint32_t)ADDED_TAB_LDS &&
+                   a.n <= (uint32_t)ADDED_LEN_LDS;
+  auto k = lds ? k_added<true> : k_added<false>;
   if (start)
-    hipExtLaunchKernelGGL(k_added_find, dim3(gf), dim3(256), 0, s, start,
-                          nullptr, 0, a, w, dm, clear_docmask ? 1 : 0, nwords);
+    hipExtLaunchKernelGGL(k, dim3(g), dim3(256), 0, s, start, nullptr, 0,
+                          a, w, host_dm, dm, nwords);
   else
-    hipLaunchKernelGGL(k_added_find, dim3(gf), dim3(256), 0, s, a, w, dm,
-                       clear_docmask ? 1 : 0, nwords);
-  const uint32_t gs = (uint32_t)((nwords + 255) / 256);
-  hipLaunchKernelGGL(k_added_select, dim3(gs), dim3(256), 0, s, a, w, dm, nwords);
+    hipLaunchKernelGGL(k, dim3(g), dim3(256), 0, s, a, w, host_dm, dm, nwords);
   return hipGetLastError();
 }
 

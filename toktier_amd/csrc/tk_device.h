@@ -124,8 +124,6 @@ struct DevWork {
   // starts; its bytes form no piece, and its id is written at tok[s]
   uint64_t* lits;
   uint64_t* litb;
-  uint64_t* cand;        // literal matches: bit per byte where one starts
-  uint32_t* litm;        // per byte: the longest literal matching there
   uint32_t* nlit;        // literals extracted (ctrl)
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
@@ -146,21 +144,33 @@ constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
               GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_NLIT = 7,
               GATE_WORDS = 8;
 
-// Added-token literals on the device: a trie over their bytes. Node v has
-// edges [first, first + n) of the edge array, sorted by byte, each edge
-// child << 8 | byte; term is the literal that ends at v plus one (0: none).
-// Node 0 is the root. gate: the literals' first bytes (bit b of word b/64).
+// Added-token literals on the device: the trie over their bytes, stored as
+// one hash table of its edges. Slot = key << 36 | child << 16 | term, key =
+// parent node << 8 | byte (node 0 is the root), term = the literal ending
+// at the child plus one (0: none); an empty slot is all ones (no node
+// reaches 2^20 - 1). A key's first slot is (hash(key) * size) >> 32, then
+// the next ones in order, wrapping (the table is at most two thirds full).
 struct DevAdded {
-  const uint2* nodes;     // {first edge, n | term << 9}
-  const uint32_t* edges;  // child << 8 | byte
-  const uint32_t* len;    // literal bytes
+  const uint64_t* tab;    // trie edges
+  uint32_t tab_size;      // slots
+  const uint8_t* len;     // literal bytes
   const uint32_t* id;     // literal token id
-  uint64_t gate[4];
+  uint64_t gate[4];       // the literals' first bytes (bit b of word b/64)
   uint32_t lmax;          // longest literal, bytes (1..255)
   uint32_t n;             // literals
 };
 constexpr int ADDED_MAX_LEN = 255;
-constexpr int ADDED_BLOCK_BYTES = 4096;  // k_added_find: 16 bytes per thread
+constexpr int ADDED_MAX_LITERALS = 65535;
+constexpr uint32_t ADDED_MAX_NODES = (1u << 20) - 2;
+constexpr int ADDED_BLOCK_BYTES = 4096;  // bytes (64 mask words) per block
+// tables up to these sizes are copied to LDS by the blocks that see a
+// literal's first byte (larger ones are read from HBM)
+constexpr int ADDED_TAB_LDS = 1536;   // edge slots (12 KiB)
+constexpr int ADDED_LEN_LDS = 1024;   // literal lengths
+__host__ __device__ __forceinline__ uint32_t added_slot(uint32_t key,
+                                                        uint32_t size) {
+  return (uint32_t)(((uint64_t)(key * 0x9E3779B1u) * size) >> 32);
+}
 // packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
 constexpr int PACK_BLOCKS = 2048;
 // slots (lanes per piece) of the length classes, and the shortest piece of
@@ -238,10 +248,12 @@ hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
 hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
-// k_added_find + k_added_select: the literal split of the request (the
-// document-start mask is cleared first unless the caller marked documents)
-hipError_t launch_added(const DevAdded& a, const DevWork& w, bool clear_docmask,
-                        hipStream_t s, hipEvent_t start = nullptr);
+// k_added: the literal split of the request into w.docmask (read-write;
+// the document starts the caller marked, if any, are read from host_dm, a
+// different buffer, and kept)
+hipError_t launch_added(const DevAdded& a, const DevWork& w,
+                        const uint64_t* host_dm, hipStream_t s,
+                        hipEvent_t start = nullptr);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);

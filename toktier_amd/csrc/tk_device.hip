@@ -36,6 +36,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 namespace tk {
 
 constexpr uint8_t CP_ = 0, CL_ = 1, CN_ = 2, CS_ = 3;
@@ -254,7 +256,10 @@ struct GCtx {
 
   __device__ __forceinline__ bool ds(int64_t i) const {
     if (i == 0) return true;
-    return dm && ((dm[i >> 6] >> (i & 63)) & 1);
+    // read as a 32-bit half: a load the compiler cannot merge with the
+    // 64-bit reads of the staged words (that merge makes a flat load, which
+    // waits for every memory operation in flight)
+    return dm && ((reinterpret_cast<const uint32_t*>(dm)[i >> 5] >> (i & 31)) & 1);
   }
   __device__ __forceinline__ int32_t cp_at(int64_t i, bool* ok) const {
     const int64_t a = nb - i;
@@ -584,7 +589,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   // the first 256 code points' class and NFC values, and the byte ids:
   // LDS copies for the common case (one entry per thread)
   static_assert(PRETOK_TPB == 256, "one table entry per thread");
-  __shared__ uint8_t lcls[256], lnfc[256];
+  // (32-bit entries, so the compiler keeps the LDS and HBM table reads
+  // apart instead of merging them into one flat load)
+  __shared__ uint32_t lcls[256], lnfc[256];
   __shared__ int32_t lbid[256];
   __shared__ uint32_t loff[PACK_CLASSES];  // class regions of plocal
   const int tid = threadIdx.x;
@@ -704,7 +711,6 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   const LCtx c{GCtx{w.text, nb, DM ? w.docmask : nullptr, t.cls}, se, lo, sdm, wlo};
   // document start at local offset L: position 0, or a marked doc head
   const int Lz = lo <= 0 ? (int)(-lo) : -1;
-  auto ds = [&](int L) { return dm ? c.ds(lo + L) : L == Lz; };
   auto prv = [&](int L) {  // local offset of the character before L
     return L - 1 - (int)((se[L - 1] >> 23) & 3);
   };
@@ -712,146 +718,176 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   uint32_t st = 0;
   // the tile's words, and the first word after it (the next block writes
   // that one; it is recomputed here to size the pieces near the tile end)
-  for (int k = wv; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
-    const int64_t wd = (base >> 6) + k;
-    if (wd >= nwords) {  // past the sentinel words: all starts
-      if (lane == 0) sw[k] = ~0ULL;
-      continue;
-    }
-    const int64_t i = base + 64 * k + lane;
-    const int Li = PT_HALO + 64 * k + lane;  // i - lo
-    const int sj = 64 * k + lane + PT_PAD;
-    // ASCII byte kinds across the word (bytes past the text are 0): the
-    // run-level cases below read them instead of walking the run
-    const uint32_t bb = sb[sj];
-    const uint64_t mWS = __ballot(bb == ' ' || bb == '\t' || bb == 0x0B || bb == 0x0C);
-    const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
-    const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
-    const uint64_t mHI = __ballot(bb >= 0x80);
-    // Every lane evaluates the fast predicate from the fixed context (only
-    // selects); the lanes it leaves open (runs to walk, the general path)
-    // are resolved in a section the wave enters only when it has any.
-    const bool in = i < nb;
-    const bool lead = in && !is_cont((uint8_t)bb);
-    // the entry's valid bit: a lead that decodes, or a continuation byte
-    // that a lead claims
-    const uint32_t e = se[Li];
-    if (in && !((e >> 27) & 1)) st |= ST_UTF8;
-    const bool d0 = ds(Li);
-    // the fixed context: every offset used lies in the LDS span (tile
-    // positions are at least PT_HALO from either end, and the four
-    // characters back cover at most 16 bytes); the one after is checked
-    Ctx5 x;
-    x.c0 = e;
-    const int L1 = prv(Li);
-    x.c1 = se[L1];
-    x.h2 = !ds(L1);
-    const int L2 = x.h2 ? prv(L1) : L1;
-    x.c2 = se[L2];
-    x.h3 = x.h2 && !ds(L2);
-    const int L3 = x.h3 ? prv(L2) : L2;
-    x.c3 = se[L3];
-    x.h4 = x.h3 && !ds(L3);
-    const int L4 = x.h4 ? prv(L3) : L3;
-    x.c4 = se[L4];
-    const int Ln = Li + 1 + (int)((e >> 25) & 3);
-    const bool nin = Ln < PT_SPAN;
-    x.hn = lo + Ln < nb && !ds(Ln);
-    x.cn = nin ? se[Ln] : 0u;
-    int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
-    const bool open = lead && !d0 && r < 0;
-    if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
-      if (open) {
-        const uint64_t below = (1ULL << lane) - 1;
-        if (r == FAST_DIGITS && !dm) {
-          // the ASCII digits before i, when the word shows where they begin
-          const uint64_t nd_ = ~mDG & below;
-          if (nd_ && !((mHI >> (63 - __builtin_clzll(nd_))) & 1))
-            r = (lane - 1 - (63 - __builtin_clzll(nd_))) % t.dmax == 0;
-        } else if (r == FAST_CRLF && !dm && bb < 0x80) {
-          // another CR/LF ahead in the run: it shows in the word before
-          // the first byte that is neither (unless that byte is not ASCII)
-          const uint64_t above = ~mask_le(lane);
-          const uint64_t stop = ~(mWS | mCR) & above;
-          const int f = stop ? __builtin_ctzll(stop) : 64;
-          const int g = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
-          if (g < f) {
-            // then the char before the CR/LF run that precedes i
-            const uint64_t nc = ~mCR & below;
-            if (nc) {
-              const int h = 63 - __builtin_clzll(nc);
-              if ((mWS >> h) & 1) r = 0;
-              else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
+  // The start words, compiled twice: with document starts in the staged
+  // mask words (D) and without (the common case, where none of the
+  // document checks is needed); a block takes one of the two.
+  auto start_words = [&](auto dflag) {
+    constexpr bool D = decltype(dflag)::value;
+    // every span position's mask word is staged (words tile - 1 .. tile +
+    // PT_TILE / 64 of the PT_DMW from tile - 3), so D reads LDS only
+    auto ds = [&](int L) {
+      if (!D) return L == Lz;
+      const int64_t i = lo + L;
+      return i == 0 || ((sdm[(i >> 6) - wlo] >> (i & 63)) & 1) != 0;
+    };
+    for (int k = wv; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
+      const int64_t wd = (base >> 6) + k;
+      if (wd >= nwords) {  // past the sentinel words: all starts
+        if (lane == 0) sw[k] = ~0ULL;
+        continue;
+      }
+      const int64_t i = base + 64 * k + lane;
+      const int Li = PT_HALO + 64 * k + lane;  // i - lo
+      const int sj = 64 * k + lane + PT_PAD;
+      // ASCII byte kinds across the word (bytes past the text are 0): the
+      // run-level cases below read them instead of walking the run
+      const uint32_t bb = sb[sj];
+      const uint64_t mWS = __ballot(bb == ' ' || bb == '\t' || bb == 0x0B || bb == 0x0C);
+      const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
+      const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
+      const uint64_t mHI = __ballot(bb >= 0x80);
+      // Every lane evaluates the fast predicate from the fixed context (only
+      // selects); the lanes it leaves open (runs to walk, the general path)
+      // are resolved in a section the wave enters only when it has any.
+      const bool in = i < nb;
+      const bool lead = in && !is_cont((uint8_t)bb);
+      // the entry's valid bit: a lead that decodes, or a continuation byte
+      // that a lead claims
+      const uint32_t e = se[Li];
+      if (in && !((e >> 27) & 1)) st |= ST_UTF8;
+      const bool d0 = ds(Li);
+      // the fixed context: every offset used lies in the LDS span (tile
+      // positions are at least PT_HALO from either end, and the four
+      // characters back cover at most 16 bytes); the one after is checked
+      Ctx5 x;
+      x.c0 = e;
+      const int L1 = prv(Li);
+      x.c1 = se[L1];
+      x.h2 = !ds(L1);
+      const int L2 = x.h2 ? prv(L1) : L1;
+      x.c2 = se[L2];
+      x.h3 = x.h2 && !ds(L2);
+      const int L3 = x.h3 ? prv(L2) : L2;
+      x.c3 = se[L3];
+      x.h4 = x.h3 && !ds(L3);
+      const int L4 = x.h4 ? prv(L3) : L3;
+      x.c4 = se[L4];
+      const int Ln = Li + 1 + (int)((e >> 25) & 3);
+      const bool nin = Ln < PT_SPAN;
+      x.hn = lo + Ln < nb && !ds(Ln);
+      x.cn = nin ? se[Ln] : 0u;
+      int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
+      const bool open = lead && !d0 && r < 0;
+      if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
+        if (open) {
+          const uint64_t below = (1ULL << lane) - 1;
+          // document starts in this word (a run ends at one, as at the
+          // text end)
+          const uint64_t dmw = D ? sdm[wd - wlo] : 0;
+          if (r == FAST_DIGITS) {
+            // the ASCII digits before i, when the word shows where they
+            // begin: after the last byte that is not one, or at a document
+            // start
+            const uint64_t nd_ = (~mDG & below) | ((dmw & below) >> 1);
+            if (nd_) {
+              const int h = 63 - __builtin_clzll(nd_);
+              if (((dmw >> (h + 1)) & 1) || !((mHI >> h) & 1))
+                r = (lane - 1 - h) % t.dmax == 0;
             }
-          } else if (f < 64 && !((mHI >> f) & 1)) {
-            r = 1;
+          } else if (r == FAST_CRLF && bb < 0x80) {
+            // another CR/LF ahead in the run: it shows in the word before
+            // the first byte that is neither (unless that byte is not
+            // ASCII) and before the next document start
+            const uint64_t above = ~mask_le(lane);
+            const uint64_t stop = ~(mWS | mCR) & above;
+            const int f = stop ? __builtin_ctzll(stop) : 64;
+            const int fd = (dmw & above) ? __builtin_ctzll(dmw & above) : 64;
+            const int g = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
+            if (g < f && g < fd) {
+              // then the char before the CR/LF run that precedes i (none
+              // when a document starts inside that run)
+              const uint64_t nc = ~mCR & below;
+              const int h = nc ? 63 - __builtin_clzll(nc) : -1;
+              if (dmw & lanes_in(h + 1, lane)) {
+                r = 0;
+              } else if (h >= 0) {
+                if ((mWS >> h) & 1) r = 0;
+                else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
+              }
+            } else if (fd < 64 && fd <= f) {
+              r = 1;
+            } else if (f < 64 && !((mHI >> f) & 1)) {
+              r = 1;
+            }
           }
-        }
-        if (r == FAST_DIGITS) {
-          // \p{N}{1,K}: count the digits before i inside the span
-          int L = L3, nd = 3;
-          r = -1;
-          for (;;) {
-            if (ds(L)) { r = nd % t.dmax == 0; break; }
-            if (L - 1 < 0) break;  // past the span: general path
-            const int Lr = prv(L);
-            if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
-            ++nd;
-            L = Lr;
-          }
-        } else if (r == FAST_CRLF) {
-          // end of \s*[\r\n]+ unless another CR/LF follows in the run;
-          // then the first char the P match's [\r\n]* left over
-          r = -1;
-          bool more = false, known = false;
-          for (int L = Ln;;) {
-            if (lo + L >= nb || ds(L)) { known = true; break; }
-            if (L >= PT_SPAN) break;
-            const uint32_t eq = se[L];
-            if (ecl(eq) != CS_) { known = true; break; }
-            if (crlf(ecp(eq))) { more = known = true; break; }
-            L += 1 + (int)((eq >> 25) & 3);
-          }
-          if (known && !more) r = 1;
-          if (known && more) {
-            for (int L = L1;;) {
-              if (ds(L)) { r = 0; break; }
-              if (L - 1 < 0) break;
+          if (r == FAST_DIGITS) {
+            // \p{N}{1,K}: count the digits before i inside the span
+            int L = L3, nd = 3;
+            r = -1;
+            for (;;) {
+              if (ds(L)) { r = nd % t.dmax == 0; break; }
+              if (L - 1 < 0) break;  // past the span: general path
               const int Lr = prv(L);
-              const uint32_t ex = se[Lr];
-              if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
-              if (!crlf(ecp(ex))) { r = 0; break; }
+              if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
+              ++nd;
               L = Lr;
             }
+          } else if (r == FAST_CRLF) {
+            // end of \s*[\r\n]+ unless another CR/LF follows in the run;
+            // then the first char the P match's [\r\n]* left over
+            r = -1;
+            bool more = false, known = false;
+            for (int L = Ln;;) {
+              if (lo + L >= nb || ds(L)) { known = true; break; }
+              if (L >= PT_SPAN) break;
+              const uint32_t eq = se[L];
+              if (ecl(eq) != CS_) { known = true; break; }
+              if (crlf(ecp(eq))) { more = known = true; break; }
+              L += 1 + (int)((eq >> 25) & 3);
+            }
+            if (known && !more) r = 1;
+            if (known && more) {
+              for (int L = L1;;) {
+                if (ds(L)) { r = 0; break; }
+                if (L - 1 < 0) break;
+                const int Lr = prv(L);
+                const uint32_t ex = se[Lr];
+                if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
+                if (!crlf(ecp(ex))) { r = 0; break; }
+                L = Lr;
+              }
+            }
+          }
+          if (r < 0) {
+            const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+            r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
           }
         }
-        if (r < 0) {
-          const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
-          r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
+      }
+      // sentinel starts past the text; no start inside a character
+      const bool s = !in || (lead && (d0 || r != 0));
+      if (w.check_nfc && lead) {
+        const uint32_t cp = e & 0x1FFFFF;
+        const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
+        if (v == 255) {
+          st |= ST_NFC;
+        } else if (v != 0 && !d0) {
+          const uint32_t pc = x.c1 & 0x1FFFFF;
+          if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
         }
       }
-    }
-    // sentinel starts past the text; no start inside a character
-    const bool s = !in || (lead && (d0 || r != 0));
-    if (w.check_nfc && lead) {
-      const uint32_t cp = e & 0x1FFFFF;
-      const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
-      if (v == 255) {
-        st |= ST_NFC;
-      } else if (v != 0 && !d0) {
-        const uint32_t pc = x.c1 & 0x1FFFFF;
-        if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
+      uint64_t m = __ballot(s);
+      // no start inside an added-token literal (its first byte is a document
+      // start already)
+      if (DM && w.litb) m &= ~w.litb[wd];
+      if (lane == 0) {
+        sw[k] = m;
+        if (k < PT_TILE / 64) w.starts[wd] = m;
       }
     }
-    uint64_t m = __ballot(s);
-    // no start inside an added-token literal (its first byte is a document
-    // start already)
-    if (DM && w.litb) m &= ~w.litb[wd];
-    if (lane == 0) {
-      sw[k] = m;
-      if (k < PT_TILE / 64) w.starts[wd] = m;
-    }
-  }
+  };
+  if (DM && dm) start_words(std::true_type{});
+  else start_words(std::false_type{});
   if (st) atomicOr(w.status, st);
   __syncthreads();
   // Stage-2 bookkeeping for the pieces that start in this tile: finish the

@@ -186,9 +186,10 @@ struct tk_engine {
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
   DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk, plocal;
   // added-token literals (tk_engine_set_added) and their per-call masks
-  DevBuf<uint2> lit_nodes;
-  DevBuf<uint32_t> lit_edges, lit_len, lit_id, litm;
-  DevBuf<uint64_t> lits, litb, cand;
+  DevBuf<uint64_t> lit_tab;
+  DevBuf<uint8_t> lit_len;
+  DevBuf<uint32_t> lit_id;
+  DevBuf<uint64_t> lits, litb, docmask_lit;
   tk::DevAdded added{};
   uint64_t last_literals = 0;
   size_t docs_cap = 0;
@@ -277,12 +278,11 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->plocal.alloc((size_t)tk::PT_LOCAL_SLOTS * tk::pretok_tiles((int64_t)need)));
     e->cap = need;
   }
-  if (e->added.n && e->litm.n < e->cap + 64) {
+  if (e->added.n && e->lits.n < e->cap / 64 + 8) {
     const size_t words = e->cap / 64 + 8;
     HIP_TRY(e->lits.alloc(words));
     HIP_TRY(e->litb.alloc(words));
-    HIP_TRY(e->cand.alloc(words));
-    HIP_TRY(e->litm.alloc(e->cap + 64));
+    HIP_TRY(e->docmask_lit.alloc(words));
   }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
@@ -341,8 +341,6 @@ tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
   w.nlit = ctrl + tk::CTRL_NLIT;
   w.lits = literals ? e->lits.p : nullptr;
   w.litb = literals ? e->litb.p : nullptr;
-  w.cand = literals ? e->cand.p : nullptr;
-  w.litm = literals ? e->litm.p : nullptr;
   w.clear_words = (int64_t)(nb / 64 + 4);
   w.clear_dwords = w.clear_words / 64 + 2;
   return w;
@@ -390,17 +388,17 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 // (host-driven passes, each removing the failed cuts) until every cut holds.
 // Nothing is cleared from the host: k_pretok clears the per-call masks and
 // the control slot of the next call, so the stages run back to back.
-// Added-token literals (literals == true): k_added_find / k_added_select
-// split the request first; the split marks document starts, so k_pretok
-// runs its document-mask instance (on e->docmask, cleared by k_added_find,
-// when the caller marked no documents).
+// Added-token literals (literals == true): k_added splits the request
+// first; the split marks document starts, so k_pretok runs its
+// document-mask instance, on a mask k_added writes whole (e->docmask_lit:
+// the caller's document starts, if any, are read from d_docmask and kept).
 int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
                  const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
                  uint32_t* out, size_t out_cap, uint32_t* status,
                  uint32_t* total, bool literals = false) {
   ++e->seq;
-  const bool own_mask = literals && d_docmask == nullptr;
-  if (own_mask) d_docmask = e->docmask.p;
+  const uint64_t* host_dm = d_docmask;
+  if (literals) d_docmask = e->docmask_lit.p;
   const tk::DevWork w =
       make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap, literals);
   uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
@@ -416,7 +414,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   const bool stages = e->timing == 1, packonly = e->timing == 2;
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
   if (literals) {
-    HIP_TRY(tk::launch_added(e->added, w, own_mask, s, at(0)));
+    HIP_TRY(tk::launch_added(e->added, w, host_dm, s, at(0)));
     HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, nullptr));
   } else {
     HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
@@ -807,7 +805,9 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
   std::lock_guard<std::mutex> lk(e->mu);
   if (n > 0 && (!contents || !offsets || !ids || !flags))
     return fail(TK_E_INVALID_ARG, "null argument");
-  if (n > 65536) return fail(TK_E_UNSUPPORTED, "%zu added tokens (at most 65536)", n);
+  if (n > (size_t)tk::ADDED_MAX_LITERALS)
+    return fail(TK_E_UNSUPPORTED, "%zu added tokens (at most %d)", n,
+                tk::ADDED_MAX_LITERALS);
   std::vector<std::string> raw, norm;
   for (size_t k = 0; k < n; ++k) {
     if (offsets[k + 1] < offsets[k])
@@ -840,12 +840,13 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
       if (can_overlap(x, y) || can_overlap(y, x))
         return fail(TK_E_UNSUPPORTED,
                     "a raw and a normalized added token can overlap");
-  // trie: node 0 is the root; children kept sorted by byte
+  // trie: node 0 is the root
   std::vector<std::map<uint8_t, uint32_t>> kids(1);
   std::vector<uint32_t> term(1, 0);
   uint32_t lmax = 0;
   uint64_t gate[4] = {0, 0, 0, 0};
-  std::vector<uint32_t> len(n), idv(n);
+  std::vector<uint32_t> idv(n);
+  std::vector<uint8_t> lens(n);
   for (size_t k = 0; k < n; ++k) {
     const uint8_t* c = contents + offsets[k];
     const uint32_t L = (uint32_t)(offsets[k + 1] - offsets[k]);
@@ -864,20 +865,24 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
     }
     if (term[v]) return fail(TK_E_INVALID_ARG, "added token %zu is a duplicate", k);
     term[v] = (uint32_t)k + 1;
-    len[k] = L;
     idv[k] = ids[k];
+    lens[k] = (uint8_t)L;
     lmax = std::max(lmax, L);
     gate[c[0] >> 6] |= 1ULL << (c[0] & 63);
   }
-  if (kids.size() >= (1u << 24))
-    return fail(TK_E_UNSUPPORTED, "added-token trie over 2^24 nodes");
-  std::vector<uint2> nodes(kids.size());
-  std::vector<uint32_t> edges;
-  for (size_t v = 0; v < kids.size(); ++v) {
-    nodes[v].x = (uint32_t)edges.size();
-    nodes[v].y = (uint32_t)kids[v].size() | (term[v] << 9);
-    for (const auto& kv : kids[v]) edges.push_back((kv.second << 8) | kv.first);
-  }
+  if (kids.size() > tk::ADDED_MAX_NODES)
+    return fail(TK_E_UNSUPPORTED, "added-token trie over %u nodes", tk::ADDED_MAX_NODES);
+  // the edges in a hash table at most two thirds full (tk_device.h)
+  size_t n_edges = kids.size() - 1;
+  const uint32_t size = (uint32_t)std::max<size_t>(64, (3 * n_edges + 1) / 2 + 1);
+  std::vector<uint64_t> tab(size, ~0ULL);
+  for (size_t v = 0; v < kids.size(); ++v)
+    for (const auto& kv : kids[v]) {
+      const uint32_t key = ((uint32_t)v << 8) | kv.first, child = kv.second;
+      uint32_t i = tk::added_slot(key, size);
+      while (tab[i] != ~0ULL) i = i + 1 == size ? 0 : i + 1;
+      tab[i] = ((uint64_t)key << 36) | ((uint64_t)child << 16) | term[child];
+    }
   HIP_TRY(hipSetDevice(e->device));
   HIP_TRY(hipStreamSynchronize(e->stream));
   e->added = tk::DevAdded{};
@@ -890,13 +895,12 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
     return TK_OK;
   };
   int rc;
-  if ((rc = up(e->lit_nodes, nodes)) != TK_OK) return rc;
-  if ((rc = up(e->lit_edges, edges)) != TK_OK) return rc;
-  if ((rc = up(e->lit_len, len)) != TK_OK) return rc;
+  if ((rc = up(e->lit_tab, tab)) != TK_OK) return rc;
+  if ((rc = up(e->lit_len, lens)) != TK_OK) return rc;
   if ((rc = up(e->lit_id, idv)) != TK_OK) return rc;
   tk::DevAdded a{};
-  a.nodes = e->lit_nodes.p;
-  a.edges = e->lit_edges.p;
+  a.tab = e->lit_tab.p;
+  a.tab_size = size;
   a.len = e->lit_len.p;
   a.id = e->lit_id.p;
   for (int k = 0; k < 4; ++k) a.gate[k] = gate[k];
@@ -905,7 +909,6 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
   e->added = a;
   // the per-call masks follow the workspace capacity
   if (e->cap) {
-    e->litm.reset();
     rc = ensure_workspace(e, e->cap, 0);
     if (rc != TK_OK) return rc;
   }
@@ -997,7 +1000,7 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   if (rc != TK_OK) return rc;
   hipStream_t s = e->stream;
   // forced piece starts at every document head (gpu.rs:644-652)
-  std::vector<uint64_t> mask(nb / 64 + 2, 0);
+  std::vector<uint64_t> mask((nb + 63) / 64 + 2, 0);
   for (size_t d = 0; d < n_docs; ++d) {
     const uint64_t p = doc_offsets[d];
     if (p < nb) mask[p >> 6] |= 1ULL << (p & 63);
