@@ -169,6 +169,11 @@ int tk_engine_set_added(tk_engine* engine, size_t n, const uint8_t* contents,
 /* Literals extracted by the last encode on this engine. */
 int tk_engine_last_literals(const tk_engine* engine, uint64_t* n);
 
+/* HIP driver version of the engine's device (hipDriverGetVersion; the
+ * reference driver surface's driver_version(), cuda-driver lib.rs:51-86),
+ * for the route's driver floor. */
+int tk_engine_driver_version(const tk_engine* engine, int* version);
+
 const char* tk_engine_delivery(const tk_engine* engine);     /* "prebuilt" */
 const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
 

@@ -30,6 +30,51 @@ def _gpu_available() -> bool:
         return False
 
 
+_GPU_OUTCOMES = {"passed": 0, "failed": 0, "skipped": 0}
+
+
+def pytest_runtest_logreport(report):
+    """Count the outcomes of GPU parity tests (the route's evidence)."""
+    if "gpu" not in report.keywords:
+        return
+    if report.when == "call" or (report.when == "setup" and not report.passed):
+        key = ("passed" if report.passed else
+               "skipped" if report.skipped else "failed")
+        _GPU_OUTCOMES[key] += 1
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """After a run that executed GPU parity tests on a device, write the
+    evidence the gfx950 route rows are generated from
+    (``python -m toktier_amd.registry gpurun_out/gfx950_evidence.v1.json``):
+    the library's build key, the device architecture and driver, and the
+    outcome counts."""
+    if _GPU_OUTCOMES["passed"] + _GPU_OUTCOMES["failed"] == 0:
+        return
+    try:
+        import json
+        import torch
+        from toktier_amd._build import MANIFEST
+        if not torch.cuda.is_available():
+            return
+        arch = torch.cuda.get_device_properties(0).gcnArchName.split(":")[0]
+        man = json.loads(MANIFEST.read_text())
+        import toktier_amd
+        t = toktier_amd.load("gpt2")
+        driver = t.engine.driver_version
+        t.close()
+        ev = {"evidence_id": f"ev-gfx950-parity-{man['build_key'][:12]}",
+              "suite": "tests -m gpu", "build_key": man["build_key"],
+              "architecture": arch, "driver_version": driver,
+              "hip_version": torch.version.hip, **_GPU_OUTCOMES}
+        out = ROOT / "gpurun_out"
+        out.mkdir(exist_ok=True)
+        (out / "gfx950_evidence.v1.json").write_text(
+            json.dumps(ev, indent=1, sort_keys=True) + "\n")
+    except Exception as err:  # evidence is a by-product; never fail the run
+        print(f"gfx950 evidence not written: {err}")
+
+
 def pytest_collection_modifyitems(config, items):
     if _gpu_available():
         return

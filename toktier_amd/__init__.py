@@ -26,7 +26,7 @@ from pathlib import Path
 
 import numpy as np
 
-from . import bpe_tables, classes, families, standin
+from . import bpe_tables, classes, families, registry, standin
 from ._ffi import (TK_ABI_VERSION, TK_ADDED_LSTRIP, TK_ADDED_NORMALIZED,
                    TK_ADDED_RSTRIP, TK_ADDED_SINGLE_WORD, TK_ADDED_SPECIAL,
                    TK_E_NEEDS_NFC, TK_FLAG_NO_ADDED, TK_FLAG_NORMALIZED,
@@ -138,7 +138,8 @@ class Tokenizer:
     """A family's tokenizer bound to one GPU engine."""
 
     def __init__(self, family: str, tokenizer_json: str, device: int = 0,
-                 expected_architecture: str | None = "gfx950"):
+                 expected_architecture: str | None = "gfx950",
+                 policy: str = registry.POLICY_EXPERIMENTAL):
         self.family = families.family(family)
         self._json = tokenizer_json
         self.artifact_sha256 = hashlib.sha256(
@@ -175,6 +176,31 @@ class Tokenizer:
                 self.engine.close()
                 raise
         self._splitter = None
+        self.admission = self._admit(policy)
+        if not self.admission.admitted:
+            self.engine.close()
+            codes = [r.code for r in self.admission.refusals]
+            raise EngineError(
+                -1, "route admission",
+                f"the gfx950 route is not admitted under policy {policy!r}: "
+                f"{codes}")
+
+    def _admit(self, policy: str) -> "registry.Admission":
+        """The gfx950 route's admission from the committed registry rows
+        (reference planner checks, ``routing/plan.py:1-39``)."""
+        from ._build import MANIFEST
+        try:
+            reg = registry.load_registry()
+        except (OSError, ValueError):
+            reg = None
+        build_key = None
+        if MANIFEST.exists():
+            build_key = json.loads(MANIFEST.read_text()).get("build_key")
+        facts = registry.Facts(
+            library_loaded=True, build_key=build_key, build_failed=False,
+            architectures=(self.engine.architecture,),
+            driver_version=self.engine.driver_version)
+        return registry.admit(reg, self.artifact_sha256, facts, policy)
 
     # -- exact normalization for texts that fail the device quick check
     def _normalize(self, text: str) -> str:
@@ -264,6 +290,7 @@ class Tokenizer:
             "artifact_sha256": self.artifact_sha256,
             "plan": ["gpu"],
             "route": "gpu",
+            "admission": self.admission.as_dict(),
             "kernel_delivery": self.engine.delivery,
             "architectures": [self.engine.architecture],
             "code_object_sha256": manifest.get("sha256"),
@@ -286,12 +313,17 @@ class Tokenizer:
 
 
 def load(family: str, tokenizer_json: str | Path | None = None,
-         device: int = 0) -> Tokenizer:
+         device: int = 0, policy: str = registry.POLICY_EXPERIMENTAL
+         ) -> Tokenizer:
     """Open ``family`` on GPU ``device``. Without ``tokenizer_json`` the
-    committed stand-in artifact of the family is used."""
+    committed stand-in artifact of the family is used. ``policy``:
+    ``experimental`` (default) runs the gfx950 route past waivable
+    refusals and reports them in ``explain()["admission"]``;
+    ``certified`` refuses any route the registry has not certified for
+    this artifact, device and build."""
     if tokenizer_json is None:
         text = standin.load_artifact_json(family)
     else:
         p = Path(tokenizer_json)
         text = p.read_text(encoding="utf-8") if p.exists() else str(tokenizer_json)
-    return Tokenizer(family, text, device=device)
+    return Tokenizer(family, text, device=device, policy=policy)

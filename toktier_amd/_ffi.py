@@ -47,7 +47,7 @@ SYMBOLS = (
     "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
-    "tk_engine_last_literals", "tk_last_error",
+    "tk_engine_last_literals", "tk_engine_driver_version", "tk_last_error",
 )
 
 
@@ -116,6 +116,8 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_last_timing.argtypes = [vp, C.POINTER(C.c_double), C.c_int]
     L.tk_engine_set_added.restype = C.c_int
     L.tk_engine_set_added.argtypes = [vp, sz, vp, vp, vp, vp]
+    L.tk_engine_driver_version.restype = C.c_int
+    L.tk_engine_driver_version.argtypes = [vp, C.POINTER(C.c_int)]
     L.tk_engine_last_literals.restype = C.c_int
     L.tk_engine_last_literals.argtypes = [vp, C.POINTER(C.c_uint64)]
     if path is None:
@@ -222,6 +224,13 @@ class Engine:
                                           offs.ctypes.data, idv.ctypes.data,
                                           fl.ctypes.data),
               "tk_engine_set_added")
+
+    @property
+    def driver_version(self) -> int:
+        v = C.c_int()
+        check(self._L.tk_engine_driver_version(self._h, C.byref(v)),
+              "tk_engine_driver_version")
+        return int(v.value)
 
     def last_literals(self) -> int:
         n = C.c_uint64()

@@ -921,6 +921,12 @@ int tk_engine_last_literals(const tk_engine* e, uint64_t* n) {
   return TK_OK;
 }
 
+int tk_engine_driver_version(const tk_engine* e, int* version) {
+  if (!e || !version) return fail(TK_E_INVALID_ARG, "null argument");
+  HIP_TRY(hipDriverGetVersion(version));
+  return TK_OK;
+}
+
 const char* tk_engine_delivery(const tk_engine* e) { return e ? "prebuilt" : ""; }
 const char* tk_engine_architecture(const tk_engine* e) { return e ? e->arch.c_str() : ""; }
 
