@@ -206,6 +206,10 @@ struct tk_engine {
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
   hipEvent_t ev_join = nullptr;  // side stream -> engine stream
+  // pieces over WIDE_MAX bytes (cut / segment / certify) on a stream of
+  // their own, beside the 65..WIDE_MAX-byte merges of stream2
+  hipStream_t stream3 = nullptr;
+  hipEvent_t ev_join3 = nullptr;
   double last_us[5] = {};
   size_t last_passes = 0;
 };
@@ -434,17 +438,23 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   const uint32_t nlong = e->gate[tk::GATE_NLONG];
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
   if (nlong > 0) {
+    // two independent jobs on two side streams: pieces of 65..WIDE_MAX
+    // bytes merged whole, and the cut / segment / certify path of the
+    // longer ones (they touch disjoint bytes and read the same lists)
     hipStream_t s2 = e->stream2;
     HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     if (big) {
-      HIP_TRY(tk::launch_long_windows(e->t, w, s2));
-      HIP_TRY(tk::launch_long_segments(e->t, w, 1, s2));
-      HIP_TRY(tk::launch_certify(e->t, w, 1, s2, at(3)));
-    } else if (stages) {
-      HIP_TRY(hipEventRecord(ev[3], s2));
+      hipStream_t s3 = e->stream3;
+      HIP_TRY(tk::launch_long_windows(e->t, w, s3));
+      HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
+      HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
+      HIP_TRY(hipEventRecord(e->ev_join3, s3));
+      HIP_TRY(hipStreamWaitEvent(s, e->ev_join3, 0));
     }
     HIP_TRY(hipEventRecord(e->ev_join, s2));
     HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
+    // (the end of both side streams, or of the packed merge if later)
+    if (stages) HIP_TRY(hipEventRecord(ev[3], s));
   }
   HIP_TRY(tk::launch_compact(w, s, ++e->ctag, nullptr, at(4)));
   // k_scan has left the outcome in the gate words: no read-back copy
@@ -656,12 +666,15 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
     return code;
   };
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipStreamCreateWithFlags(&e->stream2, hipStreamNonBlocking) != hipSuccess)
+      hipStreamCreateWithFlags(&e->stream2, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&e->stream3, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipStreamCreateWithFlags failed"));
   // join of the side stream into the engine stream (one device): no
   // system-scope fence
   if (hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming |
-                                               hipEventDisableSystemFence) != hipSuccess)
+                                               hipEventDisableSystemFence) != hipSuccess ||
+      hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
+                                                hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
@@ -774,9 +787,12 @@ void tk_engine_close(tk_engine* e) {
   for (auto& ev : e->ev)
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream2) (void)hipStreamSynchronize(e->stream2);
+  if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
+  if (e->ev_join3) (void)hipEventDestroy(e->ev_join3);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->stream2) (void)hipStreamDestroy(e->stream2);
+  if (e->stream3) (void)hipStreamDestroy(e->stream3);
   if (e->host_ctrl) (void)hipHostFree(e->host_ctrl);
   if (e->gate) (void)hipHostFree(const_cast<uint32_t*>(e->gate));
   delete e;
