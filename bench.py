@@ -79,6 +79,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, choices=[2, 4, 5])
+    ap.add_argument("--family", default=None,
+                    help="encode the config's text with another family "
+                         "(e.g. laguna_s_2_1 on C4's code-like stream)")
     ap.add_argument("--chat", action="store_true",
                     help="lay the config's text out as chat turns in the "
                          "family's template (added-token literals, split "
@@ -113,6 +116,8 @@ def main() -> int:
     from toktier_amd import workloads
 
     fam, gen = workloads.CONFIGS[args.config]
+    if args.family:
+        fam = args.family
     if args.chat:
         gen = lambda js, n_chars: workloads.chat(js, fam, n_chars=n_chars)  # noqa: E731
     tok = toktier_amd.load(fam)
@@ -275,7 +280,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": (None if args.chat else
+            "traffic": (None if args.chat or args.family else
                         measured_traffic(args.config, "k_bpe_pack")),
             "alg_bytes_per_launch": int(b_alg),
             "path_achieved": round(b_alg / (ms_per_step * 1e-3) / 1e9, 3),

@@ -56,6 +56,9 @@ extern "C" {
 /* rulesets (the reference names: gpu.rs:40-62; r50k is new) */
 #define TK_RULESET_CL100K 0 /* Qwen2 / Llama-3 split (digits_max 1 or 3) */
 #define TK_RULESET_R50K 1   /* GPT-2 split */
+#define TK_RULESET_LAGUNA 2 /* Laguna-S-2.1: (?:\r?\n)+ split MergedWithNext,
+                               then the cl100k split (digits_max 1)
+                               (pretok_kernel.cu:76-86) */
 
 /* status codes */
 #define TK_OK 0
@@ -160,8 +163,9 @@ int tk_engine_encode_device(tk_engine* engine, const void* d_text,
  * id, and encodes the text between literals segment by segment (each
  * segment is pretokenized as a document of its own). n == 0 removes the
  * table. TK_E_UNSUPPORTED: a literal with single_word / lstrip / rstrip,
- * a normalized literal when the family normalizes (NFC), or normalized and
- * raw literals that can overlap (HF extracts them in two passes). */
+ * a normalized literal when the family normalizes (NFC), normalized and
+ * raw literals that can overlap (HF extracts them in two passes), or, for
+ * TK_RULESET_LAGUNA, a literal that begins or ends with CR or LF. */
 int tk_engine_set_added(tk_engine* engine, size_t n, const uint8_t* contents,
                         const uint64_t* offsets, const uint32_t* ids,
                         const uint8_t* flags);

@@ -17,6 +17,8 @@
  *         | ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+
  *       (crates/toktier-gigatoken-core/src/pretokenize/options.rs:125,:131;
  *        K = digits_max, kernel_families.v1.json:104-117)
+ *       laguna (Laguna-S-2.1): (?:\r?\n)+ split MergedWithNext first,
+ *         then the cl100k pattern (K = 1) inside each part
  *       r50k (GPT-2):
  *         's|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+
  *         |\s+(?!\S)|\s+
@@ -231,6 +233,26 @@ static int64_t match_r50k(const int32_t* cp, const uint8_t* cl, int64_t i,
   }
 }
 
+/* Laguna's stage 0, (?:\r?\n)+ split MergedWithNext
+ * (src/toktier/kernels/pretok_kernel.cu:76-86): the first position after
+ * i where a match of the pattern starts, or n. Scanning left to right, a
+ * match starts at a '\n' or at a '\r' followed by '\n', and then takes
+ * every (\r?\n) unit that follows it. */
+static int64_t next_newline_run(const int32_t* cp, int64_t i, int64_t n) {
+  int64_t q = i;
+  /* if the part starts inside a match (the match opened it), skip it */
+  while (q < n) {
+    if (cp[q] == '\n') { ++q; continue; }
+    if (cp[q] == '\r' && q + 1 < n && cp[q + 1] == '\n') { q += 2; continue; }
+    break;
+  }
+  for (; q < n; ++q) {
+    if (cp[q] == '\n') return q;
+    if (cp[q] == '\r' && q + 1 < n && cp[q + 1] == '\n') return q;
+  }
+  return n;
+}
+
 int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
                         int64_t* starts) {
   int32_t* cp = (int32_t*)malloc(sizeof(int32_t) * (size_t)(nb + 1));
@@ -242,11 +264,17 @@ int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
   for (int64_t i = 0; i < n; ++i) cl[i] = t->cls[cp[i]];
   int64_t p = 0, i = 0;
   while (i < n) {
-    starts[p++] = bo[i];
-    int64_t e = t->ruleset == TKO_RULESET_R50K
-                    ? match_r50k(cp, cl, i, n)
-                    : match_cl100k(cp, cl, i, n, t->digits_max, 1);
-    i = e;
+    /* the part the regex runs in: the whole text, or (Laguna) up to the
+       next start of a (?:\r?\n)+ match, since that stage splits with
+       behavior MergedWithNext: each newline run opens a new part */
+    int64_t end = n;
+    if (t->ruleset == TKO_RULESET_LAGUNA) end = next_newline_run(cp, i, n);
+    while (i < end) {
+      starts[p++] = bo[i];
+      i = t->ruleset == TKO_RULESET_R50K
+              ? match_r50k(cp, cl, i, end)
+              : match_cl100k(cp, cl, i, end, t->digits_max, 1);
+    }
   }
   starts[p] = nb;
   free(cp); free(bo); free(cl);

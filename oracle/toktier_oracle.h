@@ -6,6 +6,7 @@
 
 #define TKO_RULESET_CL100K 0
 #define TKO_RULESET_R50K 1
+#define TKO_RULESET_LAGUNA 2
 
 #define TKO_E_UTF8 (-1)
 #define TKO_E_NOMEM (-2)

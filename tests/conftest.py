@@ -14,7 +14,7 @@ ROOT = Path(__file__).resolve().parent.parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
-FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2")
+FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1")
 
 
 def pytest_configure(config):

@@ -75,6 +75,13 @@ def literal_cases(name: str) -> list[str]:
             "<|reserved_special_token_12|><|reserved_special_token_1|>x",
             "<|reserved_special_token_2|>47|>", "<|python_tag|>print(1)<|eom_id|>",
         ]
+    elif name == "laguna_s_2_1":
+        # the newline-run split ahead of the regex: runs of \n and \r\n,
+        # a lone \r, runs next to literals and whitespace
+        texts += ["a\nb", "a\r\nb", "a\rb", "a\r\r\nb", "\n\r\n\n x",
+                  "  \n  \n\t", "x \r\n y", "def f():\n    return 1\n\n",
+                  "<|im_start|>\n\nuser<|im_end|>\r\n", "\r\n\r\n",
+                  "1\n2\r\n3", "'s\n's", "!\n!", "end\n"]
     else:
         texts += ["doc one.<|endoftext|>doc two<|endoftext|><|endoftext|>",
                   "<|endoftext"]
@@ -83,7 +90,7 @@ def literal_cases(name: str) -> list[str]:
 
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
-    for name in ("qwen3_8b", "llama_3_1_8b", "gpt2"):
+    for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1"):
         js = standin.load_artifact_json(name)
         tok = Tokenizer.from_str(js)
         rng = np.random.default_rng(99)

@@ -210,3 +210,31 @@ def test_document_starts_inside_runs(name):
         assert list(r.array) == k.hf_ids(d), repr(d)
     joined = "".join(docs)
     assert list(t.encode(joined).array) == k.hf_ids(joined)
+
+
+def test_laguna_newline_parts():
+    """Laguna's stage 0 (a (?:\\r?\\n)+ split that keeps each run with the
+    text after it) on the device: batch boundaries inside newline runs,
+    literals next to runs, a full-size code request, and the refusal of
+    literals that begin or end with CR / LF."""
+    from toktier_amd import _ffi, workloads
+    name = "laguna_s_2_1"
+    k, t = kit(name), tok(name)
+    rng = np.random.default_rng(31)
+    pieces = ["\n", "\r\n", "\r", "\n\n", " ", "  \n", "x", "def", "1",
+              "<|im_end|>", "\t", "!", "'s", "é"]
+    docs = ["".join(pieces[int(i)] for i in rng.integers(0, len(pieces), int(n)))
+            for n in rng.integers(1, 12, size=120)]
+    rows = t.encode_batch(docs)
+    for d, r in zip(docs, rows):
+        assert list(r.array) == k.hf_ids(d), repr(d)
+    joined = "".join(docs)
+    assert list(t.encode(joined).array) == k.hf_ids(joined)
+    data = workloads.config4(k.json).encode()
+    got = t.encode_bytes(data)
+    want = k.oracle.encode_bytes(data)
+    assert not isinstance(want, int) and np.array_equal(got, want)
+    for bad in (b"\n<x>", b"<x>\r"):
+        with pytest.raises(_ffi.EngineError) as err:
+            t.engine.set_added([bad], [100100], [0])
+        assert err.value.status == _ffi.TK_E_UNSUPPORTED

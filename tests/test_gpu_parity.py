@@ -57,7 +57,7 @@ def test_long_mixed_text(name):
     from toktier_amd import workloads
     k, t = kit(name), tok(name)
     fn = {"qwen3_8b": workloads.config2, "llama_3_1_8b": workloads.config4,
-          "gpt2": workloads.config2}[name]
+          "gpt2": workloads.config2, "laguna_s_2_1": workloads.config4}[name]
     text = fn(k.json, n_chars=300_000)
     got = t.encode(text).array
     want = k.oracle.encode_bytes(text.encode())

@@ -10,7 +10,8 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt2"])
+@pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt2",
+                                  "laguna_s_2_1"])
 def test_route_admission(name):
     import toktier_amd
     from toktier_amd import registry

@@ -178,7 +178,8 @@ def test_oracle_matches_hf_on_mixed_text(name):
     from toktier_amd import workloads
     k = kit(name)
     gen = {"qwen3_8b": workloads.config2, "gpt2": workloads.config2,
-           "llama_3_1_8b": workloads.config4}[name]
+           "llama_3_1_8b": workloads.config4,
+           "laguna_s_2_1": workloads.config4}[name]
     text = gen(k.json, n_chars=200_000)
     assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
 

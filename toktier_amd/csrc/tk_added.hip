@@ -206,7 +206,30 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
     const int64_t wd = w0 + tid;
     shdm[tid] = (wd >= 0 && wd < nwords) ? host_dm[wd] : 0;
   }
-  const bool any = __syncthreads_or(hit) != 0;
+  const bool any = __syncthreads_or(hit) != 0 && a.n > 0;
+  if (a.newline_cuts) {
+    // Laguna's stage 0: a (?:\r?\n)+ run opens a new part where it begins:
+    // at a '\n', or a '\r' before a '\n', that does not continue a run
+    // (a '\n', or the '\r' of '\r\n', just before it). A run never
+    // reaches across a caller's document start; literals never begin or
+    // end with CR or LF here (the engine refuses such tables), so the
+    // raw bytes give the same runs as the text between literals.
+    for (int k = 0; k < 16; ++k) {
+      const int j = 16 * tid + k;          // offset in the block
+      const int64_t i = B + j;
+      if (i >= nb) break;
+      const int x = j + AD_BACK;           // its index in sx
+      const uint32_t b0 = sx[x], bn = sx[x + 1], bp = sx[x - 1];
+      auto hdoc = [&](int64_t q) {
+        return host_dm && ((shdm[(q >> 6) - w0] >> (q & 63)) & 1);
+      };
+      const bool unit = b0 == '\n' ||
+          (b0 == '\r' && i + 1 < nb && bn == '\n' && !hdoc(i + 1));
+      const bool cont = i > 0 && !hdoc(i) &&
+          (bp == '\n' || (bp == '\r' && b0 == '\n'));
+      if (unit && !cont) set_bits(sdm, B, i, i + 1);
+    }
+  }
   if (any) {
     if (L) {
       for (uint32_t k = tid; k < a.tab_size; k += 256) stab[k] = a.tab[k];

@@ -157,7 +157,9 @@ struct DevAdded {
   const uint32_t* id;     // literal token id
   uint64_t gate[4];       // the literals' first bytes (bit b of word b/64)
   uint32_t lmax;          // longest literal, bytes (1..255)
-  uint32_t n;             // literals
+  uint32_t n;             // literals (0: none to extract this call)
+  int newline_cuts;       // Laguna stage 0: a document start where each
+                          // (?:\r?\n)+ run begins (split MergedWithNext)
 };
 constexpr int ADDED_MAX_LEN = 255;
 constexpr int ADDED_MAX_LITERALS = 65535;

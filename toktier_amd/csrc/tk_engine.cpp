@@ -223,9 +223,10 @@ int validate(const tk_config* cfg, size_t class_len, size_t pk_len,
   if (cfg->abi_version != TK_ABI_VERSION)
     return fail(TK_E_INVALID_ARG, "abi_version %u != %u", cfg->abi_version,
                 TK_ABI_VERSION);
-  if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K)
+  if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K &&
+      cfg->ruleset != TK_RULESET_LAGUNA)
     return fail(TK_E_INVALID_ARG, "unsupported ruleset %d", cfg->ruleset);
-  if (cfg->ruleset == TK_RULESET_CL100K &&
+  if (cfg->ruleset != TK_RULESET_R50K &&
       (cfg->digits_max < 1 || cfg->digits_max > 64))
     return fail(TK_E_INVALID_ARG, "digits_max %d out of range", cfg->digits_max);
   if (!cfg->contractions)
@@ -282,7 +283,7 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     HIP_TRY(e->plocal.alloc((size_t)tk::PT_LOCAL_SLOTS * tk::pretok_tiles((int64_t)need)));
     e->cap = need;
   }
-  if (e->added.n && e->lits.n < e->cap / 64 + 8) {
+  if ((e->added.n || e->added.newline_cuts) && e->lits.n < e->cap / 64 + 8) {
     const size_t words = e->cap / 64 + 8;
     HIP_TRY(e->lits.alloc(words));
     HIP_TRY(e->litb.alloc(words));
@@ -399,8 +400,9 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
                  const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
                  uint32_t* out, size_t out_cap, uint32_t* status,
-                 uint32_t* total, bool literals = false) {
+                 uint32_t* total, const tk::DevAdded* docs = nullptr) {
   ++e->seq;
+  const bool literals = docs != nullptr;
   const uint64_t* host_dm = d_docmask;
   if (literals) d_docmask = e->docmask_lit.p;
   const tk::DevWork w =
@@ -418,7 +420,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   const bool stages = e->timing == 1, packonly = e->timing == 2;
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
   if (literals) {
-    HIP_TRY(tk::launch_added(e->added, w, host_dm, s, at(0)));
+    HIP_TRY(tk::launch_added(*docs, w, host_dm, s, at(0)));
     HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, nullptr));
   } else {
     HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
@@ -465,7 +467,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   h[tk::CTRL_STATUS] = e->gate[tk::GATE_STATUS];
   h[tk::CTRL_TOTAL] = e->gate[tk::GATE_TOTAL];
   h[tk::CTRL_FAIL] = e->gate[tk::GATE_FAIL];
-  e->last_literals = literals ? e->gate[tk::GATE_NLIT] : 0;
+  e->last_literals = literals && docs->n ? e->gate[tk::GATE_NLIT] : 0;
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
   if (h[tk::CTRL_STATUS] & tk::ST_STALL)
@@ -560,8 +562,13 @@ bool host_nfc_ok(const std::vector<uint8_t>& qc, const uint8_t* s, size_t n) {
   return true;
 }
 
-bool literal_mode(const tk_engine* e, uint32_t flags) {
-  return e->added.n > 0 && !(flags & TK_FLAG_NO_ADDED);
+// The document-start pass (k_added) ahead of k_pretok: the literal split
+// (unless the caller did it: TK_FLAG_NO_ADDED) and Laguna's newline-run
+// parts. Null when the call needs neither.
+const tk::DevAdded* doc_pass(tk_engine* e, uint32_t flags, tk::DevAdded* a) {
+  *a = e->added;
+  if (flags & TK_FLAG_NO_ADDED) a->n = 0;
+  return (a->n > 0 || a->newline_cuts) ? a : nullptr;
 }
 
 bool utf8_ok(const uint8_t* s, size_t n) { return host_utf8_ok(s, n); }
@@ -738,8 +745,12 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.vocab = e->vocab.p;
   e->t.vocab_mask = cfg->vocab_count - 1;
   e->t.blob = e->blob.p;
-  e->t.ruleset = cfg->ruleset;
-  e->t.dmax = cfg->ruleset == TK_RULESET_CL100K ? cfg->digits_max : 0;
+  // Laguna runs the cl100k predicate inside the parts its newline-run
+  // split makes; the split is a document-start pass ahead of k_pretok
+  e->t.ruleset = cfg->ruleset == TK_RULESET_R50K ? TK_RULESET_R50K : TK_RULESET_CL100K;
+  e->t.dmax = cfg->ruleset == TK_RULESET_R50K ? 0 : cfg->digits_max;
+  e->added = tk::DevAdded{};
+  e->added.newline_cuts = cfg->ruleset == TK_RULESET_LAGUNA ? 1 : 0;
   e->t.ignore_merges = cfg->ignore_merges ? 1 : 0;
   e->t.needs_nfc = cfg->needs_nfc ? 1 : 0;
   // Long pieces are cut and certified only when every merge rule that
@@ -840,6 +851,11 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
     if (flags[k] & (TK_ADDED_SINGLE_WORD | TK_ADDED_LSTRIP | TK_ADDED_RSTRIP))
       return fail(TK_E_UNSUPPORTED,
                   "added token %zu uses single_word / lstrip / rstrip", k);
+    if (e->added.newline_cuts &&
+        (c[0] == '\r' || c[0] == '\n' || c[len - 1] == '\r' || c[len - 1] == '\n'))
+      return fail(TK_E_UNSUPPORTED,
+                  "added token %zu begins or ends with CR or LF (the newline-run "
+                  "split of this ruleset would see across it)", k);
     if ((flags[k] & TK_ADDED_NORMALIZED) && e->t.needs_nfc)
       return fail(TK_E_UNSUPPORTED,
                   "added token %zu is normalized=true and the family "
@@ -901,7 +917,9 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
     }
   HIP_TRY(hipSetDevice(e->device));
   HIP_TRY(hipStreamSynchronize(e->stream));
+  const int cuts = e->added.newline_cuts;
   e->added = tk::DevAdded{};
+  e->added.newline_cuts = cuts;
   if (n == 0) return TK_OK;
   auto up = [&](auto& buf, const auto& v) -> int {
     if (buf.alloc(v.size()) != hipSuccess)
@@ -922,6 +940,7 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
   for (int k = 0; k < 4; ++k) a.gate[k] = gate[k];
   a.lmax = lmax;
   a.n = (uint32_t)n;
+  a.newline_cuts = cuts;
   e->added = a;
   // the per-call masks follow the workspace capacity
   if (e->cap) {
@@ -960,10 +979,11 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
+  tk::DevAdded docs;
   // the compaction writes straight into the caller's buffer
   rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr,
                     check, s, static_cast<uint32_t*>(d_ids), ids_cap, &st,
-                    &total, literal_mode(e, flags));
+                    &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -988,8 +1008,9 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   HIP_TRY(hipMemcpyAsync(e->text.p, text, nbytes, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
+  tk::DevAdded docs;
   rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, e->out.p,
-                    e->out.n, &st, &total, literal_mode(e, flags));
+                    e->out.n, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -1032,8 +1053,9 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
+  tk::DevAdded docs;
   rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, e->out.p,
-                    e->out.n, &st, &total, literal_mode(e, flags));
+                    e->out.n, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check,
                                   e->out.p, e->out.n, false);

@@ -24,11 +24,21 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-__all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K"]
+__all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K",
+           "RULESET_LAGUNA"]
 
 #: Device ruleset ids (the ``ruleset`` field of the engine config).
 RULESET_CL100K = 0
 RULESET_R50K = 1
+#: Laguna-S-2.1's two-stage Split group: a newline-run split that keeps each
+#: run with the text after it, then the Qwen2 pattern inside each part
+#: (``src/toktier/kernels/pretok_kernel.cu:76-86``;
+#: ``kernel_families.v1.json`` family ``laguna_s_2_1``: band cl100k,
+#: ruleset laguna, digits_max 1, class table cl100k_v3).
+RULESET_LAGUNA = 2
+
+#: Laguna's stage 0, split with behavior MergedWithNext.
+LAGUNA_STAGE0 = r"(?:\r?\n)+"
 
 QWEN2_PATTERN = (
     r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}"
@@ -48,8 +58,8 @@ GPT2_PATTERN = (
 @dataclass(frozen=True)
 class Family:
     name: str
-    ruleset: int           # RULESET_CL100K or RULESET_R50K
-    ruleset_name: str      # "cl100k" / "r50k"
+    ruleset: int           # RULESET_CL100K, RULESET_R50K or RULESET_LAGUNA
+    ruleset_name: str      # "cl100k" / "r50k" / "laguna"
     pattern: str
     digits_max: int        # digit group width (cl100k); 0 = unbounded (r50k)
     contractions_fold: bool  # (?i:...) contractions (cl100k) vs case-sensitive
@@ -76,6 +86,18 @@ FAMILIES: dict[str, Family] = {
         hf_repo="meta-llama/Llama-3.1-8B",
         # same manifest (9,085,658 B)
         real_sha256="76e48799b099d43365bd24ccd8ecc5aedac831718da780552f03b0a6eb4412aa",
+    ),
+    "laguna_s_2_1": Family(
+        name="laguna_s_2_1", ruleset=RULESET_LAGUNA, ruleset_name="laguna",
+        pattern=QWEN2_PATTERN, digits_max=1, contractions_fold=True,
+        # the stand-in declares no normalizer; the engine takes either
+        needs_nfc=False, ignore_merges=False,
+        # vocabulary size of the stand-in (the real artifact's is not
+        # recorded in the reference)
+        vocab_size=100000,
+        hf_repo="poolside/Laguna-S-2.1",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (7,287,677 B)
+        real_sha256="809240f7a182cde859a4fc4ebc902e619a173d507e99304c1092aa04e7a6658e",
     ),
     "gpt2": Family(
         name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",

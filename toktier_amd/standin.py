@@ -183,6 +183,16 @@ def _train(name: str) -> dict:
     if name == "gpt2":
         tok.pre_tokenizer = pre_tokenizers.ByteLevel(
             add_prefix_space=False, trim_offsets=True, use_regex=True)
+    elif fam.ruleset_name == "laguna":
+        from .families import LAGUNA_STAGE0
+        tok.pre_tokenizer = pre_tokenizers.Sequence([
+            pre_tokenizers.Split(Regex(LAGUNA_STAGE0),
+                                 behavior="merged_with_next", invert=False),
+            pre_tokenizers.Split(Regex(fam.pattern), behavior="isolated",
+                                 invert=False),
+            pre_tokenizers.ByteLevel(add_prefix_space=False,
+                                     trim_offsets=False, use_regex=False),
+        ])
     else:
         tok.pre_tokenizer = pre_tokenizers.Sequence([
             pre_tokenizers.Split(Regex(fam.pattern), behavior="isolated",
@@ -197,7 +207,8 @@ def _train(name: str) -> dict:
         initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
         show_progress=False,
     )
-    corpus = _code_corpus(150_000_000 if name != "gpt2" else 60_000_000)
+    corpus = _code_corpus(150_000_000 if name not in ("gpt2", "laguna_s_2_1")
+                          else 60_000_000)
     if name == "qwen3_8b":
         corpus += _synthetic_corpus(20261201, 6_000_000, 1_500_000, 40000)
     elif name == "llama_3_1_8b":
@@ -226,6 +237,13 @@ def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
     end-of-text marker."""
     if name == "gpt2":
         return [("<|endoftext|>", 50256, True)]
+    if name == "laguna_s_2_1":
+        # (the real list is not recorded offline; chat and FIM markers in
+        # the common form)
+        names = ["<|endoftext|>", "<|im_start|>", "<|im_end|>",
+                 "<|fim_prefix|>", "<|fim_middle|>", "<|fim_suffix|>",
+                 "<think>", "</think>"]
+        return [(c, 100000 + k, k < 3) for k, c in enumerate(names)]
     if name == "qwen3_8b":
         special = ["endoftext", "im_start", "im_end", "object_ref_start",
                    "object_ref_end", "box_start", "box_end", "quad_start",
