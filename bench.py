@@ -193,7 +193,7 @@ def main() -> int:
         from oracle.oracle import Oracle
         from toktier_amd import classes
         f = tok.family
-        orc = Oracle(tok.tables, classes.class_table(), classes.nfc_qc_table(),
+        orc = Oracle(tok.tables, classes.table_for(tok.family.ruleset_name), classes.nfc_qc_table(),
                      f.ruleset, f.digits_max, f.needs_nfc)
         orc.set_added([t.content.encode() for t in tok.added_tokens],
                       [t.id for t in tok.added_tokens])
@@ -221,7 +221,7 @@ def main() -> int:
         from oracle.oracle import Oracle
         from toktier_amd import classes
         f = tok.family
-        orc = Oracle(tok.tables, classes.class_table(), classes.nfc_qc_table(),
+        orc = Oracle(tok.tables, classes.table_for(tok.family.ruleset_name), classes.nfc_qc_table(),
                      f.ruleset, f.digits_max, f.needs_nfc)
         orc.set_added([t.content.encode() for t in tok.added_tokens],
                       [t.id for t in tok.added_tokens])

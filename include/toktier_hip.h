@@ -59,6 +59,11 @@ extern "C" {
 #define TK_RULESET_LAGUNA 2 /* Laguna-S-2.1: (?:\r?\n)+ split MergedWithNext,
                                then the cl100k split (digits_max 1)
                                (pretok_kernel.cu:76-86) */
+#define TK_RULESET_DEEPSEEK 3 /* DeepSeek V3 / V4: Split stages \p{N}{1,3},
+                                 CJK-range runs, then the main pattern
+                                 (pretok_classes_deepseek.v1.meta.json
+                                 "patterns"; digits_max 3, the seven-class
+                                 table, contractions 0) */
 
 /* status codes */
 #define TK_OK 0
@@ -93,7 +98,8 @@ typedef struct tk_config {
   int32_t device_ordinal;
   int32_t ruleset;             /* TK_RULESET_* */
   int32_t digits_max;          /* cl100k: 1 (Qwen) or 3 (Llama); r50k: 0 */
-  int32_t contractions;        /* must be 1 (both rulesets split them) */
+  int32_t contractions;        /* 1, or 0 for deepseek (its pattern has
+                                  no contraction alternative) */
   int32_t needs_nfc;           /* family declares an NFC normalizer */
   int32_t ignore_merges;       /* whole-piece vocabulary hit first */
   uint64_t pair_count;         /* slots in pair_keys (power of two) */

@@ -23,6 +23,14 @@
  *         's|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+
  *         |\s+(?!\S)|\s+
  *       (options.rs:118; crates/.../pretokenize/fast/r50k.rs:1-2)
+ *       deepseek (DeepSeek V3 / V4): three Split(Isolated) stages in
+ *         order, \p{N}{1,3}, then [\u4e00-\u9fa5\u3040-\u309f\u30a0-\u30ff]+,
+ *         then [ascii punct][A-Za-z]+|[^\r\n\p{L}\p{P}\p{S}]?[\p{L}\p{M}]+
+ *         | ?[\p{P}\p{S}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+ inside each
+ *         piece, spans no alternative matches kept as pieces
+ *       (pretok_classes_deepseek.v1.meta.json "patterns";
+ *        crates/.../pretokenize/fast/deepseek_v3.rs:1-22), with the
+ *        seven-class table O L M N PS WS CRLF of that meta file
  *     with \s / \p{L} / \p{N} membership read from the probed class table
  *     (classes P=0 L=1 N=2 S=3, pretok_kernel.cu:63) and the case folding
  *     of (?i:...) restricted to A-Z and U+017F (pretok_kernel.cu:153-158);
@@ -233,6 +241,111 @@ static int64_t match_r50k(const int32_t* cp, const uint8_t* cl, int64_t i,
   }
 }
 
+/* ---- DeepSeek: classes of pretok_classes_deepseek.v1.meta.json "enum" */
+enum { DS_O = 0, DS_L = 1, DS_M = 2, DS_N = 3, DS_PS = 4, DS_WS = 5, DS_CR = 6 };
+
+static int ds_cjk(int32_t c) {  /* the stage-2 class (meta "cjk_ranges") */
+  return (c >= 0x4E00 && c <= 0x9FA5) || (c >= 0x3040 && c <= 0x30FF);
+}
+static int ascii_punct(int32_t c) {  /* meta "apunct" */
+  return (c >= 0x21 && c <= 0x2F) || (c >= 0x3A && c <= 0x40) ||
+         (c >= 0x5B && c <= 0x60) || (c >= 0x7B && c <= 0x7E);
+}
+static int ascii_alpha(int32_t c) {
+  return (c >= 'A' && c <= 'Z') || (c >= 'a' && c <= 'z');
+}
+static int ds_lm(uint8_t k) { return k == DS_L || k == DS_M; }
+static int ds_space(uint8_t k) { return k == DS_WS || k == DS_CR; }
+
+/* End of the stage-3 match that starts at char i inside a piece ending at
+ * n, or -1 when no alternative matches there. */
+static int64_t match_deepseek(const int32_t* cp, const uint8_t* cl, int64_t i,
+                              int64_t n) {
+  const uint8_t k = cl[i];
+  /* [ascii punct][A-Za-z]+ */
+  if (ascii_punct(cp[i]) && i + 1 < n && ascii_alpha(cp[i + 1])) {
+    int64_t j = i + 2;
+    while (j < n && ascii_alpha(cp[j])) ++j;
+    return j;
+  }
+  /* [^\r\n\p{L}\p{P}\p{S}]?[\p{L}\p{M}]+ : the optional class is O, M,
+     N or non-CR/LF whitespace; it takes cp[i] when [\p{L}\p{M}]+ can
+     follow, else the run has to start at i */
+  if (k != DS_L && k != DS_PS && k != DS_CR && i + 1 < n && ds_lm(cl[i + 1])) {
+    int64_t j = i + 2;
+    while (j < n && ds_lm(cl[j])) ++j;
+    return j;
+  }
+  if (ds_lm(k)) {
+    int64_t j = i + 1;
+    while (j < n && ds_lm(cl[j])) ++j;
+    return j;
+  }
+  /*  ?[\p{P}\p{S}]+[\r\n]* */
+  {
+    int64_t j = -1;
+    if (cp[i] == ' ') {
+      if (i + 1 < n && cl[i + 1] == DS_PS) j = i + 1;
+    } else if (k == DS_PS) {
+      j = i;
+    }
+    if (j >= 0) {
+      while (j < n && cl[j] == DS_PS) ++j;
+      while (j < n && cl[j] == DS_CR) ++j;
+      return j;
+    }
+  }
+  if (!ds_space(k)) return -1;
+  {
+    int64_t e = i;
+    while (e < n && ds_space(cl[e])) ++e;
+    /* \s*[\r\n]+ ends right after the run's last CR/LF */
+    for (int64_t q = e - 1; q >= i; --q)
+      if (cl[q] == DS_CR) return q + 1;
+    if (e == n) return e;         /* \s+(?!\S) at the end of the piece */
+    if (e - 1 > i) return e - 1;  /* backed off by one */
+    return e;                     /* \s+ */
+  }
+}
+
+/* The three stages over chars [0, n): stage 1 cuts \p{N}{1,K} groups
+ * (leftmost, so a run splits into K-char groups from its start) and keeps
+ * the text between them; stage 2 cuts each such text into CJK runs and the
+ * rest; stage 3 runs the main pattern inside each of those, and a span no
+ * alternative matches at (a run of O chars not followed by a letter or
+ * mark) stays one piece. */
+static int64_t pieces_deepseek(const int32_t* cp, const uint8_t* cl,
+                               const int64_t* bo, int64_t n, int K,
+                               int64_t* starts) {
+  int64_t p = 0, i = 0;
+  while (i < n) {
+    if (cl[i] == DS_N) {
+      starts[p++] = bo[i];
+      int64_t j = i + 1;
+      while (j < n && cl[j] == DS_N && j - i < K) ++j;
+      i = j;
+      continue;
+    }
+    const int c = ds_cjk(cp[i]);
+    int64_t end = i + 1;
+    while (end < n && cl[end] != DS_N && ds_cjk(cp[end]) == c) ++end;
+    int gap = 0;
+    while (i < end) {
+      const int64_t m = match_deepseek(cp, cl, i, end);
+      if (m < 0) {
+        if (!gap) starts[p++] = bo[i];
+        gap = 1;
+        ++i;
+      } else {
+        starts[p++] = bo[i];
+        gap = 0;
+        i = m;
+      }
+    }
+  }
+  return p;
+}
+
 /* Laguna's stage 0, (?:\r?\n)+ split MergedWithNext
  * (src/toktier/kernels/pretok_kernel.cu:76-86): the first position after
  * i where a match of the pattern starts, or n. Scanning left to right, a
@@ -263,6 +376,9 @@ int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
   if (n < 0) { free(cp); free(bo); free(cl); return -1; }
   for (int64_t i = 0; i < n; ++i) cl[i] = t->cls[cp[i]];
   int64_t p = 0, i = 0;
+  if (t->ruleset == TKO_RULESET_DEEPSEEK) i = n;
+  if (t->ruleset == TKO_RULESET_DEEPSEEK)
+    p = pieces_deepseek(cp, cl, bo, n, t->digits_max, starts);
   while (i < n) {
     /* the part the regex runs in: the whole text, or (Laguna) up to the
        next start of a (?:\r?\n)+ match, since that stage splits with

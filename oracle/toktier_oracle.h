@@ -7,6 +7,7 @@
 #define TKO_RULESET_CL100K 0
 #define TKO_RULESET_R50K 1
 #define TKO_RULESET_LAGUNA 2
+#define TKO_RULESET_DEEPSEEK 3
 
 #define TKO_E_UTF8 (-1)
 #define TKO_E_NOMEM (-2)
@@ -14,7 +15,7 @@
 #define TKO_E_CAP (-4)
 
 typedef struct tko_tables {
-  const uint8_t* cls;          /* 0x110000 class bytes (P/L/N/S) */
+  const uint8_t* cls;          /* 0x110000 class bytes (P/L/N/S; deepseek: O L M N PS WS CRLF) */
   const uint64_t* pair_keys;
   const uint64_t* pair_vals;
   uint64_t pair_count;         /* power of two */

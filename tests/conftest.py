@@ -14,7 +14,8 @@ ROOT = Path(__file__).resolve().parent.parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
-FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1")
+FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
+                "deepseek_v3")
 
 
 def pytest_configure(config):
@@ -95,7 +96,7 @@ class FamilyKit:
         self.family = families.family(name)
         self.json = standin.load_artifact_json(name)
         self.tables = bpe_tables.load_tables(self.json)
-        self.oracle = Oracle(self.tables, classes.class_table(),
+        self.oracle = Oracle(self.tables, classes.table_for(self.family.ruleset_name),
                              classes.nfc_qc_table(), self.family.ruleset,
                              self.family.digits_max, self.family.needs_nfc)
         # the artifact's added-token literals, split out as HF does

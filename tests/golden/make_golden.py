@@ -82,15 +82,42 @@ def literal_cases(name: str) -> list[str]:
                   "  \n  \n\t", "x \r\n y", "def f():\n    return 1\n\n",
                   "<|im_start|>\n\nuser<|im_end|>\r\n", "\r\n\r\n",
                   "1\n2\r\n3", "'s\n's", "!\n!", "end\n"]
+    elif name == "deepseek_v3":
+        texts += [
+            "<｜begin▁of▁sentence｜><｜User｜>1+1=?<｜Assistant｜><think>\n"
+            "easy</think>2<｜end▁of▁sentence｜>",
+            "<｜fim▁begin｜>def f(x):<｜fim▁hole｜>\n<｜fim▁end｜>",
+            "<｜tool▁calls▁begin｜><｜tool▁call▁begin｜>f<｜tool▁sep｜>{}"
+            "<｜tool▁call▁end｜><｜tool▁calls▁end｜>", "<|EOT|>123<|EOT|>4567",
+        ]
     else:
         texts += ["doc one.<|endoftext|>doc two<|endoftext|><|endoftext|>",
                   "<|endoftext"]
     return texts
 
 
+#: strings that reach each branch of the DeepSeek split: digit groups of
+#: three (ASCII, other \p{N}), CJK-range runs and their non-letters
+#: (U+3099 marks, U+309B symbols, U+30FB punctuation, unassigned U+3040),
+#: [ascii punct][A-Za-z]+ against longer punctuation runs and non-ASCII
+#: letters, marks, O characters (controls, ZWJ) before letters and not,
+#: CR/LF runs after punctuation and whitespace
+DEEPSEEK_CASES = [
+    "1234567", "12 345", "a1234b", "½²³⁴", "٣٤٥٦", "x=12345678;",
+    "中文abc中文", "かな゛カナ・テスト", "\u3040か\u3040", "漢字123漢字",
+    "゙か", ".abc", "..abc", " .abc", "!.abc", ".héllo", ".abcé", "a.b.c",
+    "'s 'S don't", "\x01abc", "\x01\x02a", "\x01.", "a\u200db",
+    "👨\u200d👩\u200d👧", "❤️", "e\u0301\u0301", "\u0301x",
+    ".\n\n x", "a \n \nb", "\t.x", "  \u3000x", "x\r\n\r\n",
+    "!!\r\n\r\n  y", "a  1", "  1", "中 文", "中\n文", "（中文）",
+    "Hello, 世界! 123", "price: $100.00", "«quote»", "a\u00a0b",
+]
+
+
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
-    for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1"):
+    for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
+                 "deepseek_v3"):
         js = standin.load_artifact_json(name)
         tok = Tokenizer.from_str(js)
         rng = np.random.default_rng(99)
@@ -102,6 +129,8 @@ def main() -> None:
         cjk = workloads.config5(js, n_chars=4000, n_runs=1, run_chars=500)
         texts += [cjk[i:i + 800] for i in range(0, 4000, 800)]
         texts += literal_cases(name)
+        if name == "deepseek_v3":
+            texts += DEEPSEEK_CASES
         cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}
                  for t in texts]
         out["families"][name] = {

@@ -83,6 +83,27 @@ def test_preflight_rejects_bad_shapes_and_config():
     assert _preflight(_cfg(k), k, ub=np.zeros(3, np.uint8)) == _ffi.TK_E_SHAPE
 
 
+def test_preflight_checks_the_ruleset_class_table():
+    """deepseek reads a seven-class table and has no contractions; the
+    other rulesets read four classes (values above a ruleset's top class
+    are refused before anything reaches the device)."""
+    k = kit("gpt2")
+    L = _ffi.lib()
+    ds = classes.deepseek_class_table()
+    DS = _ffi.TK_RULESET_DEEPSEEK
+    assert _preflight(_cfg(k, ruleset=DS, digits_max=3, contractions=0), k,
+                      cls=ds) == _ffi.TK_OK
+    assert _preflight(_cfg(k, ruleset=DS, digits_max=3, contractions=1), k,
+                      cls=ds) == _ffi.TK_E_INVALID_ARG
+    assert b"contractions" in L.tk_last_error()
+    assert _preflight(_cfg(k, ruleset=0, digits_max=1), k, cls=ds) == _ffi.TK_E_SHAPE
+    bad = ds.copy()
+    bad[0x4E00] = 7
+    assert _preflight(_cfg(k, ruleset=DS, digits_max=3, contractions=0), k,
+                      cls=bad) == _ffi.TK_E_SHAPE
+    assert b"class table value" in L.tk_last_error()
+
+
 def test_open_without_a_device_fails_cleanly():
     try:
         import torch

@@ -57,7 +57,9 @@ def test_long_mixed_text(name):
     from toktier_amd import workloads
     k, t = kit(name), tok(name)
     fn = {"qwen3_8b": workloads.config2, "llama_3_1_8b": workloads.config4,
-          "gpt2": workloads.config2, "laguna_s_2_1": workloads.config4}[name]
+          "gpt2": workloads.config2, "laguna_s_2_1": workloads.config4,
+          "deepseek_v3": lambda js, n_chars: workloads.config5(
+              js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
     text = fn(k.json, n_chars=300_000)
     got = t.encode(text).array
     want = k.oracle.encode_bytes(text.encode())

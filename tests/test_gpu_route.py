@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt2",
-                                  "laguna_s_2_1"])
+                                  "laguna_s_2_1", "deepseek_v3"])
 def test_route_admission(name):
     import toktier_amd
     from toktier_amd import registry

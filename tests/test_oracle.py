@@ -43,6 +43,17 @@ def test_class_table_matches_reference_digest():
     assert tab[ord("!")] == 0 and tab[0x4E2D] == 1 and tab[0xA0] == 3
 
 
+def test_deepseek_class_table_matches_reference_digest():
+    tab = classes.deepseek_class_table()  # raises unless the digest matches
+    assert classes.npy_sha256(tab) == classes.DEEPSEEK_TABLE_SHA256
+    # pretok_classes_deepseek.v1.meta.json "class_histogram"
+    assert np.bincount(tab, minlength=7).tolist() == [
+        957230, 141028, 2501, 1911, 11417, 23, 2]
+    assert tab[ord("a")] == 1 and tab[0x301] == 2 and tab[ord("7")] == 3
+    assert tab[ord("!")] == 4 and tab[ord(" ")] == 5 and tab[ord("\n")] == 6
+    assert tab[0x01] == 0 and tab[0x200D] == 0 and tab[0x309B] == 4
+
+
 def test_nfc_table_matches_reference_digest():
     qc = classes.nfc_qc_table()
     assert classes.npy_sha256(qc) == classes.NFC_QC_SHA256
@@ -152,6 +163,51 @@ def test_split_rules_fuzz(name):
         assert k.oracle.pretokenize(s.encode("utf-8")) == _hf_split_starts(k, s), s
 
 
+#: every class of the DeepSeek split and its special members: ASCII and
+#: other letters, a combining mark, CJK-range letters and non-letters
+#: (U+309B symbol, U+30FB punctuation, unassigned U+3040), ASCII and other
+#: digits, ASCII punctuation and symbols, a non-ASCII symbol, O characters
+#: (ZWJ, a control), space / tab / CR / LF / other whitespace, a variation
+#: selector
+DS_ALPHABET = ["a", "Z", "é", "\u0301", "中", "か", "\u309b", "\u30fb",
+               "\u3040", "1", "½", ".", "'", "!", "$", "\U0001f600",
+               "\u200d", "\x01", " ", "\t", "\n", "\r", "\u00a0",
+               "\u3000", "\ufe0f", "\u0663"]
+
+
+def test_deepseek_split_brute_force():
+    """Every string of length <= 3 over the DeepSeek alphabet, every
+    length-5 string over a core subset, and seeded fuzz split like the
+    certified engine's three-stage pre-tokenizer."""
+    k = kit("deepseek_v3")
+    core = ["a", "é", ".", " ", "\n", "1", "\x01", "中", "\u0301", "\t"]
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 4)
+         for p in itertools.product(DS_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(core, repeat=5)),
+    )
+    bad = [s for s in cases
+           if k.oracle.pretokenize(s.encode("utf-8")) != _hf_split_starts(k, s)]
+    assert not bad, [repr(s) for s in bad[:10]]
+    rng = np.random.default_rng(8)
+    for _ in range(5000):
+        s = "".join(DS_ALPHABET[int(i)] for i in
+                    rng.integers(0, len(DS_ALPHABET), int(rng.integers(1, 40))))
+        assert k.oracle.pretokenize(s.encode("utf-8")) == _hf_split_starts(k, s), repr(s)
+
+
+def test_planted_deepseek_mistakes_are_caught():
+    """The cl100k rules on the DeepSeek classes, or digit groups of one,
+    must disagree with the certified engine on the DeepSeek cases."""
+    from oracle.oracle import Oracle
+    k = kit("deepseek_v3")
+    texts = [".abc", "12345", "中文abc", "\x01\x02a", "!!\n\n x"]
+    for rs, dm in ((0, 3), (3, 1)):
+        wrong = Oracle(k.tables, classes.deepseek_class_table(), None, rs, dm, False)
+        assert any(wrong.pretokenize(t.encode()) != _hf_split_starts(k, t)
+                   for t in texts), (rs, dm)
+
+
 # ------------------------------------------------------------ encodes
 
 def _expected(k, text: str, ids: list[int]):
@@ -179,7 +235,9 @@ def test_oracle_matches_hf_on_mixed_text(name):
     k = kit(name)
     gen = {"qwen3_8b": workloads.config2, "gpt2": workloads.config2,
            "llama_3_1_8b": workloads.config4,
-           "laguna_s_2_1": workloads.config4}[name]
+           "laguna_s_2_1": workloads.config4,
+           "deepseek_v3": lambda js, n_chars: workloads.config5(
+               js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
     text = gen(k.json, n_chars=200_000)
     assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
 

@@ -153,7 +153,8 @@ class Tokenizer:
         cfg = TkConfig(
             abi_version=TK_ABI_VERSION, device_ordinal=device,
             ruleset=fam.ruleset, digits_max=fam.digits_max,
-            contractions=1, needs_nfc=int(fam.needs_nfc),
+            contractions=int(fam.ruleset != families.RULESET_DEEPSEEK),
+            needs_nfc=int(fam.needs_nfc),
             ignore_merges=int(self.tables.ignore_merges),
             pair_count=self.tables.pair_count,
             vocab_count=self.tables.vocab_count,
@@ -161,7 +162,8 @@ class Tokenizer:
             expected_architecture=(expected_architecture.encode()
                                    if expected_architecture else None))
         nfc = classes.nfc_qc_table() if fam.needs_nfc else None
-        self.engine = Engine(cfg, classes.class_table(), self.tables, nfc)
+        self.engine = Engine(cfg, classes.table_for(fam.ruleset_name),
+                             self.tables, nfc)
         self._lock = threading.Lock()
         self._counters = _Counters()
         self._nfc = None

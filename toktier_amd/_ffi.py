@@ -24,6 +24,10 @@ TK_E_NEEDS_NFC = -6
 TK_E_CAPACITY = -7
 TK_E_INTERNAL = -8
 TK_E_UNSUPPORTED = -9
+TK_RULESET_CL100K = 0
+TK_RULESET_R50K = 1
+TK_RULESET_LAGUNA = 2
+TK_RULESET_DEEPSEEK = 3
 TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
 # added-token flags (tokenizer.json "added_tokens" fields)

@@ -22,8 +22,11 @@ PLANE = 0x110000
 
 CLASS_TABLE_SHA256 = "aab53c6705260d07f65d9762aecba729b18e11cb9710a4aea54157475cbfdf97"
 NFC_QC_SHA256 = "1a7d121e9092cdf577d992452393d25116b2577ab74dd5a067e6ca00a535d311"
+#: kernel_families.v1.json class_tables.deepseek_v1
+DEEPSEEK_TABLE_SHA256 = "b4242c04ffc981d9f457981546c43b2a82b53e3d18bf6f7d1ee1e7625c423bf7"
 
-__all__ = ["class_table", "nfc_qc_table", "npy_sha256", "PLANE"]
+__all__ = ["class_table", "deepseek_class_table", "nfc_qc_table",
+           "npy_sha256", "PLANE", "table_for"]
 
 
 def npy_sha256(arr: np.ndarray) -> str:
@@ -54,3 +57,14 @@ def class_table() -> np.ndarray:
 def nfc_qc_table() -> np.ndarray:
     """NFC quick-check values: 0 safe starter, 1..K class rank, 255 unsafe."""
     return _load("nfc_qc.npz", "nfc_qc", NFC_QC_SHA256)
+
+
+@lru_cache(maxsize=None)
+def deepseek_class_table() -> np.ndarray:
+    """DeepSeek classes O=0 L=1 M=2 N=3 PS=4 WS=5 CRLF=6 for every codepoint."""
+    return _load("classes_deepseek.npz", "deepseek", DEEPSEEK_TABLE_SHA256)
+
+
+def table_for(ruleset_name: str) -> np.ndarray:
+    """The class table a family's ruleset reads."""
+    return deepseek_class_table() if ruleset_name == "deepseek" else class_table()

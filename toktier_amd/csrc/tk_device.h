@@ -48,7 +48,7 @@ __host__ __device__ __forceinline__ uint32_t pair_alt(uint32_t b1, uint32_t tag,
 
 // Device copies of the family tables, in the engine's own layout.
 struct DevTables {
-  const uint8_t* cls;          // [0x110000] P/L/N/S
+  const uint8_t* cls;          // [0x110000] P/L/N/S (deepseek: O L M N PS WS CRLF)
   const uint8_t* nfc;          // [0x110000] quick-check values or nullptr
   const ulonglong2* pairs;     // interleaved {key, val} merge hash slots
   uint64_t pair_mask;
@@ -57,7 +57,7 @@ struct DevTables {
   const ulonglong2* vocab;     // interleaved {fnv key, val} vocabulary slots
   uint64_t vocab_mask;
   const uint8_t* blob;         // vocabulary bytes
-  int32_t ruleset;             // 0 cl100k, 1 r50k
+  int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek
   int32_t dmax;                // digit group width (cl100k)
   int32_t ignore_merges;
   int32_t needs_nfc;

@@ -29,7 +29,11 @@
 // (Qwen2 / Llama-3: crates/toktier-gigatoken-core/src/pretokenize/
 // options.rs:125,:131; GPT-2: options.rs:118), restated per character in
 // the way src/toktier/kernels/pretok_kernel.cu:8-27 describes for the
-// cl100k rules; the r50k predicate is this project's own derivation.
+// cl100k rules; the r50k and deepseek predicates are this project's own
+// derivations (deepseek: the three Split stages of
+// pretok_classes_deepseek.v1.meta.json "patterns" as one per-character rule
+// with the stage-1 / stage-2 pieces as regions, checked against the
+// sequential restatement by brute force over short strings).
 // BPE semantics: HF tokenizers 0.22.2 (lowest rank first, leftmost on
 // ties; pretok_kernel.cu:872-881); table formats: bpe_tables.py:99-132.
 #include "tk_device.h"
@@ -41,6 +45,10 @@
 namespace tk {
 
 constexpr uint8_t CP_ = 0, CL_ = 1, CN_ = 2, CS_ = 3;
+// DeepSeek's seven classes (pretok_classes_deepseek.v1.meta.json "enum")
+constexpr uint8_t DS_O = 0, DS_L = 1, DS_M = 2, DS_N = 3, DS_PS = 4,
+                  DS_WS = 5, DS_CR = 6;
+constexpr int RS_DEEPSEEK = 3;
 
 // ------------------------------------------------------------ helpers
 
@@ -293,10 +301,11 @@ struct GCtx {
 // side in LDS and decodes one entry per byte position for the tile plus
 // PT_HALO positions each side:
 //   bits  0..20 code point (decode at that byte; U+FFFD if invalid there)
-//   bits 21..22 class
+//   bits 21..22 class (bits 0..1)
 //   bits 23..24 back: prev(p) = p - 1 - back(p - 1)
 //   bits 25..26 fwd:  next(p) = p + 1 + fwd(p) (before the end checks)
 //   bit  27     the decode at p is valid UTF-8
+//   bit  28     class bit 2 (the seven DeepSeek classes)
 constexpr int PT_HALO = 64;
 constexpr int PT_SPAN = PT_TILE + 2 * PT_HALO;
 constexpr int PT_PAD = 80;  // >= PT_HALO + 4, a multiple of 16
@@ -325,7 +334,7 @@ struct LCtx {
   __device__ __forceinline__ Ch at(int64_t p) const {
     if (!in(p)) return g.at(p);
     const uint32_t e = se[p - lo];
-    return Ch{p, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
+    return Ch{p, (int32_t)(e & 0x1FFFFF), (uint8_t)(((e >> 21) & 3) | ((e >> 26) & 4))};
   }
   __device__ __forceinline__ int64_t prev(int64_t p) const {
     if (ds(p)) return -1;
@@ -552,6 +561,177 @@ __device__ __forceinline__ int fast_r50k(const Ctx5& x) {
   return p3 == '\'' && is_re_ve_ll(p2, p1) && arrives_after(x.c4, x.h4);
 }
 
+// ---- DeepSeek (DeepSeek V3 / V4) piece-start predicate. Three Split
+// stages run in order: \p{N}{1,3}; the CJK-range runs
+// [一-龥぀-ゟ゠-ヿ]+; then
+// [ascii punct][A-Za-z]+|[^\r\n\p{L}\p{P}\p{S}]?[\p{L}\p{M}]+
+// | ?[\p{P}\p{S}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+ inside each piece, the
+// spans it does not match kept as pieces. The stage-1 and stage-2 pieces
+// are regions: digits (grouped by 3 from the run start), CJK-range runs,
+// and the rest. A region change starts a piece, and the stage-3 rule reads
+// no character across one (a region end is an end of text to it). Inside a
+// region, with p1 the character before c0 in it:
+//   c0 letter / mark: after a letter / mark, only where an ASCII-alpha run
+//     that [ascii punct][A-Za-z]+ took ends (c0 not ASCII alpha, p1 is, and
+//     the run is led by an ASCII punct that starts its own match); after P
+//     or S unless c0 is ASCII alpha taken by that alternative; after CR/LF
+//   c0 P / S: unless p1 is P / S (the run) or U+0020 (" ?" takes it)
+//   c0 CR/LF: after a letter, mark or other (O) character
+//   c0 O: unless p1 is O and c0 is no match start (none begins at an O
+//     character that is not followed by a letter or mark)
+//   c0 other whitespace: after a non-space; after whitespace before a
+//     non-space (\s+(?!\S) backs off one); right after a CR/LF unless
+//     another CR/LF follows in the run and the CR/LF run before c0 was not
+//     the [\r\n]* of a P / S match
+__device__ __forceinline__ int dcl(uint32_t e) {
+  return (int)(((e >> 21) & 3) | ((e >> 26) & 4));
+}
+__device__ __forceinline__ bool ds_cjk(int c) {
+  return (c >= 0x4E00 && c <= 0x9FA5) || (c >= 0x3040 && c <= 0x30FF);
+}
+__device__ __forceinline__ int ds_region(int k, int cp) {
+  return k == DS_N ? 2 : ds_cjk(cp) ? 1 : 0;
+}
+__device__ __forceinline__ bool ascii_punct(int c) {
+  return (c >= 0x21 && c <= 0x2F) || (c >= 0x3A && c <= 0x40) ||
+         (c >= 0x5B && c <= 0x60) || (c >= 0x7B && c <= 0x7E);
+}
+__device__ __forceinline__ bool ascii_alpha(int c) {
+  return (uint32_t)((c | 32) - 'a') < 26u;
+}
+__device__ __forceinline__ bool ds_lm(int k) { return k == DS_L || k == DS_M; }
+__device__ __forceinline__ bool ds_space(int k) { return k >= DS_WS; }
+
+template <class C>
+__device__ bool start_deepseek(const C& c, const Ch& ci, int dmax) {
+  const int r0 = ds_region(ci.cl, ci.cp);
+  // the character before / after p inside c0's region (-1 at its edge)
+  auto prev_in = [&](int64_t p) -> int64_t {
+    const int64_t q = c.prev(p);
+    if (q < 0) return -1;
+    const Ch x = c.at(q);
+    return ds_region(x.cl, x.cp) == r0 ? q : -1;
+  };
+  auto next_in = [&](int64_t p) -> int64_t {
+    const int64_t q = c.next(p);
+    if (q < 0) return -1;
+    const Ch x = c.at(q);
+    return ds_region(x.cl, x.cp) == r0 ? q : -1;
+  };
+  // does the P/S character at q start its own match
+  auto arrives = [&](int64_t q) {
+    const int64_t r = prev_in(q);
+    if (r < 0) return true;
+    const Ch x = c.at(r);
+    return x.cl != DS_PS && x.cp != ' ';
+  };
+  const int64_t q1 = prev_in(ci.pos);
+  if (q1 < 0) return true;
+  if (ci.cl == DS_N) {
+    if (dmax <= 1) return true;
+    int64_t n = 0;
+    for (int64_t q = q1; q >= 0; q = prev_in(q)) ++n;
+    return n % dmax == 0;
+  }
+  const Ch p1 = c.at(q1);
+  if (ds_lm(ci.cl)) {
+    if (ds_lm(p1.cl)) {
+      if (ascii_alpha(ci.cp) || !ascii_alpha(p1.cp)) return false;
+      for (int64_t q = q1;;) {
+        const int64_t r = prev_in(q);
+        if (r < 0) return false;
+        const Ch x = c.at(r);
+        if (!ascii_alpha(x.cp)) return ascii_punct(x.cp) && arrives(r);
+        q = r;
+      }
+    }
+    if (p1.cl == DS_PS)
+      return !(ascii_alpha(ci.cp) && ascii_punct(p1.cp) && arrives(q1));
+    return p1.cl == DS_CR;
+  }
+  if (ci.cl == DS_PS) return p1.cl != DS_PS && p1.cp != ' ';
+  if (ci.cl == DS_CR) return ds_lm(p1.cl) || p1.cl == DS_O;
+  if (ci.cl == DS_O) {
+    if (p1.cl != DS_O) return true;
+    const int64_t q = next_in(ci.pos);
+    return q >= 0 && ds_lm(c.at(q).cl);
+  }
+  // other whitespace
+  if (!ds_space(p1.cl)) return true;
+  if (p1.cl == DS_WS) {
+    const int64_t q = next_in(ci.pos);
+    return q >= 0 && !ds_space(c.at(q).cl);
+  }
+  bool more = false;
+  for (int64_t q = next_in(ci.pos); q >= 0; q = next_in(q)) {
+    const Ch x = c.at(q);
+    if (!ds_space(x.cl)) break;
+    if (x.cl == DS_CR) { more = true; break; }
+  }
+  if (!more) return true;
+  for (int64_t q = q1;;) {
+    const int64_t r = prev_in(q);
+    if (r < 0) return false;
+    const Ch x = c.at(r);
+    if (!ds_space(x.cl)) return x.cl == DS_PS;
+    if (x.cl != DS_CR) return false;
+    q = r;
+  }
+}
+
+// The same from the fixed context; FAST_GENERAL: an ASCII-alpha run longer
+// than the context, walked by the general predicate.
+constexpr int FAST_GENERAL = -4;
+__device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
+  const int k0 = dcl(x.c0), p0 = ecp(x.c0);
+  const int k1 = dcl(x.c1), p1 = ecp(x.c1);
+  const int r0 = ds_region(k0, p0);
+  if (ds_region(k1, p1) != r0) return 1;
+  const int k2 = dcl(x.c2), p2 = ecp(x.c2), k3 = dcl(x.c3), p3 = ecp(x.c3);
+  const int k4 = dcl(x.c4), p4 = ecp(x.c4), kn = dcl(x.cn);
+  // present inside c0's region
+  const bool h2 = x.h2 && ds_region(k2, p2) == r0;
+  const bool h3 = h2 && x.h3 && ds_region(k3, p3) == r0;
+  const bool h4 = h3 && x.h4 && ds_region(k4, p4) == r0;
+  const bool hn = x.hn && ds_region(kn, ecp(x.cn)) == r0;
+  if (k0 == DS_N) {
+    if (dmax <= 1) return 1;
+    if (!h2) return 1 % dmax == 0;
+    if (!h3) return 2 % dmax == 0;
+    return FAST_DIGITS;
+  }
+  // does a P/S character whose predecessor (present: h) is k, p start a match
+  auto arrives = [](bool h, int k, int p) { return !h || (k != DS_PS && p != ' '); };
+  if (ds_lm(k0)) {
+    if (ds_lm(k1)) {
+      if (ascii_alpha(p0) || !ascii_alpha(p1)) return 0;
+      if (!h2) return 0;
+      if (!ascii_alpha(p2)) return ascii_punct(p2) && arrives(h3, k3, p3);
+      if (!h3) return 0;
+      if (!ascii_alpha(p3)) return ascii_punct(p3) && arrives(h4, k4, p4);
+      return FAST_GENERAL;
+    }
+    if (k1 == DS_PS) return !(ascii_alpha(p0) && ascii_punct(p1) && arrives(h2, k2, p2));
+    return k1 == DS_CR;
+  }
+  if (k0 == DS_PS) return k1 != DS_PS && p1 != ' ';
+  if (k0 == DS_CR) return ds_lm(k1) || k1 == DS_O;
+  if (k0 == DS_O) return k1 != DS_O || (hn && ds_lm(kn));
+  if (!ds_space(k1)) return 1;
+  if (k1 == DS_WS) return hn && !ds_space(kn);
+  // right after a CR/LF: a start unless another CR/LF follows in the run
+  // and the CR/LF run before c0 is not a P / S match's [\r\n]*
+  if (!hn || !ds_space(kn)) return 1;
+  if (kn == DS_WS) return FAST_CRLF;
+  if (!h2) return 0;
+  if (k2 == DS_PS) return 1;
+  if (k2 != DS_CR) return 0;
+  if (!h3) return 0;
+  if (k3 == DS_PS) return 1;
+  if (k3 != DS_CR) return 0;
+  return FAST_CRLF;
+}
+
 // exclusive scan of one value per thread over a 256-thread block
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   __shared__ uint32_t wsum[4];
@@ -702,8 +882,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2 : l >= 0xC0 ? 1 : 0;
         ok = d <= pg && need >= d;
       }
-      e = cp | (cl << 21) | ((uint32_t)back << 23) | ((uint32_t)fwd << 25) |
-          (ok ? 1u << 27 : 0u);
+      e = cp | ((cl & 3) << 21) | ((cl >> 2) << 28) | ((uint32_t)back << 23) |
+          ((uint32_t)fwd << 25) | (ok ? 1u << 27 : 0u);
     }
     se[j] = e;
   }
@@ -715,6 +895,11 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     return L - 1 - (int)((se[L - 1] >> 23) & 3);
   };
   const int lane = tid & 63, wv = wave_id();
+  // the ruleset's class of an entry, and its digit / P / whitespace classes
+  auto kcl = [](uint32_t e) { return RS == RS_DEEPSEEK ? dcl(e) : ecl(e); };
+  constexpr int KN = RS == RS_DEEPSEEK ? DS_N : CN_;
+  constexpr int KP = RS == RS_DEEPSEEK ? DS_PS : CP_;
+  auto kws = [](int k) { return RS == RS_DEEPSEEK ? k >= DS_WS : k == CS_; };
   uint32_t st = 0;
   // the tile's words, and the first word after it (the next block writes
   // that one; it is recomputed here to size the pieces near the tile end)
@@ -776,7 +961,10 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       const bool nin = Ln < PT_SPAN;
       x.hn = lo + Ln < nb && !ds(Ln);
       x.cn = nin ? se[Ln] : 0u;
-      int r = !nin ? -1 : RS == 1 ? fast_r50k(x) : fast_cl100k(x, t.dmax);
+      int r = !nin ? -1
+            : RS == 1 ? fast_r50k(x)
+            : RS == RS_DEEPSEEK ? fast_deepseek(x, t.dmax)
+                                : fast_cl100k(x, t.dmax);
       const bool open = lead && !d0 && r < 0;
       if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
         if (open) {
@@ -812,7 +1000,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
                 r = 0;
               } else if (h >= 0) {
                 if ((mWS >> h) & 1) r = 0;
-                else if (!((mHI >> h) & 1)) r = ecl(se[Li - (lane - h)]) == CP_;
+                else if (!((mHI >> h) & 1)) r = kcl(se[Li - (lane - h)]) == KP;
               }
             } else if (fd < 64 && fd <= f) {
               r = 1;
@@ -828,7 +1016,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
               if (ds(L)) { r = nd % t.dmax == 0; break; }
               if (L - 1 < 0) break;  // past the span: general path
               const int Lr = prv(L);
-              if (ecl(se[Lr]) != CN_) { r = nd % t.dmax == 0; break; }
+              if (kcl(se[Lr]) != KN) { r = nd % t.dmax == 0; break; }
               ++nd;
               L = Lr;
             }
@@ -841,7 +1029,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
               if (lo + L >= nb || ds(L)) { known = true; break; }
               if (L >= PT_SPAN) break;
               const uint32_t eq = se[L];
-              if (ecl(eq) != CS_) { known = true; break; }
+              if (!kws(kcl(eq))) { known = true; break; }
               if (crlf(ecp(eq))) { more = known = true; break; }
               L += 1 + (int)((eq >> 25) & 3);
             }
@@ -852,15 +1040,22 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
                 if (L - 1 < 0) break;
                 const int Lr = prv(L);
                 const uint32_t ex = se[Lr];
-                if (ecl(ex) != CS_) { r = ecl(ex) == CP_; break; }
+                // (a DeepSeek P/S character of a CJK run is another region:
+                // the CR/LF run starts its own)
+                if (!kws(kcl(ex))) {
+                  r = kcl(ex) == KP && !(RS == RS_DEEPSEEK && ds_cjk(ecp(ex)));
+                  break;
+                }
                 if (!crlf(ecp(ex))) { r = 0; break; }
                 L = Lr;
               }
             }
           }
           if (r < 0) {
-            const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)((e >> 21) & 3)};
-            r = RS == 1 ? start_r50k(c, ci) : start_cl100k(c, ci, t.dmax);
+            const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)kcl(e)};
+            r = RS == 1 ? start_r50k(c, ci)
+              : RS == RS_DEEPSEEK ? start_deepseek(c, ci, t.dmax)
+                                  : start_cl100k(c, ci, t.dmax);
           }
         }
       }
@@ -955,6 +1150,9 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
   if (t.ruleset == 1) {
     if (dm) launch_ev(k_pretok<1, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<1, false>, g, b, s, start, stop, t, w, nwords);
+  } else if (t.ruleset == RS_DEEPSEEK) {
+    if (dm) launch_ev(k_pretok<RS_DEEPSEEK, true>, g, b, s, start, stop, t, w, nwords);
+    else launch_ev(k_pretok<RS_DEEPSEEK, false>, g, b, s, start, stop, t, w, nwords);
   } else {
     if (dm) launch_ev(k_pretok<0, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<0, false>, g, b, s, start, stop, t, w, nwords);

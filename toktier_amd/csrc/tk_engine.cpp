@@ -216,7 +216,7 @@ struct tk_engine {
 
 namespace {
 
-int validate(const tk_config* cfg, size_t class_len, size_t pk_len,
+int validate(const tk_config* cfg, const uint8_t* class_table, size_t class_len, size_t pk_len,
              size_t pv_len, size_t byte_id_len, size_t vk_len, size_t vv_len,
              size_t unsafe_len) {
   if (!cfg) return fail(TK_E_INVALID_ARG, "config is null");
@@ -224,16 +224,27 @@ int validate(const tk_config* cfg, size_t class_len, size_t pk_len,
     return fail(TK_E_INVALID_ARG, "abi_version %u != %u", cfg->abi_version,
                 TK_ABI_VERSION);
   if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K &&
-      cfg->ruleset != TK_RULESET_LAGUNA)
+      cfg->ruleset != TK_RULESET_LAGUNA && cfg->ruleset != TK_RULESET_DEEPSEEK)
     return fail(TK_E_INVALID_ARG, "unsupported ruleset %d", cfg->ruleset);
   if (cfg->ruleset != TK_RULESET_R50K &&
       (cfg->digits_max < 1 || cfg->digits_max > 64))
     return fail(TK_E_INVALID_ARG, "digits_max %d out of range", cfg->digits_max);
-  if (!cfg->contractions)
-    return fail(TK_E_INVALID_ARG, "rulesets without contractions are not supported");
+  // the deepseek pattern has no contraction alternative; the others do
+  if ((cfg->contractions != 0) != (cfg->ruleset != TK_RULESET_DEEPSEEK))
+    return fail(TK_E_INVALID_ARG, "contractions=%d does not match ruleset %d",
+                cfg->contractions, cfg->ruleset);
   // shape rules of the reference executor (gpu.rs:1642-1679)
   if (class_len < PLANE)
     return fail(TK_E_SHAPE, "class table does not cover U+10FFFF");
+  {
+    // four classes (P L N S), seven for deepseek (O L M N PS WS CRLF)
+    const uint8_t top = cfg->ruleset == TK_RULESET_DEEPSEEK ? 6 : 3;
+    uint8_t mx = 0;
+    for (size_t i = 0; i < PLANE; ++i) mx = class_table[i] > mx ? class_table[i] : mx;
+    if (mx > top)
+      return fail(TK_E_SHAPE, "class table value %u above %u for ruleset %d",
+                  mx, top, cfg->ruleset);
+  }
   if (!pow2(cfg->pair_count) || pk_len != 8 * cfg->pair_count || pv_len != pk_len)
     return fail(TK_E_SHAPE, "pair tables have an invalid shape");
   if (!pow2(cfg->vocab_count) || vk_len != 8 * cfg->vocab_count || vv_len != vk_len)
@@ -600,7 +611,7 @@ int tk_engine_preflight(const tk_config* cfg, const uint8_t* class_table,
       !vocab_vals)
     return fail(TK_E_INVALID_ARG, "a table pointer is null");
   (void)unsafe_bits;
-  return validate(cfg, class_len, pair_keys_len, pair_vals_len, byte_id_len,
+  return validate(cfg, class_table, class_len, pair_keys_len, pair_vals_len, byte_id_len,
                   vocab_keys_len, vocab_vals_len, unsafe_len);
 }
 
@@ -747,7 +758,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.blob = e->blob.p;
   // Laguna runs the cl100k predicate inside the parts its newline-run
   // split makes; the split is a document-start pass ahead of k_pretok
-  e->t.ruleset = cfg->ruleset == TK_RULESET_R50K ? TK_RULESET_R50K : TK_RULESET_CL100K;
+  e->t.ruleset = cfg->ruleset == TK_RULESET_LAGUNA ? TK_RULESET_CL100K : cfg->ruleset;
   e->t.dmax = cfg->ruleset == TK_RULESET_R50K ? 0 : cfg->digits_max;
   e->added = tk::DevAdded{};
   e->added.newline_cuts = cfg->ruleset == TK_RULESET_LAGUNA ? 1 : 0;

@@ -15,6 +15,11 @@ Reference data this mirrors:
   ``contractions``, ``needs_nfc``, ``ignore_merges``
   (``crates/toktier-routing-core/src/gpu.rs:22-38``).
 
+DeepSeek V3 (``kernel_families.v1.json`` family ``deepseek_v3``: band and
+ruleset deepseek, class table deepseek_v1, contractions false, digits_max
+3 from ``pretok_classes_deepseek.v1.meta.json``) splits in three stages
+(that meta file's ``patterns``); its device ruleset is ``deepseek``.
+
 GPT-2 is not a GPU family in the reference (its r50k split exists only in
 the CPU scanner ``crates/toktier-gigatoken-core/src/pretokenize/fast/r50k.rs``);
 here it gets its own device ruleset, ``r50k``.
@@ -25,7 +30,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 __all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K",
-           "RULESET_LAGUNA"]
+           "RULESET_LAGUNA", "RULESET_DEEPSEEK", "DEEPSEEK_STAGES"]
 
 #: Device ruleset ids (the ``ruleset`` field of the engine config).
 RULESET_CL100K = 0
@@ -36,6 +41,10 @@ RULESET_R50K = 1
 #: ``kernel_families.v1.json`` family ``laguna_s_2_1``: band cl100k,
 #: ruleset laguna, digits_max 1, class table cl100k_v3).
 RULESET_LAGUNA = 2
+
+#: DeepSeek V3 / V4: three Split(Isolated) stages, applied in order
+#: (``pretok_classes_deepseek.v1.meta.json`` ``patterns``).
+RULESET_DEEPSEEK = 3
 
 #: Laguna's stage 0, split with behavior MergedWithNext.
 LAGUNA_STAGE0 = r"(?:\r?\n)+"
@@ -48,6 +57,15 @@ LLAMA3_PATTERN = (
     r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}"
     r"| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+"
 )
+DEEPSEEK_STAGES = (
+    r"\p{N}{1,3}",
+    "[\u4e00-\u9fa5\u3040-\u309f\u30a0-\u30ff]+",
+    # (CR and LF are literal characters in the artifact's pattern)
+    "[!\"#$%&'()*+,\\-./:;<=>?@\\[\\\\\\]^_`{|}~][A-Za-z]+"
+    "|[^\r\n\\p{L}\\p{P}\\p{S}]?[\\p{L}\\p{M}]+| ?[\\p{P}\\p{S}]+[\r\n]*"
+    "|\\s*[\r\n]+|\\s+(?!\\S)|\\s+",
+)
+
 #: The pattern HF ``ByteLevel(use_regex=True)`` applies (GPT-2).
 GPT2_PATTERN = (
     r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+"
@@ -58,8 +76,8 @@ GPT2_PATTERN = (
 @dataclass(frozen=True)
 class Family:
     name: str
-    ruleset: int           # RULESET_CL100K, RULESET_R50K or RULESET_LAGUNA
-    ruleset_name: str      # "cl100k" / "r50k" / "laguna"
+    ruleset: int           # RULESET_CL100K / _R50K / _LAGUNA / _DEEPSEEK
+    ruleset_name: str      # "cl100k" / "r50k" / "laguna" / "deepseek"
     pattern: str
     digits_max: int        # digit group width (cl100k); 0 = unbounded (r50k)
     contractions_fold: bool  # (?i:...) contractions (cl100k) vs case-sensitive
@@ -98,6 +116,15 @@ FAMILIES: dict[str, Family] = {
         hf_repo="poolside/Laguna-S-2.1",
         # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (7,287,677 B)
         real_sha256="809240f7a182cde859a4fc4ebc902e619a173d507e99304c1092aa04e7a6658e",
+    ),
+    "deepseek_v3": Family(
+        name="deepseek_v3", ruleset=RULESET_DEEPSEEK, ruleset_name="deepseek",
+        pattern=DEEPSEEK_STAGES[2], digits_max=3, contractions_fold=False,
+        # the artifact declares an empty normalizer sequence
+        needs_nfc=False, ignore_merges=False, vocab_size=128000,
+        hf_repo="deepseek-ai/DeepSeek-V3",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (7,847,652 B)
+        real_sha256="621ac2e32d0dba658404412318818aaa8ce8cda492e59830109d8da6b517fb41",
     ),
     "gpt2": Family(
         name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",

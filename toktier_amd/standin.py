@@ -21,6 +21,10 @@ Shapes follow the real artifacts:
   entries, ordered by the merged token's rank), which gives more merges
   than vocabulary entries and duplicate merged ids, as the real artifact
   has (``src/toktier/kernels/bpe_tables.py`` module notes).
+- ``deepseek_v3``: an empty normalizer sequence; the three
+  ``Split(isolated)`` stages (digits, CJK-range runs, main pattern) +
+  ``ByteLevel(use_regex=False)``; BPE over a 128,000-entry vocabulary,
+  ``ignore_merges`` false.
 - ``gpt2``: ``ByteLevel(use_regex=True)`` pre-tokenizer; 50,000 merges,
   50,257 entries including ``<|endoftext|>``.
 
@@ -183,6 +187,14 @@ def _train(name: str) -> dict:
     if name == "gpt2":
         tok.pre_tokenizer = pre_tokenizers.ByteLevel(
             add_prefix_space=False, trim_offsets=True, use_regex=True)
+    elif fam.ruleset_name == "deepseek":
+        from .families import DEEPSEEK_STAGES
+        tok.normalizer = normalizers.Sequence([])
+        tok.pre_tokenizer = pre_tokenizers.Sequence(
+            [pre_tokenizers.Split(Regex(p), behavior="isolated", invert=False)
+             for p in DEEPSEEK_STAGES]
+            + [pre_tokenizers.ByteLevel(add_prefix_space=False,
+                                        trim_offsets=False, use_regex=False)])
     elif fam.ruleset_name == "laguna":
         from .families import LAGUNA_STAGE0
         tok.pre_tokenizer = pre_tokenizers.Sequence([
@@ -213,6 +225,8 @@ def _train(name: str) -> dict:
         corpus += _synthetic_corpus(20261201, 6_000_000, 1_500_000, 40000)
     elif name == "llama_3_1_8b":
         corpus += _synthetic_corpus(20261202, 1_500_000, 800_000, 10000)
+    elif name == "deepseek_v3":
+        corpus += _synthetic_corpus(20261203, 8_000_000, 1_000_000, 40000)
     tok.train_from_iterator(corpus, trainer)
     spec = json.loads(tok.to_str())
     model = spec["model"]
@@ -237,6 +251,18 @@ def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
     end-of-text marker."""
     if name == "gpt2":
         return [("<|endoftext|>", 50256, True)]
+    if name == "deepseek_v3":
+        # (the real artifact keeps its sentence markers at ids 0-2 inside
+        # the vocabulary; the stand-in numbers its markers from 128000)
+        names = ["<｜begin▁of▁sentence｜>", "<｜end▁of▁sentence｜>",
+                 "<｜▁pad▁｜>", "<｜fim▁hole｜>", "<｜fim▁begin｜>",
+                 "<｜fim▁end｜>", "<｜User｜>", "<｜Assistant｜>", "<|EOT|>",
+                 "<｜tool▁calls▁begin｜>", "<｜tool▁calls▁end｜>",
+                 "<｜tool▁call▁begin｜>", "<｜tool▁call▁end｜>",
+                 "<｜tool▁outputs▁begin｜>", "<｜tool▁outputs▁end｜>",
+                 "<｜tool▁output▁begin｜>", "<｜tool▁output▁end｜>",
+                 "<｜tool▁sep｜>", "<think>", "</think>"]
+        return [(c, 128000 + k, k < 3) for k, c in enumerate(names)]
     if name == "laguna_s_2_1":
         # (the real list is not recorded offline; chat and FIM markers in
         # the common form)

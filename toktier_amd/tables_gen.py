@@ -76,6 +76,39 @@ def build_classes() -> np.ndarray:
     return tab
 
 
+#: DeepSeek seven-class encoding (the reference's
+#: pretok_classes_deepseek.v1.meta.json enum)
+DS_O, DS_L, DS_M, DS_N, DS_PS, DS_WS, DS_CRLF = range(7)
+
+
+def build_deepseek_classes() -> np.ndarray:
+    """Seven classes for the DeepSeek V3 split patterns: O (none of the
+    below), L (``\p{L}``), M (``\p{M}``), N (``\p{N}``), PS
+    (``[\p{P}\p{S}]``), WS (``\s`` other than CR / LF), CRLF. Surrogates
+    (never in valid UTF-8) take PS, as in the reference table (whose sha256
+    this reproduces, ``kernel_families.v1.json`` ``deepseek_v1``)."""
+    ws = _probe_membership(r"\s")
+    let = _probe_membership(r"\p{L}")
+    mark = _probe_membership(r"\p{M}")
+    num = _probe_membership(r"\p{N}")
+    ps = _probe_membership(r"[\p{P}\p{S}]")
+    crlf = _probe_membership(r"[\r\n]")
+    sets = (ws, let, mark, num, ps)
+    for i in range(len(sets)):
+        for j in range(i + 1, len(sets)):
+            if (sets[i] & sets[j]).any():
+                raise RuntimeError("class probes overlap")
+    tab = np.full(PLANE, DS_O, dtype=np.uint8)
+    tab[let] = DS_L
+    tab[mark] = DS_M
+    tab[num] = DS_N
+    tab[ps] = DS_PS
+    tab[ws] = DS_WS
+    tab[crlf] = DS_CRLF
+    tab[0xD800:0xE000] = DS_PS
+    return tab
+
+
 def _batch_norm(norm, items: list[str]) -> list[str]:
     """Normalize many short strings at once, separated by U+0020 (a starter
     with no composition or decomposition role)."""
@@ -193,6 +226,9 @@ def main() -> None:
     cls = build_classes()
     np.savez_compressed(TABLE_DIR / "classes.npz", cl100k=cls)
     print("classes", np.bincount(cls, minlength=4), flush=True)
+    ds = build_deepseek_classes()
+    np.savez_compressed(TABLE_DIR / "classes_deepseek.npz", deepseek=ds)
+    print("deepseek classes", np.bincount(ds, minlength=7), flush=True)
     qc = build_nfc_qc()
     np.savez_compressed(TABLE_DIR / "nfc_qc.npz", nfc_qc=qc)
     print("nfc_qc 0:", int((qc == 0).sum()), "1..K:",

@@ -271,12 +271,15 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
     """C2-style text laid out as chat turns in the family's template, so
     the request carries added-token literals: Qwen3 ``<|im_start|>role``
     ... ``<|im_end|>`` (assistant turns with a ``<think>`` block), Llama-3
-    header / ``<|eot_id|>`` turns after ``<|begin_of_text|>``, GPT-2
+    header / ``<|eot_id|>`` turns after ``<|begin_of_text|>``, DeepSeek
+    ``<｜User｜>`` / ``<｜Assistant｜>`` turns after the sentence marker
+    (assistant turns closed by ``<｜end▁of▁sentence｜>``), GPT-2
     documents joined by ``<|endoftext|>``. Turns hold U[200, 3000] chars."""
     rng = np.random.default_rng(SEED_BASE + 6 + 1000 * sample)
     body = config2(tokenizer_json, n_chars=n_chars, sample=sample)
     roles = ["system", "user", "assistant"]
-    out: list[str] = ["<|begin_of_text|>"] if family == "llama_3_1_8b" else []
+    out: list[str] = (["<|begin_of_text|>"] if family == "llama_3_1_8b" else
+                      ["<｜begin▁of▁sentence｜>"] if family == "deepseek_v3" else [])
     total, at, turn = sum(map(len, out)), 0, 0
     while total < n_chars and at < len(body):
         n = int(rng.integers(200, 3001))
@@ -289,6 +292,10 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
             piece = f"<|im_start|>{role}\n{content}<|im_end|>\n"
         elif family == "llama_3_1_8b":
             piece = f"<|start_header_id|>{role}<|end_header_id|>\n\n{content}<|eot_id|>"
+        elif family == "deepseek_v3":
+            piece = (f"<｜Assistant｜>{content}<｜end▁of▁sentence｜>"
+                     if role == "assistant" else
+                     f"<｜User｜>{content}" if role == "user" else content)
         else:
             piece = content + "<|endoftext|>"
         out.append(piece)
