@@ -31,6 +31,15 @@
  *       (pretok_classes_deepseek.v1.meta.json "patterns";
  *        crates/.../pretokenize/fast/deepseek_v3.rs:1-22), with the
  *        seven-class table O L M N PS WS CRLF of that meta file
+ *       o200k (gpt-oss, o200k_base with contractions):
+ *         [^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]*[\p{Ll}\p{Lm}\p{Lo}\p{M}]+C?
+ *         |[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]+[\p{Ll}\p{Lm}\p{Lo}\p{M}]*C?
+ *         |\p{N}{1,K}| ?[^\s\p{L}\p{N}]+[\r\n/]*|\s*[\r\n]+|\s+(?!\S)|\s+
+ *         with C = (?i:'s|'t|'re|'ve|'m|'ll|'d)
+ *       (crates/.../pretokenize/options.rs O200k row; kernel_families.v1.json
+ *        gpt_oss_120b: digits_max 3, contractions), with the seven-class
+ *        table P U L C N S M (U = Lu Lt, L = Ll, C = Lm Lo; class table
+ *        o200k_v4, whose sha256 the probed table reproduces)
  *     with \s / \p{L} / \p{N} membership read from the probed class table
  *     (classes P=0 L=1 N=2 S=3, pretok_kernel.cu:63) and the case folding
  *     of (?i:...) restricted to A-Z and U+017F (pretok_kernel.cu:153-158);
@@ -346,6 +355,99 @@ static int64_t pieces_deepseek(const int32_t* cp, const uint8_t* cl,
   return p;
 }
 
+/* ---- o200k: classes P U L C N S M (o200k_v4) */
+enum { OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4, OK_S = 5, OK_M = 6 };
+
+static int ok_a(uint8_t k) { return k == OK_U || k == OK_C || k == OK_M; }
+static int ok_b(uint8_t k) { return k == OK_L || k == OK_C || k == OK_M; }
+/* [^\r\n\p{L}\p{N}] */
+static int ok_q(uint8_t k, int32_t c) {
+  return (k == OK_P || k == OK_M || k == OK_S) && !is_crlf(c);
+}
+
+/* [A]*[B]+ from t (A = Lu Lt Lm Lo M, B = Ll Lm Lo M): A* takes the
+ * longest run, then gives characters back until B+ can start; B+ then runs
+ * to the end of the B characters. End, or -1. */
+static int64_t ok_letters1(const uint8_t* cl, int64_t t, int64_t n) {
+  int64_t a = t;
+  while (a < n && ok_a(cl[a])) ++a;
+  if (a < n && cl[a] == OK_L) {
+    int64_t b = a + 1;
+    while (b < n && ok_b(cl[b])) ++b;
+    return b;
+  }
+  /* backing off: the last character of the run that B+ accepts (C or M);
+     the one after it is U or ends the run, so B+ takes just it */
+  for (int64_t j = a - 1; j >= t; --j)
+    if (ok_b(cl[j])) return j + 1;
+  return -1;
+}
+
+/* [A]+[B]* from t. */
+static int64_t ok_letters2(const uint8_t* cl, int64_t t, int64_t n) {
+  int64_t a = t;
+  while (a < n && ok_a(cl[a])) ++a;
+  if (a == t) return -1;
+  while (a < n && ok_b(cl[a])) ++a;
+  return a;
+}
+
+/* (?i:'s|'t|'re|'ve|'m|'ll|'d)? after a letter match ending at e */
+static int64_t ok_contraction(const int32_t* cp, int64_t e, int64_t n) {
+  if (e + 1 < n && cp[e] == '\'') {
+    int a = fold(cp[e + 1]);
+    if (a == 's' || a == 't' || a == 'm' || a == 'd') return e + 2;
+    if (e + 2 < n) {
+      int b = fold(cp[e + 2]);
+      if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') ||
+          (a == 'l' && b == 'l'))
+        return e + 3;
+    }
+  }
+  return e;
+}
+
+/* End of the o200k match that starts at char i. Each letter alternative is
+ * tried with the optional prefix first taking cp[i], then without it. */
+static int64_t match_o200k(const int32_t* cp, const uint8_t* cl, int64_t i,
+                           int64_t n, int K) {
+  const int q = ok_q(cl[i], cp[i]);
+  int64_t e = -1;
+  if (q && i + 1 < n) e = ok_letters1(cl, i + 1, n);
+  if (e < 0) e = ok_letters1(cl, i, n);
+  if (e < 0 && q && i + 1 < n) e = ok_letters2(cl, i + 1, n);
+  if (e < 0) e = ok_letters2(cl, i, n);
+  if (e >= 0) return ok_contraction(cp, e, n);
+  if (cl[i] == OK_N) {
+    int64_t j = i + 1;
+    while (j < n && cl[j] == OK_N && j - i < K) ++j;
+    return j;
+  }
+  /*  ?[^\s\p{L}\p{N}]+[\r\n/]* */
+  {
+    int64_t j = -1;
+    if (cp[i] == ' ') {
+      if (i + 1 < n && (cl[i + 1] == OK_P || cl[i + 1] == OK_M)) j = i + 1;
+    } else if (cl[i] == OK_P || cl[i] == OK_M) {
+      j = i;
+    }
+    if (j >= 0) {
+      while (j < n && (cl[j] == OK_P || cl[j] == OK_M)) ++j;
+      while (j < n && (is_crlf(cp[j]) || cp[j] == '/')) ++j;
+      return j;
+    }
+  }
+  {
+    int64_t e2 = i;
+    while (e2 < n && cl[e2] == OK_S) ++e2;
+    for (int64_t k = e2 - 1; k >= i; --k)
+      if (is_crlf(cp[k])) return k + 1;
+    if (e2 == n) return e2;
+    if (e2 - 1 > i) return e2 - 1;
+    return e2;
+  }
+}
+
 /* Laguna's stage 0, (?:\r?\n)+ split MergedWithNext
  * (src/toktier/kernels/pretok_kernel.cu:76-86): the first position after
  * i where a match of the pattern starts, or n. Scanning left to right, a
@@ -389,6 +491,8 @@ int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
       starts[p++] = bo[i];
       i = t->ruleset == TKO_RULESET_R50K
               ? match_r50k(cp, cl, i, end)
+              : t->ruleset == TKO_RULESET_O200K
+              ? match_o200k(cp, cl, i, end, t->digits_max)
               : match_cl100k(cp, cl, i, end, t->digits_max, 1);
     }
   }

@@ -8,6 +8,7 @@
 #define TKO_RULESET_R50K 1
 #define TKO_RULESET_LAGUNA 2
 #define TKO_RULESET_DEEPSEEK 3
+#define TKO_RULESET_O200K 4
 
 #define TKO_E_UTF8 (-1)
 #define TKO_E_NOMEM (-2)

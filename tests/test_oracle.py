@@ -208,6 +208,57 @@ def test_planted_deepseek_mistakes_are_caught():
                    for t in texts), (rs, dm)
 
 
+def test_o200k_class_table_matches_reference_digest():
+    tab = classes.o200k_class_table()  # raises unless the digest matches
+    assert classes.npy_sha256(tab) == classes.O200K_TABLE_SHA256
+    assert tab[ord("A")] == 1 and tab[0x1C5] == 1      # Lu, Lt
+    assert tab[ord("b")] == 2 and tab[0x4E2D] == 3     # Ll, Lo
+    assert tab[0x2B0] == 3 and tab[ord("7")] == 4      # Lm, N
+    assert tab[ord(" ")] == 5 and tab[0x301] == 6 and tab[ord("!")] == 0
+
+
+#: each o200k class and the characters its rules name: U, L, Lo, Lm, Lt,
+#: a mark, a digit, P, space / tab / CR / LF, the apostrophe and the
+#: contraction letters in both cases (and U+017F, which folds to s), "/"
+O2K_ALPHABET = ["A", "b", "中", "ʰ", "ǅ", "\u0301", "1", ".", "!", " ", "\t",
+                "\n", "\r", "'", "s", "S", "ſ", "r", "e", "/"]
+
+
+def test_o200k_split_brute_force():
+    """The o200k restatement (oracle ruleset 4) splits like the certified
+    engine with the o200k pattern: every string of length <= 3 over the
+    alphabet, every length-5 string over a 10-symbol core, seeded fuzz."""
+    from tokenizers import Regex, pre_tokenizers
+    from oracle.oracle import Oracle
+    from toktier_amd.families import O200K_PATTERN
+    pre = pre_tokenizers.Split(Regex(O200K_PATTERN), behavior="isolated",
+                               invert=False)
+    o = Oracle(kit("gpt2").tables, classes.o200k_class_table(), None, 4, 3, False)
+
+    def hf(text):
+        offs = [b for _, b in pre.pre_tokenize_str(text)]
+        st = sorted({len(text[:a].encode("utf-8")) for a, _ in offs})
+        return st + [len(text.encode("utf-8"))]
+
+    core = ["A", "b", "中", "\u0301", ".", " ", "'", "s", "\n", "/"]
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 4)
+         for p in itertools.product(O2K_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(core, repeat=5)),
+    )
+    bad = [s for s in cases if o.pretokenize(s.encode("utf-8")) != hf(s)]
+    assert not bad, [repr(s) for s in bad[:10]]
+    rng = np.random.default_rng(9)
+    for _ in range(5000):
+        s = "".join(O2K_ALPHABET[int(i)] for i in
+                    rng.integers(0, len(O2K_ALPHABET), int(rng.integers(1, 40))))
+        assert o.pretokenize(s.encode("utf-8")) == hf(s), repr(s)
+    # planted: the cl100k rules on these classes disagree
+    wrong = Oracle(kit("gpt2").tables, classes.o200k_class_table(), None, 0, 3, False)
+    assert any(wrong.pretokenize(t.encode()) != hf(t)
+               for t in ("HelloWorld", "ABCdef", "x'S", "!\n/"))
+
+
 # ------------------------------------------------------------ encodes
 
 def _expected(k, text: str, ids: list[int]):

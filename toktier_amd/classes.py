@@ -24,8 +24,11 @@ CLASS_TABLE_SHA256 = "aab53c6705260d07f65d9762aecba729b18e11cb9710a4aea54157475c
 NFC_QC_SHA256 = "1a7d121e9092cdf577d992452393d25116b2577ab74dd5a067e6ca00a535d311"
 #: kernel_families.v1.json class_tables.deepseek_v1
 DEEPSEEK_TABLE_SHA256 = "b4242c04ffc981d9f457981546c43b2a82b53e3d18bf6f7d1ee1e7625c423bf7"
+#: kernel_families.v1.json class_tables.o200k_v4
+O200K_TABLE_SHA256 = "28e6d9e468b2c83db4188787515fa0e89d49750c20c966a9a89481aaf3b9e8ea"
 
-__all__ = ["class_table", "deepseek_class_table", "nfc_qc_table",
+__all__ = ["class_table", "deepseek_class_table", "o200k_class_table",
+           "nfc_qc_table",
            "npy_sha256", "PLANE", "table_for"]
 
 
@@ -63,6 +66,12 @@ def nfc_qc_table() -> np.ndarray:
 def deepseek_class_table() -> np.ndarray:
     """DeepSeek classes O=0 L=1 M=2 N=3 PS=4 WS=5 CRLF=6 for every codepoint."""
     return _load("classes_deepseek.npz", "deepseek", DEEPSEEK_TABLE_SHA256)
+
+
+@lru_cache(maxsize=None)
+def o200k_class_table() -> np.ndarray:
+    """o200k classes P=0 U=1 L=2 C=3 N=4 S=5 M=6 for every codepoint."""
+    return _load("classes_o200k.npz", "o200k", O200K_TABLE_SHA256)
 
 
 def table_for(ruleset_name: str) -> np.ndarray:

@@ -66,6 +66,16 @@ DEEPSEEK_STAGES = (
     "|\\s*[\r\n]+|\\s+(?!\\S)|\\s+",
 )
 
+#: o200k_base with contractions (gpt-oss; ``options.rs`` O200k row). The
+#: oracle restates it (ruleset 4 there); the device ruleset is not built.
+O200K_PATTERN = (
+    r"[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]*[\p{Ll}\p{Lm}\p{Lo}\p{M}]+"
+    r"(?i:'s|'t|'re|'ve|'m|'ll|'d)?"
+    r"|[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]+[\p{Ll}\p{Lm}\p{Lo}\p{M}]*"
+    r"(?i:'s|'t|'re|'ve|'m|'ll|'d)?"
+    r"|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n/]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+)
+
 #: The pattern HF ``ByteLevel(use_regex=True)`` applies (GPT-2).
 GPT2_PATTERN = (
     r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+"

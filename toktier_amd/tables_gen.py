@@ -109,6 +109,24 @@ def build_deepseek_classes() -> np.ndarray:
     return tab
 
 
+#: o200k seven-class encoding (kimi meta "class_enum" order, first seven)
+OK_P, OK_U, OK_L, OK_C, OK_N, OK_S, OK_M = range(7)
+
+
+def build_o200k_classes() -> np.ndarray:
+    """Seven classes for the o200k split: U (``\p{Lu}``, ``\p{Lt}``), L
+    (``\p{Ll}``), C (``\p{Lm}``, ``\p{Lo}``: both letter sets of the
+    pattern), N, S (``\s``), M and P (the rest). Reproduces the reference
+    table's sha256 (``kernel_families.v1.json`` ``o200k_v4``)."""
+    tab = np.full(PLANE, OK_P, dtype=np.uint8)
+    for val, pats in ((OK_U, (r"\p{Lu}", r"\p{Lt}")), (OK_L, (r"\p{Ll}",)),
+                      (OK_C, (r"\p{Lm}", r"\p{Lo}")), (OK_N, (r"\p{N}",)),
+                      (OK_S, (r"\s",)), (OK_M, (r"\p{M}",))):
+        for pat in pats:
+            tab[_probe_membership(pat)] = val
+    return tab
+
+
 def _batch_norm(norm, items: list[str]) -> list[str]:
     """Normalize many short strings at once, separated by U+0020 (a starter
     with no composition or decomposition role)."""
@@ -229,6 +247,9 @@ def main() -> None:
     ds = build_deepseek_classes()
     np.savez_compressed(TABLE_DIR / "classes_deepseek.npz", deepseek=ds)
     print("deepseek classes", np.bincount(ds, minlength=7), flush=True)
+    ok = build_o200k_classes()
+    np.savez_compressed(TABLE_DIR / "classes_o200k.npz", o200k=ok)
+    print("o200k classes", np.bincount(ok, minlength=7), flush=True)
     qc = build_nfc_qc()
     np.savez_compressed(TABLE_DIR / "nfc_qc.npz", nfc_qc=qc)
     print("nfc_qc 0:", int((qc == 0).sum()), "1..K:",
