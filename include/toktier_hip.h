@@ -160,6 +160,23 @@ int tk_engine_encode_device(tk_engine* engine, const void* d_text,
                             size_t nbytes, uint32_t flags, void* d_ids,
                             size_t ids_cap, size_t* n_ids, void* stream);
 
+/* Session seed: tk_engine_encode_device plus the sparse span checkpoints
+ * the session store adopts with the ids (replaces the span bridge of the
+ * GPU seed: crates/toktier-store-core/src/tail.rs:17-31 SpanCheckpoint,
+ * :173-205 build_span_checkpoints; SPAN_CHECKPOINT_STRIDE = 4096 there).
+ * For every token index k * stride below *n_ids, d_points[3k .. 3k+2]
+ * (device, uint64) receive: the token's first byte offset, the offset of
+ * the first byte of the character holding it, and that character's index
+ * in the text. *n_points = ceil(*n_ids / stride); TK_E_CAPACITY when that
+ * exceeds points_cap (the ids are valid then). The tokens close over the
+ * text by construction: the byte offsets are the prefix sums of the
+ * tokens' byte lengths. */
+int tk_engine_encode_seed(tk_engine* engine, const void* d_text,
+                          size_t nbytes, uint32_t flags, void* d_ids,
+                          size_t ids_cap, uint32_t stride, void* d_points,
+                          size_t points_cap, size_t* n_ids, size_t* n_points,
+                          void* stream);
+
 /* Added tokens of the artifact (tokenizer.json "added_tokens", in artifact
  * order): literal k is contents[offsets[k] .. offsets[k+1]) (UTF-8, 1..255
  * bytes, all distinct), its id ids[k], its flags flags[k] (TK_ADDED_*).

@@ -143,3 +143,49 @@ class Oracle:
         if n < 0:
             return int(n)
         return out[:n]
+
+
+def span_checkpoints(data: bytes, ids, token_len, stride: int) -> np.ndarray:
+    """The session store's sparse span checkpoints of an encoding, restated
+    from ``crates/toktier-store-core/src/tail.rs:173-205``
+    (``build_span_checkpoints``): walking the ids with a byte cursor (the
+    sum of the token byte lengths so far), at every token index that is a
+    multiple of ``stride`` record (byte, first byte of the character holding
+    it, that character's index). Raises unless the tokens close exactly
+    over ``data``. ``token_len[id]`` is the id's byte length."""
+    out = []
+    byte = 0
+    # characters before each byte offset: the lead bytes before it
+    lead = (np.frombuffer(data, dtype=np.uint8) & 0xC0) != 0x80
+    before = np.concatenate([[0], np.cumsum(lead)])
+    for k, t in enumerate(ids):
+        if k % stride == 0:
+            a = byte
+            while a > 0 and (data[a] & 0xC0) == 0x80:
+                a -= 1
+            out.append((byte, a, int(before[a])))
+        n = int(token_len[int(t)])
+        if n <= 0:
+            raise ValueError(f"id {int(t)} has no byte length")
+        byte += n
+    if byte != len(data):
+        raise ValueError(f"tokens close at byte {byte}, text has {len(data)}")
+    return np.asarray(out, dtype=np.uint64).reshape(-1, 3)
+
+
+def token_byte_lengths(tokenizer_json: str) -> np.ndarray:
+    """Byte length of every id of a byte-level BPE artifact: its vocabulary
+    string mapped back through the ByteLevel alphabet (printable bytes are
+    themselves, the others shifted to U+0100 onward); added tokens are their
+    UTF-8 contents."""
+    import json
+    spec = json.loads(tokenizer_json)
+    vocab = spec["model"]["vocab"]
+    added = spec.get("added_tokens") or []
+    n = max([*vocab.values(), *(a["id"] for a in added)], default=-1) + 1
+    out = np.zeros(n, dtype=np.int64)
+    for tok, i in vocab.items():
+        out[i] = len(tok)  # one alphabet character per byte
+    for a in added:
+        out[a["id"]] = len(a["content"].encode("utf-8"))
+    return out

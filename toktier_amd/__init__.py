@@ -134,6 +134,23 @@ class LiteralSplitter:
         return out
 
 
+#: token stride between span checkpoints of a session seed
+#: (``crates/toktier-store-core/src/tail.rs:17-18``)
+SPAN_CHECKPOINT_STRIDE = 4096
+
+
+@dataclass(frozen=True)
+class Seed:
+    """A session seed: ``ids`` and, for every token index ``k * stride``,
+    ``checkpoints[k] = (byte, anchor_byte, anchor_char)``: the token's first
+    byte, the first byte of the character holding it, that character's
+    index (``tail.rs:20-31``)."""
+
+    ids: np.ndarray
+    checkpoints: np.ndarray
+    stride: int
+
+
 class Tokenizer:
     """A family's tokenizer bound to one GPU engine."""
 
@@ -257,6 +274,32 @@ class Tokenizer:
 
     def encode(self, text: str) -> Encoding:
         return Encoding(self.encode_bytes(text.encode("utf-8")))
+
+    def seed(self, text: str, stride: int = SPAN_CHECKPOINT_STRIDE) -> "Seed":
+        """Ids plus the sparse span checkpoints the session store adopts
+        (``crates/toktier-store-core/src/tail.rs:173-205``), computed on the
+        device with the bytes resident in HBM. A text that fails the NFC
+        quick check raises (``TK_E_NEEDS_NFC``): the store seeds the
+        normalized text it holds."""
+        import torch
+        data = text.encode("utf-8")
+        dev = torch.device("cuda", self.engine.device)
+        n_pts_cap = max(1, len(data) // max(1, stride) + 1)
+        d_text = torch.frombuffer(bytearray(data or b"\0"), dtype=torch.uint8).to(dev)
+        d_ids = torch.empty(max(1, len(data)), dtype=torch.int32, device=dev)
+        d_pts = torch.empty(3 * n_pts_cap, dtype=torch.int64, device=dev)
+        n, m = self.engine.encode_seed(d_text.data_ptr(), len(data),
+                                       d_ids.data_ptr(), d_ids.numel(), stride,
+                                       d_pts.data_ptr(), n_pts_cap)
+        ids = d_ids[:n].cpu().numpy().view(np.uint32).copy()
+        pts = d_pts[:3 * m].cpu().numpy().view(np.uint64).reshape(m, 3).copy()
+        with self._lock:
+            c = self._counters
+            c.executions += 1
+            c.last_bytes = len(data)
+            c.last_ids = int(ids.size)
+            c.last_literals = self.engine.last_literals()
+        return Seed(ids, pts, stride)
 
     def encode_batch(self, texts: list[str]) -> list[Encoding]:
         """Row ``i`` equals ``encode(texts[i])``

@@ -49,6 +49,7 @@ STATUS_NAMES = {
 SYMBOLS = (
     "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
     "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
+    "tk_engine_encode_seed",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
     "tk_engine_last_literals", "tk_engine_driver_version", "tk_last_error",
@@ -110,6 +111,10 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_encode_device.restype = C.c_int
     L.tk_engine_encode_device.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
                                           C.POINTER(sz), vp]
+    L.tk_engine_encode_seed.restype = C.c_int
+    L.tk_engine_encode_seed.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
+                                        C.c_uint32, vp, sz, C.POINTER(sz),
+                                        C.POINTER(sz), vp]
     L.tk_engine_delivery.restype = C.c_char_p
     L.tk_engine_delivery.argtypes = [vp]
     L.tk_engine_architecture.restype = C.c_char_p
@@ -160,6 +165,7 @@ class Engine:
         check(self._L.tk_engine_open(C.byref(cfg), *args, C.byref(handle)),
               "tk_engine_open")
         self._h = handle
+        self.device = int(cfg.device_ordinal)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -212,6 +218,21 @@ class Engine:
                                              stream)
         check(st, "tk_engine_encode_device")
         return n.value
+
+    def encode_seed(self, d_text: int, nbytes: int, d_ids: int, ids_cap: int,
+                    stride: int, d_points: int, points_cap: int,
+                    flags: int = 0, stream: int | None = None
+                    ) -> tuple[int, int]:
+        """Device-resident encode plus span checkpoints (three uint64 per
+        checkpoint at d_points); returns (n_ids, n_points)."""
+        n = C.c_size_t()
+        m = C.c_size_t()
+        st = self._L.tk_engine_encode_seed(self._h, d_text, nbytes, flags,
+                                           d_ids, ids_cap, stride, d_points,
+                                           points_cap, C.byref(n), C.byref(m),
+                                           stream)
+        check(st, "tk_engine_encode_seed")
+        return n.value, m.value
 
     def set_added(self, contents: list[bytes], ids: list[int],
                   flags: list[int]) -> None:

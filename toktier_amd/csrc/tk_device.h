@@ -253,6 +253,11 @@ hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
 // k_added: the literal split of the request into w.docmask (read-write;
 // the document starts the caller marked, if any, are read from host_dm, a
 // different buffer, and kept)
+// session-seed checkpoints of the encode just compacted from w.tok (see
+// k_seed_points); ccount: (nb + COMPACT_BLOCK - 1) / COMPACT_BLOCK words
+hipError_t launch_seed(const DevWork& w, const uint8_t* text, int64_t nb,
+                       uint32_t n_points, uint32_t stride, uint32_t* ccount,
+                       uint64_t* pts, hipStream_t s);
 hipError_t launch_added(const DevAdded& a, const DevWork& w,
                         const uint64_t* host_dm, hipStream_t s,
                         hipEvent_t start = nullptr);

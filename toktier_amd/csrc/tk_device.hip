@@ -2631,6 +2631,128 @@ hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
   return hipGetLastError();
 }
 
+// ------------------------------------------------- session-seed checkpoints
+// The session store adopts an encoding as ids plus sparse span checkpoints:
+// for token k * stride (k = 0, 1, ...) its first byte, the first byte of
+// the character holding it, and that character's index
+// (crates/toktier-store-core/src/tail.rs:17-31, :173-205). Token j's id
+// sits at its first byte in tok, and k_compact leaves the tokens before
+// each COMPACT_BLOCK-byte block in blkprefix, so a checkpoint is found in
+// one block.
+
+// characters (UTF-8 lead bytes) of each COMPACT_BLOCK-byte block
+__global__ __launch_bounds__(COMPACT_TPB) void k_seed_chars(const uint8_t* text,
+                                                            int64_t nb,
+                                                            uint32_t* ccount) {
+  const int64_t p0 = (int64_t)blockIdx.x * COMPACT_BLOCK +
+                     (int64_t)threadIdx.x * COMPACT_PER_THREAD;
+  uint32_t c = 0;
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = p0 + k;
+    if (p < nb) c += !is_cont(text[p]);
+  }
+  uint32_t tot;
+  block_excl_scan(c, &tot);
+  if (threadIdx.x == 0) ccount[blockIdx.x] = tot;
+}
+
+// exclusive scan of the block counts, in place (one workgroup)
+__global__ __launch_bounds__(COMPACT_TPB) void k_seed_scan(uint32_t* ccount,
+                                                           int64_t nblk) {
+  uint32_t carry = 0;
+  for (int64_t base = 0; base < nblk; base += COMPACT_TPB) {
+    const int64_t j = base + threadIdx.x;
+    const uint32_t v = j < nblk ? ccount[j] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(v, &tot);
+    if (j < nblk) ccount[j] = carry + ex;
+    carry += tot;
+  }
+}
+
+// one workgroup per checkpoint k: token T = k * stride (T < the token
+// count, which the host checks); pts[3k..3k+2] = byte, anchor byte,
+// anchor character
+__global__ __launch_bounds__(COMPACT_TPB) void k_seed_points(
+    const uint32_t* tok, const uint8_t* text, int64_t nb,
+    const uint32_t* blkprefix, int64_t nblk, const uint32_t* cprefix,
+    uint32_t stride, uint64_t* pts) {
+  __shared__ int64_t s_b, s_pos;
+  const int tid = threadIdx.x;
+  const uint64_t T = (uint64_t)blockIdx.x * stride;
+  if (tid == 0) {
+    // the block holding token T: the last b with blkprefix[b] <= T
+    int64_t lo = 0, hi = nblk - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (blkprefix[mid] <= T) lo = mid;
+      else hi = mid - 1;
+    }
+    s_b = lo;
+    s_pos = -1;
+  }
+  __syncthreads();
+  const int64_t b = s_b;
+  const uint64_t r = T - blkprefix[b];
+  const int64_t p0 = b * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
+  uint32_t c = 0;
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = p0 + k;
+    c += p < nb && tok[p] != INVALID_ID;
+  }
+  uint32_t tot;
+  const uint32_t ex = block_excl_scan(c, &tot);
+  if (r >= ex && r < (uint64_t)ex + c) {
+    uint64_t q = ex;
+    for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+      const int64_t p = p0 + k;
+      if (p < nb && tok[p] != INVALID_ID) {
+        if (q == r) { s_pos = p; break; }
+        ++q;
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t pos = s_pos;
+  if (pos < 0) {  // not reached when T is below the token count
+    if (tid == 0) pts[3 * (int64_t)blockIdx.x] = ~0ULL;
+    return;
+  }
+  int64_t a = pos;
+  while (a > 0 && is_cont(text[a])) --a;
+  // characters before a: the blocks before a's, then a's block up to a
+  const int64_t ab = a / COMPACT_BLOCK;
+  const int64_t q0 = ab * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
+  uint32_t lc = 0;
+  for (int k = 0; k < COMPACT_PER_THREAD; ++k) {
+    const int64_t p = q0 + k;
+    if (p < a) lc += !is_cont(text[p]);
+  }
+  uint32_t ltot;
+  block_excl_scan(lc, &ltot);
+  if (tid == 0) {
+    uint64_t* o = pts + 3 * (int64_t)blockIdx.x;
+    o[0] = (uint64_t)pos;
+    o[1] = (uint64_t)a;
+    o[2] = (uint64_t)cprefix[ab] + ltot;
+  }
+}
+
+hipError_t launch_seed(const DevWork& w, const uint8_t* text, int64_t nb,
+                       uint32_t n_points, uint32_t stride, uint32_t* ccount,
+                       uint64_t* pts, hipStream_t s) {
+  const int64_t nblk = (nb + COMPACT_BLOCK - 1) / COMPACT_BLOCK;
+  if (nblk <= 0 || n_points == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_seed_chars, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0,
+                     s, text, nb, ccount);
+  hipLaunchKernelGGL(k_seed_scan, dim3(1), dim3(COMPACT_TPB), 0, s, ccount, nblk);
+  hipLaunchKernelGGL(k_seed_points, dim3(n_points), dim3(COMPACT_TPB), 0, s,
+                     (const uint32_t*)w.tok, text, nb,
+                     (const uint32_t*)w.blkprefix, nblk,
+                     (const uint32_t*)ccount, stride, pts);
+  return hipGetLastError();
+}
+
 // row d starts at the number of tokens whose first byte lies before
 // doc_offsets[d]
 __global__ void k_doc_offsets(DevWork w, const uint64_t* doc_offsets,

@@ -182,6 +182,7 @@ struct tk_engine {
   DevBuf<uint8_t> text;
   DevBuf<uint64_t> starts, docmask, heap, docoffs, rows, cstat;
   DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
+  DevBuf<uint32_t> seedc;  // per-block character counts (session seed)
   DevBuf<int32_t> nx, pv;
   DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
   DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk, plocal;
@@ -976,12 +977,12 @@ int tk_engine_driver_version(const tk_engine* e, int* version) {
 const char* tk_engine_delivery(const tk_engine* e) { return e ? "prebuilt" : ""; }
 const char* tk_engine_architecture(const tk_engine* e) { return e ? e->arch.c_str() : ""; }
 
-int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
-                            uint32_t flags, void* d_ids, size_t ids_cap,
-                            size_t* n_ids, void* stream) {
-  if (!e || !n_ids || (nbytes && (!d_text || !d_ids)))
-    return fail(TK_E_INVALID_ARG, "null argument");
-  std::lock_guard<std::mutex> lk(e->mu);
+namespace {
+
+// tk_engine_encode_device with the engine's lock held
+int device_encode(tk_engine* e, const void* d_text, size_t nbytes,
+                  uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
+                  void* stream) {
   *n_ids = 0;
   if (nbytes == 0) return TK_OK;
   HIP_TRY(hipSetDevice(e->device));
@@ -1001,6 +1002,50 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   if ((st & tk::ST_CAPACITY) || total > ids_cap)
     return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   *n_ids = total;
+  return TK_OK;
+}
+
+}  // namespace
+
+int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
+                            uint32_t flags, void* d_ids, size_t ids_cap,
+                            size_t* n_ids, void* stream) {
+  if (!e || !n_ids || (nbytes && (!d_text || !d_ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  return device_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
+}
+
+int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
+                          uint32_t flags, void* d_ids, size_t ids_cap,
+                          uint32_t stride, void* d_points, size_t points_cap,
+                          size_t* n_ids, size_t* n_points, void* stream) {
+  if (!e || !n_ids || !n_points || (nbytes && (!d_text || !d_ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  if (stride == 0) return fail(TK_E_INVALID_ARG, "stride must be positive");
+  std::lock_guard<std::mutex> lk(e->mu);
+  *n_points = 0;
+  int rc = device_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
+  if (rc != TK_OK || *n_ids == 0) return rc;
+  // one checkpoint at every token index that is a multiple of the stride
+  const size_t n = (*n_ids + stride - 1) / stride;
+  if (n > points_cap || !d_points)
+    return fail(TK_E_CAPACITY, "%zu checkpoints exceed the %zu-entry buffer", n,
+                points_cap);
+  if (n > 0x7FFFFFFFu) return fail(TK_E_CAPACITY, "too many checkpoints");
+  const size_t nblk = (nbytes + tk::COMPACT_BLOCK - 1) / tk::COMPACT_BLOCK;
+  if (e->seedc.n < nblk) HIP_TRY(e->seedc.alloc(nblk));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
+  // the pipeline's workspace still holds this encode's per-byte tokens
+  // and the compaction's block prefix
+  tk::DevWork w{};
+  w.tok = e->tok.p;
+  w.blkprefix = e->blkprefix.p;
+  HIP_TRY(tk::launch_seed(w, static_cast<const uint8_t*>(d_text), (int64_t)nbytes,
+                          (uint32_t)n, stride, e->seedc.p,
+                          static_cast<uint64_t*>(d_points), s));
+  HIP_TRY(hipStreamSynchronize(s));
+  *n_points = n;
   return TK_OK;
 }
 
