@@ -86,6 +86,10 @@ def main() -> int:
                     help="lay the config's text out as chat turns in the "
                          "family's template (added-token literals, split "
                          "out on the device)")
+    ap.add_argument("--seed", action="store_true",
+                    help="time the session seed instead (tk_engine_encode_seed: "
+                         "ids plus span checkpoints every 4096 tokens), a "
+                         "second workload line, not the contract line")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--no-check", action="store_true",
@@ -146,8 +150,16 @@ def main() -> int:
     torch.cuda.synchronize()
     eng.set_timing(2)  # k_bpe_pack's own dispatch only
 
+    stride = toktier_amd.SPAN_CHECKPOINT_STRIDE
+    n_pts = cap // stride + 1
+    d_pts = ([torch.empty(3 * n_pts, dtype=torch.int64, device=dev)
+              for _ in range(n_req)] if args.seed else [])
+
     def run(i):
         d = d_texts[i]
+        if args.seed:
+            return eng.encode_seed(d.data_ptr(), d.numel(), d_ids[i].data_ptr(),
+                                   cap, stride, d_pts[i].data_ptr(), n_pts)[0]
         return eng.encode_device(d.data_ptr(), d.numel(), d_ids[i].data_ptr(),
                                  cap)
 
@@ -202,6 +214,20 @@ def main() -> int:
             if isinstance(want, int) or not np.array_equal(want, ids_dev[i]):
                 mism += 1
         log(f"parity: {K - mism}/{K} requests bit-identical to the oracle")
+        if args.seed:
+            # the checkpoints of two requests against the store's restated
+            # construction over the oracle's ids
+            from oracle.oracle import span_checkpoints, token_byte_lengths
+            lens = token_byte_lengths(tok._json)
+            for t in tok.added_tokens:
+                lens[t.id] = len(t.content.encode("utf-8"))
+            for i in range(min(K, 2)):
+                m = (ids_dev[i].size + stride - 1) // stride
+                got = d_pts[i][:3 * m].cpu().numpy().view(np.uint64).reshape(m, 3)
+                want = span_checkpoints(reqs[i], ids_dev[i], lens, stride)
+                if not np.array_equal(got, want):
+                    mism += 1
+                    log(f"seed checkpoints differ on request {i}")
 
     n_tok = float(np.mean([a.size for a in ids_dev]))
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
@@ -255,10 +281,12 @@ def main() -> int:
         "data": "synthetic: seeded Zipf token-concat generator over the "
                 "stand-in vocabulary of the family",
         "config": {
-            "workload": f"C{args.config}{' chat' if args.chat else ''}: "
+            "workload": f"C{args.config}{' chat' if args.chat else ''}"
+                        f"{' seed' if args.seed else ''}: "
                         f"{fam}, one fresh request of {n_chars:,} chars"
                         f"{' in chat turns (added-token literals)' if args.chat else ''}"
-                        ", bytes resident in HBM",
+                        ", bytes resident in HBM"
+                        f"{'; ids plus span checkpoints every 4096 tokens (tk_engine_encode_seed)' if args.seed else ''}",
             "family": fam, "chars": n_chars, "bytes": int(n_bytes),
             "tokens": int(n_tok), "requests": K,
         },
@@ -280,7 +308,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": (None if args.chat or args.family else
+            "traffic": (None if args.chat or args.family or args.seed else
                         measured_traffic(args.config, "k_bpe_pack")),
             "alg_bytes_per_launch": int(b_alg),
             "path_achieved": round(b_alg / (ms_per_step * 1e-3) / 1e9, 3),
