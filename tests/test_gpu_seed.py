@@ -93,3 +93,9 @@ def test_seed_capacity_and_arguments():
                                 len(data), 4096, d_pts.data_ptr(), 1)
     assert n > 1000 and m == 1
     assert d_pts.cpu().tolist() == [0, 0, 0]
+
+
+def test_seed_past_one_launch_of_checkpoints():
+    """More than 2^22 checkpoints (stride 1 over 5,000,000 tokens): the
+    checkpoint workgroups go out in several launches."""
+    _check("gpt2", "a " * 5_000_000, 1)

@@ -2670,29 +2670,37 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_seed_scan(uint32_t* ccount,
   }
 }
 
-// one workgroup per checkpoint k: token T = k * stride (T < the token
-// count, which the host checks); pts[3k..3k+2] = byte, anchor byte,
-// anchor character
+// one workgroup per checkpoint k = first + blockIdx.x: token T = k * stride
+// (T < the token count, which the host checks); pts[3k..3k+2] = byte,
+// anchor byte, anchor character
 __global__ __launch_bounds__(COMPACT_TPB) void k_seed_points(
     const uint32_t* tok, const uint8_t* text, int64_t nb,
     const uint32_t* blkprefix, int64_t nblk, const uint32_t* cprefix,
-    uint32_t stride, uint64_t* pts) {
-  __shared__ int64_t s_b, s_pos;
+    uint32_t stride, uint32_t first, uint64_t* pts) {
+  __shared__ unsigned long long s_lo;
+  __shared__ int64_t s_pos;
   const int tid = threadIdx.x;
-  const uint64_t T = (uint64_t)blockIdx.x * stride;
-  if (tid == 0) {
-    // the block holding token T: the last b with blkprefix[b] <= T
-    int64_t lo = 0, hi = nblk - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) / 2;
-      if (blkprefix[mid] <= T) lo = mid;
-      else hi = mid - 1;
-    }
-    s_b = lo;
-    s_pos = -1;
+  const int64_t kpt = (int64_t)first + blockIdx.x;
+  const uint64_t T = (uint64_t)kpt * stride;
+  // The block holding token T: the last b in [0, nblk) with blkprefix[b]
+  // <= T (non-decreasing, blkprefix[0] = 0). Each round the workgroup
+  // samples COMPACT_TPB evenly spaced candidates of [lo, hi) and keeps the
+  // span after the last one at or below T: two rounds for a 4 MiB request.
+  int64_t lo = 0, hi = nblk;
+  while (hi - lo > 1) {
+    const int64_t step = (hi - lo + COMPACT_TPB - 1) / COMPACT_TPB;
+    if (tid == 0) s_lo = (unsigned long long)lo;
+    __syncthreads();
+    const int64_t j = lo + (int64_t)tid * step;
+    if (j < hi && blkprefix[j] <= T) atomicMax(&s_lo, (unsigned long long)j);
+    __syncthreads();
+    lo = (int64_t)s_lo;
+    hi = lo + step < hi ? lo + step : hi;
+    __syncthreads();  // every thread has read s_lo before the next round
   }
+  if (tid == 0) s_pos = -1;
   __syncthreads();
-  const int64_t b = s_b;
+  const int64_t b = lo;
   const uint64_t r = T - blkprefix[b];
   const int64_t p0 = b * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
   uint32_t c = 0;
@@ -2715,7 +2723,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_seed_points(
   __syncthreads();
   const int64_t pos = s_pos;
   if (pos < 0) {  // not reached when T is below the token count
-    if (tid == 0) pts[3 * (int64_t)blockIdx.x] = ~0ULL;
+    if (tid == 0) pts[3 * kpt] = ~0ULL;
     return;
   }
   int64_t a = pos;
@@ -2731,7 +2739,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_seed_points(
   uint32_t ltot;
   block_excl_scan(lc, &ltot);
   if (tid == 0) {
-    uint64_t* o = pts + 3 * (int64_t)blockIdx.x;
+    uint64_t* o = pts + 3 * kpt;
     o[0] = (uint64_t)pos;
     o[1] = (uint64_t)a;
     o[2] = (uint64_t)cprefix[ab] + ltot;
@@ -2746,10 +2754,16 @@ hipError_t launch_seed(const DevWork& w, const uint8_t* text, int64_t nb,
   hipLaunchKernelGGL(k_seed_chars, dim3((uint32_t)nblk), dim3(COMPACT_TPB), 0,
                      s, text, nb, ccount);
   hipLaunchKernelGGL(k_seed_scan, dim3(1), dim3(COMPACT_TPB), 0, s, ccount, nblk);
-  hipLaunchKernelGGL(k_seed_points, dim3(n_points), dim3(COMPACT_TPB), 0, s,
-                     (const uint32_t*)w.tok, text, nb,
-                     (const uint32_t*)w.blkprefix, nblk,
-                     (const uint32_t*)ccount, stride, pts);
+  // launches of at most 2^22 workgroups (grid size times workgroup size
+  // stays below 2^32)
+  constexpr uint32_t CHUNK = 1u << 22;
+  for (uint32_t first = 0; first < n_points; first += CHUNK) {
+    const uint32_t n = n_points - first < CHUNK ? n_points - first : CHUNK;
+    hipLaunchKernelGGL(k_seed_points, dim3(n), dim3(COMPACT_TPB), 0, s,
+                       (const uint32_t*)w.tok, text, nb,
+                       (const uint32_t*)w.blkprefix, nblk,
+                       (const uint32_t*)ccount, stride, first, pts);
+  }
   return hipGetLastError();
 }
 
