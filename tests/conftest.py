@@ -47,9 +47,9 @@ def pytest_runtest_logreport(report):
 def pytest_sessionfinish(session, exitstatus):
     """After a run that executed GPU parity tests on a device, write the
     evidence the gfx950 route rows are generated from
-    (``python -m toktier_amd.registry gpurun_out/gfx950_evidence.v1.json``):
-    the library's build key, the device architecture and driver, and the
-    outcome counts."""
+    (``python -m toktier_amd.registry <evidence file>``): the library's build
+    key, the device architecture and driver, and the outcome counts. It goes
+    to the output folder that GPU runs hand back."""
     if _GPU_OUTCOMES["passed"] + _GPU_OUTCOMES["failed"] == 0:
         return
     try:
