@@ -194,3 +194,24 @@ def test_device_resident_entry_and_determinism():
                                    d_ids.data_ptr(), len(data))
         got = d_ids[:n].cpu().numpy().view(np.uint32)
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["deepseek_v3", "laguna_s_2_1"])
+def test_batch_rows_equal_single_with_region_cuts(name):
+    """Document boundaries at arbitrary offsets of CJK / digit / newline
+    runs: every row equals the oracle's encode of that document alone."""
+    from toktier_amd import workloads
+    k, t = kit(name), tok(name)
+    rng = np.random.default_rng(21)
+    base = workloads.config5(k.json, n_chars=60_000, n_runs=2, run_chars=3_000)
+    base += "12345678901234 中文かな゛・テスト 99\n\n\r\n x " * 50
+    docs = []
+    at = 0
+    while at < len(base) and len(docs) < 300:
+        n = int(rng.integers(0, 400))
+        docs.append(base[at:at + n])
+        at += n
+    rows = t.encode_batch(docs)
+    for d, r in zip(docs, rows):
+        want = k.oracle.encode_bytes(d.encode("utf-8"))
+        assert np.array_equal(r.array, want), (name, d[:40])
