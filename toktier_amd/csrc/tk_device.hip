@@ -931,6 +931,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
       const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
       const uint64_t mHI = __ballot(bb >= 0x80);
+      // (deepseek) ASCII letters, for [ascii punct][A-Za-z]+ runs
+      const uint64_t mAL = RS == RS_DEEPSEEK ? __ballot(ascii_alpha((int)bb)) : 0ULL;
       // Every lane evaluates the fast predicate from the fixed context (only
       // selects); the lanes it leaves open (runs to walk, the general path)
       // are resolved in a section the wave enters only when it has any.
@@ -1006,6 +1008,32 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
               r = 1;
             } else if (f < 64 && !((mHI >> f) & 1)) {
               r = 1;
+            }
+          } else if (RS == RS_DEEPSEEK && r == FAST_GENERAL) {
+            // a letter / mark after an ASCII-alpha run longer than the
+            // context: it starts a piece exactly when the run was taken by
+            // [ascii punct][A-Za-z]+, i.e. the byte before the run is ASCII
+            // punctuation that starts its own match (no P/S or U+0020
+            // before it, or a document start at it). Resolved here when
+            // the run starts inside this word.
+            const uint64_t na = ~mAL & below;
+            if (na) {
+              const int h = 63 - __builtin_clzll(na);
+              const int64_t ph = i - (lane - h);  // the byte before the run
+              if (dmw & lanes_in(h + 1, lane)) {
+                r = 0;  // a document starts inside the run
+              } else if (!((mHI >> h) & 1)) {
+                const int bh = sb[64 * k + h + PT_PAD];
+                if (!ascii_punct(bh)) {
+                  r = 0;
+                } else if (ph == 0 || ((dmw >> h) & 1)) {
+                  r = 1;
+                } else {
+                  // the byte before the punctuation (staged even for h = 0)
+                  const int bq = sb[64 * k + h - 1 + PT_PAD];
+                  if (bq < 0x80) r = !(ascii_punct(bq) || bq == ' ');
+                }
+              }
             }
           }
           if (r == FAST_DIGITS) {
