@@ -32,6 +32,18 @@ def _gpu_available() -> bool:
 
 
 _GPU_OUTCOMES = {"passed": 0, "failed": 0, "skipped": 0}
+# per family (a test whose parameters name a family), and "shared" for the
+# GPU tests that cover no single family
+_FAMILY_OUTCOMES: dict[str, dict[str, int]] = {}
+_SELECTION = {"deselected_gpu": 0}
+
+
+def _family_of(nodeid: str) -> str:
+    params = nodeid.split("[", 1)[1] if "[" in nodeid else ""
+    for name in FAMILY_NAMES:
+        if name in params:
+            return name
+    return "shared"
 
 
 def pytest_runtest_logreport(report):
@@ -42,20 +54,40 @@ def pytest_runtest_logreport(report):
         key = ("passed" if report.passed else
                "skipped" if report.skipped else "failed")
         _GPU_OUTCOMES[key] += 1
+        fam = _FAMILY_OUTCOMES.setdefault(
+            _family_of(report.nodeid), {"passed": 0, "failed": 0, "skipped": 0})
+        fam[key] += 1
+
+
+def pytest_deselected(items):
+    _SELECTION["deselected_gpu"] += sum(1 for i in items if "gpu" in i.keywords)
+
+
+def _complete_selection(config) -> bool:
+    """The whole GPU suite was selected: no -k, every gpu-marked test of
+    the tests directory collected and none deselected."""
+    if getattr(config.option, "keyword", ""):
+        return False
+    if _SELECTION["deselected_gpu"]:
+        return False
+    tests_dir = Path(__file__).resolve().parent
+    args = [Path(str(a).split("::", 1)[0]).resolve() for a in config.args]
+    return any(a in (tests_dir, ROOT) for a in args)
 
 
 def pytest_sessionfinish(session, exitstatus):
     """After a run that executed GPU parity tests on a device, write the
     evidence the gfx950 route rows are generated from
     (``python -m toktier_amd.registry <evidence file>``): the library's build
-    key, the device architecture and driver, and the outcome counts. It goes
-    to the output folder that GPU runs hand back."""
+    key, the device architecture and driver, the outcome counts overall and
+    per family, and whether the whole GPU suite was selected. It goes to the
+    output folder that GPU runs hand back."""
     if _GPU_OUTCOMES["passed"] + _GPU_OUTCOMES["failed"] == 0:
         return
     try:
         import json
         import torch
-        from toktier_amd._build import MANIFEST
+        from toktier_amd._build import MANIFEST, verify
         if not torch.cuda.is_available():
             return
         arch = torch.cuda.get_device_properties(0).gcnArchName.split(":")[0]
@@ -66,8 +98,18 @@ def pytest_sessionfinish(session, exitstatus):
         t.close()
         ev = {"evidence_id": f"ev-gfx950-parity-{man['build_key'][:12]}",
               "suite": "tests -m gpu", "build_key": man["build_key"],
+              "build_mismatch": verify(man),
               "architecture": arch, "driver_version": driver,
-              "hip_version": torch.version.hip, **_GPU_OUTCOMES}
+              "hip_version": torch.version.hip, **_GPU_OUTCOMES,
+              "families": _FAMILY_OUTCOMES,
+              "selection": {
+                  "complete": _complete_selection(session.config),
+                  "collected_gpu": session.testscollected and sum(
+                      1 for i in session.items if "gpu" in i.keywords),
+                  "deselected_gpu": _SELECTION["deselected_gpu"],
+                  "markexpr": getattr(session.config.option, "markexpr", ""),
+                  "keyword": getattr(session.config.option, "keyword", ""),
+                  "exitstatus": int(exitstatus)}}
         out = ROOT / "gpurun_out"
         out.mkdir(exist_ok=True)
         (out / "gfx950_evidence.v1.json").write_text(

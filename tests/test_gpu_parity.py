@@ -215,3 +215,35 @@ def test_batch_rows_equal_single_with_region_cuts(name):
     for d, r in zip(docs, rows):
         want = k.oracle.encode_bytes(d.encode("utf-8"))
         assert np.array_equal(r.array, want), (name, d[:40])
+
+
+# DeepSeek's `[ascii punct][A-Za-z]+` alternative meets an accented letter
+# after a run of three or more ASCII letters (the word-level branch of the
+# fast predicate): every arm of the character before the punctuation, a
+# run that crosses a 64-byte word, and document starts at the punctuation
+# and inside the run
+DEEPSEEK_PUNCT_RUNS = [
+    " !abcdé", "!!abcdé", "a!abcdé", "1!abcdé", "!abcdé", "x" * 60 + "!abcdé",
+    "\t!abcdé", "x" * 61 + " !abcdé", "é!abcdé", "中!abcdé", "!abcdéfg!hij",
+    " !abcdé " * 20, "\n!abcdé", "ab!cdé", "!" + "q" * 70 + "é",
+]
+
+
+def test_deepseek_punct_letter_runs_match_hf():
+    k, t = kit("deepseek_v3"), tok("deepseek_v3")
+    for s in DEEPSEEK_PUNCT_RUNS:
+        assert list(t.encode(s).array) == k.hf_ids(s), s
+        for pre in ("", "z", " ", "x" * 40):
+            u = pre + s + "é"
+            assert list(t.encode(u).array) == k.hf_ids(u), u
+
+
+def test_deepseek_batch_rows_cut_at_the_punctuation_and_inside_the_run():
+    k, t = kit("deepseek_v3"), tok("deepseek_v3")
+    for s in DEEPSEEK_PUNCT_RUNS:
+        p = s.index("!")
+        for cut in sorted({p, p + 1, p + 2, min(len(s), p + 4), len(s) - 1}):
+            docs = [s[:cut], s[cut:], s]
+            rows = t.encode_batch(docs)
+            for d, r in zip(docs, rows):
+                assert list(r.array) == k.hf_ids(d), (s, cut, d)

@@ -95,22 +95,93 @@ def test_checks_run_in_the_reference_order():
     assert _codes(dead) == [R.R_SM_UNCERTIFIED, R.R_KERNEL_BUILD_FAILED]
 
 
+def _evidence(**kw):
+    ev = {"evidence_id": "ev1", "build_key": KEY, "build_mismatch": None,
+          "architecture": "gfx950", "passed": 40, "failed": 0, "skipped": 0,
+          "driver_version": 70226015,
+          "families": {"qwen3_8b": {"passed": 30, "failed": 0, "skipped": 0},
+                       "gpt2": {"passed": 0, "failed": 0, "skipped": 0},
+                       "shared": {"passed": 10, "failed": 0, "skipped": 0}},
+          "selection": {"complete": True, "collected_gpu": 40,
+                        "deselected_gpu": 0, "markexpr": "gpu", "keyword": ""}}
+    ev.update(kw)
+    return ev
+
+
+def _status(reg, i=0):
+    return reg["artifacts"][i]["backends"]["gpu"]["deliveries"]["prebuilt"]
+
+
 def test_generate_certifies_only_a_judged_build():
     man = {"build_key": KEY, "hipcc": ["HIP version: 7.2"], "flags": ["-O3"]}
-    ok = {"evidence_id": "ev1", "build_key": KEY, "architecture": "gfx950",
-          "passed": 40, "failed": 0, "skipped": 0, "driver_version": 70226015}
-    reg = R.generate(ok, man, {"qwen3_8b": SHA})
-    row = reg["artifacts"][0]["backends"]["gpu"]["deliveries"]["prebuilt"]
+    reg = R.generate(_evidence(), man, {"qwen3_8b": SHA})
+    row = _status(reg)
     assert row["status"] == R.STATUS_CERTIFIED and row["devices"] == ["gfx950"]
+    assert row["readings"] == {"passed": 30, "failed": 0, "skipped": 0}
     assert R.architecture_statuses(row) == {"gfx950": R.STATUS_CERTIFIED}
     assert R.admit(reg, SHA, _facts(), R.POLICY_CERTIFIED).admitted
+    sel = _evidence()["selection"]
     for bad in (dict(failed=1), dict(build_key="b" * 64),
-                dict(architecture="gfx942"), dict(passed=0)):
-        reg = R.generate({**ok, **bad}, man, {"qwen3_8b": SHA})
-        row = reg["artifacts"][0]["backends"]["gpu"]["deliveries"]["prebuilt"]
+                dict(architecture="gfx942"), dict(passed=0),
+                dict(skipped=1),
+                dict(build_mismatch="library bytes differ from the manifest"),
+                # a subset of the suite (-k, deselected tests, a single file)
+                dict(selection={**sel, "complete": False}),
+                dict(selection={**sel, "deselected_gpu": 3}),
+                dict(selection={**sel, "collected_gpu": 41}),
+                # the family's own tests failed, were skipped or never ran
+                dict(families={"qwen3_8b": {"passed": 29, "failed": 1, "skipped": 0}}),
+                dict(families={"qwen3_8b": {"passed": 29, "failed": 0, "skipped": 1}}),
+                dict(families={"shared": {"passed": 40, "failed": 0, "skipped": 0}}),
+                dict(families=None)):
+        reg = R.generate(_evidence(**bad), man, {"qwen3_8b": SHA})
+        row = _status(reg)
         assert row["status"] == R.STATUS_EXPERIMENTAL, bad
         assert R.architecture_statuses(row) == {"gfx950": R.STATUS_EXPERIMENTAL}
         assert not R.admit(reg, SHA, _facts(), R.POLICY_CERTIFIED).admitted
+
+
+def test_generate_judges_each_family_on_its_own_tests():
+    # gpt2's parity tests did not run in this evidence: its row stays
+    # experimental while qwen3's is certified
+    man = {"build_key": KEY, "hipcc": [], "flags": []}
+    reg = R.generate(_evidence(), man, {"qwen3_8b": SHA, "gpt2": "b" * 64})
+    by_family = {a["family"]: a["backends"]["gpu"]["status"]
+                 for a in reg["artifacts"]}
+    assert by_family == {"qwen3_8b": R.STATUS_CERTIFIED,
+                         "gpt2": R.STATUS_EXPERIMENTAL}
+
+
+def test_a_library_that_is_not_the_manifest_build_is_refused():
+    facts = _facts(build_mismatch="sources changed since the build: csrc/tk_device.h")
+    strict = R.admit(_row(), SHA, facts, R.POLICY_CERTIFIED)
+    assert not strict.admitted
+    assert _codes(strict) == [R.R_KERNEL_DIGEST_MISMATCH]
+    assert strict.refusals[0].detail["cause"].startswith("sources changed")
+    loose = R.admit(_row(), SHA, facts, R.POLICY_EXPERIMENTAL)
+    assert loose.admitted and [w.code for w in loose.waivers] == [
+        R.R_KERNEL_DIGEST_MISMATCH]
+
+
+def test_build_key_covers_every_source_and_the_abi_header(tmp_path, monkeypatch):
+    from toktier_amd import _build
+    names = set(_build.hashed_files())
+    assert "include/toktier_hip.h" in names
+    assert {"csrc/tk_device.h", "csrc/tk_device.hip", "csrc/tk_added.hip",
+            "csrc/tk_engine.cpp"} <= names
+    # an edit to a header alone changes the key and is caught by verify()
+    base = _build.source_digests()
+    k0 = _build.build_key(base, ["-O3"], ["v"])
+    edited = dict(base, **{"csrc/tk_device.h": "0" * 64})
+    assert _build.build_key(edited, ["-O3"], ["v"]) != k0
+    man = {"sha256": "x", "sources": base}
+    lib = tmp_path / "lib.so"
+    lib.write_bytes(b"abc")
+    monkeypatch.setattr(_build, "LIB", lib)
+    man["sha256"] = _build.library_digest(lib)
+    assert _build.verify(man) is None
+    assert "sources changed" in _build.verify(dict(man, sources=edited))
+    assert "library bytes" in _build.verify(dict(man, sha256="0" * 64))
 
 
 def test_root_digest_binds_the_rows(tmp_path):

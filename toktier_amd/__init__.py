@@ -207,7 +207,7 @@ class Tokenizer:
     def _admit(self, policy: str) -> "registry.Admission":
         """The gfx950 route's admission from the committed registry rows
         (reference planner checks, ``routing/plan.py:1-39``)."""
-        from ._build import MANIFEST
+        from ._build import MANIFEST, verify
         try:
             reg = registry.load_registry()
         except (OSError, ValueError):
@@ -218,7 +218,8 @@ class Tokenizer:
         facts = registry.Facts(
             library_loaded=True, build_key=build_key, build_failed=False,
             architectures=(self.engine.architecture,),
-            driver_version=self.engine.driver_version)
+            driver_version=self.engine.driver_version,
+            build_mismatch=verify())
         return registry.admit(reg, self.artifact_sha256, facts, policy)
 
     # -- exact normalization for texts that fail the device quick check

@@ -16,13 +16,36 @@ import sys
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
 CSRC = PKG / "csrc"
+ABI_HEADER = ROOT / "include" / "toktier_hip.h"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libtoktier_hip.so"
 MANIFEST = LIBDIR / "manifest.json"
 ARCH = "gfx950"
 
 SOURCES = ["tk_device.hip", "tk_added.hip", "tk_engine.cpp"]
+
+
+def hashed_files() -> dict[str, Path]:
+    """Every file the code object depends on, by the name the manifest
+    records: all of ``csrc/`` (the compiled sources and the headers they
+    include) and the C-ABI header."""
+    files = {f"csrc/{f.name}": f for f in sorted(CSRC.iterdir())
+             if f.is_file() and f.suffix in (".hip", ".cpp", ".h")}
+    files["include/toktier_hip.h"] = ABI_HEADER
+    return files
+
+
+def source_digests() -> dict[str, str]:
+    return {name: hashlib.sha256(f.read_bytes()).hexdigest()
+            for name, f in hashed_files().items()}
+
+
+def library_digest(lib: Path | None = None) -> str:
+    lib = LIB if lib is None else lib
+    return hashlib.sha256(b"toktier-hip-lib\0" + lib.read_bytes()).hexdigest()
+
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -74,9 +97,8 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     ver = subprocess.run([_hipcc(), "--version"], capture_output=True,
                          text=True).stdout.strip().splitlines()
-    digest = hashlib.sha256(b"toktier-hip-lib\0" + LIB.read_bytes()).hexdigest()
-    sources = {s: hashlib.sha256((CSRC / s).read_bytes()).hexdigest()
-               for s in SOURCES}
+    digest = library_digest()
+    sources = source_digests()
     MANIFEST.write_text(json.dumps({
         "library": LIB.name,
         "sha256_domain": "toktier-hip-lib",
@@ -89,6 +111,26 @@ def build(verbose: bool = False) -> Path:
         "symbols": exported_symbols(LIB),
     }, indent=1) + "\n")
     return LIB
+
+
+def verify(manifest: dict | None = None) -> str | None:
+    """None when the library on disk is the one the manifest describes and
+    the sources it was built from are unchanged; else what differs (a
+    stale library, or sources edited after the build)."""
+    try:
+        m = manifest if manifest is not None else json.loads(MANIFEST.read_text())
+    except (OSError, ValueError) as err:
+        return f"manifest unreadable: {err}"
+    if not LIB.exists():
+        return "library missing"
+    if library_digest() != m.get("sha256"):
+        return "library bytes differ from the manifest"
+    now = source_digests()
+    was = m.get("sources", {})
+    changed = sorted(k for k in set(now) | set(was) if now.get(k) != was.get(k))
+    if changed:
+        return "sources changed since the build: " + ", ".join(changed)
+    return None
 
 
 if __name__ == "__main__":

@@ -186,8 +186,13 @@ class Engine:
     def architecture(self) -> str:
         return self._L.tk_engine_architecture(self._h).decode()
 
-    def encode(self, data: bytes, flags: int = 0) -> np.ndarray:
-        out = np.empty(max(1, len(data)), dtype=np.uint32)
+    def encode(self, data: bytes, flags: int = 0,
+               out: np.ndarray | None = None) -> np.ndarray:
+        """Host bytes in, host ids out. ``out``: a reusable uint32 buffer of
+        at least ``len(data)`` entries (the result is a view of it)."""
+        if (out is None or out.dtype != np.uint32 or out.ndim != 1
+                or not out.flags.c_contiguous or out.size < max(1, len(data))):
+            out = np.empty(max(1, len(data)), dtype=np.uint32)
         n = C.c_size_t()
         st = self._L.tk_engine_encode(self._h, data, len(data), flags,
                                       out.ctypes.data, out.size, C.byref(n))

@@ -68,6 +68,9 @@ class Facts:
     architectures: tuple[str, ...]  # of the devices the probe saw
     driver_version: int | None      # hipDriverGetVersion
     oracle_version: str | None = ORACLE["version"]
+    # why the loaded library is not the build the manifest names (its bytes
+    # differ, or the sources changed since it was built); None when it is
+    build_mismatch: str | None = None
 
 
 @dataclass(frozen=True)
@@ -207,8 +210,15 @@ def admit(reg: dict | None, artifact_sha256: str, facts: Facts,
     if facts.build_failed:
         refuse(R_KERNEL_BUILD_FAILED, False)
         return verdict(row, False)
-    # 12. bound digest: the code object the row was judged on
-    if row.get("binary_digest") != facts.build_key:
+    # 12. bound digest: the code object the row was judged on (a library
+    # that is not the manifest's build, or sources edited after it, carry
+    # no judged digest at all)
+    if facts.build_mismatch is not None:
+        if not refuse(R_KERNEL_DIGEST_MISMATCH, True,
+                      expected_digest=row.get("binary_digest"),
+                      observed_digest=None, cause=facts.build_mismatch):
+            return verdict(row, False)
+    elif row.get("binary_digest") != facts.build_key:
         if not refuse(R_KERNEL_DIGEST_MISMATCH, True,
                       expected_digest=row.get("binary_digest"),
                       observed_digest=facts.build_key):
@@ -218,18 +228,46 @@ def admit(reg: dict | None, artifact_sha256: str, facts: Facts,
 
 # ------------------------------------------------------- generating rows
 
+def suite_judged(evidence: dict, manifest: dict) -> bool:
+    """The evidence is a complete, clean run of the GPU suite on this very
+    build on gfx950: the library was the manifest's build, the whole
+    ``-m gpu`` selection ran (no ``-k``, nothing deselected), and no test
+    failed or was skipped."""
+    sel = evidence.get("selection") or {}
+    ran = (evidence.get("passed", 0) + evidence.get("failed", 0)
+           + evidence.get("skipped", 0))
+    return (evidence.get("build_key") == manifest["build_key"]
+            and evidence.get("build_mismatch") is None
+            and evidence.get("architecture") == ARCH
+            and evidence.get("failed", 1) == 0
+            and evidence.get("skipped", 1) == 0
+            and evidence.get("passed", 0) > 0
+            and sel.get("complete") is True
+            and sel.get("deselected_gpu", 1) == 0
+            and sel.get("collected_gpu") == ran)
+
+
+def family_judged(evidence: dict, manifest: dict, family: str) -> bool:
+    """Certified for `family`: the suite as a whole is judged, and the
+    family's own parity tests ran and all passed."""
+    fam = (evidence.get("families") or {}).get(family) or {}
+    return (suite_judged(evidence, manifest)
+            and fam.get("passed", 0) > 0
+            and fam.get("failed", 1) == 0
+            and fam.get("skipped", 1) == 0)
+
+
 def generate(evidence: dict, manifest: dict, artifacts: dict[str, str]) -> dict:
     """Registry rows for `artifacts` (family -> artifact sha256) from the
     library manifest and the evidence the GPU parity suite wrote. A row is
-    certified when the evidence is for this build key, on gfx950, with no
-    failed or skipped parity test."""
-    judged = (evidence.get("build_key") == manifest["build_key"]
-              and evidence.get("architecture") == ARCH
-              and evidence.get("failed", 1) == 0
-              and evidence.get("passed", 0) > 0)
-    status = STATUS_CERTIFIED if judged else STATUS_EXPERIMENTAL
+    certified only when the whole suite ran clean on this build on gfx950
+    (``suite_judged``) and the family's own tests ran and passed
+    (``family_judged``); otherwise it is experimental."""
     rows = []
     for family, sha in sorted(artifacts.items()):
+        judged = family_judged(evidence, manifest, family)
+        status = STATUS_CERTIFIED if judged else STATUS_EXPERIMENTAL
+        fam = (evidence.get("families") or {}).get(family) or {}
         rows.append({
             "artifact_sha256": sha,
             "family": family,
@@ -246,7 +284,7 @@ def generate(evidence: dict, manifest: dict, artifacts: dict[str, str]) -> dict:
                     "devices": [ARCH] if judged else [],
                     "devices_experimental": [] if judged else [ARCH],
                     "driver_min": evidence.get("driver_version"),
-                    "readings": {k: evidence.get(k) for k in
+                    "readings": {k: fam.get(k) for k in
                                  ("passed", "failed", "skipped")},
                 }},
             }},
