@@ -196,6 +196,18 @@ int tk_engine_set_added(tk_engine* engine, size_t n, const uint8_t* contents,
 /* Literals extracted by the last encode on this engine. */
 int tk_engine_last_literals(const tk_engine* engine, uint64_t* n);
 
+/* Facts of the last encode on this engine (the reference's per-execution
+ * ledger facts, runtime.rs:641-697, as counts): [0] added-token literals
+ * extracted, [1] pieces over 64 bytes, [2] pieces over 512 bytes (cut and
+ * certified), [3] certification repair passes (each removes the cuts whose
+ * certificate failed and redoes the joined segments). Returns the number
+ * of values written (<= n). */
+#define TK_STAT_LITERALS 0
+#define TK_STAT_LONG 1
+#define TK_STAT_BIG 2
+#define TK_STAT_REPAIRS 3
+int tk_engine_last_stats(const tk_engine* engine, uint64_t* out, int n);
+
 /* HIP driver version of the engine's device (hipDriverGetVersion; the
  * reference driver surface's driver_version(), cuda-driver lib.rs:51-86),
  * for the route's driver floor. */

@@ -247,3 +247,42 @@ def test_deepseek_batch_rows_cut_at_the_punctuation_and_inside_the_run():
             rows = t.encode_batch(docs)
             for d, r in zip(docs, rows):
                 assert list(r.array) == k.hf_ids(d), (s, cut, d)
+
+
+@pytest.mark.parametrize("name", ["llama_3_1_8b", "qwen3_8b"])
+def test_c5_style_long_runs_match_oracle_and_repairs_run(name):
+    """C5's text (ten 65,536-char letter runs, five Latin and five CJK) at
+    full size: the pieces over 512 bytes are cut and certified (from the
+    first / last-token events on the monotone Qwen table, from every merge
+    round on the non-monotone Llama table), some cuts fail and are
+    repaired, and the ids equal the oracle's."""
+    from toktier_amd import workloads
+    k, t = kit(name), tok(name)
+    for sample in (0, 3):
+        data = workloads.config5(k.json, sample=sample).encode()
+        got = t.encode_bytes(data)
+        st = t.engine.last_stats()
+        want = k.oracle.encode_bytes(data)
+        assert not isinstance(want, int)
+        assert np.array_equal(got, want), (name, sample)
+        assert st["big_pieces"] >= 10, st
+        assert st["repair_passes"] > 0, st
+        assert t.explain()["last_execution"]["repair_passes"] == st["repair_passes"]
+
+
+def test_non_monotone_long_pieces_match_hf():
+    """Pieces over 512 bytes on the non-monotone Llama table (flagged
+    ranks), against the certified engine."""
+    k, t = kit("llama_3_1_8b"), tok("llama_3_1_8b")
+    from toktier_amd import workloads
+    base = workloads.config5(k.json, n_chars=200_000, n_runs=4,
+                             run_chars=3_000, sample=11)
+    letters = "".join(ch for ch in base if ch.isalpha())
+    rng = np.random.default_rng(13)
+    for _ in range(12):
+        n = int(rng.integers(513, 9000))
+        a = int(rng.integers(0, len(letters) - n))
+        s = " " + letters[a:a + n]
+        assert list(t.encode(s).array) == k.hf_ids(s), (n, s[:60])
+    for s in ("a" * 3000, "ab" * 1500, "xyz" * 700 + "中" * 400):
+        assert list(t.encode(s).array) == k.hf_ids(s), s[:40]

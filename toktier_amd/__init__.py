@@ -59,6 +59,7 @@ class _Counters:
     last_ids: int = 0
     last_stage_us: list = field(default_factory=list)
     last_literals: int = 0
+    last_stats: dict = field(default_factory=dict)
 
 
 @dataclass(frozen=True)
@@ -271,6 +272,7 @@ class Tokenizer:
             c.last_bytes = len(data)
             c.last_ids = int(ids.size)
             c.last_literals = self.engine.last_literals()
+            c.last_stats = self.engine.last_stats()
         return ids
 
     def encode(self, text: str) -> Encoding:
@@ -300,6 +302,7 @@ class Tokenizer:
             c.last_bytes = len(data)
             c.last_ids = int(ids.size)
             c.last_literals = self.engine.last_literals()
+            c.last_stats = self.engine.last_stats()
         return Seed(ids, pts, stride)
 
     def encode_batch(self, texts: list[str]) -> list[Encoding]:
@@ -350,7 +353,8 @@ class Tokenizer:
             "nfc_renormalized": c.renormalized,
             "added_tokens": len(self.added_tokens),
             "added_token_frontend": "device" if self.added_tokens else None,
-            "last_execution": {"bytes": c.last_bytes, "ids": c.last_ids,
+            "last_execution": {**c.last_stats,
+                               "bytes": c.last_bytes, "ids": c.last_ids,
                                "added_literals": c.last_literals},
         }
 

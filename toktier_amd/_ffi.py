@@ -52,7 +52,8 @@ SYMBOLS = (
     "tk_engine_encode_seed",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
-    "tk_engine_last_literals", "tk_engine_driver_version", "tk_last_error",
+    "tk_engine_last_literals", "tk_engine_last_stats",
+    "tk_engine_driver_version", "tk_last_error",
 )
 
 
@@ -129,6 +130,8 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_driver_version.argtypes = [vp, C.POINTER(C.c_int)]
     L.tk_engine_last_literals.restype = C.c_int
     L.tk_engine_last_literals.argtypes = [vp, C.POINTER(C.c_uint64)]
+    L.tk_engine_last_stats.restype = C.c_int
+    L.tk_engine_last_stats.argtypes = [vp, C.POINTER(C.c_uint64), C.c_int]
     if path is None:
         _lib = L
     return L
@@ -267,6 +270,16 @@ class Engine:
         check(self._L.tk_engine_last_literals(self._h, C.byref(n)),
               "tk_engine_last_literals")
         return int(n.value)
+
+    def last_stats(self) -> dict[str, int]:
+        """Facts of the last encode: literals extracted, pieces over 64
+        and over 512 bytes, certification repair passes."""
+        buf = (C.c_uint64 * 4)()
+        k = self._L.tk_engine_last_stats(self._h, buf, 4)
+        if k < 0:
+            check(k, "tk_engine_last_stats")
+        names = ("literals", "long_pieces", "big_pieces", "repair_passes")
+        return {n: int(buf[i]) for i, n in enumerate(names[:k])}
 
     def set_timing(self, mode: int) -> None:
         """0 off, 1 (or True) every stage, 2 the packed merge kernel only."""

@@ -61,8 +61,12 @@ struct DevTables {
   int32_t dmax;                // digit group width (cl100k)
   int32_t ignore_merges;
   int32_t needs_nfc;
-  int32_t cert;                // long pieces may be cut and certified:
-                               // rank-ordered table, every byte has an id
+  int32_t cert;                // long pieces over 512 bytes: 0 merged
+                               // serially (a byte without an id); 1 cut and
+                               // certified from first / last-token events
+                               // (every rule that consumes a token ranks
+                               // above the rule that makes it); 2 cut and
+                               // certified from every merge round (any table)
   int32_t all_bytes;           // every byte has an id (no dropped bytes)
   const uint32_t* unsafe;      // unsafe-rank bitmap or nullptr
   uint32_t unsafe_words;
@@ -100,8 +104,9 @@ struct DevWork {
   uint64_t* cuts;        // candidate segment starts inside long pieces
   uint64_t* failm;       // cuts whose certificate failed this pass
   uint64_t* hfirst;      // first-token merge events, at the segment start
+                         // (cert 2: every merge round, see HR_FIRST)
   uint64_t* hlast;       // last-token merge events, at the segment start
-  uint32_t* hmeta;       // event counts (first | last << 16)
+  uint32_t* hmeta;       // event counts (first | last << 16; cert 2: rounds)
   uint32_t* seglist;     // segments that fit no grid window
   uint32_t* segcount;    // ctrl[3]
   uint32_t seg_cap;
@@ -130,6 +135,13 @@ struct DevWork {
   int64_t clear_words;   // inlong / failm words
   int64_t clear_dwords;  // dirty_next words
 };
+
+// A merge-round record of a segment (cert 2): rank << 32 | flags | product
+// id. HR_FIRST / HR_LAST: the round changed the segment's first / last
+// token (into the product). A round merges one pair, or every leftmost
+// non-overlapping occurrence of a rank whose product no earlier rule
+// consumes.
+constexpr uint64_t HR_FIRST = 1ull << 31, HR_LAST = 1ull << 30;
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,

@@ -1309,7 +1309,17 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     const uint64_t stop = rrec | rstarts;
     const uint64_t wm = __brevll(((~stop + rends) & stop) & rrec);
     const bool win_ = lane_bit(wm);
-    if (hist) {
+    if (hist && t.cert == 2) {
+      // every merge of the segment, in order (one per round here)
+      const uint32_t nr = __shfl(nfirst, src_ps);
+      if (win_) {
+        const bool lastev = nx + 1 >= pe || ((live & lanes_in(nx + 1, pe)) == 0);
+        w.hfirst[base + ps + nr] =
+            ((uint64_t)((kx >> 6) & 0xFFFFFu) << 32) |
+            (lane == ps ? HR_FIRST : 0) | (lastev ? HR_LAST : 0) | mid;
+      }
+      if (elig && lane == ps && (wm & lanes_in(ps, pe))) ++nfirst;
+    } else if (hist) {
       const uint32_t nf = __shfl(nfirst, src_ps);
       const uint32_t nl = __shfl(nlast, src_ps);
       bool lastev = false;
@@ -1338,7 +1348,8 @@ __device__ uint64_t wave_bpe(const DevTables& t, const DevWork& w,
     const uint64_t prevw = __brevll((~lr + (__brevll(wm) << 1)) & lr);
     dirty = wm | prevw;
   }
-  if (hist && elig && lane == ps) w.hmeta[base + ps] = nfirst | (nlast << 16);
+  if (hist && elig && lane == ps)
+    w.hmeta[base + ps] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
   if (write && elig) w.tok[pos] = lane_bit(live) ? (sym & SYM_ID) : INVALID_ID;
   return live;
 }
@@ -1660,7 +1671,11 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
     const int32_t q = nx[p];
     const uint64_t v = pair_lookup(t, tok[p], tok[q]);
     if (v == ~0ULL || (uint32_t)(v >> 32) != r) continue;  // stale entry
-    if (hist) {
+    if (hist && t.cert == 2) {
+      w.hfirst[a + nfirst++] = (v & 0xFFFFFFFF00000000ULL) |
+                               (p == a ? HR_FIRST : 0) |
+                               (nx[q] < 0 ? HR_LAST : 0) | (uint32_t)v;
+    } else if (hist) {
       if (p == a) w.hfirst[a + nfirst++] = v;
       if (nx[q] < 0) w.hlast[a + nlast++] = v;
     }
@@ -1677,7 +1692,7 @@ __device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
       if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | p);
     }
   }
-  if (hist) w.hmeta[a] = nfirst | (nlast << 16);
+  if (hist) w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
 }
 
 // ---- wide pieces: one wave per piece / segment of 65..WIDE_MAX bytes,
@@ -1828,13 +1843,24 @@ __device__ void wave_bpe_wide(const DevTables& t, const DevWork& w,
       for (int r = rows - 1; r >= 0; --r)
         if (live[r]) { l = r * 64 + 63 - __builtin_clzll(live[r]); break; }
       const int pl = L.pv[l];
-      if ((sel[f >> 6] >> (f & 63)) & 1) {
-        if (lane == 0) w.hfirst[a + nfirst] = ((uint64_t)R << 32) | L.mid[f];
+      const bool fsel = (sel[f >> 6] >> (f & 63)) & 1;
+      const bool lsel = pl >= 0 && ((sel[pl >> 6] >> (pl & 63)) & 1);
+      if (t.cert == 2) {
+        // the round: its rank, the product (one rule, so one id), and
+        // whether it took the first / last token
+        if (lane == 0)
+          w.hfirst[a + nfirst] = ((uint64_t)R << 32) | (fsel ? HR_FIRST : 0) |
+                                 (lsel ? HR_LAST : 0) | L.mid[s0];
         ++nfirst;
-      }
-      if (pl >= 0 && ((sel[pl >> 6] >> (pl & 63)) & 1)) {
-        if (lane == 0) w.hlast[a + nlast] = ((uint64_t)R << 32) | L.mid[pl];
-        ++nlast;
+      } else {
+        if (fsel) {
+          if (lane == 0) w.hfirst[a + nfirst] = ((uint64_t)R << 32) | L.mid[f];
+          ++nfirst;
+        }
+        if (lsel) {
+          if (lane == 0) w.hlast[a + nlast] = ((uint64_t)R << 32) | L.mid[pl];
+          ++nlast;
+        }
       }
     }
     // a slot dies when its left neighbour is a selected left symbol
@@ -1892,7 +1918,8 @@ __device__ void wave_bpe_wide(const DevTables& t, const DevWork& w,
     if (s < len)
       w.tok[a + s] = ((live[r] >> lane) & 1) ? (L.sym[s] & ~SYM_RAW) : INVALID_ID;
   }
-  if (hist && lane == 0) w.hmeta[a] = nfirst | (nlast << 16);
+  if (hist && lane == 0)
+    w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
 }
 
 // Wave-wide minimum (the prefix minimum's last lane), as a scalar.
@@ -2411,15 +2438,43 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
     uint64_t word = seg_word(w, wd) & ((1ULL << bit) - 1);
     while (word == 0) word = seg_word(w, --wd);
     const int64_t a = wd * 64 + (63 - __builtin_clzll(word));
-    const uint32_t ma = w.hmeta[a], mb = w.hmeta[c];
-    const uint32_t na = ma >> 16, nbv = mb & 0xFFFF;
-    const uint64_t* ea = w.hlast + a;
-    const uint64_t* eb = w.hfirst + c;
     uint32_t L = (uint32_t)t.byte_id[w.text[c - 1]];
     uint32_t R = (uint32_t)t.byte_id[w.text[c]];
     uint32_t i = 0, j = 0;
     bool ok = true;
-    for (;;) {
+    if (t.cert == 2) {
+      // Any table: the two segments' merge rounds in the order the whole
+      // piece would run them (the left segment's next round first when its
+      // rank is at most the right one's: its pairs lie to the left), and
+      // at every state the pair across c must lose to one of the two
+      // heads. A round of several merges runs at a rank no earlier rule
+      // consumes the product of, so the pair it leaves across c while it
+      // goes on ranks above it and cannot merge then: the states between
+      // rounds are the ones to check.
+      const uint32_t na = w.hmeta[a], nbv = w.hmeta[c];
+      const uint64_t* ea = w.hfirst + a;
+      const uint64_t* eb = w.hfirst + c;
+      for (;;) {
+        const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
+        const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
+        const uint64_t x = pair_lookup(t, L, R);
+        const uint32_t rho = x != ~0ULL ? (uint32_t)(x >> 32) : RANK_INF;
+        if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
+        if (ra == RANK_INF && rb == RANK_INF) break;
+        if (ra <= rb) {
+          const uint64_t e = ea[i++];
+          if (e & HR_LAST) L = (uint32_t)e & SYM_ID;
+        } else {
+          const uint64_t e = eb[j++];
+          if (e & HR_FIRST) R = (uint32_t)e & SYM_ID;
+        }
+      }
+    }
+    const uint32_t ma = w.hmeta[a], mb = w.hmeta[c];
+    const uint32_t na = ma >> 16, nbv = mb & 0xFFFF;
+    const uint64_t* ea = w.hlast + a;
+    const uint64_t* eb = w.hfirst + c;
+    for (; t.cert != 2;) {
       const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
       const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
       const uint64_t x = pair_lookup(t, L, R);

@@ -22,6 +22,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/toktier_hip.h"
@@ -162,6 +163,82 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
   return false;
 }
 
+// One request's device workspace: every per-call buffer, carved out of one
+// region (the engine's own allocation).
+// `slot` and `ctag` are the region's own call state: the control slot the
+// next call uses (each call's k_pretok clears the other one) and the last
+// compaction tag (the look-back status words carry it, so they are never
+// cleared between calls).
+struct Workspace {
+  size_t cap = 0;  // input bytes the workspace holds
+  uint8_t* text = nullptr;
+  uint64_t *starts = nullptr, *docmask = nullptr, *heap = nullptr;
+  uint64_t *cstat = nullptr, *inlong = nullptr, *cuts = nullptr;
+  uint64_t *failm = nullptr, *hfirst = nullptr, *hlast = nullptr;
+  uint64_t *dirty_cur = nullptr, *dirty_next = nullptr;
+  uint64_t *lits = nullptr, *litb = nullptr, *docmask_lit = nullptr;
+  uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
+  uint32_t *blkcount = nullptr, *blkprefix = nullptr, *out = nullptr;
+  uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
+  uint32_t *pblk = nullptr, *plocal = nullptr;
+  int32_t *nx = nullptr, *pv = nullptr;
+  size_t long_pairs = 0, seg_pairs = 0, out_n = 0, nblk = 0;
+  uint32_t slot = 0;
+  uint32_t ctag = 0;
+};
+
+// Lays a workspace for `cap` input bytes out at `base` (each buffer
+// 256-byte aligned) and returns the bytes it spans; base == nullptr only
+// sizes it. About 84 bytes per input byte.
+size_t carve(Workspace& w, uint8_t* base, size_t cap) {
+  size_t at = 0;
+  auto take = [&](auto*& p, size_t count) {
+    using T = std::remove_reference_t<decltype(*p)>;
+    at = (at + 255) & ~(size_t)255;
+    p = base ? reinterpret_cast<T*>(base + at) : nullptr;
+    at += (count ? count : 1) * sizeof(T);
+  };
+  const size_t words = cap / 64 + 8;
+  const size_t nblk = cap / tk::COMPACT_BLOCK + 2;
+  const size_t long_cap = cap / 32 + 64;
+  const size_t seg_cap = cap / 2 + 64;
+  const int64_t tiles = tk::pretok_tiles((int64_t)cap);
+  take(w.text, cap + 64);
+  take(w.starts, words);
+  take(w.docmask, words);
+  take(w.tok, cap + 64);
+  take(w.nx, cap);
+  take(w.pv, cap);
+  take(w.heap, 3 * cap);
+  take(w.longlist, 2 * long_cap);
+  take(w.ctrl, 2 * tk::CTRL_WORDS);  // two control slots
+  take(w.inlong, words);
+  take(w.cuts, words);
+  take(w.failm, words);
+  take(w.hfirst, cap);
+  take(w.hlast, cap);
+  take(w.hmeta, cap);
+  take(w.seglist, 2 * seg_cap);
+  take(w.dirty_cur, words / 64 + 2);
+  take(w.dirty_next, words / 64 + 2);
+  take(w.blkcount, nblk);
+  take(w.blkprefix, nblk);
+  take(w.cstat, nblk);
+  take(w.out, cap);
+  take(w.plist, (size_t)tk::pack_off((int64_t)cap, tk::PACK_CLASSES));
+  take(w.pblk, (size_t)tk::PACK_CLASSES * tiles);
+  take(w.plocal, (size_t)tk::PT_LOCAL_SLOTS * tiles);
+  take(w.lits, words);
+  take(w.litb, words);
+  take(w.docmask_lit, words);
+  w.cap = cap;
+  w.long_pairs = long_cap;
+  w.seg_pairs = seg_cap;
+  w.out_n = cap;
+  w.nblk = nblk;
+  return at;
+}
+
 }  // namespace
 
 struct tk_engine {
@@ -177,30 +254,24 @@ struct tk_engine {
   DevBuf<int32_t> byte_id;
   std::vector<uint8_t> host_nfc;
   tk::DevTables t{};
-  // workspace
-  size_t cap = 0;
-  DevBuf<uint8_t> text;
-  DevBuf<uint64_t> starts, docmask, heap, docoffs, rows, cstat;
-  DevBuf<uint32_t> tok, longlist, ctrl, blkcount, blkprefix, out;
+  // workspace (carved from one allocation) and the batch / seed buffers
+  DevBuf<uint8_t> wsmem;
+  Workspace ws;
+  DevBuf<uint64_t> docoffs, rows;
   DevBuf<uint32_t> seedc;  // per-block character counts (session seed)
-  DevBuf<int32_t> nx, pv;
-  DevBuf<uint64_t> inlong, cuts, failm, hfirst, hlast, dirty_cur, dirty_next;
-  DevBuf<uint32_t> hmeta, seglist, unsafe, plist, pblk, plocal;
-  // added-token literals (tk_engine_set_added) and their per-call masks
+  DevBuf<uint32_t> unsafe;
+  // added-token literals (tk_engine_set_added)
   DevBuf<uint64_t> lit_tab;
   DevBuf<uint8_t> lit_len;
   DevBuf<uint32_t> lit_id;
-  DevBuf<uint64_t> lits, litb, docmask_lit;
   tk::DevAdded added{};
   uint64_t last_literals = 0;
   size_t docs_cap = 0;
-  uint32_t slot = 0;  // control slot of the next call
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
   // gate words: host memory the device writes mid-pipeline
   volatile uint32_t* gate = nullptr;
   uint32_t* gate_dev = nullptr;
   uint32_t seq = 0;
-  uint32_t ctag = 0;  // compaction launches (status-word tags)
   // timing
   int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
   hipEvent_t ev[8] = {};
@@ -213,6 +284,7 @@ struct tk_engine {
   hipEvent_t ev_join3 = nullptr;
   double last_us[5] = {};
   size_t last_passes = 0;
+  uint32_t last_nlong = 0, last_big = 0;
 };
 
 namespace {
@@ -259,47 +331,16 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
   size_t need = 1u << 16;
   while (need < nb) need <<= 1;
   if (need > (size_t)1 << 30) return fail(TK_E_CAPACITY, "input of %zu bytes exceeds 1 GiB", nb);
-  if (need > e->cap) {
-    const size_t words = need / 64 + 8;
-    const size_t nblk = need / tk::COMPACT_BLOCK + 2;
-    const size_t long_cap = need / 32 + 64;
-    HIP_TRY(e->text.alloc(need + 64));
-    HIP_TRY(e->starts.alloc(words));
-    HIP_TRY(e->docmask.alloc(words));
-    HIP_TRY(e->tok.alloc(need + 64));
-    HIP_TRY(e->nx.alloc(need));
-    HIP_TRY(e->pv.alloc(need));
-    HIP_TRY(e->heap.alloc(3 * need));
-    HIP_TRY(e->longlist.alloc(2 * long_cap));
-    // two control slots: each call's k_pretok clears the slot of the next
-    HIP_TRY(e->ctrl.alloc(2 * tk::CTRL_WORDS));
-    HIP_TRY(hipMemset(e->ctrl.p, 0, 2 * tk::CTRL_WORDS * sizeof(uint32_t)));
-    e->slot = 0;
-    HIP_TRY(e->inlong.alloc(words));
-    HIP_TRY(e->cuts.alloc(words));
-    HIP_TRY(e->failm.alloc(words));
-    HIP_TRY(e->hfirst.alloc(need));
-    HIP_TRY(e->hlast.alloc(need));
-    HIP_TRY(e->hmeta.alloc(need));
-    HIP_TRY(e->seglist.alloc(2 * (need / 2 + 64)));
-    HIP_TRY(e->dirty_cur.alloc(words / 64 + 2));
-    HIP_TRY(e->dirty_next.alloc(words / 64 + 2));
-    HIP_TRY(e->blkcount.alloc(nblk));
-    HIP_TRY(e->blkprefix.alloc(nblk));
-    // compaction status words: tags start at 1, so zeroed words never match
-    HIP_TRY(e->cstat.alloc(nblk));
-    HIP_TRY(hipMemset(e->cstat.p, 0, nblk * sizeof(uint64_t)));
-    HIP_TRY(e->out.alloc(need));
-    HIP_TRY(e->plist.alloc((size_t)tk::pack_off((int64_t)need, tk::PACK_CLASSES)));
-    HIP_TRY(e->pblk.alloc((size_t)tk::PACK_CLASSES * tk::pretok_tiles((int64_t)need)));
-    HIP_TRY(e->plocal.alloc((size_t)tk::PT_LOCAL_SLOTS * tk::pretok_tiles((int64_t)need)));
-    e->cap = need;
-  }
-  if ((e->added.n || e->added.newline_cuts) && e->lits.n < e->cap / 64 + 8) {
-    const size_t words = e->cap / 64 + 8;
-    HIP_TRY(e->lits.alloc(words));
-    HIP_TRY(e->litb.alloc(words));
-    HIP_TRY(e->docmask_lit.alloc(words));
+  if (need > e->ws.cap) {
+    Workspace w;
+    const size_t bytes = carve(w, nullptr, need);
+    e->ws = Workspace{};
+    HIP_TRY(e->wsmem.alloc(bytes));
+    carve(e->ws, e->wsmem.p, need);
+    // the control slots start clear, and the compaction status words carry
+    // tags from 1 up, so zeroed words never match
+    HIP_TRY(hipMemset(e->ws.ctrl, 0, 2 * tk::CTRL_WORDS * sizeof(uint32_t)));
+    HIP_TRY(hipMemset(e->ws.cstat, 0, e->ws.nblk * sizeof(uint64_t)));
   }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
@@ -309,55 +350,55 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
   return TK_OK;
 }
 
-tk::DevWork make_work(tk_engine* e, const uint8_t* d_text, size_t nb,
-                      const uint64_t* d_docmask, bool check_nfc,
+tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
+                      size_t nb, const uint64_t* d_docmask, bool check_nfc,
                       uint32_t* out, size_t out_cap, bool literals) {
-  uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
+  uint32_t* ctrl = ws.ctrl + ws.slot * tk::CTRL_WORDS;
   tk::DevWork w{};
   w.text = d_text;
   w.nb = (int64_t)nb;
   w.docmask = d_docmask;
   w.check_nfc = check_nfc ? 1 : 0;
-  w.starts = e->starts.p;
-  w.tok = e->tok.p;
-  w.nx = e->nx.p;
-  w.pv = e->pv.p;
-  w.heap = e->heap.p;
-  w.longlist = e->longlist.p;
+  w.starts = ws.starts;
+  w.tok = ws.tok;
+  w.nx = ws.nx;
+  w.pv = ws.pv;
+  w.heap = ws.heap;
+  w.longlist = ws.longlist;
   w.longcount = ctrl + tk::CTRL_LONG;
-  w.long_cap = (uint32_t)(e->longlist.n / 2);
+  w.long_cap = (uint32_t)ws.long_pairs;
   w.status = ctrl + tk::CTRL_STATUS;
-  w.blkcount = e->blkcount.p;
-  w.blkprefix = e->blkprefix.p;
-  w.cstat = e->cstat.p;
+  w.blkcount = ws.blkcount;
+  w.blkprefix = ws.blkprefix;
+  w.cstat = ws.cstat;
   w.out = out;
   w.out_cap = (uint32_t)std::min<size_t>(out_cap, 0xFFFFFFFFu);
-  w.inlong = e->inlong.p;
-  w.cuts = e->cuts.p;
-  w.failm = e->failm.p;
-  w.hfirst = e->hfirst.p;
-  w.hlast = e->hlast.p;
-  w.hmeta = e->hmeta.p;
-  w.seglist = e->seglist.p;
+  w.inlong = ws.inlong;
+  w.cuts = ws.cuts;
+  w.failm = ws.failm;
+  w.hfirst = ws.hfirst;
+  w.hlast = ws.hlast;
+  w.hmeta = ws.hmeta;
+  w.seglist = ws.seglist;
   w.segcount = ctrl + tk::CTRL_SEG;
-  w.seg_cap = (uint32_t)(e->seglist.n / 2);
+  w.seg_cap = (uint32_t)ws.seg_pairs;
   w.nfail = ctrl + tk::CTRL_FAIL;
-  w.dirty_cur = e->dirty_cur.p;
-  w.dirty_next = e->dirty_next.p;
-  w.plist = e->plist.p;
-  w.plocal = e->plocal.p;
+  w.dirty_cur = ws.dirty_cur;
+  w.dirty_next = ws.dirty_next;
+  w.plist = ws.plist;
+  w.plocal = ws.plocal;
   for (int c = 0; c < tk::PACK_CLASSES; ++c)
     w.poff[c] = (uint32_t)tk::pack_off((int64_t)nb, c);  // < 2^32 for nb <= 1 GiB
-  w.pblk = e->pblk.p;
+  w.pblk = ws.pblk;
   w.pcount = ctrl + tk::CTRL_PCOUNT;
   w.uend = ctrl + tk::CTRL_UEND;
   w.nbig = ctrl + tk::CTRL_BIG;
   w.gate = e->gate_dev;
   w.seq = e->seq;
-  w.ctrl_next = e->ctrl.p + (e->slot ^ 1) * tk::CTRL_WORDS;
+  w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
   w.nlit = ctrl + tk::CTRL_NLIT;
-  w.lits = literals ? e->lits.p : nullptr;
-  w.litb = literals ? e->litb.p : nullptr;
+  w.lits = literals ? ws.lits : nullptr;
+  w.litb = literals ? ws.litb : nullptr;
   w.clear_words = (int64_t)(nb / 64 + 4);
   w.clear_dwords = w.clear_words / 64 + 2;
   return w;
@@ -407,19 +448,20 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 // the control slot of the next call, so the stages run back to back.
 // Added-token literals (literals == true): k_added splits the request
 // first; the split marks document starts, so k_pretok runs its
-// document-mask instance, on a mask k_added writes whole (e->docmask_lit:
+// document-mask instance, on a mask k_added writes whole (ws.docmask_lit:
 // the caller's document starts, if any, are read from d_docmask and kept).
-int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
-                 const uint64_t* d_docmask, bool check_nfc, hipStream_t s,
-                 uint32_t* out, size_t out_cap, uint32_t* status,
-                 uint32_t* total, const tk::DevAdded* docs = nullptr) {
+int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
+                 size_t nb, const uint64_t* d_docmask, bool check_nfc,
+                 hipStream_t s, uint32_t* out, size_t out_cap,
+                 uint32_t* status, uint32_t* total,
+                 const tk::DevAdded* docs = nullptr) {
   ++e->seq;
   const bool literals = docs != nullptr;
   const uint64_t* host_dm = d_docmask;
-  if (literals) d_docmask = e->docmask_lit.p;
-  const tk::DevWork w =
-      make_work(e, d_text, nb, d_docmask, check_nfc, out, out_cap, literals);
-  uint32_t* ctrl = e->ctrl.p + e->slot * tk::CTRL_WORDS;
+  if (literals) d_docmask = ws.docmask_lit;
+  const tk::DevWork w = make_work(e, ws, d_text, nb, d_docmask, check_nfc,
+                                  out, out_cap, literals);
+  uint32_t* ctrl = ws.ctrl + ws.slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
   // Timing mode 1, stage boundaries taken by the dispatches themselves:
   // ev[0] start of k_pretok; ev[1] end of the piece listing (k_lists,
@@ -437,7 +479,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   } else {
     HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
   }
-  e->slot ^= 1;  // this call's k_pretok clears the other slot
+  ws.slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_lists(e->t, w, s));
   HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
@@ -451,6 +493,8 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
   if (grc != TK_OK) return grc;
   const uint32_t nlong = e->gate[tk::GATE_NLONG];
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
+  e->last_nlong = nlong;
+  e->last_big = e->gate[tk::GATE_BIG];
   if (nlong > 0) {
     // two independent jobs on two side streams: pieces of 65..WIDE_MAX
     // bytes merged whole, and the cut / segment / certify path of the
@@ -470,7 +514,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
     // (the end of both side streams, or of the packed merge if later)
     if (stages) HIP_TRY(hipEventRecord(ev[3], s));
   }
-  HIP_TRY(tk::launch_compact(w, s, ++e->ctag, nullptr, at(4)));
+  HIP_TRY(tk::launch_compact(w, s, ++ws.ctag, nullptr, at(4)));
   // k_scan has left the outcome in the gate words: no read-back copy
   HIP_TRY(hipStreamSynchronize(s));
   uint32_t* h = e->host_ctrl;
@@ -513,7 +557,7 @@ int run_pipeline(tk_engine* e, const uint8_t* d_text, size_t nb,
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     }
     if (stages) HIP_TRY(hipEventRecord(ev[6], s));
-    HIP_TRY(tk::launch_compact(w, s, ++e->ctag));
+    HIP_TRY(tk::launch_compact(w, s, ++ws.ctag));
     if (stages) HIP_TRY(hipEventRecord(ev[7], s));
     if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     if (stages) {
@@ -765,15 +809,16 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->added.newline_cuts = cfg->ruleset == TK_RULESET_LAGUNA ? 1 : 0;
   e->t.ignore_merges = cfg->ignore_merges ? 1 : 0;
   e->t.needs_nfc = cfg->needs_nfc ? 1 : 0;
-  // Long pieces are cut and certified only when every merge rule that
-  // consumes a token ranks above every rule that produces it (no bit set
-  // in unsafe_bits) and every byte has an initial id.
-  bool cert = true;
-  for (size_t i = 0; i < unsafe_len / 4; ++i) cert = cert && unsafe_bits[i] == 0;
-  for (int b = 0; b < 256; ++b) cert = cert && byte_id[b] >= 0;
-  e->t.cert = cert ? 1 : 0;
+  // Pieces over 512 bytes are cut and certified when every byte has an
+  // initial id: from the segments' first / last-token events when every
+  // merge rule that consumes a token ranks above every rule that produces
+  // it (no bit set in unsafe_bits), else from every merge round of the
+  // segments. A table that drops bytes merges them serially.
+  bool monotone = true;
+  for (size_t i = 0; i < unsafe_len / 4; ++i) monotone = monotone && unsafe_bits[i] == 0;
   bool all_bytes = true;
   for (int b = 0; b < 256; ++b) all_bytes = all_bytes && byte_id[b] >= 0;
+  e->t.cert = !all_bytes ? 0 : monotone ? 1 : 2;
   e->t.all_bytes = all_bytes ? 1 : 0;
   e->t.ctab = nullptr;
   {
@@ -792,7 +837,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   }
   e->t.unsafe = nullptr;
   e->t.unsafe_words = 0;
-  if (!cert && unsafe_len >= 4) {
+  if (!monotone) {
     if ((rc = up(e->unsafe, unsafe_bits, unsafe_len / 4)) != TK_OK) return bail(rc);
     e->t.unsafe = e->unsafe.p;
     e->t.unsafe_words = (uint32_t)(unsafe_len / 4);
@@ -954,11 +999,6 @@ int tk_engine_set_added(tk_engine* e, size_t n, const uint8_t* contents,
   a.n = (uint32_t)n;
   a.newline_cuts = cuts;
   e->added = a;
-  // the per-call masks follow the workspace capacity
-  if (e->cap) {
-    rc = ensure_workspace(e, e->cap, 0);
-    if (rc != TK_OK) return rc;
-  }
   return TK_OK;
 }
 
@@ -966,6 +1006,15 @@ int tk_engine_last_literals(const tk_engine* e, uint64_t* n) {
   if (!e || !n) return fail(TK_E_INVALID_ARG, "null argument");
   *n = e->last_literals;
   return TK_OK;
+}
+
+int tk_engine_last_stats(const tk_engine* e, uint64_t* out, int n) {
+  if (!e || !out) return fail(TK_E_INVALID_ARG, "null argument");
+  const uint64_t v[4] = {e->last_literals, e->last_nlong, e->last_big,
+                         e->last_passes};
+  int k = 0;
+  for (; k < n && k < 4; ++k) out[k] = v[k];
+  return k;
 }
 
 int tk_engine_driver_version(const tk_engine* e, int* version) {
@@ -979,23 +1028,20 @@ const char* tk_engine_architecture(const tk_engine* e) { return e ? e->arch.c_st
 
 namespace {
 
-// tk_engine_encode_device with the engine's lock held
-int device_encode(tk_engine* e, const void* d_text, size_t nbytes,
-                  uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
-                  void* stream) {
+// tk_engine_encode_device with the engine's lock held, the device current
+// and a workspace that holds nbytes
+int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
+                  size_t nbytes, uint32_t flags, void* d_ids, size_t ids_cap,
+                  size_t* n_ids, void* stream) {
   *n_ids = 0;
-  if (nbytes == 0) return TK_OK;
-  HIP_TRY(hipSetDevice(e->device));
-  int rc = ensure_workspace(e, nbytes, 0);
-  if (rc != TK_OK) return rc;
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
   // the compaction writes straight into the caller's buffer
-  rc = run_pipeline(e, static_cast<const uint8_t*>(d_text), nbytes, nullptr,
-                    check, s, static_cast<uint32_t*>(d_ids), ids_cap, &st,
-                    &total, doc_pass(e, flags, &docs));
+  int rc = run_pipeline(e, ws, static_cast<const uint8_t*>(d_text), nbytes,
+                        nullptr, check, s, static_cast<uint32_t*>(d_ids),
+                        ids_cap, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -1003,6 +1049,19 @@ int device_encode(tk_engine* e, const void* d_text, size_t nbytes,
     return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   *n_ids = total;
   return TK_OK;
+}
+
+// the engine's own workspace, grown to hold nbytes
+int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
+               uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
+               void* stream) {
+  *n_ids = 0;
+  if (nbytes == 0) return TK_OK;
+  HIP_TRY(hipSetDevice(e->device));
+  int rc = ensure_workspace(e, nbytes, 0);
+  if (rc != TK_OK) return rc;
+  return device_encode(e, e->ws, d_text, nbytes, flags, d_ids, ids_cap, n_ids,
+                       stream);
 }
 
 }  // namespace
@@ -1013,7 +1072,7 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
   if (!e || !n_ids || (nbytes && (!d_text || !d_ids)))
     return fail(TK_E_INVALID_ARG, "null argument");
   std::lock_guard<std::mutex> lk(e->mu);
-  return device_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
+  return own_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
 }
 
 int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
@@ -1025,7 +1084,7 @@ int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
   if (stride == 0) return fail(TK_E_INVALID_ARG, "stride must be positive");
   std::lock_guard<std::mutex> lk(e->mu);
   *n_points = 0;
-  int rc = device_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
+  int rc = own_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
   if (rc != TK_OK || *n_ids == 0) return rc;
   // one checkpoint at every token index that is a multiple of the stride
   const size_t n = (*n_ids + stride - 1) / stride;
@@ -1039,8 +1098,8 @@ int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
   // the pipeline's workspace still holds this encode's per-byte tokens
   // and the compaction's block prefix
   tk::DevWork w{};
-  w.tok = e->tok.p;
-  w.blkprefix = e->blkprefix.p;
+  w.tok = e->ws.tok;
+  w.blkprefix = e->ws.blkprefix;
   HIP_TRY(tk::launch_seed(w, static_cast<const uint8_t*>(d_text), (int64_t)nbytes,
                           (uint32_t)n, stride, e->seedc.p,
                           static_cast<uint64_t*>(d_points), s));
@@ -1061,17 +1120,17 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   int rc = ensure_workspace(e, nbytes, 0);
   if (rc != TK_OK) return rc;
   hipStream_t s = e->stream;
-  HIP_TRY(hipMemcpyAsync(e->text.p, text, nbytes, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(e->ws.text, text, nbytes, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
-  rc = run_pipeline(e, e->text.p, nbytes, nullptr, check, s, e->out.p,
-                    e->out.n, &st, &total, doc_pass(e, flags, &docs));
+  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, e->ws.out,
+                    e->ws.out_n, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
-  HIP_TRY(hipMemcpyAsync(ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(ids, e->ws.out, (size_t)total * 4, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   *n_ids = total;
   return TK_OK;
@@ -1104,21 +1163,22 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
     const uint64_t p = doc_offsets[d];
     if (p < nb) mask[p >> 6] |= 1ULL << (p & 63);
   }
-  HIP_TRY(hipMemcpyAsync(e->text.p, joined, nb, hipMemcpyHostToDevice, s));
-  HIP_TRY(hipMemcpyAsync(e->docmask.p, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(e->ws.text, joined, nb, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(e->ws.docmask, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
-  rc = run_pipeline(e, e->text.p, nb, e->docmask.p, check, s, e->out.p,
-                    e->out.n, &st, &total, doc_pass(e, flags, &docs));
+  rc = run_pipeline(e, e->ws, e->ws.text, nb, e->ws.docmask, check, s,
+                    e->ws.out, e->ws.out_n, &st, &total,
+                    doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
-  const tk::DevWork w = make_work(e, e->text.p, nb, e->docmask.p, check,
-                                  e->out.p, e->out.n, false);
+  const tk::DevWork w = make_work(e, e->ws, e->ws.text, nb, e->ws.docmask,
+                                  check, e->ws.out, e->ws.out_n, false);
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipMemcpyAsync(ids, e->out.p, (size_t)total * 4, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(ids, e->ws.out, (size_t)total * 4, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
     // find the rows that failed; their ids are dropped, the others stand
