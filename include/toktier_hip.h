@@ -160,6 +160,26 @@ int tk_engine_encode_device(tk_engine* engine, const void* d_text,
                             size_t nbytes, uint32_t flags, void* d_ids,
                             size_t ids_cap, size_t* n_ids, void* stream);
 
+/* Allocation-free form of tk_engine_encode_device. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It calls no hipMalloc / hipFree and no allocating library
+ * routine: the per-request workspace is carved from a static device array
+ * (one copy per device, about 96 MiB, held until the process ends) instead
+ * of the engine's own workspace; the tables are the ones tk_engine_open
+ * uploaded. Same arguments, results and errors as tk_engine_encode_device,
+ * for inputs of at most TK_NOALLOC_MAX_BYTES bytes (larger inputs:
+ * TK_E_CAPACITY, nothing run). Every engine on a device shares that
+ * device's array, which keeps the last call's contents (each call clears
+ * what must start at zero): calls that would overlap on one device are
+ * serialized by a process-wide lock per device, and work that used the
+ * array from outside this library would race with them. */
+#define TK_NOALLOC_MAX_BYTES 1048576u
+int tk_engine_encode_device_noalloc(tk_engine* engine, const void* d_text,
+                                    size_t nbytes, uint32_t flags, void* d_ids,
+                                    size_t ids_cap, size_t* n_ids,
+                                    void* stream);
+
 /* Session seed: tk_engine_encode_device plus the sparse span checkpoints
  * the session store adopts with the ids (replaces the span bridge of the
  * GPU seed: crates/toktier-store-core/src/tail.rs:17-31 SpanCheckpoint,

@@ -30,6 +30,7 @@ TK_RULESET_LAGUNA = 2
 TK_RULESET_DEEPSEEK = 3
 TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
+TK_NOALLOC_MAX_BYTES = 1 << 20
 # added-token flags (tokenizer.json "added_tokens" fields)
 TK_ADDED_SPECIAL = 1
 TK_ADDED_SINGLE_WORD = 2
@@ -49,7 +50,7 @@ STATUS_NAMES = {
 SYMBOLS = (
     "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
     "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
-    "tk_engine_encode_seed",
+    "tk_engine_encode_device_noalloc", "tk_engine_encode_seed",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
     "tk_engine_last_literals", "tk_engine_last_stats",
@@ -112,6 +113,9 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_encode_device.restype = C.c_int
     L.tk_engine_encode_device.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
                                           C.POINTER(sz), vp]
+    L.tk_engine_encode_device_noalloc.restype = C.c_int
+    L.tk_engine_encode_device_noalloc.argtypes = [vp, vp, sz, C.c_uint32, vp,
+                                                  sz, C.POINTER(sz), vp]
     L.tk_engine_encode_seed.restype = C.c_int
     L.tk_engine_encode_seed.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
                                         C.c_uint32, vp, sz, C.POINTER(sz),
@@ -225,6 +229,18 @@ class Engine:
                                              d_ids, ids_cap, C.byref(n),
                                              stream)
         check(st, "tk_engine_encode_device")
+        return n.value
+
+    def encode_device_noalloc(self, d_text: int, nbytes: int, d_ids: int,
+                              ids_cap: int, flags: int = 0,
+                              stream: int | None = None) -> int:
+        """``encode_device`` with the workspace in the library's static
+        scratch array (no device allocation); inputs of at most
+        ``TK_NOALLOC_MAX_BYTES``."""
+        n = C.c_size_t()
+        st = self._L.tk_engine_encode_device_noalloc(
+            self._h, d_text, nbytes, flags, d_ids, ids_cap, C.byref(n), stream)
+        check(st, "tk_engine_encode_device_noalloc")
         return n.value
 
     def encode_seed(self, d_text: int, nbytes: int, d_ids: int, ids_cap: int,

@@ -277,4 +277,16 @@ hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);
 
+// The allocation-free entry (tk_engine_encode_device_noalloc) carves its
+// workspace out of a static device array of SCRATCH_BYTES, one copy per
+// device, held until the process ends. scratch_region returns that copy's
+// device address on `device` (looked up once per device, with the device
+// made current; the array's name in host code is not a device address).
+constexpr size_t SCRATCH_BYTES = (size_t)96 << 20;
+hipError_t scratch_region(int device, uint8_t** p);
+// clears a[0..na) and b[0..nb) with a kernel (no memset node, so the call
+// stays capturable)
+hipError_t launch_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb,
+                        hipStream_t s);
+
 }  // namespace tk

@@ -40,6 +40,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <mutex>
 #include <type_traits>
 
 namespace tk {
@@ -2870,6 +2871,50 @@ hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
   const uint32_t n = n_docs + 1;
   hipLaunchKernelGGL(k_doc_offsets, dim3((n + 63) / 64), dim3(64), 0, s, w,
                      doc_offsets, n_docs, row_offsets);
+  return hipGetLastError();
+}
+
+// ------------------------------------------- the allocation-free workspace
+
+// The workspace of tk_engine_encode_device_noalloc: a file-scope device
+// array, one copy per device. Host code reaches it only through the address
+// scratch_region looks up.
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+hipError_t scratch_region(int device, uint8_t** p) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  *p = nullptr;
+  if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!addr[device]) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return e;
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != device) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return e;
+    if (!ptr) return hipErrorInvalidSymbol;
+    addr[device] = ptr;
+  }
+  *p = static_cast<uint8_t*>(addr[device]);
+  return hipSuccess;
+}
+
+__global__ void k_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < na) a[i] = 0;
+  if (i < nb) b[i] = 0;
+}
+
+hipError_t launch_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb,
+                        hipStream_t s) {
+  const uint32_t n = na > nb ? na : nb;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_clear, dim3((n + 255) / 256), dim3(256), 0, s, a, na,
+                     b, nb);
   return hipGetLastError();
 }
 

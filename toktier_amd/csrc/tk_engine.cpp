@@ -164,7 +164,8 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
 }
 
 // One request's device workspace: every per-call buffer, carved out of one
-// region (the engine's own allocation).
+// region -- the engine's own allocation, or, for
+// tk_engine_encode_device_noalloc, the library's static scratch array.
 // `slot` and `ctag` are the region's own call state: the control slot the
 // next call uses (each call's k_pretok clears the other one) and the last
 // compaction tag (the look-back status words carry it, so they are never
@@ -267,6 +268,9 @@ struct tk_engine {
   tk::DevAdded added{};
   uint64_t last_literals = 0;
   size_t docs_cap = 0;
+  // the static scratch array on this engine's device
+  // (tk_engine_encode_device_noalloc)
+  uint8_t* scratch = nullptr;
   uint32_t* host_ctrl = nullptr;  // pinned read-back of 8 control words
   // gate words: host memory the device writes mid-pipeline
   volatile uint32_t* gate = nullptr;
@@ -743,6 +747,15 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
     // timing-only events: no system-scope fence between the stages
     if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
       return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
+  // the device's copy of the static scratch array (the allocation-free
+  // entry's workspace), looked up once per device with the device current
+  {
+    Workspace probe;
+    if (carve(probe, nullptr, TK_NOALLOC_MAX_BYTES) > tk::SCRATCH_BYTES)
+      return bail(fail(TK_E_INTERNAL, "scratch array smaller than its workspace"));
+    if (tk::scratch_region(e->device, &e->scratch) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipGetSymbolAddress of the scratch array failed"));
+  }
   if (hipHostMalloc(reinterpret_cast<void**>(&e->host_ctrl),
                     tk::CTRL_WORDS * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipHostMalloc failed"));
@@ -1064,6 +1077,13 @@ int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
                        stream);
 }
 
+// One lock per device for the static scratch array: every engine on a
+// device shares that device's copy of the array.
+std::mutex& scratch_lock(int device) {
+  static std::mutex locks[64];
+  return locks[device & 63];
+}
+
 }  // namespace
 
 int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
@@ -1073,6 +1093,36 @@ int tk_engine_encode_device(tk_engine* e, const void* d_text, size_t nbytes,
     return fail(TK_E_INVALID_ARG, "null argument");
   std::lock_guard<std::mutex> lk(e->mu);
   return own_encode(e, d_text, nbytes, flags, d_ids, ids_cap, n_ids, stream);
+}
+
+int tk_engine_encode_device_noalloc(tk_engine* e, const void* d_text,
+                                    size_t nbytes, uint32_t flags, void* d_ids,
+                                    size_t ids_cap, size_t* n_ids,
+                                    void* stream) {
+  if (!e || !n_ids || (nbytes && (!d_text || !d_ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  *n_ids = 0;
+  if (nbytes > TK_NOALLOC_MAX_BYTES)
+    return fail(TK_E_CAPACITY,
+                "input of %zu bytes exceeds the %u-byte limit of the "
+                "allocation-free entry (use tk_engine_encode_device)",
+                nbytes, (unsigned)TK_NOALLOC_MAX_BYTES);
+  if (!e->scratch)
+    return fail(TK_E_DEVICE, "the static scratch array has no device address");
+  std::lock_guard<std::mutex> lk(e->mu);
+  if (nbytes == 0) return TK_OK;
+  std::lock_guard<std::mutex> sk(scratch_lock(e->device));
+  HIP_TRY(hipSetDevice(e->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
+  // the workspace over the device's scratch array; the array keeps the last
+  // call's contents, so the words that must start clear (the control slots
+  // and the compaction status words) are cleared by a kernel first
+  Workspace ws;
+  carve(ws, e->scratch, TK_NOALLOC_MAX_BYTES);
+  HIP_TRY(tk::launch_clear(ws.ctrl, 2 * tk::CTRL_WORDS, ws.cstat,
+                           (uint32_t)ws.nblk, s));
+  return device_encode(e, ws, d_text, nbytes, flags, d_ids, ids_cap, n_ids,
+                       stream);
 }
 
 int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
