@@ -441,11 +441,12 @@ def main() -> int:
     out = np.empty(cap + 1, dtype=np.uint32)
     for i in range(W):
         eng.encode(reqs[K + i], out=out)
-    host_lat, host_ok = [], True
+    host_lat, host_parts, host_ok = [], [], True
     for i in range(K):
         t1 = time.perf_counter()
         got = eng.encode(reqs[i], out=out)
         host_lat.append((time.perf_counter() - t1) * 1e3)
+        host_parts.append(eng.last_timing()[5:8])
         if not np.array_equal(got, ids_dev[i]):
             log(f"host/device id mismatch on request {i}")
             host_ok = False
@@ -503,6 +504,12 @@ def main() -> int:
                       "(tk_engine_encode, transfers included)",
             "latency_ms": pcts(host_lat),
             "mean_ms": round(host_ms, 4),
+            "all_ms": [round(x, 3) for x in host_lat],
+            "parts_us": {n: round(float(v), 1) for n, v in zip(
+                ["bytes in (pinned staging, copy threads, DMA)",
+                 "pipeline to final ids in device memory",
+                 "ids out (DMA, copy threads)"],
+                np.mean(np.asarray(host_parts), axis=0))},
             "mchars_per_s": round(chars / (host_ms * 1e-3) / 1e6, 2),
             "tokens_per_s": round(n_tok / (host_ms * 1e-3), 1),
             "target_ms": TARGET_MS,

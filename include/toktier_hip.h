@@ -242,9 +242,20 @@ const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
  * long-piece BPE (run beside the short-piece BPE) went past it, [3]
  * compaction, [4] total. Mode 2 (least disturbance): [1] the short-piece
  * BPE kernel's own duration, the others 0. Mode 0 (default): nothing is
- * recorded. Returns the number of values written (<= n). */
+ * recorded. Host wall times of the last tk_engine_encode, in every mode:
+ * [5] the request bytes into device memory, [6] the pipeline up to the ids
+ * being final in device memory, [7] the ids into the caller's buffer.
+ * Returns the number of values written (<= n). */
 int tk_engine_set_timing(tk_engine* engine, int mode);
 int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
+
+/* Engine options (no reference counterpart). TK_OPT_COMPACT_PAIRS: 1
+ * (default) probe the compact pair table the engine builds at open when
+ * the artifact fits it, 0 probe the boundary-format table (the reference's
+ * splitmix64 open addressing) on every path. Returns TK_OK, or
+ * TK_E_INVALID_ARG for an unknown option or value. */
+#define TK_OPT_COMPACT_PAIRS 1
+int tk_engine_set_option(tk_engine* engine, int option, int64_t value);
 
 /* Thread-local description of the last failure on this thread. */
 const char* tk_last_error(void);

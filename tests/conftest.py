@@ -203,3 +203,19 @@ def _oracle_built():
     from oracle import oracle
     if not oracle.LIB.exists():
         oracle.build()
+
+
+def drop_byte_tokens(tokenizer_json: str, drop: bytes) -> str:
+    """A variant of a byte-level artifact without the single-byte tokens of
+    `drop` (and the merges that use a token holding one): those bytes have
+    no id, so the engine and HF drop them before merging."""
+    import json
+    from toktier_amd import bpe_tables
+    spec = json.loads(tokenizer_json)
+    b2u = bpe_tables.bytes_to_unicode()
+    gone = {b2u[b] for b in drop}
+    model = spec["model"]
+    model["vocab"] = {t: i for t, i in model["vocab"].items() if t not in gone}
+    model["merges"] = [[a, b] for a, b in bpe_tables._merge_pairs(model["merges"])
+                       if not any(ch in gone for ch in a + b)]
+    return json.dumps(spec)

@@ -286,3 +286,113 @@ def test_non_monotone_long_pieces_match_hf():
         assert list(t.encode(s).array) == k.hf_ids(s), (n, s[:60])
     for s in ("a" * 3000, "ab" * 1500, "xyz" * 700 + "中" * 400):
         assert list(t.encode(s).array) == k.hf_ids(s), s[:40]
+
+
+def _digit_texts(rng):
+    """Digit runs of every length class around the 64-byte word, the
+    64-byte halo and the 3072-byte tile, at shifted offsets, with ASCII and
+    non-ASCII N characters (Arabic-Indic, fullwidth, superscript, Roman
+    numeral), runs broken by other characters, and runs at the text ends."""
+    out = []
+    for n in (1, 2, 3, 4, 5, 63, 64, 65, 127, 128, 129, 3071, 3072, 3073,
+              3135, 3136, 3137, 6143, 6144, 6145, 9300):
+        for pre in ("", "x", "ab ", " " * 61, "y" * 3070):
+            out.append(pre + "7" * n + " z")
+    digits = "0123456789" + "٠١٢٣" + "０１２" + "²³" + "Ⅻ"
+    for _ in range(40):
+        n = int(rng.integers(1, 9000))
+        s = "".join(digits[int(i)] for i in rng.integers(0, len(digits), n))
+        a = int(rng.integers(0, 100))
+        out.append("q" * a + s + ("" if rng.random() < 0.3 else " end"))
+    out.append("12 34\n56a78\t9" * 300)
+    return out
+
+
+@pytest.mark.parametrize("name", ["llama_3_1_8b", "deepseek_v3"])
+def test_digit_runs_of_any_length_match_hf(name):
+    """\\p{N}{1,3}: the group count carried across 64-byte words, the halo
+    and tiles (each tile's run count looked up from the tiles before)."""
+    k, t = kit(name), tok(name)
+    rng = np.random.default_rng(31)
+    for s in _digit_texts(rng):
+        got = t.encode(s).array
+        want = k.oracle.encode_bytes(s.encode())
+        assert np.array_equal(got, want), (name, len(s), s[:30])
+    for s in _digit_texts(rng)[::7]:
+        assert list(t.encode(s).array) == k.hf_ids(s), (name, len(s), s[:30])
+    # document starts inside long runs (batch rows cut anywhere)
+    base = "3" * 7000 + " x " + "4" * 5000
+    docs, at = [], 0
+    while at < len(base):
+        n = int(rng.integers(0, 4000))
+        docs.append(base[at:at + n])
+        at += n
+    for d, r in zip(docs, t.encode_batch(docs)):
+        assert np.array_equal(r.array, k.oracle.encode_bytes(d.encode())), len(d)
+
+
+@pytest.mark.parametrize("name", ["llama_3_1_8b", "deepseek_v3"])
+def test_million_digit_request_is_linear(name):
+    """A request of one 1,000,000-digit run (and one of 4,194,304) encodes
+    in linear time: each digit's group is one lookup, each tile reads its
+    predecessors' run counts once."""
+    import time
+    k, t = kit(name), tok(name)
+    for n in (1_000_000, 4_194_304):
+        s = "1234567890" * (n // 10) + "5" * (n % 10)
+        t.encode(s)  # warm the workspace for this size
+        t0 = time.perf_counter()
+        got = t.encode(s).array
+        dt = time.perf_counter() - t0
+        want = k.oracle.encode_bytes(s.encode())
+        assert np.array_equal(got, want), (name, n)
+        assert dt < 0.25, (name, n, dt)
+
+
+@pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt2"])
+def test_boundary_pair_table_matches(name):
+    """Every merge path with the compact pair table switched off: lookups
+    probe the boundary-format table (splitmix64 open addressing)."""
+    from toktier_amd import workloads
+    from toktier_amd._ffi import TK_OPT_COMPACT_PAIRS
+    k, t = kit(name), tok(name)
+    texts = [workloads.config2(k.json, n_chars=60_000, sample=4)]
+    texts += _long_texts(name)[:12] + SAMPLES
+    try:
+        t.engine.set_option(TK_OPT_COMPACT_PAIRS, 0)
+        for s in texts:
+            got = t.encode(s).array
+            want = k.oracle.encode_bytes(s.encode())
+            assert np.array_equal(got, want), (name, s[:40])
+    finally:
+        t.engine.set_option(TK_OPT_COMPACT_PAIRS, 1)
+    with pytest.raises(Exception):
+        t.engine.set_option(TK_OPT_COMPACT_PAIRS, 2)
+
+
+def test_dropped_bytes_match_hf():
+    """An artifact without some single-byte tokens ('q', 'Z', TAB, the
+    second byte of U+00A9): those bytes are dropped before merging, on the
+    short, wide and long (serial) paths and in batches."""
+    import toktier_amd
+    from conftest import drop_byte_tokens
+    from tokenizers import Tokenizer
+    from toktier_amd import workloads
+    k = kit("gpt2")
+    js = drop_byte_tokens(k.json, bytes([ord("q"), ord("Z"), 9, 0xA9]))
+    hf = Tokenizer.from_str(js)
+    t = toktier_amd.load("gpt2", tokenizer_json=js)
+    try:
+        assert t.tables.byte_id[ord("q")] == -1
+        base = workloads.config2(k.json, n_chars=20_000, sample=5)
+        texts = ["quiz Zebra\tq", "aqa", "©q", "qqqq", "q" * 100,
+                 " " + "aqZb" * 200, "Q\tq\t" * 50, base,
+                 " " + "".join(ch for ch in base if ch.isalpha())[:3000]]
+        for s in texts:
+            assert list(t.encode(s).array) == hf.encode(
+                s, add_special_tokens=False).ids, s[:40]
+        rows = t.encode_batch(texts)
+        for s, r in zip(texts, rows):
+            assert list(r.array) == hf.encode(s, add_special_tokens=False).ids
+    finally:
+        t.close()

@@ -373,6 +373,8 @@ def load(family: str, tokenizer_json: str | Path | None = None,
     this artifact, device and build."""
     if tokenizer_json is None:
         text = standin.load_artifact_json(family)
+    elif isinstance(tokenizer_json, str) and tokenizer_json.lstrip().startswith("{"):
+        text = tokenizer_json  # the artifact's text itself
     else:
         p = Path(tokenizer_json)
         text = p.read_text(encoding="utf-8") if p.exists() else str(tokenizer_json)

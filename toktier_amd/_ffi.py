@@ -31,6 +31,7 @@ TK_RULESET_DEEPSEEK = 3
 TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
 TK_NOALLOC_MAX_BYTES = 1 << 20
+TK_OPT_COMPACT_PAIRS = 1
 # added-token flags (tokenizer.json "added_tokens" fields)
 TK_ADDED_SPECIAL = 1
 TK_ADDED_SINGLE_WORD = 2
@@ -53,7 +54,7 @@ SYMBOLS = (
     "tk_engine_encode_device_noalloc", "tk_engine_encode_seed",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
-    "tk_engine_last_literals", "tk_engine_last_stats",
+    "tk_engine_last_literals", "tk_engine_last_stats", "tk_engine_set_option",
     "tk_engine_driver_version", "tk_last_error",
 )
 
@@ -134,6 +135,8 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_driver_version.argtypes = [vp, C.POINTER(C.c_int)]
     L.tk_engine_last_literals.restype = C.c_int
     L.tk_engine_last_literals.argtypes = [vp, C.POINTER(C.c_uint64)]
+    L.tk_engine_set_option.restype = C.c_int
+    L.tk_engine_set_option.argtypes = [vp, C.c_int, C.c_int64]
     L.tk_engine_last_stats.restype = C.c_int
     L.tk_engine_last_stats.argtypes = [vp, C.POINTER(C.c_uint64), C.c_int]
     if path is None:
@@ -287,6 +290,12 @@ class Engine:
               "tk_engine_last_literals")
         return int(n.value)
 
+    def set_option(self, option: int, value: int) -> None:
+        """``TK_OPT_COMPACT_PAIRS``: 1 probe the compact pair table (the
+        default when the artifact fits it), 0 the boundary-format table."""
+        check(self._L.tk_engine_set_option(self._h, int(option), int(value)),
+              "tk_engine_set_option")
+
     def last_stats(self) -> dict[str, int]:
         """Facts of the last encode: literals extracted, pieces over 64
         and over 512 bytes, certification repair passes."""
@@ -303,6 +312,9 @@ class Engine:
               "tk_engine_set_timing")
 
     def last_timing(self) -> list[float]:
-        buf = (C.c_double * 5)()
-        k = self._L.tk_engine_last_timing(self._h, buf, 5)
+        """Device stage times [0..4] (timing modes 1 / 2) and the host wall
+        times [5..7] of the last host-to-host encode (bytes in, pipeline,
+        ids out), microseconds."""
+        buf = (C.c_double * 8)()
+        k = self._L.tk_engine_last_timing(self._h, buf, 8)
         return list(buf[:k])

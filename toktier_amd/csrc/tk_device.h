@@ -56,6 +56,7 @@ struct DevTables {
   const int32_t* byte_id;      // [256]
   const ulonglong2* vocab;     // interleaved {fnv key, val} vocabulary slots
   uint64_t vocab_mask;
+  uint32_t vocab_max_len;      // bytes of the longest vocabulary entry
   const uint8_t* blob;         // vocabulary bytes
   int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek
   int32_t dmax;                // digit group width (cl100k)
@@ -130,6 +131,9 @@ struct DevWork {
   uint64_t* lits;
   uint64_t* litb;
   uint32_t* nlit;        // literals extracted (ctrl)
+  // per tile of k_pretok: the digit run at its end (call tag << 32 | whole
+  // tile | N characters), or nullptr
+  uint64_t* nrun;
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
   int64_t clear_words;   // inlong / failm words
@@ -287,6 +291,6 @@ hipError_t scratch_region(int device, uint8_t** p);
 // clears a[0..na) and b[0..nb) with a kernel (no memset node, so the call
 // stays capturable)
 hipError_t launch_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb,
-                        hipStream_t s);
+                        uint64_t* c, uint32_t nc, hipStream_t s);
 
 }  // namespace tk

@@ -120,9 +120,11 @@ __device__ __forceinline__ bool ctab_find(const DevTables& t, uint32_t l,
   return (k0 | k1 | k2 | k3) != 0u;
 }
 
-// whole-piece vocabulary id (ignore_merges) or -1
+// whole-piece vocabulary id (ignore_merges) or -1; a piece longer than the
+// longest vocabulary entry is none (no hash over it)
 __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
                                 int64_t m) {
+  if (m > (int64_t)t.vocab_max_len) return -1;
   uint64_t h = 0xCBF29CE484222325ULL;
   for (int64_t j = 0; j < m; ++j) h = (h ^ s[j]) * 0x100000001B3ULL;
   uint64_t i = splitmix64(h) & t.vocab_mask;
@@ -307,6 +309,20 @@ struct GCtx {
 //   bits 25..26 fwd:  next(p) = p + 1 + fwd(p) (before the end checks)
 //   bit  27     the decode at p is valid UTF-8
 //   bit  28     class bit 2 (the seven DeepSeek classes)
+// packed LDS table entry of k_pretok: byte id (LTAB_NOID: none), class of
+// the code point, its NFC quick-check value
+constexpr uint32_t LTAB_NOID = 0xFFFFFu;
+constexpr int LTAB_CLS = 20, LTAB_NFC = 24;
+// a tile's digit-run word (nrun): call tag << 32 | NRUN_FULL (the run
+// spans the whole tile) | N characters of the run at the tile's end
+constexpr uint64_t NRUN_FULL = 1ull << 31;
+constexpr int NRUN_SPIN = 1 << 20;
+__device__ __forceinline__ void nrun_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t nrun_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 constexpr int PT_HALO = 64;
 constexpr int PT_SPAN = PT_TILE + 2 * PT_HALO;
 constexpr int PT_PAD = 80;  // >= PT_HALO + 4, a multiple of 16
@@ -767,23 +783,31 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   __shared__ uint32_t lcnt[PACK_CLASSES];
   // pieces over 64 bytes that start in the tile (at most PT_TILE / 65)
   __shared__ uint32_t llong[PT_TILE / 64], nlong, longbase;
-  // the first 256 code points' class and NFC values, and the byte ids:
-  // LDS copies for the common case (one entry per thread)
+  // the first 256 code points' class and NFC value and the 256 byte ids,
+  // one 32-bit word per entry (LTAB_*): LDS copies for the common case (one
+  // entry per thread; 32-bit words, so the compiler keeps the LDS and HBM
+  // table reads apart instead of merging them into one flat load)
   static_assert(PRETOK_TPB == 256, "one table entry per thread");
-  // (32-bit entries, so the compiler keeps the LDS and HBM table reads
-  // apart instead of merging them into one flat load)
-  __shared__ uint32_t lcls[256], lnfc[256];
-  __shared__ int32_t lbid[256];
+  __shared__ uint32_t ltab[256];
   __shared__ uint32_t loff[PACK_CLASSES];  // class regions of plocal
+  // digit groups (\p{N}{1,K}, K > 1), per word from the halo word to the
+  // first word after the tile: N-class character starts, run breaks (other
+  // character starts and document starts), and the N characters of the run
+  // at the word's end
+  __shared__ uint64_t gNL[PT_TILE / 64 + 2], gBR[PT_TILE / 64 + 2];
+  __shared__ uint32_t gC[PT_TILE / 64 + 1];
   const int tid = threadIdx.x;
   if (tid < PACK_CLASSES) {
     lcnt[tid] = 0;
     loff[tid] = PACK_LOCAL_OFF[tid];
   }
   if (tid == 0) nlong = 0;
-  lcls[tid] = t.cls[tid];
-  lnfc[tid] = w.check_nfc ? t.nfc[tid] : 0;
-  lbid[tid] = t.byte_id[tid];
+  {
+    const int32_t bid = t.byte_id[tid];
+    ltab[tid] = (bid >= 0 ? (uint32_t)bid : LTAB_NOID) |
+                ((uint32_t)t.cls[tid] << LTAB_CLS) |
+                ((w.check_nfc ? (uint32_t)t.nfc[tid] : 0u) << LTAB_NFC);
+  }
   const int64_t base = (int64_t)blockIdx.x * PT_TILE;
   const int64_t nb = w.nb;
   const bool al = ((uintptr_t)w.text & 15) == 0;
@@ -871,7 +895,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
                        (n == 3 && v < 0x10000) || v > 0x10FFFF ||
                        (v >= 0xD800 && v <= 0xDFFF);
       const uint32_t cp = bad ? 0xFFFDu : v;
-      const uint32_t cl = cp < 256 ? lcls[cp] : t.cls[cp];
+      const uint32_t cl = cp < 256 ? (ltab[cp] >> LTAB_CLS) & 7 : t.cls[cp];
       // a continuation byte is valid when the first byte back that is not
       // one (at most three back, not before position 0) is a lead that
       // announces at least that many continuation bytes
@@ -889,19 +913,96 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     se[j] = e;
   }
   __syncthreads();
-  const LCtx c{GCtx{w.text, nb, DM ? w.docmask : nullptr, t.cls}, se, lo, sdm, wlo};
-  // document start at local offset L: position 0, or a marked doc head
-  const int Lz = lo <= 0 ? (int)(-lo) : -1;
-  auto prv = [&](int L) {  // local offset of the character before L
-    return L - 1 - (int)((se[L - 1] >> 23) & 3);
-  };
   const int lane = tid & 63, wv = wave_id();
   // the ruleset's class of an entry, and its digit / P / whitespace classes
   auto kcl = [](uint32_t e) { return RS == RS_DEEPSEEK ? dcl(e) : ecl(e); };
   constexpr int KN = RS == RS_DEEPSEEK ? DS_N : CN_;
   constexpr int KP = RS == RS_DEEPSEEK ? DS_PS : CP_;
   auto kws = [](int k) { return RS == RS_DEEPSEEK ? k >= DS_WS : k == CS_; };
-  uint32_t st = 0;
+  // Digit groups (\p{N}{1,K}, K > 1) count the N characters of the run
+  // before a digit, and a run can be any length. Per word of the span from
+  // the halo word on, the N-class character starts (gNL) and the run breaks
+  // (gBR: the starts of other characters, and document starts, where a run
+  // begins), index k + 1 for word k (-1: the halo word, PT_TILE / 64: the
+  // first word after the tile, which the start words recompute); thread 0
+  // counts the run's N characters at every word end up to the tile's (gC,
+  // index k + 1 for tile word k, 0 for the halo word). A run that reaches
+  // back past the halo takes its count before the tile from the tiles
+  // before: each tile publishes, before it waits on anything, the N
+  // characters of the run at its end and whether the run spans it whole,
+  // tagged with the call number, and a tile whose halo holds no break reads
+  // its predecessors' (bounded waits). Every digit is then one lookup.
+  uint32_t st = 0;  // status bits of the tile
+  const bool groups = (RS == 0 || RS == RS_DEEPSEEK) && t.dmax > 1;
+  if (groups) {
+    for (int k = wv - 1; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
+      const int64_t p = base + 64 * k + lane;
+      const int L = PT_HALO + 64 * k + lane;
+      const bool ld = p >= 0 && p < nb && !is_cont(sb[L + (PT_PAD - PT_HALO)]);
+      const bool isn = ld && kcl(se[L]) == KN;
+      bool dsp = p == 0;
+      if (DM && dm && ld && !dsp) dsp = (sdm[(p >> 6) - wlo] >> (p & 63)) & 1;
+      const uint64_t mn = __ballot(isn);
+      const uint64_t mb = __ballot(ld && (!isn || dsp));
+      if (lane == 0) {
+        gNL[k + 1] = mn;
+        gBR[k + 1] = mb;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      // N characters after the last break of word k (a document start that
+      // is an N character opens the run and counts)
+      auto after_break = [&](int k) {
+        const uint64_t b = gBR[k], n = gNL[k];
+        const int h = 63 - __builtin_clzll(b);
+        return (uint32_t)__popcll(n & ~mask_le(h)) + (uint32_t)((n >> h) & 1);
+      };
+      uint32_t run = 0;
+      int fb = PT_TILE / 64;  // the tile's first word with a break
+      for (int k = 1; k <= PT_TILE / 64; ++k) {
+        if (gBR[k]) {
+          run = after_break(k);
+          if (fb == PT_TILE / 64) fb = k - 1;
+        } else {
+          run += (uint32_t)__popcll(gNL[k]);
+        }
+        gC[k] = run;
+      }
+      if (w.nrun)
+        nrun_store(&w.nrun[blockIdx.x], ((uint64_t)w.seq << 32) |
+                                            (fb == PT_TILE / 64 ? NRUN_FULL : 0) | run);
+      uint32_t c0 = 0;
+      if (gBR[0]) {
+        c0 = after_break(0);
+      } else if (gNL[0] && w.nrun) {
+        // the run reaches back past the halo: the tiles before it
+        for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0; --u) {
+          uint64_t v;
+          int spin = 0;
+          while ((uint32_t)((v = nrun_load(&w.nrun[u])) >> 32) != w.seq) {
+            if (++spin > NRUN_SPIN) break;
+            __builtin_amdgcn_s_sleep(2);
+          }
+          if ((uint32_t)(v >> 32) != w.seq) {
+            st |= ST_STALL;
+            break;
+          }
+          c0 += (uint32_t)(v & (NRUN_FULL - 1));
+          if (!(v & NRUN_FULL)) break;
+        }
+      }
+      gC[0] = c0;
+      for (int k = 1; k <= fb; ++k) gC[k] += c0;
+    }
+    __syncthreads();
+  }
+  const LCtx c{GCtx{w.text, nb, DM ? w.docmask : nullptr, t.cls}, se, lo, sdm, wlo};
+  // document start at local offset L: position 0, or a marked doc head
+  const int Lz = lo <= 0 ? (int)(-lo) : -1;
+  auto prv = [&](int L) {  // local offset of the character before L
+    return L - 1 - (int)((se[L - 1] >> 23) & 3);
+  };
   // the tile's words, and the first word after it (the next block writes
   // that one; it is recomputed here to size the pieces near the tile end)
   // The start words, compiled twice: with document starts in the staged
@@ -968,6 +1069,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
             : RS == 1 ? fast_r50k(x)
             : RS == RS_DEEPSEEK ? fast_deepseek(x, t.dmax)
                                 : fast_cl100k(x, t.dmax);
+      // a digit's group needs nothing after it: the run count decides
+      // (also at the span's last byte, where the fixed context stops)
+      if (groups && kcl(e) == KN) r = FAST_DIGITS;
       const bool open = lead && !d0 && r < 0;
       if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
         if (open) {
@@ -976,15 +1080,18 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
           // text end)
           const uint64_t dmw = D ? sdm[wd - wlo] : 0;
           if (r == FAST_DIGITS) {
-            // the ASCII digits before i, when the word shows where they
-            // begin: after the last byte that is not one, or at a document
-            // start
-            const uint64_t nd_ = (~mDG & below) | ((dmw & below) >> 1);
-            if (nd_) {
-              const int h = 63 - __builtin_clzll(nd_);
-              if (((dmw >> (h + 1)) & 1) || !((mHI >> h) & 1))
-                r = (lane - 1 - h) % t.dmax == 0;
+            // the N characters of the run before i: after the last break
+            // below it in the word, else the count at the previous word's
+            // end plus the word's N characters below it
+            const uint64_t n = gNL[k + 1], b = gBR[k + 1] & below;
+            uint32_t cnt;
+            if (b) {
+              const int h = 63 - __builtin_clzll(b);
+              cnt = (uint32_t)__popcll(n & below & ~mask_le(h)) + (uint32_t)((n >> h) & 1);
+            } else {
+              cnt = gC[k] + (uint32_t)__popcll(n & below);
             }
+            r = cnt % (uint32_t)t.dmax == 0;
           } else if (r == FAST_CRLF && bb < 0x80) {
             // another CR/LF ahead in the run: it shows in the word before
             // the first byte that is neither (unless that byte is not
@@ -1037,19 +1144,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
               }
             }
           }
-          if (r == FAST_DIGITS) {
-            // \p{N}{1,K}: count the digits before i inside the span
-            int L = L3, nd = 3;
-            r = -1;
-            for (;;) {
-              if (ds(L)) { r = nd % t.dmax == 0; break; }
-              if (L - 1 < 0) break;  // past the span: general path
-              const int Lr = prv(L);
-              if (kcl(se[Lr]) != KN) { r = nd % t.dmax == 0; break; }
-              ++nd;
-              L = Lr;
-            }
-          } else if (r == FAST_CRLF) {
+          if (r == FAST_CRLF) {
             // end of \s*[\r\n]+ unless another CR/LF follows in the run;
             // then the first char the P match's [\r\n]* left over
             r = -1;
@@ -1092,12 +1187,12 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       const bool s = !in || (lead && (d0 || r != 0));
       if (w.check_nfc && lead) {
         const uint32_t cp = e & 0x1FFFFF;
-        const uint8_t v = cp < 256 ? lnfc[cp] : t.nfc[cp];
+        const uint8_t v = cp < 256 ? ltab[cp] >> LTAB_NFC : t.nfc[cp];
         if (v == 255) {
           st |= ST_NFC;
         } else if (v != 0 && !d0) {
           const uint32_t pc = x.c1 & 0x1FFFFF;
-          if ((pc < 256 ? lnfc[pc] : t.nfc[pc]) > v) st |= ST_NFC;
+          if ((pc < 256 ? ltab[pc] >> LTAB_NFC : t.nfc[pc]) > v) st |= ST_NFC;
         }
       }
       uint64_t m = __ballot(s);
@@ -1128,15 +1223,16 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       const uint32_t j = atomicAdd(&lcnt[kind], 1u);
       w.plocal[(int64_t)blockIdx.x * PT_LOCAL_SLOTS + loff[kind] + j] = (uint32_t)a;
     } else if (kind == PIECE_ONE) {
-      const int32_t id = lbid[sb[64 * k + lane + PT_PAD]];
-      w.tok[a] = id >= 0 ? (uint32_t)id : INVALID_ID;
+      const uint32_t id = ltab[sb[64 * k + lane + PT_PAD]] & LTAB_NOID;
+      w.tok[a] = id != LTAB_NOID ? id : INVALID_ID;
     } else if (kind == PIECE_TWO) {
       const uint32_t b0 = sb[64 * k + lane + PT_PAD];
       const uint32_t b1 = sb[64 * k + lane + PT_PAD + 1];
-      const int32_t i0 = lbid[b0], i1 = lbid[b1];
-      const uint64_t mg = (i0 >= 0 && i1 >= 0) ? t.bytepair[(b0 << 8) | b1] : ~0ULL;
-      w.tok[a] = mg != ~0ULL ? (uint32_t)mg : i0 >= 0 ? (uint32_t)i0 : INVALID_ID;
-      w.tok[a + 1] = (mg == ~0ULL && i1 >= 0) ? (uint32_t)i1 : INVALID_ID;
+      const uint32_t i0 = ltab[b0] & LTAB_NOID, i1 = ltab[b1] & LTAB_NOID;
+      const bool h0 = i0 != LTAB_NOID, h1 = i1 != LTAB_NOID;
+      const uint64_t mg = (h0 && h1) ? t.bytepair[(b0 << 8) | b1] : ~0ULL;
+      w.tok[a] = mg != ~0ULL ? (uint32_t)mg : h0 ? i0 : INVALID_ID;
+      w.tok[a + 1] = (mg == ~0ULL && h1) ? i1 : INVALID_ID;
     } else if (kind == PIECE_LONG) {
       llong[atomicAdd(&nlong, 1u)] = (uint32_t)a;
     }
@@ -1504,33 +1600,53 @@ __constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
     pack_geo(10), pack_geo(11), pack_geo(12)};
 static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 
-// Work units in order, the longest class first (class c owns units
-// [uend[c + 1], uend[c])); wave g takes units g, g + G, g + 2G, ... (G waves
-// in the grid), so every wave gets a share of each class. Classes of up to
-// PACK_LANE_MAX bytes: 64 pieces per unit, one per lane (lane_bpe); longer
-// ones: 64 / slot pieces per unit, a slot of lanes each (wave_bpe).
+// Work units by class (class c's list, in text order, makes uend[c] -
+// uend[c + 1] units). Workgroups go to the XCDs in turn (block b on XCD
+// b % PACK_XCDS), and each XCD has its own L2: so each class's units are
+// split into PACK_XCDS contiguous runs, run x (one stretch of the text) for
+// the blocks of XCD x, and an XCD reads the text, start words and lists of
+// its own stretch only. Inside an XCD the units go longest class first and
+// its wave g takes units g, g + G, g + 2G, ... (G waves per XCD), so every
+// wave gets a share of each class. Classes of up to PACK_LANE_MAX bytes: 64
+// pieces per unit, one per lane (lane_bpe); longer ones: 64 / slot pieces
+// per unit, a slot of lanes each (wave_bpe).
+constexpr int PACK_XCDS = 8;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
   const int lane = threadIdx.x & 63, wv = wave_id();
-  // lane q < PACK_CLASSES holds class q's unit end, piece count and
-  // geometry (slot | pieces per unit << 8 | pack_magic << 16 | lane flag);
-  // lane PACK_CLASSES holds a zero unit end
+  const int x = blockIdx.x % PACK_XCDS;
+  // lane q < PACK_CLASSES holds class q's run of units for this XCD (its
+  // first unit in the class, and the end of its units in the XCD's order,
+  // longest class first), piece count and geometry (slot | pieces per unit
+  // << 8 | pack_magic << 16 | lane flag); lane PACK_CLASSES holds a zero end
   const bool cl = lane < PACK_CLASSES;
-  const uint32_t ue_l = cl ? w.uend[lane] : 0u;
+  const uint32_t ue = cl ? w.uend[lane] : 0u;
+  const uint32_t nu = ue - (uint32_t)__shfl_down((int)ue, 1);  // class units
+  const uint32_t s0_l = cl ? (uint32_t)(((uint64_t)nu * x) / PACK_XCDS) : 0u;
+  const uint32_t len = cl ? (uint32_t)(((uint64_t)nu * (x + 1)) / PACK_XCDS) - s0_l : 0u;
+  // ends in the XCD's order: a suffix sum over the classes
+  uint32_t ue_l = len;
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_down((int)ue_l, d);
+    ue_l += lane + d < PACK_CLASSES ? o : 0u;
+  }
+  if (!cl) ue_l = 0u;
   const uint32_t pc_l = cl ? w.pcount[lane] : 0u;
   const uint32_t geo_l = cl ? PACK_GEO[lane] : 0u;
   const uint32_t total = __builtin_amdgcn_readfirstlane(ue_l);
-  const uint32_t G = gridDim.x * 4;
-  for (uint32_t u0 = blockIdx.x * 4 + wv; u0 < total; u0 += G) {
+  const uint32_t G = (gridDim.x / PACK_XCDS) * 4;
+  for (uint32_t u0 = (blockIdx.x / PACK_XCDS) * 4 + wv; u0 < total; u0 += G) {
     // the unit's class: the last class whose unit end lies past u0
     const uint64_t inq = __ballot(cl && u0 < ue_l);
     const int c = 63 - __builtin_clzll(inq);
     const uint32_t geo = __builtin_amdgcn_readlane(geo_l, c);
     const uint32_t ubeg = __builtin_amdgcn_readlane(ue_l, c + 1);
+    const uint32_t s0 = __builtin_amdgcn_readlane(s0_l, c);
     const uint32_t cnt = __builtin_amdgcn_readlane(pc_l, c);
     const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
-    const uint32_t first = (u0 - ubeg) * k;  // the unit's first piece
+    const uint32_t first = (s0 + u0 - ubeg) * k;  // the unit's first piece
     if ((geo & PACK_GEO_LANE) && t.all_bytes) {  // wave-uniform
       const uint32_t idx = first + lane;
       int64_t a = 0;
@@ -2421,82 +2537,92 @@ __global__ __launch_bounds__(64) void k_seg_serial(DevTables t, DevWork w) {
   }
 }
 
-// Certify every cut (thread per bitmask word; in a repair pass only the
-// dirty words). A failing cut is recorded in failm and counted, and the
-// words of the two segments it joins are marked dirty for the next pass.
+// Certify every cut: one wave per bitmask word, one lane per cut (in a
+// repair pass only the dirty words). A failing cut is recorded in failm and
+// counted, and the words of the two segments it joins are marked dirty for
+// the next pass.
+__device__ __forceinline__ uint32_t pair_rank(const DevTables& t, uint32_t l,
+                                              uint32_t r) {
+  uint32_t rank, id;
+  return pair_find(t, l, r, &rank, &id) ? rank : RANK_INF;
+}
+
 __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
                                                  int64_t nwords, int all) {
-  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v >= nwords) return;
-  if (!all && !word_dirty(w.dirty_cur, v)) return;
-  uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
-  while (cuts) {
-    const int bit = __builtin_ctzll(cuts);
-    cuts &= cuts - 1;
-    const int64_t c = v * 64 + bit;
-    // start of the segment that ends at c
-    int64_t wd = v;
-    uint64_t word = seg_word(w, wd) & ((1ULL << bit) - 1);
-    while (word == 0) word = seg_word(w, --wd);
-    const int64_t a = wd * 64 + (63 - __builtin_clzll(word));
-    uint32_t L = (uint32_t)t.byte_id[w.text[c - 1]];
-    uint32_t R = (uint32_t)t.byte_id[w.text[c]];
-    uint32_t i = 0, j = 0;
-    bool ok = true;
-    if (t.cert == 2) {
-      // Any table: the two segments' merge rounds in the order the whole
-      // piece would run them (the left segment's next round first when its
-      // rank is at most the right one's: its pairs lie to the left), and
-      // at every state the pair across c must lose to one of the two
-      // heads. A round of several merges runs at a rank no earlier rule
-      // consumes the product of, so the pair it leaves across c while it
-      // goes on ranks above it and cannot merge then: the states between
-      // rounds are the ones to check.
-      const uint32_t na = w.hmeta[a], nbv = w.hmeta[c];
-      const uint64_t* ea = w.hfirst + a;
-      const uint64_t* eb = w.hfirst + c;
-      for (;;) {
-        const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
-        const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
-        const uint64_t x = pair_lookup(t, L, R);
-        const uint32_t rho = x != ~0ULL ? (uint32_t)(x >> 32) : RANK_INF;
-        if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
-        if (ra == RANK_INF && rb == RANK_INF) break;
-        if (ra <= rb) {
-          const uint64_t e = ea[i++];
-          if (e & HR_LAST) L = (uint32_t)e & SYM_ID;
-        } else {
-          const uint64_t e = eb[j++];
-          if (e & HR_FIRST) R = (uint32_t)e & SYM_ID;
+  if (!all && !word_dirty(w.dirty_cur, v)) return;  // wave-uniform
+  const uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
+  if (!((cuts >> lane) & 1)) return;
+  const int bit = lane;
+  const int64_t c = v * 64 + bit;
+  // start of the segment that ends at c
+  int64_t wd = v;
+  uint64_t word = seg_word(w, wd) & ((1ULL << bit) - 1);
+  while (word == 0) word = seg_word(w, --wd);
+  const int64_t a = wd * 64 + (63 - __builtin_clzll(word));
+  uint32_t L = (uint32_t)t.byte_id[w.text[c - 1]];
+  uint32_t R = (uint32_t)t.byte_id[w.text[c]];
+  uint32_t i = 0, j = 0;
+  bool ok = true;
+  uint32_t rho = pair_rank(t, L, R);
+  if (t.cert == 2) {
+    // Any table: the two segments' merge rounds in the order the whole
+    // piece would run them (the left segment's next round first when its
+    // rank is at most the right one's: its pairs lie to the left), and at
+    // every state the pair across c must lose to one of the two heads. A
+    // round of several merges runs at a rank no earlier rule consumes the
+    // product of, so the pair it leaves across c while it goes on ranks
+    // above it and cannot merge then: the states between rounds are the
+    // ones to check.
+    const uint32_t na = w.hmeta[a], nbv = w.hmeta[c];
+    const uint64_t* ea = w.hfirst + a;
+    const uint64_t* eb = w.hfirst + c;
+    for (;;) {
+      const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
+      const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
+      if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
+      if (ra == RANK_INF && rb == RANK_INF) break;
+      if (ra <= rb) {
+        const uint64_t e = ea[i++];
+        if (e & HR_LAST) {
+          L = (uint32_t)e & SYM_ID;
+          rho = pair_rank(t, L, R);
+        }
+      } else {
+        const uint64_t e = eb[j++];
+        if (e & HR_FIRST) {
+          R = (uint32_t)e & SYM_ID;
+          rho = pair_rank(t, L, R);
         }
       }
     }
-    const uint32_t ma = w.hmeta[a], mb = w.hmeta[c];
-    const uint32_t na = ma >> 16, nbv = mb & 0xFFFF;
+  } else {
+    const uint32_t na = w.hmeta[a] >> 16, nbv = w.hmeta[c] & 0xFFFF;
     const uint64_t* ea = w.hlast + a;
     const uint64_t* eb = w.hfirst + c;
-    for (; t.cert != 2;) {
+    for (;;) {
       const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
       const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
-      const uint64_t x = pair_lookup(t, L, R);
-      const uint32_t rho = x != ~0ULL ? (uint32_t)(x >> 32) : RANK_INF;
       if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
       if (ra == RANK_INF && rb == RANK_INF) break;
       if (ra <= rb) { L = (uint32_t)ea[i]; ++i; }
       if (rb <= ra) { R = (uint32_t)eb[j]; ++j; }
+      rho = pair_rank(t, L, R);
     }
-    if (!ok) {
-      atomicOr(reinterpret_cast<unsigned long long*>(&w.failm[v]), 1ULL << bit);
-      atomicAdd(w.nfail, 1u);
-      // end of the segment that starts at c
-      int64_t we = v;
-      uint64_t up = seg_word(w, we) & ~mask_le(bit);
-      while (up == 0) up = seg_word(w, ++we);
-      const int64_t e = we * 64 + __builtin_ctzll(up);
-      for (int64_t q = a >> 6; q <= (e >> 6); ++q)
-        atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
-                 1ULL << (q & 63));
-    }
+  }
+  if (!ok) {
+    atomicOr(reinterpret_cast<unsigned long long*>(&w.failm[v]), 1ULL << bit);
+    atomicAdd(w.nfail, 1u);
+    // end of the segment that starts at c
+    int64_t we = v;
+    uint64_t up = seg_word(w, we) & ~mask_le(bit);
+    while (up == 0) up = seg_word(w, ++we);
+    const int64_t e = we * 64 + __builtin_ctzll(up);
+    for (int64_t q = a >> 6; q <= (e >> 6); ++q)
+      atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
+               1ULL << (q & 63));
   }
 }
 
@@ -2571,7 +2697,7 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop) {
   const int64_t nwords = (w.nb + 63) / 64;
-  launch_ev(k_certify, dim3((uint32_t)((nwords + 255) / 256)), dim3(256), s,
+  launch_ev(k_certify, dim3((uint32_t)((nwords + 3) / 4)), dim3(256), s,
             nullptr, stop, t, w, nwords, all);
   return hipGetLastError();
 }
@@ -2903,18 +3029,21 @@ hipError_t scratch_region(int device, uint8_t** p) {
   return hipSuccess;
 }
 
-__global__ void k_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb) {
+__global__ void k_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb,
+                        uint64_t* c, uint32_t nc) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < na) a[i] = 0;
   if (i < nb) b[i] = 0;
+  if (i < nc) c[i] = 0;
 }
 
 hipError_t launch_clear(uint32_t* a, uint32_t na, uint64_t* b, uint32_t nb,
-                        hipStream_t s) {
-  const uint32_t n = na > nb ? na : nb;
+                        uint64_t* c, uint32_t nc, hipStream_t s) {
+  uint32_t n = na > nb ? na : nb;
+  n = n > nc ? n : nc;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(k_clear, dim3((n + 255) / 256), dim3(256), 0, s, a, na,
-                     b, nb);
+                     b, nb, c, nc);
   return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@
 #include <chrono>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -27,6 +28,7 @@
 
 #include "../../include/toktier_hip.h"
 #include "tk_device.h"
+#include "tk_staging.h"
 
 namespace {
 
@@ -178,12 +180,13 @@ struct Workspace {
   uint64_t *failm = nullptr, *hfirst = nullptr, *hlast = nullptr;
   uint64_t *dirty_cur = nullptr, *dirty_next = nullptr;
   uint64_t *lits = nullptr, *litb = nullptr, *docmask_lit = nullptr;
+  uint64_t* nrun = nullptr;  // per k_pretok tile
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
   uint32_t *blkcount = nullptr, *blkprefix = nullptr, *out = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
   uint32_t *pblk = nullptr, *plocal = nullptr;
   int32_t *nx = nullptr, *pv = nullptr;
-  size_t long_pairs = 0, seg_pairs = 0, out_n = 0, nblk = 0;
+  size_t long_pairs = 0, seg_pairs = 0, out_n = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
   uint32_t ctag = 0;
 };
@@ -232,7 +235,9 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.lits, words);
   take(w.litb, words);
   take(w.docmask_lit, words);
+  take(w.nrun, (size_t)tiles);
   w.cap = cap;
+  w.tiles = (size_t)tiles;
   w.long_pairs = long_cap;
   w.seg_pairs = seg_cap;
   w.out_n = cap;
@@ -286,7 +291,13 @@ struct tk_engine {
   // their own, beside the 65..WIDE_MAX-byte merges of stream2
   hipStream_t stream3 = nullptr;
   hipEvent_t ev_join3 = nullptr;
-  double last_us[5] = {};
+  // host-to-host entries: pinned staging of the request bytes and the ids,
+  // copy threads, and one event per chunk of ids coming back
+  tk::PinnedBuf pin_in, pin_out;
+  std::unique_ptr<tk::CopyPool> pool;
+  static constexpr int OUT_CHUNKS = 64;
+  hipEvent_t ev_out[OUT_CHUNKS] = {};
+  double last_us[8] = {};
   size_t last_passes = 0;
   uint32_t last_nlong = 0, last_big = 0;
 };
@@ -345,6 +356,7 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     // tags from 1 up, so zeroed words never match
     HIP_TRY(hipMemset(e->ws.ctrl, 0, 2 * tk::CTRL_WORDS * sizeof(uint32_t)));
     HIP_TRY(hipMemset(e->ws.cstat, 0, e->ws.nblk * sizeof(uint64_t)));
+    HIP_TRY(hipMemset(e->ws.nrun, 0, e->ws.tiles * sizeof(uint64_t)));
   }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
@@ -401,6 +413,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.seq = e->seq;
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
   w.nlit = ctrl + tk::CTRL_NLIT;
+  w.nrun = ws.nrun;
   w.lits = literals ? ws.lits : nullptr;
   w.litb = literals ? ws.litb : nullptr;
   w.clear_words = (int64_t)(nb / 64 + 4);
@@ -578,6 +591,104 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   return TK_OK;
 }
 
+// ---- host <-> device through the pinned staging
+constexpr size_t STAGE_SMALL = (size_t)256 << 10;  // one copy, this thread
+constexpr size_t STAGE_IN_CHUNK = (size_t)512 << 10;
+constexpr size_t STAGE_OUT_CHUNK = (size_t)1 << 20;
+
+tk::CopyPool* copy_pool(tk_engine* e) {
+  if (!e->pool) e->pool.reset(new tk::CopyPool(tk::copy_threads()));
+  return e->pool.get();
+}
+
+// Waits for the copy threads' current job when it leaves scope (their
+// chunks refer to the caller's buffers and to flags on this stack).
+struct PoolJob {
+  tk::CopyPool* pool;
+  ~PoolJob() { pool->wait(); }
+};
+
+// n request bytes at src (host) into d_dst (device) on stream s: the copy
+// threads fill the pinned staging chunk by chunk, in order, and this thread
+// starts each chunk's transfer as soon as its copy is done.
+int stage_in(tk_engine* e, uint8_t* d_dst, const uint8_t* src, size_t n,
+             hipStream_t s) {
+  HIP_TRY(e->pin_in.ensure(std::max(n, e->ws.cap) + 64));
+  uint8_t* pin = e->pin_in.p;
+  if (n <= STAGE_SMALL) {
+    std::memcpy(pin, src, n);
+    HIP_TRY(hipMemcpyAsync(d_dst, pin, n, hipMemcpyHostToDevice, s));
+    return TK_OK;
+  }
+  const size_t ch = tk::chunk_bytes(n, STAGE_IN_CHUNK, tk_engine::OUT_CHUNKS);
+  const size_t nch = (n + ch - 1) / ch;
+  std::atomic<uint8_t> ready[tk_engine::OUT_CHUNKS];
+  for (auto& r : ready) r.store(0, std::memory_order_relaxed);
+  tk::CopyPool* pool = copy_pool(e);
+  pool->start(nch, [&](size_t k) {
+    const size_t off = k * ch, len = std::min(ch, n - off);
+    std::memcpy(pin + off, src + off, len);
+    ready[k].store(1, std::memory_order_release);
+  });
+  PoolJob job{pool};
+  for (size_t k = 0; k < nch; ++k) {
+    while (!ready[k].load(std::memory_order_acquire)) std::this_thread::yield();
+    const size_t off = k * ch, len = std::min(ch, n - off);
+    HIP_TRY(hipMemcpyAsync(d_dst + off, pin + off, len, hipMemcpyHostToDevice, s));
+  }
+  return TK_OK;
+}
+
+// n ids at d_src (device) into dst (host) on stream s, after the work
+// already on s: each chunk's transfer into the pinned staging records an
+// event, and the copy threads move a chunk on to dst once this thread has
+// seen its event.
+int stage_out(tk_engine* e, uint32_t* dst, const uint32_t* d_src, size_t n,
+              hipStream_t s) {
+  const size_t bytes = n * sizeof(uint32_t);
+  HIP_TRY(e->pin_out.ensure(std::max(bytes, e->ws.cap * sizeof(uint32_t)) + 64));
+  uint8_t* pin = e->pin_out.p;
+  const uint8_t* dsrc = reinterpret_cast<const uint8_t*>(d_src);
+  uint8_t* out = reinterpret_cast<uint8_t*>(dst);
+  if (bytes <= STAGE_SMALL) {
+    HIP_TRY(hipMemcpyAsync(pin, dsrc, bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    std::memcpy(out, pin, bytes);
+    return TK_OK;
+  }
+  const size_t ch = tk::chunk_bytes(bytes, STAGE_OUT_CHUNK, tk_engine::OUT_CHUNKS);
+  const size_t nch = (bytes + ch - 1) / ch;
+  for (size_t k = 0; k < nch; ++k) {
+    const size_t off = k * ch, len = std::min(ch, bytes - off);
+    HIP_TRY(hipMemcpyAsync(pin + off, dsrc + off, len, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipEventRecord(e->ev_out[k], s));
+  }
+  std::atomic<uint8_t> ready[tk_engine::OUT_CHUNKS];
+  for (auto& r : ready) r.store(0, std::memory_order_relaxed);
+  std::atomic<uint8_t> abort{0};
+  tk::CopyPool* pool = copy_pool(e);
+  pool->start(nch, [&](size_t k) {
+    for (;;) {
+      if (ready[k].load(std::memory_order_acquire)) break;
+      if (abort.load(std::memory_order_acquire)) return;
+      std::this_thread::yield();
+    }
+    const size_t off = k * ch, len = std::min(ch, bytes - off);
+    std::memcpy(out + off, pin + off, len);
+  });
+  PoolJob job{pool};
+  for (size_t k = 0; k < nch; ++k) {
+    const hipError_t err = hipEventSynchronize(e->ev_out[k]);
+    if (err != hipSuccess) {
+      abort.store(1, std::memory_order_release);
+      return fail(TK_E_DEVICE, "hipEventSynchronize failed: %s",
+                  hipGetErrorName(err));
+    }
+    ready[k].store(1, std::memory_order_release);
+  }
+  return TK_OK;
+}
+
 // host-side checks used only on a batch whose device status flagged a
 // failure, to find the failing rows
 bool host_utf8_ok(const uint8_t* s, size_t n) {
@@ -700,8 +811,8 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
       return fail(TK_E_SHAPE, "merge token id exceeds 2^20");
   }
   for (int b = 0; b < 256; ++b)
-    if (byte_id[b] >= (1 << 20))
-      return fail(TK_E_SHAPE, "byte token id exceeds 2^20");
+    if (byte_id[b] >= (1 << 20) - 1)
+      return fail(TK_E_SHAPE, "byte token id exceeds 2^20 - 2");
 
   int ndev = 0;
   HIP_TRY(hipGetDeviceCount(&ndev));
@@ -743,6 +854,9 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
+  for (auto& ev : e->ev_out)
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+      return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
     if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
@@ -813,6 +927,11 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.byte_id = e->byte_id.p;
   e->t.vocab = e->vocab.p;
   e->t.vocab_mask = cfg->vocab_count - 1;
+  e->t.vocab_max_len = 0;
+  for (uint64_t i = 0; i < cfg->vocab_count; ++i)
+    if (vocab_keys[i] != ~0ULL)
+      e->t.vocab_max_len = std::max(e->t.vocab_max_len,
+                                    (uint32_t)((vocab_vals[i] >> 20) & 0x3FF));
   e->t.blob = e->blob.p;
   // Laguna runs the cl100k predicate inside the parts its newline-run
   // split makes; the split is a document-start pass ahead of k_pretok
@@ -867,6 +986,8 @@ void tk_engine_close(tk_engine* e) {
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   for (auto& ev : e->ev)
     if (ev) (void)hipEventDestroy(ev);
+  for (auto& ev : e->ev_out)
+    if (ev) (void)hipEventDestroy(ev);
   if (e->stream2) (void)hipStreamSynchronize(e->stream2);
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
@@ -891,7 +1012,7 @@ int tk_engine_set_timing(tk_engine* e, int enabled) {
 int tk_engine_last_timing(const tk_engine* e, double* us, int n) {
   if (!e || !us) return fail(TK_E_INVALID_ARG, "null argument");
   int k = 0;
-  for (; k < n && k < 5; ++k) us[k] = e->last_us[k];
+  for (; k < n && k < 8; ++k) us[k] = e->last_us[k];
   return k;
 }
 
@@ -1021,6 +1142,18 @@ int tk_engine_last_literals(const tk_engine* e, uint64_t* n) {
   return TK_OK;
 }
 
+int tk_engine_set_option(tk_engine* e, int option, int64_t value) {
+  if (!e) return fail(TK_E_INVALID_ARG, "engine is null");
+  std::lock_guard<std::mutex> lk(e->mu);
+  if (option == TK_OPT_COMPACT_PAIRS) {
+    if (value != 0 && value != 1)
+      return fail(TK_E_INVALID_ARG, "TK_OPT_COMPACT_PAIRS takes 0 or 1");
+    e->t.ctab = value && e->ctab.p ? e->ctab.p : nullptr;
+    return TK_OK;
+  }
+  return fail(TK_E_INVALID_ARG, "unknown option %d", option);
+}
+
 int tk_engine_last_stats(const tk_engine* e, uint64_t* out, int n) {
   if (!e || !out) return fail(TK_E_INVALID_ARG, "null argument");
   const uint64_t v[4] = {e->last_literals, e->last_nlong, e->last_big,
@@ -1120,7 +1253,7 @@ int tk_engine_encode_device_noalloc(tk_engine* e, const void* d_text,
   Workspace ws;
   carve(ws, e->scratch, TK_NOALLOC_MAX_BYTES);
   HIP_TRY(tk::launch_clear(ws.ctrl, 2 * tk::CTRL_WORDS, ws.cstat,
-                           (uint32_t)ws.nblk, s));
+                           (uint32_t)ws.nblk, ws.nrun, (uint32_t)ws.tiles, s));
   return device_encode(e, ws, d_text, nbytes, flags, d_ids, ids_cap, n_ids,
                        stream);
 }
@@ -1170,18 +1303,28 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   int rc = ensure_workspace(e, nbytes, 0);
   if (rc != TK_OK) return rc;
   hipStream_t s = e->stream;
-  HIP_TRY(hipMemcpyAsync(e->ws.text, text, nbytes, hipMemcpyHostToDevice, s));
+  using clk = std::chrono::steady_clock;
+  const auto h0 = clk::now();
+  if ((rc = stage_in(e, e->ws.text, text, nbytes, s)) != TK_OK) return rc;
+  const auto h1 = clk::now();
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
   rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, e->ws.out,
                     e->ws.out_n, &st, &total, doc_pass(e, flags, &docs));
+  const auto h2 = clk::now();
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
-  HIP_TRY(hipMemcpyAsync(ids, e->ws.out, (size_t)total * 4, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
+  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
+  const auto h3 = clk::now();
+  auto us = [](clk::duration d) {
+    return std::chrono::duration<double, std::micro>(d).count();
+  };
+  e->last_us[5] = us(h1 - h0);
+  e->last_us[6] = us(h2 - h1);
+  e->last_us[7] = us(h3 - h2);
   *n_ids = total;
   return TK_OK;
 }
@@ -1213,7 +1356,7 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
     const uint64_t p = doc_offsets[d];
     if (p < nb) mask[p >> 6] |= 1ULL << (p & 63);
   }
-  HIP_TRY(hipMemcpyAsync(e->ws.text, joined, nb, hipMemcpyHostToDevice, s));
+  if ((rc = stage_in(e, e->ws.text, joined, nb, s)) != TK_OK) return rc;
   HIP_TRY(hipMemcpyAsync(e->ws.docmask, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
@@ -1228,8 +1371,7 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipMemcpyAsync(ids, e->ws.out, (size_t)total * 4, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
+  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
   if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
     // find the rows that failed; their ids are dropped, the others stand
     std::vector<uint32_t> keep;
