@@ -136,7 +136,9 @@ int tk_engine_open(const tk_config* cfg,
 void tk_engine_close(tk_engine* engine);
 
 /* One request: host UTF-8 in, host ids out. ids_cap >= nbytes always
- * suffices (a token covers at least one byte). */
+ * suffices (a token covers at least one byte). Pageable buffers go through
+ * the engine's pinned staging (copy threads pipelined with the transfers);
+ * pinned host buffers (hipHostMalloc) are transferred directly. */
 int tk_engine_encode(tk_engine* engine, const uint8_t* text, size_t nbytes,
                      uint32_t flags, uint32_t* ids, size_t ids_cap,
                      size_t* n_ids);

@@ -111,7 +111,11 @@ struct DevWork {
   uint32_t* seglist;     // segments that fit no grid window
   uint32_t* segcount;    // ctrl[3]
   uint32_t seg_cap;
-  uint32_t* nfail;       // ctrl[4]
+  uint32_t* nfail;       // this certify pass's failed cuts (ctrl[4] / [8])
+  uint32_t* nfail_prev;  // a device-side repair pass: the previous pass's
+                         // count (the pass runs only when it is not 0);
+                         // nullptr for the first pass and every other stage
+  uint32_t* npass;       // device-side repair passes that ran (ctrl)
   uint64_t* dirty_cur;   // repair pass: words (64 bytes) to redo, 1 bit each
   uint64_t* dirty_next;  // words marked by the current certify pass
   // packed short-piece BPE
@@ -149,8 +153,8 @@ constexpr uint64_t HR_FIRST = 1ull << 31, HR_LAST = 1ull << 30;
 
 // ctrl word layout (device -> host)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
-              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PCOUNT = 16,
-              CTRL_UEND = 32, CTRL_WORDS = 64;
+              CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PASS = 7,
+              CTRL_FAIL2 = 8, CTRL_PCOUNT = 16, CTRL_UEND = 32, CTRL_WORDS = 64;
 // gate words in host memory: k_pack_copy writes GATE_NLONG / GATE_BIG and
 // then GATE_SEQ (the host learns, while the packed merge runs, whether the
 // long-piece stages have any work), k_compact's last block
@@ -158,7 +162,7 @@ constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
 // GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
               GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_NLIT = 7,
-              GATE_WORDS = 8;
+              GATE_PASS = 8, GATE_WORDS = 16;
 
 // Added-token literals on the device: the trie over their bytes, stored as
 // one hash table of its edges. Slot = key << 36 | child << 16 | term, key =

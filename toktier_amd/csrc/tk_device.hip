@@ -144,6 +144,12 @@ __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
   }
 }
 
+// A device-side repair pass runs only when the pass before it failed cuts.
+__device__ __forceinline__ bool pass_live(const DevWork& w) {
+  return !w.nfail_prev ||
+         __hip_atomic_load(w.nfail_prev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
 // the wave's index in its block, as a wave-uniform (scalar) value
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1031,7 +1037,6 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       const uint32_t bb = sb[sj];
       const uint64_t mWS = __ballot(bb == ' ' || bb == '\t' || bb == 0x0B || bb == 0x0C);
       const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
-      const uint64_t mDG = __ballot(bb >= '0' && bb <= '9');
       const uint64_t mHI = __ballot(bb >= 0x80);
       // (deepseek) ASCII letters, for [ascii punct][A-Za-z]+ runs
       const uint64_t mAL = RS == RS_DEEPSEEK ? __ballot(ascii_alpha((int)bb)) : 0ULL;
@@ -1692,6 +1697,7 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
                                                   const uint32_t* count,
                                                   uint32_t cap, int hist) {
   const int lane = threadIdx.x & 63;
+  if (!pass_live(w)) return;
   uint32_t n = *count;
   if (n > cap) n = cap;
   const uint32_t waves = gridDim.x * 4;
@@ -2221,6 +2227,7 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
                                                   const uint32_t* count,
                                                   uint32_t cap, int hist) {
   __shared__ WideLds lds[4];
+  if (!pass_live(w)) return;
   uint32_t n = *count;
   if (n > cap) n = cap;
   const int wv = wave_id();
@@ -2495,7 +2502,7 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
                                                        int64_t nwin, int all) {
   const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
-  if (v > nwin) return;
+  if (v > nwin || !pass_live(w)) return;
   auto seg = [&](int64_t wd) { return seg_word(w, wd); };
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
     if (!all && !word_dirty(w.dirty_cur, v) &&
@@ -2528,6 +2535,7 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
 
 // seglist entries over WIDE_MAX bytes: serial merge with histories.
 __global__ __launch_bounds__(64) void k_seg_serial(DevTables t, DevWork w) {
+  if (!pass_live(w)) return;
   uint32_t n = *w.segcount;
   if (n > w.seg_cap) n = w.seg_cap;
   const uint32_t stride = gridDim.x * blockDim.x;
@@ -2551,7 +2559,7 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
                                                  int64_t nwords, int all) {
   const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
-  if (v >= nwords) return;
+  if (v >= nwords || !pass_live(w)) return;
   if (!all && !word_dirty(w.dirty_cur, v)) return;  // wave-uniform
   const uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
   if (!((cuts >> lane) & 1)) return;
@@ -2627,10 +2635,21 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
 }
 
 // Between passes: drop the failed cuts, and make the words marked by the
-// last certify pass the dirty set of the next one.
+// last certify pass the dirty set of the next one. It starts a pass: its
+// failed-cut count starts at zero (a pass that does not run leaves zero,
+// so none after it runs either), and, when the pass runs, its segment list
+// is emptied and the pass counted.
 __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (v >= nwords) return;
+  const bool live = pass_live(w);
+  if (v == 0) {
+    *w.nfail = 0;
+    if (live) {
+      *w.segcount = 0;
+      if (w.npass) *w.npass += 1;
+    }
+  }
+  if (v >= nwords || !live) return;
   const uint64_t f = w.failm[v];
   if (f) {
     w.cuts[v] &= ~f;
@@ -2826,6 +2845,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
       w.gate[GATE_TOTAL] = total;
       w.gate[GATE_FAIL] = *w.nfail;
       w.gate[GATE_NLIT] = w.nlit ? *w.nlit : 0u;
+      w.gate[GATE_PASS] = w.npass ? *w.npass : 0u;
       __threadfence_system();
       w.gate[GATE_DONE] = w.seq;
       __threadfence_system();

@@ -399,6 +399,8 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.segcount = ctrl + tk::CTRL_SEG;
   w.seg_cap = (uint32_t)ws.seg_pairs;
   w.nfail = ctrl + tk::CTRL_FAIL;
+  w.nfail_prev = nullptr;
+  w.npass = ctrl + tk::CTRL_PASS;
   w.dirty_cur = ws.dirty_cur;
   w.dirty_next = ws.dirty_next;
   w.plist = ws.plist;
@@ -421,8 +423,25 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   return w;
 }
 
+// Certification passes over the long pieces: pass 0 certifies every cut;
+// repair pass p >= 1 drops the cuts pass p - 1 failed, redoes the joined
+// segments and certifies them again, and runs only when pass p - 1 failed
+// any cut (its count: the other of two alternating control words). Up to
+// DEV_REPAIRS repair passes are queued on the long-piece stream without
+// the host; the host continues only if cuts still fail after them.
+constexpr int DEV_REPAIRS = 6;
+uint32_t* fail_count(uint32_t* ctrl, int p) {
+  return ctrl + ((p & 1) ? tk::CTRL_FAIL2 : tk::CTRL_FAIL);
+}
+tk::DevWork pass_work(const tk::DevWork& w, uint32_t* ctrl, int p) {
+  tk::DevWork q = w;
+  q.nfail = fail_count(ctrl, p);
+  q.nfail_prev = p == 0 ? nullptr : fail_count(ctrl, p - 1);
+  return q;
+}
+
 int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
-  HIP_TRY(hipMemcpyAsync(h, ctrl, 8 * sizeof(uint32_t),
+  HIP_TRY(hipMemcpyAsync(h, ctrl, 16 * sizeof(uint32_t),
                          hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
@@ -519,10 +538,18 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     hipStream_t s2 = e->stream2;
     HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     if (big) {
+      // cut / segment / certify, then the repair passes, all on their own
+      // stream beside the packed merge and the wide merges
       hipStream_t s3 = e->stream3;
       HIP_TRY(tk::launch_long_windows(e->t, w, s3));
       HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
+      for (int p = 1; p <= DEV_REPAIRS; ++p) {
+        const tk::DevWork wp = pass_work(w, ctrl, p);
+        HIP_TRY(tk::launch_apply_fail(wp, s3));
+        HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s3));
+        HIP_TRY(tk::launch_certify(e->t, wp, 0, s3));
+      }
       HIP_TRY(hipEventRecord(e->ev_join3, s3));
       HIP_TRY(hipStreamWaitEvent(s, e->ev_join3, 0));
     }
@@ -531,7 +558,10 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     // (the end of both side streams, or of the packed merge if later)
     if (stages) HIP_TRY(hipEventRecord(ev[3], s));
   }
-  HIP_TRY(tk::launch_compact(w, s, ++ws.ctag, nullptr, at(4)));
+  // the compaction reports the failed cuts left after the last queued pass
+  tk::DevWork wc = w;
+  if (big) wc.nfail = fail_count(ctrl, DEV_REPAIRS);
+  HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag, nullptr, at(4)));
   // k_scan has left the outcome in the gate words: no read-back copy
   HIP_TRY(hipStreamSynchronize(s));
   uint32_t* h = e->host_ctrl;
@@ -539,7 +569,8 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     return fail(TK_E_INTERNAL, "outcome words were not written");
   h[tk::CTRL_STATUS] = e->gate[tk::GATE_STATUS];
   h[tk::CTRL_TOTAL] = e->gate[tk::GATE_TOTAL];
-  h[tk::CTRL_FAIL] = e->gate[tk::GATE_FAIL];
+  uint32_t residual = e->gate[tk::GATE_FAIL];
+  e->last_passes = e->gate[tk::GATE_PASS];
   e->last_literals = literals && docs->n ? e->gate[tk::GATE_NLIT] : 0;
   if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
     return fail(TK_E_INTERNAL, "piece queue overflow");
@@ -560,21 +591,26 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     for (double& x : e->last_us) x = 0.0;
     e->last_us[1] = elapsed_us(ev[1], ev[2]);
   }
-  if (h[tk::CTRL_FAIL] != 0) {
-    // every pass removes at least one cut, so this ends (at worst with each
-    // long piece as one segment); the bound only guards against a defect
-    size_t passes = 0;
+  if (residual != 0) {
+    // cuts still fail after the queued passes: more passes from the host,
+    // one at a time. Every pass removes at least one cut, so this ends (at
+    // worst with each long piece as one segment); the bound only guards
+    // against a defect.
+    int p = DEV_REPAIRS;
     if (stages) HIP_TRY(hipEventRecord(ev[5], s));
-    while (h[tk::CTRL_FAIL] != 0) {
-      if (++passes > nb + 1) return fail(TK_E_INTERNAL, "certification did not converge");
-      HIP_TRY(hipMemsetAsync(ctrl + tk::CTRL_SEG, 0, 2 * sizeof(uint32_t), s));
-      HIP_TRY(tk::launch_apply_fail(w, s));
-      HIP_TRY(tk::launch_long_segments(e->t, w, 0, s));
-      HIP_TRY(tk::launch_certify(e->t, w, 0, s));
+    while (residual != 0) {
+      if (++p > (int64_t)nb + DEV_REPAIRS + 1)
+        return fail(TK_E_INTERNAL, "certification did not converge");
+      const tk::DevWork wp = pass_work(w, ctrl, p);
+      HIP_TRY(tk::launch_apply_fail(wp, s));
+      HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s));
+      HIP_TRY(tk::launch_certify(e->t, wp, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
+      residual = h[(p & 1) ? tk::CTRL_FAIL2 : tk::CTRL_FAIL];
     }
     if (stages) HIP_TRY(hipEventRecord(ev[6], s));
-    HIP_TRY(tk::launch_compact(w, s, ++ws.ctag));
+    wc.nfail = fail_count(ctrl, p);
+    HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag));
     if (stages) HIP_TRY(hipEventRecord(ev[7], s));
     if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     if (stages) {
@@ -582,9 +618,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       e->last_us[3] = elapsed_us(ev[6], ev[7]);
       e->last_us[4] = elapsed_us(ev[0], ev[7]);
     }
-    e->last_passes = passes;
-  } else {
-    e->last_passes = 0;
+    e->last_passes = h[tk::CTRL_PASS];
   }
   *status = h[tk::CTRL_STATUS];
   *total = h[tk::CTRL_TOTAL];
@@ -608,11 +642,28 @@ struct PoolJob {
   ~PoolJob() { pool->wait(); }
 };
 
+// Pinned (page-locked, device-visible) host memory, e.g. from hipHostMalloc:
+// transfers use it directly instead of going through the staging. A
+// pageable pointer makes the query fail (hipErrorInvalidValue); that error
+// is taken back at once so no later check reports it.
+bool host_pinned(const void* p) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return a.type == hipMemoryTypeHost;
+}
+
 // n request bytes at src (host) into d_dst (device) on stream s: the copy
 // threads fill the pinned staging chunk by chunk, in order, and this thread
 // starts each chunk's transfer as soon as its copy is done.
 int stage_in(tk_engine* e, uint8_t* d_dst, const uint8_t* src, size_t n,
              hipStream_t s) {
+  if (host_pinned(src) && host_pinned(src + n - 1)) {
+    HIP_TRY(hipMemcpyAsync(d_dst, src, n, hipMemcpyHostToDevice, s));
+    return TK_OK;
+  }
   HIP_TRY(e->pin_in.ensure(std::max(n, e->ws.cap) + 64));
   uint8_t* pin = e->pin_in.p;
   if (n <= STAGE_SMALL) {
@@ -646,6 +697,12 @@ int stage_in(tk_engine* e, uint8_t* d_dst, const uint8_t* src, size_t n,
 int stage_out(tk_engine* e, uint32_t* dst, const uint32_t* d_src, size_t n,
               hipStream_t s) {
   const size_t bytes = n * sizeof(uint32_t);
+  if (bytes == 0) return TK_OK;
+  if (host_pinned(dst) && host_pinned(reinterpret_cast<uint8_t*>(dst) + bytes - 1)) {
+    HIP_TRY(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return TK_OK;
+  }
   HIP_TRY(e->pin_out.ensure(std::max(bytes, e->ws.cap * sizeof(uint32_t)) + 64));
   uint8_t* pin = e->pin_out.p;
   const uint8_t* dsrc = reinterpret_cast<const uint8_t*>(d_src);
