@@ -64,6 +64,10 @@ extern "C" {
                                  (pretok_classes_deepseek.v1.meta.json
                                  "patterns"; digits_max 3, the seven-class
                                  table, contractions 0) */
+#define TK_RULESET_O200K 4 /* gpt-oss: o200k_base with contractions
+                              (options.rs O200k row; kernel_families.v1.json
+                              gpt_oss_120b: digits_max 3, the seven-class
+                              table P U L C N S M of class table o200k_v4) */
 
 /* status codes */
 #define TK_OK 0

@@ -90,6 +90,16 @@ def literal_cases(name: str) -> list[str]:
             "<｜tool▁calls▁begin｜><｜tool▁call▁begin｜>f<｜tool▁sep｜>{}"
             "<｜tool▁call▁end｜><｜tool▁calls▁end｜>", "<|EOT|>123<|EOT|>4567",
         ]
+    elif name == "gpt_oss_120b":
+        texts += [
+            "<|start|>system<|message|>Reasoning: low<|end|><|start|>user"
+            "<|message|>What's 2+2?<|end|><|start|>assistant<|channel|>"
+            "analysis<|message|>easy<|end|><|start|>assistant<|channel|>"
+            "final<|message|>4<|return|>",
+            "<|start|>assistant<|channel|>commentary to=functions.f "
+            "<|constrain|>json<|message|>{}<|call|>",
+            "<|reserved_200013|>x<|endoftext|>", "<|start|", "|start|>",
+        ]
     else:
         texts += ["doc one.<|endoftext|>doc two<|endoftext|><|endoftext|>",
                   "<|endoftext"]
@@ -114,10 +124,28 @@ DEEPSEEK_CASES = [
 ]
 
 
+#: strings that reach each branch of the o200k split: letters split by
+#: case (upper-case runs before lower case, C letters after a lower-case
+#: letter or not, title case), contractions in either case and with long
+#: s, marks inside letter runs and between punctuation, the [\r\n/]* tail
+#: of a punctuation run, whitespace runs with and without CR/LF, digit
+#: groups of three
+O200K_CASES = [
+    "HelloWorld", "HTTPServer", "ABCdef", "iPhone", "camelCaseWord",
+    "ÀÉÎ'll", "x'S", "X'RE", "it'sſ", "don'tcha", "'s", "!'s", "a'b",
+    "e\u0301\u0301", "!\u0301!", "!!\u0301a", " \u0301a", "a \u0301!",
+    "\u0301x", "中文ABC def", "中ABCd", "a中文Abc", "ʰABC", "ǅungla ǅUNG ǆx",
+    "!\n/\n/x", "...\n\n  x", "!\r\n/!", "a!\n/\u0301b", "\n   x",
+    "  \n  \n\t", "x \r\n y", "\t\tword", "end   ", "1234567", "12 345",
+    "a1234b", "½²³⁴", "SHOUT'S Mc'Donald O'NEIL", "中" * 30 + "AB cd",
+    "!" + "\u0301!" * 20, "!!" + "\u0301!" * 20, "\n" + " " * 40 + "x",
+]
+
+
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
     for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
-                 "deepseek_v3"):
+                 "deepseek_v3", "gpt_oss_120b"):
         js = standin.load_artifact_json(name)
         tok = Tokenizer.from_str(js)
         rng = np.random.default_rng(99)
@@ -131,6 +159,8 @@ def main() -> None:
         texts += literal_cases(name)
         if name == "deepseek_v3":
             texts += DEEPSEEK_CASES
+        if name == "gpt_oss_120b":
+            texts += O200K_CASES
         cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}
                  for t in texts]
         out["families"][name] = {

@@ -58,6 +58,8 @@ def test_long_mixed_text(name):
     k, t = kit(name), tok(name)
     fn = {"qwen3_8b": workloads.config2, "llama_3_1_8b": workloads.config4,
           "gpt2": workloads.config2, "laguna_s_2_1": workloads.config4,
+          "gpt_oss_120b": lambda js, n_chars: workloads.config5(
+              js, n_chars=n_chars, n_runs=4, run_chars=20_000),
           "deepseek_v3": lambda js, n_chars: workloads.config5(
               js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
     text = fn(k.json, n_chars=300_000)
@@ -396,3 +398,110 @@ def test_dropped_bytes_match_hf():
             assert list(r.array) == hf.encode(s, add_special_tokens=False).ids
     finally:
         t.close()
+
+
+# o200k (gpt-oss): strings through every state of the split automaton
+# (letters split by case, contractions, marks in letter runs and between
+# punctuation, the [\r\n/]* tail, whitespace after CR/LF, digit groups)
+O200K_BRANCHES = [
+    "HelloWorld", "HTTPServer", "ABCdef", "iPhone", "camelCaseWord",
+    "ÀÉÎ'll", "x'S", "X'RE", "it'sſ", "don'tcha", "'s", "!'s", "a'b",
+    "é́", "!́!", "!!́a", " ́a", "a ́!",
+    "́x", "中文ABC def", "中ABCd", "a中文Abc", "ʰABC", "ǅungla ǅUNG ǆx",
+    "!\n/\n/x", "...\n\n  x", "!\r\n/!", "a!\n/́b", "\n   x",
+    "  \n  \n\t", "x \r\n y", "\t\tword", "end   ", "1234567", "12 345",
+    "a1234b", "½²³⁴", "SHOUT'S Mc'Donald O'NEIL", "I'M HERE'LL 'VE",
+]
+
+
+def _o200k_long_runs(rng):
+    """Runs no word or tile resolves alone: C letters after a lower-case
+    letter or not (the state differs until an upper-case letter ends the
+    run), P / mark alternations after one P or two, whitespace after a
+    CR/LF, upper-case runs after a C letter; at lengths around the 64-byte
+    word and the 3072-byte tile, with and without a lead-in. The long C
+    runs are random ideographs (each run is one piece; a periodic piece of
+    tens of KB would be merged serially)."""
+    def cjk(n):
+        return "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, n))
+    out = []
+    for n in (20, 21, 22, 1023, 1024, 1025, 3071, 3072, 3073, 12_000, 40_000):
+        run = cjk(n)
+        for lead in ("", "a", "A", " ", "x" * 61, "y" * 3070):
+            out.append(lead + run + "ABC d")
+            out.append(lead + run + "ABCd")
+        if n > 3100:
+            continue
+        out.append("!" + "\u0301!" * n + "x")
+        out.append("!!" + "\u0301!" * n + "x")
+        out.append("\n" + " " * n + "x")
+        out.append("\n" + " " * n + "\n x")
+        out.append("\u4e2d" + "A" * n + " b")
+        out.append("\u4e2d" + "A" * n + "b")
+    for _ in range(20):
+        alpha = ["\u4e2d", "\u6587", "a", "A", "\u0301", "!", ".", " ", "\n",
+                 "/", "'", "s"]
+        w = rng.dirichlet(np.ones(len(alpha)))
+        n = int(rng.integers(1, 20_000))
+        out.append("".join(alpha[int(i)] for i in rng.choice(len(alpha), size=n, p=w)))
+    return out
+
+
+def test_o200k_branches_match_hf():
+    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    for s in O200K_BRANCHES:
+        for pre in ("", "z", " ", "中", "x" * 62):
+            u = pre + s
+            assert list(t.encode(u).array) == k.hf_ids(u), repr(u)
+
+
+def test_o200k_long_runs_match_oracle():
+    """The automaton's state carried across words, the waves' blocks and
+    tiles (a tile whose halo word does not fix its entry state composes
+    its function and looks back over the tiles before it)."""
+    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    rng = np.random.default_rng(41)
+    texts = _o200k_long_runs(rng)
+    for s in texts:
+        got = t.encode(s).array
+        want = k.oracle.encode_bytes(s.encode())
+        assert np.array_equal(got, want), (len(s), s[:20])
+    for s in texts[::9]:
+        assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
+
+
+def test_o200k_documents_cut_inside_runs():
+    """Batch rows cut anywhere in long runs: a document start resets the
+    state, and each row equals the oracle's encode of that document."""
+    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    rng = np.random.default_rng(43)
+    run = "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, 9000))
+    base = ("a" + run + "ABC d " + "!!" + "\u0301!" * 3000 + "\n" +
+            " " * 3000 + "x" + "\u4e2d" + "A" * 3000 + "b")
+    docs, at = [], 0
+    while at < len(base):
+        n = int(rng.integers(0, 5000))
+        docs.append(base[at:at + n])
+        at += n
+    for d, r in zip(docs, t.encode_batch(docs)):
+        assert np.array_equal(r.array, k.oracle.encode_bytes(d.encode())), len(d)
+
+
+def test_o200k_long_cjk_request_is_linear():
+    """900 KB of C letters (random ideographs) after a lower-case letter,
+    then an upper-case run: no halo word fixes a tile's entry state, so
+    every tile composes its function and looks back (a decoupled
+    look-back: each tile reads the tiles before it only until one has
+    published the state after it). The request is one letter match, a
+    single 900 KB piece."""
+    import time
+    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    rng = np.random.default_rng(47)
+    s = ("a" + "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, 300_000))
+         + "ABC d")
+    t.encode(s)
+    t0 = time.perf_counter()
+    got = t.encode(s).array
+    dt = time.perf_counter() - t0
+    assert np.array_equal(got, k.oracle.encode_bytes(s.encode()))
+    assert dt < 0.5, dt

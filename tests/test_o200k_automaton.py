@@ -1,0 +1,247 @@
+"""CPU model of the o200k split automaton (the device's ``o2k_char`` with
+the state carried across lanes, words and tiles in ``k_pretok<4, ...>``).
+
+The o200k split (oracle ruleset 4) is a left-to-right automaton over ten
+states: each character maps the state after the character before it to the
+state after itself and says, per previous state, whether it starts a
+piece; digits take the group rule instead. The model here is that
+automaton character by character. Checked: it splits every string of
+length <= 4 over the o200k alphabet of the oracle's brute-force test, every
+length-5 string over a ten-symbol core, seeded fuzz with document starts
+(each document split on its own), and composing the transitions in blocks
+(as the wave scan and the tile look-back do) gives the same states. Planted
+mistakes in the transitions (a C letter resetting LBL, the tail dropping
+'/', a two-letter contraction taking one letter, the whitespace rule
+ignoring the CR/LF before it) each split some string differently.
+"""
+
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+
+from conftest import kit
+from test_oracle import O2K_ALPHABET
+
+P, U, L, C, N, S, M = range(7)
+W = (U, L, C, M)
+PUN, TAIL, LPRE, LU, LBL, LBN, AP2, LAST1, FRESH, WS = range(10)
+NSTATE = 10
+
+
+def _classes():
+    from toktier_amd import classes
+    return classes.o200k_class_table()
+
+
+def _fold(c: int) -> int:
+    if 65 <= c <= 90:
+        return c + 32
+    return ord("s") if c == 0x17F else c
+
+
+def _crlf(c: int) -> bool:
+    return c in (10, 13)
+
+
+def transitions(cps, ds, plant=None):
+    """Per character (f, g): f[s] the state after it, g[s] its start bit
+    (None: the digit group rule), for the previous state s."""
+    cls = _classes()
+    n = len(cps)
+    cl = [int(cls[c]) for c in cps]
+
+    def nxt(j):
+        q = j + 1
+        return None if q >= n or ds[q] else q
+
+    out = []
+    for j in range(n):
+        k, c = cl[j], cps[j]
+        n1 = nxt(j)
+        n2 = nxt(n1) if n1 is not None else None
+        k1 = cl[n1] if n1 is not None else None
+        if k == N:
+            ns = FRESH
+        elif k in (U, L):
+            ns = LU if k == U else LBL
+        elif k in (C, M):
+            ns = LBN
+        elif k == P or (k == S and not _crlf(c)):
+            ns = (LPRE if k1 in W else
+                  PUN if k == P or (c == 32 and k1 == P) else WS)
+        else:
+            ns = WS
+        ap = None
+        if c == ord("'") and n1 is not None:
+            a = _fold(cps[n1])
+            if chr(a) in "stmd":
+                ap = LAST1
+            elif n2 is not None and (chr(a), chr(_fold(cps[n2]))) in (
+                    ("r", "e"), ("v", "e"), ("l", "l")):
+                ap = LAST1 if plant == "two_takes_one" else AP2
+        f1 = False  # every character from j to the letter run's end is U
+        if k == U:
+            q = nxt(j)
+            while q is not None and cl[q] == U:
+                q = nxt(q)
+            f1 = q is None or cl[q] not in W
+        f3 = True  # no CR/LF from j to the whitespace run's end
+        q = j
+        while q is not None and cl[q] == S:
+            if _crlf(cps[q]):
+                f3 = False
+                break
+            q = nxt(q)
+        prev_crlf = (j > 0 and not ds[j] and _crlf(cps[j - 1])
+                     and plant != "ws_no_crlf")
+        f, g = [ns] * NSTATE, [1] * NSTATE
+        for s in range(NSTATE):
+            if ds[j]:
+                continue
+            st, nx = 1, ns
+            if s == PUN:
+                if k in (P, M):
+                    st, nx = 0, PUN
+                elif _crlf(c):
+                    st, nx = 0, TAIL
+            elif s == TAIL:
+                if _crlf(c) or (c == ord("/") and plant != "tail_no_slash"):
+                    st, nx = 0, TAIL
+            elif s == LPRE:
+                if k in W:
+                    st = 0
+            elif s in (LU, LBL, LBN):
+                if k == U:
+                    st, nx = (1 if s == LBL else f1 if s == LBN else 0), LU
+                elif k == L:
+                    st, nx = 0, LBL
+                elif k in (C, M):
+                    keep = s if plant != "c_resets" else LBN
+                    st, nx = 0, (LBN if s == LU else keep)
+                elif ap is not None:
+                    st, nx = 0, ap
+            elif s == AP2:
+                st, nx = 0, LAST1
+            elif s == LAST1:
+                st, nx = 0, FRESH
+            elif s == WS and k == S:
+                if _crlf(c):
+                    st, nx = 0, WS
+                else:
+                    st = f3 if prev_crlf else (n1 is not None and k1 != S)
+                    nx = ns if st else WS
+            f[s], g[s] = nx, (None if k == N else int(st))
+        out.append((tuple(f), tuple(g)))
+    return out, cl
+
+
+def split(text: str, docs=(), plant=None, block: int = 0):
+    """Piece starts (char indices) of `text` with documents starting at
+    the indices `docs`; block > 0: the states come from compositions of
+    `block` transitions at a time (the state after each block from its
+    composed function, the states inside it from prefix compositions)."""
+    cps = [ord(ch) for ch in text]
+    n = len(cps)
+    ds = [i == 0 or i in docs for i in range(n)]
+    fg, cl = transitions(cps, ds, plant)
+    states = [0] * n
+    if block:
+        s = FRESH
+        for a in range(0, n, block):
+            F = tuple(range(NSTATE))
+            for j in range(a, min(n, a + block)):
+                F = tuple(fg[j][0][F[x]] for x in range(NSTATE))
+                states[j] = F[s]
+            s = F[s]
+    else:
+        s = FRESH
+        for j in range(n):
+            s = fg[j][0][s]
+            states[j] = s
+    out, run = [], 0
+    for j in range(n):
+        prev = states[j - 1] if j else FRESH
+        st = fg[j][1][prev]
+        if cl[j] == N:
+            run = 0 if ds[j] or cl[j - 1] != N else run
+            st = int(ds[j] or run % 3 == 0)
+            run += 1
+        if st:
+            out.append(j)
+    return out
+
+
+def _oracle():
+    from oracle.oracle import Oracle
+    return Oracle(kit("gpt2").tables, _classes(), None, 4, 3, False)
+
+
+def oracle_split(o, text: str, docs=()) -> list[int]:
+    cuts = [0, *sorted(d for d in docs if 0 < d < len(text)), len(text)]
+    out = []
+    for a, b in zip(cuts, cuts[1:]):
+        seg = text[a:b]
+        idx = {len(seg[:i].encode()): i for i in range(len(seg) + 1)}
+        out += [a + idx[x] for x in o.pretokenize(seg.encode())[:-1]]
+    return out
+
+
+CORE = ["A", "b", "中", "́", ".", " ", "'", "s", "\n", "/"]
+
+
+@pytest.mark.slow
+def test_automaton_splits_like_the_oracle_exhaustively():
+    o = _oracle()
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 5)
+         for p in itertools.product(O2K_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(CORE, repeat=5)))
+    bad = [t for t in cases if split(t) != oracle_split(o, t)]
+    assert not bad, [repr(t) for t in bad[:10]]
+
+
+def test_automaton_splits_like_the_oracle():
+    o = _oracle()
+    for t in ("".join(p) for n in range(1, 4)
+              for p in itertools.product(O2K_ALPHABET, repeat=n)):
+        assert split(t) == oracle_split(o, t), repr(t)
+    rng = np.random.default_rng(11)
+    for _ in range(3000):
+        n = int(rng.integers(1, 60))
+        t = "".join(O2K_ALPHABET[int(i)] for i in rng.integers(0, len(O2K_ALPHABET), n))
+        docs = sorted(set(int(x) for x in rng.integers(1, n + 1, size=int(rng.integers(0, 4)))))
+        want = oracle_split(o, t, docs)
+        assert split(t, docs) == want, (repr(t), docs)
+        assert split(t, docs, block=int(rng.integers(1, 9))) == want, (repr(t), docs)
+
+
+def test_automaton_on_long_runs():
+    """Runs no fixed context resolves: C letters after an L letter or not,
+    P / M alternations after one P or two, whitespace runs after a CR/LF."""
+    o = _oracle()
+    texts = ["a" + "中" * 200 + "ABC d", "中" * 200 + "ABC d", "中" * 200 + "ABCd",
+             "!" + "́!" * 100 + "x", "!!" + "́!" * 100 + "x",
+             "\n" + " " * 150 + "x", "\n" + " " * 150 + "\n x",
+             "x" + "'" * 99 + "s", "It'" + "s" * 50 + "'LL", "a!\n/\n/" * 30]
+    for t in texts:
+        assert split(t) == oracle_split(o, t), repr(t)
+        assert split(t, block=64) == oracle_split(o, t), repr(t)
+
+
+PLANTS = ["c_resets", "tail_no_slash", "two_takes_one", "ws_no_crlf"]
+
+
+@pytest.mark.parametrize("plant", PLANTS)
+def test_planted_transition_mistakes_are_caught(plant):
+    o = _oracle()
+    hits = [t for t in ("".join(p) for n in range(1, 5)
+                        for p in itertools.product(CORE + ["r", "e", "\t"], repeat=n))
+            if split(t, plant=plant) != oracle_split(o, t)]
+    found = {"c_resets": "b中Ad", "tail_no_slash": "./\n/",
+             "ws_no_crlf": "\n \t\t"}.get(plant)
+    assert hits, plant
+    if found:
+        assert split(found, plant=plant) != oracle_split(o, found), plant

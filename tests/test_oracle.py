@@ -287,6 +287,8 @@ def test_oracle_matches_hf_on_mixed_text(name):
     gen = {"qwen3_8b": workloads.config2, "gpt2": workloads.config2,
            "llama_3_1_8b": workloads.config4,
            "laguna_s_2_1": workloads.config4,
+           "gpt_oss_120b": lambda js, n_chars: workloads.config5(
+               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
            "deepseek_v3": lambda js, n_chars: workloads.config5(
                js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
     text = gen(k.json, n_chars=200_000)

@@ -76,4 +76,8 @@ def o200k_class_table() -> np.ndarray:
 
 def table_for(ruleset_name: str) -> np.ndarray:
     """The class table a family's ruleset reads."""
-    return deepseek_class_table() if ruleset_name == "deepseek" else class_table()
+    if ruleset_name == "deepseek":
+        return deepseek_class_table()
+    if ruleset_name == "o200k":
+        return o200k_class_table()
+    return class_table()

@@ -48,7 +48,8 @@ __host__ __device__ __forceinline__ uint32_t pair_alt(uint32_t b1, uint32_t tag,
 
 // Device copies of the family tables, in the engine's own layout.
 struct DevTables {
-  const uint8_t* cls;          // [0x110000] P/L/N/S (deepseek: O L M N PS WS CRLF)
+  const uint8_t* cls;          // [0x110000] P/L/N/S (deepseek: O L M N PS WS CRLF;
+                               // o200k: P U L C N S M)
   const uint8_t* nfc;          // [0x110000] quick-check values or nullptr
   const ulonglong2* pairs;     // interleaved {key, val} merge hash slots
   uint64_t pair_mask;
@@ -58,7 +59,7 @@ struct DevTables {
   uint64_t vocab_mask;
   uint32_t vocab_max_len;      // bytes of the longest vocabulary entry
   const uint8_t* blob;         // vocabulary bytes
-  int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek
+  int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek, 4 o200k
   int32_t dmax;                // digit group width (cl100k)
   int32_t ignore_merges;
   int32_t needs_nfc;
@@ -138,6 +139,9 @@ struct DevWork {
   // per tile of k_pretok: the digit run at its end (call tag << 32 | whole
   // tile | N characters), or nullptr
   uint64_t* nrun;
+  // (o200k) per tile of k_pretok: two words of its automaton function /
+  // the state after it (o2_publish)
+  uint64_t* ostate;
   // per-call clearing done by k_pretok for the stages after it
   uint32_t* ctrl_next;   // the other control slot (used by the next call)
   int64_t clear_words;   // inlong / failm words

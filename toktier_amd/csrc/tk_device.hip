@@ -755,6 +755,211 @@ __device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
   return FAST_CRLF;
 }
 
+// ---- o200k (gpt-oss): o200k_base with contractions,
+// [^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]*[\p{Ll}\p{Lm}\p{Lo}\p{M}]+C?
+// |[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]+[\p{Ll}\p{Lm}\p{Lo}\p{M}]*C?
+// |\p{N}{1,K}| ?[^\s\p{L}\p{N}]+[\r\n/]*|\s*[\r\n]+|\s+(?!\S)|\s+
+// with C = (?i:'s|'t|'re|'ve|'m|'ll|'d), over the classes P U L C N S M
+// (U = Lu Lt, L = Ll, C = Lm Lo; W = U L C M are the letter classes).
+// Whether a character starts a piece depends on context of any length to
+// its left (a mark continues a P match or a letter match; a run of C
+// characters after a lower-case letter is one letter match, after
+// anything else it can end before an upper-case run), so the split is a
+// left-to-right automaton: the state after each character, one of ten,
+// is what the character after it needs. Each character is a transition
+// function of the previous state (a nibble per state) and a start bit per
+// previous state; the functions compose by a wave scan, and a tile's
+// entry state comes from the word before it or from the tiles before it.
+// States (the previous character is ...):
+//   PUN   in a P match's [PM]+ (or the U+0020 that opens one)
+//   TAIL  in its [\r\n/]* tail
+//   LPRE  the prefix character of a letter match (a letter follows)
+//   LU    a U letter of a letter match
+//   LBL   a B letter (L C M) whose run of B letters since the last U (or
+//         the match's first letter) holds an L
+//   LBN   a B letter whose run holds no L
+//   AP2   an apostrophe that takes the next two letters ('re 've 'll)
+//   LAST1 the match holds exactly one more character (an apostrophe
+//         taking one letter, or the first of two)
+//   FRESH the match ends after it (digits, the last contraction letter)
+//   WS    in a whitespace match
+// Inside a letter run only U letters start pieces: after LBL always (the
+// [A]*[B]+ alternative stopped there), after LBN exactly when every
+// character from it to the run's end is U (A* gave the run back to its
+// last B letter); the letter match's first letter starts at its own
+// class state, and a prefix character or mark that opens one changes
+// nothing about where it ends.
+constexpr int RS_O200K = 4;
+constexpr uint8_t OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4,
+                  OK_S = 5, OK_M = 6;
+enum : uint32_t {
+  O2_PUN = 0, O2_TAIL, O2_LPRE, O2_LU, O2_LBL, O2_LBN, O2_AP2, O2_LAST1,
+  O2_FRESH, O2_WS, O2_NSTATE
+};
+constexpr uint64_t O2_REP = 0x1111111111ull;  // a nibble in every state
+constexpr uint64_t O2_ID = 0x9876543210ull;   // the identity
+constexpr uint32_t O2_ALL = (1u << O2_NSTATE) - 1;
+__device__ __forceinline__ uint32_t o2_at(uint64_t f, uint32_t s) {
+  return (uint32_t)(f >> (4 * s)) & 15u;
+}
+__device__ __forceinline__ uint64_t o2_set(uint64_t f, uint32_t s, uint32_t v) {
+  return (f & ~(15ull << (4 * s))) | ((uint64_t)v << (4 * s));
+}
+// a, then b
+__device__ __forceinline__ uint64_t o2_then(uint64_t a, uint64_t b) {
+  uint64_t h = 0;
+#pragma unroll
+  for (uint32_t s = 0; s < O2_NSTATE; ++s)
+    h |= (uint64_t)o2_at(b, o2_at(a, s)) << (4 * s);
+  return h;
+}
+__device__ __forceinline__ bool o2_const(uint64_t f) {
+  return f == (f & 15u) * O2_REP;
+}
+__device__ __forceinline__ bool ok_w(int k) {
+  return k == OK_U || k == OK_L || k == OK_C || k == OK_M;
+}
+__device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int d) {
+  const uint32_t lo = __shfl_up((uint32_t)v, d), hi = __shfl_up((uint32_t)(v >> 32), d);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// The transition of the character at i (code point cp, class k; d0: a
+// document starts at i): *fo the next state per previous state, *go the
+// start bit per previous state (digits: the caller's group rule replaces
+// it). `need_g` false skips what only the start bits read.
+template <class C>
+__device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
+                         bool need_g, uint64_t* fo, uint32_t* go) {
+  const int64_t n1 = c.next(i);
+  const Ch x1 = n1 >= 0 ? c.at(n1) : Ch{-1, -1, 0xFF};
+  const int k1 = n1 >= 0 ? x1.cl : -1;
+  const bool cr = crlf(cp);
+  // the state of a match that starts here
+  uint32_t ns;
+  if (k == OK_N) ns = O2_FRESH;
+  else if (k == OK_U) ns = O2_LU;
+  else if (k == OK_L) ns = O2_LBL;
+  else if (k == OK_C || k == OK_M) ns = O2_LBN;
+  else if (k == OK_P || (k == OK_S && !cr))
+    ns = ok_w(k1) ? O2_LPRE
+       : (k == OK_P || (cp == ' ' && k1 == OK_P)) ? O2_PUN : O2_WS;
+  else ns = O2_WS;
+  uint64_t f = (uint64_t)ns * O2_REP;
+  uint32_t g = O2_ALL;
+  if (d0) {
+    *fo = f;
+    *go = g;
+    return;
+  }
+  // a P match: [PM]+ goes on, a CR/LF opens the [\r\n/]* tail
+  if (k == OK_P || k == OK_M) {
+    f = o2_set(f, O2_PUN, O2_PUN);
+    g &= ~(1u << O2_PUN);
+  } else if (cr) {
+    f = o2_set(f, O2_PUN, O2_TAIL);
+    g &= ~(1u << O2_PUN);
+  }
+  if (cr || cp == '/') {
+    f = o2_set(f, O2_TAIL, O2_TAIL);
+    g &= ~(1u << O2_TAIL);
+  }
+  if (ok_w(k)) {
+    // a letter after a prefix or inside a letter run (the class state is
+    // ns already, except that a C or M letter keeps LBL)
+    g &= ~((1u << O2_LPRE) | (1u << O2_LU) | (1u << O2_LBL) | (1u << O2_LBN));
+    if (k == OK_U) {
+      g |= 1u << O2_LBL;
+      if (need_g) {
+        // after a C or M letter: a start when the U run reaches the
+        // letter run's end (LBN is reached only over C or M letters)
+        const int64_t p = c.prev(i);
+        const int kp = p >= 0 ? c.at(p).cl : -1;
+        if (kp == OK_C || kp == OK_M) {
+          int64_t q = n1;
+          int kq = k1;
+          while (q >= 0 && kq == OK_U) {
+            q = c.next(q);
+            kq = q >= 0 ? c.at(q).cl : -1;
+          }
+          if (!ok_w(kq)) g |= 1u << O2_LBN;
+        }
+      }
+    } else if (k != OK_L) {
+      f = o2_set(f, O2_LBL, O2_LBL);
+    }
+    // the letters a contraction takes ('s 't 'm 'd: one; 're 've 'll: two)
+    const int a = fold(cp);
+    if (a == 's' || a == 't' || a == 'm' || a == 'd' || a == 'r' ||
+        a == 'e' || a == 'v' || a == 'l') {
+      f = o2_set(o2_set(f, O2_AP2, O2_LAST1), O2_LAST1, O2_FRESH);
+      g &= ~((1u << O2_AP2) | (1u << O2_LAST1));
+    }
+  } else if (cp == '\'' && n1 >= 0) {
+    // a contraction after a letter match
+    const int a = fold(x1.cp);
+    uint32_t ap = 0;
+    if (a == 's' || a == 't' || a == 'm' || a == 'd') {
+      ap = O2_LAST1;
+    } else if (a == 'r' || a == 'v' || a == 'l') {
+      const int64_t n2 = c.next(n1);
+      if (n2 >= 0) {
+        const int b = fold(c.at(n2).cp);
+        if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') || (a == 'l' && b == 'l'))
+          ap = O2_AP2;
+      }
+    }
+    if (ap) {
+      f = o2_set(o2_set(o2_set(f, O2_LU, ap), O2_LBL, ap), O2_LBN, ap);
+      g &= ~((1u << O2_LU) | (1u << O2_LBL) | (1u << O2_LBN));
+    }
+  }
+  if (k == OK_S) {
+    // whitespace: \s*[\r\n]+ ends after the run's last CR/LF; after that
+    // (or with none) \s+(?!\S) leaves the run's last character
+    bool s = false;
+    if (!cr && need_g) {
+      const int64_t p = c.prev(i);
+      if (p >= 0 && crlf(c.at(p).cp)) {
+        s = true;
+        for (int64_t q = n1; q >= 0;) {
+          const Ch x = c.at(q);
+          if (x.cl != OK_S) break;
+          if (crlf(x.cp)) { s = false; break; }
+          q = c.next(q);
+        }
+      } else {
+        s = n1 >= 0 && k1 != OK_S;
+      }
+    } else if (!cr) {
+      // (the state does not need the walk: a start inside the run before
+      // its last character leaves the state WS either way)
+      s = n1 >= 0 && k1 != OK_S;
+    }
+    if (!s) {
+      f = o2_set(f, O2_WS, O2_WS);
+      g &= ~(1u << O2_WS);
+    }
+  }
+  *fo = f;
+  *go = g;
+}
+
+// a tile's automaton word pair (ostate[2t], ostate[2t + 1]): call tag << 32
+// | the low 32 bits of the tile's function, and call tag << 32 | kind << 8
+// | state << 12 | the function's high 8 bits, kind O2_AGG (the function)
+// or O2_INCL (the state after the tile)
+constexpr uint32_t O2_AGG = 1, O2_INCL = 2;
+__device__ __forceinline__ void o2_publish(uint64_t* p, uint32_t seq, uint32_t kind,
+                                           uint64_t f, uint32_t s) {
+  if (kind == O2_AGG)
+    __hip_atomic_store(p, ((uint64_t)seq << 32) | (uint32_t)f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p + 1, ((uint64_t)seq << 32) | (kind << 8) | (s << 12) |
+                                (uint32_t)((f >> 32) & 0xFF),
+                     __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // exclusive scan of one value per thread over a 256-thread block
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   __shared__ uint32_t wsum[4];
@@ -802,6 +1007,10 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   // at the word's end
   __shared__ uint64_t gNL[PT_TILE / 64 + 2], gBR[PT_TILE / 64 + 2];
   __shared__ uint32_t gC[PT_TILE / 64 + 1];
+  // (o200k) the functions of the words before the waves' blocks, the
+  // blocks' functions, and the blocks' entry states
+  __shared__ uint64_t o2w[4], o2b[4];
+  __shared__ uint32_t o2e[4];
   const int tid = threadIdx.x;
   if (tid < PACK_CLASSES) {
     lcnt[tid] = 0;
@@ -921,8 +1130,10 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   __syncthreads();
   const int lane = tid & 63, wv = wave_id();
   // the ruleset's class of an entry, and its digit / P / whitespace classes
-  auto kcl = [](uint32_t e) { return RS == RS_DEEPSEEK ? dcl(e) : ecl(e); };
-  constexpr int KN = RS == RS_DEEPSEEK ? DS_N : CN_;
+  auto kcl = [](uint32_t e) {
+    return RS == RS_DEEPSEEK || RS == RS_O200K ? dcl(e) : ecl(e);
+  };
+  constexpr int KN = RS == RS_DEEPSEEK ? DS_N : RS == RS_O200K ? OK_N : CN_;
   constexpr int KP = RS == RS_DEEPSEEK ? DS_PS : CP_;
   auto kws = [](int k) { return RS == RS_DEEPSEEK ? k >= DS_WS : k == CS_; };
   // Digit groups (\p{N}{1,K}, K > 1) count the N characters of the run
@@ -939,7 +1150,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   // tagged with the call number, and a tile whose halo holds no break reads
   // its predecessors' (bounded waits). Every digit is then one lookup.
   uint32_t st = 0;  // status bits of the tile
-  const bool groups = (RS == 0 || RS == RS_DEEPSEEK) && t.dmax > 1;
+  const bool groups = (RS == 0 || RS == RS_DEEPSEEK || RS == RS_O200K) && t.dmax > 1;
   if (groups) {
     for (int k = wv - 1; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
       const int64_t p = base + 64 * k + lane;
@@ -1210,8 +1421,200 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       }
     }
   };
-  if (DM && dm) start_words(std::true_type{});
-  else start_words(std::false_type{});
+  // o200k: the automaton over the tile (o2k_char). Wave wv takes the
+  // contiguous words [12 wv, 12 wv + 12) (wave 3 also the word after the
+  // tile) and carries the state from word to word. Its entry state is the
+  // function of the word before its block when that function is constant
+  // (on ordinary text it is). Otherwise every wave first composes its
+  // block's function, and thread 0 takes the tile's entry from the word
+  // before the tile or from the tiles before it (each tile publishes its
+  // whole function before it looks back, and the state after it once
+  // known: a decoupled look-back with bounded waits) and derives the
+  // blocks' entries. Every tile publishes the state after it.
+  auto o2k_words = [&](auto dflag) {
+    constexpr bool D = decltype(dflag)::value;
+    auto ds = [&](int L) {
+      if (!D) return L == Lz;
+      const int64_t i = lo + L;
+      return i == 0 || ((sdm[(i >> 6) - wlo] >> (i & 63)) & 1) != 0;
+    };
+    constexpr int WPB = PT_TILE / 64 / (PRETOK_TPB / 64);  // words per wave
+    // the lane's transition and start bits in word k (-1 .. PT_TILE / 64);
+    // positions outside the text and inside a character pass the state on
+    auto lane_fn = [&](int k, bool need_g, uint64_t* f, uint32_t* g) {
+      const int64_t i = base + 64 * k + lane;
+      const int Li = PT_HALO + 64 * k + lane;
+      *f = O2_ID;
+      *g = 0;
+      if (i < 0 || i >= nb || is_cont(sb[64 * k + lane + PT_PAD])) return;
+      const uint32_t e = se[Li];
+      const int kc = dcl(e);
+      const bool d0 = ds(Li);
+      o2k_char(c, i, (int32_t)(e & 0x1FFFFF), kc, d0, need_g, f, g);
+      if (need_g && kc == OK_N && !d0) {
+        // \p{N}{1,K}: the N characters of the run before i decide
+        bool r = true;
+        if (groups) {
+          const uint64_t below = (1ULL << lane) - 1;
+          const uint64_t n = gNL[k + 1], b = gBR[k + 1] & below;
+          uint32_t cnt;
+          if (b) {
+            const int h = 63 - __builtin_clzll(b);
+            cnt = (uint32_t)__popcll(n & below & ~mask_le(h)) + (uint32_t)((n >> h) & 1);
+          } else {
+            cnt = gC[k] + (uint32_t)__popcll(n & below);
+          }
+          r = cnt % (uint32_t)t.dmax == 0;
+        }
+        *g = r ? O2_ALL : 0u;
+      }
+    };
+    // inclusive composition over the lanes (lane 0 first): windows of four
+    // when every window from lane 4 on is constant (then each is the state
+    // after its lane whatever came before), else the whole prefix
+    auto scan = [&](uint64_t F) {
+      uint64_t o = shfl_up64(F, 1);
+      if (lane >= 1) F = o2_then(o, F);
+      o = shfl_up64(F, 2);
+      if (lane >= 2) F = o2_then(o, F);
+      if (__any(lane >= 4 && !o2_const(F))) {
+        for (int d = 4; d < 64; d <<= 1) {
+          o = shfl_up64(F, d);
+          if (lane >= d) F = o2_then(o, F);
+        }
+      }
+      return F;
+    };
+    auto lane63 = [&](uint64_t v) {
+      const uint32_t a = __shfl((uint32_t)v, 63), b = __shfl((uint32_t)(v >> 32), 63);
+      return ((uint64_t)b << 32) | a;
+    };
+    // the function of word k (lane 63's composition), wave-uniform
+    auto word_fn = [&](int k) {
+      uint64_t f;
+      uint32_t g;
+      lane_fn(k, false, &f, &g);
+      return lane63(scan(f));
+    };
+    // word k from entry state `carry`: its start word; returns the state
+    // after it
+    auto word = [&](int k, uint32_t carry) -> uint32_t {
+      const int64_t wd = (base >> 6) + k;
+      if (wd >= nwords) {  // past the sentinel words: all starts
+        if (lane == 0) sw[k] = ~0ULL;
+        return carry;
+      }
+      uint64_t f;
+      uint32_t g;
+      lane_fn(k, true, &f, &g);
+      const uint32_t sj = o2_at(scan(f), carry);  // the state after the lane
+      uint32_t sp = __shfl_up(sj, 1);
+      if (lane == 0) sp = carry;
+      const int64_t i = base + 64 * k + lane;
+      const int Li = PT_HALO + 64 * k + lane;
+      const uint32_t bb = sb[64 * k + lane + PT_PAD];
+      const bool in = i < nb;
+      const bool lead = in && !is_cont((uint8_t)bb);
+      const uint32_t e = se[Li];
+      if (in && !((e >> 27) & 1)) st |= ST_UTF8;
+      // sentinel starts past the text; no start inside a character
+      const bool s = !in || (lead && ((g >> sp) & 1));
+      if (w.check_nfc && lead) {
+        const uint32_t cp = e & 0x1FFFFF;
+        const uint8_t v = cp < 256 ? ltab[cp] >> LTAB_NFC : t.nfc[cp];
+        if (v == 255) {
+          st |= ST_NFC;
+        } else if (v != 0 && !ds(Li)) {
+          const uint32_t pc = se[prv(Li)] & 0x1FFFFF;
+          if ((pc < 256 ? ltab[pc] >> LTAB_NFC : t.nfc[pc]) > v) st |= ST_NFC;
+        }
+      }
+      uint64_t m = __ballot(s);
+      if (DM && w.litb) m &= ~w.litb[wd];
+      if (lane == 0) {
+        sw[k] = m;
+        if (k < PT_TILE / 64) w.starts[wd] = m;
+      }
+      return (uint32_t)__shfl((int)sj, 63);
+    };
+    const int k0 = WPB * wv;
+    // the word before the block (the tile's halo word for wave 0); the
+    // first tile starts at a document start, whatever came before
+    uint64_t T = word_fn(k0 - 1);
+    if (blockIdx.x == 0 && wv == 0) T = (uint64_t)O2_FRESH * O2_REP;
+    if (lane == 0) o2w[wv] = T;
+    __syncthreads();
+    bool fast = true;
+    for (int j = 0; j < PRETOK_TPB / 64; ++j) fast &= o2_const(o2w[j]);
+    uint32_t carry;
+    uint64_t* op = w.ostate + 2 * (int64_t)blockIdx.x;
+    if (fast) {
+      carry = (uint32_t)(o2w[wv] & 15);
+    } else {
+      uint64_t B = O2_ID;
+      for (int k = k0; k < k0 + WPB; ++k) B = o2_then(B, word_fn(k));
+      if (lane == 0) o2b[wv] = B;
+      __syncthreads();
+      if (tid == 0) {
+        uint64_t A = o2b[0];
+        for (int j = 1; j < PRETOK_TPB / 64; ++j) A = o2_then(A, o2b[j]);
+        uint32_t entry = O2_FRESH;
+        if (o2_const(o2w[0])) {
+          entry = (uint32_t)(o2w[0] & 15);
+        } else {
+          o2_publish(op, w.seq, O2_AGG, A, 0);
+          // G: the function of the tiles after u up to this one
+          uint64_t G = O2_ID;
+          bool done = false;
+          for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0 && !done; --u) {
+            const uint64_t* q = w.ostate + 2 * u;
+            uint64_t v1;
+            int spin = 0;
+            while ((uint32_t)((v1 = __hip_atomic_load(q + 1, __ATOMIC_ACQUIRE,
+                                                      __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
+                   w.seq) {
+              if (++spin > NRUN_SPIN) break;
+              __builtin_amdgcn_s_sleep(2);
+            }
+            if ((uint32_t)(v1 >> 32) != w.seq) {
+              st |= ST_STALL;
+              done = true;
+            } else if (((v1 >> 8) & 3) == O2_INCL) {
+              entry = o2_at(G, (uint32_t)(v1 >> 12) & 15);
+              done = true;
+            } else {
+              const uint64_t v0 = __hip_atomic_load(q, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+              G = o2_then((uint32_t)v0 | ((v1 & 0xFF) << 32), G);
+              if (o2_const(G)) {
+                entry = (uint32_t)(G & 15);
+                done = true;
+              }
+            }
+          }
+          // (past tile 0 nothing came before: position 0 starts a document)
+          if (!done) entry = o2_at(G, O2_FRESH);
+        }
+        o2_publish(op, w.seq, O2_INCL, 0, o2_at(A, entry));
+        o2e[0] = entry;
+        for (int j = 1; j < PRETOK_TPB / 64; ++j) o2e[j] = o2_at(o2b[j - 1], o2e[j - 1]);
+      }
+      __syncthreads();
+      carry = o2e[wv];
+    }
+    for (int k = k0; k < k0 + WPB; ++k) carry = word(k, carry);
+    if (wv == PRETOK_TPB / 64 - 1) {
+      if (fast && lane == 0) o2_publish(op, w.seq, O2_INCL, 0, carry);
+      word(PT_TILE / 64, carry);
+    }
+  };
+  if constexpr (RS == RS_O200K) {
+    if (DM && dm) o2k_words(std::true_type{});
+    else o2k_words(std::false_type{});
+  } else {
+    if (DM && dm) start_words(std::true_type{});
+    else start_words(std::false_type{});
+  }
   if (st) atomicOr(w.status, st);
   __syncthreads();
   // Stage-2 bookkeeping for the pieces that start in this tile: finish the
@@ -1283,6 +1686,9 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
   } else if (t.ruleset == RS_DEEPSEEK) {
     if (dm) launch_ev(k_pretok<RS_DEEPSEEK, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<RS_DEEPSEEK, false>, g, b, s, start, stop, t, w, nwords);
+  } else if (t.ruleset == RS_O200K) {
+    if (dm) launch_ev(k_pretok<RS_O200K, true>, g, b, s, start, stop, t, w, nwords);
+    else launch_ev(k_pretok<RS_O200K, false>, g, b, s, start, stop, t, w, nwords);
   } else {
     if (dm) launch_ev(k_pretok<0, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<0, false>, g, b, s, start, stop, t, w, nwords);

@@ -180,7 +180,8 @@ struct Workspace {
   uint64_t *failm = nullptr, *hfirst = nullptr, *hlast = nullptr;
   uint64_t *dirty_cur = nullptr, *dirty_next = nullptr;
   uint64_t *lits = nullptr, *litb = nullptr, *docmask_lit = nullptr;
-  uint64_t* nrun = nullptr;  // per k_pretok tile
+  uint64_t* nrun = nullptr;  // per k_pretok tile: the digit run, then two
+                             // automaton words (o200k)
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
   uint32_t *blkcount = nullptr, *blkprefix = nullptr, *out = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
@@ -235,7 +236,7 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.lits, words);
   take(w.litb, words);
   take(w.docmask_lit, words);
-  take(w.nrun, (size_t)tiles);
+  take(w.nrun, 3 * (size_t)tiles);
   w.cap = cap;
   w.tiles = (size_t)tiles;
   w.long_pairs = long_cap;
@@ -312,7 +313,8 @@ int validate(const tk_config* cfg, const uint8_t* class_table, size_t class_len,
     return fail(TK_E_INVALID_ARG, "abi_version %u != %u", cfg->abi_version,
                 TK_ABI_VERSION);
   if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K &&
-      cfg->ruleset != TK_RULESET_LAGUNA && cfg->ruleset != TK_RULESET_DEEPSEEK)
+      cfg->ruleset != TK_RULESET_LAGUNA && cfg->ruleset != TK_RULESET_DEEPSEEK &&
+      cfg->ruleset != TK_RULESET_O200K)
     return fail(TK_E_INVALID_ARG, "unsupported ruleset %d", cfg->ruleset);
   if (cfg->ruleset != TK_RULESET_R50K &&
       (cfg->digits_max < 1 || cfg->digits_max > 64))
@@ -325,8 +327,10 @@ int validate(const tk_config* cfg, const uint8_t* class_table, size_t class_len,
   if (class_len < PLANE)
     return fail(TK_E_SHAPE, "class table does not cover U+10FFFF");
   {
-    // four classes (P L N S), seven for deepseek (O L M N PS WS CRLF)
-    const uint8_t top = cfg->ruleset == TK_RULESET_DEEPSEEK ? 6 : 3;
+    // four classes (P L N S), seven for deepseek (O L M N PS WS CRLF) and
+    // for o200k (P U L C N S M)
+    const uint8_t top =
+        cfg->ruleset == TK_RULESET_DEEPSEEK || cfg->ruleset == TK_RULESET_O200K ? 6 : 3;
     uint8_t mx = 0;
     for (size_t i = 0; i < PLANE; ++i) mx = class_table[i] > mx ? class_table[i] : mx;
     if (mx > top)
@@ -356,7 +360,7 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
     // tags from 1 up, so zeroed words never match
     HIP_TRY(hipMemset(e->ws.ctrl, 0, 2 * tk::CTRL_WORDS * sizeof(uint32_t)));
     HIP_TRY(hipMemset(e->ws.cstat, 0, e->ws.nblk * sizeof(uint64_t)));
-    HIP_TRY(hipMemset(e->ws.nrun, 0, e->ws.tiles * sizeof(uint64_t)));
+    HIP_TRY(hipMemset(e->ws.nrun, 0, 3 * e->ws.tiles * sizeof(uint64_t)));
   }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
@@ -416,6 +420,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
   w.nlit = ctrl + tk::CTRL_NLIT;
   w.nrun = ws.nrun;
+  w.ostate = ws.nrun + ws.tiles;
   w.lits = literals ? ws.lits : nullptr;
   w.litb = literals ? ws.litb : nullptr;
   w.clear_words = (int64_t)(nb / 64 + 4);
@@ -734,12 +739,17 @@ int stage_out(tk_engine* e, uint32_t* dst, const uint32_t* d_src, size_t n,
     std::memcpy(out + off, pin + off, len);
   });
   PoolJob job{pool};
+  // poll the chunks' events (a blocking wait can sleep for far longer than
+  // a chunk's transfer takes)
   for (size_t k = 0; k < nch; ++k) {
-    const hipError_t err = hipEventSynchronize(e->ev_out[k]);
-    if (err != hipSuccess) {
-      abort.store(1, std::memory_order_release);
-      return fail(TK_E_DEVICE, "hipEventSynchronize failed: %s",
-                  hipGetErrorName(err));
+    for (;;) {
+      const hipError_t err = hipEventQuery(e->ev_out[k]);
+      if (err == hipSuccess) break;
+      if (err != hipErrorNotReady) {
+        abort.store(1, std::memory_order_release);
+        return fail(TK_E_DEVICE, "hipEventQuery failed: %s", hipGetErrorName(err));
+      }
+      std::this_thread::yield();
     }
     ready[k].store(1, std::memory_order_release);
   }
@@ -1310,7 +1320,7 @@ int tk_engine_encode_device_noalloc(tk_engine* e, const void* d_text,
   Workspace ws;
   carve(ws, e->scratch, TK_NOALLOC_MAX_BYTES);
   HIP_TRY(tk::launch_clear(ws.ctrl, 2 * tk::CTRL_WORDS, ws.cstat,
-                           (uint32_t)ws.nblk, ws.nrun, (uint32_t)ws.tiles, s));
+                           (uint32_t)ws.nblk, ws.nrun, 3 * (uint32_t)ws.tiles, s));
   return device_encode(e, ws, d_text, nbytes, flags, d_ids, ids_cap, n_ids,
                        stream);
 }

@@ -30,7 +30,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 __all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K",
-           "RULESET_LAGUNA", "RULESET_DEEPSEEK", "DEEPSEEK_STAGES"]
+           "RULESET_LAGUNA", "RULESET_DEEPSEEK", "RULESET_O200K",
+           "DEEPSEEK_STAGES", "O200K_PATTERN"]
 
 #: Device ruleset ids (the ``ruleset`` field of the engine config).
 RULESET_CL100K = 0
@@ -45,6 +46,12 @@ RULESET_LAGUNA = 2
 #: DeepSeek V3 / V4: three Split(Isolated) stages, applied in order
 #: (``pretok_classes_deepseek.v1.meta.json`` ``patterns``).
 RULESET_DEEPSEEK = 3
+
+#: o200k (gpt-oss; ``kernel_families.v1.json`` family ``gpt_oss_120b``:
+#: band and ruleset o200k, class table o200k_v4, digits_max 3,
+#: contractions true): letters split by case, contraction suffixes,
+#: digit groups of three.
+RULESET_O200K = 4
 
 #: Laguna's stage 0, split with behavior MergedWithNext.
 LAGUNA_STAGE0 = r"(?:\r?\n)+"
@@ -66,8 +73,8 @@ DEEPSEEK_STAGES = (
     "|\\s*[\r\n]+|\\s+(?!\\S)|\\s+",
 )
 
-#: o200k_base with contractions (gpt-oss; ``options.rs`` O200k row). The
-#: oracle restates it (ruleset 4 there); the device ruleset is not built.
+#: o200k_base with contractions (gpt-oss; ``options.rs`` O200k row; the
+#: oracle's and the device's ruleset 4).
 O200K_PATTERN = (
     r"[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]*[\p{Ll}\p{Lm}\p{Lo}\p{M}]+"
     r"(?i:'s|'t|'re|'ve|'m|'ll|'d)?"
@@ -86,8 +93,8 @@ GPT2_PATTERN = (
 @dataclass(frozen=True)
 class Family:
     name: str
-    ruleset: int           # RULESET_CL100K / _R50K / _LAGUNA / _DEEPSEEK
-    ruleset_name: str      # "cl100k" / "r50k" / "laguna" / "deepseek"
+    ruleset: int           # RULESET_CL100K / _R50K / _LAGUNA / _DEEPSEEK / _O200K
+    ruleset_name: str      # "cl100k" / "r50k" / "laguna" / "deepseek" / "o200k"
     pattern: str
     digits_max: int        # digit group width (cl100k); 0 = unbounded (r50k)
     contractions_fold: bool  # (?i:...) contractions (cl100k) vs case-sensitive
@@ -135,6 +142,16 @@ FAMILIES: dict[str, Family] = {
         hf_repo="deepseek-ai/DeepSeek-V3",
         # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (7,847,652 B)
         real_sha256="621ac2e32d0dba658404412318818aaa8ce8cda492e59830109d8da6b517fb41",
+    ),
+    "gpt_oss_120b": Family(
+        name="gpt_oss_120b", ruleset=RULESET_O200K, ruleset_name="o200k",
+        pattern=O200K_PATTERN, digits_max=3, contractions_fold=True,
+        # tiktoken-derived, as Llama-3: no normalizer, whole-vocabulary
+        # pieces first
+        needs_nfc=False, ignore_merges=True, vocab_size=199998,
+        hf_repo="openai/gpt-oss-120b",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (27,868,174 B)
+        real_sha256="0614fe83cadab421296e664e1f48f4261fa8fef6e03e63bb75c20f38e37d07d3",
     ),
     "gpt2": Family(
         name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",

@@ -27,6 +27,10 @@ Shapes follow the real artifacts:
   ``ignore_merges`` false.
 - ``gpt2``: ``ByteLevel(use_regex=True)`` pre-tokenizer; 50,000 merges,
   50,257 entries including ``<|endoftext|>``.
+- ``gpt_oss_120b``: no normalizer; ``Split(o200k regex, isolated)`` +
+  ``ByteLevel(use_regex=False)``; BPE with ``ignore_merges`` true over
+  199,998 regular entries, merges re-derived tiktoken-style as for
+  Llama-3, and the harmony markers from id 199,998.
 
 The committed artifacts live in ``toktier_amd/data/artifacts`` (xz
 compressed); this module regenerates them (``python -m toktier_amd.standin``),
@@ -227,6 +231,8 @@ def _train(name: str) -> dict:
         corpus += _synthetic_corpus(20261202, 1_500_000, 800_000, 10000)
     elif name == "deepseek_v3":
         corpus += _synthetic_corpus(20261203, 8_000_000, 1_000_000, 40000)
+    elif name == "gpt_oss_120b":
+        corpus += _synthetic_corpus(20261204, 6_000_000, 1_500_000, 40000)
     tok.train_from_iterator(corpus, trainer)
     spec = json.loads(tok.to_str())
     model = spec["model"]
@@ -235,7 +241,7 @@ def _train(name: str) -> dict:
         raise RuntimeError(
             f"{name}: corpus too small: vocab {len(vocab)} < {n_regular}")
     model["ignore_merges"] = bool(fam.ignore_merges)
-    if name == "llama_3_1_8b":
+    if name in ("llama_3_1_8b", "gpt_oss_120b"):
         model["merges"] = _tiktoken_style_merges(vocab)
     if name == "gpt2":
         vocab["<|endoftext|>"] = 50256
@@ -263,6 +269,15 @@ def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
                  "<｜tool▁output▁begin｜>", "<｜tool▁output▁end｜>",
                  "<｜tool▁sep｜>", "<think>", "</think>"]
         return [(c, 128000 + k, k < 3) for k, c in enumerate(names)]
+    if name == "gpt_oss_120b":
+        # the harmony markers after the 199,998 regular tokens (the named
+        # ones, and the reserved slots between them)
+        named = {199998: "<|startoftext|>", 199999: "<|endoftext|>",
+                 200002: "<|return|>", 200003: "<|constrain|>",
+                 200005: "<|channel|>", 200006: "<|start|>",
+                 200007: "<|end|>", 200008: "<|message|>", 200012: "<|call|>"}
+        return [(named.get(i, f"<|reserved_{i}|>"), i, True)
+                for i in range(199998, 200019)]
     if name == "laguna_s_2_1":
         # (the real list is not recorded offline; chat and FIM markers in
         # the common form)

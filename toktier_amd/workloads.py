@@ -273,7 +273,9 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
     ... ``<|im_end|>`` (assistant turns with a ``<think>`` block), Llama-3
     header / ``<|eot_id|>`` turns after ``<|begin_of_text|>``, DeepSeek
     ``<｜User｜>`` / ``<｜Assistant｜>`` turns after the sentence marker
-    (assistant turns closed by ``<｜end▁of▁sentence｜>``), GPT-2
+    (assistant turns closed by ``<｜end▁of▁sentence｜>``), gpt-oss harmony
+    ``<|start|>role<|message|>`` ... ``<|end|>`` turns (assistant turns on
+    the final channel, some after an analysis one), GPT-2
     documents joined by ``<|endoftext|>``. Turns hold U[200, 3000] chars."""
     rng = np.random.default_rng(SEED_BASE + 6 + 1000 * sample)
     body = config2(tokenizer_json, n_chars=n_chars, sample=sample)
@@ -296,6 +298,15 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
             piece = (f"<｜Assistant｜>{content}<｜end▁of▁sentence｜>"
                      if role == "assistant" else
                      f"<｜User｜>{content}" if role == "user" else content)
+        elif family == "gpt_oss_120b":
+            if role == "assistant":
+                cut = n // 3 if rng.random() < 0.5 else 0
+                piece = ((f"<|start|>assistant<|channel|>analysis<|message|>"
+                          f"{content[:cut]}<|end|>" if cut else "") +
+                         f"<|start|>assistant<|channel|>final<|message|>"
+                         f"{content[cut:]}<|return|>")
+            else:
+                piece = f"<|start|>{role}<|message|>{content}<|end|>"
         else:
             piece = content + "<|endoftext|>"
         out.append(piece)
