@@ -64,10 +64,17 @@ extern "C" {
                                  (pretok_classes_deepseek.v1.meta.json
                                  "patterns"; digits_max 3, the seven-class
                                  table, contractions 0) */
-#define TK_RULESET_O200K 4 /* gpt-oss: o200k_base with contractions
-                              (options.rs O200k row; kernel_families.v1.json
-                              gpt_oss_120b: digits_max 3, the seven-class
-                              table P U L C N S M of class table o200k_v4) */
+#define TK_RULESET_O200K 4 /* gpt-oss: o200k_base (options.rs O200k row;
+                              kernel_families.v1.json gpt_oss_120b: digits_max
+                              3, contractions; the rows with contractions
+                              false and digits_max 1 too), the seven-class
+                              table P U L C N S M of class table o200k_v4 */
+#define TK_RULESET_KIMI 5  /* Kimi K3: [\p{Han}]+ first, the o200k letter
+                              alternatives without Han, \p{N}{1,3}, a
+                              punctuation tail without '/' (conversion.py
+                              KIMI_PATTERN; kernel_families.v1.json kimi_k3:
+                              digits_max 3, contractions), the ten-class
+                              table of kimi_v1 (P U L C N S M HL HN HP) */
 
 /* status codes */
 #define TK_OK 0
@@ -101,9 +108,11 @@ typedef struct tk_config {
   uint32_t abi_version;        /* TK_ABI_VERSION */
   int32_t device_ordinal;
   int32_t ruleset;             /* TK_RULESET_* */
-  int32_t digits_max;          /* cl100k: 1 (Qwen) or 3 (Llama); r50k: 0 */
+  int32_t digits_max;          /* cl100k: 1 (Qwen) or 3 (Llama); r50k: 0;
+                                  kimi: 3 */
   int32_t contractions;        /* 1, or 0 for deepseek (its pattern has
-                                  no contraction alternative) */
+                                  no contraction alternative); o200k: 1 or
+                                  0 (the rows without the suffix) */
   int32_t needs_nfc;           /* family declares an NFC normalizer */
   int32_t ignore_merges;       /* whole-piece vocabulary hit first */
   uint64_t pair_count;         /* slots in pair_keys (power of two) */

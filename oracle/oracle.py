@@ -28,6 +28,7 @@ class _Tables(C.Structure):
         ("vocab_blob", C.c_void_p), ("nfc_qc", C.c_void_p),
         ("ruleset", C.c_int32), ("digits_max", C.c_int32),
         ("ignore_merges", C.c_int32), ("needs_nfc", C.c_int32),
+        ("contractions", C.c_int32),
     ]
 
 
@@ -70,7 +71,8 @@ class Oracle:
     """Sequential restatement bound to one family's tables."""
 
     def __init__(self, tables, cls: np.ndarray, nfc_qc: np.ndarray | None,
-                 ruleset: int, digits_max: int, needs_nfc: bool):
+                 ruleset: int, digits_max: int, needs_nfc: bool,
+                 contractions: bool = True):
         self._keep = [tables.pair_keys, tables.pair_vals, tables.byte_id,
                       tables.vocab_keys, tables.vocab_vals,
                       tables.vocab_blob, cls, nfc_qc]
@@ -83,7 +85,8 @@ class Oracle:
             tables.vocab_vals.ctypes.data, tables.vocab_keys.size,
             blob.ctypes.data,
             nfc_qc.ctypes.data if nfc_qc is not None else None,
-            ruleset, digits_max, int(tables.ignore_merges), int(needs_nfc))
+            ruleset, digits_max, int(tables.ignore_merges), int(needs_nfc),
+            int(contractions))
         self._lib = lib()
         self._added = None
 

@@ -39,7 +39,15 @@
  *       (crates/.../pretokenize/options.rs O200k row; kernel_families.v1.json
  *        gpt_oss_120b: digits_max 3, contractions), with the seven-class
  *        table P U L C N S M (U = Lu Lt, L = Ll, C = Lm Lo; class table
- *        o200k_v4, whose sha256 the probed table reproduces)
+ *        o200k_v4, whose sha256 the probed table reproduces); the o200k
+ *        rows with contractions false drop C
+ *       kimi (Kimi K3): [\p{Han}]+ first, then the o200k alternatives with
+ *         the letter classes minus Han, \p{N}{1,3} (Han numbers too),
+ *         ' ?[^\s\p{L}\p{N}]+[\r\n]*' (no '/' in the tail) and the
+ *         whitespace ones (src/toktier/artifacts/conversion.py
+ *         KIMI_PATTERN), with the ten-class table of kimi_v1 (the o200k
+ *         seven without Han, HL HN HP; its sha256 the probed table
+ *         reproduces)
  *     with \s / \p{L} / \p{N} membership read from the probed class table
  *     (classes P=0 L=1 N=2 S=3, pretok_kernel.cu:63) and the case folding
  *     of (?i:...) restricted to A-Z and U+017F (pretok_kernel.cu:153-158);
@@ -355,15 +363,21 @@ static int64_t pieces_deepseek(const int32_t* cp, const uint8_t* cl,
   return p;
 }
 
-/* ---- o200k: classes P U L C N S M (o200k_v4) */
-enum { OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4, OK_S = 5, OK_M = 6 };
+/* ---- o200k: classes P U L C N S M (o200k_v4); kimi adds HL HN HP
+ * (kimi_v1: Han letters, Han numbers, other Han), and its letter classes
+ * hold no Han */
+enum { OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4, OK_S = 5, OK_M = 6,
+       OK_HL = 7, OK_HN = 8, OK_HP = 9 };
 
 static int ok_a(uint8_t k) { return k == OK_U || k == OK_C || k == OK_M; }
 static int ok_b(uint8_t k) { return k == OK_L || k == OK_C || k == OK_M; }
-/* [^\r\n\p{L}\p{N}] */
+static int ok_han(uint8_t k) { return k >= OK_HL; }
+/* [^\r\n\p{L}\p{N}] (kimi: Han that is neither letter nor number too) */
 static int ok_q(uint8_t k, int32_t c) {
-  return (k == OK_P || k == OK_M || k == OK_S) && !is_crlf(c);
+  return (k == OK_P || k == OK_M || k == OK_S || k == OK_HP) && !is_crlf(c);
 }
+/* [^\s\p{L}\p{N}] */
+static int ok_pm(uint8_t k) { return k == OK_P || k == OK_M || k == OK_HP; }
 
 /* [A]*[B]+ from t (A = Lu Lt Lm Lo M, B = Ll Lm Lo M): A* takes the
  * longest run, then gives characters back until B+ can start; B+ then runs
@@ -407,33 +421,41 @@ static int64_t ok_contraction(const int32_t* cp, int64_t e, int64_t n) {
   return e;
 }
 
-/* End of the o200k match that starts at char i. Each letter alternative is
- * tried with the optional prefix first taking cp[i], then without it. */
+/* End of the o200k / kimi match that starts at char i. kimi: [\p{Han}]+
+ * first, \p{N} and [^\s\p{L}\p{N}] take the Han numbers and the other Han,
+ * and the punctuation tail is [\r\n]* (o200k: [\r\n/]*). Each letter
+ * alternative is tried with the optional prefix first taking cp[i], then
+ * without it; `contr` false drops the contraction suffix. */
 static int64_t match_o200k(const int32_t* cp, const uint8_t* cl, int64_t i,
-                           int64_t n, int K) {
+                           int64_t n, int K, int kimi, int contr) {
+  if (kimi && ok_han(cl[i])) {
+    int64_t j = i + 1;
+    while (j < n && ok_han(cl[j])) ++j;
+    return j;
+  }
   const int q = ok_q(cl[i], cp[i]);
   int64_t e = -1;
   if (q && i + 1 < n) e = ok_letters1(cl, i + 1, n);
   if (e < 0) e = ok_letters1(cl, i, n);
   if (e < 0 && q && i + 1 < n) e = ok_letters2(cl, i + 1, n);
   if (e < 0) e = ok_letters2(cl, i, n);
-  if (e >= 0) return ok_contraction(cp, e, n);
-  if (cl[i] == OK_N) {
+  if (e >= 0) return contr ? ok_contraction(cp, e, n) : e;
+  if (cl[i] == OK_N || cl[i] == OK_HN) {
     int64_t j = i + 1;
-    while (j < n && cl[j] == OK_N && j - i < K) ++j;
+    while (j < n && (cl[j] == OK_N || cl[j] == OK_HN) && j - i < K) ++j;
     return j;
   }
-  /*  ?[^\s\p{L}\p{N}]+[\r\n/]* */
+  /*  ?[^\s\p{L}\p{N}]+[\r\n/]* (kimi: [\r\n]*) */
   {
     int64_t j = -1;
     if (cp[i] == ' ') {
-      if (i + 1 < n && (cl[i + 1] == OK_P || cl[i + 1] == OK_M)) j = i + 1;
-    } else if (cl[i] == OK_P || cl[i] == OK_M) {
+      if (i + 1 < n && ok_pm(cl[i + 1])) j = i + 1;
+    } else if (ok_pm(cl[i])) {
       j = i;
     }
     if (j >= 0) {
-      while (j < n && (cl[j] == OK_P || cl[j] == OK_M)) ++j;
-      while (j < n && (is_crlf(cp[j]) || cp[j] == '/')) ++j;
+      while (j < n && ok_pm(cl[j])) ++j;
+      while (j < n && (is_crlf(cp[j]) || (!kimi && cp[j] == '/'))) ++j;
       return j;
     }
   }
@@ -489,11 +511,17 @@ int64_t tko_pretokenize(const tko_tables* t, const uint8_t* s, int64_t nb,
     if (t->ruleset == TKO_RULESET_LAGUNA) end = next_newline_run(cp, i, n);
     while (i < end) {
       starts[p++] = bo[i];
-      i = t->ruleset == TKO_RULESET_R50K
+      const int64_t j = t->ruleset == TKO_RULESET_R50K
               ? match_r50k(cp, cl, i, end)
-              : t->ruleset == TKO_RULESET_O200K
-              ? match_o200k(cp, cl, i, end, t->digits_max)
+              : t->ruleset == TKO_RULESET_O200K || t->ruleset == TKO_RULESET_KIMI
+              ? match_o200k(cp, cl, i, end, t->digits_max,
+                            t->ruleset == TKO_RULESET_KIMI, t->contractions)
               : match_cl100k(cp, cl, i, end, t->digits_max, 1);
+      if (j <= i) {  /* a class the ruleset does not know: no match */
+        free(cp); free(bo); free(cl);
+        return TKO_E_CLASS;
+      }
+      i = j;
     }
   }
   starts[p] = nb;

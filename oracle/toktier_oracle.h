@@ -9,14 +9,17 @@
 #define TKO_RULESET_LAGUNA 2
 #define TKO_RULESET_DEEPSEEK 3
 #define TKO_RULESET_O200K 4
+#define TKO_RULESET_KIMI 5
 
 #define TKO_E_UTF8 (-1)
 #define TKO_E_NOMEM (-2)
 #define TKO_E_NEEDS_NFC (-3)
 #define TKO_E_CAP (-4)
+#define TKO_E_CLASS (-5)  /* a class value the ruleset does not define */
 
 typedef struct tko_tables {
-  const uint8_t* cls;          /* 0x110000 class bytes (P/L/N/S; deepseek: O L M N PS WS CRLF) */
+  const uint8_t* cls;          /* 0x110000 class bytes (P/L/N/S; deepseek: O L M N PS WS
+                                  CRLF; o200k: P U L C N S M; kimi: + HL HN HP) */
   const uint64_t* pair_keys;
   const uint64_t* pair_vals;
   uint64_t pair_count;         /* power of two */
@@ -30,6 +33,7 @@ typedef struct tko_tables {
   int32_t digits_max;
   int32_t ignore_merges;
   int32_t needs_nfc;
+  int32_t contractions;         /* o200k / kimi: the (?i:'s|...) suffix */
 } tko_tables;
 
 int64_t tko_utf8_decode(const uint8_t* s, int64_t nb, int32_t* cp, int64_t* bo);

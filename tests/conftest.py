@@ -15,7 +15,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
-                "deepseek_v3", "gpt_oss_120b")
+                "deepseek_v3", "gpt_oss_120b", "kimi_k3")
 
 
 def pytest_configure(config):

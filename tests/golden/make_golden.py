@@ -90,6 +90,16 @@ def literal_cases(name: str) -> list[str]:
             "<｜tool▁calls▁begin｜><｜tool▁call▁begin｜>f<｜tool▁sep｜>{}"
             "<｜tool▁call▁end｜><｜tool▁calls▁end｜>", "<|EOT|>123<|EOT|>4567",
         ]
+    elif name == "kimi_k3":
+        texts += [
+            "<|im_system|>system<|im_middle|>You are Kimi.<|im_end|>"
+            "<|im_user|>user<|im_middle|>1+1=?<|im_end|><|im_assistant|>"
+            "assistant<|im_middle|>2<|im_end|>",
+            "<|tool_calls_section_begin|><|tool_call_begin|>f"
+            "<|tool_call_argument_begin|>{}<|tool_call_end|>"
+            "<|tool_calls_section_end|>", "[BOS]x[EOS]", "<|reserved_token_163600|>",
+            "<|im_end", "[UNK][PAD]",
+        ]
     elif name == "gpt_oss_120b":
         texts += [
             "<|start|>system<|message|>Reasoning: low<|end|><|start|>user"
@@ -142,10 +152,23 @@ O200K_CASES = [
 ]
 
 
+#: strings that reach each branch of the kimi split: Han runs of every
+#: subclass (letters, numbers U+3007 / U+3021, other Han U+2E80), Han
+#: numbers inside and at the start of digit groups, other Han inside
+#: punctuation runs, the tail without '/', letters split by case next to
+#: Han, contractions
+KIMI_CASES = [
+    "中文ABC def", "中ABCd", "a中文Abc", "Hello世界's", "世界's", "12〇〇34",
+    "〇1234〇〇〇5678", "1〇2〇3〇4", "〡〢〣12", "!⺀x", " ⺀!", "⺀⺀中〇",
+    "a!\n/b", "!\r\n/!", "x'S 中'S", "ǅungla ǅUNG", "e\u0301中", "中\u0301",
+    "中" * 30 + "AB cd", "1" * 20 + "〇" * 5 + "2" * 7, "々々ABC",
+]
+
+
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
     for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
-                 "deepseek_v3", "gpt_oss_120b"):
+                 "deepseek_v3", "gpt_oss_120b", "kimi_k3"):
         js = standin.load_artifact_json(name)
         tok = Tokenizer.from_str(js)
         rng = np.random.default_rng(99)
@@ -161,6 +184,8 @@ def main() -> None:
             texts += DEEPSEEK_CASES
         if name == "gpt_oss_120b":
             texts += O200K_CASES
+        if name == "kimi_k3":
+            texts += KIMI_CASES
         cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}
                  for t in texts]
         out["families"][name] = {

@@ -60,6 +60,8 @@ def test_long_mixed_text(name):
           "gpt2": workloads.config2, "laguna_s_2_1": workloads.config4,
           "gpt_oss_120b": lambda js, n_chars: workloads.config5(
               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+          "kimi_k3": lambda js, n_chars: workloads.config5(
+              js, n_chars=n_chars, n_runs=4, run_chars=20_000),
           "deepseek_v3": lambda js, n_chars: workloads.config5(
               js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
     text = fn(k.json, n_chars=300_000)
@@ -505,3 +507,85 @@ def test_o200k_long_cjk_request_is_linear():
     dt = time.perf_counter() - t0
     assert np.array_equal(got, k.oracle.encode_bytes(s.encode()))
     assert dt < 0.5, dt
+
+
+# kimi: Han runs of every subclass, Han numbers inside and at the start of
+# digit groups, other Han in punctuation runs, the tail without '/'
+KIMI_BRANCHES = [
+    "中文ABC def", "中ABCd", "a中文Abc", "Hello世界's", "世界's", "12〇〇34",
+    "〇1234〇〇〇5678", "1〇2〇3〇4", "〡〢〣12", "!⺀x", " ⺀!", "⺀⺀中〇",
+    "a!\n/b", "!\r\n/!", "x'S 中'S", "ǅungla ǅUNG", "é中", "中́",
+    "々々ABC", "I'M HERE'LL", "12345678901",
+]
+
+
+def test_kimi_branches_match_hf():
+    k, t = kit("kimi_k3"), tok("kimi_k3")
+    for s in KIMI_BRANCHES:
+        for pre in ("", "z", " ", "中", "1", "x" * 62):
+            u = pre + s
+            assert list(t.encode(u).array) == k.hf_ids(u), repr(u)
+
+
+def _kimi_runs(rng):
+    out = []
+    for n in (20, 63, 64, 65, 1023, 1024, 1025, 3071, 3072, 3073, 9000):
+        for lead in ("", "a", "1", "〇", "x" * 61, "y" * 3070):
+            digits = "".join("0123456789〇〡〢"[int(i)] for i in rng.integers(0, 13, n))
+            out.append(lead + digits + " z")
+            out.append(lead + "7" * n + "〇" + "8" * 5)
+            han = "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, n))
+            out.append(lead + han + "ABC d")
+        out.append("!" + "⺀!" * n + "x")
+        out.append("\n" + " " * n + "x")
+    for _ in range(20):
+        alpha = ["中", "〇", "⺀", "a", "A", "1", "2", "!", " ", "\n", "/", "'"]
+        w = rng.dirichlet(np.ones(len(alpha)))
+        n = int(rng.integers(1, 20_000))
+        out.append("".join(alpha[int(i)] for i in rng.choice(len(alpha), size=n, p=w)))
+    return out
+
+
+def test_kimi_long_runs_match_oracle():
+    """Digit groups counted in the automaton's state across words and
+    tiles (a long digit run leaves no word function constant, so tiles
+    compose theirs and look back), Han runs, punctuation runs."""
+    k, t = kit("kimi_k3"), tok("kimi_k3")
+    rng = np.random.default_rng(53)
+    texts = _kimi_runs(rng)
+    for s in texts:
+        got = t.encode(s).array
+        want = k.oracle.encode_bytes(s.encode())
+        assert np.array_equal(got, want), (len(s), s[:20])
+    for s in texts[::9]:
+        assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
+
+
+def test_kimi_documents_cut_inside_runs():
+    k, t = kit("kimi_k3"), tok("kimi_k3")
+    rng = np.random.default_rng(59)
+    base = ("1" * 7000 + "〇" * 3 + "2" * 500 + " " +
+            "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, 4000)) +
+            "ABC" + "!⺀" * 2000 + "\n/" + "a" * 100)
+    docs, at = [], 0
+    while at < len(base):
+        n = int(rng.integers(0, 4000))
+        docs.append(base[at:at + n])
+        at += n
+    for d, r in zip(docs, t.encode_batch(docs)):
+        assert np.array_equal(r.array, k.oracle.encode_bytes(d.encode())), len(d)
+
+
+def test_kimi_million_digit_request_is_linear():
+    """A 1,000,000-digit request: every tile composes its function (the
+    digit states cycle, so no word fixes the state) and looks back over
+    published tile functions (decoupled look-back), in linear time."""
+    import time
+    k, t = kit("kimi_k3"), tok("kimi_k3")
+    s = "1234567890" * 100_000
+    t.encode(s)
+    t0 = time.perf_counter()
+    got = t.encode(s).array
+    dt = time.perf_counter() - t0
+    assert np.array_equal(got, k.oracle.encode_bytes(s.encode()))
+    assert dt < 0.25, dt

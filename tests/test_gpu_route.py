@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt2",
                                   "laguna_s_2_1", "deepseek_v3",
-                                  "gpt_oss_120b"])
+                                  "gpt_oss_120b", "kimi_k3"])
 def test_route_admission(name):
     import toktier_amd
     from toktier_amd import registry

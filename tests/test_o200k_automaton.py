@@ -1,5 +1,6 @@
-"""CPU model of the o200k split automaton (the device's ``o2k_char`` with
-the state carried across lanes, words and tiles in ``k_pretok<4, ...>``).
+"""CPU model of the o200k and kimi split automaton (the device's
+``o2k_char`` with the state carried across lanes, words and tiles in
+``k_pretok<4, ...>`` / ``k_pretok<5, ...>``).
 
 The o200k split (oracle ruleset 4) is a left-to-right automaton over ten
 states: each character maps the state after the character before it to the
@@ -13,6 +14,11 @@ length-5 string over a ten-symbol core, seeded fuzz with document starts
 mistakes in the transitions (a C letter resetting LBL, the tail dropping
 '/', a two-letter contraction taking one letter, the whitespace rule
 ignoring the CR/LF before it) each split some string differently.
+
+kimi adds three states (in a Han run; one or two digits into a
+\p{N}{1,3} group, since a Han number continues a group but opens a Han
+run at a group's start) and the same checks run against oracle ruleset 5
+over an alphabet with a Han letter, a Han number and other Han.
 """
 
 from __future__ import annotations
@@ -23,17 +29,16 @@ import numpy as np
 import pytest
 
 from conftest import kit
-from test_oracle import O2K_ALPHABET
+from test_oracle import KIMI_ALPHABET, O2K_ALPHABET
 
-P, U, L, C, N, S, M = range(7)
+P, U, L, C, N, S, M, HL, HN, HP = range(10)
 W = (U, L, C, M)
-PUN, TAIL, LPRE, LU, LBL, LBN, AP2, LAST1, FRESH, WS = range(10)
-NSTATE = 10
+PUN, TAIL, LPRE, LU, LBL, LBN, AP2, LAST1, FRESH, WS, HAN, D1, D2 = range(13)
 
 
-def _classes():
+def _classes(kimi=False):
     from toktier_amd import classes
-    return classes.o200k_class_table()
+    return classes.kimi_class_table() if kimi else classes.o200k_class_table()
 
 
 def _fold(c: int) -> int:
@@ -46,10 +51,11 @@ def _crlf(c: int) -> bool:
     return c in (10, 13)
 
 
-def transitions(cps, ds, plant=None):
+def transitions(cps, ds, plant=None, kimi=False):
     """Per character (f, g): f[s] the state after it, g[s] its start bit
-    (None: the digit group rule), for the previous state s."""
-    cls = _classes()
+    (None: the digit group rule, o200k), for the previous state s."""
+    cls = _classes(kimi)
+    nstate = 13 if kimi else 10
     n = len(cps)
     cl = [int(cls[c]) for c in cps]
 
@@ -63,15 +69,20 @@ def transitions(cps, ds, plant=None):
         n1 = nxt(j)
         n2 = nxt(n1) if n1 is not None else None
         k1 = cl[n1] if n1 is not None else None
-        if k == N:
-            ns = FRESH
+        han = kimi and k >= HL
+        pm = k in (P, M) or (kimi and k == HP)
+        if han:
+            ns = HAN
+        elif k == N:
+            ns = D1 if kimi else FRESH
         elif k in (U, L):
             ns = LU if k == U else LBL
         elif k in (C, M):
             ns = LBN
         elif k == P or (k == S and not _crlf(c)):
             ns = (LPRE if k1 in W else
-                  PUN if k == P or (c == 32 and k1 == P) else WS)
+                  PUN if k == P or (c == 32 and (k1 == P or (kimi and k1 == HP)))
+                  else WS)
         else:
             ns = WS
         ap = None
@@ -97,18 +108,19 @@ def transitions(cps, ds, plant=None):
             q = nxt(q)
         prev_crlf = (j > 0 and not ds[j] and _crlf(cps[j - 1])
                      and plant != "ws_no_crlf")
-        f, g = [ns] * NSTATE, [1] * NSTATE
-        for s in range(NSTATE):
+        f, g = [ns] * nstate, [1] * nstate
+        for s in range(nstate):
             if ds[j]:
                 continue
             st, nx = 1, ns
             if s == PUN:
-                if k in (P, M):
+                if pm:
                     st, nx = 0, PUN
                 elif _crlf(c):
                     st, nx = 0, TAIL
             elif s == TAIL:
-                if _crlf(c) or (c == ord("/") and plant != "tail_no_slash"):
+                if _crlf(c) or (c == ord("/") and not kimi
+                                and plant != "tail_no_slash"):
                     st, nx = 0, TAIL
             elif s == LPRE:
                 if k in W:
@@ -127,18 +139,22 @@ def transitions(cps, ds, plant=None):
                 st, nx = 0, LAST1
             elif s == LAST1:
                 st, nx = 0, FRESH
+            elif s == HAN and han:
+                st, nx = 0, HAN
+            elif s in (D1, D2) and k in (N, HN):
+                st, nx = 0, (D2 if s == D1 else FRESH)
             elif s == WS and k == S:
                 if _crlf(c):
                     st, nx = 0, WS
                 else:
                     st = f3 if prev_crlf else (n1 is not None and k1 != S)
                     nx = ns if st else WS
-            f[s], g[s] = nx, (None if k == N else int(st))
+            f[s], g[s] = nx, (None if k == N and not kimi else int(st))
         out.append((tuple(f), tuple(g)))
     return out, cl
 
 
-def split(text: str, docs=(), plant=None, block: int = 0):
+def split(text: str, docs=(), plant=None, block: int = 0, kimi=False):
     """Piece starts (char indices) of `text` with documents starting at
     the indices `docs`; block > 0: the states come from compositions of
     `block` transitions at a time (the state after each block from its
@@ -146,14 +162,15 @@ def split(text: str, docs=(), plant=None, block: int = 0):
     cps = [ord(ch) for ch in text]
     n = len(cps)
     ds = [i == 0 or i in docs for i in range(n)]
-    fg, cl = transitions(cps, ds, plant)
+    fg, cl = transitions(cps, ds, plant, kimi)
+    nstate = 13 if kimi else 10
     states = [0] * n
     if block:
         s = FRESH
         for a in range(0, n, block):
-            F = tuple(range(NSTATE))
+            F = tuple(range(nstate))
             for j in range(a, min(n, a + block)):
-                F = tuple(fg[j][0][F[x]] for x in range(NSTATE))
+                F = tuple(fg[j][0][F[x]] for x in range(nstate))
                 states[j] = F[s]
             s = F[s]
     else:
@@ -165,7 +182,7 @@ def split(text: str, docs=(), plant=None, block: int = 0):
     for j in range(n):
         prev = states[j - 1] if j else FRESH
         st = fg[j][1][prev]
-        if cl[j] == N:
+        if cl[j] == N and not kimi:
             run = 0 if ds[j] or cl[j - 1] != N else run
             st = int(ds[j] or run % 3 == 0)
             run += 1
@@ -174,9 +191,10 @@ def split(text: str, docs=(), plant=None, block: int = 0):
     return out
 
 
-def _oracle():
+def _oracle(kimi=False):
     from oracle.oracle import Oracle
-    return Oracle(kit("gpt2").tables, _classes(), None, 4, 3, False)
+    return Oracle(kit("gpt2").tables, _classes(kimi), None, 5 if kimi else 4,
+                  3, False)
 
 
 def oracle_split(o, text: str, docs=()) -> list[int]:
@@ -245,3 +263,45 @@ def test_planted_transition_mistakes_are_caught(plant):
     assert hits, plant
     if found:
         assert split(found, plant=plant) != oracle_split(o, found), plant
+
+
+KIMI_CORE = ["A", "b", "中", "〇", "⺀", "\u0301", ".", " ", "'", "1", "\n"]
+
+
+def test_kimi_automaton_splits_like_the_oracle():
+    o = _oracle(kimi=True)
+    for t in itertools.chain(
+            ("".join(p) for n in range(1, 4)
+             for p in itertools.product(KIMI_ALPHABET, repeat=n)),
+            ("".join(p) for p in itertools.product(KIMI_CORE, repeat=4))):
+        assert split(t, kimi=True) == oracle_split(o, t), repr(t)
+    rng = np.random.default_rng(13)
+    for _ in range(3000):
+        n = int(rng.integers(1, 60))
+        t = "".join(KIMI_ALPHABET[int(i)] for i in rng.integers(0, len(KIMI_ALPHABET), n))
+        docs = sorted(set(int(x) for x in rng.integers(1, n + 1, size=int(rng.integers(0, 4)))))
+        want = oracle_split(o, t, docs)
+        assert split(t, docs, kimi=True) == want, (repr(t), docs)
+        assert split(t, docs, block=int(rng.integers(1, 9)), kimi=True) == want, (repr(t), docs)
+
+
+@pytest.mark.slow
+def test_kimi_automaton_splits_like_the_oracle_exhaustively():
+    o = _oracle(kimi=True)
+    cases = itertools.chain(
+        ("".join(p) for p in itertools.product(KIMI_ALPHABET, repeat=4)),
+        ("".join(p) for p in itertools.product(KIMI_CORE, repeat=5)))
+    bad = [t for t in cases if split(t, kimi=True) != oracle_split(o, t)]
+    assert not bad, [repr(t) for t in bad[:10]]
+
+
+def test_kimi_automaton_on_long_runs():
+    """Digit runs with Han numbers inside and at group starts, Han runs of
+    every subclass, the tail without '/'."""
+    o = _oracle(kimi=True)
+    texts = ["1" * 40 + "〇" * 7 + "2" * 11, "〇1234〇〇〇5678", "12〇〇34" * 20,
+             "中" * 100 + "〇⺀中1234", "!⺀!" * 30 + "x", " ⺀" * 40,
+             "a!\n/\n/b" * 20, "x" + "1〇" * 60]
+    for t in texts:
+        assert split(t, kimi=True) == oracle_split(o, t), repr(t)
+        assert split(t, block=64, kimi=True) == oracle_split(o, t), repr(t)

@@ -259,6 +259,85 @@ def test_o200k_split_brute_force():
                for t in ("HelloWorld", "ABCdef", "x'S", "!\n/"))
 
 
+#: the kimi alphabet: the o200k one with the Han letter in the Han
+#: classes, plus a Han number (U+3007) and other Han (U+2E80, a radical)
+KIMI_ALPHABET = ["A", "b", "中", "ʰ", "ǅ", "\u0301", "1", "〇", "⺀", ".", "!",
+                 " ", "\t", "\n", "\r", "'", "s", "S", "ſ", "r", "e", "/"]
+
+
+def _hf_starts(pattern):
+    from tokenizers import Regex, pre_tokenizers
+    pre = pre_tokenizers.Split(Regex(pattern), behavior="isolated", invert=False)
+
+    def hf(text):
+        offs = [b for _, b in pre.pre_tokenize_str(text)]
+        st = sorted({len(text[:a].encode("utf-8")) for a, _ in offs})
+        return st + [len(text.encode("utf-8"))]
+    return hf
+
+
+def test_kimi_class_table():
+    tab = classes.kimi_class_table()
+    assert classes.npy_sha256(tab) == classes.KIMI_TABLE_SHA256
+    # the o200k classes outside Han; Han letters, numbers and the rest
+    o2 = classes.o200k_class_table()
+    han = tab >= 7
+    assert np.array_equal(tab[~han], o2[~han])
+    assert tab[0x4E2D] == 7 and tab[0x3005] == 7   # Lo, Lm
+    assert tab[0x3007] == 8 and tab[0x3021] == 8   # Nl
+    assert tab[0x2E80] == 9                        # So
+    assert np.bincount(tab, minlength=10)[7:].tolist() == [98685, 13, 332]
+
+
+def test_kimi_split_brute_force():
+    """The kimi restatement (oracle ruleset 5) splits like the certified
+    engine with the Kimi pattern (``[\\p{Han}]+`` first, Han-free letter
+    classes, a tail without '/'): every string of length <= 3 over the
+    alphabet, every length-5 string over an 11-symbol core, seeded fuzz."""
+    from oracle.oracle import Oracle
+    from toktier_amd.families import KIMI_PATTERN
+    hf = _hf_starts(KIMI_PATTERN)
+    o = Oracle(kit("gpt2").tables, classes.kimi_class_table(), None, 5, 3, False)
+    core = ["A", "b", "中", "〇", "⺀", "\u0301", ".", " ", "'", "1", "\n"]
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 4)
+         for p in itertools.product(KIMI_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(core, repeat=5)),
+    )
+    bad = [s for s in cases if o.pretokenize(s.encode("utf-8")) != hf(s)]
+    assert not bad, [repr(s) for s in bad[:10]]
+    rng = np.random.default_rng(19)
+    for _ in range(5000):
+        s = "".join(KIMI_ALPHABET[int(i)] for i in
+                    rng.integers(0, len(KIMI_ALPHABET), int(rng.integers(1, 40))))
+        assert o.pretokenize(s.encode("utf-8")) == hf(s), repr(s)
+    # planted: the o200k split (no Han branch, the '/' tail) disagrees
+    wrong = Oracle(kit("gpt2").tables, classes.o200k_class_table(), None, 4, 3, False)
+    assert all(wrong.pretokenize(t.encode()) != hf(t)
+               for t in ("Hello世界's", "!\n/x", "12〇〇34"))
+    # and the o200k rules cannot read the Han classes at all
+    bad_cfg = Oracle(kit("gpt2").tables, classes.kimi_class_table(), None, 4, 3, False)
+    with pytest.raises(ValueError):
+        bad_cfg.pretokenize("中".encode())
+
+
+def test_o200k_without_contractions_brute_force():
+    """The o200k restatement with the contraction suffix off splits like
+    the o200k pattern without it (the o200k families whose
+    ``kernel_families.v1.json`` rows say contractions false)."""
+    from oracle.oracle import Oracle
+    from toktier_amd.families import O200K_PATTERN
+    pat = O200K_PATTERN.replace("(?i:'s|'t|'re|'ve|'m|'ll|'d)?", "")
+    assert pat != O200K_PATTERN
+    hf = _hf_starts(pat.replace(r"\p{N}{1,3}", r"\p{N}"))
+    o = Oracle(kit("gpt2").tables, classes.o200k_class_table(), None, 4, 1,
+               False, contractions=False)
+    for s in ("".join(p) for n in range(1, 4)
+              for p in itertools.product(O2K_ALPHABET, repeat=n)):
+        assert o.pretokenize(s.encode("utf-8")) == hf(s), repr(s)
+    assert o.pretokenize(b"it's") != _hf_starts(O200K_PATTERN)("it's")
+
+
 # ------------------------------------------------------------ encodes
 
 def _expected(k, text: str, ids: list[int]):
@@ -288,6 +367,8 @@ def test_oracle_matches_hf_on_mixed_text(name):
            "llama_3_1_8b": workloads.config4,
            "laguna_s_2_1": workloads.config4,
            "gpt_oss_120b": lambda js, n_chars: workloads.config5(
+               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+           "kimi_k3": lambda js, n_chars: workloads.config5(
                js, n_chars=n_chars, n_runs=4, run_chars=20_000),
            "deepseek_v3": lambda js, n_chars: workloads.config5(
                js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]

@@ -29,6 +29,7 @@ TK_RULESET_R50K = 1
 TK_RULESET_LAGUNA = 2
 TK_RULESET_DEEPSEEK = 3
 TK_RULESET_O200K = 4
+TK_RULESET_KIMI = 5
 TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
 TK_NOALLOC_MAX_BYTES = 1 << 20

@@ -26,8 +26,11 @@ NFC_QC_SHA256 = "1a7d121e9092cdf577d992452393d25116b2577ab74dd5a067e6ca00a535d31
 DEEPSEEK_TABLE_SHA256 = "b4242c04ffc981d9f457981546c43b2a82b53e3d18bf6f7d1ee1e7625c423bf7"
 #: kernel_families.v1.json class_tables.o200k_v4
 O200K_TABLE_SHA256 = "28e6d9e468b2c83db4188787515fa0e89d49750c20c966a9a89481aaf3b9e8ea"
+#: kernel_families.v1.json class_tables.kimi_v1
+KIMI_TABLE_SHA256 = "9b752f3757bdec444ed745f27bac35fdb2aca8893521ef3d40cff7b17f681383"
 
 __all__ = ["class_table", "deepseek_class_table", "o200k_class_table",
+           "kimi_class_table",
            "nfc_qc_table",
            "npy_sha256", "PLANE", "table_for"]
 
@@ -74,10 +77,19 @@ def o200k_class_table() -> np.ndarray:
     return _load("classes_o200k.npz", "o200k", O200K_TABLE_SHA256)
 
 
+@lru_cache(maxsize=None)
+def kimi_class_table() -> np.ndarray:
+    """kimi classes: the o200k seven (letters without Han) plus HL=7 HN=8
+    HP=9 (Han letters, Han numbers, other Han)."""
+    return _load("classes_kimi.npz", "kimi", KIMI_TABLE_SHA256)
+
+
 def table_for(ruleset_name: str) -> np.ndarray:
     """The class table a family's ruleset reads."""
     if ruleset_name == "deepseek":
         return deepseek_class_table()
     if ruleset_name == "o200k":
         return o200k_class_table()
+    if ruleset_name == "kimi":
+        return kimi_class_table()
     return class_table()

@@ -49,7 +49,7 @@ __host__ __device__ __forceinline__ uint32_t pair_alt(uint32_t b1, uint32_t tag,
 // Device copies of the family tables, in the engine's own layout.
 struct DevTables {
   const uint8_t* cls;          // [0x110000] P/L/N/S (deepseek: O L M N PS WS CRLF;
-                               // o200k: P U L C N S M)
+                               // o200k: P U L C N S M; kimi: + HL HN HP)
   const uint8_t* nfc;          // [0x110000] quick-check values or nullptr
   const ulonglong2* pairs;     // interleaved {key, val} merge hash slots
   uint64_t pair_mask;
@@ -59,10 +59,11 @@ struct DevTables {
   uint64_t vocab_mask;
   uint32_t vocab_max_len;      // bytes of the longest vocabulary entry
   const uint8_t* blob;         // vocabulary bytes
-  int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek, 4 o200k
+  int32_t ruleset;             // 0 cl100k, 1 r50k, 3 deepseek, 4 o200k, 5 kimi
   int32_t dmax;                // digit group width (cl100k)
   int32_t ignore_merges;
   int32_t needs_nfc;
+  int32_t contractions;        // o200k: the contraction suffix is on
   int32_t cert;                // long pieces over 512 bytes: 0 merged
                                // serially (a byte without an id); 1 cut and
                                // certified from first / last-token events

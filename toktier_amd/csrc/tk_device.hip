@@ -314,7 +314,8 @@ struct GCtx {
 //   bits 23..24 back: prev(p) = p - 1 - back(p - 1)
 //   bits 25..26 fwd:  next(p) = p + 1 + fwd(p) (before the end checks)
 //   bit  27     the decode at p is valid UTF-8
-//   bit  28     class bit 2 (the seven DeepSeek classes)
+//   bits 28..29 class bits 2..3 (the seven DeepSeek / o200k classes, the
+//               ten kimi classes)
 // packed LDS table entry of k_pretok: byte id (LTAB_NOID: none), class of
 // the code point, its NFC quick-check value
 constexpr uint32_t LTAB_NOID = 0xFFFFFu;
@@ -357,7 +358,7 @@ struct LCtx {
   __device__ __forceinline__ Ch at(int64_t p) const {
     if (!in(p)) return g.at(p);
     const uint32_t e = se[p - lo];
-    return Ch{p, (int32_t)(e & 0x1FFFFF), (uint8_t)(((e >> 21) & 3) | ((e >> 26) & 4))};
+    return Ch{p, (int32_t)(e & 0x1FFFFF), (uint8_t)(((e >> 21) & 3) | ((e >> 26) & 0xC))};
   }
   __device__ __forceinline__ int64_t prev(int64_t p) const {
     if (ds(p)) return -1;
@@ -607,7 +608,7 @@ __device__ __forceinline__ int fast_r50k(const Ctx5& x) {
 //     another CR/LF follows in the run and the CR/LF run before c0 was not
 //     the [\r\n]* of a P / S match
 __device__ __forceinline__ int dcl(uint32_t e) {
-  return (int)(((e >> 21) & 3) | ((e >> 26) & 4));
+  return (int)(((e >> 21) & 3) | ((e >> 26) & 0xC));
 }
 __device__ __forceinline__ bool ds_cjk(int c) {
   return (c >= 0x4E00 && c <= 0x9FA5) || (c >= 0x3040 && c <= 0x30FF);
@@ -790,15 +791,27 @@ __device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
 // class state, and a prefix character or mark that opens one changes
 // nothing about where it ends.
 constexpr int RS_O200K = 4;
+constexpr int RS_KIMI = 5;
 constexpr uint8_t OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4,
-                  OK_S = 5, OK_M = 6;
+                  OK_S = 5, OK_M = 6, OK_HL = 7, OK_HN = 8, OK_HP = 9;
 enum : uint32_t {
   O2_PUN = 0, O2_TAIL, O2_LPRE, O2_LU, O2_LBL, O2_LBN, O2_AP2, O2_LAST1,
-  O2_FRESH, O2_WS, O2_NSTATE
+  O2_FRESH, O2_WS,
+  // (kimi) in a Han run; one or two digits into a \p{N}{1,3} group
+  O2_HAN, O2_D1, O2_D2
 };
-constexpr uint64_t O2_REP = 0x1111111111ull;  // a nibble in every state
-constexpr uint64_t O2_ID = 0x9876543210ull;   // the identity
-constexpr uint32_t O2_ALL = (1u << O2_NSTATE) - 1;
+// states of the o200k / kimi automaton
+template <int RS> constexpr int o2_nst() { return RS == RS_KIMI ? 13 : 10; }
+template <int N> constexpr uint64_t o2_rep() {  // a nibble in every state
+  uint64_t r = 0;
+  for (int i = 0; i < N; ++i) r |= 1ull << (4 * i);
+  return r;
+}
+template <int N> constexpr uint64_t o2_id() {   // the identity
+  uint64_t r = 0;
+  for (int i = 0; i < N; ++i) r |= (uint64_t)i << (4 * i);
+  return r;
+}
 __device__ __forceinline__ uint32_t o2_at(uint64_t f, uint32_t s) {
   return (uint32_t)(f >> (4 * s)) & 15u;
 }
@@ -806,15 +819,17 @@ __device__ __forceinline__ uint64_t o2_set(uint64_t f, uint32_t s, uint32_t v) {
   return (f & ~(15ull << (4 * s))) | ((uint64_t)v << (4 * s));
 }
 // a, then b
+template <int N>
 __device__ __forceinline__ uint64_t o2_then(uint64_t a, uint64_t b) {
   uint64_t h = 0;
 #pragma unroll
-  for (uint32_t s = 0; s < O2_NSTATE; ++s)
+  for (uint32_t s = 0; s < (uint32_t)N; ++s)
     h |= (uint64_t)o2_at(b, o2_at(a, s)) << (4 * s);
   return h;
 }
+template <int N>
 __device__ __forceinline__ bool o2_const(uint64_t f) {
-  return f == (f & 15u) * O2_REP;
+  return f == (f & 15u) * o2_rep<N>();
 }
 __device__ __forceinline__ bool ok_w(int k) {
   return k == OK_U || k == OK_L || k == OK_C || k == OK_M;
@@ -826,43 +841,66 @@ __device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int d) {
 
 // The transition of the character at i (code point cp, class k; d0: a
 // document starts at i): *fo the next state per previous state, *go the
-// start bit per previous state (digits: the caller's group rule replaces
-// it). `need_g` false skips what only the start bits read.
-template <class C>
+// start bit per previous state (o200k digits: the caller's group rule
+// replaces it). `need_g` false skips what only the start bits read;
+// `contr` false drops the contraction suffix (o200k rows without it).
+// kimi (RS_KIMI): a Han character (HL HN HP) opens or continues a Han run;
+// \p{N}{1,3} counts its digits in the state (a Han number inside a group
+// is a digit, at a group's start it opens a Han run); P matches take the
+// other Han (HP) and their tail is [\r\n]* (no '/').
+template <int RS, class C>
 __device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
-                         bool need_g, uint64_t* fo, uint32_t* go) {
+                         bool need_g, bool contr, uint64_t* fo, uint32_t* go) {
+  constexpr bool KIMI = RS == RS_KIMI;
+  constexpr uint32_t ALL = (1u << o2_nst<RS>()) - 1;
   const int64_t n1 = c.next(i);
   const Ch x1 = n1 >= 0 ? c.at(n1) : Ch{-1, -1, 0xFF};
   const int k1 = n1 >= 0 ? x1.cl : -1;
   const bool cr = crlf(cp);
+  const bool han = KIMI && k >= OK_HL;
+  // [^\s\p{L}\p{N}]: the characters a P match's [PM]+ takes
+  const bool pm = k == OK_P || k == OK_M || (KIMI && k == OK_HP);
   // the state of a match that starts here
   uint32_t ns;
-  if (k == OK_N) ns = O2_FRESH;
+  if (han) ns = O2_HAN;
+  else if (k == OK_N) ns = KIMI ? O2_D1 : O2_FRESH;
   else if (k == OK_U) ns = O2_LU;
   else if (k == OK_L) ns = O2_LBL;
   else if (k == OK_C || k == OK_M) ns = O2_LBN;
   else if (k == OK_P || (k == OK_S && !cr))
     ns = ok_w(k1) ? O2_LPRE
-       : (k == OK_P || (cp == ' ' && k1 == OK_P)) ? O2_PUN : O2_WS;
+       : (k == OK_P || (cp == ' ' && (k1 == OK_P || (KIMI && k1 == OK_HP))))
+       ? O2_PUN : O2_WS;
   else ns = O2_WS;
-  uint64_t f = (uint64_t)ns * O2_REP;
-  uint32_t g = O2_ALL;
+  uint64_t f = (uint64_t)ns * o2_rep<o2_nst<RS>()>();
+  uint32_t g = ALL;
   if (d0) {
     *fo = f;
     *go = g;
     return;
   }
-  // a P match: [PM]+ goes on, a CR/LF opens the [\r\n/]* tail
-  if (k == OK_P || k == OK_M) {
+  // a P match: [PM]+ goes on, a CR/LF opens the tail
+  if (pm) {
     f = o2_set(f, O2_PUN, O2_PUN);
     g &= ~(1u << O2_PUN);
   } else if (cr) {
     f = o2_set(f, O2_PUN, O2_TAIL);
     g &= ~(1u << O2_PUN);
   }
-  if (cr || cp == '/') {
+  if (cr || (!KIMI && cp == '/')) {
     f = o2_set(f, O2_TAIL, O2_TAIL);
     g &= ~(1u << O2_TAIL);
+  }
+  if (KIMI) {
+    // a Han run goes on; a \p{N} character continues a digit group
+    if (han) {
+      f = o2_set(f, O2_HAN, O2_HAN);
+      g &= ~(1u << O2_HAN);
+    }
+    if (k == OK_N || k == OK_HN) {
+      f = o2_set(o2_set(f, O2_D1, O2_D2), O2_D2, O2_FRESH);
+      g &= ~((1u << O2_D1) | (1u << O2_D2));
+    }
   }
   if (ok_w(k)) {
     // a letter after a prefix or inside a letter run (the class state is
@@ -890,12 +928,12 @@ __device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
     }
     // the letters a contraction takes ('s 't 'm 'd: one; 're 've 'll: two)
     const int a = fold(cp);
-    if (a == 's' || a == 't' || a == 'm' || a == 'd' || a == 'r' ||
-        a == 'e' || a == 'v' || a == 'l') {
+    if (contr && (a == 's' || a == 't' || a == 'm' || a == 'd' || a == 'r' ||
+                  a == 'e' || a == 'v' || a == 'l')) {
       f = o2_set(o2_set(f, O2_AP2, O2_LAST1), O2_LAST1, O2_FRESH);
       g &= ~((1u << O2_AP2) | (1u << O2_LAST1));
     }
-  } else if (cp == '\'' && n1 >= 0) {
+  } else if (contr && cp == '\'' && n1 >= 0) {
     // a contraction after a letter match
     const int a = fold(x1.cp);
     uint32_t ap = 0;
@@ -946,8 +984,8 @@ __device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
 }
 
 // a tile's automaton word pair (ostate[2t], ostate[2t + 1]): call tag << 32
-// | the low 32 bits of the tile's function, and call tag << 32 | kind << 8
-// | state << 12 | the function's high 8 bits, kind O2_AGG (the function)
+// | the low 32 bits of the tile's function, and call tag << 32 | kind << 30
+// | state << 26 | the function's high 20 bits, kind O2_AGG (the function)
 // or O2_INCL (the state after the tile)
 constexpr uint32_t O2_AGG = 1, O2_INCL = 2;
 __device__ __forceinline__ void o2_publish(uint64_t* p, uint32_t seq, uint32_t kind,
@@ -955,8 +993,8 @@ __device__ __forceinline__ void o2_publish(uint64_t* p, uint32_t seq, uint32_t k
   if (kind == O2_AGG)
     __hip_atomic_store(p, ((uint64_t)seq << 32) | (uint32_t)f, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(p + 1, ((uint64_t)seq << 32) | (kind << 8) | (s << 12) |
-                                (uint32_t)((f >> 32) & 0xFF),
+  __hip_atomic_store(p + 1, ((uint64_t)seq << 32) | (kind << 30) | (s << 26) |
+                                (uint32_t)((f >> 32) & 0xFFFFF),
                      __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1131,9 +1169,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   const int lane = tid & 63, wv = wave_id();
   // the ruleset's class of an entry, and its digit / P / whitespace classes
   auto kcl = [](uint32_t e) {
-    return RS == RS_DEEPSEEK || RS == RS_O200K ? dcl(e) : ecl(e);
+    return RS == RS_DEEPSEEK || RS == RS_O200K || RS == RS_KIMI ? dcl(e) : ecl(e);
   };
-  constexpr int KN = RS == RS_DEEPSEEK ? DS_N : RS == RS_O200K ? OK_N : CN_;
+  constexpr int KN = RS == RS_DEEPSEEK ? DS_N : RS == RS_O200K || RS == RS_KIMI ? OK_N : CN_;
   constexpr int KP = RS == RS_DEEPSEEK ? DS_PS : CP_;
   auto kws = [](int k) { return RS == RS_DEEPSEEK ? k >= DS_WS : k == CS_; };
   // Digit groups (\p{N}{1,K}, K > 1) count the N characters of the run
@@ -1421,7 +1459,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       }
     }
   };
-  // o200k: the automaton over the tile (o2k_char). Wave wv takes the
+  // o200k / kimi: the automaton over the tile (o2k_char). Wave wv takes the
   // contiguous words [12 wv, 12 wv + 12) (wave 3 also the word after the
   // tile) and carries the state from word to word. Its entry state is the
   // function of the word before its block when that function is constant
@@ -1439,19 +1477,23 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       return i == 0 || ((sdm[(i >> 6) - wlo] >> (i & 63)) & 1) != 0;
     };
     constexpr int WPB = PT_TILE / 64 / (PRETOK_TPB / 64);  // words per wave
+    constexpr int NST = o2_nst<RS>();
+    constexpr uint64_t ID = o2_id<NST>();
+    constexpr uint32_t ALL = (1u << NST) - 1;
+    const bool contr = t.contractions != 0;
     // the lane's transition and start bits in word k (-1 .. PT_TILE / 64);
     // positions outside the text and inside a character pass the state on
     auto lane_fn = [&](int k, bool need_g, uint64_t* f, uint32_t* g) {
       const int64_t i = base + 64 * k + lane;
       const int Li = PT_HALO + 64 * k + lane;
-      *f = O2_ID;
+      *f = ID;
       *g = 0;
       if (i < 0 || i >= nb || is_cont(sb[64 * k + lane + PT_PAD])) return;
       const uint32_t e = se[Li];
       const int kc = dcl(e);
       const bool d0 = ds(Li);
-      o2k_char(c, i, (int32_t)(e & 0x1FFFFF), kc, d0, need_g, f, g);
-      if (need_g && kc == OK_N && !d0) {
+      o2k_char<RS>(c, i, (int32_t)(e & 0x1FFFFF), kc, d0, need_g, contr, f, g);
+      if (RS == RS_O200K && need_g && kc == OK_N && !d0) {
         // \p{N}{1,K}: the N characters of the run before i decide
         bool r = true;
         if (groups) {
@@ -1466,7 +1508,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
           }
           r = cnt % (uint32_t)t.dmax == 0;
         }
-        *g = r ? O2_ALL : 0u;
+        *g = r ? ALL : 0u;
       }
     };
     // inclusive composition over the lanes (lane 0 first): windows of four
@@ -1474,13 +1516,13 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     // after its lane whatever came before), else the whole prefix
     auto scan = [&](uint64_t F) {
       uint64_t o = shfl_up64(F, 1);
-      if (lane >= 1) F = o2_then(o, F);
+      if (lane >= 1) F = o2_then<NST>(o, F);
       o = shfl_up64(F, 2);
-      if (lane >= 2) F = o2_then(o, F);
-      if (__any(lane >= 4 && !o2_const(F))) {
+      if (lane >= 2) F = o2_then<NST>(o, F);
+      if (__any(lane >= 4 && !o2_const<NST>(F))) {
         for (int d = 4; d < 64; d <<= 1) {
           o = shfl_up64(F, d);
-          if (lane >= d) F = o2_then(o, F);
+          if (lane >= d) F = o2_then<NST>(o, F);
         }
       }
       return F;
@@ -1541,30 +1583,30 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     // the word before the block (the tile's halo word for wave 0); the
     // first tile starts at a document start, whatever came before
     uint64_t T = word_fn(k0 - 1);
-    if (blockIdx.x == 0 && wv == 0) T = (uint64_t)O2_FRESH * O2_REP;
+    if (blockIdx.x == 0 && wv == 0) T = (uint64_t)O2_FRESH * o2_rep<NST>();
     if (lane == 0) o2w[wv] = T;
     __syncthreads();
     bool fast = true;
-    for (int j = 0; j < PRETOK_TPB / 64; ++j) fast &= o2_const(o2w[j]);
+    for (int j = 0; j < PRETOK_TPB / 64; ++j) fast &= o2_const<NST>(o2w[j]);
     uint32_t carry;
     uint64_t* op = w.ostate + 2 * (int64_t)blockIdx.x;
     if (fast) {
       carry = (uint32_t)(o2w[wv] & 15);
     } else {
-      uint64_t B = O2_ID;
-      for (int k = k0; k < k0 + WPB; ++k) B = o2_then(B, word_fn(k));
+      uint64_t B = ID;
+      for (int k = k0; k < k0 + WPB; ++k) B = o2_then<NST>(B, word_fn(k));
       if (lane == 0) o2b[wv] = B;
       __syncthreads();
       if (tid == 0) {
         uint64_t A = o2b[0];
-        for (int j = 1; j < PRETOK_TPB / 64; ++j) A = o2_then(A, o2b[j]);
+        for (int j = 1; j < PRETOK_TPB / 64; ++j) A = o2_then<NST>(A, o2b[j]);
         uint32_t entry = O2_FRESH;
-        if (o2_const(o2w[0])) {
+        if (o2_const<NST>(o2w[0])) {
           entry = (uint32_t)(o2w[0] & 15);
         } else {
           o2_publish(op, w.seq, O2_AGG, A, 0);
           // G: the function of the tiles after u up to this one
-          uint64_t G = O2_ID;
+          uint64_t G = ID;
           bool done = false;
           for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0 && !done; --u) {
             const uint64_t* q = w.ostate + 2 * u;
@@ -1579,14 +1621,14 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
             if ((uint32_t)(v1 >> 32) != w.seq) {
               st |= ST_STALL;
               done = true;
-            } else if (((v1 >> 8) & 3) == O2_INCL) {
-              entry = o2_at(G, (uint32_t)(v1 >> 12) & 15);
+            } else if (((v1 >> 30) & 3) == O2_INCL) {
+              entry = o2_at(G, (uint32_t)(v1 >> 26) & 15);
               done = true;
             } else {
               const uint64_t v0 = __hip_atomic_load(q, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
-              G = o2_then((uint32_t)v0 | ((v1 & 0xFF) << 32), G);
-              if (o2_const(G)) {
+              G = o2_then<NST>((uint32_t)v0 | ((v1 & 0xFFFFF) << 32), G);
+              if (o2_const<NST>(G)) {
                 entry = (uint32_t)(G & 15);
                 done = true;
               }
@@ -1608,7 +1650,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       word(PT_TILE / 64, carry);
     }
   };
-  if constexpr (RS == RS_O200K) {
+  if constexpr (RS == RS_O200K || RS == RS_KIMI) {
     if (DM && dm) o2k_words(std::true_type{});
     else o2k_words(std::false_type{});
   } else {
@@ -1689,6 +1731,9 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
   } else if (t.ruleset == RS_O200K) {
     if (dm) launch_ev(k_pretok<RS_O200K, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<RS_O200K, false>, g, b, s, start, stop, t, w, nwords);
+  } else if (t.ruleset == RS_KIMI) {
+    if (dm) launch_ev(k_pretok<RS_KIMI, true>, g, b, s, start, stop, t, w, nwords);
+    else launch_ev(k_pretok<RS_KIMI, false>, g, b, s, start, stop, t, w, nwords);
   } else {
     if (dm) launch_ev(k_pretok<0, true>, g, b, s, start, stop, t, w, nwords);
     else launch_ev(k_pretok<0, false>, g, b, s, start, stop, t, w, nwords);

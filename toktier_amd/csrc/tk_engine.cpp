@@ -314,23 +314,30 @@ int validate(const tk_config* cfg, const uint8_t* class_table, size_t class_len,
                 TK_ABI_VERSION);
   if (cfg->ruleset != TK_RULESET_CL100K && cfg->ruleset != TK_RULESET_R50K &&
       cfg->ruleset != TK_RULESET_LAGUNA && cfg->ruleset != TK_RULESET_DEEPSEEK &&
-      cfg->ruleset != TK_RULESET_O200K)
+      cfg->ruleset != TK_RULESET_O200K && cfg->ruleset != TK_RULESET_KIMI)
     return fail(TK_E_INVALID_ARG, "unsupported ruleset %d", cfg->ruleset);
   if (cfg->ruleset != TK_RULESET_R50K &&
       (cfg->digits_max < 1 || cfg->digits_max > 64))
     return fail(TK_E_INVALID_ARG, "digits_max %d out of range", cfg->digits_max);
-  // the deepseek pattern has no contraction alternative; the others do
-  if ((cfg->contractions != 0) != (cfg->ruleset != TK_RULESET_DEEPSEEK))
+  // the deepseek pattern has no contraction alternative; o200k rows come
+  // with and without one; the others always have it
+  if (cfg->ruleset != TK_RULESET_O200K &&
+      (cfg->contractions != 0) != (cfg->ruleset != TK_RULESET_DEEPSEEK))
     return fail(TK_E_INVALID_ARG, "contractions=%d does not match ruleset %d",
                 cfg->contractions, cfg->ruleset);
+  // the kimi digit alternative is \p{N}{1,3}, counted in the split's state
+  if (cfg->ruleset == TK_RULESET_KIMI && cfg->digits_max != 3)
+    return fail(TK_E_INVALID_ARG, "digits_max %d: the kimi split groups digits by 3",
+                cfg->digits_max);
   // shape rules of the reference executor (gpu.rs:1642-1679)
   if (class_len < PLANE)
     return fail(TK_E_SHAPE, "class table does not cover U+10FFFF");
   {
     // four classes (P L N S), seven for deepseek (O L M N PS WS CRLF) and
-    // for o200k (P U L C N S M)
-    const uint8_t top =
-        cfg->ruleset == TK_RULESET_DEEPSEEK || cfg->ruleset == TK_RULESET_O200K ? 6 : 3;
+    // for o200k (P U L C N S M), ten for kimi (those and HL HN HP)
+    const uint8_t top = cfg->ruleset == TK_RULESET_KIMI ? 9
+                      : cfg->ruleset == TK_RULESET_DEEPSEEK ||
+                        cfg->ruleset == TK_RULESET_O200K ? 6 : 3;
     uint8_t mx = 0;
     for (size_t i = 0; i < PLANE; ++i) mx = class_table[i] > mx ? class_table[i] : mx;
     if (mx > top)
@@ -1007,6 +1014,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->added = tk::DevAdded{};
   e->added.newline_cuts = cfg->ruleset == TK_RULESET_LAGUNA ? 1 : 0;
   e->t.ignore_merges = cfg->ignore_merges ? 1 : 0;
+  e->t.contractions = cfg->contractions ? 1 : 0;
   e->t.needs_nfc = cfg->needs_nfc ? 1 : 0;
   // Pieces over 512 bytes are cut and certified when every byte has an
   // initial id: from the segments' first / last-token events when every

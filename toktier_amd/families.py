@@ -31,7 +31,7 @@ from dataclasses import dataclass
 
 __all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K",
            "RULESET_LAGUNA", "RULESET_DEEPSEEK", "RULESET_O200K",
-           "DEEPSEEK_STAGES", "O200K_PATTERN"]
+           "RULESET_KIMI", "DEEPSEEK_STAGES", "O200K_PATTERN", "KIMI_PATTERN"]
 
 #: Device ruleset ids (the ``ruleset`` field of the engine config).
 RULESET_CL100K = 0
@@ -52,6 +52,28 @@ RULESET_DEEPSEEK = 3
 #: contractions true): letters split by case, contraction suffixes,
 #: digit groups of three.
 RULESET_O200K = 4
+
+#: kimi (``kernel_families.v1.json`` family ``kimi_k3``: band and ruleset
+#: kimi, class table kimi_v1, digits_max 3, contractions true): o200k with
+#: a leading [\p{Han}]+ branch, letter classes without Han, and a
+#: punctuation tail without '/'.
+RULESET_KIMI = 5
+
+#: The Kimi pre-tokenizer pattern (``src/toktier/artifacts/conversion.py``
+#: KIMI_PATTERN; sha256 de5781783b19... as pretok_classes_kimi.v1.meta.json
+#: ``pattern_sha256``).
+KIMI_PATTERN = "|".join((
+    r"[\p{Han}]+",
+    r"[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}&&[^\p{Han}]]*"
+    r"[\p{Ll}\p{Lm}\p{Lo}\p{M}&&[^\p{Han}]]+(?i:'s|'t|'re|'ve|'m|'ll|'d)?",
+    r"[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}&&[^\p{Han}]]+"
+    r"[\p{Ll}\p{Lm}\p{Lo}\p{M}&&[^\p{Han}]]*(?i:'s|'t|'re|'ve|'m|'ll|'d)?",
+    r"\p{N}{1,3}",
+    r" ?[^\s\p{L}\p{N}]+[\r\n]*",
+    r"\s*[\r\n]+",
+    r"\s+(?!\S)",
+    r"\s+",
+))
 
 #: Laguna's stage 0, split with behavior MergedWithNext.
 LAGUNA_STAGE0 = r"(?:\r?\n)+"
@@ -93,8 +115,8 @@ GPT2_PATTERN = (
 @dataclass(frozen=True)
 class Family:
     name: str
-    ruleset: int           # RULESET_CL100K / _R50K / _LAGUNA / _DEEPSEEK / _O200K
-    ruleset_name: str      # "cl100k" / "r50k" / "laguna" / "deepseek" / "o200k"
+    ruleset: int           # RULESET_CL100K / _R50K / _LAGUNA / _DEEPSEEK / _O200K / _KIMI
+    ruleset_name: str      # "cl100k" / "r50k" / "laguna" / "deepseek" / "o200k" / "kimi"
     pattern: str
     digits_max: int        # digit group width (cl100k); 0 = unbounded (r50k)
     contractions_fold: bool  # (?i:...) contractions (cl100k) vs case-sensitive
@@ -152,6 +174,16 @@ FAMILIES: dict[str, Family] = {
         hf_repo="openai/gpt-oss-120b",
         # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (27,868,174 B)
         real_sha256="0614fe83cadab421296e664e1f48f4261fa8fef6e03e63bb75c20f38e37d07d3",
+    ),
+    "kimi_k3": Family(
+        name="kimi_k3", ruleset=RULESET_KIMI, ruleset_name="kimi",
+        pattern=KIMI_PATTERN, digits_max=3, contractions_fold=True,
+        # converted from tiktoken ranks (artifact_conversions.v1.json
+        # kimi_tiktoken_v1): no normalizer, whole-vocabulary pieces first
+        needs_nfc=False, ignore_merges=True, vocab_size=163584,
+        hf_repo="moonshotai/Kimi-K3",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (9,703,692 B)
+        real_sha256="773c2476259d9e092bba48d1f4840aaf584fa87cd5083a7e33b54d6d6f9feb77",
     ),
     "gpt2": Family(
         name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",

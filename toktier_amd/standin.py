@@ -27,6 +27,10 @@ Shapes follow the real artifacts:
   ``ignore_merges`` false.
 - ``gpt2``: ``ByteLevel(use_regex=True)`` pre-tokenizer; 50,000 merges,
   50,257 entries including ``<|endoftext|>``.
+- ``kimi_k3``: no normalizer; ``Split(kimi regex, isolated)`` +
+  ``ByteLevel(use_regex=False)``; BPE with ``ignore_merges`` true over
+  163,584 regular entries, merges every two-way split of each token in
+  the order of the Kimi conversion, and 256 marker ids above them.
 - ``gpt_oss_120b``: no normalizer; ``Split(o200k regex, isolated)`` +
   ``ByteLevel(use_regex=False)``; BPE with ``ignore_merges`` true over
   199,998 regular entries, merges re-derived tiktoken-style as for
@@ -233,6 +237,8 @@ def _train(name: str) -> dict:
         corpus += _synthetic_corpus(20261203, 8_000_000, 1_000_000, 40000)
     elif name == "gpt_oss_120b":
         corpus += _synthetic_corpus(20261204, 6_000_000, 1_500_000, 40000)
+    elif name == "kimi_k3":
+        corpus += _synthetic_corpus(20261205, 10_000_000, 1_500_000, 40000)
     tok.train_from_iterator(corpus, trainer)
     spec = json.loads(tok.to_str())
     model = spec["model"]
@@ -243,6 +249,8 @@ def _train(name: str) -> dict:
     model["ignore_merges"] = bool(fam.ignore_merges)
     if name in ("llama_3_1_8b", "gpt_oss_120b"):
         model["merges"] = _tiktoken_style_merges(vocab)
+    elif name == "kimi_k3":
+        model["merges"] = _tiktoken_style_merges(vocab, ties="cut")
     if name == "gpt2":
         vocab["<|endoftext|>"] = 50256
     spec["added_tokens"] = added_token_entries(name)
@@ -269,6 +277,21 @@ def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
                  "<｜tool▁output▁begin｜>", "<｜tool▁output▁end｜>",
                  "<｜tool▁sep｜>", "<think>", "</think>"]
         return [(c, 128000 + k, k < 3) for k, c in enumerate(names)]
+    if name == "kimi_k3":
+        # 256 ids above the 163,584 ranks: the named markers in the form of
+        # the Kimi-K2 configuration, reserved spellings for the rest
+        named = {163584: "[BOS]", 163585: "[EOS]", 163586: "<|im_end|>",
+                 163587: "<|im_user|>", 163588: "<|im_assistant|>",
+                 163590: "<|start_header_id|>", 163591: "<|end_header_id|>",
+                 163593: "[EOT]", 163594: "<|im_system|>",
+                 163595: "<|tool_calls_section_begin|>",
+                 163596: "<|tool_calls_section_end|>",
+                 163597: "<|tool_call_begin|>",
+                 163598: "<|tool_call_argument_begin|>",
+                 163599: "<|tool_call_end|>", 163601: "<|im_middle|>",
+                 163838: "[UNK]", 163839: "[PAD]"}
+        return [(named.get(i, f"<|reserved_token_{i}|>"), i, True)
+                for i in range(163584, 163840)]
     if name == "gpt_oss_120b":
         # the harmony markers after the 199,998 regular tokens (the named
         # ones, and the reserved slots between them)
@@ -330,9 +353,12 @@ def patch_added_tokens(names: list[str]) -> None:
     _SHA_FILE.write_text(json.dumps(sums, indent=1, sort_keys=True) + "\n")
 
 
-def _tiktoken_style_merges(vocab: dict[str, int]) -> list[list[str]]:
+def _tiktoken_style_merges(vocab: dict[str, int],
+                           ties: str = "ids") -> list[list[str]]:
     """Every split ``t = a + b`` with ``a, b`` in the vocabulary, ordered by
-    the merged token's id, then by ``(id(a), id(b))``."""
+    the merged token's id, then by ``(id(a), id(b))`` (``ties="ids"``) or
+    by the split position (``ties="cut"``, as the Kimi conversion orders
+    them: ``src/toktier/artifacts/conversion.py`` ``convert_kimi_tiktoken``)."""
     merges: list[tuple[int, int, int, str, str]] = []
     for token, rank in vocab.items():
         if len(token) < 2:
@@ -341,7 +367,8 @@ def _tiktoken_style_merges(vocab: dict[str, int]) -> list[list[str]]:
             a, b = token[:k], token[k:]
             ia, ib = vocab.get(a), vocab.get(b)
             if ia is not None and ib is not None:
-                merges.append((rank, ia, ib, a, b))
+                merges.append((rank, ia, ib, a, b) if ties == "ids"
+                              else (rank, k, 0, a, b))
     merges.sort()
     return [[a, b] for _, _, _, a, b in merges]
 

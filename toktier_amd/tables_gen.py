@@ -127,6 +127,31 @@ def build_o200k_classes() -> np.ndarray:
     return tab
 
 
+#: kimi's three Han subclasses on top of the o200k seven
+OK_HL, OK_HN, OK_HP = 7, 8, 9
+
+
+def build_kimi_classes(o200k: np.ndarray) -> np.ndarray:
+    """Ten classes for the kimi split: the o200k seven with every
+    ``\p{Han}`` codepoint moved to HL (Han and ``\p{Lm}`` or ``\p{Lo}``:
+    only the Han branch takes it), HN (Han and ``\p{N}``: the digit
+    branch takes it too) or HP (Han and neither: the punctuation branch
+    takes it), since the pattern's letter classes exclude Han.
+    Reproduces the reference table's sha256 (``kernel_families.v1.json``
+    ``kimi_v1``; subclass sizes ``pretok_classes_kimi.v1.meta.json``)."""
+    han = _probe_membership(r"\p{Han}")
+    lm_lo = _probe_membership(r"\p{Lm}") | _probe_membership(r"\p{Lo}")
+    let = _probe_membership(r"\p{L}")
+    num = _probe_membership(r"\p{N}")
+    tab = o200k.copy()
+    tab[han & lm_lo] = OK_HL
+    tab[han & num] = OK_HN
+    tab[han & ~let & ~num] = OK_HP
+    if ((tab >= OK_HL) != han).any():
+        raise RuntimeError("the Han subclasses do not cover \\p{Han}")
+    return tab
+
+
 def _batch_norm(norm, items: list[str]) -> list[str]:
     """Normalize many short strings at once, separated by U+0020 (a starter
     with no composition or decomposition role)."""
@@ -250,6 +275,9 @@ def main() -> None:
     ok = build_o200k_classes()
     np.savez_compressed(TABLE_DIR / "classes_o200k.npz", o200k=ok)
     print("o200k classes", np.bincount(ok, minlength=7), flush=True)
+    km = build_kimi_classes(ok)
+    np.savez_compressed(TABLE_DIR / "classes_kimi.npz", kimi=km)
+    print("kimi classes", np.bincount(km, minlength=10), flush=True)
     qc = build_nfc_qc()
     np.savez_compressed(TABLE_DIR / "nfc_qc.npz", nfc_qc=qc)
     print("nfc_qc 0:", int((qc == 0).sum()), "1..K:",

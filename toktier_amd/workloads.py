@@ -275,7 +275,8 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
     ``<｜User｜>`` / ``<｜Assistant｜>`` turns after the sentence marker
     (assistant turns closed by ``<｜end▁of▁sentence｜>``), gpt-oss harmony
     ``<|start|>role<|message|>`` ... ``<|end|>`` turns (assistant turns on
-    the final channel, some after an analysis one), GPT-2
+    the final channel, some after an analysis one), Kimi
+    ``<|im_role|>role<|im_middle|>`` ... ``<|im_end|>`` turns, GPT-2
     documents joined by ``<|endoftext|>``. Turns hold U[200, 3000] chars."""
     rng = np.random.default_rng(SEED_BASE + 6 + 1000 * sample)
     body = config2(tokenizer_json, n_chars=n_chars, sample=sample)
@@ -298,6 +299,10 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
             piece = (f"<｜Assistant｜>{content}<｜end▁of▁sentence｜>"
                      if role == "assistant" else
                      f"<｜User｜>{content}" if role == "user" else content)
+        elif family == "kimi_k3":
+            piece = (f"<|im_{role}|>{role}<|im_middle|>{content}<|im_end|>"
+                     if role != "assistant" else
+                     f"<|im_assistant|>assistant<|im_middle|>{content}<|im_end|>")
         elif family == "gpt_oss_120b":
             if role == "assistant":
                 cut = n // 3 if rng.random() < 0.5 else 0
