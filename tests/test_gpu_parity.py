@@ -589,3 +589,28 @@ def test_kimi_million_digit_request_is_linear():
     dt = time.perf_counter() - t0
     assert np.array_equal(got, k.oracle.encode_bytes(s.encode()))
     assert dt < 0.25, dt
+
+
+@pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b", "gpt_oss_120b",
+                                  "kimi_k3"])
+def test_long_whitespace_and_periodic_pieces(name):
+    """Pieces of one repeated character or pair (whitespace runs, rules,
+    repeated syllables): a 64-byte window of them is one or two tokens, so
+    the cut selection finds no cut and the piece is one segment, merged by
+    a workgroup (safe ranks in batch rounds). Against the oracle, and a
+    40,000-space run in well under 50 ms."""
+    import time
+    k, t = kit(name), tok(name)
+    texts = []
+    for n in (513, 600, 1023, 5000, 40_000):
+        texts += [" " * n + "x", "\t" * n + "y", "=" * n + "\n", "ab" * (n // 2) + " c",
+                  " \t" * (n // 2) + "z", "x" + " " * n]
+    for s in texts:
+        got = t.encode(s).array
+        want = k.oracle.encode_bytes(s.encode())
+        assert np.array_equal(got, want), (name, len(s), s[:4])
+    s = " " * 40_000 + "x"
+    t0 = time.perf_counter()
+    t.encode(s)
+    dt = time.perf_counter() - t0
+    assert dt < 0.05, (name, dt)

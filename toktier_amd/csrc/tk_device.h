@@ -270,6 +270,9 @@ hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
                                 int all, hipStream_t s);
+// pieces over WIDE_MAX bytes merged whole, a workgroup each (tables that
+// drop bytes: no cut certification)
+hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s);
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop = nullptr);
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);

@@ -2175,99 +2175,10 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
 // ranks at which its two tokens are next consumed). A failed cut is
 // removed and the joined segment redone, until every remaining cut holds;
 // the worst case is the whole piece as one segment. Tables with a rule
-// out of that order, or bytes without an id, take the serial path.
+// out of that order are certified from every merge round; with bytes
+// without an id, pieces are merged whole. Segments (and such pieces) over
+// WIDE_MAX bytes are merged by a workgroup each (block_bpe).
 
-__device__ __forceinline__ void heap_push(uint64_t* h, uint32_t& n, uint64_t e) {
-  uint32_t i = n++;
-  h[i] = e;
-  while (i > 0) {
-    const uint32_t p = (i - 1) >> 1;
-    if (h[p] <= h[i]) break;
-    const uint64_t x = h[p]; h[p] = h[i]; h[i] = x;
-    i = p;
-  }
-}
-
-__device__ __forceinline__ uint64_t heap_pop(uint64_t* h, uint32_t& n) {
-  const uint64_t top = h[0];
-  h[0] = h[--n];
-  uint32_t i = 0;
-  for (;;) {
-    const uint32_t l = 2 * i + 1, r = l + 1;
-    uint32_t m = i;
-    if (l < n && h[l] < h[m]) m = l;
-    if (r < n && h[r] < h[m]) m = r;
-    if (m == i) break;
-    const uint64_t x = h[m]; h[m] = h[i]; h[i] = x;
-    i = m;
-  }
-  return top;
-}
-
-// Exact merge of [a, b) by one thread (heap of rank<<32|position, stale
-// entries skipped -- the HF algorithm), with the same history recording as
-// wave_bpe when `hist`.
-__device__ void bpe_serial(const DevTables& t, const DevWork& w, uint32_t a,
-                           uint32_t b, bool vocab_first, bool hist) {
-  uint32_t* tok = w.tok;
-  if (vocab_first && t.ignore_merges) {
-    const int32_t hit = vocab_lookup(t, w.text + a, (int64_t)(b - a));
-    if (hit >= 0) {
-      tok[a] = (uint32_t)hit;
-      for (uint32_t p = a + 1; p < b; ++p) tok[p] = INVALID_ID;
-      return;
-    }
-  }
-  int32_t* nx = w.nx;
-  int32_t* pv = w.pv;
-  uint64_t* h = w.heap + 3ull * a;
-  uint32_t hn = 0, nfirst = 0, nlast = 0;
-  int32_t prev = -1;
-  for (uint32_t p = a; p < b; ++p) {
-    const int32_t id = t.byte_id[w.text[p]];
-    if (id < 0) { tok[p] = INVALID_ID; continue; }
-    tok[p] = (uint32_t)id;
-    pv[p] = prev;
-    if (prev >= 0) nx[prev] = (int32_t)p;
-    prev = (int32_t)p;
-  }
-  if (prev >= 0) nx[prev] = -1;
-  for (uint32_t p = a; p < b; ++p) {
-    if (tok[p] == INVALID_ID || nx[p] < 0) continue;
-    const uint64_t v = t.bytepair[((uint32_t)w.text[p] << 8) | w.text[nx[p]]];
-    if (v != ~0ULL) heap_push(h, hn, (v & 0xFFFFFFFF00000000ULL) | p);
-  }
-  while (hn > 0) {
-    const uint64_t e = heap_pop(h, hn);
-    const uint32_t p = (uint32_t)e;
-    const uint32_t r = (uint32_t)(e >> 32);
-    if (tok[p] == INVALID_ID || nx[p] < 0) continue;
-    const int32_t q = nx[p];
-    const uint64_t v = pair_lookup(t, tok[p], tok[q]);
-    if (v == ~0ULL || (uint32_t)(v >> 32) != r) continue;  // stale entry
-    if (hist && t.cert == 2) {
-      w.hfirst[a + nfirst++] = (v & 0xFFFFFFFF00000000ULL) |
-                               (p == a ? HR_FIRST : 0) |
-                               (nx[q] < 0 ? HR_LAST : 0) | (uint32_t)v;
-    } else if (hist) {
-      if (p == a) w.hfirst[a + nfirst++] = v;
-      if (nx[q] < 0) w.hlast[a + nlast++] = v;
-    }
-    tok[p] = (uint32_t)v;
-    tok[q] = INVALID_ID;
-    nx[p] = nx[q];
-    if (nx[p] >= 0) pv[nx[p]] = (int32_t)p;
-    if (pv[p] >= 0) {
-      const uint64_t u = pair_lookup(t, tok[pv[p]], tok[p]);
-      if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | (uint32_t)pv[p]);
-    }
-    if (nx[p] >= 0) {
-      const uint64_t u = pair_lookup(t, tok[p], tok[nx[p]]);
-      if (u != ~0ULL) heap_push(h, hn, (u & 0xFFFFFFFF00000000ULL) | p);
-    }
-  }
-  if (hist) w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
-}
 
 // ---- wide pieces: one wave per piece / segment of 65..WIDE_MAX bytes,
 // state in LDS (slot s = 64*row + lane). Each round merges every leftmost
@@ -2301,6 +2212,242 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) v = min(v, (uint32_t)__shfl_xor(v, d));
   return v;
+}
+
+// ---- segments over WIDE_MAX bytes: one workgroup each
+//
+// block_bpe merges the segment [a, b) in the HF order with the guarded
+// batch rounds of wave_bpe_wide: each round takes the lowest-ranked pair; a
+// safe rank merges every leftmost non-overlapping occurrence at once, an
+// unsafe one its leftmost alone. Its state lives in the segment's per-byte
+// scratch: tok (the symbol at its first byte, INVALID_ID elsewhere), nx /
+// pv (the neighbouring symbols), and in heap (3 words per byte) each
+// symbol's pair (rank << 32 | product id), the round that selected it, and
+// per 1024-byte chunk the lowest key (rank << 32 | offset; SEGB_NOPAIR
+// ranks a symbol with no pair, all ones a chunk with no symbol) and the
+// round that last touched it. A round reads the chunk minima, scans only
+// the chunks that hold its rank (taking a pair when the pair before it was
+// not taken: a two-state automaton composed over the block), merges, and
+// recomputes the pairs and minima of the chunks it touched. Histories as
+// wave_bpe_wide's (a record per round for certification from every round,
+// else the first / last-token events).
+constexpr int SEGB_TPB = 1024;
+constexpr int SEGB_WAVES = SEGB_TPB / 64;
+constexpr uint32_t SEGB_NOPAIR = 0xFFFFFFFEu;
+// the selection automaton's functions of the previous pair's "taken" bit:
+// bit x is the image of x
+constexpr uint32_t SF_ID = 2, SF_ZERO = 0, SF_NOT = 1;
+__device__ __forceinline__ uint32_t sf_at(uint32_t f, uint32_t x) { return (f >> x) & 1; }
+__device__ __forceinline__ uint32_t sf_then(uint32_t f, uint32_t g) {
+  return sf_at(g, sf_at(f, 0)) | (sf_at(g, sf_at(f, 1)) << 1);
+}
+struct SegLds {
+  uint64_t wmin[SEGB_WAVES];
+  uint32_t wfn[SEGB_WAVES];
+  uint32_t queue[SEGB_TPB];
+  uint32_t nq;
+  int32_t hit, last;
+};
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// the workgroup's lowest 64-bit key, in every thread
+__device__ uint64_t block_min64(uint64_t v, SegLds& L) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = shfl_xor64(v, d);
+    v = o < v ? o : v;
+  }
+  if (lane == 0) L.wmin[wv] = v;
+  __syncthreads();
+  uint64_t m = L.wmin[0];
+  for (int i = 1; i < SEGB_WAVES; ++i) m = L.wmin[i] < m ? L.wmin[i] : m;
+  __syncthreads();
+  return m;
+}
+
+// a symbol's key in its chunk's minimum
+__device__ __forceinline__ uint64_t segb_key(uint64_t pair, uint32_t off) {
+  const uint32_t r = pair == ~0ULL ? SEGB_NOPAIR : (uint32_t)(pair >> 32);
+  return ((uint64_t)r << 32) | off;
+}
+
+__device__ void block_bpe(const DevTables& t, const DevWork& w, uint32_t a,
+                          uint32_t b, bool vocab_first, bool hist, SegLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t n = b - a;
+  const uint32_t nch = (n + SEGB_TPB - 1) / SEGB_TPB;
+  uint64_t* pair = w.heap + 3ull * a;
+  uint32_t* selr = reinterpret_cast<uint32_t*>(pair + n);
+  uint32_t* dirty = selr + n;
+  uint64_t* cmin = pair + 2ull * n;
+  uint32_t* tok = w.tok;
+  int32_t* nx = w.nx;
+  int32_t* pv = w.pv;
+  if (vocab_first && t.ignore_merges) {
+    if (tid == 0) L.hit = vocab_lookup(t, w.text + a, (int64_t)n);
+    __syncthreads();
+    const int32_t hit = L.hit;
+    __syncthreads();
+    if (hit >= 0) {
+      for (uint32_t i = tid; i < n; i += SEGB_TPB)
+        tok[a + i] = i == 0 ? (uint32_t)hit : INVALID_ID;
+      return;
+    }
+  }
+  for (uint32_t i = tid; i < n; i += SEGB_TPB) {
+    const int32_t id = t.byte_id[w.text[a + i]];
+    tok[a + i] = id >= 0 ? (uint32_t)id : INVALID_ID;
+    selr[i] = 0;
+  }
+  for (uint32_t c = tid; c < nch; c += SEGB_TPB) dirty[c] = 0;
+  __syncthreads();
+  // neighbour links over the symbols (bytes without an id dropped)
+  for (uint32_t i = tid; i < n; i += SEGB_TPB) {
+    if (tok[a + i] == INVALID_ID) continue;
+    uint32_t j = i + 1;
+    while (j < n && tok[a + j] == INVALID_ID) ++j;
+    nx[a + i] = j < n ? (int32_t)(a + j) : -1;
+    int64_t q = (int64_t)i - 1;
+    while (q >= 0 && tok[a + q] == INVALID_ID) --q;
+    pv[a + i] = q >= 0 ? (int32_t)(a + q) : -1;
+  }
+  __syncthreads();
+  // pairs and chunk minima; the first and the last symbol
+  uint64_t fst = ~0ULL, lst = ~0ULL;
+  for (uint32_t c = 0; c < nch; ++c) {
+    const uint32_t i = c * SEGB_TPB + tid;
+    uint64_t k = ~0ULL;
+    if (i < n && tok[a + i] != INVALID_ID) {
+      const int32_t q = nx[a + i];
+      const uint64_t v = q >= 0 ? pair_lookup(t, tok[a + i], tok[q]) : ~0ULL;
+      pair[i] = v;
+      k = segb_key(v, i);
+      fst = fst < i ? fst : i;
+      lst = lst < (uint64_t)(n - 1 - i) ? lst : (uint64_t)(n - 1 - i);
+    }
+    const uint64_t m = block_min64(k, L);
+    if (tid == 0) cmin[c] = m;
+  }
+  fst = block_min64(fst, L);
+  lst = block_min64(lst, L);
+  if (fst == ~0ULL) {  // no symbol at all
+    if (hist && tid == 0) w.hmeta[a] = 0;
+    return;
+  }
+  const uint32_t first = (uint32_t)fst;
+  if (tid == 0) L.last = (int32_t)(n - 1 - (uint32_t)lst);
+  uint32_t nfirst = 0, nlast = 0;  // (thread 0's)
+  for (uint32_t round = 1;; ++round) {
+    uint64_t m = ~0ULL;
+    for (uint32_t c = tid; c < nch; c += SEGB_TPB) m = cmin[c] < m ? cmin[c] : m;
+    m = block_min64(m, L);
+    const uint32_t R = (uint32_t)(m >> 32);
+    if (R >= SEGB_NOPAIR) break;
+    // every round merges at least its leftmost lowest pair, so n rounds
+    // end it; past that the state is broken: report it, never spin
+    if (round > n) {
+      if (tid == 0) atomicOr(w.status, ST_STALL);
+      break;
+    }
+    const uint32_t s0 = (uint32_t)m;
+    const uint32_t prod = (uint32_t)pair[s0];
+    const bool single = rank_unsafe(t, R);
+    // the selection
+    if (single) {
+      if (tid == 0) selr[s0] = round;
+    } else {
+      uint32_t carry = 0;  // the pair before the chunk was taken
+      for (uint32_t c = 0; c < nch; ++c) {
+        const uint64_t cm = cmin[c];
+        if ((uint32_t)(cm >> 32) != R) {
+          if (cm != ~0ULL) carry = 0;  // its last symbol's pair is not taken
+          continue;
+        }
+        const uint32_t i = c * SEGB_TPB + tid;
+        uint32_t fn = SF_ID;
+        if (i < n && tok[a + i] != INVALID_ID)
+          fn = (pair[i] != ~0ULL && (uint32_t)(pair[i] >> 32) == R) ? SF_NOT : SF_ZERO;
+        uint32_t F = fn;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t o = __shfl_up(F, d);
+          if (lane >= d) F = sf_then(o, F);
+        }
+        if (lane == 63) L.wfn[wv] = F;
+        __syncthreads();
+        uint32_t P = SF_ID, T = SF_ID;
+        for (int j = 0; j < SEGB_WAVES; ++j) {
+          if (j < wv) P = sf_then(P, L.wfn[j]);
+          T = sf_then(T, L.wfn[j]);
+        }
+        __syncthreads();
+        uint32_t E = __shfl_up(F, 1);
+        if (lane == 0) E = SF_ID;
+        const uint32_t in = sf_at(sf_then(P, E), carry);
+        if (fn == SF_NOT && !in) selr[i] = round;
+        carry = sf_at(T, carry);
+      }
+    }
+    __syncthreads();
+    if (hist && tid == 0) {
+      const int32_t l = L.last;
+      const int32_t pl = pv[a + l] >= 0 ? pv[a + l] - (int32_t)a : -1;
+      const bool fsel = selr[first] == round;
+      const bool lsel = pl >= 0 && selr[pl] == round;
+      if (t.cert == 2) {
+        w.hfirst[a + nfirst++] = ((uint64_t)R << 32) | (fsel ? HR_FIRST : 0) |
+                                 (lsel ? HR_LAST : 0) | prod;
+      } else {
+        if (fsel) w.hfirst[a + nfirst++] = ((uint64_t)R << 32) | prod;
+        if (lsel) w.hlast[a + nlast++] = ((uint64_t)R << 32) | prod;
+      }
+      if (lsel) L.last = pl;
+    }
+    // the merges: a selected symbol takes its right neighbour
+    auto merge = [&](uint32_t i) {
+      const int32_t p = (int32_t)(a + i), q = nx[p], nn = nx[q];
+      tok[p] = prod;
+      tok[q] = INVALID_ID;
+      nx[p] = nn;
+      if (nn >= 0) pv[nn] = p;
+      dirty[i / SEGB_TPB] = round;
+      dirty[(uint32_t)(q - (int32_t)a) / SEGB_TPB] = round;
+      const int32_t pp = pv[p];
+      if (pp >= 0) dirty[(uint32_t)(pp - (int32_t)a) / SEGB_TPB] = round;
+    };
+    if (single) {
+      if (tid == 0) merge(s0);
+    } else {
+      for (uint32_t c = 0; c < nch; ++c) {
+        if ((uint32_t)(cmin[c] >> 32) != R) continue;
+        const uint32_t i = c * SEGB_TPB + tid;
+        if (i < n && selr[i] == round) merge(i);
+      }
+    }
+    __syncthreads();
+    // the pairs that changed (the selected symbols and the symbols before
+    // them) and the minima of the chunks touched
+    for (uint32_t c = 0; c < nch; ++c) {
+      if (dirty[c] != round) continue;
+      const uint32_t i = c * SEGB_TPB + tid;
+      uint64_t k = ~0ULL;
+      if (i < n && tok[a + i] != INVALID_ID) {
+        const int32_t q = nx[a + i];
+        if (selr[i] == round || (q >= 0 && selr[q - (int32_t)a] == round))
+          pair[i] = q >= 0 ? pair_lookup(t, tok[a + i], tok[q]) : ~0ULL;
+        k = segb_key(pair[i], i);
+      }
+      const uint64_t mc = block_min64(k, L);
+      if (tid == 0) cmin[c] = mc;
+    }
+  }
+  if (hist && tid == 0) w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
+  __syncthreads();
 }
 
 // pair value for the symbols at slots s and n of a piece starting at a
@@ -2794,10 +2941,7 @@ __device__ void long_prep(const DevTables& t, const DevWork& w, uint32_t blk,
           continue;
         }
       }
-      if (!t.cert) {
-        if (lane == 0) bpe_serial(t, w, pa, pb, false, false);
-        continue;
-      }
+      if (!t.cert) continue;  // merged whole by k_seg_block (mode 1)
       // mark the piece's bytes: whole words directly, the two edge words
       // (shared with neighbouring pieces) with an atomic OR
       const uint32_t wa = pa >> 6, wb = (pb - 1) >> 6;
@@ -2984,15 +3128,32 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
   }
 }
 
-// seglist entries over WIDE_MAX bytes: serial merge with histories.
-__global__ __launch_bounds__(64) void k_seg_serial(DevTables t, DevWork w) {
-  if (!pass_live(w)) return;
-  uint32_t n = *w.segcount;
-  if (n > w.seg_cap) n = w.seg_cap;
-  const uint32_t stride = gridDim.x * blockDim.x;
-  for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride) {
-    const uint32_t a = w.seglist[2 * k], b = w.seglist[2 * k + 1];
-    if (b - a > (uint32_t)WIDE_MAX) bpe_serial(t, w, a, b, false, true);
+// Segments (mode 0: seglist, with histories) or whole pieces (mode 1:
+// longlist, a whole-vocabulary entry first; tables that drop bytes) over
+// WIDE_MAX bytes, one workgroup each: the block's threads look through the
+// block's share of the list for them, then merge them one by one.
+constexpr int SEGB_GRID = 128;
+__global__ __launch_bounds__(SEGB_TPB) void k_seg_block(DevTables t, DevWork w,
+                                                        const uint32_t* list,
+                                                        const uint32_t* count,
+                                                        uint32_t cap, int mode) {
+  __shared__ SegLds L;
+  if (mode == 0 && !pass_live(w)) return;
+  uint32_t n = *count;
+  if (n > cap) n = cap;
+  for (uint32_t base = blockIdx.x * SEGB_TPB; base < n; base += gridDim.x * SEGB_TPB) {
+    if (threadIdx.x == 0) L.nq = 0;
+    __syncthreads();
+    const uint32_t k = base + threadIdx.x;
+    if (k < n && list[2 * k + 1] - list[2 * k] > (uint32_t)WIDE_MAX)
+      L.queue[atomicAdd(&L.nq, 1u)] = k;
+    __syncthreads();
+    const uint32_t nq = L.nq;
+    for (uint32_t j = 0; j < nq; ++j) {
+      const uint32_t kk = L.queue[j];
+      block_bpe(t, w, list[2 * kk], list[2 * kk + 1], mode == 1, mode == 0, L);
+    }
+    __syncthreads();
   }
 }
 
@@ -3160,7 +3321,16 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
   hipLaunchKernelGGL(k_bpe_wide, dim3(512), dim3(256), 0, s, t, w,
                      (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
                      w.seg_cap, 1);
-  hipLaunchKernelGGL(k_seg_serial, dim3(256), dim3(64), 0, s, t, w);
+  hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
+                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
+                     w.seg_cap, 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s) {
+  hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
+                     (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
+                     w.long_cap, 1);
   return hipGetLastError();
 }
 

@@ -549,6 +549,10 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     // longer ones (they touch disjoint bytes and read the same lists)
     hipStream_t s2 = e->stream2;
     HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
+    // (a table that drops bytes merges its pieces over WIDE_MAX bytes
+    // whole, a workgroup each, after the wide merges)
+    if (!e->t.cert && e->gate[tk::GATE_BIG] > 0)
+      HIP_TRY(tk::launch_long_block(e->t, w, s2));
     if (big) {
       // cut / segment / certify, then the repair passes, all on their own
       // stream beside the packed merge and the wide merges
