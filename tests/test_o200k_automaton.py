@@ -2,8 +2,11 @@
 ``o2k_char`` with the state carried across lanes, words and tiles in
 ``k_pretok<4, ...>`` / ``k_pretok<5, ...>``).
 
-The o200k split (oracle ruleset 4) is a left-to-right automaton over ten
-states: each character maps the state after the character before it to the
+The o200k split (oracle ruleset 4) is a left-to-right automaton over eight
+states (the whitespace match shares the state that ends a match: a
+whitespace character after another one reads it as the former; the
+contraction letters share one state: the character before a letter tells
+whether another follows): each character maps the state after the character before it to the
 state after itself and says, per previous state, whether it starts a
 piece; digits take the group rule instead. The model here is that
 automaton character by character. Checked: it splits every string of
@@ -15,7 +18,7 @@ mistakes in the transitions (a C letter resetting LBL, the tail dropping
 '/', a two-letter contraction taking one letter, the whitespace rule
 ignoring the CR/LF before it) each split some string differently.
 
-kimi adds three states (in a Han run; one or two digits into a
+kimi adds three states, eleven in all (in a Han run; one or two digits into a
 \p{N}{1,3} group, since a Han number continues a group but opens a Han
 run at a group's start) and the same checks run against oracle ruleset 5
 over an alphabet with a Han letter, a Han number and other Han.
@@ -33,7 +36,11 @@ from test_oracle import KIMI_ALPHABET, O2K_ALPHABET
 
 P, U, L, C, N, S, M, HL, HN, HP = range(10)
 W = (U, L, C, M)
-PUN, TAIL, LPRE, LU, LBL, LBN, AP2, LAST1, FRESH, WS, HAN, D1, D2 = range(13)
+PUN, TAIL, LPRE, LU, LBL, LBN, CONTR, FRESH, HAN, D1, D2 = range(11)
+
+
+def _nstate(kimi):
+    return 11 if kimi else 8
 
 
 def _classes(kimi=False):
@@ -53,9 +60,11 @@ def _crlf(c: int) -> bool:
 
 def transitions(cps, ds, plant=None, kimi=False):
     """Per character (f, g): f[s] the state after it, g[s] its start bit
-    (None: the digit group rule, o200k), for the previous state s."""
+    (None: the digit group rule, o200k), for the previous state s. FRESH
+    is also the whitespace match's state: a whitespace character after
+    another one reads it as such (the character before it tells)."""
     cls = _classes(kimi)
-    nstate = 13 if kimi else 10
+    nstate = _nstate(kimi)
     n = len(cps)
     cl = [int(cls[c]) for c in cps]
 
@@ -69,6 +78,9 @@ def transitions(cps, ds, plant=None, kimi=False):
         n1 = nxt(j)
         n2 = nxt(n1) if n1 is not None else None
         k1 = cl[n1] if n1 is not None else None
+        has_prev = j > 0 and not ds[j]
+        prev_s = has_prev and cl[j - 1] == S
+        prev_ap = has_prev and cps[j - 1] == ord("'")
         han = kimi and k >= HL
         pm = k in (P, M) or (kimi and k == HP)
         if han:
@@ -82,17 +94,17 @@ def transitions(cps, ds, plant=None, kimi=False):
         elif k == P or (k == S and not _crlf(c)):
             ns = (LPRE if k1 in W else
                   PUN if k == P or (c == 32 and (k1 == P or (kimi and k1 == HP)))
-                  else WS)
+                  else FRESH)
         else:
-            ns = WS
-        ap = None
+            ns = FRESH
+        ap = False  # an apostrophe that a contraction takes
         if c == ord("'") and n1 is not None:
             a = _fold(cps[n1])
             if chr(a) in "stmd":
-                ap = LAST1
+                ap = True
             elif n2 is not None and (chr(a), chr(_fold(cps[n2]))) in (
                     ("r", "e"), ("v", "e"), ("l", "l")):
-                ap = LAST1 if plant == "two_takes_one" else AP2
+                ap = True
         f1 = False  # every character from j to the letter run's end is U
         if k == U:
             q = nxt(j)
@@ -106,8 +118,7 @@ def transitions(cps, ds, plant=None, kimi=False):
                 f3 = False
                 break
             q = nxt(q)
-        prev_crlf = (j > 0 and not ds[j] and _crlf(cps[j - 1])
-                     and plant != "ws_no_crlf")
+        prev_crlf = (has_prev and _crlf(cps[j - 1]) and plant != "ws_no_crlf")
         f, g = [ns] * nstate, [1] * nstate
         for s in range(nstate):
             if ds[j]:
@@ -133,22 +144,24 @@ def transitions(cps, ds, plant=None, kimi=False):
                 elif k in (C, M):
                     keep = s if plant != "c_resets" else LBN
                     st, nx = 0, (LBN if s == LU else keep)
-                elif ap is not None:
-                    st, nx = 0, ap
-            elif s == AP2:
-                st, nx = 0, LAST1
-            elif s == LAST1:
-                st, nx = 0, FRESH
+                elif ap:
+                    st, nx = 0, CONTR
+            elif s == CONTR:
+                two = prev_ap and chr(_fold(c)) in "rvl"
+                if plant == "two_takes_one":
+                    two = False
+                st, nx = 0, (CONTR if two else FRESH)
+            elif s == FRESH and k == S and prev_s:
+                # inside a whitespace match
+                if _crlf(c):
+                    st, nx = 0, FRESH
+                else:
+                    st = f3 if prev_crlf else (n1 is not None and k1 != S)
+                    nx = ns if st else FRESH
             elif s == HAN and han:
                 st, nx = 0, HAN
             elif s in (D1, D2) and k in (N, HN):
                 st, nx = 0, (D2 if s == D1 else FRESH)
-            elif s == WS and k == S:
-                if _crlf(c):
-                    st, nx = 0, WS
-                else:
-                    st = f3 if prev_crlf else (n1 is not None and k1 != S)
-                    nx = ns if st else WS
             f[s], g[s] = nx, (None if k == N and not kimi else int(st))
         out.append((tuple(f), tuple(g)))
     return out, cl
@@ -163,7 +176,7 @@ def split(text: str, docs=(), plant=None, block: int = 0, kimi=False):
     n = len(cps)
     ds = [i == 0 or i in docs for i in range(n)]
     fg, cl = transitions(cps, ds, plant, kimi)
-    nstate = 13 if kimi else 10
+    nstate = _nstate(kimi)
     states = [0] * n
     if block:
         s = FRESH

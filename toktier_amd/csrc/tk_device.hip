@@ -766,11 +766,12 @@ __device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
 // its left (a mark continues a P match or a letter match; a run of C
 // characters after a lower-case letter is one letter match, after
 // anything else it can end before an upper-case run), so the split is a
-// left-to-right automaton: the state after each character, one of ten,
+// left-to-right automaton: the state after each character, one of eight,
 // is what the character after it needs. Each character is a transition
-// function of the previous state (a nibble per state) and a start bit per
-// previous state; the functions compose by a wave scan, and a tile's
-// entry state comes from the word before it or from the tiles before it.
+// function of the previous state (a byte per state: the functions compose
+// by byte permutes) and a start bit per previous state; the functions
+// compose by a wave scan, and a tile's entry state comes from the word
+// before it or from the tiles before it.
 // States (the previous character is ...):
 //   PUN   in a P match's [PM]+ (or the U+0020 that opens one)
 //   TAIL  in its [\r\n/]* tail
@@ -779,11 +780,13 @@ __device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
 //   LBL   a B letter (L C M) whose run of B letters since the last U (or
 //         the match's first letter) holds an L
 //   LBN   a B letter whose run holds no L
-//   AP2   an apostrophe that takes the next two letters ('re 've 'll)
-//   LAST1 the match holds exactly one more character (an apostrophe
-//         taking one letter, or the first of two)
-//   FRESH the match ends after it (digits, the last contraction letter)
-//   WS    in a whitespace match
+//   CONTR a contraction's apostrophe or first letter, more letters follow
+//         (the letter's own predecessor tells whether it is the first of
+//         two: 're 've 'll)
+//   FRESH the match ends after it (digits, the last contraction letter),
+//         or it is in a whitespace match (a whitespace character after
+//         another one reads it so: no other state follows a whitespace
+//         character that a whitespace character can follow)
 // Inside a letter run only U letters start pieces: after LBL always (the
 // [A]*[B]+ alternative stopped there), after LBN exactly when every
 // character from it to the run's end is U (A* gave the run back to its
@@ -795,84 +798,133 @@ constexpr int RS_KIMI = 5;
 constexpr uint8_t OK_P = 0, OK_U = 1, OK_L = 2, OK_C = 3, OK_N = 4,
                   OK_S = 5, OK_M = 6, OK_HL = 7, OK_HN = 8, OK_HP = 9;
 enum : uint32_t {
-  O2_PUN = 0, O2_TAIL, O2_LPRE, O2_LU, O2_LBL, O2_LBN, O2_AP2, O2_LAST1,
-  O2_FRESH, O2_WS,
+  O2_PUN = 0, O2_TAIL, O2_LPRE, O2_LU, O2_LBL, O2_LBN, O2_CONTR, O2_FRESH,
   // (kimi) in a Han run; one or two digits into a \p{N}{1,3} group
   O2_HAN, O2_D1, O2_D2
 };
-// states of the o200k / kimi automaton
-template <int RS> constexpr int o2_nst() { return RS == RS_KIMI ? 13 : 10; }
-template <int N> constexpr uint64_t o2_rep() {  // a nibble in every state
-  uint64_t r = 0;
-  for (int i = 0; i < N; ++i) r |= 1ull << (4 * i);
-  return r;
-}
-template <int N> constexpr uint64_t o2_id() {   // the identity
-  uint64_t r = 0;
-  for (int i = 0; i < N; ++i) r |= (uint64_t)i << (4 * i);
-  return r;
-}
-__device__ __forceinline__ uint32_t o2_at(uint64_t f, uint32_t s) {
-  return (uint32_t)(f >> (4 * s)) & 15u;
-}
-__device__ __forceinline__ uint64_t o2_set(uint64_t f, uint32_t s, uint32_t v) {
-  return (f & ~(15ull << (4 * s))) | ((uint64_t)v << (4 * s));
-}
-// a, then b
-template <int N>
-__device__ __forceinline__ uint64_t o2_then(uint64_t a, uint64_t b) {
-  uint64_t h = 0;
+// states of the o200k / kimi automaton, and the 32-bit words of a
+// function (a byte per state; kimi's eleven padded to sixteen)
+template <int RS> constexpr int o2_nst() { return RS == RS_KIMI ? 11 : 8; }
+template <int RS> constexpr int o2_words() { return RS == RS_KIMI ? 4 : 2; }
+template <int W> struct O2Fn { uint32_t d[W]; };
+template <int W> __device__ __forceinline__ O2Fn<W> o2_rep(uint32_t v) {
+  O2Fn<W> f;
 #pragma unroll
-  for (uint32_t s = 0; s < (uint32_t)N; ++s)
-    h |= (uint64_t)o2_at(b, o2_at(a, s)) << (4 * s);
+  for (int k = 0; k < W; ++k) f.d[k] = v * 0x01010101u;
+  return f;
+}
+template <int W> __device__ __forceinline__ O2Fn<W> o2_ident() {
+  O2Fn<W> f;
+#pragma unroll
+  for (int k = 0; k < W; ++k) f.d[k] = 0x03020100u + (uint32_t)k * 0x04040404u;
+  return f;
+}
+template <int W> __device__ __forceinline__ uint32_t o2_at(const O2Fn<W>& f, uint32_t s) {
+  uint32_t d = f.d[0];
+#pragma unroll
+  for (int k = 1; k < W; ++k) d = (s >> 2) == (uint32_t)k ? f.d[k] : d;
+  return (d >> (8 * (s & 3))) & 0xFFu;
+}
+template <int W> __device__ __forceinline__ void o2_set(O2Fn<W>& f, uint32_t s, uint32_t v) {
+  f.d[s >> 2] = (f.d[s >> 2] & ~(0xFFu << (8 * (s & 3)))) | (v << (8 * (s & 3)));
+}
+// a, then b: byte s of the result is b's byte a[s] (v_perm_b32 picks bytes
+// 0..7 of its two sources; kimi's states 8..15 come from the second pair)
+template <int W>
+__device__ __forceinline__ O2Fn<W> o2_then(const O2Fn<W>& a, const O2Fn<W>& b) {
+  O2Fn<W> h;
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const uint32_t x = a.d[k];
+    const uint32_t lo = __builtin_amdgcn_perm(b.d[1], b.d[0], x);
+    if (W == 2) {
+      h.d[k] = lo;
+    } else {
+      const uint32_t hi = __builtin_amdgcn_perm(b.d[W - 1], b.d[W - 2], x ^ 0x08080808u);
+      const uint32_t m = ((x >> 3) & 0x01010101u) * 0xFFu;
+      h.d[k] = (hi & m) | (lo & ~m);
+    }
+  }
   return h;
 }
-template <int N>
-__device__ __forceinline__ bool o2_const(uint64_t f) {
-  return f == (f & 15u) * o2_rep<N>();
+template <int RS>
+__device__ __forceinline__ bool o2_const(const O2Fn<o2_words<RS>()>& f) {
+  const uint32_t r = (f.d[0] & 0xFFu) * 0x01010101u;
+  if (RS == RS_KIMI)
+    return f.d[0] == r && f.d[1] == r && ((f.d[2] ^ r) & 0x00FFFFFFu) == 0;
+  return f.d[0] == r && f.d[1] == r;
+}
+// a function as a nibble per state (the tiles' published form) and back
+template <int RS> __device__ __forceinline__ uint64_t o2_pack(const O2Fn<o2_words<RS>()>& f) {
+  uint64_t x = 0;
+#pragma unroll
+  for (int s = 0; s < o2_nst<RS>(); ++s) x |= (uint64_t)(o2_at(f, s) & 15u) << (4 * s);
+  return x;
+}
+template <int RS> __device__ __forceinline__ O2Fn<o2_words<RS>()> o2_unpack(uint64_t x) {
+  O2Fn<o2_words<RS>()> f = o2_ident<o2_words<RS>()>();
+#pragma unroll
+  for (int s = 0; s < o2_nst<RS>(); ++s) o2_set(f, s, (uint32_t)(x >> (4 * s)) & 15u);
+  return f;
+}
+template <int W> __device__ __forceinline__ O2Fn<W> o2_shfl_up(const O2Fn<W>& f, int d) {
+  O2Fn<W> g;
+#pragma unroll
+  for (int k = 0; k < W; ++k) g.d[k] = __shfl_up(f.d[k], d);
+  return g;
+}
+template <int W> __device__ __forceinline__ O2Fn<W> o2_shfl(const O2Fn<W>& f, int l) {
+  O2Fn<W> g;
+#pragma unroll
+  for (int k = 0; k < W; ++k) g.d[k] = __shfl(f.d[k], l);
+  return g;
 }
 __device__ __forceinline__ bool ok_w(int k) {
   return k == OK_U || k == OK_L || k == OK_C || k == OK_M;
 }
-__device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int d) {
-  const uint32_t lo = __shfl_up((uint32_t)v, d), hi = __shfl_up((uint32_t)(v >> 32), d);
-  return ((uint64_t)hi << 32) | lo;
-}
 
-// The transition of the character at i (code point cp, class k; d0: a
-// document starts at i): *fo the next state per previous state, *go the
-// start bit per previous state (o200k digits: the caller's group rule
-// replaces it). `need_g` false skips what only the start bits read;
-// `contr` false drops the contraction suffix (o200k rows without it).
+// The transition of the character at i: *fo the next state per previous
+// state, *go the start bit per previous state (o200k digits: the caller's
+// group rule replaces it). x0 is its entry (code point | class), xp / x1
+// the entries of the characters before / after it in its document (hp /
+// h1: present; d0: a document starts at i). `need_g` false skips what only
+// the start bits read; `contr` false drops the contraction suffix (o200k
+// rows without it). The function is built from the three entries with
+// selects; the rare cases that read further (an upper-case run after a C
+// or M letter, a whitespace run after a CR/LF, the second letter of
+// 're 've 'll) walk through the context.
 // kimi (RS_KIMI): a Han character (HL HN HP) opens or continues a Han run;
 // \p{N}{1,3} counts its digits in the state (a Han number inside a group
 // is a digit, at a group's start it opens a Han run); P matches take the
 // other Han (HP) and their tail is [\r\n]* (no '/').
 template <int RS, class C>
-__device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
-                         bool need_g, bool contr, uint64_t* fo, uint32_t* go) {
+__device__ __forceinline__ void o2k_char(const C& c, int64_t i, uint32_t x0, bool d0,
+                                         uint32_t xp, bool hp, uint32_t x1, bool h1,
+                                         bool need_g, bool contr,
+                                         O2Fn<o2_words<RS>()>* fo, uint32_t* go) {
   constexpr bool KIMI = RS == RS_KIMI;
+  constexpr int W = o2_words<RS>();
   constexpr uint32_t ALL = (1u << o2_nst<RS>()) - 1;
-  const int64_t n1 = c.next(i);
-  const Ch x1 = n1 >= 0 ? c.at(n1) : Ch{-1, -1, 0xFF};
-  const int k1 = n1 >= 0 ? x1.cl : -1;
+  const int32_t cp = ecp(x0), cp1 = ecp(x1), cpp = ecp(xp);
+  const int k = dcl(x0);
+  const int k1 = h1 ? dcl(x1) : -1, kp = hp ? dcl(xp) : -1;
   const bool cr = crlf(cp);
   const bool han = KIMI && k >= OK_HL;
+  const bool w0 = ok_w(k), w1 = ok_w(k1);
   // [^\s\p{L}\p{N}]: the characters a P match's [PM]+ takes
   const bool pm = k == OK_P || k == OK_M || (KIMI && k == OK_HP);
   // the state of a match that starts here
-  uint32_t ns;
-  if (han) ns = O2_HAN;
-  else if (k == OK_N) ns = KIMI ? O2_D1 : O2_FRESH;
-  else if (k == OK_U) ns = O2_LU;
-  else if (k == OK_L) ns = O2_LBL;
-  else if (k == OK_C || k == OK_M) ns = O2_LBN;
-  else if (k == OK_P || (k == OK_S && !cr))
-    ns = ok_w(k1) ? O2_LPRE
-       : (k == OK_P || (cp == ' ' && (k1 == OK_P || (KIMI && k1 == OK_HP))))
-       ? O2_PUN : O2_WS;
-  else ns = O2_WS;
-  uint64_t f = (uint64_t)ns * o2_rep<o2_nst<RS>()>();
+  const bool q0 = k == OK_P || (k == OK_S && !cr);
+  const uint32_t ns =
+      han ? O2_HAN
+      : k == OK_N ? (KIMI ? O2_D1 : O2_FRESH)
+      : k == OK_U ? O2_LU
+      : k == OK_L ? O2_LBL
+      : (k == OK_C || k == OK_M) ? O2_LBN
+      : (q0 && w1) ? O2_LPRE
+      : (k == OK_P || (cp == ' ' && (k1 == OK_P || (KIMI && k1 == OK_HP)))) ? O2_PUN
+      : O2_FRESH;
+  O2Fn<W> f = o2_rep<W>(ns);
   uint32_t g = ALL;
   if (d0) {
     *fo = f;
@@ -880,103 +932,97 @@ __device__ void o2k_char(const C& c, int64_t i, int32_t cp, int k, bool d0,
     return;
   }
   // a P match: [PM]+ goes on, a CR/LF opens the tail
-  if (pm) {
-    f = o2_set(f, O2_PUN, O2_PUN);
-    g &= ~(1u << O2_PUN);
-  } else if (cr) {
-    f = o2_set(f, O2_PUN, O2_TAIL);
+  if (pm || cr) {
+    o2_set(f, O2_PUN, pm ? O2_PUN : O2_TAIL);
     g &= ~(1u << O2_PUN);
   }
   if (cr || (!KIMI && cp == '/')) {
-    f = o2_set(f, O2_TAIL, O2_TAIL);
+    o2_set(f, O2_TAIL, O2_TAIL);
     g &= ~(1u << O2_TAIL);
   }
   if (KIMI) {
     // a Han run goes on; a \p{N} character continues a digit group
     if (han) {
-      f = o2_set(f, O2_HAN, O2_HAN);
+      o2_set(f, O2_HAN, O2_HAN);
       g &= ~(1u << O2_HAN);
     }
     if (k == OK_N || k == OK_HN) {
-      f = o2_set(o2_set(f, O2_D1, O2_D2), O2_D2, O2_FRESH);
+      o2_set(f, O2_D1, O2_D2);
+      o2_set(f, O2_D2, O2_FRESH);
       g &= ~((1u << O2_D1) | (1u << O2_D2));
     }
   }
-  if (ok_w(k)) {
+  if (w0) {
     // a letter after a prefix or inside a letter run (the class state is
     // ns already, except that a C or M letter keeps LBL)
-    g &= ~((1u << O2_LPRE) | (1u << O2_LU) | (1u << O2_LBL) | (1u << O2_LBN));
-    if (k == OK_U) {
-      g |= 1u << O2_LBL;
-      if (need_g) {
-        // after a C or M letter: a start when the U run reaches the
-        // letter run's end (LBN is reached only over C or M letters)
-        const int64_t p = c.prev(i);
-        const int kp = p >= 0 ? c.at(p).cl : -1;
-        if (kp == OK_C || kp == OK_M) {
-          int64_t q = n1;
-          int kq = k1;
-          while (q >= 0 && kq == OK_U) {
-            q = c.next(q);
-            kq = q >= 0 ? c.at(q).cl : -1;
-          }
-          if (!ok_w(kq)) g |= 1u << O2_LBN;
-        }
-      }
-    } else if (k != OK_L) {
-      f = o2_set(f, O2_LBL, O2_LBL);
-    }
-    // the letters a contraction takes ('s 't 'm 'd: one; 're 've 'll: two)
+    g &= ~((1u << O2_LPRE) | (1u << O2_LU) | (1u << O2_LBN));
+    if (k != OK_U) g &= ~(1u << O2_LBL);
+    if (k == OK_C || k == OK_M) o2_set(f, O2_LBL, O2_LBL);
+    // a contraction's letters ('s 't 'm 'd: one; 're 've 'll: two): the
+    // first of two follows the apostrophe itself
     const int a = fold(cp);
     if (contr && (a == 's' || a == 't' || a == 'm' || a == 'd' || a == 'r' ||
                   a == 'e' || a == 'v' || a == 'l')) {
-      f = o2_set(o2_set(f, O2_AP2, O2_LAST1), O2_LAST1, O2_FRESH);
-      g &= ~((1u << O2_AP2) | (1u << O2_LAST1));
+      const bool two = (a == 'r' || a == 'v' || a == 'l') && hp && cpp == '\'';
+      o2_set(f, O2_CONTR, two ? O2_CONTR : O2_FRESH);
+      g &= ~(1u << O2_CONTR);
     }
-  } else if (contr && cp == '\'' && n1 >= 0) {
+    // after a C or M letter an upper-case letter starts a piece when the
+    // U run reaches the letter run's end (LBN is reached only over C or M
+    // letters)
+    if (need_g && k == OK_U && (kp == OK_C || kp == OK_M)) {
+      bool end = !w1;
+      if (k1 == OK_U) {
+        int64_t q = c.next(c.next(i));
+        int kq = q >= 0 ? c.at(q).cl : -1;
+        while (q >= 0 && kq == OK_U) {
+          q = c.next(q);
+          kq = q >= 0 ? c.at(q).cl : -1;
+        }
+        end = !ok_w(kq);
+      }
+      if (end) g |= 1u << O2_LBN;
+    }
+  } else if (contr && cp == '\'' && h1) {
     // a contraction after a letter match
-    const int a = fold(x1.cp);
-    uint32_t ap = 0;
-    if (a == 's' || a == 't' || a == 'm' || a == 'd') {
-      ap = O2_LAST1;
-    } else if (a == 'r' || a == 'v' || a == 'l') {
-      const int64_t n2 = c.next(n1);
+    const int a = fold(cp1);
+    bool ap = a == 's' || a == 't' || a == 'm' || a == 'd';
+    if (a == 'r' || a == 'v' || a == 'l') {
+      const int64_t n2 = c.next(c.next(i));
       if (n2 >= 0) {
         const int b = fold(c.at(n2).cp);
-        if ((a == 'r' && b == 'e') || (a == 'v' && b == 'e') || (a == 'l' && b == 'l'))
-          ap = O2_AP2;
+        ap = (a == 'r' && b == 'e') || (a == 'v' && b == 'e') || (a == 'l' && b == 'l');
       }
     }
     if (ap) {
-      f = o2_set(o2_set(o2_set(f, O2_LU, ap), O2_LBL, ap), O2_LBN, ap);
+      o2_set(f, O2_LU, O2_CONTR);
+      o2_set(f, O2_LBL, O2_CONTR);
+      o2_set(f, O2_LBN, O2_CONTR);
       g &= ~((1u << O2_LU) | (1u << O2_LBL) | (1u << O2_LBN));
     }
   }
-  if (k == OK_S) {
-    // whitespace: \s*[\r\n]+ ends after the run's last CR/LF; after that
-    // (or with none) \s+(?!\S) leaves the run's last character
-    bool s = false;
-    if (!cr && need_g) {
-      const int64_t p = c.prev(i);
-      if (p >= 0 && crlf(c.at(p).cp)) {
-        s = true;
-        for (int64_t q = n1; q >= 0;) {
+  if (k == OK_S && kp == OK_S) {
+    // after another whitespace character FRESH is the whitespace match:
+    // \s*[\r\n]+ ends after the run's last CR/LF; after that (or with
+    // none) \s+(?!\S) leaves the run's last character
+    bool s = !cr && h1 && k1 != OK_S;
+    if (!cr && need_g && crlf(cpp)) {
+      // right after a CR/LF: a start unless another CR/LF follows in the
+      // run (only the start bit reads this: a start inside the run before
+      // its last character leaves FRESH either way)
+      s = true;
+      if (k1 == OK_S) {
+        for (int64_t q = c.next(i); q >= 0;) {
           const Ch x = c.at(q);
           if (x.cl != OK_S) break;
           if (crlf(x.cp)) { s = false; break; }
           q = c.next(q);
         }
-      } else {
-        s = n1 >= 0 && k1 != OK_S;
       }
-    } else if (!cr) {
-      // (the state does not need the walk: a start inside the run before
-      // its last character leaves the state WS either way)
-      s = n1 >= 0 && k1 != OK_S;
     }
     if (!s) {
-      f = o2_set(f, O2_WS, O2_WS);
-      g &= ~(1u << O2_WS);
+      o2_set(f, O2_FRESH, O2_FRESH);
+      g &= ~(1u << O2_FRESH);
     }
   }
   *fo = f;
@@ -1047,7 +1093,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   __shared__ uint32_t gC[PT_TILE / 64 + 1];
   // (o200k) the functions of the words before the waves' blocks, the
   // blocks' functions, and the blocks' entry states
-  __shared__ uint64_t o2w[4], o2b[4];
+  __shared__ uint32_t o2w[4][4], o2b[4][4];
   __shared__ uint32_t o2e[4];
   const int tid = threadIdx.x;
   if (tid < PACK_CLASSES) {
@@ -1478,21 +1524,53 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     };
     constexpr int WPB = PT_TILE / 64 / (PRETOK_TPB / 64);  // words per wave
     constexpr int NST = o2_nst<RS>();
-    constexpr uint64_t ID = o2_id<NST>();
+    constexpr int W = o2_words<RS>();
+    using Fn = O2Fn<W>;
     constexpr uint32_t ALL = (1u << NST) - 1;
     const bool contr = t.contractions != 0;
     // the lane's transition and start bits in word k (-1 .. PT_TILE / 64);
     // positions outside the text and inside a character pass the state on
-    auto lane_fn = [&](int k, bool need_g, uint64_t* f, uint32_t* g) {
+    auto lane_fn = [&](int k, bool need_g, Fn* f, uint32_t* g) {
       const int64_t i = base + 64 * k + lane;
       const int Li = PT_HALO + 64 * k + lane;
-      *f = ID;
+      *f = o2_ident<W>();
       *g = 0;
       if (i < 0 || i >= nb || is_cont(sb[64 * k + lane + PT_PAD])) return;
       const uint32_t e = se[Li];
       const int kc = dcl(e);
       const bool d0 = ds(Li);
-      o2k_char<RS>(c, i, (int32_t)(e & 0x1FFFFF), kc, d0, need_g, contr, f, g);
+      // the characters before and after it (from the staged entries; the
+      // first lanes of the halo word and the last of the word after the
+      // tile read the text)
+      uint32_t xp = 0, x1 = 0;
+      bool hp = false, h1 = false;
+      if (!d0) {
+        if (Li >= 4) {
+          const int Lp = prv(Li);
+          xp = se[Lp];
+          hp = true;
+        } else {
+          const int64_t q = c.prev(i);
+          if (q >= 0) {
+            const Ch x = c.at(q);
+            xp = (uint32_t)x.cp | ((uint32_t)(x.cl & 3) << 21) | ((uint32_t)(x.cl >> 2) << 28);
+            hp = true;
+          }
+        }
+      }
+      const int Ln = Li + 1 + (int)((e >> 25) & 3);
+      if (Ln < PT_SPAN) {
+        h1 = lo + Ln < nb && !ds(Ln);
+        if (h1) x1 = se[Ln];
+      } else {
+        const int64_t q = c.next(i);
+        if (q >= 0) {
+          const Ch x = c.at(q);
+          x1 = (uint32_t)x.cp | ((uint32_t)(x.cl & 3) << 21) | ((uint32_t)(x.cl >> 2) << 28);
+          h1 = true;
+        }
+      }
+      o2k_char<RS>(c, i, e, d0, xp, hp, x1, h1, need_g, contr, f, g);
       if (RS == RS_O200K && need_g && kc == OK_N && !d0) {
         // \p{N}{1,K}: the N characters of the run before i decide
         bool r = true;
@@ -1514,29 +1592,25 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     // inclusive composition over the lanes (lane 0 first): windows of four
     // when every window from lane 4 on is constant (then each is the state
     // after its lane whatever came before), else the whole prefix
-    auto scan = [&](uint64_t F) {
-      uint64_t o = shfl_up64(F, 1);
-      if (lane >= 1) F = o2_then<NST>(o, F);
-      o = shfl_up64(F, 2);
-      if (lane >= 2) F = o2_then<NST>(o, F);
-      if (__any(lane >= 4 && !o2_const<NST>(F))) {
+    auto scan = [&](Fn F) {
+      Fn o = o2_shfl_up(F, 1);
+      if (lane >= 1) F = o2_then(o, F);
+      o = o2_shfl_up(F, 2);
+      if (lane >= 2) F = o2_then(o, F);
+      if (__any(lane >= 4 && !o2_const<RS>(F))) {
         for (int d = 4; d < 64; d <<= 1) {
-          o = shfl_up64(F, d);
-          if (lane >= d) F = o2_then<NST>(o, F);
+          o = o2_shfl_up(F, d);
+          if (lane >= d) F = o2_then(o, F);
         }
       }
       return F;
     };
-    auto lane63 = [&](uint64_t v) {
-      const uint32_t a = __shfl((uint32_t)v, 63), b = __shfl((uint32_t)(v >> 32), 63);
-      return ((uint64_t)b << 32) | a;
-    };
     // the function of word k (lane 63's composition), wave-uniform
     auto word_fn = [&](int k) {
-      uint64_t f;
+      Fn f;
       uint32_t g;
       lane_fn(k, false, &f, &g);
-      return lane63(scan(f));
+      return o2_shfl(scan(f), 63);
     };
     // word k from entry state `carry`: its start word; returns the state
     // after it
@@ -1546,7 +1620,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         if (lane == 0) sw[k] = ~0ULL;
         return carry;
       }
-      uint64_t f;
+      Fn f;
       uint32_t g;
       lane_fn(k, true, &f, &g);
       const uint32_t sj = o2_at(scan(f), carry);  // the state after the lane
@@ -1582,31 +1656,40 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     const int k0 = WPB * wv;
     // the word before the block (the tile's halo word for wave 0); the
     // first tile starts at a document start, whatever came before
-    uint64_t T = word_fn(k0 - 1);
-    if (blockIdx.x == 0 && wv == 0) T = (uint64_t)O2_FRESH * o2_rep<NST>();
-    if (lane == 0) o2w[wv] = T;
+    Fn T = word_fn(k0 - 1);
+    if (blockIdx.x == 0 && wv == 0) T = o2_rep<W>(O2_FRESH);
+    if (lane == 0)
+      for (int q = 0; q < W; ++q) o2w[wv][q] = T.d[q];
     __syncthreads();
+    auto lds_fn = [&](const uint32_t (*a)[4], int j) {
+      Fn f;
+#pragma unroll
+      for (int q = 0; q < W; ++q) f.d[q] = a[j][q];
+      return f;
+    };
     bool fast = true;
-    for (int j = 0; j < PRETOK_TPB / 64; ++j) fast &= o2_const<NST>(o2w[j]);
+    for (int j = 0; j < PRETOK_TPB / 64; ++j) fast &= o2_const<RS>(lds_fn(o2w, j));
     uint32_t carry;
     uint64_t* op = w.ostate + 2 * (int64_t)blockIdx.x;
     if (fast) {
-      carry = (uint32_t)(o2w[wv] & 15);
+      carry = o2w[wv][0] & 0xFFu;
     } else {
-      uint64_t B = ID;
-      for (int k = k0; k < k0 + WPB; ++k) B = o2_then<NST>(B, word_fn(k));
-      if (lane == 0) o2b[wv] = B;
+      Fn B = o2_ident<W>();
+      for (int k = k0; k < k0 + WPB; ++k) B = o2_then(B, word_fn(k));
+      if (lane == 0)
+        for (int q = 0; q < W; ++q) o2b[wv][q] = B.d[q];
       __syncthreads();
       if (tid == 0) {
-        uint64_t A = o2b[0];
-        for (int j = 1; j < PRETOK_TPB / 64; ++j) A = o2_then<NST>(A, o2b[j]);
+        Fn A = lds_fn(o2b, 0);
+        for (int j = 1; j < PRETOK_TPB / 64; ++j) A = o2_then(A, lds_fn(o2b, j));
         uint32_t entry = O2_FRESH;
-        if (o2_const<NST>(o2w[0])) {
-          entry = (uint32_t)(o2w[0] & 15);
+        const Fn H = lds_fn(o2w, 0);
+        if (o2_const<RS>(H)) {
+          entry = o2_at(H, 0);
         } else {
-          o2_publish(op, w.seq, O2_AGG, A, 0);
+          o2_publish(op, w.seq, O2_AGG, o2_pack<RS>(A), 0);
           // G: the function of the tiles after u up to this one
-          uint64_t G = ID;
+          Fn G = o2_ident<W>();
           bool done = false;
           for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0 && !done; --u) {
             const uint64_t* q = w.ostate + 2 * u;
@@ -1627,9 +1710,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
             } else {
               const uint64_t v0 = __hip_atomic_load(q, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
-              G = o2_then<NST>((uint32_t)v0 | ((v1 & 0xFFFFF) << 32), G);
-              if (o2_const<NST>(G)) {
-                entry = (uint32_t)(G & 15);
+              G = o2_then(o2_unpack<RS>((uint32_t)v0 | ((v1 & 0xFFFFF) << 32)), G);
+              if (o2_const<RS>(G)) {
+                entry = o2_at(G, 0);
                 done = true;
               }
             }
@@ -1639,7 +1722,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         }
         o2_publish(op, w.seq, O2_INCL, 0, o2_at(A, entry));
         o2e[0] = entry;
-        for (int j = 1; j < PRETOK_TPB / 64; ++j) o2e[j] = o2_at(o2b[j - 1], o2e[j - 1]);
+        for (int j = 1; j < PRETOK_TPB / 64; ++j) o2e[j] = o2_at(lds_fn(o2b, j - 1), o2e[j - 1]);
       }
       __syncthreads();
       carry = o2e[wv];
