@@ -867,16 +867,35 @@ template <int RS> __device__ __forceinline__ O2Fn<o2_words<RS>()> o2_unpack(uint
   for (int s = 0; s < o2_nst<RS>(); ++s) o2_set(f, s, (uint32_t)(x >> (4 * s)) & 15u);
   return f;
 }
-template <int W> __device__ __forceinline__ O2Fn<W> o2_shfl_up(const O2Fn<W>& f, int d) {
+// f moved by a DPP control over the wave; lanes with no source (or outside
+// the rows of row_mask) get the identity
+template <int ctrl, int row_mask, int W>
+__device__ __forceinline__ O2Fn<W> o2_dpp(const O2Fn<W>& f) {
+  const O2Fn<W> id = o2_ident<W>();
   O2Fn<W> g;
 #pragma unroll
-  for (int k = 0; k < W; ++k) g.d[k] = __shfl_up(f.d[k], d);
+  for (int k = 0; k < W; ++k)
+    g.d[k] = (uint32_t)__builtin_amdgcn_update_dpp((int)id.d[k], (int)f.d[k], ctrl,
+                                                   row_mask, 0xF, false);
   return g;
 }
-template <int W> __device__ __forceinline__ O2Fn<W> o2_shfl(const O2Fn<W>& f, int l) {
+// inclusive composition over the wave's lanes, lane 0 first: within each
+// row of 16 (row_shr 1, 2, 4, 8), then rows 1 and 3 after lane 15 of the
+// row before (row_bcast:15), rows 2 and 3 after lane 31 (row_bcast:31)
+template <int W>
+__device__ __forceinline__ O2Fn<W> o2_scan(O2Fn<W> F) {
+  F = o2_then(o2_dpp<0x111, 0xF>(F), F);
+  F = o2_then(o2_dpp<0x112, 0xF>(F), F);
+  F = o2_then(o2_dpp<0x114, 0xF>(F), F);
+  F = o2_then(o2_dpp<0x118, 0xF>(F), F);
+  F = o2_then(o2_dpp<0x142, 0xA>(F), F);
+  F = o2_then(o2_dpp<0x143, 0xC>(F), F);
+  return F;
+}
+template <int W> __device__ __forceinline__ O2Fn<W> o2_lane63(const O2Fn<W>& f) {
   O2Fn<W> g;
 #pragma unroll
-  for (int k = 0; k < W; ++k) g.d[k] = __shfl(f.d[k], l);
+  for (int k = 0; k < W; ++k) g.d[k] = (uint32_t)__builtin_amdgcn_readlane((int)f.d[k], 63);
   return g;
 }
 __device__ __forceinline__ bool ok_w(int k) {
@@ -889,10 +908,13 @@ __device__ __forceinline__ bool ok_w(int k) {
 // the entries of the characters before / after it in its document (hp /
 // h1: present; d0: a document starts at i). `need_g` false skips what only
 // the start bits read; `contr` false drops the contraction suffix (o200k
-// rows without it). The function is built from the three entries with
-// selects; the rare cases that read further (an upper-case run after a C
-// or M letter, a whitespace run after a CR/LF, the second letter of
-// 're 've 'll) walk through the context.
+// rows without it); ws_hint: for a whitespace character right after a
+// CR/LF, whether no CR/LF follows in its run (1 / 0, from the word's byte
+// masks), -1 when the masks do not tell. The function is built from the
+// three entries with selects; the rare cases that read further (an
+// upper-case run after a C or M letter, a whitespace run after a CR/LF that
+// the masks do not resolve, the second letter of 're 've 'll) walk
+// through the context.
 // kimi (RS_KIMI): a Han character (HL HN HP) opens or continues a Han run;
 // \p{N}{1,3} counts its digits in the state (a Han number inside a group
 // is a digit, at a group's start it opens a Han run); P matches take the
@@ -900,7 +922,7 @@ __device__ __forceinline__ bool ok_w(int k) {
 template <int RS, class C>
 __device__ __forceinline__ void o2k_char(const C& c, int64_t i, uint32_t x0, bool d0,
                                          uint32_t xp, bool hp, uint32_t x1, bool h1,
-                                         bool need_g, bool contr,
+                                         bool need_g, bool contr, int ws_hint,
                                          O2Fn<o2_words<RS>()>* fo, uint32_t* go) {
   constexpr bool KIMI = RS == RS_KIMI;
   constexpr int W = o2_words<RS>();
@@ -1011,7 +1033,9 @@ __device__ __forceinline__ void o2k_char(const C& c, int64_t i, uint32_t x0, boo
       // run (only the start bit reads this: a start inside the run before
       // its last character leaves FRESH either way)
       s = true;
-      if (k1 == OK_S) {
+      if (k1 == OK_S && ws_hint >= 0) {
+        s = ws_hint != 0;
+      } else if (k1 == OK_S) {
         for (int64_t q = c.next(i); q >= 0;) {
           const Ch x = c.at(q);
           if (x.cl != OK_S) break;
@@ -1533,9 +1557,29 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     auto lane_fn = [&](int k, bool need_g, Fn* f, uint32_t* g) {
       const int64_t i = base + 64 * k + lane;
       const int Li = PT_HALO + 64 * k + lane;
+      const uint32_t bb = sb[64 * k + lane + PT_PAD];
+      // ASCII whitespace, CR/LF and non-ASCII bytes across the word (bytes
+      // past the text are staged as 0): a whitespace character after a
+      // CR/LF reads whether another CR/LF follows in its run from them
+      int ws_hint = -1;
+      if (need_g) {
+        const uint64_t mWS = __ballot(bb == ' ' || bb == '\t' || bb == 0x0B || bb == 0x0C);
+        const uint64_t mCR = __ballot(bb == '\n' || bb == '\r');
+        const uint64_t mHI = __ballot(bb >= 0x80);
+        const uint64_t above = ~mask_le(lane);
+        const uint64_t stop = ~(mWS | mCR) & above;
+        const int fs = stop ? __builtin_ctzll(stop) : 64;
+        const uint64_t dmw = D ? sdm[(base >> 6) + k - wlo] & above : 0;
+        const int fd = dmw ? __builtin_ctzll(dmw) : 64;
+        const int gc = (mCR & above) ? __builtin_ctzll(mCR & above) : 64;
+        const int end = fd < fs ? fd : fs;  // the run's end, as far as the masks go
+        if (gc < end) ws_hint = 0;
+        else if (fd <= fs && fd < 64) ws_hint = 1;
+        else if (fs < 64 && !((mHI >> fs) & 1)) ws_hint = 1;
+      }
       *f = o2_ident<W>();
       *g = 0;
-      if (i < 0 || i >= nb || is_cont(sb[64 * k + lane + PT_PAD])) return;
+      if (i < 0 || i >= nb || is_cont((uint8_t)bb)) return;
       const uint32_t e = se[Li];
       const int kc = dcl(e);
       const bool d0 = ds(Li);
@@ -1570,7 +1614,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
           h1 = true;
         }
       }
-      o2k_char<RS>(c, i, e, d0, xp, hp, x1, h1, need_g, contr, f, g);
+      o2k_char<RS>(c, i, e, d0, xp, hp, x1, h1, need_g, contr, ws_hint, f, g);
       if (RS == RS_O200K && need_g && kc == OK_N && !d0) {
         // \p{N}{1,K}: the N characters of the run before i decide
         bool r = true;
@@ -1589,28 +1633,12 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         *g = r ? ALL : 0u;
       }
     };
-    // inclusive composition over the lanes (lane 0 first): windows of four
-    // when every window from lane 4 on is constant (then each is the state
-    // after its lane whatever came before), else the whole prefix
-    auto scan = [&](Fn F) {
-      Fn o = o2_shfl_up(F, 1);
-      if (lane >= 1) F = o2_then(o, F);
-      o = o2_shfl_up(F, 2);
-      if (lane >= 2) F = o2_then(o, F);
-      if (__any(lane >= 4 && !o2_const<RS>(F))) {
-        for (int d = 4; d < 64; d <<= 1) {
-          o = o2_shfl_up(F, d);
-          if (lane >= d) F = o2_then(o, F);
-        }
-      }
-      return F;
-    };
     // the function of word k (lane 63's composition), wave-uniform
     auto word_fn = [&](int k) {
       Fn f;
       uint32_t g;
       lane_fn(k, false, &f, &g);
-      return o2_shfl(scan(f), 63);
+      return o2_lane63(o2_scan(f));
     };
     // word k from entry state `carry`: its start word; returns the state
     // after it
@@ -1623,9 +1651,10 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       Fn f;
       uint32_t g;
       lane_fn(k, true, &f, &g);
-      const uint32_t sj = o2_at(scan(f), carry);  // the state after the lane
-      uint32_t sp = __shfl_up(sj, 1);
-      if (lane == 0) sp = carry;
+      const uint32_t sj = o2_at(o2_scan(f), carry);  // the state after the lane
+      // the state before it: the lane before's (wave_shr:1), carry at lane 0
+      const uint32_t sp = (uint32_t)__builtin_amdgcn_update_dpp((int)carry, (int)sj, 0x138,
+                                                                0xF, 0xF, false);
       const int64_t i = base + 64 * k + lane;
       const int Li = PT_HALO + 64 * k + lane;
       const uint32_t bb = sb[64 * k + lane + PT_PAD];
@@ -1651,7 +1680,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         sw[k] = m;
         if (k < PT_TILE / 64) w.starts[wd] = m;
       }
-      return (uint32_t)__shfl((int)sj, 63);
+      return (uint32_t)__builtin_amdgcn_readlane((int)sj, 63);
     };
     const int k0 = WPB * wv;
     // the word before the block (the tile's halo word for wave 0); the
