@@ -212,6 +212,18 @@ int tk_engine_encode_seed(tk_engine* engine, const void* d_text,
                           size_t points_cap, size_t* n_ids, size_t* n_points,
                           void* stream);
 
+/* tk_engine_encode_seed with host buffers: the text is read from host
+ * memory through the engine's pinned staging, the ids and the checkpoints
+ * (three uint64 each, as above) are written to host memory; the device
+ * buffers are the engine's own. Replaces the same reference call as
+ * tk_engine_encode_seed, for hosts that keep the session store in host
+ * memory (crates/toktier-store-core/src/tail.rs:173-205). */
+int tk_engine_encode_seed_host(tk_engine* engine, const uint8_t* text,
+                               size_t nbytes, uint32_t flags, uint32_t* ids,
+                               size_t ids_cap, uint32_t stride,
+                               uint64_t* points, size_t points_cap,
+                               size_t* n_ids, size_t* n_points);
+
 /* Added tokens of the artifact (tokenizer.json "added_tokens", in artifact
  * order): literal k is contents[offsets[k] .. offsets[k+1]) (UTF-8, 1..255
  * bytes, all distinct), its id ids[k], its flags flags[k] (TK_ADDED_*).
@@ -271,6 +283,17 @@ int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
  * TK_E_INVALID_ARG for an unknown option or value. */
 #define TK_OPT_COMPACT_PAIRS 1
 int tk_engine_set_option(tk_engine* engine, int option, int64_t value);
+
+/* Test-only fault injection (no counterpart in the reference; the hook its
+ * tests drive with a stand-in encoder, gpu.rs:1828-1854, made a property
+ * of the engine so the error contract can be driven through the real
+ * path): while a marker is set (len > 0; len 0 clears it), a call of
+ * tk_engine_encode, tk_engine_encode_batch or tk_engine_encode_seed_host
+ * whose input holds the marker bytes runs its pipeline, then fails as a
+ * whole with TK_E_INTERNAL and writes no ids (a batch fails when any of
+ * its documents holds it, as a device guard trip fails the batch). */
+int tk_engine_set_fault_marker(tk_engine* engine, const uint8_t* marker,
+                               size_t len);
 
 /* Thread-local description of the last failure on this thread. */
 const char* tk_last_error(void);

@@ -614,3 +614,42 @@ def test_long_whitespace_and_periodic_pieces(name):
     t.encode(s)
     dt = time.perf_counter() - t0
     assert dt < 0.05, (name, dt)
+
+
+def test_injected_fault_isolates_rows_and_writes_no_ids():
+    """The error contract through the real path: with a fault marker set,
+    a call whose input holds it fails as a whole after its pipeline ran;
+    a batch is resolved by halving, so exactly the poisoned rows fail and
+    every other row keeps the oracle's ids; a single call raises and no
+    ids are returned."""
+    import toktier_amd
+    from toktier_amd import _ffi, workloads
+    k, t = kit("qwen3_8b"), tok("qwen3_8b")
+    base = workloads.config2(k.json, n_chars=40_000, sample=6)
+    docs = [base[i * 300:(i + 1) * 300] for i in range(100)]
+    poison = {3, 50, 51, 99}
+    for d in poison:
+        docs[d] = docs[d][:100] + "⁣POISON⁣" + docs[d][100:]
+    try:
+        t.engine.set_fault_marker("⁣POISON⁣".encode())
+        with pytest.raises(toktier_amd.BatchError) as err:
+            t.encode_batch(docs)
+        assert sorted(err.value.rows) == sorted(poison)
+        assert all(e.status == _ffi.TK_E_INTERNAL for e in err.value.errors)
+        rows = t.encode_batch(docs, errors="return")
+        for d, r in enumerate(rows):
+            if d in poison:
+                assert isinstance(r, _ffi.EngineError)
+            else:
+                assert np.array_equal(r.array, k.oracle.encode_bytes(docs[d].encode())), d
+        with pytest.raises(_ffi.EngineError) as e1:
+            t.engine.encode(docs[3].encode())
+        assert e1.value.status == _ffi.TK_E_INTERNAL
+        with pytest.raises(_ffi.EngineError):
+            t.seed(docs[50])
+        # clean inputs are untouched by the marker
+        assert np.array_equal(t.encode(docs[0]).array,
+                              k.oracle.encode_bytes(docs[0].encode()))
+    finally:
+        t.engine.set_fault_marker(b"")
+    assert np.array_equal(t.encode(docs[3]).array, k.oracle.encode_bytes(docs[3].encode()))

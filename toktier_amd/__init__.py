@@ -32,8 +32,58 @@ from ._ffi import (TK_ABI_VERSION, TK_ADDED_LSTRIP, TK_ADDED_NORMALIZED,
                    TK_E_NEEDS_NFC, TK_FLAG_NO_ADDED, TK_FLAG_NORMALIZED,
                    Engine, EngineError, TkConfig)
 
-__all__ = ["load", "Tokenizer", "Encoding", "EngineError", "families"]
+__all__ = ["load", "Tokenizer", "Encoding", "EngineError", "BatchError",
+           "resolve_failed_chunk", "families"]
 __version__ = "0.1.0"
+
+
+class BatchError(RuntimeError):
+    """Rows of a batch that failed on their own: ``rows`` their indices,
+    ``errors`` the ``EngineError`` of each."""
+
+    def __init__(self, rows: list[int], errors: list):
+        self.rows = rows
+        self.errors = errors
+        super().__init__(f"{len(rows)} row(s) failed: {rows[:8]}"
+                         + (f"; first: {errors[0]}" if errors else ""))
+
+
+def resolve_failed_chunk(encode_chunk, indices: list[int], error) -> list:
+    """Rows of a chunk whose batched attempt failed as a whole, found by
+    halving (``crates/toktier-routing-core/src/gpu.rs:1567-1639``): a half
+    that succeeds is adopted whole and never split again, a half that still
+    fails is divided, and a half of one document is that row's attempt, so
+    its error is the row's. ``encode_chunk(indices)`` returns one entry per
+    index or raises; ``error`` is the failure of the whole chunk. Returns
+    the rows in order (an entry per index, the error for the rows that
+    fail alone). A document's ids do not depend on the other documents of
+    its batch, so the ids are those of encoding each document alone."""
+    out: list = [None] * len(indices)
+    if len(indices) <= 1:
+        if indices:
+            out[0] = error
+        return out
+    mid = len(indices) // 2
+    pending = [(mid, len(indices)), (0, mid)]  # popped from the end: left first
+    while pending:
+        lo, hi = pending.pop()
+        try:
+            rows = encode_chunk(indices[lo:hi])
+        except Exception as err:  # noqa: BLE001 -- the chunk's own failure
+            if hi - lo <= 1:
+                out[lo] = err
+            else:
+                m = lo + (hi - lo) // 2
+                pending.append((m, hi))
+                pending.append((lo, m))
+            continue
+        if len(rows) != hi - lo:
+            bad = RuntimeError("batch returned the wrong row count")
+            for k in range(lo, hi):
+                out[k] = bad
+            continue
+        out[lo:hi] = rows
+    return out
 
 
 @dataclass(frozen=True)
@@ -281,21 +331,12 @@ class Tokenizer:
     def seed(self, text: str, stride: int = SPAN_CHECKPOINT_STRIDE) -> "Seed":
         """Ids plus the sparse span checkpoints the session store adopts
         (``crates/toktier-store-core/src/tail.rs:173-205``), computed on the
-        device with the bytes resident in HBM. A text that fails the NFC
+        device (``tk_engine_encode_seed_host``: host buffers in, engine-owned
+        device buffers, host ids and checkpoints out). A text that fails the NFC
         quick check raises (``TK_E_NEEDS_NFC``): the store seeds the
         normalized text it holds."""
-        import torch
         data = text.encode("utf-8")
-        dev = torch.device("cuda", self.engine.device)
-        n_pts_cap = max(1, len(data) // max(1, stride) + 1)
-        d_text = torch.frombuffer(bytearray(data or b"\0"), dtype=torch.uint8).to(dev)
-        d_ids = torch.empty(max(1, len(data)), dtype=torch.int32, device=dev)
-        d_pts = torch.empty(3 * n_pts_cap, dtype=torch.int64, device=dev)
-        n, m = self.engine.encode_seed(d_text.data_ptr(), len(data),
-                                       d_ids.data_ptr(), d_ids.numel(), stride,
-                                       d_pts.data_ptr(), n_pts_cap)
-        ids = d_ids[:n].cpu().numpy().view(np.uint32).copy()
-        pts = d_pts[:3 * m].cpu().numpy().view(np.uint64).reshape(m, 3).copy()
+        ids, pts = self.engine.encode_seed_host(data, stride)
         with self._lock:
             c = self._counters
             c.executions += 1
@@ -305,26 +346,53 @@ class Tokenizer:
             c.last_stats = self.engine.last_stats()
         return Seed(ids, pts, stride)
 
-    def encode_batch(self, texts: list[str]) -> list[Encoding]:
+    def encode_batch(self, texts: list[str], errors: str = "raise"
+                     ) -> list[Encoding]:
         """Row ``i`` equals ``encode(texts[i])``
-        (``docs/contracts/api.md:106`` in the reference)."""
+        (``docs/contracts/api.md:106`` in the reference). A row whose text
+        fails on its own (invalid UTF-8) is that row's error; a batch that
+        fails as a whole (a device guard, an injected fault) is resolved by
+        halving (``resolve_failed_chunk``), so only the documents that fail
+        alone end in an error and the others keep their ids. Rows that end
+        in an error raise ``BatchError`` (``errors="raise"``, naming every
+        failed row; no ids are returned), or stand as ``EngineError``
+        entries in the returned list (``errors="return"``)."""
         docs = [t.encode("utf-8") for t in texts]
-        ids, rows, status = self.engine.encode_batch(docs)
-        out: list[Encoding | None] = [None] * len(docs)
-        redo = []
-        for d in range(len(docs)):
-            if status[d] == 0:
-                out[d] = Encoding(ids[int(rows[d]):int(rows[d + 1])].copy())
-            elif status[d] == TK_E_NEEDS_NFC:
-                redo.append(d)
-            else:
-                raise EngineError(int(status[d]), "tk_engine_encode_batch",
-                                  f"row {d} failed")
+        out: list = [None] * len(docs)
+        redo: list[int] = []
+
+        def chunk(idx: list[int]) -> list:
+            ids, rows, status = self.engine.encode_batch([docs[d] for d in idx])
+            res = []
+            for j, d in enumerate(idx):
+                if status[j] == 0:
+                    res.append(Encoding(ids[int(rows[j]):int(rows[j + 1])].copy()))
+                elif status[j] == TK_E_NEEDS_NFC:
+                    redo.append(d)
+                    res.append(None)
+                else:
+                    res.append(EngineError(int(status[j]), "tk_engine_encode_batch",
+                                           f"row {d} failed"))
+            return res
+
+        idx = list(range(len(docs)))
+        try:
+            rows = chunk(idx)
+        except EngineError as err:
+            rows = resolve_failed_chunk(chunk, idx, err)
+        for d, r in zip(idx, rows):
+            out[d] = r
         for d in redo:
-            out[d] = Encoding(self._encode_normalized(texts[d]))
+            try:
+                out[d] = Encoding(self._encode_normalized(texts[d]))
+            except EngineError as err:
+                out[d] = err
         with self._lock:
             self._counters.executions += 1
-        return out  # type: ignore[return-value]
+        failed = [d for d, r in enumerate(out) if isinstance(r, EngineError)]
+        if failed and errors == "raise":
+            raise BatchError(failed, [out[d] for d in failed])
+        return out
 
     def explain(self) -> dict:
         """Route and execution report (reference ``explain()`` fields that

@@ -54,9 +54,11 @@ SYMBOLS = (
     "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
     "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
     "tk_engine_encode_device_noalloc", "tk_engine_encode_seed",
+    "tk_engine_encode_seed_host",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
     "tk_engine_last_timing", "tk_engine_set_added",
     "tk_engine_last_literals", "tk_engine_last_stats", "tk_engine_set_option",
+    "tk_engine_set_fault_marker",
     "tk_engine_driver_version", "tk_last_error",
 )
 
@@ -123,6 +125,11 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_encode_seed.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
                                         C.c_uint32, vp, sz, C.POINTER(sz),
                                         C.POINTER(sz), vp]
+    L.tk_engine_encode_seed_host.restype = C.c_int
+    L.tk_engine_encode_seed_host.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
+                                             C.c_uint32, vp, sz,
+                                             C.POINTER(C.c_size_t),
+                                             C.POINTER(C.c_size_t)]
     L.tk_engine_delivery.restype = C.c_char_p
     L.tk_engine_delivery.argtypes = [vp]
     L.tk_engine_architecture.restype = C.c_char_p
@@ -139,6 +146,8 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_last_literals.argtypes = [vp, C.POINTER(C.c_uint64)]
     L.tk_engine_set_option.restype = C.c_int
     L.tk_engine_set_option.argtypes = [vp, C.c_int, C.c_int64]
+    L.tk_engine_set_fault_marker.restype = C.c_int
+    L.tk_engine_set_fault_marker.argtypes = [vp, vp, sz]
     L.tk_engine_last_stats.restype = C.c_int
     L.tk_engine_last_stats.argtypes = [vp, C.POINTER(C.c_uint64), C.c_int]
     if path is None:
@@ -263,6 +272,23 @@ class Engine:
         check(st, "tk_engine_encode_seed")
         return n.value, m.value
 
+    def encode_seed_host(self, data: bytes, stride: int, flags: int = 0
+                         ) -> tuple[np.ndarray, np.ndarray]:
+        """Host-buffer encode plus span checkpoints: (ids uint32, points
+        uint64 of shape (n, 3))."""
+        nb = len(data)
+        ids = np.empty(max(1, nb), dtype=np.uint32)
+        cap = max(1, nb // max(1, stride) + 1)
+        pts = np.empty(3 * cap, dtype=np.uint64)
+        n = C.c_size_t()
+        m = C.c_size_t()
+        st = self._L.tk_engine_encode_seed_host(self._h, data, nb, flags,
+                                                ids.ctypes.data, ids.size, stride,
+                                                pts.ctypes.data, cap,
+                                                C.byref(n), C.byref(m))
+        check(st, "tk_engine_encode_seed_host")
+        return ids[:n.value].copy(), pts[:3 * m.value].reshape(m.value, 3).copy()
+
     def set_added(self, contents: list[bytes], ids: list[int],
                   flags: list[int]) -> None:
         """Install the artifact's added tokens (``TK_ADDED_*`` flags); an
@@ -297,6 +323,13 @@ class Engine:
         default when the artifact fits it), 0 the boundary-format table."""
         check(self._L.tk_engine_set_option(self._h, int(option), int(value)),
               "tk_engine_set_option")
+
+    def set_fault_marker(self, marker: bytes) -> None:
+        """Test-only: while set, a host-buffer call whose input holds
+        ``marker`` fails as a whole (``TK_E_INTERNAL``) after its pipeline
+        ran, writing no ids; ``b""`` clears it."""
+        check(self._L.tk_engine_set_fault_marker(self._h, marker or None, len(marker)),
+              "tk_engine_set_fault_marker")
 
     def last_stats(self) -> dict[str, int]:
         """Facts of the last encode: literals extracted, pieces over 64

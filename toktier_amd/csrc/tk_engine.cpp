@@ -266,6 +266,10 @@ struct tk_engine {
   Workspace ws;
   DevBuf<uint64_t> docoffs, rows;
   DevBuf<uint32_t> seedc;  // per-block character counts (session seed)
+  DevBuf<uint64_t> seedp;  // span checkpoints of the host-buffer seed
+  // test-only: a host-buffer call whose input holds these bytes fails as a
+  // whole after its pipeline ran (tk_engine_set_fault_marker)
+  std::string fault_marker;
   DevBuf<uint32_t> unsafe;
   // added-token literals (tk_engine_set_added)
   DevBuf<uint64_t> lit_tab;
@@ -1233,6 +1237,13 @@ int tk_engine_set_option(tk_engine* e, int option, int64_t value) {
   return fail(TK_E_INVALID_ARG, "unknown option %d", option);
 }
 
+int tk_engine_set_fault_marker(tk_engine* e, const uint8_t* marker, size_t len) {
+  if (!e || (len && !marker)) return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  e->fault_marker.assign(reinterpret_cast<const char*>(marker), len);
+  return TK_OK;
+}
+
 int tk_engine_last_stats(const tk_engine* e, uint64_t* out, int n) {
   if (!e || !out) return fail(TK_E_INVALID_ARG, "null argument");
   const uint64_t v[4] = {e->last_literals, e->last_nlong, e->last_big,
@@ -1370,6 +1381,72 @@ int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
   return TK_OK;
 }
 
+namespace {
+// the injected fault of a host-buffer call (tk_engine_set_fault_marker)
+bool injected_fault(const tk_engine* e, const uint8_t* data, size_t n) {
+  const std::string& m = e->fault_marker;
+  if (m.empty() || n < m.size()) return false;
+  const uint8_t* end = data + n;
+  return std::search(data, end, m.begin(), m.end(),
+                     [](uint8_t a, char b) { return a == (uint8_t)b; }) != end;
+}
+
+}  // namespace
+
+int tk_engine_encode_seed_host(tk_engine* e, const uint8_t* text, size_t nbytes,
+                               uint32_t flags, uint32_t* ids, size_t ids_cap,
+                               uint32_t stride, uint64_t* points,
+                               size_t points_cap, size_t* n_ids,
+                               size_t* n_points) {
+  if (!e || !n_ids || !n_points || (nbytes && (!text || !ids)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  if (stride == 0) return fail(TK_E_INVALID_ARG, "stride must be positive");
+  std::lock_guard<std::mutex> lk(e->mu);
+  *n_ids = 0;
+  *n_points = 0;
+  if (nbytes == 0) return TK_OK;
+  HIP_TRY(hipSetDevice(e->device));
+  int rc = ensure_workspace(e, nbytes, 0);
+  if (rc != TK_OK) return rc;
+  hipStream_t s = e->stream;
+  if ((rc = stage_in(e, e->ws.text, text, nbytes, s)) != TK_OK) return rc;
+  const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
+  uint32_t st, total;
+  tk::DevAdded docs;
+  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, e->ws.out,
+                    e->ws.out_n, &st, &total, doc_pass(e, flags, &docs));
+  if (rc != TK_OK) return rc;
+  if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
+  if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
+  if (total > ids_cap)
+    return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  if (injected_fault(e, text, nbytes)) return fail(TK_E_INTERNAL, "injected fault");
+  const size_t n = total ? (total + stride - 1) / stride : 0;
+  if (n > points_cap || (n && !points))
+    return fail(TK_E_CAPACITY, "%zu checkpoints exceed the %zu-entry buffer", n,
+                points_cap);
+  if (n) {
+    // the checkpoints into engine-owned device memory, behind the ids
+    const size_t nblk = (nbytes + tk::COMPACT_BLOCK - 1) / tk::COMPACT_BLOCK;
+    if (e->seedc.n < nblk) HIP_TRY(e->seedc.alloc(nblk));
+    if (e->seedp.n < 3 * n) HIP_TRY(e->seedp.alloc(3 * n));
+    tk::DevWork w{};
+    w.tok = e->ws.tok;
+    w.blkprefix = e->ws.blkprefix;
+    HIP_TRY(tk::launch_seed(w, e->ws.text, (int64_t)nbytes, (uint32_t)n, stride,
+                            e->seedc.p, e->seedp.p, s));
+  }
+  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
+  if (n) {
+    HIP_TRY(hipMemcpyAsync(points, e->seedp.p, 3 * n * sizeof(uint64_t),
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+  }
+  *n_ids = total;
+  *n_points = n;
+  return TK_OK;
+}
+
 int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
                      uint32_t flags, uint32_t* ids, size_t ids_cap,
                      size_t* n_ids) {
@@ -1396,6 +1473,7 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  if (injected_fault(e, text, nbytes)) return fail(TK_E_INTERNAL, "injected fault");
   if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
   const auto h3 = clk::now();
   auto us = [](clk::duration d) {
@@ -1449,6 +1527,13 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
                                   check, e->ws.out, e->ws.out_n, false);
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
+  // a batch holding a poisoned document fails as a whole, as a device
+  // guard trip would
+  for (size_t d = 0; d < n_docs && !e->fault_marker.empty(); ++d)
+    if (injected_fault(e, joined + doc_offsets[d], doc_offsets[d + 1] - doc_offsets[d])) {
+      HIP_TRY(hipStreamSynchronize(s));
+      return fail(TK_E_INTERNAL, "injected fault (document %zu)", d);
+    }
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
   if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
   if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
