@@ -149,9 +149,16 @@ int tk_engine_open(const tk_config* cfg,
 void tk_engine_close(tk_engine* engine);
 
 /* One request: host UTF-8 in, host ids out. ids_cap >= nbytes always
- * suffices (a token covers at least one byte). Pageable buffers go through
- * the engine's pinned staging (copy threads pipelined with the transfers);
- * pinned host buffers (hipHostMalloc) are transferred directly. */
+ * suffices (a token covers at least one byte). Pageable request bytes are
+ * copied into the engine's pinned staging by its copy threads and sent in
+ * one transfer; page-locked ones (hipHostMalloc) are sent directly. The
+ * compaction kernel writes the ids straight into a page-locked, 4-byte
+ * aligned ids buffer (the serving configuration: no transfer command, no
+ * host copy), or into the engine's pinned staging, from which the copy
+ * threads fill a pageable one. After a failure (*n_ids == 0) the first
+ * ids_cap entries of a page-locked ids buffer hold no defined values; a
+ * pageable one is left as it was. The same holds for the batch and the
+ * host-buffer seed entries. */
 int tk_engine_encode(tk_engine* engine, const uint8_t* text, size_t nbytes,
                      uint32_t flags, uint32_t* ids, size_t ids_cap,
                      size_t* n_ids);

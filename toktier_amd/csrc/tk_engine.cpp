@@ -183,18 +183,18 @@ struct Workspace {
   uint64_t* nrun = nullptr;  // per k_pretok tile: the digit run, then two
                              // automaton words (o200k)
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
-  uint32_t *blkcount = nullptr, *blkprefix = nullptr, *out = nullptr;
+  uint32_t *blkcount = nullptr, *blkprefix = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
   uint32_t *pblk = nullptr, *plocal = nullptr;
   int32_t *nx = nullptr, *pv = nullptr;
-  size_t long_pairs = 0, seg_pairs = 0, out_n = 0, nblk = 0, tiles = 0;
+  size_t long_pairs = 0, seg_pairs = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
   uint32_t ctag = 0;
 };
 
 // Lays a workspace for `cap` input bytes out at `base` (each buffer
 // 256-byte aligned) and returns the bytes it spans; base == nullptr only
-// sizes it. About 84 bytes per input byte.
+// sizes it. About 80 bytes per input byte.
 size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   size_t at = 0;
   auto take = [&](auto*& p, size_t count) {
@@ -229,7 +229,6 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.blkcount, nblk);
   take(w.blkprefix, nblk);
   take(w.cstat, nblk);
-  take(w.out, cap);
   take(w.plist, (size_t)tk::pack_off((int64_t)cap, tk::PACK_CLASSES));
   take(w.pblk, (size_t)tk::PACK_CLASSES * tiles);
   take(w.plocal, (size_t)tk::PT_LOCAL_SLOTS * tiles);
@@ -241,7 +240,6 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   w.tiles = (size_t)tiles;
   w.long_pairs = long_cap;
   w.seg_pairs = seg_cap;
-  w.out_n = cap;
   w.nblk = nblk;
   return at;
 }
@@ -296,12 +294,10 @@ struct tk_engine {
   // their own, beside the 65..WIDE_MAX-byte merges of stream2
   hipStream_t stream3 = nullptr;
   hipEvent_t ev_join3 = nullptr;
-  // host-to-host entries: pinned staging of the request bytes and the ids,
-  // copy threads, and one event per chunk of ids coming back
+  // host-to-host entries: pinned staging of the request bytes and of the
+  // ids (written there by the compaction kernel), and the copy threads
   tk::PinnedBuf pin_in, pin_out;
   std::unique_ptr<tk::CopyPool> pool;
-  static constexpr int OUT_CHUNKS = 64;
-  hipEvent_t ev_out[OUT_CHUNKS] = {};
   double last_us[8] = {};
   size_t last_passes = 0;
   uint32_t last_nlong = 0, last_big = 0;
@@ -647,128 +643,89 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
 
 // ---- host <-> device through the pinned staging
 constexpr size_t STAGE_SMALL = (size_t)256 << 10;  // one copy, this thread
-constexpr size_t STAGE_IN_CHUNK = (size_t)512 << 10;
-constexpr size_t STAGE_OUT_CHUNK = (size_t)1 << 20;
+constexpr size_t STAGE_CHUNK = (size_t)64 << 10;   // one claim of the copy threads
 
 tk::CopyPool* copy_pool(tk_engine* e) {
   if (!e->pool) e->pool.reset(new tk::CopyPool(tk::copy_threads()));
   return e->pool.get();
 }
 
-// Waits for the copy threads' current job when it leaves scope (their
-// chunks refer to the caller's buffers and to flags on this stack).
-struct PoolJob {
-  tk::CopyPool* pool;
-  ~PoolJob() { pool->wait(); }
-};
-
-// Pinned (page-locked, device-visible) host memory, e.g. from hipHostMalloc:
-// transfers use it directly instead of going through the staging. A
-// pageable pointer makes the query fail (hipErrorInvalidValue); that error
-// is taken back at once so no later check reports it.
-bool host_pinned(const void* p) {
+// Page-locked (pinned, device-visible) host memory, e.g. from
+// hipHostMalloc: the device's address of p, or nullptr for pageable memory.
+// A pageable pointer makes the query fail (hipErrorInvalidValue); that
+// error is taken back at once so no later check reports it.
+uint8_t* pinned_dev(const void* p) {
   hipPointerAttribute_t a{};
   if (hipPointerGetAttributes(&a, p) != hipSuccess) {
     (void)hipGetLastError();
-    return false;
+    return nullptr;
   }
-  return a.type == hipMemoryTypeHost;
+  if (a.type != hipMemoryTypeHost || !a.devicePointer || !a.hostPointer) return nullptr;
+  return static_cast<uint8_t*>(a.devicePointer) +
+         (static_cast<const uint8_t*>(p) - static_cast<const uint8_t*>(a.hostPointer));
 }
 
-// n request bytes at src (host) into d_dst (device) on stream s: the copy
-// threads fill the pinned staging chunk by chunk, in order, and this thread
-// starts each chunk's transfer as soon as its copy is done.
+// the device's address of [p, p + bytes) when the whole range is
+// page-locked and mapped in one piece, else nullptr
+uint8_t* pinned_range(const void* p, size_t bytes) {
+  if (bytes == 0) return nullptr;
+  uint8_t* d0 = pinned_dev(p);
+  if (!d0) return nullptr;
+  uint8_t* d1 = pinned_dev(static_cast<const uint8_t*>(p) + bytes - 1);
+  return d1 && (size_t)(d1 - d0) == bytes - 1 ? d0 : nullptr;
+}
+
+// n bytes between host buffers by the copy threads and this thread
+void host_copy(tk_engine* e, uint8_t* dst, const uint8_t* src, size_t n) {
+  if (n <= STAGE_SMALL) {
+    std::memcpy(dst, src, n);
+    return;
+  }
+  copy_pool(e)->run((n + STAGE_CHUNK - 1) / STAGE_CHUNK, [&](size_t k) {
+    const size_t off = k * STAGE_CHUNK;
+    std::memcpy(dst + off, src + off, std::min(STAGE_CHUNK, n - off));
+  });
+}
+
+// n request bytes at src (host) into d_dst (device) on stream s: page-locked
+// bytes in one transfer; pageable ones copied into the pinned staging
+// first, then one transfer (the staging is free again once the call has
+// synchronized, as every host entry does before it returns).
 int stage_in(tk_engine* e, uint8_t* d_dst, const uint8_t* src, size_t n,
              hipStream_t s) {
-  if (host_pinned(src) && host_pinned(src + n - 1)) {
+  if (pinned_range(src, n)) {
     HIP_TRY(hipMemcpyAsync(d_dst, src, n, hipMemcpyHostToDevice, s));
     return TK_OK;
   }
   HIP_TRY(e->pin_in.ensure(std::max(n, e->ws.cap) + 64));
-  uint8_t* pin = e->pin_in.p;
-  if (n <= STAGE_SMALL) {
-    std::memcpy(pin, src, n);
-    HIP_TRY(hipMemcpyAsync(d_dst, pin, n, hipMemcpyHostToDevice, s));
-    return TK_OK;
-  }
-  const size_t ch = tk::chunk_bytes(n, STAGE_IN_CHUNK, tk_engine::OUT_CHUNKS);
-  const size_t nch = (n + ch - 1) / ch;
-  std::atomic<uint8_t> ready[tk_engine::OUT_CHUNKS];
-  for (auto& r : ready) r.store(0, std::memory_order_relaxed);
-  tk::CopyPool* pool = copy_pool(e);
-  pool->start(nch, [&](size_t k) {
-    const size_t off = k * ch, len = std::min(ch, n - off);
-    std::memcpy(pin + off, src + off, len);
-    ready[k].store(1, std::memory_order_release);
-  });
-  PoolJob job{pool};
-  for (size_t k = 0; k < nch; ++k) {
-    while (!ready[k].load(std::memory_order_acquire)) std::this_thread::yield();
-    const size_t off = k * ch, len = std::min(ch, n - off);
-    HIP_TRY(hipMemcpyAsync(d_dst + off, pin + off, len, hipMemcpyHostToDevice, s));
-  }
+  host_copy(e, e->pin_in.p, src, n);
+  HIP_TRY(hipMemcpyAsync(d_dst, e->pin_in.p, n, hipMemcpyHostToDevice, s));
   return TK_OK;
 }
 
-// n ids at d_src (device) into dst (host) on stream s, after the work
-// already on s: each chunk's transfer into the pinned staging records an
-// event, and the copy threads move a chunk on to dst once this thread has
-// seen its event.
-int stage_out(tk_engine* e, uint32_t* dst, const uint32_t* d_src, size_t n,
-              hipStream_t s) {
-  const size_t bytes = n * sizeof(uint32_t);
-  if (bytes == 0) return TK_OK;
-  if (host_pinned(dst) && host_pinned(reinterpret_cast<uint8_t*>(dst) + bytes - 1)) {
-    HIP_TRY(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipStreamSynchronize(s));
-    return TK_OK;
-  }
-  HIP_TRY(e->pin_out.ensure(std::max(bytes, e->ws.cap * sizeof(uint32_t)) + 64));
-  uint8_t* pin = e->pin_out.p;
-  const uint8_t* dsrc = reinterpret_cast<const uint8_t*>(d_src);
-  uint8_t* out = reinterpret_cast<uint8_t*>(dst);
-  if (bytes <= STAGE_SMALL) {
-    HIP_TRY(hipMemcpyAsync(pin, dsrc, bytes, hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipStreamSynchronize(s));
-    std::memcpy(out, pin, bytes);
-    return TK_OK;
-  }
-  const size_t ch = tk::chunk_bytes(bytes, STAGE_OUT_CHUNK, tk_engine::OUT_CHUNKS);
-  const size_t nch = (bytes + ch - 1) / ch;
-  for (size_t k = 0; k < nch; ++k) {
-    const size_t off = k * ch, len = std::min(ch, bytes - off);
-    HIP_TRY(hipMemcpyAsync(pin + off, dsrc + off, len, hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipEventRecord(e->ev_out[k], s));
-  }
-  std::atomic<uint8_t> ready[tk_engine::OUT_CHUNKS];
-  for (auto& r : ready) r.store(0, std::memory_order_relaxed);
-  std::atomic<uint8_t> abort{0};
-  tk::CopyPool* pool = copy_pool(e);
-  pool->start(nch, [&](size_t k) {
-    for (;;) {
-      if (ready[k].load(std::memory_order_acquire)) break;
-      if (abort.load(std::memory_order_acquire)) return;
-      std::this_thread::yield();
+// Where the compaction kernel writes a host call's ids: straight into the
+// caller's buffer when it is page-locked and 4-byte aligned (capacity
+// ids_cap), else into the pinned out staging (capacity ws.cap), which
+// ids_from_staging copies to the caller afterwards.
+struct HostOut {
+  uint32_t* dev = nullptr;  // the device's address of the target
+  size_t cap = 0;
+  bool staged = false;
+};
+int host_out(tk_engine* e, uint32_t* ids, size_t ids_cap, HostOut* o) {
+  if (ids_cap > 0 && ((uintptr_t)ids & 3) == 0) {
+    if (uint8_t* d = pinned_range(ids, ids_cap * sizeof(uint32_t))) {
+      *o = {reinterpret_cast<uint32_t*>(d), ids_cap, false};
+      return TK_OK;
     }
-    const size_t off = k * ch, len = std::min(ch, bytes - off);
-    std::memcpy(out + off, pin + off, len);
-  });
-  PoolJob job{pool};
-  // poll the chunks' events (a blocking wait can sleep for far longer than
-  // a chunk's transfer takes)
-  for (size_t k = 0; k < nch; ++k) {
-    for (;;) {
-      const hipError_t err = hipEventQuery(e->ev_out[k]);
-      if (err == hipSuccess) break;
-      if (err != hipErrorNotReady) {
-        abort.store(1, std::memory_order_release);
-        return fail(TK_E_DEVICE, "hipEventQuery failed: %s", hipGetErrorName(err));
-      }
-      std::this_thread::yield();
-    }
-    ready[k].store(1, std::memory_order_release);
   }
+  HIP_TRY(e->pin_out.ensure(e->ws.cap * sizeof(uint32_t) + 64));
+  *o = {reinterpret_cast<uint32_t*>(e->pin_out.dev), e->ws.cap, true};
   return TK_OK;
+}
+void ids_from_staging(tk_engine* e, const HostOut& o, uint32_t* ids, size_t n) {
+  if (o.staged && n)
+    host_copy(e, reinterpret_cast<uint8_t*>(ids), e->pin_out.p, n * sizeof(uint32_t));
 }
 
 // host-side checks used only on a batch whose device status flagged a
@@ -936,9 +893,6 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
-  for (auto& ev : e->ev_out)
-    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
-      return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
     if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
@@ -1068,8 +1022,6 @@ void tk_engine_close(tk_engine* e) {
   (void)hipSetDevice(e->device);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   for (auto& ev : e->ev)
-    if (ev) (void)hipEventDestroy(ev);
-  for (auto& ev : e->ev_out)
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream2) (void)hipStreamSynchronize(e->stream2);
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
@@ -1410,11 +1362,13 @@ int tk_engine_encode_seed_host(tk_engine* e, const uint8_t* text, size_t nbytes,
   if (rc != TK_OK) return rc;
   hipStream_t s = e->stream;
   if ((rc = stage_in(e, e->ws.text, text, nbytes, s)) != TK_OK) return rc;
+  HostOut o;
+  if ((rc = host_out(e, ids, ids_cap, &o)) != TK_OK) return rc;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
-  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, e->ws.out,
-                    e->ws.out_n, &st, &total, doc_pass(e, flags, &docs));
+  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, o.dev,
+                    o.cap, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
@@ -1436,12 +1390,11 @@ int tk_engine_encode_seed_host(tk_engine* e, const uint8_t* text, size_t nbytes,
     HIP_TRY(tk::launch_seed(w, e->ws.text, (int64_t)nbytes, (uint32_t)n, stride,
                             e->seedc.p, e->seedp.p, s));
   }
-  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
-  if (n) {
+  if (n)
     HIP_TRY(hipMemcpyAsync(points, e->seedp.p, 3 * n * sizeof(uint64_t),
                            hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipStreamSynchronize(s));
-  }
+  ids_from_staging(e, o, ids, total);
+  if (n) HIP_TRY(hipStreamSynchronize(s));
   *n_ids = total;
   *n_points = n;
   return TK_OK;
@@ -1462,19 +1415,21 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   using clk = std::chrono::steady_clock;
   const auto h0 = clk::now();
   if ((rc = stage_in(e, e->ws.text, text, nbytes, s)) != TK_OK) return rc;
+  HostOut o;
+  if ((rc = host_out(e, ids, ids_cap, &o)) != TK_OK) return rc;
   const auto h1 = clk::now();
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
-  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, e->ws.out,
-                    e->ws.out_n, &st, &total, doc_pass(e, flags, &docs));
+  rc = run_pipeline(e, e->ws, e->ws.text, nbytes, nullptr, check, s, o.dev,
+                    o.cap, &st, &total, doc_pass(e, flags, &docs));
   const auto h2 = clk::now();
   if (rc != TK_OK) return rc;
   if (st & tk::ST_UTF8) return fail(TK_E_UTF8, "input is not valid UTF-8");
   if (st & tk::ST_NFC) return fail(TK_E_NEEDS_NFC, "NFC quick check failed");
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   if (injected_fault(e, text, nbytes)) return fail(TK_E_INTERNAL, "injected fault");
-  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
+  ids_from_staging(e, o, ids, total);
   const auto h3 = clk::now();
   auto us = [](clk::duration d) {
     return std::chrono::duration<double, std::micro>(d).count();
@@ -1516,15 +1471,16 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   if ((rc = stage_in(e, e->ws.text, joined, nb, s)) != TK_OK) return rc;
   HIP_TRY(hipMemcpyAsync(e->ws.docmask, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
+  HostOut o;
+  if ((rc = host_out(e, ids, ids_cap, &o)) != TK_OK) return rc;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
   rc = run_pipeline(e, e->ws, e->ws.text, nb, e->ws.docmask, check, s,
-                    e->ws.out, e->ws.out_n, &st, &total,
-                    doc_pass(e, flags, &docs));
+                    o.dev, o.cap, &st, &total, doc_pass(e, flags, &docs));
   if (rc != TK_OK) return rc;
   const tk::DevWork w = make_work(e, e->ws, e->ws.text, nb, e->ws.docmask,
-                                  check, e->ws.out, e->ws.out_n, false);
+                                  check, o.dev, o.cap, false);
   HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   // a batch holding a poisoned document fails as a whole, as a device
@@ -1535,7 +1491,8 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
       return fail(TK_E_INTERNAL, "injected fault (document %zu)", d);
     }
   HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
-  if ((rc = stage_out(e, ids, e->ws.out, total, s)) != TK_OK) return rc;
+  ids_from_staging(e, o, ids, total);
+  HIP_TRY(hipStreamSynchronize(s));
   if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
     // find the rows that failed; their ids are dropped, the others stand
     std::vector<uint32_t> keep;
