@@ -443,9 +443,9 @@ def main() -> int:
 
     # the protocol window: host bytes in -> host ids out, into a reused
     # numpy id buffer as a serving loop keeps one: page-locked (the serving
-    # configuration: the ids are transferred straight into it), and plain
-    # pageable memory (through the engine's pinned staging); the request
-    # bytes are ordinary Python bytes either way
+    # configuration: the compaction kernel writes the ids straight into
+    # it), and plain pageable memory (through the engine's pinned staging);
+    # the request bytes are ordinary Python bytes either way
     out_pinned = torch.empty(cap + 1, dtype=torch.int32,
                              pin_memory=True).numpy().view(np.uint32)
     out_plain = np.zeros(cap + 1, dtype=np.uint32)  # pages touched once
@@ -524,9 +524,10 @@ def main() -> int:
             "mean_ms": round(host_ms, 4),
             "all_ms": [round(x, 3) for x in host_lat],
             "parts_us": {n: round(float(v), 1) for n, v in zip(
-                ["bytes in (pinned staging, copy threads, DMA)",
-                 "pipeline to final ids in device memory",
-                 "ids out (DMA, copy threads)"],
+                ["bytes in (copy threads into the pinned staging)",
+                 "pipeline (one DMA in, the kernels, ids written into the "
+                 "page-locked buffer by k_compact)",
+                 "ids out (copy threads; none for a page-locked buffer)"],
                 np.mean(np.asarray(host_parts), axis=0))},
             "mchars_per_s": round(chars / (host_ms * 1e-3) / 1e6, 2),
             "tokens_per_s": round(n_tok / (host_ms * 1e-3), 1),
@@ -534,7 +535,8 @@ def main() -> int:
             "meets_target_p99": bool(pct(host_lat, 99) <= TARGET_MS),
             "pageable_ids": {
                 "window": "the same, ids into a reused pageable numpy buffer "
-                          "(through the engine's pinned staging)",
+                          "(k_compact writes the engine's pinned staging, the "
+                          "copy threads fill the buffer from it)",
                 "latency_ms": pcts(plain_lat),
                 "mean_ms": round(float(np.mean(plain_lat)), 4),
                 "parts_us": {n: round(float(v), 1) for n, v in zip(
