@@ -2090,8 +2090,7 @@ __device__ __forceinline__ bool pair_find(const DevTables& t, uint32_t l,
 // words). Every byte has an id (the engine's all_bytes flag).
 template <int L>
 __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
-                         int64_t a, int n) {
-  const int lane = threadIdx.x & 63;
+                         int64_t a, int n, int lane) {
   uint32_t rk[L], md[L];
   uint32_t live = n > 0 ? (1u << n) - 1 : 0u;  // n <= 16
   bool done = n == 0;
@@ -2173,50 +2172,95 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 // b % PACK_XCDS), and each XCD has its own L2: so each class's units are
 // split into PACK_XCDS contiguous runs, run x (one stretch of the text) for
 // the blocks of XCD x, and an XCD reads the text, start words and lists of
-// its own stretch only. Inside an XCD the units go longest class first and
-// its wave g takes units g, g + G, g + 2G, ... (G waves per XCD), so every
-// wave gets a share of each class. Classes of up to PACK_LANE_MAX bytes: 64
-// pieces per unit, one per lane (lane_bpe); longer ones: 64 / slot pieces
-// per unit, a slot of lanes each (wave_bpe).
+// its own stretch only. Each run is cut again into PACK_RUNS sub-runs (the
+// r-th fraction of every class's units: about the r-th fraction of the
+// stretch), and an XCD goes sub-run by sub-run, longest class first inside
+// each: all the classes' pieces of one short stretch of text are merged
+// close together in time, so its token-slot lines are complete before L2
+// evicts them (one write-back each instead of one per class) and its text
+// lines are fetched once. Wave g of an XCD takes units g, g + G, g + 2G,
+// ... of that order (G waves per XCD), so every wave gets a share of each
+// class. Classes of up to PACK_LANE_MAX bytes: 64 pieces per unit, one per
+// lane (lane_bpe); longer ones: 64 / slot pieces per unit, a slot of lanes
+// each (wave_bpe).
 constexpr int PACK_XCDS = 8;
+constexpr int PACK_RUNS = 8;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
+  // the unit order of this block's XCD, built by wave 0: per class c,
+  // mc[c] = (its units in the XCD's run, its first unit in the class), then
+  // its piece count and geometry (slot | pieces per unit << 8 |
+  // pack_magic << 16 | lane flag); mr[r] = the XCD's units before
+  // sub-run r (every class). Kept in LDS, not registers: the merge paths
+  // need every register they can get.
+  __shared__ uint2 mc[16];
+  __shared__ uint2 mg2[16];
+  __shared__ uint32_t mr[PACK_RUNS + 1];
   const int lane = threadIdx.x & 63, wv = wave_id();
-  const int x = blockIdx.x % PACK_XCDS;
-  // lane q < PACK_CLASSES holds class q's run of units for this XCD (its
-  // first unit in the class, and the end of its units in the XCD's order,
-  // longest class first), piece count and geometry (slot | pieces per unit
-  // << 8 | pack_magic << 16 | lane flag); lane PACK_CLASSES holds a zero end
   const bool cl = lane < PACK_CLASSES;
-  const uint32_t ue = cl ? w.uend[lane] : 0u;
-  const uint32_t nu = ue - (uint32_t)__shfl_down((int)ue, 1);  // class units
-  const uint32_t s0_l = cl ? (uint32_t)(((uint64_t)nu * x) / PACK_XCDS) : 0u;
-  const uint32_t len = cl ? (uint32_t)(((uint64_t)nu * (x + 1)) / PACK_XCDS) - s0_l : 0u;
-  // ends in the XCD's order: a suffix sum over the classes
-  uint32_t ue_l = len;
+  if (wv == 0) {
+    const int x = blockIdx.x % PACK_XCDS;
+    const uint32_t ue = cl ? w.uend[lane] : 0u;
+    const uint32_t nu = ue - (uint32_t)__shfl_down((int)ue, 1);  // class units
+    const uint32_t s0 = cl ? (uint32_t)(((uint64_t)nu * x) / PACK_XCDS) : 0u;
+    const uint32_t len = cl ? (uint32_t)(((uint64_t)nu * (x + 1)) / PACK_XCDS) - s0 : 0u;
+    if (lane < 16) {
+      mc[lane] = make_uint2(len, s0);
+      mg2[lane] = make_uint2(cl ? w.pcount[lane] : 0u, cl ? PACK_GEO[lane] : 0u);
+    }
 #pragma unroll
-  for (int d = 1; d < 16; d <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_down((int)ue_l, d);
-    ue_l += lane + d < PACK_CLASSES ? o : 0u;
+    for (int r = 0; r <= PACK_RUNS; ++r) {
+      const uint32_t sr = (uint32_t)__builtin_amdgcn_readlane(
+          (int)wave_incl_scan((uint32_t)(((uint64_t)len * r) / PACK_RUNS), lane), 63);
+      if (lane == 0) mr[r] = sr;
+    }
   }
-  if (!cl) ue_l = 0u;
-  const uint32_t pc_l = cl ? w.pcount[lane] : 0u;
-  const uint32_t geo_l = cl ? PACK_GEO[lane] : 0u;
-  const uint32_t total = __builtin_amdgcn_readfirstlane(ue_l);
+  __syncthreads();
+  // (values read from LDS are wave-uniform here: readfirstlane keeps them
+  // in scalar registers)
+  const uint32_t total = __builtin_amdgcn_readfirstlane(mr[PACK_RUNS]);
   const uint32_t G = (gridDim.x / PACK_XCDS) * 4;
+  uint32_t r = 0, pbeg = 0;  // the current sub-run: [pbeg, pend)
+  uint32_t pend = __builtin_amdgcn_readfirstlane(mr[1]);
   for (uint32_t u0 = (blockIdx.x / PACK_XCDS) * 4 + wv; u0 < total; u0 += G) {
-    // the unit's class: the last class whose unit end lies past u0
-    const uint64_t inq = __ballot(cl && u0 < ue_l);
+    // The lane index, opaque to the compiler for each unit: without it the
+    // per-lane LDS addresses of the merge paths are hoisted out of this
+    // loop, and holding them across it spills registers to scratch (a few
+    // MB of scratch written back per launch).
+    int lane_u = lane;
+    asm volatile("" : "+v"(lane_u));
+    const bool cl_u = lane_u < PACK_CLASSES;
+    // the unit's sub-run r (a wave's units only go up) and its place v in it
+    while (u0 >= pend) {
+      ++r;
+      pbeg = pend;
+      pend = __builtin_amdgcn_readfirstlane(mr[r + 1]);
+    }
+    const uint32_t v = u0 - pbeg;
+    // the classes' units in sub-run r, ends in its order (a suffix sum
+    // over the classes, longest class first)
+    const uint2 m = cl_u ? mc[lane_u] : make_uint2(0u, 0u);
+    const uint32_t c0 = (uint32_t)(((uint64_t)m.x * r) / PACK_RUNS);
+    uint32_t ue_l = (uint32_t)(((uint64_t)m.x * (r + 1)) / PACK_RUNS) - c0;
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_down((int)ue_l, d);
+      ue_l += lane_u + d < PACK_CLASSES ? o : 0u;
+    }
+    if (!cl_u) ue_l = 0u;
+    // the unit's class: the last class whose unit end lies past v
+    const uint64_t inq = __ballot(cl_u && v < ue_l);
     const int c = 63 - __builtin_clzll(inq);
-    const uint32_t geo = __builtin_amdgcn_readlane(geo_l, c);
     const uint32_t ubeg = __builtin_amdgcn_readlane(ue_l, c + 1);
-    const uint32_t s0 = __builtin_amdgcn_readlane(s0_l, c);
-    const uint32_t cnt = __builtin_amdgcn_readlane(pc_l, c);
+    const uint32_t s0 = __builtin_amdgcn_readlane(m.y + c0, c);
+    const uint2 gc = mg2[c];
+    const uint32_t cnt = __builtin_amdgcn_readfirstlane(gc.x);
+    const uint32_t geo = __builtin_amdgcn_readfirstlane(gc.y);
     const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
-    const uint32_t first = (s0 + u0 - ubeg) * k;  // the unit's first piece
+    const uint32_t first = (s0 + v - ubeg) * k;  // the unit's first piece
     if ((geo & PACK_GEO_LANE) && t.all_bytes) {  // wave-uniform
-      const uint32_t idx = first + lane;
+      const uint32_t idx = first + lane_u;
       int64_t a = 0;
       int n = 0;
       if (idx < cnt) {
@@ -2224,15 +2268,15 @@ void k_bpe_pack(DevTables t, DevWork w) {
         n = (int)(piece_end(w, a) - a);
       }
       uint32_t* ls = lds[wv];
-      if (sl <= 4) lane_bpe<4>(t, w, ls, a, n);
-      else if (sl <= 8) lane_bpe<8>(t, w, ls, a, n);
-      else lane_bpe<16>(t, w, ls, a, n);
+      if (sl <= 4) lane_bpe<4>(t, w, ls, a, n, lane_u);
+      else if (sl <= 8) lane_bpe<8>(t, w, ls, a, n, lane_u);
+      else lane_bpe<16>(t, w, ls, a, n, lane_u);
       continue;
     }
     // slot-packed: 64 / slot pieces at a time (a lane-class unit without
     // the lane path takes several passes)
     const int per = 64 / sl;
-    const int slot = (lane * mg) >> 12, off = lane - slot * sl;
+    const int slot = (lane_u * mg) >> 12, off = lane_u - slot * sl;
     for (int j0 = 0; j0 < k; j0 += per) {
       const uint32_t idx = first + j0 + slot;
       int64_t a = 0, L = 0;
@@ -2241,8 +2285,8 @@ void k_bpe_pack(DevTables t, DevWork w) {
         L = piece_end(w, a) - a;
       }
       const bool elig = off < L;
-      const int ps = elig ? slot * sl : lane, pe = elig ? slot * sl + (int)L : lane + 1;
-      wave_bpe<true, false, true>(t, w, 0, a + off, lane, elig, ps, pe);
+      const int ps = elig ? slot * sl : lane_u, pe = elig ? slot * sl + (int)L : lane_u + 1;
+      wave_bpe<true, false, true>(t, w, 0, a + off, lane_u, elig, ps, pe);
     }
   }
 }
