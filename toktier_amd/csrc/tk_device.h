@@ -129,6 +129,7 @@ struct DevWork {
   uint32_t* uend;        // [PACK_CLASSES] end of each class's work units in
                          // k_bpe_pack's order, longest class first (ctrl)
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
+  uint32_t* pqueue;      // [PACK_XCDS * PACK_QSTRIDE] k_bpe_pack's counters
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
   // added-token literals (nullptr when the call extracts none): a literal
@@ -200,6 +201,11 @@ __host__ __device__ __forceinline__ uint32_t added_slot(uint32_t key,
 }
 // packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
 constexpr int PACK_BLOCKS = 2048;
+// k_bpe_pack's work: one run of every class per XCD (block b on XCD b %
+// PACK_XCDS), each XCD's later units handed out by a counter of its own
+// (pqueue[x * PACK_QSTRIDE], a line each)
+constexpr int PACK_XCDS = 8;
+constexpr int PACK_QSTRIDE = 64;
 // slots (lanes per piece) of the length classes, and the shortest piece of
 // each class: class c holds pieces of pack_lmin(c)..pack_slot(c) bytes
 __host__ __device__ constexpr int pack_slot(int c) {
@@ -207,17 +213,22 @@ __host__ __device__ constexpr int pack_slot(int c) {
        : c == 10 ? 21 : c == 11 ? 32 : 64;
 }
 // Classes of up to PACK_LANE_MAX bytes are merged one piece per lane (64
-// pieces per work unit, each merged serially by its lane); longer ones one
-// piece per slot of pack_slot(c) lanes (64 / slot pieces per unit, merged by
-// the lanes together).
+// pieces per work unit, each merged serially by its lane); classes of up to
+// PACK_GROUP_MAX bytes one piece per group of four lanes (16 pieces per unit,
+// 8 positions per lane); longer ones one piece per slot of pack_slot(c) lanes
+// (64 / slot pieces per unit, merged by the lanes together).
 constexpr int PACK_LANE_MAX = 16;
+constexpr int PACK_GROUP_MAX = 32;
 __host__ __device__ constexpr bool pack_lane(int c) {
   return pack_slot(c) <= PACK_LANE_MAX;
+}
+__host__ __device__ constexpr bool pack_group(int c) {
+  return !pack_lane(c) && pack_slot(c) <= PACK_GROUP_MAX;
 }
 // pieces per work unit, and a multiplier m with (lane * m) >> 12 == lane /
 // pack_slot(c) for every lane < 64
 __host__ __device__ constexpr int pack_per_unit(int c) {
-  return pack_lane(c) ? 64 : 64 / pack_slot(c);
+  return pack_lane(c) ? 64 : pack_group(c) ? 16 : 64 / pack_slot(c);
 }
 __host__ __device__ constexpr int pack_magic(int c) {
   return (4096 + pack_slot(c) - 1) / pack_slot(c);
@@ -264,6 +275,7 @@ hipError_t launch_pack_copy(const DevWork& w, hipStream_t s,
                             hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop);
+hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s);
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop, uint32_t nlong);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,

@@ -106,7 +106,12 @@ __device__ __forceinline__ bool ctab_find(const DevTables& t, uint32_t l,
   const uint32_t tag = __builtin_amdgcn_alignbit(hi, lo, t.cbits);
   const uint32_t b2 = pair_alt(b1, tag, t.cbits);
   const uint4* tab = reinterpret_cast<const uint4*>(t.ctab);
-  const uint4 u = tab[b1], v = tab[b2];
+  uint4 u = tab[b1], v = tab[b2];
+  // Every word of both buckets is taken here: left to itself the compiler
+  // loads the high words first and the low ones only once a tag matched,
+  // two dependent memory round trips instead of one.
+  asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w), "+v"(v.x),
+               "+v"(v.y), "+v"(v.z), "+v"(v.w));
   // a slot's high word >> 5 is tag << 1 | (second bucket)
   const uint32_t w0 = tag << 1, w1 = w0 | 1u;
   // (masks rather than selects: the slot words are picked with no branch,
@@ -2156,10 +2161,129 @@ __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
       w.tok[a + i] = ((live >> i) & 1) ? (lsym[i * 64 + lane] & SYM_ID) : INVALID_ID;
 }
 
+// One piece of up to 32 bytes per group of K = 32 / P lanes (lanes Kj ..
+// Kj + K - 1 hold the same piece, at a, n bytes; n == 0: none): the lane r =
+// lane % K of the group keeps positions g = rP + i (i < P), the pair
+// starting at each as a key rank << 5 | g and its product in registers, the
+// symbols in LDS at [i][lane]. Each step the group's lanes agree on the
+// piece's lowest key -- lowest rank, leftmost on ties, the HF order -- and
+// its product with log2(K) DPP exchanges inside the quad; the lane holding
+// the pair merges it, and the lanes holding the two changed pairs look them
+// up. Needs every byte to have an id and the compact pair table (ranks
+// below 2^19, so the keys fit 32 bits).
+constexpr int DPP_QUAD_SWAP1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int DPP_QUAD_SWAP2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+template <int ctrl>
+__device__ __forceinline__ uint32_t quad_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+}
+
+template <int P>
+__device__ __forceinline__ void group_bpe(const DevTables& t, const DevWork& w,
+                                          uint32_t* lsym, int64_t a, int n,
+                                          int lane) {
+  constexpr int K = 32 / P;
+  static_assert(K == 2 || K == 4, "a group is two or four lanes of a quad");
+  const int r = lane & (K - 1), g0 = P * r, lb = lane - r;
+  uint32_t rk[P], md[P];
+  uint32_t live = n >= 32 ? ~0u : (1u << n) - 1u;  // the piece's positions
+  bool done = n == 0;
+  if (t.ignore_merges) {
+    // whole-piece vocabulary hit first (pretok_kernel.cu:921-943 role), by
+    // the group's first lane
+    int32_t hit = -1;
+    if (!done && r == 0) hit = vocab_lookup(t, w.text + a, n);
+    hit = (int32_t)quad_dpp<K == 2 ? 0xA0 : 0x00>((uint32_t)hit);  // [0,0,2,2] / [0,0,0,0]
+    if (!done && hit >= 0) {
+      if (r == 0) lsym[lane] = (uint32_t)hit;
+      live = 1u;
+      done = true;
+    }
+  }
+  {
+    uint32_t by[P + 1];
+#pragma unroll
+    for (int i = 0; i < P + 1; ++i) {
+      by[i] = g0 + i < n ? w.text[a + g0 + i] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      rk[i] = RANK_INF;
+      md[i] = 0;
+      if (!done && g0 + i < n) lsym[i * 64 + lane] = (uint32_t)t.byte_id[by[i]];
+      if (!done && g0 + i + 1 < n) {
+        const uint64_t v = t.bytepair[(by[i] << 8) | by[i + 1]];
+        if (v != ~0ULL) {
+          rk[i] = (uint32_t)(v >> 32) << 5 | (uint32_t)(g0 + i);
+          md[i] = (uint32_t)v;
+        }
+      }
+    }
+  }
+  for (;;) {
+    // this lane's lowest key and its product, then the group's (keys are
+    // distinct: each holds its position)
+    uint32_t km = RANK_INF, mid = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      if (rk[i] < km) {
+        km = rk[i];
+        mid = md[i];
+      }
+    }
+    {
+      const uint32_t ko = quad_dpp<DPP_QUAD_SWAP1>(km), mo = quad_dpp<DPP_QUAD_SWAP1>(mid);
+      if (ko < km) { km = ko; mid = mo; }
+    }
+    if constexpr (K == 4) {
+      const uint32_t ko = quad_dpp<DPP_QUAD_SWAP2>(km), mo = quad_dpp<DPP_QUAD_SWAP2>(mid);
+      if (ko < km) { km = ko; mid = mo; }
+    }
+    if (km == RANK_INF) break;  // this group's piece is finished
+    const int bi = (int)(km & 31);
+    const bool own_b = bi / P == r;
+    // bi absorbs the next live position nb (bi <= 30); p and nn: its live
+    // neighbours after the merge
+    const int nb = __builtin_ctz(live & ~((2u << bi) - 1u));
+    const uint32_t after = live & ~((2u << nb) - 1u);  // (nb == 31: none)
+    const uint32_t before = live & ((1u << bi) - 1u);
+    const int nn = after ? __builtin_ctz(after) : -1;
+    const int p = before ? 31 - __builtin_clz(before) : -1;
+    live &= ~(1u << nb);
+    if (own_b) lsym[(bi % P) * 64 + lane] = mid;
+    uint32_t rp = RANK_INF, mp = 0, rb = RANK_INF, mb = 0, r_, m_;
+    if (p >= 0 && p / P == r &&
+        ctab_find(t, lsym[(p % P) * 64 + lane], mid, &r_, &m_)) {
+      rp = r_ << 5 | (uint32_t)p;
+      mp = m_;
+    }
+    if (nn >= 0 && own_b &&
+        ctab_find(t, mid, lsym[(nn % P) * 64 + lb + nn / P], &r_, &m_)) {
+      rb = r_ << 5 | (uint32_t)bi;
+      mb = m_;
+    }
+    // (positions relative to this lane's first)
+    const int pl = p - g0, bl = bi - g0, nl = nb - g0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      rk[i] = i == pl ? rp : i == bl ? rb : i == nl ? RANK_INF : rk[i];
+      md[i] = i == pl ? mp : i == bl ? mb : md[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    if (g0 + i < n)
+      w.tok[a + g0 + i] =
+          ((live >> (g0 + i)) & 1) ? (lsym[i * 64 + lane] & SYM_ID) : INVALID_ID;
+  }
+}
+
 constexpr uint32_t PACK_GEO_LANE = 1u << 31;  // one piece per lane
+constexpr uint32_t PACK_GEO_GROUP = 1u << 30;  // one piece per group of lanes
 constexpr uint32_t pack_geo(int c) {
   return (uint32_t)pack_slot(c) | (uint32_t)pack_per_unit(c) << 8 |
-         (uint32_t)pack_magic(c) << 16 | (pack_lane(c) ? PACK_GEO_LANE : 0u);
+         (uint32_t)pack_magic(c) << 16 | (pack_lane(c) ? PACK_GEO_LANE : 0u) |
+         (pack_group(c) ? PACK_GEO_GROUP : 0u);
 }
 __constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
     pack_geo(0), pack_geo(1), pack_geo(2), pack_geo(3), pack_geo(4),
@@ -2172,31 +2296,34 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 // b % PACK_XCDS), and each XCD has its own L2: so each class's units are
 // split into PACK_XCDS contiguous runs, run x (one stretch of the text) for
 // the blocks of XCD x, and an XCD reads the text, start words and lists of
-// its own stretch only. Each run is cut again into PACK_RUNS sub-runs (the
-// r-th fraction of every class's units: about the r-th fraction of the
-// stretch), and an XCD goes sub-run by sub-run, longest class first inside
-// each: all the classes' pieces of one short stretch of text are merged
-// close together in time, so its token-slot lines are complete before L2
-// evicts them (one write-back each instead of one per class) and its text
-// lines are fetched once. Wave g of an XCD takes units g, g + G, g + 2G,
-// ... of that order (G waves per XCD), so every wave gets a share of each
-// class. Classes of up to PACK_LANE_MAX bytes: 64 pieces per unit, one per
-// lane (lane_bpe); longer ones: 64 / slot pieces per unit, a slot of lanes
-// each (wave_bpe).
-constexpr int PACK_XCDS = 8;
-constexpr int PACK_RUNS = 8;
+// its own stretch only. An XCD's units go in one order, class by class,
+// longest merge chains first (PACK_ORDER: the 17..32-byte groups and the
+// 9..16-byte lanes, then the shorter lane classes; 33..64-byte pieces, one
+// per unit, among them by their measured length). Wave g of the XCD's G
+// waves takes unit g first; every later unit comes from the XCD's counter
+// (pqueue, set to G by k_pack_copy), one at a time as waves finish theirs.
+// The long units thus all start at once, and the SIMDs end on the short
+// ones, each SIMD busy until its share is done (with a fixed share per wave
+// a SIMD holding a few long units ran on alone, latency-bound, long after
+// the others). Classes of up to PACK_LANE_MAX bytes: 64 pieces per unit,
+// one per lane (lane_bpe); up to PACK_GROUP_MAX bytes: 16 pieces per unit,
+// four lanes each (group_bpe); longer ones: 64 / slot pieces per unit, a
+// slot of lanes each (wave_bpe).
+__constant__ int8_t PACK_ORDER[PACK_CLASSES] = {11, 9, 10, 8, 7, 6, 5, 12,
+                                                4, 3, 2, 1, 0};
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
-  // the unit order of this block's XCD, built by wave 0: per class c,
-  // mc[c] = (its units in the XCD's run, its first unit in the class), then
-  // its piece count and geometry (slot | pieces per unit << 8 |
-  // pack_magic << 16 | lane flag); mr[r] = the XCD's units before
-  // sub-run r (every class). Kept in LDS, not registers: the merge paths
-  // need every register they can get.
-  __shared__ uint2 mc[16];
+  // the unit order of this block's XCD, built by wave 0: mo[k] = (the first
+  // unit of the k-th class of the order, that class's first unit in its
+  // list for this XCD's run), mk[k] = the class; mg2[c] = class c's piece
+  // count and geometry (slot | pieces per unit << 8 | pack_magic << 16 |
+  // lane / group flags); mtot = the XCD's units. Kept in LDS, not registers:
+  // the merge paths need every register they can get.
+  __shared__ uint2 mo[16];
   __shared__ uint2 mg2[16];
-  __shared__ uint32_t mr[PACK_RUNS + 1];
+  __shared__ int32_t mk[16];
+  __shared__ uint32_t mtot;
   const int lane = threadIdx.x & 63, wv = wave_id();
   const bool cl = lane < PACK_CLASSES;
   if (wv == 0) {
@@ -2205,60 +2332,55 @@ void k_bpe_pack(DevTables t, DevWork w) {
     const uint32_t nu = ue - (uint32_t)__shfl_down((int)ue, 1);  // class units
     const uint32_t s0 = cl ? (uint32_t)(((uint64_t)nu * x) / PACK_XCDS) : 0u;
     const uint32_t len = cl ? (uint32_t)(((uint64_t)nu * (x + 1)) / PACK_XCDS) - s0 : 0u;
+    const int oc = cl ? PACK_ORDER[lane] : 0;
+    const uint32_t lk = cl ? (uint32_t)__shfl((int)len, oc) : 0u;
+    const uint32_t sk = (uint32_t)__shfl((int)s0, oc);
+    const uint32_t incl = wave_incl_scan(lk, lane);
     if (lane < 16) {
-      mc[lane] = make_uint2(len, s0);
+      mo[lane] = make_uint2(cl ? incl - lk : ~0u, sk);
+      mk[lane] = oc;
       mg2[lane] = make_uint2(cl ? w.pcount[lane] : 0u, cl ? PACK_GEO[lane] : 0u);
     }
-#pragma unroll
-    for (int r = 0; r <= PACK_RUNS; ++r) {
-      const uint32_t sr = (uint32_t)__builtin_amdgcn_readlane(
-          (int)wave_incl_scan((uint32_t)(((uint64_t)len * r) / PACK_RUNS), lane), 63);
-      if (lane == 0) mr[r] = sr;
-    }
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    if (lane == 0) mtot = tot;
   }
   __syncthreads();
   // (values read from LDS are wave-uniform here: readfirstlane keeps them
   // in scalar registers)
-  const uint32_t total = __builtin_amdgcn_readfirstlane(mr[PACK_RUNS]);
-  const uint32_t G = (gridDim.x / PACK_XCDS) * 4;
-  uint32_t r = 0, pbeg = 0;  // the current sub-run: [pbeg, pend)
-  uint32_t pend = __builtin_amdgcn_readfirstlane(mr[1]);
-  for (uint32_t u0 = (blockIdx.x / PACK_XCDS) * 4 + wv; u0 < total; u0 += G) {
+  const uint32_t total = __builtin_amdgcn_readfirstlane(mtot);
+  uint32_t* const queue = w.pqueue + (blockIdx.x % PACK_XCDS) * PACK_QSTRIDE;
+  uint32_t u0 = (blockIdx.x / PACK_XCDS) * 4 + wv;  // the first unit
+  for (bool first_unit = true;; first_unit = false) {
+    if (!first_unit) {
+      // the next unit of the XCD's order (a vector atomic by lane 0)
+      uint32_t got = 0;
+      if (lane == 0)
+        got = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+      u0 = __builtin_amdgcn_readfirstlane(got);
+    }
+    if (u0 >= total) break;  // every wave leaves once the units are taken
     // The lane index, opaque to the compiler for each unit: without it the
     // per-lane LDS addresses of the merge paths are hoisted out of this
     // loop, and holding them across it spills registers to scratch (a few
     // MB of scratch written back per launch).
     int lane_u = lane;
     asm volatile("" : "+v"(lane_u));
-    const bool cl_u = lane_u < PACK_CLASSES;
-    // the unit's sub-run r (a wave's units only go up) and its place v in it
-    while (u0 >= pend) {
-      ++r;
-      pbeg = pend;
-      pend = __builtin_amdgcn_readfirstlane(mr[r + 1]);
-    }
-    const uint32_t v = u0 - pbeg;
-    // the classes' units in sub-run r, ends in its order (a suffix sum
-    // over the classes, longest class first)
-    const uint2 m = cl_u ? mc[lane_u] : make_uint2(0u, 0u);
-    const uint32_t c0 = (uint32_t)(((uint64_t)m.x * r) / PACK_RUNS);
-    uint32_t ue_l = (uint32_t)(((uint64_t)m.x * (r + 1)) / PACK_RUNS) - c0;
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-      const uint32_t o = (uint32_t)__shfl_down((int)ue_l, d);
-      ue_l += lane_u + d < PACK_CLASSES ? o : 0u;
-    }
-    if (!cl_u) ue_l = 0u;
-    // the unit's class: the last class whose unit end lies past v
-    const uint64_t inq = __ballot(cl_u && v < ue_l);
-    const int c = 63 - __builtin_clzll(inq);
-    const uint32_t ubeg = __builtin_amdgcn_readlane(ue_l, c + 1);
-    const uint32_t s0 = __builtin_amdgcn_readlane(m.y + c0, c);
+    // the unit's place in the order: the last class whose first unit is at
+    // or before u0 (a class without units shares the next one's first unit)
+    const uint2 m = lane_u < PACK_CLASSES ? mo[lane_u] : make_uint2(~0u, 0u);
+    const uint64_t le = __ballot(m.x <= u0);
+    const int ko = 63 - __builtin_clzll(le);
+    const uint32_t kbeg = __builtin_amdgcn_readlane(m.x, ko);
+    const uint32_t s0 = __builtin_amdgcn_readlane(m.y, ko);
+    const int c = __builtin_amdgcn_readfirstlane(mk[ko]);
+    // (the unit's index in its class list: u0 - kbeg + s0, modulo 2^32)
+    const uint32_t ubeg = kbeg - s0;
     const uint2 gc = mg2[c];
     const uint32_t cnt = __builtin_amdgcn_readfirstlane(gc.x);
     const uint32_t geo = __builtin_amdgcn_readfirstlane(gc.y);
     const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
-    const uint32_t first = (s0 + v - ubeg) * k;  // the unit's first piece
+    const uint32_t first = (u0 - ubeg) * k;  // the unit's first piece
     if ((geo & PACK_GEO_LANE) && t.all_bytes) {  // wave-uniform
       const uint32_t idx = first + lane_u;
       int64_t a = 0;
@@ -2271,6 +2393,17 @@ void k_bpe_pack(DevTables t, DevWork w) {
       if (sl <= 4) lane_bpe<4>(t, w, ls, a, n, lane_u);
       else if (sl <= 8) lane_bpe<8>(t, w, ls, a, n, lane_u);
       else lane_bpe<16>(t, w, ls, a, n, lane_u);
+      continue;
+    }
+    if ((geo & PACK_GEO_GROUP) && t.all_bytes && t.ctab) {  // wave-uniform
+      const uint32_t idx = first + (lane_u >> 2);
+      int64_t a = 0;
+      int n = 0;
+      if (idx < cnt) {
+        a = w.plist[w.poff[c] + idx];
+        n = (int)(piece_end(w, a) - a);
+      }
+      group_bpe<8>(t, w, lds[wv], a, n, lane_u);
       continue;
     }
     // slot-packed: 64 / slot pieces at a time (a lane-class unit without
@@ -3005,14 +3138,17 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
 constexpr uint32_t ROWS_UNSAFE_LDS = 12288;
 __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   extern __shared__ uint32_t unsafe_lds[];
+  // (launched before the host knows how many pieces there are: a block
+  // without one leaves at once)
+  uint32_t n = *w.longcount;
+  if (n > w.long_cap) n = w.long_cap;
+  if (blockIdx.x * 4 >= n) return;
   const bool lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS;
   if (lds) {
     for (uint32_t j = threadIdx.x; j < t.unsafe_words; j += 256)
       unsafe_lds[j] = t.unsafe[j];
     __syncthreads();
   }
-  uint32_t n = *w.longcount;
-  if (n > w.long_cap) n = w.long_cap;
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
   // few, latency-bound waves beside k_bpe_pack on the same SIMDs
@@ -3174,6 +3310,8 @@ __global__ __launch_bounds__(256) void k_pack_copy(DevWork w, int64_t ntile) {
     const uint32_t k = j - cbeg[c];
     w.plist[cdst[c] + k] = src[csrc[c] + k];
   }
+  if (blockIdx.x == 0 && tid < PACK_XCDS)  // k_bpe_pack's per-XCD counters
+    w.pqueue[tid * PACK_QSTRIDE] = (PACK_BLOCKS / PACK_XCDS) * 4;
   if (blockIdx.x == 0 && tid == 0) {
     uint32_t run = 0;
 #pragma unroll
@@ -3443,15 +3581,24 @@ hipError_t launch_pack_copy(const DevWork& w, hipStream_t s, hipEvent_t stop) {
   return hipGetLastError();
 }
 
-hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
-                           hipEvent_t stop, uint32_t nlong) {
-  // pieces of 65..WIDE_MAX bytes are merged whole, one wave each (a wave
-  // per queued long piece, up to 2048 blocks of four): up to 256 bytes in
-  // registers (k_bpe_rows), longer ones with their state in LDS
-  const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
+// Pieces of 65..WIDE_MAX bytes are merged whole, one wave each. Up to 256
+// bytes in registers (k_bpe_rows): launched right after k_lists, before the
+// host knows the count (the most blocks a count can use; those past it
+// leave at once), so these latency-bound merges start with the packed merge.
+constexpr uint32_t ROWS_BLOCKS = 2048;
+hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s) {
   const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
                          ? (size_t)t.unsafe_words * 4 : 0;
-  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, t, w);
+  hipLaunchKernelGGL(k_bpe_rows, dim3(ROWS_BLOCKS), dim3(256), lds, s, t, w);
+  return hipGetLastError();
+}
+
+// Longer ones with their state in LDS (k_bpe_wide), once the host knows
+// there are pieces over 64 bytes (a wave per queued piece, up to 2048
+// blocks of four).
+hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
+                           hipEvent_t stop, uint32_t nlong) {
+  const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
   launch_ev(k_bpe_wide, dim3(blocks), dim3(256), s, nullptr, stop, t, w,
             (const uint32_t*)w.longlist, (const uint32_t*)w.longcount,
             w.long_cap, 0);

@@ -185,7 +185,7 @@ struct Workspace {
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
   uint32_t *blkcount = nullptr, *blkprefix = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
-  uint32_t *pblk = nullptr, *plocal = nullptr;
+  uint32_t *pblk = nullptr, *plocal = nullptr, *pqueue = nullptr;
   int32_t *nx = nullptr, *pv = nullptr;
   size_t long_pairs = 0, seg_pairs = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
@@ -236,6 +236,7 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.litb, words);
   take(w.docmask_lit, words);
   take(w.nrun, 3 * (size_t)tiles);
+  take(w.pqueue, (size_t)tk::PACK_XCDS * tk::PACK_QSTRIDE);
   w.cap = cap;
   w.tiles = (size_t)tiles;
   w.long_pairs = long_cap;
@@ -290,6 +291,7 @@ struct tk_engine {
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
   hipEvent_t ev_join = nullptr;  // side stream -> engine stream
+  hipEvent_t ev_lists = nullptr;  // engine stream (k_lists done) -> side stream
   // pieces over WIDE_MAX bytes (cut / segment / certify) on a stream of
   // their own, beside the 65..WIDE_MAX-byte merges of stream2
   hipStream_t stream3 = nullptr;
@@ -422,6 +424,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.pcount = ctrl + tk::CTRL_PCOUNT;
   w.uend = ctrl + tk::CTRL_UEND;
   w.nbig = ctrl + tk::CTRL_BIG;
+  w.pqueue = ws.pqueue;
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
@@ -529,6 +532,12 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   }
   ws.slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_lists(e->t, w, s));
+  // The merges of pieces of 65..256 bytes need k_lists alone: on the side
+  // stream from here, beside k_pack_copy and the packed merge (the device
+  // reads the count; no host decision waits for them).
+  HIP_TRY(hipEventRecord(e->ev_lists, s));
+  HIP_TRY(hipStreamWaitEvent(e->stream2, e->ev_lists, 0));
+  HIP_TRY(tk::launch_bpe_rows(e->t, w, e->stream2));
   HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
                               stages || packonly ? ev[2] : nullptr));
@@ -543,11 +552,12 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
+  hipStream_t s2 = e->stream2;
   if (nlong > 0) {
     // two independent jobs on two side streams: pieces of 65..WIDE_MAX
-    // bytes merged whole, and the cut / segment / certify path of the
-    // longer ones (they touch disjoint bytes and read the same lists)
-    hipStream_t s2 = e->stream2;
+    // bytes merged whole (k_bpe_rows already queued), and the cut /
+    // segment / certify path of the longer ones (they touch disjoint bytes
+    // and read the same lists)
     HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     // (a table that drops bytes merges its pieces over WIDE_MAX bytes
     // whole, a workgroup each, after the wide merges)
@@ -569,11 +579,12 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       HIP_TRY(hipEventRecord(e->ev_join3, s3));
       HIP_TRY(hipStreamWaitEvent(s, e->ev_join3, 0));
     }
-    HIP_TRY(hipEventRecord(e->ev_join, s2));
-    HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
-    // (the end of both side streams, or of the packed merge if later)
-    if (stages) HIP_TRY(hipEventRecord(ev[3], s));
   }
+  // (k_bpe_rows is on the side stream in every call: always joined)
+  HIP_TRY(hipEventRecord(e->ev_join, s2));
+  HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
+  // (the end of both side streams, or of the packed merge if later)
+  if (stages && nlong > 0) HIP_TRY(hipEventRecord(ev[3], s));
   // the compaction reports the failed cuts left after the last queued pass
   tk::DevWork wc = w;
   if (big) wc.nfail = fail_count(ctrl, DEV_REPAIRS);
@@ -891,6 +902,8 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming |
                                                hipEventDisableSystemFence) != hipSuccess ||
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
+                                                hipEventDisableSystemFence) != hipSuccess ||
+      hipEventCreateWithFlags(&e->ev_lists, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
@@ -1027,6 +1040,7 @@ void tk_engine_close(tk_engine* e) {
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->ev_join3) (void)hipEventDestroy(e->ev_join3);
+  if (e->ev_lists) (void)hipEventDestroy(e->ev_lists);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->stream2) (void)hipStreamDestroy(e->stream2);
   if (e->stream3) (void)hipStreamDestroy(e->stream3);
