@@ -3154,8 +3154,26 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   // few, latency-bound waves beside k_bpe_pack on the same SIMDs
   if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
-    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
-    const int len = (int)(b - a);
+    // k_pretok queued the start; the end is the next start bit, looked for
+    // here in the next 256 bytes (k_lists has not run yet: these merges
+    // start right after k_pretok). A piece without one there is longer
+    // than this kernel's, and a sentinel bit ends the search at the text's
+    // end (the words past it are readable).
+    const uint32_t a = w.longlist[2 * k];
+    int len = 257;
+    {
+      const int64_t wd = a >> 6;
+      uint64_t word = w.starts[wd] & ~mask_le((int)(a & 63));
+#pragma unroll
+      for (int j = 1; j <= 5 && len > 256; ++j) {
+        if (word) {
+          const int64_t e = (wd + j - 1) * 64 + __builtin_ctzll(word);
+          len = e - a <= 256 ? (int)(e - a) : 257;
+          break;
+        }
+        word = w.starts[wd + j];
+      }
+    }
     if (len <= 64 || len > 256) continue;  // wave-uniform
     const uint32_t* ul = lds ? unsafe_lds : nullptr;
     if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, ul);
@@ -3582,9 +3600,10 @@ hipError_t launch_pack_copy(const DevWork& w, hipStream_t s, hipEvent_t stop) {
 }
 
 // Pieces of 65..WIDE_MAX bytes are merged whole, one wave each. Up to 256
-// bytes in registers (k_bpe_rows): launched right after k_lists, before the
+// bytes in registers (k_bpe_rows): launched right after k_pretok, before the
 // host knows the count (the most blocks a count can use; those past it
-// leave at once), so these latency-bound merges start with the packed merge.
+// leave at once), so these latency-bound merges run beside the piece lists
+// and the packed merge.
 constexpr uint32_t ROWS_BLOCKS = 2048;
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s) {
   const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS

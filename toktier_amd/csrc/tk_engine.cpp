@@ -291,7 +291,7 @@ struct tk_engine {
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
   hipEvent_t ev_join = nullptr;  // side stream -> engine stream
-  hipEvent_t ev_lists = nullptr;  // engine stream (k_lists done) -> side stream
+  hipEvent_t ev_pretok = nullptr;  // engine stream (k_pretok done) -> side stream
   // pieces over WIDE_MAX bytes (cut / segment / certify) on a stream of
   // their own, beside the 65..WIDE_MAX-byte merges of stream2
   hipStream_t stream3 = nullptr;
@@ -530,14 +530,15 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   } else {
     HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
   }
+  // The merges of pieces of 65..256 bytes need k_pretok alone (the queued
+  // starts and the start bits): on the side stream from here, beside the
+  // piece lists and the packed merge (the device reads the count; no host
+  // decision waits for them).
+  HIP_TRY(hipEventRecord(e->ev_pretok, s));
+  HIP_TRY(hipStreamWaitEvent(e->stream2, e->ev_pretok, 0));
+  HIP_TRY(tk::launch_bpe_rows(e->t, w, e->stream2));
   ws.slot ^= 1;  // this call's k_pretok clears the other slot
   HIP_TRY(tk::launch_lists(e->t, w, s));
-  // The merges of pieces of 65..256 bytes need k_lists alone: on the side
-  // stream from here, beside k_pack_copy and the packed merge (the device
-  // reads the count; no host decision waits for them).
-  HIP_TRY(hipEventRecord(e->ev_lists, s));
-  HIP_TRY(hipStreamWaitEvent(e->stream2, e->ev_lists, 0));
-  HIP_TRY(tk::launch_bpe_rows(e->t, w, e->stream2));
   HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
                               stages || packonly ? ev[2] : nullptr));
@@ -903,7 +904,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
                                                hipEventDisableSystemFence) != hipSuccess ||
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess ||
-      hipEventCreateWithFlags(&e->ev_lists, hipEventDisableTiming |
+      hipEventCreateWithFlags(&e->ev_pretok, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
@@ -1040,7 +1041,7 @@ void tk_engine_close(tk_engine* e) {
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->ev_join3) (void)hipEventDestroy(e->ev_join3);
-  if (e->ev_lists) (void)hipEventDestroy(e->ev_lists);
+  if (e->ev_pretok) (void)hipEventDestroy(e->ev_pretok);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->stream2) (void)hipStreamDestroy(e->stream2);
   if (e->stream3) (void)hipStreamDestroy(e->stream3);
