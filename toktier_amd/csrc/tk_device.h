@@ -213,22 +213,24 @@ __host__ __device__ constexpr int pack_slot(int c) {
        : c == 10 ? 21 : c == 11 ? 32 : 64;
 }
 // Classes of up to PACK_LANE_MAX bytes are merged one piece per lane (64
-// pieces per work unit, each merged serially by its lane); classes of up to
-// PACK_GROUP_MAX bytes one piece per group of four lanes (16 pieces per unit,
-// 8 positions per lane); longer ones one piece per slot of pack_slot(c) lanes
-// (64 / slot pieces per unit, merged by the lanes together).
+// pieces per work unit, each merged serially by its lane); up to
+// PACK_GROUP_MAX bytes one piece per group of four lanes, 8 positions per
+// lane (16 pieces per unit); longer ones lane per byte, 64 / slot pieces at
+// a time (pieces per unit 64 / slot; lanes per piece recorded as 0).
 constexpr int PACK_LANE_MAX = 16;
 constexpr int PACK_GROUP_MAX = 32;
 __host__ __device__ constexpr bool pack_lane(int c) {
   return pack_slot(c) <= PACK_LANE_MAX;
 }
-__host__ __device__ constexpr bool pack_group(int c) {
-  return !pack_lane(c) && pack_slot(c) <= PACK_GROUP_MAX;
+// lanes per piece of class c (0: lane per byte)
+__host__ __device__ constexpr int pack_lanes(int c) {
+  return pack_lane(c) ? 1 : pack_slot(c) <= PACK_GROUP_MAX ? 4 : 0;
 }
 // pieces per work unit, and a multiplier m with (lane * m) >> 12 == lane /
-// pack_slot(c) for every lane < 64
+// pack_slot(c) for every lane < 64 (the lane-per-byte path, also taken by
+// tables without the lane and group paths)
 __host__ __device__ constexpr int pack_per_unit(int c) {
-  return pack_lane(c) ? 64 : pack_group(c) ? 16 : 64 / pack_slot(c);
+  return pack_lanes(c) ? 64 / pack_lanes(c) : 64 / pack_slot(c);
 }
 __host__ __device__ constexpr int pack_magic(int c) {
   return (4096 + pack_slot(c) - 1) / pack_slot(c);

@@ -2278,12 +2278,11 @@ __device__ __forceinline__ void group_bpe(const DevTables& t, const DevWork& w,
   }
 }
 
-constexpr uint32_t PACK_GEO_LANE = 1u << 31;  // one piece per lane
-constexpr uint32_t PACK_GEO_GROUP = 1u << 30;  // one piece per group of lanes
+// geometry word of a class: slot | pieces per unit << 8 | pack_magic << 16 |
+// lanes per piece << 28
 constexpr uint32_t pack_geo(int c) {
   return (uint32_t)pack_slot(c) | (uint32_t)pack_per_unit(c) << 8 |
-         (uint32_t)pack_magic(c) << 16 | (pack_lane(c) ? PACK_GEO_LANE : 0u) |
-         (pack_group(c) ? PACK_GEO_GROUP : 0u);
+         (uint32_t)pack_magic(c) << 16 | (uint32_t)pack_lanes(c) << 28;
 }
 __constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
     pack_geo(0), pack_geo(1), pack_geo(2), pack_geo(3), pack_geo(4),
@@ -2293,22 +2292,26 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 
 // Work units by class (class c's list, in text order, makes uend[c] -
 // uend[c + 1] units). Workgroups go to the XCDs in turn (block b on XCD
-// b % PACK_XCDS), and each XCD has its own L2: so each class's units are
-// split into PACK_XCDS contiguous runs, run x (one stretch of the text) for
-// the blocks of XCD x, and an XCD reads the text, start words and lists of
-// its own stretch only. An XCD's units go in one order, class by class,
-// longest merge chains first (PACK_ORDER: the 17..32-byte groups and the
-// 9..16-byte lanes, then the shorter lane classes; 33..64-byte pieces, one
-// per unit, among them by their measured length). Wave g of the XCD's G
+// b % PACK_XCDS, up to a rotation), and each XCD has its own L2: so each
+// class's units are split into PACK_XCDS contiguous runs, run x (one stretch
+// of the text) for the blocks of XCD x, and an XCD reads the text, start
+// words and lists of its own stretch only. An XCD's units go in one order,
+// class by class, longest merge chains first (PACK_ORDER, from the per-class
+// unit times of a cycle-counter probe build: the 17..32-byte groups and the
+// 9..16-byte lanes first). Wave g of the XCD's G
 // waves takes unit g first; every later unit comes from the XCD's counter
 // (pqueue, set to G by k_pack_copy), one at a time as waves finish theirs.
 // The long units thus all start at once, and the SIMDs end on the short
 // ones, each SIMD busy until its share is done (with a fixed share per wave
 // a SIMD holding a few long units ran on alone, latency-bound, long after
 // the others). Classes of up to PACK_LANE_MAX bytes: 64 pieces per unit,
-// one per lane (lane_bpe); up to PACK_GROUP_MAX bytes: 16 pieces per unit,
-// four lanes each (group_bpe); longer ones: 64 / slot pieces per unit, a
-// slot of lanes each (wave_bpe).
+// one per lane (lane_bpe); up to 32 bytes: 16 pieces per unit, four lanes
+// each (group_bpe); longer ones, and every class of a table without an id
+// for every byte or without the compact pair table: 64 / slot pieces at a
+// time, a slot of lanes each (wave_bpe). (Groups of eight lanes for 33..64
+// bytes were slower: one merge per step makes their units the longest
+// chains of the launch, where one piece per wave merges every occurrence of
+// a rank per round.)
 __constant__ int8_t PACK_ORDER[PACK_CLASSES] = {11, 9, 10, 8, 7, 6, 5, 12,
                                                 4, 3, 2, 1, 0};
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
@@ -2381,7 +2384,8 @@ void k_bpe_pack(DevTables t, DevWork w) {
     const uint32_t geo = __builtin_amdgcn_readfirstlane(gc.y);
     const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
     const uint32_t first = (u0 - ubeg) * k;  // the unit's first piece
-    if ((geo & PACK_GEO_LANE) && t.all_bytes) {  // wave-uniform
+    const int lanes = (int)(geo >> 28);
+    if (lanes == 1 && t.all_bytes) {  // wave-uniform
       const uint32_t idx = first + lane_u;
       int64_t a = 0;
       int n = 0;
@@ -2395,8 +2399,8 @@ void k_bpe_pack(DevTables t, DevWork w) {
       else lane_bpe<16>(t, w, ls, a, n, lane_u);
       continue;
     }
-    if ((geo & PACK_GEO_GROUP) && t.all_bytes && t.ctab) {  // wave-uniform
-      const uint32_t idx = first + (lane_u >> 2);
+    if (lanes == 4 && t.all_bytes && t.ctab) {  // wave-uniform
+      const uint32_t idx = first + (uint32_t)(lane_u / lanes);
       int64_t a = 0;
       int n = 0;
       if (idx < cnt) {
@@ -3734,7 +3738,8 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
     } else {
       if (lane == 0) cst_store(&w.cstat[b], hi | tot);
       // COMPACT_LOOK * 64 predecessors per step, nearest first: lane l of
-      // part k reads block j - 64k - l
+      // part k reads block j - 64k - l (blocks before 0 read as a running
+      // total of 0)
       for (int64_t j = b - 1;; j -= 64 * COMPACT_LOOK) {
         uint64_t st[COMPACT_LOOK];
 #pragma unroll
@@ -3742,14 +3747,32 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
           const int64_t q = j - 64 * k - lane;
           st[k] = q >= 0 ? cst_load(&w.cstat[q]) : (hi | CST_TOTAL);
         }
+        // Only the words before the nearest published running total are
+        // needed: wait for those (every unpublished one re-read at once,
+        // one round trip per round), and never for the words behind it.
+        for (int spin = 0;; ++spin) {
+          bool need = false, found = false;
 #pragma unroll
-        for (int k = 0; k < COMPACT_LOOK; ++k) {
-          const int64_t q = j - 64 * k - lane;
-          for (int spin = 0; q >= 0 && (st[k] >> 32) != tag && spin < COMPACT_SPIN; ++spin)
-            st[k] = cst_load(&w.cstat[q]);
-          if ((st[k] >> 32) != tag) {  // only after the bounded wait
+          for (int k = 0; k < COMPACT_LOOK; ++k) {
+            if (found) break;  // wave-uniform
+            const bool pub = (st[k] >> 32) == tag;
+            const uint64_t tm = __ballot(pub && ((uint32_t)st[k] & CST_TOTAL) != 0);
+            const int l = tm ? __builtin_ctzll(tm) : 64;
+            need |= __ballot(!pub && lane < l) != 0;
+            found = tm != 0;
+          }
+          if (!need) break;
+          if (spin >= COMPACT_SPIN) {  // only after the bounded wait
             ok = false;
-            st[k] = hi | CST_TOTAL;
+#pragma unroll
+            for (int k = 0; k < COMPACT_LOOK; ++k)
+              if ((st[k] >> 32) != tag) st[k] = hi | CST_TOTAL;
+            break;
+          }
+#pragma unroll
+          for (int k = 0; k < COMPACT_LOOK; ++k) {
+            const int64_t q = j - 64 * k - lane;
+            if ((st[k] >> 32) != tag) st[k] = cst_load(&w.cstat[q]);
           }
         }
         bool done = false;
