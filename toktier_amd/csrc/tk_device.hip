@@ -3689,7 +3689,7 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 // publish their counts without waiting, and every wait is bounded.
 constexpr uint32_t CST_TOTAL = 1u << 31;
 constexpr int COMPACT_SPIN = 1 << 20;
-constexpr int COMPACT_LOOK = 16;
+constexpr int COMPACT_LOOK = 1;
 
 __device__ __forceinline__ void cst_store(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
