@@ -64,14 +64,15 @@ def test_probe_tables(probe):
 
 
 def test_literals_across_tile_and_block_edges():
-    """A literal starting at every offset around the pretokenizer's 3072-
-    byte tiles and the literal kernels' 4096-byte blocks."""
+    """A literal starting at every offset around the pretokenizer's tiles
+    (PT_TILE bytes) and the literal kernels' 4096-byte blocks."""
     from toktier_amd import workloads
     k, t = kit("qwen3_8b"), tok("qwen3_8b")
     base = workloads.config2(k.json, n_chars=20_000)
     base = "".join(ch for ch in base if ord(ch) < 128)[:13_000]
     lit = "<|im_end|>"
-    for edge in (3072, 4096, 6144, 8192, 12288):
+    from test_gpu_parity import TILE
+    for edge in (TILE, 2 * TILE, 3072, 4096, 6144, 8192, 12288):
         for d in range(-12, 3):
             p = edge + d
             s = base[:p] + lit + base[p:]

@@ -10,6 +10,17 @@ from conftest import FAMILY_NAMES, kit
 
 pytestmark = pytest.mark.gpu
 
+
+def _pt_tile() -> int:
+    """The pretokenizer's tile in bytes (PT_TILE in the device header)."""
+    import re
+    from pathlib import Path
+    h = Path(__file__).resolve().parent.parent / "toktier_amd" / "csrc" / "tk_device.h"
+    return int(re.search(r"constexpr int PT_TILE = (\d+);", h.read_text()).group(1))
+
+
+TILE = _pt_tile()
+
 _TOKS: dict = {}
 
 
@@ -294,13 +305,15 @@ def test_non_monotone_long_pieces_match_hf():
 
 def _digit_texts(rng):
     """Digit runs of every length class around the 64-byte word, the
-    64-byte halo and the 3072-byte tile, at shifted offsets, with ASCII and
-    non-ASCII N characters (Arabic-Indic, fullwidth, superscript, Roman
-    numeral), runs broken by other characters, and runs at the text ends."""
+    64-byte halo and the pretokenizer's tile (TILE bytes; also the former
+    3072), at shifted offsets, with ASCII and non-ASCII N characters
+    (Arabic-Indic, fullwidth, superscript, Roman numeral), runs broken by
+    other characters, and runs at the text ends."""
     out = []
-    for n in (1, 2, 3, 4, 5, 63, 64, 65, 127, 128, 129, 3071, 3072, 3073,
-              3135, 3136, 3137, 6143, 6144, 6145, 9300):
-        for pre in ("", "x", "ab ", " " * 61, "y" * 3070):
+    for n in (1, 2, 3, 4, 5, 63, 64, 65, 127, 128, 129,
+              TILE - 1, TILE, TILE + 1, TILE + 63, TILE + 64, TILE + 65,
+              2 * TILE - 1, 2 * TILE, 2 * TILE + 1, 3071, 3072, 3073, 9300):
+        for pre in ("", "x", "ab ", " " * 61, "y" * (TILE - 2)):
             out.append(pre + "7" * n + " z")
     digits = "0123456789" + "٠١٢٣" + "０１２" + "²³" + "Ⅻ"
     for _ in range(40):
@@ -421,15 +434,16 @@ def _o200k_long_runs(rng):
     letter or not (the state differs until an upper-case letter ends the
     run), P / mark alternations after one P or two, whitespace after a
     CR/LF, upper-case runs after a C letter; at lengths around the 64-byte
-    word and the 3072-byte tile, with and without a lead-in. The long C
+    word and the pretokenizer's tile, with and without a lead-in. The long C
     runs are random ideographs (each run is one piece; a periodic piece of
     tens of KB would be merged serially)."""
     def cjk(n):
         return "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, n))
     out = []
-    for n in (20, 21, 22, 1023, 1024, 1025, 3071, 3072, 3073, 12_000, 40_000):
+    for n in (20, 21, 22, 1023, 1024, 1025, TILE - 1, TILE, TILE + 1, 12_000,
+              40_000):
         run = cjk(n)
-        for lead in ("", "a", "A", " ", "x" * 61, "y" * 3070):
+        for lead in ("", "a", "A", " ", "x" * 61, "y" * (TILE - 2)):
             out.append(lead + run + "ABC d")
             out.append(lead + run + "ABCd")
         if n > 3100:
@@ -529,8 +543,8 @@ def test_kimi_branches_match_hf():
 
 def _kimi_runs(rng):
     out = []
-    for n in (20, 63, 64, 65, 1023, 1024, 1025, 3071, 3072, 3073, 9000):
-        for lead in ("", "a", "1", "〇", "x" * 61, "y" * 3070):
+    for n in (20, 63, 64, 65, 1023, 1024, 1025, TILE - 1, TILE, TILE + 1, 9000):
+        for lead in ("", "a", "1", "〇", "x" * 61, "y" * (TILE - 2)):
             digits = "".join("0123456789〇〡〢"[int(i)] for i in rng.integers(0, 13, n))
             out.append(lead + digits + " z")
             out.append(lead + "7" * n + "〇" + "8" * 5)

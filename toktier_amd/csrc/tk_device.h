@@ -247,7 +247,7 @@ __host__ __device__ inline int64_t pack_off(int64_t nb, int c) {
 }
 
 constexpr int PRETOK_TPB = 256;
-constexpr int PT_TILE = 3072;  // bytes per k_pretok block (48 start words)
+constexpr int PT_TILE = 2816;  // bytes per k_pretok block (44 start words)
 // k_pretok blocks: the start words 0..nwin+1 (nwin = ceil(nb / 64))
 __host__ __device__ inline int64_t pretok_tiles(int64_t nb) {
   return (((nb + 63) / 64 + 2) * 64 + PT_TILE - 1) / PT_TILE;
