@@ -46,6 +46,7 @@ constexpr int AD_AHEAD = 256;   // > ADDED_MAX_LEN: a walk from the block's
                                 // last byte stays staged
 constexpr int AD_STAGE = AD_BACK + ADDED_BLOCK_BYTES + AD_AHEAD;
 constexpr int AD_CAND = AD_BACK + ADDED_BLOCK_BYTES;  // candidates staged
+constexpr int AD_LIST = 1024;   // listed first-byte positions per block
 static_assert(AD_STAGE % 16 == 0, "16-byte staging");
 static_assert(2 * ADDED_MAX_LEN < AD_BACK && ADDED_MAX_LEN < AD_AHEAD,
               "staged margins hold a literal and its certainty window");
@@ -171,16 +172,31 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
   __shared__ unsigned long long sdm[64], slits[64], slitb[64];
   __shared__ uint64_t shdm[AD_STAGE / 64];  // caller's document starts
   __shared__ uint32_t scount;
+  __shared__ uint16_t slist[AD_LIST];  // staged positions of first bytes
+  __shared__ uint32_t slist_n;
   const int tid = threadIdx.x;
   const int64_t B = (int64_t)blockIdx.x * ADDED_BLOCK_BYTES;
   const int64_t s0 = B - AD_BACK, nb = w.nb;
   int hit = 0;
-  for (int j = tid; j < AD_STAGE / 16; j += 256) {
+  // (the staging's 16-byte loads all issued before any is used)
+  constexpr int SPT = (AD_STAGE / 16 + 255) / 256;
+  uint4 sv[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const int j = tid + 256 * i;
     const int64_t p = s0 + 16 * j;
-    uint4 v;
-    if (p >= 0 && p + 16 <= nb && ((uintptr_t)(w.text + p) & 15) == 0) {
-      v = *reinterpret_cast<const uint4*>(w.text + p);
-    } else {
+    sv[i] = make_uint4(0, 0, 0, 0);
+    if (j < AD_STAGE / 16 && p >= 0 && p + 16 <= nb &&
+        ((uintptr_t)(w.text + p) & 15) == 0)
+      sv[i] = *reinterpret_cast<const uint4*>(w.text + p);
+  }
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const int j = tid + 256 * i;
+    if (j >= AD_STAGE / 16) break;
+    const int64_t p = s0 + 16 * j;
+    uint4 v = sv[i];
+    if (!(p >= 0 && p + 16 <= nb && ((uintptr_t)(w.text + p) & 15) == 0)) {
       uint32_t x[4] = {0, 0, 0, 0};
       for (int k = 0; k < 16; ++k) {
         const int64_t q = p + k;
@@ -200,7 +216,7 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
     }
   }
   if (tid < 64) sdm[tid] = slits[tid] = slitb[tid] = 0;
-  if (tid == 0) scount = 0;
+  if (tid == 0) scount = slist_n = 0;
   const int64_t w0 = s0 >> 6;  // s0 is a multiple of 64
   if (host_dm && tid < AD_STAGE / 64) {
     const int64_t wd = w0 + tid;
@@ -232,11 +248,52 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
   }
   if (any) {
     if (L) {
-      for (uint32_t k = tid; k < a.tab_size; k += 256) stab[k] = a.tab[k];
-      for (uint32_t k = tid; k < a.n; k += 256) slen_l[k] = a.len[k];
+      // every load first, then the stores (a load-store loop waits for
+      // each load in turn)
+      constexpr int TPT = (ADDED_TAB_LDS + 255) / 256, LPT = (ADDED_LEN_LDS + 255) / 256;
+      uint64_t te[TPT];
+      uint8_t le[LPT];
+#pragma unroll
+      for (int i = 0; i < TPT; ++i) {
+        const uint32_t k = tid + 256 * i;
+        te[i] = k < a.tab_size ? a.tab[k] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < LPT; ++i) {
+        const uint32_t k = tid + 256 * i;
+        le[i] = k < a.n ? a.len[k] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < TPT; ++i)
+        if (tid + 256 * i < a.tab_size) stab[tid + 256 * i] = te[i];
+#pragma unroll
+      for (int i = 0; i < LPT; ++i)
+        if (tid + 256 * i < a.n) slen_l[tid + 256 * i] = le[i];
+    }
+    // The staged positions that hold some literal's first byte, listed
+    // (one LDS counter update per wave): the trie walks then run one
+    // position per lane, instead of every lane's walk holding up its wave
+    // on each of its positions in turn. More than AD_LIST of them (a text
+    // of first bytes): every position is walked in place.
+    for (int j = tid; j < AD_CAND; j += 256) scand[j] = 0;
+    {
+      const int lane = tid & 63;
+      for (int j0 = tid - lane; j0 < AD_CAND; j0 += 256) {
+        const int j = j0 + lane;
+        const int64_t p = s0 + j;
+        const bool g = j < AD_CAND && p >= 0 && p < nb && gate_hit(a, sx[j]);
+        const uint64_t bm = __ballot(g);
+        if (!bm) continue;  // wave-uniform
+        uint32_t at = 0;
+        if (lane == 0) at = atomicAdd(&slist_n, (uint32_t)__popcll(bm));
+        at = __shfl(at, 0) + (uint32_t)__popcll(bm & ((1ULL << lane) - 1));
+        if (g && at < AD_LIST) slist[at] = (uint16_t)j;
+      }
     }
     __syncthreads();
-    for (int j = tid; j < AD_CAND; j += 256) {
+    const uint32_t nlist = slist_n;
+    const bool listed = nlist <= AD_LIST;
+    auto match = [&](int j) {
       const int64_t p = s0 + j;
       uint16_t c = 0;
       if (p >= 0 && p < nb) {
@@ -246,13 +303,22 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
           c = (uint16_t)trie_match(a, sx, s0, nb, nullptr, 0, L ? stab : a.tab, p);
       }
       scand[j] = c;
+    };
+    if (listed) {
+      for (uint32_t k = tid; k < nlist; k += 256) match(slist[k]);
+    } else {
+      for (int j = tid; j < AD_CAND; j += 256) match(j);
     }
     __syncthreads();
     const Block<L> blk{a, w.text, nb, host_dm, scand, slen_l, s0};
     // every candidate whose literal, or the document start just past it,
-    // falls on the block's bytes
+    // falls on the block's bytes (candidates are listed positions, when
+    // listed)
     uint32_t mine = 0;
-    for (int j = AD_BACK - ADDED_MAX_LEN + tid; j < AD_CAND; j += 256) {
+    const uint32_t nj = listed ? nlist : (uint32_t)AD_CAND;
+    for (uint32_t k = tid; k < nj; k += 256) {
+      const int j = listed ? (int)slist[k] : (int)k;
+      if (j < AD_BACK - ADDED_MAX_LEN) continue;
       const uint32_t c = scand[j];
       if (!c) continue;
       const int64_t s = s0 + j, e = s + blk.len(c);
