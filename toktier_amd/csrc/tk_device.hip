@@ -2092,7 +2092,9 @@ __device__ __forceinline__ bool pair_find(const DevTables& t, uint32_t l,
 // per step. Positions keep their byte offsets: a live mask per lane, the
 // rank and product of the pair each live position starts in registers (rk,
 // md), the symbols in LDS at [position][lane] (lsym: this wave's L x 64
-// words). Every byte has an id (the engine's all_bytes flag).
+// words). Every byte has an id (the engine's all_bytes flag). A step costs
+// a few instructions per position of L, so each class takes the smallest
+// instance that holds it (4, 8, 12, 16; a 6 gained nothing, a 10 spilled).
 template <int L>
 __device__ void lane_bpe(const DevTables& t, const DevWork& w, uint32_t* lsym,
                          int64_t a, int n, int lane) {
@@ -2396,6 +2398,7 @@ void k_bpe_pack(DevTables t, DevWork w) {
       uint32_t* ls = lds[wv];
       if (sl <= 4) lane_bpe<4>(t, w, ls, a, n, lane_u);
       else if (sl <= 8) lane_bpe<8>(t, w, ls, a, n, lane_u);
+      else if (sl <= 12) lane_bpe<12>(t, w, ls, a, n, lane_u);
       else lane_bpe<16>(t, w, ls, a, n, lane_u);
       continue;
     }
