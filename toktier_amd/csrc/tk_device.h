@@ -263,8 +263,8 @@ __host__ __device__ constexpr int pack_local_off(int c) {
 }
 constexpr int PT_LOCAL_SLOTS = pack_local_off(PACK_CLASSES);
 constexpr int COMPACT_TPB = 256;
-constexpr int COMPACT_PER_THREAD = 16;
-constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 4096
+constexpr int COMPACT_PER_THREAD = 32;
+constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 8192
 
 // start / stop: optional timing events taken from the start of the stage's
 // first dispatch / the end of its last one

@@ -3684,8 +3684,11 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 // COMPACT_BLOCK slots (COMPACT_PER_THREAD consecutive slots per thread) and
 // stages them in LDS, publishes the count, takes its offset from its
 // predecessors' words (decoupled look-back: the nearest predecessor that has
-// published a running total, plus the counts in between, 1024 predecessors
-// per step), publishes its running total and stores its ids contiguously.
+// published a running total, plus the counts in between, 64 * COMPACT_LOOK
+// predecessors per step), publishes its running total and stores its ids
+// contiguously. The status words are read past L2 (agent scope), so every
+// word read costs a trip to the memory side for every block of the launch:
+// a short window per step and large blocks keep those reads few.
 // A status word is tag << 32 | CST_TOTAL (a running total, else a count) |
 // value: words left by other launches carry other tags and read as not yet
 // published. A block waits only for blocks dispatched before it, which
