@@ -477,7 +477,7 @@ def main() -> int:
     n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
     chars = float(np.mean([n_chars_of(r) for r in reqs[:K]]))
     st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["pretokenize + piece lists (k_pretok, k_lists, k_pack_copy)",
+    names = ["pretokenize and piece lists (k_added, k_pretok)",
              "k_bpe_pack",
              "long pieces past k_bpe_pack (k_bpe_rows, k_bpe_wide, k_long_*, "
              "k_certify; side stream)",

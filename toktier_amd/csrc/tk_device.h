@@ -120,16 +120,14 @@ struct DevWork {
   uint32_t* npass;       // device-side repair passes that ran (ctrl)
   uint64_t* dirty_cur;   // repair pass: words (64 bytes) to redo, 1 bit each
   uint64_t* dirty_next;  // words marked by the current certify pass
-  // packed short-piece BPE
-  uint32_t* plist;       // piece starts by length class
-  uint32_t* plocal;      // [tiles][PT_LOCAL_SLOTS] the same, tile by tile
-  uint32_t poff[PACK_CLASSES];  // start of each class's list (pack_off)
-  uint32_t* pblk;        // [PACK_CLASSES][tiles] counts, then offsets
-  uint32_t* pcount;      // [PACK_CLASSES] pieces per class (ctrl)
-  uint32_t* uend;        // [PACK_CLASSES] end of each class's work units in
-                         // k_bpe_pack's order, longest class first (ctrl)
+  // packed short-piece BPE: the piece starts of each length class, one
+  // list per class and segment (pack_seg_list), in the order k_pretok's
+  // tiles took their room
+  uint32_t* plist;
+  uint32_t* pseg;        // ctrl + CTRL_PSEG: per segment, k_bpe_pack's unit
+                         // counter and the pieces listed per class
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
-  uint32_t* pqueue;      // [PACK_XCDS * PACK_QSTRIDE] k_bpe_pack's counters
+  uint32_t* prepdone;    // k_bpe_pack waves done with the long pieces (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
   // added-token literals (nullptr when the call extracts none): a literal
@@ -158,10 +156,14 @@ struct DevWork {
 constexpr uint64_t HR_FIRST = 1ull << 31, HR_LAST = 1ull << 30;
 
 // ctrl word layout (device -> host)
+// (the words of segment x of the piece lists start at CTRL_PSEG + x *
+// CTRL_PSEG_STRIDE: k_bpe_pack's unit counter, then on the next 128-byte
+// line the pieces listed per class, at CTRL_PSEG_COUNT + class)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PASS = 7,
-              CTRL_FAIL2 = 8, CTRL_PCOUNT = 16, CTRL_UEND = 32, CTRL_WORDS = 64;
-// gate words in host memory: k_pack_copy writes GATE_NLONG / GATE_BIG and
+              CTRL_FAIL2 = 8, CTRL_PREP = 9, CTRL_PSEG = 64, CTRL_PSEG_STRIDE = 64,
+              CTRL_PSEG_COUNT = 32, CTRL_WORDS = CTRL_PSEG + 8 * CTRL_PSEG_STRIDE;
+// gate words in host memory: k_bpe_pack writes GATE_NLONG / GATE_BIG and
 // then GATE_SEQ (the host learns, while the packed merge runs, whether the
 // long-piece stages have any work), k_compact's last block
 // writes the request's outcome (status, id count, failed cuts) and then
@@ -199,13 +201,17 @@ __host__ __device__ __forceinline__ uint32_t added_slot(uint32_t key,
                                                         uint32_t size) {
   return (uint32_t)(((uint64_t)(key * 0x9E3779B1u) * size) >> 32);
 }
-// packed short-piece BPE: grid of k_bpe_pack (class counts at CTRL_PCOUNT)
-constexpr int PACK_BLOCKS = 2048;
-// k_bpe_pack's work: one run of every class per XCD (block b on XCD b %
-// PACK_XCDS), each XCD's later units handed out by a counter of its own
-// (pqueue[x * PACK_QSTRIDE], a line each)
+// packed short-piece BPE: grid of k_bpe_pack, seven waves on every SIMD
+// (blocks of four waves, 256 CUs); the eighth wave slot is left to
+// k_bpe_rows, which runs beside it from the end of k_pretok
+constexpr int PACK_BLOCKS = 1792;
+// The piece lists come in PACK_XCDS segments: segment x holds the pieces of
+// the k_pretok tiles b with b % PACK_XCDS == x (those of one XCD: workgroups
+// go to the XCDs in turn), and the k_bpe_pack blocks of the same residue
+// merge them, each XCD's units handed out by a counter of its own
 constexpr int PACK_XCDS = 8;
-constexpr int PACK_QSTRIDE = 64;
+static_assert(CTRL_WORDS == CTRL_PSEG + PACK_XCDS * CTRL_PSEG_STRIDE,
+              "one control line per segment");
 // slots (lanes per piece) of the length classes, and the shortest piece of
 // each class: class c holds pieces of pack_lmin(c)..pack_slot(c) bytes
 __host__ __device__ constexpr int pack_slot(int c) {
@@ -238,13 +244,6 @@ __host__ __device__ constexpr int pack_magic(int c) {
 __host__ __device__ constexpr int pack_lmin(int c) {
   return c <= 7 ? c + 2 : pack_slot(c - 1) + 1;
 }
-// start of class c's list; each class has room for every piece of its
-// shortest length that nb bytes can hold (c == PACK_CLASSES: total length)
-__host__ __device__ inline int64_t pack_off(int64_t nb, int c) {
-  int64_t o = 0;
-  for (int k = 0; k < c; ++k) o += nb / pack_lmin(k) + 1;
-  return o;
-}
 
 constexpr int PRETOK_TPB = 256;
 constexpr int PT_TILE = 2816;  // bytes per k_pretok block (44 start words)
@@ -252,9 +251,11 @@ constexpr int PT_TILE = 2816;  // bytes per k_pretok block (44 start words)
 __host__ __device__ inline int64_t pretok_tiles(int64_t nb) {
   return (((nb + 63) / 64 + 2) * 64 + PT_TILE - 1) / PT_TILE;
 }
-// k_pretok lists each tile's packed pieces by class in a region of its own
-// (plocal): class c may hold every piece of pack_lmin(c) or more bytes that
-// starts in the tile
+// Room in the piece lists: a tile holds at most pack_local_cap(c) pieces of
+// class c (every piece of pack_lmin(c) or more bytes that starts in it), so
+// the lists take PT_LOCAL_SLOTS words per tile. Segment x's lists follow
+// those of the segments before it; its class c list starts pack_local_off(c)
+// words per tile of the segment into them.
 __host__ __device__ constexpr int pack_local_cap(int c) {
   return PT_TILE / pack_lmin(c) + 1;
 }
@@ -262,6 +263,21 @@ __host__ __device__ constexpr int pack_local_off(int c) {
   return c == 0 ? 0 : pack_local_off(c - 1) + pack_local_cap(c - 1);
 }
 constexpr int PT_LOCAL_SLOTS = pack_local_off(PACK_CLASSES);
+// tiles of segment x, and of the segments before it, out of ntile
+__host__ __device__ inline uint32_t pack_seg_tiles(uint32_t ntile, int x) {
+  return ntile > (uint32_t)x ? (ntile - (uint32_t)x + PACK_XCDS - 1) / PACK_XCDS : 0u;
+}
+__host__ __device__ inline uint32_t pack_seg_first(uint32_t ntile, int x) {
+  uint32_t n = 0;
+  for (int y = 0; y < x; ++y) n += pack_seg_tiles(ntile, y);
+  return n;
+}
+// start of segment x's class c list (local_off = pack_local_off(c))
+__host__ __device__ inline uint32_t pack_seg_list(uint32_t ntile, int x,
+                                                  uint32_t local_off) {
+  return pack_seg_first(ntile, x) * (uint32_t)PT_LOCAL_SLOTS +
+         pack_seg_tiles(ntile, x) * local_off;
+}
 constexpr int COMPACT_TPB = 256;
 constexpr int COMPACT_PER_THREAD = 32;
 constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 8192
@@ -270,11 +286,6 @@ constexpr int COMPACT_BLOCK = COMPACT_TPB * COMPACT_PER_THREAD;  // 8192
 // first dispatch / the end of its last one
 hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
-// k_lists (per-class offsets of the tiles' piece lists, and the long
-// pieces' ends) and k_pack_copy (one list per class; the gate words)
-hipError_t launch_lists(const DevTables& t, const DevWork& w, hipStream_t s);
-hipError_t launch_pack_copy(const DevWork& w, hipStream_t s,
-                            hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop);
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s);

@@ -6,12 +6,11 @@
 //                     piece-start predicate -> one start bit per byte.
 //      (k_pretok also sizes the pieces that start in its tile: pieces of
 //                     1-2 bytes are finished there, longer than 64 queued
-//                     for stage 3, the rest listed by length class in the
-//                     tile's own region.)
-//   2. k_lists / k_pack_copy gather the pieces of 2..64 bytes into one list
-//                     per length class; k_bpe_pack merges them (lowest rank
-//                     pair, leftmost first) with segmented wave reductions,
-//                     lane = byte, 64 / slot pieces of one class per wave.
+//                     for stage 3, the rest listed by length class.)
+//   2. k_bpe_pack     merges the listed pieces of 2..64 bytes (lowest rank
+//                     pair, leftmost first), one wave per work unit of one
+//                     length class: a piece per lane, per four lanes, or
+//                     (lane = byte) per slot of lanes.
 //   3. long pieces    (> 64 bytes): up to 256 bytes merged whole, one wave
 //                     each, state in registers (k_bpe_rows), up to 512 in
 //                     LDS (k_bpe_wide); longer ones are cut into short
@@ -1113,7 +1112,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   // table reads apart instead of merging them into one flat load)
   static_assert(PRETOK_TPB == 256, "one table entry per thread");
   __shared__ uint32_t ltab[256];
-  __shared__ uint32_t loff[PACK_CLASSES];  // class regions of plocal
+  // where the tile's pieces of each class go in plist
+  __shared__ uint32_t lbase[PACK_CLASSES];
   // digit groups (\p{N}{1,K}, K > 1), per word from the halo word to the
   // first word after the tile: N-class character starts, run breaks (other
   // character starts and document starts), and the N characters of the run
@@ -1125,10 +1125,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   __shared__ uint32_t o2w[4][4], o2b[4][4];
   __shared__ uint32_t o2e[4];
   const int tid = threadIdx.x;
-  if (tid < PACK_CLASSES) {
-    lcnt[tid] = 0;
-    loff[tid] = PACK_LOCAL_OFF[tid];
-  }
+  if (tid < PACK_CLASSES) lcnt[tid] = 0;
   if (tid == 0) nlong = 0;
   {
     const int32_t bid = t.byte_id[tid];
@@ -1172,7 +1169,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     for (int64_t j = dw0 + tid; j < w.clear_dwords && (j < dw1 || last);
          j += PRETOK_TPB)
       w.dirty_next[j] = 0;
-    if (blockIdx.x == 0 && tid < CTRL_WORDS) w.ctrl_next[tid] = 0;
+    if (blockIdx.x == 0)
+      for (int j = tid; j < CTRL_WORDS; j += PRETOK_TPB) w.ctrl_next[j] = 0;
   }
   const int64_t wlo = (base >> 6) - 3;
   // dm: the staged mask words hold a document start. A block without one
@@ -1777,8 +1775,11 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   if (st) atomicOr(w.status, st);
   __syncthreads();
   // Stage-2 bookkeeping for the pieces that start in this tile: finish the
-  // one- and two-byte ones, queue the long ones, list the rest by class in
-  // the tile's region of plocal (the counts are scanned by k_lists).
+  // one- and two-byte ones, queue the long ones, and list the rest by class.
+  // se (free from here) takes, per position, 0 or the listed piece's class
+  // + 1 and index among the tile's pieces of that class; the tile then takes
+  // room in its segment's class lists, one counter update per class, and
+  // writes the positions there.
   const bool two = !t.ignore_merges;
   for (int k = wv; k < PT_TILE / 64; k += PRETOK_TPB / 64) {
     const int64_t a = base + 64 * k + lane;
@@ -1786,9 +1787,9 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     int kind = piece_kind(sw[k], sw[k + 1], lane, two);
     // a literal's piece is done: its id is in tok already
     if (DM && w.lits && ((w.lits[(base >> 6) + k] >> lane) & 1)) kind = PIECE_NONE;
+    uint32_t tag = 0;
     if (kind >= 0) {
-      const uint32_t j = atomicAdd(&lcnt[kind], 1u);
-      w.plocal[(int64_t)blockIdx.x * PT_LOCAL_SLOTS + loff[kind] + j] = (uint32_t)a;
+      tag = (uint32_t)(kind + 1) | atomicAdd(&lcnt[kind], 1u) << 4;
     } else if (kind == PIECE_ONE) {
       const uint32_t id = ltab[sb[64 * k + lane + PT_PAD]] & LTAB_NOID;
       w.tok[a] = id != LTAB_NOID ? id : INVALID_ID;
@@ -1803,14 +1804,29 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
     } else if (kind == PIECE_LONG) {
       llong[atomicAdd(&nlong, 1u)] = (uint32_t)a;
     }
+    se[64 * k + lane] = tag;
   }
   __syncthreads();
-  if (tid < PACK_CLASSES) w.pblk[(int64_t)tid * gridDim.x + blockIdx.x] = lcnt[tid];
-  // queue the long pieces with one counter update per tile; their ends are
-  // filled in by k_long_prep once every start word is known
+  // (the long pieces take their room in the queue with one counter update
+  // per tile too; their ends are filled in by k_bpe_pack's first waves
+  // once every start word is known)
+  if (tid < PACK_CLASSES && lcnt[tid]) {
+    const int x = blockIdx.x % PACK_XCDS;
+    lbase[tid] = pack_seg_list(gridDim.x, x, PACK_LOCAL_OFF[tid]) +
+                 atomicAdd(&w.pseg[x * CTRL_PSEG_STRIDE + CTRL_PSEG_COUNT + tid],
+                           lcnt[tid]);
+  } else if (tid == 64 && nlong) {
+    longbase = atomicAdd(w.longcount, nlong);
+  }
+  __syncthreads();
+  {
+    const int nt = nb - base < PT_TILE ? (int)(nb - base) : PT_TILE;
+    for (int i = tid; i < nt; i += PRETOK_TPB) {
+      const uint32_t e = se[i];
+      if (e) w.plist[lbase[(e & 15) - 1] + (e >> 4)] = (uint32_t)(base + i);
+    }
+  }
   if (nlong) {
-    if (tid == 0) longbase = atomicAdd(w.longcount, nlong);
-    __syncthreads();
     for (uint32_t j = tid; j < nlong; j += PRETOK_TPB) {
       const uint32_t k = longbase + j;
       if (k < w.long_cap) {
@@ -2059,12 +2075,10 @@ __device__ __forceinline__ void window_bits(int64_t v, int phase, SegBits seg,
 
 // ---- pieces of up to 64 bytes, packed by length
 //
-// k_pretok counted the pieces of each tile by length class (pieces of
-// pack_lmin(c)..pack_slot(c) bytes); k_lists turns the counts into
-// per-tile offsets, k_pack_copy gathers the tiles' lists by class, and
-// k_bpe_pack merges them with one wave per work unit: 64 / slot pieces of
-// one class on slot lanes each. The rounds a wave runs then follow its own
-// pieces' lengths rather than the longest piece of a stretch of text.
+// k_pretok listed the pieces by length class (pieces of
+// pack_lmin(c)..pack_slot(c) bytes), and k_bpe_pack merges them with one
+// wave per work unit of one class. The rounds a wave runs then follow its
+// own pieces' lengths rather than the longest piece of a stretch of text.
 
 // end of the piece that starts at a (the next start bit; sentinel bits at
 // and past nb end the search)
@@ -2292,17 +2306,93 @@ __constant__ uint32_t PACK_GEO[PACK_CLASSES] = {
     pack_geo(10), pack_geo(11), pack_geo(12)};
 static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 
-// Work units by class (class c's list, in text order, makes uend[c] -
-// uend[c + 1] units). Workgroups go to the XCDs in turn (block b on XCD
-// b % PACK_XCDS, up to a rotation), and each XCD has its own L2: so each
-// class's units are split into PACK_XCDS contiguous runs, run x (one stretch
-// of the text) for the blocks of XCD x, and an XCD reads the text, start
-// words and lists of its own stretch only. An XCD's units go in one order,
-// class by class, longest merge chains first (PACK_ORDER, from the per-class
-// unit times of a cycle-counter probe build: the 17..32-byte groups and the
-// 9..16-byte lanes first). Wave g of the XCD's G
-// waves takes unit g first; every later unit comes from the XCD's counter
-// (pqueue, set to G by k_pack_copy), one at a time as waves finish theirs.
+// Long pieces (k_pretok queued their starts), entries k0..k0+63 of the
+// queue by one wave: their ends, and the pieces over WIDE_MAX bytes -- a
+// whole-vocabulary hit (ignore_merges), else (certification on) their
+// bytes marked in inlong for the cut / segment / certify stages. Returns
+// how many are over WIDE_MAX bytes (wave-uniform).
+constexpr int WIDE_MAX = 512;
+__device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
+                                                   const DevWork& w,
+                                                   uint32_t k0, uint32_t n,
+                                                   int lane) {
+  const uint32_t k = k0 + lane;
+  uint32_t a = 0, b = 0;
+  bool far = false;
+  if (k < n) {
+    // the end is the next start bit, found here when it lies in the
+    // piece's first two words
+    a = w.longlist[2 * k];
+    const int64_t wd = a >> 6;
+    const uint64_t gt = w.starts[wd] & ~mask_le((int)(a & 63));
+    const uint64_t nx = w.starts[wd + 1];
+    if (gt) b = (uint32_t)(wd * 64 + __builtin_ctzll(gt));
+    else if (nx) b = (uint32_t)((wd + 1) * 64 + __builtin_ctzll(nx));
+    else far = true;
+  }
+  // longer pieces: the wave reads 64 words at a time (the words pretok
+  // wrote end at nwords, and the word holding byte nb has a start bit at
+  // or after nb, so the search ends before them)
+  const int64_t nwords = (w.nb + 63) / 64 + 2;
+  for (uint64_t pend = __ballot(far); pend; pend &= pend - 1) {
+    const int j = __builtin_ctzll(pend);
+    const uint32_t pa = __shfl(a, j);
+    uint32_t end = 0;
+    for (int64_t wd = (pa >> 6) + 2;; wd += 64) {
+      const uint64_t word = wd + lane < nwords ? w.starts[wd + lane] : ~0ULL;
+      const uint64_t nz = __ballot(word != 0);
+      if (nz) {
+        const int l = __builtin_ctzll(nz);
+        const uint64_t wl = __shfl(word, l);
+        end = (uint32_t)((wd + l) * 64 + __builtin_ctzll(wl));
+        break;
+      }
+    }
+    if (lane == j) b = end;
+  }
+  if (k < n) w.longlist[2 * k + 1] = b;
+  uint64_t big = __ballot(k < n && b - a > (uint32_t)WIDE_MAX);
+  const uint32_t nbig = (uint32_t)__popcll(big);
+  while (big) {  // wave-uniform
+    const int j = __builtin_ctzll(big);
+    big &= big - 1;
+    const uint32_t pa = __shfl(a, j), pb = __shfl(b, j);
+    if (t.ignore_merges) {
+      int32_t hit = -1;
+      if (lane == 0) hit = vocab_lookup(t, w.text + pa, (int64_t)(pb - pa));
+      hit = __shfl(hit, 0);
+      if (hit >= 0) {
+        for (uint32_t p = pa + lane; p < pb; p += 64)
+          w.tok[p] = p == pa ? (uint32_t)hit : INVALID_ID;
+        continue;
+      }
+    }
+    if (!t.cert) continue;  // merged whole by k_seg_block (mode 1)
+    // mark the piece's bytes: whole words directly, the two edge words
+    // (shared with neighbouring pieces) with an atomic OR
+    const uint32_t wa = pa >> 6, wb = (pb - 1) >> 6;
+    for (uint32_t wd = wa + lane; wd <= wb; wd += 64) {
+      const uint32_t lo = wd == wa ? (pa & 63) : 0;
+      const uint32_t hi = wd == wb ? ((pb - 1) & 63) + 1 : 64;
+      const uint64_t m = lanes_in((int)lo, (int)hi);
+      if (m == ~0ULL) w.inlong[wd] = m;
+      else atomicOr(reinterpret_cast<unsigned long long*>(&w.inlong[wd]), m);
+    }
+  }
+  return nbig;
+}
+
+// Work units by class: pack_per_unit(c) pieces of class c each. Workgroups
+// go to the XCDs in turn (block b on XCD b % PACK_XCDS, up to a rotation),
+// as k_pretok's did, and each XCD has its own L2: so the blocks of residue x
+// merge segment x of the lists, the pieces of the tiles that XCD
+// pretokenized (whose text and start words it last read). An XCD's units go
+// in one order, class by class, longest merge chains first (PACK_ORDER, from
+// the per-class unit times of a cycle-counter probe build: the 17..32-byte
+// groups and the 9..16-byte lanes first). Wave g of the XCD's G waves takes
+// unit g first; every later unit comes from the segment's counter (G plus
+// the count so far, which starts at 0 in each call's control slot), one at
+// a time as waves finish theirs.
 // The long units thus all start at once, and the SIMDs end on the short
 // ones, each SIMD busy until its share is done (with a fixed share per wave
 // a SIMD holding a few long units ran on alone, latency-bound, long after
@@ -2319,50 +2409,88 @@ __constant__ int8_t PACK_ORDER[PACK_CLASSES] = {11, 9, 10, 8, 7, 6, 5, 12,
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
-  // the unit order of this block's XCD, built by wave 0: mo[k] = (the first
-  // unit of the k-th class of the order, that class's first unit in its
-  // list for this XCD's run), mk[k] = the class; mg2[c] = class c's piece
-  // count and geometry (slot | pieces per unit << 8 | pack_magic << 16 |
-  // lane / group flags); mtot = the XCD's units. Kept in LDS, not registers:
-  // the merge paths need every register they can get.
-  __shared__ uint2 mo[16];
+  // the unit order of this block's segment, built by wave 0: mo[k] = the
+  // first unit of the k-th class of the order, mk[k] = the class; mg2[c] =
+  // class c's piece count and geometry (slot | pieces per unit << 8 |
+  // pack_magic << 16 | lane / group flags), ml[c] = the start of its list;
+  // mtot = the segment's units. Kept in LDS, not registers: the merge paths
+  // need every register they can get.
+  __shared__ uint32_t mo[16];
   __shared__ uint2 mg2[16];
+  __shared__ uint32_t ml[16];
   __shared__ int32_t mk[16];
   __shared__ uint32_t mtot;
   const int lane = threadIdx.x & 63, wv = wave_id();
   const bool cl = lane < PACK_CLASSES;
+  const int x = blockIdx.x % PACK_XCDS;
+  const uint32_t* const seg = w.pseg + x * CTRL_PSEG_STRIDE;
   if (wv == 0) {
-    const int x = blockIdx.x % PACK_XCDS;
-    const uint32_t ue = cl ? w.uend[lane] : 0u;
-    const uint32_t nu = ue - (uint32_t)__shfl_down((int)ue, 1);  // class units
-    const uint32_t s0 = cl ? (uint32_t)(((uint64_t)nu * x) / PACK_XCDS) : 0u;
-    const uint32_t len = cl ? (uint32_t)(((uint64_t)nu * (x + 1)) / PACK_XCDS) - s0 : 0u;
+    const uint32_t cnt = cl ? seg[CTRL_PSEG_COUNT + lane] : 0u;
+    const uint32_t geo = cl ? PACK_GEO[lane] : 0u;
+    const uint32_t per = cl ? (geo >> 8) & 0xFF : 1u;
+    const uint32_t nu = (cnt + per - 1) / per;  // the class's units
     const int oc = cl ? PACK_ORDER[lane] : 0;
-    const uint32_t lk = cl ? (uint32_t)__shfl((int)len, oc) : 0u;
-    const uint32_t sk = (uint32_t)__shfl((int)s0, oc);
+    const uint32_t lk = cl ? (uint32_t)__shfl((int)nu, oc) : 0u;
     const uint32_t incl = wave_incl_scan(lk, lane);
     if (lane < 16) {
-      mo[lane] = make_uint2(cl ? incl - lk : ~0u, sk);
+      mo[lane] = cl ? incl - lk : ~0u;
       mk[lane] = oc;
-      mg2[lane] = make_uint2(cl ? w.pcount[lane] : 0u, cl ? PACK_GEO[lane] : 0u);
+      mg2[lane] = make_uint2(cnt, geo);
+      ml[lane] = cl ? pack_seg_list((uint32_t)pretok_tiles(w.nb), x,
+                                    PACK_LOCAL_OFF[lane])
+                    : 0u;
     }
     const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
     if (lane == 0) mtot = tot;
   }
   __syncthreads();
+  {
+    // The long pieces first, 64 a wave, by the first waves of the grid
+    // (long_prep_step). The last of them opens the gate: how many pieces
+    // are over 64 bytes and how many over WIDE_MAX, then the call's number
+    // (with no long piece, wave 0 of block 0 does).
+    constexpr uint32_t GW = PACK_BLOCKS * 4;
+    uint32_t n = *w.longcount;
+    if (n > w.long_cap) n = w.long_cap;
+    const uint32_t P = (n + 63) / 64 < GW ? (n + 63) / 64 : GW;
+    const uint32_t gw = blockIdx.x * 4 + wv;
+    if (gw < P || (P == 0 && gw == 0)) {
+      uint32_t big = 0;
+      for (uint32_t k0 = gw * 64; k0 < n; k0 += GW * 64)
+        big += long_prep_step(t, w, k0, n, lane);
+      if (lane == 0) {
+        bool last = true;
+        if (P) {
+          if (big) atomicAdd(w.nbig, big);
+          __threadfence();
+          last = atomicAdd(w.prepdone, 1u) == P - 1;
+        }
+        if (last && w.gate) {
+          __threadfence();
+          w.gate[GATE_NLONG] = n;
+          w.gate[GATE_BIG] = __hip_atomic_load(w.nbig, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+          __threadfence_system();
+          w.gate[GATE_SEQ] = w.seq;
+          __threadfence_system();
+        }
+      }
+    }
+  }
   // (values read from LDS are wave-uniform here: readfirstlane keeps them
   // in scalar registers)
   const uint32_t total = __builtin_amdgcn_readfirstlane(mtot);
-  uint32_t* const queue = w.pqueue + (blockIdx.x % PACK_XCDS) * PACK_QSTRIDE;
+  uint32_t* const queue = w.pseg + x * CTRL_PSEG_STRIDE;
+  constexpr uint32_t G = (PACK_BLOCKS / PACK_XCDS) * 4;  // waves per XCD
   uint32_t u0 = (blockIdx.x / PACK_XCDS) * 4 + wv;  // the first unit
   for (bool first_unit = true;; first_unit = false) {
     if (!first_unit) {
-      // the next unit of the XCD's order (a vector atomic by lane 0)
+      // the next unit of the segment's order (a vector atomic by lane 0)
       uint32_t got = 0;
       if (lane == 0)
         got = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
-      u0 = __builtin_amdgcn_readfirstlane(got);
+      u0 = G + __builtin_amdgcn_readfirstlane(got);
     }
     if (u0 >= total) break;  // every wave leaves once the units are taken
     // The lane index, opaque to the compiler for each unit: without it the
@@ -2373,26 +2501,24 @@ void k_bpe_pack(DevTables t, DevWork w) {
     asm volatile("" : "+v"(lane_u));
     // the unit's place in the order: the last class whose first unit is at
     // or before u0 (a class without units shares the next one's first unit)
-    const uint2 m = lane_u < PACK_CLASSES ? mo[lane_u] : make_uint2(~0u, 0u);
-    const uint64_t le = __ballot(m.x <= u0);
+    const uint32_t m = lane_u < PACK_CLASSES ? mo[lane_u] : ~0u;
+    const uint64_t le = __ballot(m <= u0);
     const int ko = 63 - __builtin_clzll(le);
-    const uint32_t kbeg = __builtin_amdgcn_readlane(m.x, ko);
-    const uint32_t s0 = __builtin_amdgcn_readlane(m.y, ko);
+    const uint32_t kbeg = __builtin_amdgcn_readlane(m, ko);
     const int c = __builtin_amdgcn_readfirstlane(mk[ko]);
-    // (the unit's index in its class list: u0 - kbeg + s0, modulo 2^32)
-    const uint32_t ubeg = kbeg - s0;
     const uint2 gc = mg2[c];
     const uint32_t cnt = __builtin_amdgcn_readfirstlane(gc.x);
     const uint32_t geo = __builtin_amdgcn_readfirstlane(gc.y);
+    const uint32_t* const list = w.plist + __builtin_amdgcn_readfirstlane(ml[c]);
     const int sl = geo & 0xFF, k = (geo >> 8) & 0xFF, mg = (geo >> 16) & 0xFFF;
-    const uint32_t first = (u0 - ubeg) * k;  // the unit's first piece
+    const uint32_t first = (u0 - kbeg) * k;  // the unit's first piece
     const int lanes = (int)(geo >> 28);
     if (lanes == 1 && t.all_bytes) {  // wave-uniform
       const uint32_t idx = first + lane_u;
       int64_t a = 0;
       int n = 0;
       if (idx < cnt) {
-        a = w.plist[w.poff[c] + idx];
+        a = list[idx];
         n = (int)(piece_end(w, a) - a);
       }
       uint32_t* ls = lds[wv];
@@ -2407,7 +2533,7 @@ void k_bpe_pack(DevTables t, DevWork w) {
       int64_t a = 0;
       int n = 0;
       if (idx < cnt) {
-        a = w.plist[w.poff[c] + idx];
+        a = list[idx];
         n = (int)(piece_end(w, a) - a);
       }
       group_bpe<8>(t, w, lds[wv], a, n, lane_u);
@@ -2421,7 +2547,7 @@ void k_bpe_pack(DevTables t, DevWork w) {
       const uint32_t idx = first + j0 + slot;
       int64_t a = 0, L = 0;
       if (slot < per && j0 + slot < k && idx < cnt) {
-        a = w.plist[w.poff[c] + idx];
+        a = list[idx];
         L = piece_end(w, a) - a;
       }
       const bool elig = off < L;
@@ -2483,7 +2609,6 @@ __global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
 // ranks; a rank flagged in unsafe_bits merges its leftmost occurrence
 // alone (src/toktier/kernels/bpe_tables.py:435-501 guard,
 // pretok_kernel.cu:1174-1186).
-constexpr int WIDE_MAX = 512;
 constexpr int WIDE_ROWS = WIDE_MAX / 64;
 constexpr uint32_t SYM_RAW = 0x80000000u;  // symbol is still its raw byte
 
@@ -3162,8 +3287,8 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     // k_pretok queued the start; the end is the next start bit, looked for
-    // here in the next 256 bytes (k_lists has not run yet: these merges
-    // start right after k_pretok). A piece without one there is longer
+    // here in the next 256 bytes (k_bpe_pack's first waves look for it
+    // too: these merges start right after k_pretok). A piece without one there is longer
     // than this kernel's, and a sentinel bit ends the search at the text's
     // end (the words past it are readable).
     const uint32_t a = w.longlist[2 * k];
@@ -3185,173 +3310,6 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
     const uint32_t* ul = lds ? unsafe_lds : nullptr;
     if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, ul);
     else wave_bpe_rows<4>(t, w, a, len, true, ul);
-  }
-}
-
-// Queued pieces over WIDE_MAX bytes: a whole-vocabulary hit
-// (ignore_merges), the serial path when certification is off, else mark
-// their bytes in inlong for the cut / segment / certify stages.
-// Long pieces (blocks blk of nblk, 256 threads each): the ends of the queued
-// starts, and the pieces over WIDE_MAX bytes -- a whole-vocabulary hit, the
-// serial merge when certification is off, else their bytes marked in
-// inlong and counted in nbig.
-__device__ void long_prep(const DevTables& t, const DevWork& w, uint32_t blk,
-                          uint32_t nblk) {
-  __shared__ uint32_t nbig;
-  if (threadIdx.x == 0) nbig = 0;
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  uint32_t n = *w.longcount;
-  if (n > w.long_cap) n = w.long_cap;
-  const uint32_t waves = nblk * 4;
-  // 64 entries per wave and step: lane j resolves entry k0 + j, then the
-  // wave handles the entries over WIDE_MAX bytes one by one
-  for (uint32_t k0 = (blk * 4 + wave_id()) * 64; k0 < n; k0 += waves * 64) {
-    const uint32_t k = k0 + lane;
-    uint32_t a = 0, b = 0;
-    bool far = false;
-    if (k < n) {
-      // k_pretok queued the start only; the end is the next start bit,
-      // found here when it lies in the piece's first two words
-      a = w.longlist[2 * k];
-      const int64_t wd = a >> 6;
-      const uint64_t gt = w.starts[wd] & ~mask_le((int)(a & 63));
-      const uint64_t nx = w.starts[wd + 1];
-      if (gt) b = (uint32_t)(wd * 64 + __builtin_ctzll(gt));
-      else if (nx) b = (uint32_t)((wd + 1) * 64 + __builtin_ctzll(nx));
-      else far = true;
-    }
-    // longer pieces: the wave reads 64 words at a time (the words pretok
-    // wrote end at nwords, and the word holding byte nb has a start bit at
-    // or after nb, so the search ends before them)
-    const int64_t nwords = (w.nb + 63) / 64 + 2;
-    for (uint64_t pend = __ballot(far); pend; pend &= pend - 1) {
-      const int j = __builtin_ctzll(pend);
-      const uint32_t pa = __shfl(a, j);
-      uint32_t end = 0;
-      for (int64_t wd = (pa >> 6) + 2;; wd += 64) {
-        const uint64_t word = wd + lane < nwords ? w.starts[wd + lane] : ~0ULL;
-        const uint64_t nz = __ballot(word != 0);
-        if (nz) {
-          const int l = __builtin_ctzll(nz);
-          const uint64_t wl = __shfl(word, l);
-          end = (uint32_t)((wd + l) * 64 + __builtin_ctzll(wl));
-          break;
-        }
-      }
-      if (lane == j) b = end;
-    }
-    if (k < n) w.longlist[2 * k + 1] = b;
-    uint64_t big = __ballot(k < n && b - a > (uint32_t)WIDE_MAX);
-    if (lane == 0 && big) atomicAdd(&nbig, (uint32_t)__popcll(big));
-    while (big) {  // wave-uniform
-      const int j = __builtin_ctzll(big);
-      big &= big - 1;
-      const uint32_t pa = __shfl(a, j), pb = __shfl(b, j);
-      if (t.ignore_merges) {
-        int32_t hit = -1;
-        if (lane == 0) hit = vocab_lookup(t, w.text + pa, (int64_t)(pb - pa));
-        hit = __shfl(hit, 0);
-        if (hit >= 0) {
-          for (uint32_t p = pa + lane; p < pb; p += 64)
-            w.tok[p] = p == pa ? (uint32_t)hit : INVALID_ID;
-          continue;
-        }
-      }
-      if (!t.cert) continue;  // merged whole by k_seg_block (mode 1)
-      // mark the piece's bytes: whole words directly, the two edge words
-      // (shared with neighbouring pieces) with an atomic OR
-      const uint32_t wa = pa >> 6, wb = (pb - 1) >> 6;
-      for (uint32_t wd = wa + lane; wd <= wb; wd += 64) {
-        const uint32_t lo = wd == wa ? (pa & 63) : 0;
-        const uint32_t hi = wd == wb ? ((pb - 1) & 63) + 1 : 64;
-        const uint64_t m = lanes_in((int)lo, (int)hi);
-        if (m == ~0ULL) w.inlong[wd] = m;
-        else atomicOr(reinterpret_cast<unsigned long long*>(&w.inlong[wd]), m);
-      }
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0 && nbig) atomicAdd(w.nbig, nbig);
-}
-
-// The piece lists, one launch after k_pretok: block c < PACK_CLASSES turns
-// class c's per-tile counts into per-tile offsets (exclusive prefix over the
-// tiles, in place) and its total; the other blocks run long_prep.
-constexpr int LONG_PREP_BLOCKS = 256;
-__global__ __launch_bounds__(256) void k_lists(DevTables t, DevWork w,
-                                               int64_t ntile) {
-  if (blockIdx.x < PACK_CLASSES) {
-    const int c = blockIdx.x;
-    uint32_t* row = w.pblk + (int64_t)c * ntile;
-    const int64_t per = (ntile + 255) / 256;
-    const int64_t lo = threadIdx.x * per, hi = lo + per < ntile ? lo + per : ntile;
-    uint32_t sum = 0;
-    for (int64_t j = lo; j < hi; ++j) sum += row[j];
-    uint32_t tot;
-    uint32_t acc = block_excl_scan(sum, &tot);
-    for (int64_t j = lo; j < hi; ++j) {
-      const uint32_t v = row[j];
-      row[j] = acc;
-      acc += v;
-    }
-    if (threadIdx.x == 0) w.pcount[c] = tot;
-    return;
-  }
-  long_prep(t, w, blockIdx.x - PACK_CLASSES, gridDim.x - PACK_CLASSES);
-}
-
-// Gathers the tiles' class lists into one list per class (tile t's pieces of
-// class c at poff[c] + its offset; the order inside a tile's share does not
-// matter: each piece is merged on its own). Block 0 also lays out
-// k_bpe_pack's work units and opens the gate: how many pieces are over 64
-// bytes (k_pretok queued them) and how many over WIDE_MAX (k_lists counted
-// them).
-__global__ __launch_bounds__(256) void k_pack_copy(DevWork w, int64_t ntile) {
-  __shared__ uint32_t cbeg[PACK_CLASSES + 1];  // prefix of the tile's counts
-  __shared__ uint32_t cdst[PACK_CLASSES], csrc[PACK_CLASSES];
-  const int tid = threadIdx.x;
-  const int64_t tl = blockIdx.x;
-  if (tid < PACK_CLASSES) {
-    const uint32_t off = w.pblk[(int64_t)tid * ntile + tl];
-    const uint32_t nxt = tl + 1 < ntile ? w.pblk[(int64_t)tid * ntile + tl + 1]
-                                        : w.pcount[tid];
-    cdst[tid] = w.poff[tid] + off;
-    csrc[tid] = PACK_LOCAL_OFF[tid];
-    cbeg[tid + 1] = nxt - off;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    cbeg[0] = 0;
-    for (int c = 0; c < PACK_CLASSES; ++c) cbeg[c + 1] += cbeg[c];
-  }
-  __syncthreads();
-  const uint32_t n = cbeg[PACK_CLASSES];
-  const uint32_t* src = w.plocal + tl * PT_LOCAL_SLOTS;
-  for (uint32_t j = tid; j < n; j += 256) {
-    int c = 0;
-#pragma unroll
-    for (int q = 1; q < PACK_CLASSES; ++q) c += j >= cbeg[q];
-    const uint32_t k = j - cbeg[c];
-    w.plist[cdst[c] + k] = src[csrc[c] + k];
-  }
-  if (blockIdx.x == 0 && tid < PACK_XCDS)  // k_bpe_pack's per-XCD counters
-    w.pqueue[tid * PACK_QSTRIDE] = (PACK_BLOCKS / PACK_XCDS) * 4;
-  if (blockIdx.x == 0 && tid == 0) {
-    uint32_t run = 0;
-#pragma unroll
-    for (int c = PACK_CLASSES - 1; c >= 0; --c) {
-      run += (w.pcount[c] + pack_per_unit(c) - 1) / pack_per_unit(c);
-      w.uend[c] = run;
-    }
-    if (w.gate) {
-      const uint32_t nl = *w.longcount;
-      w.gate[GATE_NLONG] = nl < w.long_cap ? nl : w.long_cap;
-      w.gate[GATE_BIG] = *w.nbig;
-      __threadfence_system();
-      w.gate[GATE_SEQ] = w.seq;
-      __threadfence_system();
-    }
   }
 }
 
@@ -3590,20 +3548,6 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
     w.dirty_cur[v] = w.dirty_next[v];
     w.dirty_next[v] = 0;
   }
-}
-
-hipError_t launch_lists(const DevTables& t, const DevWork& w, hipStream_t s) {
-  const int64_t ntile = pretok_tiles(w.nb);
-  hipLaunchKernelGGL(k_lists, dim3(PACK_CLASSES + LONG_PREP_BLOCKS), dim3(256),
-                     0, s, t, w, ntile);
-  return hipGetLastError();
-}
-
-hipError_t launch_pack_copy(const DevWork& w, hipStream_t s, hipEvent_t stop) {
-  const int64_t ntile = pretok_tiles(w.nb);
-  launch_ev(k_pack_copy, dim3((uint32_t)ntile), dim3(256), s, nullptr, stop, w,
-            ntile);
-  return hipGetLastError();
 }
 
 // Pieces of 65..WIDE_MAX bytes are merged whole, one wave each. Up to 256

@@ -185,7 +185,6 @@ struct Workspace {
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
   uint32_t *blkcount = nullptr, *blkprefix = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
-  uint32_t *pblk = nullptr, *plocal = nullptr, *pqueue = nullptr;
   int32_t *nx = nullptr, *pv = nullptr;
   size_t long_pairs = 0, seg_pairs = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
@@ -194,7 +193,7 @@ struct Workspace {
 
 // Lays a workspace for `cap` input bytes out at `base` (each buffer
 // 256-byte aligned) and returns the bytes it spans; base == nullptr only
-// sizes it. About 80 bytes per input byte.
+// sizes it. About 70 bytes per input byte.
 size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   size_t at = 0;
   auto take = [&](auto*& p, size_t count) {
@@ -229,14 +228,11 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.blkcount, nblk);
   take(w.blkprefix, nblk);
   take(w.cstat, nblk);
-  take(w.plist, (size_t)tk::pack_off((int64_t)cap, tk::PACK_CLASSES));
-  take(w.pblk, (size_t)tk::PACK_CLASSES * tiles);
-  take(w.plocal, (size_t)tk::PT_LOCAL_SLOTS * tiles);
+  take(w.plist, (size_t)tk::PT_LOCAL_SLOTS * tiles);
   take(w.lits, words);
   take(w.litb, words);
   take(w.docmask_lit, words);
   take(w.nrun, 3 * (size_t)tiles);
-  take(w.pqueue, (size_t)tk::PACK_XCDS * tk::PACK_QSTRIDE);
   w.cap = cap;
   w.tiles = (size_t)tiles;
   w.long_pairs = long_cap;
@@ -416,15 +412,10 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.npass = ctrl + tk::CTRL_PASS;
   w.dirty_cur = ws.dirty_cur;
   w.dirty_next = ws.dirty_next;
-  w.plist = ws.plist;
-  w.plocal = ws.plocal;
-  for (int c = 0; c < tk::PACK_CLASSES; ++c)
-    w.poff[c] = (uint32_t)tk::pack_off((int64_t)nb, c);  // < 2^32 for nb <= 1 GiB
-  w.pblk = ws.pblk;
-  w.pcount = ctrl + tk::CTRL_PCOUNT;
-  w.uend = ctrl + tk::CTRL_UEND;
+  w.plist = ws.plist;  // (tiles * PT_LOCAL_SLOTS < 2^32 for nb <= 1 GiB)
+  w.pseg = ctrl + tk::CTRL_PSEG;
   w.nbig = ctrl + tk::CTRL_BIG;
-  w.pqueue = ws.pqueue;
+  w.prepdone = ctrl + tk::CTRL_PREP;
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
@@ -466,7 +457,7 @@ int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
   return TK_OK;
 }
 
-// Wait until k_pack_copy of call `seq` has written the gate words (a
+// Wait until k_bpe_pack of call `seq` has written the gate words (a
 // spin on host memory). A device fault would stop the writer, so after a
 // generous bound the stream is synchronized to surface its error.
 int wait_gate(tk_engine* e, uint32_t seq, hipStream_t s) {
@@ -515,8 +506,8 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   uint32_t* ctrl = ws.ctrl + ws.slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
   // Timing mode 1, stage boundaries taken by the dispatches themselves:
-  // ev[0] start of k_pretok; ev[1] end of the piece listing (k_lists,
-  // k_pack_copy); ev[2] end of k_bpe_pack; ev[3] end of the
+  // ev[0] start of k_added or k_pretok; ev[1] end of k_pretok (the pieces
+  // listed); ev[2] end of k_bpe_pack; ev[3] end of the
   // long-piece stages on the side stream (when there are long pieces); ev[4] end
   // of the compaction. Mode 2: ev[1] / ev[2] are the start / end of
   // k_bpe_pack's own dispatch only. (Each timed dispatch delays the next
@@ -524,36 +515,39 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   // they can.)
   const bool stages = e->timing == 1, packonly = e->timing == 2;
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
+  // (the end of k_pretok is recorded by its own dispatch, no marker packet
+  // before k_bpe_pack: in ev[1] when the stages are timed, else ev_pretok)
+  hipEvent_t pe = stages ? ev[1] : e->ev_pretok;
   if (literals) {
     HIP_TRY(tk::launch_added(*docs, w, host_dm, s, at(0)));
-    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, nullptr));
+    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, pe));
   } else {
-    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), nullptr));
+    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), pe));
   }
   // The merges of pieces of 65..256 bytes need k_pretok alone (the queued
   // starts and the start bits): on the side stream from here, beside the
-  // piece lists and the packed merge (the device reads the count; no host
-  // decision waits for them).
-  HIP_TRY(hipEventRecord(e->ev_pretok, s));
-  HIP_TRY(hipStreamWaitEvent(e->stream2, e->ev_pretok, 0));
-  HIP_TRY(tk::launch_bpe_rows(e->t, w, e->stream2));
+  // packed merge (the device reads the count; no host decision waits for
+  // them). k_bpe_pack leaves them a wave slot on every SIMD.
+  hipStream_t s2 = e->stream2, s3 = e->stream3;
+  HIP_TRY(hipStreamWaitEvent(s2, pe, 0));
+  HIP_TRY(tk::launch_bpe_rows(e->t, w, s2));
   ws.slot ^= 1;  // this call's k_pretok clears the other slot
-  HIP_TRY(tk::launch_lists(e->t, w, s));
-  HIP_TRY(tk::launch_pack_copy(w, s, at(1)));  // k_pack_copy writes the gate
+  // (k_bpe_pack's first waves resolve the long pieces' ends and open the
+  // gate before they take their work units)
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
                               stages || packonly ? ev[2] : nullptr));
   // The gate words tell, while the packed merge runs, how many pieces are
   // over 64 bytes and whether any is over WIDE_MAX. Only then do the
-  // long-piece stages go on the side stream, beside k_bpe_pack: they need
-  // k_lists alone, which ran before k_pack_copy opened the gate, so no
-  // event orders them (and none is needed when there is no long piece).
+  // long-piece stages go on the side streams, beside k_bpe_pack: they need
+  // the long pieces' ends alone, which the device had written and made
+  // visible before it opened the gate, so no event orders them (and none is
+  // needed when there is no long piece).
   int grc = wait_gate(e, w.seq, s);
   if (grc != TK_OK) return grc;
   const uint32_t nlong = e->gate[tk::GATE_NLONG];
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
-  hipStream_t s2 = e->stream2;
   if (nlong > 0) {
     // two independent jobs on two side streams: pieces of 65..WIDE_MAX
     // bytes merged whole (k_bpe_rows already queued), and the cut /
@@ -567,7 +561,6 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     if (big) {
       // cut / segment / certify, then the repair passes, all on their own
       // stream beside the packed merge and the wide merges
-      hipStream_t s3 = e->stream3;
       HIP_TRY(tk::launch_long_windows(e->t, w, s3));
       HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
@@ -905,7 +898,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
                                                 hipEventDisableSystemFence) != hipSuccess ||
       hipEventCreateWithFlags(&e->ev_pretok, hipEventDisableTiming |
-                                                hipEventDisableSystemFence) != hipSuccess)
+                                                hipEventDisableSystemFence) != hipSuccess )
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
