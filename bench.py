@@ -480,7 +480,7 @@ def main() -> int:
     names = ["pretokenize and piece lists (k_added, k_pretok)",
              "k_bpe_pack",
              "long pieces past k_bpe_pack (k_bpe_rows, k_bpe_wide, k_long_*, "
-             "k_certify; side stream)",
+             "k_certify; side streams)",
              "compaction (k_compact)"]
     avg = st[:, :4].mean(axis=0)
     pack_avg_us = float(np.mean(pack_us))

@@ -127,6 +127,8 @@ struct DevWork {
   uint32_t* pseg;        // ctrl + CTRL_PSEG: per segment, k_bpe_pack's unit
                          // counter and the pieces listed per class
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
+  uint32_t* nrows;       // queued pieces of 129..256 bytes (ctrl)
+  uint32_t* nwide;       // queued pieces of 257..WIDE_MAX bytes (ctrl)
   uint32_t* prepdone;    // k_bpe_pack waves done with the long pieces (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
@@ -161,16 +163,17 @@ constexpr uint64_t HR_FIRST = 1ull << 31, HR_LAST = 1ull << 30;
 // line the pieces listed per class, at CTRL_PSEG_COUNT + class)
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PASS = 7,
-              CTRL_FAIL2 = 8, CTRL_PREP = 9, CTRL_PSEG = 64, CTRL_PSEG_STRIDE = 64,
+              CTRL_FAIL2 = 8, CTRL_PREP = 9, CTRL_WIDE = 10, CTRL_ROWS = 11,
+              CTRL_PSEG = 64, CTRL_PSEG_STRIDE = 64,
               CTRL_PSEG_COUNT = 32, CTRL_WORDS = CTRL_PSEG + 8 * CTRL_PSEG_STRIDE;
-// gate words in host memory: k_bpe_pack writes GATE_NLONG / GATE_BIG and
-// then GATE_SEQ (the host learns, while the packed merge runs, whether the
-// long-piece stages have any work), k_compact's last block
-// writes the request's outcome (status, id count, failed cuts) and then
-// GATE_DONE, so no copy is needed to read it
+// gate words in host memory: k_bpe_pack writes GATE_NLONG / GATE_NROWS /
+// GATE_NWIDE / GATE_BIG and then GATE_SEQ (the host learns, while the packed merge runs,
+// whether the side streams' long-piece stages have any work), k_compact's
+// last block writes the request's outcome (status, id count, failed cuts)
+// and then GATE_DONE, so no copy is needed to read it
 constexpr int GATE_SEQ = 0, GATE_BIG = 1, GATE_STATUS = 2, GATE_TOTAL = 3,
               GATE_FAIL = 4, GATE_DONE = 5, GATE_NLONG = 6, GATE_NLIT = 7,
-              GATE_PASS = 8, GATE_WORDS = 16;
+              GATE_PASS = 8, GATE_NWIDE = 9, GATE_NROWS = 10, GATE_WORDS = 16;
 
 // Added-token literals on the device: the trie over their bytes, stored as
 // one hash table of its edges. Slot = key << 36 | child << 16 | term, key =
@@ -202,8 +205,8 @@ __host__ __device__ __forceinline__ uint32_t added_slot(uint32_t key,
   return (uint32_t)(((uint64_t)(key * 0x9E3779B1u) * size) >> 32);
 }
 // packed short-piece BPE: grid of k_bpe_pack, seven waves on every SIMD
-// (blocks of four waves, 256 CUs); the eighth wave slot is left to
-// k_bpe_rows, which runs beside it from the end of k_pretok
+// (blocks of four waves, 256 CUs); the eighth wave slot is left to the
+// side streams' long-piece kernels, which run beside it
 constexpr int PACK_BLOCKS = 1792;
 // The piece lists come in PACK_XCDS segments: segment x holds the pieces of
 // the k_pretok tiles b with b % PACK_XCDS == x (those of one XCD: workgroups
@@ -288,7 +291,8 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
                          hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop);
-hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s);
+hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
+                           uint32_t nlong);
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop, uint32_t nlong);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,

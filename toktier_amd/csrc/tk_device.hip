@@ -10,10 +10,12 @@
 //   2. k_bpe_pack     merges the listed pieces of 2..64 bytes (lowest rank
 //                     pair, leftmost first), one wave per work unit of one
 //                     length class: a piece per lane, per four lanes, or
-//                     (lane = byte) per slot of lanes.
-//   3. long pieces    (> 64 bytes): up to 256 bytes merged whole, one wave
-//                     each, state in registers (k_bpe_rows), up to 512 in
-//                     LDS (k_bpe_wide); longer ones are cut into short
+//                     (lane = byte) per slot of lanes; and, first, the long
+//                     pieces of up to 128 bytes, one wave each, state in
+//                     registers (wave_bpe_rows).
+//   3. longer pieces  (side streams): up to 256 bytes merged whole, one
+//                     wave each, state in registers (k_bpe_rows), up to 512
+//                     in LDS (k_bpe_wide); longer ones are cut into short
 //                     segments at likely token boundaries (k_long_windows),
 //                     merged segment by segment with boundary-token
 //                     histories (k_long_segments), and every cut is
@@ -2310,12 +2312,14 @@ static_assert(PACK_CLASSES == 13, "PACK_GEO lists every class");
 // queue by one wave: their ends, and the pieces over WIDE_MAX bytes -- a
 // whole-vocabulary hit (ignore_merges), else (certification on) their
 // bytes marked in inlong for the cut / segment / certify stages. Returns
-// how many are over WIDE_MAX bytes (wave-uniform).
+// how many are over WIDE_MAX bytes, and adds to nrows and nwide how many
+// have 129..256 and 257..WIDE_MAX (wave-uniform).
 constexpr int WIDE_MAX = 512;
 __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
                                                    const DevWork& w,
                                                    uint32_t k0, uint32_t n,
-                                                   int lane) {
+                                                   int lane, uint32_t& nrows,
+                                                   uint32_t& nwide) {
   const uint32_t k = k0 + lane;
   uint32_t a = 0, b = 0;
   bool far = false;
@@ -2351,6 +2355,9 @@ __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
     if (lane == j) b = end;
   }
   if (k < n) w.longlist[2 * k + 1] = b;
+  nrows += (uint32_t)__popcll(__ballot(k < n && b - a > 128u && b - a <= 256u));
+  nwide += (uint32_t)__popcll(
+      __ballot(k < n && b - a > 256u && b - a <= (uint32_t)WIDE_MAX));
   uint64_t big = __ballot(k < n && b - a > (uint32_t)WIDE_MAX);
   const uint32_t nbig = (uint32_t)__popcll(big);
   while (big) {  // wave-uniform
@@ -2382,6 +2389,13 @@ __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
   return nbig;
 }
 
+// (defined with the long-piece merges below)
+template <int R>
+__device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
+                                              const DevWork& w, uint32_t a,
+                                              int len, bool vocab_first,
+                                              const uint32_t* unsafe_lds);
+
 // Work units by class: pack_per_unit(c) pieces of class c each. Workgroups
 // go to the XCDs in turn (block b on XCD b % PACK_XCDS, up to a rotation),
 // as k_pretok's did, and each XCD has its own L2: so the blocks of residue x
@@ -2392,7 +2406,12 @@ __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
 // groups and the 9..16-byte lanes first). Wave g of the XCD's G waves takes
 // unit g first; every later unit comes from the segment's counter (G plus
 // the count so far, which starts at 0 in each call's control slot), one at
-// a time as waves finish theirs.
+// a time as waves finish theirs. Ahead of the classes in every XCD's order
+// come the queued long pieces of 65..128 bytes (entries k of the long-piece
+// queue with k % PACK_XCDS == x), one per unit, merged by the wave with its
+// state in registers (wave_bpe_rows): the longest chains of all. (Longer
+// ones go to the side streams: the 256-byte instance does not fit this
+// kernel's registers.)
 // The long units thus all start at once, and the SIMDs end on the short
 // ones, each SIMD busy until its share is done (with a fixed share per wave
 // a SIMD holding a few long units ran on alone, latency-bound, long after
@@ -2410,11 +2429,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void k_bpe_pack(DevTables t, DevWork w) {
   __shared__ uint32_t lds[4][PACK_LANE_MAX * 64];
   // the unit order of this block's segment, built by wave 0: mo[k] = the
-  // first unit of the k-th class of the order, mk[k] = the class; mg2[c] =
-  // class c's piece count and geometry (slot | pieces per unit << 8 |
-  // pack_magic << 16 | lane / group flags), ml[c] = the start of its list;
-  // mtot = the segment's units. Kept in LDS, not registers: the merge paths
-  // need every register they can get.
+  // first unit of the k-th class of the order, mk[k] = the class
+  // (PACK_CLASSES: the long pieces, k = 0); mg2[c] = class c's piece count
+  // and geometry (slot | pieces per unit << 8 | pack_magic << 16 | lane /
+  // group flags), ml[c] = the start of its list; mtot = the segment's
+  // units. Kept in LDS, not registers: the merge paths need every register
+  // they can get.
   __shared__ uint32_t mo[16];
   __shared__ uint2 mg2[16];
   __shared__ uint32_t ml[16];
@@ -2424,16 +2444,22 @@ void k_bpe_pack(DevTables t, DevWork w) {
   const bool cl = lane < PACK_CLASSES;
   const int x = blockIdx.x % PACK_XCDS;
   const uint32_t* const seg = w.pseg + x * CTRL_PSEG_STRIDE;
+  uint32_t nl = *w.longcount;  // queued long pieces
+  if (nl > w.long_cap) nl = w.long_cap;
   if (wv == 0) {
     const uint32_t cnt = cl ? seg[CTRL_PSEG_COUNT + lane] : 0u;
     const uint32_t geo = cl ? PACK_GEO[lane] : 0u;
     const uint32_t per = cl ? (geo >> 8) & 0xFF : 1u;
     const uint32_t nu = (cnt + per - 1) / per;  // the class's units
-    const int oc = cl ? PACK_ORDER[lane] : 0;
-    const uint32_t lk = cl ? (uint32_t)__shfl((int)nu, oc) : 0u;
+    // order position k: 0 the long pieces, k >= 1 class PACK_ORDER[k - 1]
+    const bool ko = lane <= PACK_CLASSES;
+    const int oc = lane == 0 ? PACK_CLASSES : ko ? PACK_ORDER[lane - 1] : 0;
+    const uint32_t nuo = (uint32_t)__shfl((int)nu, oc);
+    const uint32_t nr = nl > (uint32_t)x ? (nl - x + PACK_XCDS - 1) / PACK_XCDS : 0u;
+    const uint32_t lk = lane == 0 ? nr : ko ? nuo : 0u;
     const uint32_t incl = wave_incl_scan(lk, lane);
     if (lane < 16) {
-      mo[lane] = cl ? incl - lk : ~0u;
+      mo[lane] = ko ? incl - lk : ~0u;
       mk[lane] = oc;
       mg2[lane] = make_uint2(cnt, geo);
       ml[lane] = cl ? pack_seg_list((uint32_t)pretok_tiles(w.nb), x,
@@ -2450,24 +2476,29 @@ void k_bpe_pack(DevTables t, DevWork w) {
     // are over 64 bytes and how many over WIDE_MAX, then the call's number
     // (with no long piece, wave 0 of block 0 does).
     constexpr uint32_t GW = PACK_BLOCKS * 4;
-    uint32_t n = *w.longcount;
-    if (n > w.long_cap) n = w.long_cap;
+    const uint32_t n = nl;
     const uint32_t P = (n + 63) / 64 < GW ? (n + 63) / 64 : GW;
     const uint32_t gw = blockIdx.x * 4 + wv;
     if (gw < P || (P == 0 && gw == 0)) {
-      uint32_t big = 0;
+      uint32_t big = 0, rows = 0, wide = 0;
       for (uint32_t k0 = gw * 64; k0 < n; k0 += GW * 64)
-        big += long_prep_step(t, w, k0, n, lane);
+        big += long_prep_step(t, w, k0, n, lane, rows, wide);
       if (lane == 0) {
         bool last = true;
         if (P) {
           if (big) atomicAdd(w.nbig, big);
+          if (rows) atomicAdd(w.nrows, rows);
+          if (wide) atomicAdd(w.nwide, wide);
           __threadfence();
           last = atomicAdd(w.prepdone, 1u) == P - 1;
         }
         if (last && w.gate) {
           __threadfence();
           w.gate[GATE_NLONG] = n;
+          w.gate[GATE_NROWS] = __hip_atomic_load(w.nrows, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+          w.gate[GATE_NWIDE] = __hip_atomic_load(w.nwide, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
           w.gate[GATE_BIG] = __hip_atomic_load(w.nbig, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
           __threadfence_system();
@@ -2501,11 +2532,34 @@ void k_bpe_pack(DevTables t, DevWork w) {
     asm volatile("" : "+v"(lane_u));
     // the unit's place in the order: the last class whose first unit is at
     // or before u0 (a class without units shares the next one's first unit)
-    const uint32_t m = lane_u < PACK_CLASSES ? mo[lane_u] : ~0u;
+    const uint32_t m = lane_u <= PACK_CLASSES ? mo[lane_u] : ~0u;
     const uint64_t le = __ballot(m <= u0);
     const int ko = 63 - __builtin_clzll(le);
     const uint32_t kbeg = __builtin_amdgcn_readlane(m, ko);
     const int c = __builtin_amdgcn_readfirstlane(mk[ko]);
+    if (c == PACK_CLASSES) {  // wave-uniform: a queued long piece
+      // its end is the next start bit, looked for here in the next 128
+      // bytes (the first waves may not have written it yet); a piece
+      // without one there is longer, left to the side streams, and a
+      // sentinel bit ends the search at the text's end
+      const uint32_t a = w.longlist[2 * ((u0 - kbeg) * PACK_XCDS + x)];
+      int len = 129;
+      {
+        const int64_t wd = a >> 6;
+        uint64_t word = w.starts[wd] & ~mask_le((int)(a & 63));
+#pragma unroll
+        for (int j = 1; j <= 3 && len > 128; ++j) {
+          if (word) {
+            const int64_t e = (wd + j - 1) * 64 + __builtin_ctzll(word);
+            len = e - a <= 128 ? (int)(e - a) : 129;
+            break;
+          }
+          word = w.starts[wd + j];
+        }
+      }
+      if (len > 64 && len <= 128) wave_bpe_rows<2>(t, w, a, len, true, nullptr);
+      continue;
+    }
     const uint2 gc = mg2[c];
     const uint32_t cnt = __builtin_amdgcn_readfirstlane(gc.x);
     const uint32_t geo = __builtin_amdgcn_readfirstlane(gc.y);
@@ -3084,9 +3138,10 @@ __device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
 // lookups for the positions whose pair changed (the winners and the live
 // positions before them).
 template <int R>
-__device__ void wave_bpe_rows(const DevTables& t, const DevWork& w, uint32_t a,
-                              int len, bool vocab_first,
-                              const uint32_t* unsafe_lds) {
+__device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
+                                              const DevWork& w, uint32_t a,
+                                              int len, bool vocab_first,
+                                              const uint32_t* unsafe_lds) {
   const int lane = threadIdx.x & 63;
   if (vocab_first && t.ignore_merges) {
     int32_t hit = -1;
@@ -3257,21 +3312,19 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
-    // (pieces of up to 256 bytes without histories: k_bpe_rows)
+    // (pieces of up to 256 bytes without histories: k_bpe_pack, k_bpe_rows)
     if (len <= (hist ? 64 : 256) || len > WIDE_MAX) continue;  // wave-uniform
     wave_bpe_wide(t, w, a, len, !hist, hist != 0, lds[wv]);
   }
 }
 
-// Long-list entries of 65..256 bytes (no histories), one wave each, state in
-// registers.
-// With an unsafe-rank bitmap of at most ROWS_UNSAFE_LDS words, the launch
-// gives each block a copy of it in LDS (one lookup per merge round).
+// Long-queue entries of 129..256 bytes, one wave each, state in registers
+// (those of 65..128 bytes were merged by k_bpe_pack). With an unsafe-rank
+// bitmap of at most ROWS_UNSAFE_LDS words, the launch gives each block a
+// copy of it in LDS (one lookup per merge round).
 constexpr uint32_t ROWS_UNSAFE_LDS = 12288;
 __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   extern __shared__ uint32_t unsafe_lds[];
-  // (launched before the host knows how many pieces there are: a block
-  // without one leaves at once)
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   if (blockIdx.x * 4 >= n) return;
@@ -3284,32 +3337,12 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
   // few, latency-bound waves beside k_bpe_pack on the same SIMDs
-  if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
+  __builtin_amdgcn_s_setprio(3);
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
-    // k_pretok queued the start; the end is the next start bit, looked for
-    // here in the next 256 bytes (k_bpe_pack's first waves look for it
-    // too: these merges start right after k_pretok). A piece without one there is longer
-    // than this kernel's, and a sentinel bit ends the search at the text's
-    // end (the words past it are readable).
-    const uint32_t a = w.longlist[2 * k];
-    int len = 257;
-    {
-      const int64_t wd = a >> 6;
-      uint64_t word = w.starts[wd] & ~mask_le((int)(a & 63));
-#pragma unroll
-      for (int j = 1; j <= 5 && len > 256; ++j) {
-        if (word) {
-          const int64_t e = (wd + j - 1) * 64 + __builtin_ctzll(word);
-          len = e - a <= 256 ? (int)(e - a) : 257;
-          break;
-        }
-        word = w.starts[wd + j];
-      }
-    }
-    if (len <= 64 || len > 256) continue;  // wave-uniform
-    const uint32_t* ul = lds ? unsafe_lds : nullptr;
-    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, ul);
-    else wave_bpe_rows<4>(t, w, a, len, true, ul);
+    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    const int len = (int)(b - a);
+    if (len <= 128 || len > 256) continue;  // wave-uniform
+    wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
   }
 }
 
@@ -3550,22 +3583,19 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   }
 }
 
-// Pieces of 65..WIDE_MAX bytes are merged whole, one wave each. Up to 256
-// bytes in registers (k_bpe_rows): launched right after k_pretok, before the
-// host knows the count (the most blocks a count can use; those past it
-// leave at once), so these latency-bound merges run beside the piece lists
-// and the packed merge.
-constexpr uint32_t ROWS_BLOCKS = 2048;
-hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s) {
+// Pieces of 129..256 bytes (k_bpe_rows) and of 257..WIDE_MAX bytes
+// (k_bpe_wide, state in LDS) are merged whole, one wave each, once the host
+// knows there are any (a wave per queued piece, up to 2048 blocks of four;
+// those of 65..128 bytes were merged by k_bpe_pack).
+hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
+                           uint32_t nlong) {
+  const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
   const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
                          ? (size_t)t.unsafe_words * 4 : 0;
-  hipLaunchKernelGGL(k_bpe_rows, dim3(ROWS_BLOCKS), dim3(256), lds, s, t, w);
+  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, t, w);
   return hipGetLastError();
 }
 
-// Longer ones with their state in LDS (k_bpe_wide), once the host knows
-// there are pieces over 64 bytes (a wave per queued piece, up to 2048
-// blocks of four).
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop, uint32_t nlong) {
   const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;

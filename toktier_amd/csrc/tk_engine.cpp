@@ -287,9 +287,8 @@ struct tk_engine {
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
   hipEvent_t ev_join = nullptr;  // side stream -> engine stream
-  hipEvent_t ev_pretok = nullptr;  // engine stream (k_pretok done) -> side stream
   // pieces over WIDE_MAX bytes (cut / segment / certify) on a stream of
-  // their own, beside the 65..WIDE_MAX-byte merges of stream2
+  // their own, beside the 129..WIDE_MAX-byte merges of stream2
   hipStream_t stream3 = nullptr;
   hipEvent_t ev_join3 = nullptr;
   // host-to-host entries: pinned staging of the request bytes and of the
@@ -416,6 +415,8 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.pseg = ctrl + tk::CTRL_PSEG;
   w.nbig = ctrl + tk::CTRL_BIG;
   w.prepdone = ctrl + tk::CTRL_PREP;
+  w.nwide = ctrl + tk::CTRL_WIDE;
+  w.nrows = ctrl + tk::CTRL_ROWS;
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
@@ -508,52 +509,48 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   // Timing mode 1, stage boundaries taken by the dispatches themselves:
   // ev[0] start of k_added or k_pretok; ev[1] end of k_pretok (the pieces
   // listed); ev[2] end of k_bpe_pack; ev[3] end of the
-  // long-piece stages on the side stream (when there are long pieces); ev[4] end
+  // long-piece stages on the side streams (when they have work); ev[4] end
   // of the compaction. Mode 2: ev[1] / ev[2] are the start / end of
   // k_bpe_pack's own dispatch only. (Each timed dispatch delays the next
   // one by a few microseconds, so the events sit on as few dispatches as
   // they can.)
   const bool stages = e->timing == 1, packonly = e->timing == 2;
   auto at = [&](int k) { return stages ? ev[k] : nullptr; };
-  // (the end of k_pretok is recorded by its own dispatch, no marker packet
-  // before k_bpe_pack: in ev[1] when the stages are timed, else ev_pretok)
-  hipEvent_t pe = stages ? ev[1] : e->ev_pretok;
   if (literals) {
     HIP_TRY(tk::launch_added(*docs, w, host_dm, s, at(0)));
-    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, pe));
+    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, at(1)));
   } else {
-    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), pe));
+    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
   }
-  // The merges of pieces of 65..256 bytes need k_pretok alone (the queued
-  // starts and the start bits): on the side stream from here, beside the
-  // packed merge (the device reads the count; no host decision waits for
-  // them). k_bpe_pack leaves them a wave slot on every SIMD.
   hipStream_t s2 = e->stream2, s3 = e->stream3;
-  HIP_TRY(hipStreamWaitEvent(s2, pe, 0));
-  HIP_TRY(tk::launch_bpe_rows(e->t, w, s2));
   ws.slot ^= 1;  // this call's k_pretok clears the other slot
   // (k_bpe_pack's first waves resolve the long pieces' ends and open the
-  // gate before they take their work units)
+  // gate before they take their work units; its first units are the long
+  // pieces of up to 128 bytes)
   HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
                               stages || packonly ? ev[2] : nullptr));
   // The gate words tell, while the packed merge runs, how many pieces are
-  // over 64 bytes and whether any is over WIDE_MAX. Only then do the
-  // long-piece stages go on the side streams, beside k_bpe_pack: they need
-  // the long pieces' ends alone, which the device had written and made
-  // visible before it opened the gate, so no event orders them (and none is
-  // needed when there is no long piece).
+  // over 64 bytes, how many of them have 129..256 bytes, 257..WIDE_MAX bytes
+  // and more. Only then do the stages of those pieces go on the side streams,
+  // beside k_bpe_pack, and only those with work: they need the long
+  // pieces' ends alone, which the device had written and made visible
+  // before it opened the gate, so no event orders them.
   int grc = wait_gate(e, w.seq, s);
   if (grc != TK_OK) return grc;
   const uint32_t nlong = e->gate[tk::GATE_NLONG];
+  const uint32_t nrows = e->gate[tk::GATE_NROWS];
+  const uint32_t nwide = e->gate[tk::GATE_NWIDE];
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
-  if (nlong > 0) {
-    // two independent jobs on two side streams: pieces of 65..WIDE_MAX
-    // bytes merged whole (k_bpe_rows already queued), and the cut /
-    // segment / certify path of the longer ones (they touch disjoint bytes
-    // and read the same lists)
-    HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
+  const bool side2 = nrows > 0 || nwide > 0 ||
+                     (!e->t.cert && e->gate[tk::GATE_BIG] > 0);
+  {
+    // two independent jobs on two side streams: pieces of 129..WIDE_MAX
+    // bytes merged whole, and the cut / segment / certify path of the
+    // longer ones (they touch disjoint bytes and read the same lists)
+    if (nrows > 0) HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong));
+    if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     // (a table that drops bytes merges its pieces over WIDE_MAX bytes
     // whole, a workgroup each, after the wide merges)
     if (!e->t.cert && e->gate[tk::GATE_BIG] > 0)
@@ -574,16 +571,19 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       HIP_TRY(hipStreamWaitEvent(s, e->ev_join3, 0));
     }
   }
-  // (k_bpe_rows is on the side stream in every call: always joined)
-  HIP_TRY(hipEventRecord(e->ev_join, s2));
-  HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
-  // (the end of both side streams, or of the packed merge if later)
-  if (stages && nlong > 0) HIP_TRY(hipEventRecord(ev[3], s));
+  if (side2) {
+    HIP_TRY(hipEventRecord(e->ev_join, s2));
+    HIP_TRY(hipStreamWaitEvent(s, e->ev_join, 0));
+  }
+  // (the end of the side streams, or of the packed merge if later)
+  const bool side = side2 || big;
+  if (stages && side) HIP_TRY(hipEventRecord(ev[3], s));
   // the compaction reports the failed cuts left after the last queued pass
   tk::DevWork wc = w;
   if (big) wc.nfail = fail_count(ctrl, DEV_REPAIRS);
   HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag, nullptr, at(4)));
-  // k_scan has left the outcome in the gate words: no read-back copy
+  // k_compact's last block has left the outcome in the gate words: no
+  // read-back copy
   HIP_TRY(hipStreamSynchronize(s));
   uint32_t* h = e->host_ctrl;
   if (e->gate[tk::GATE_DONE] != w.seq)
@@ -601,7 +601,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
     const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
-    const double t3 = nlong > 0 ? elapsed_us(ev[0], ev[3]) : 0.0;
+    const double t3 = side ? elapsed_us(ev[0], ev[3]) : 0.0;
     const double t4 = elapsed_us(ev[0], ev[4]);
     e->last_us[0] = t1;
     e->last_us[1] = t2 - t1;
@@ -896,9 +896,7 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   if (hipEventCreateWithFlags(&e->ev_join, hipEventDisableTiming |
                                                hipEventDisableSystemFence) != hipSuccess ||
       hipEventCreateWithFlags(&e->ev_join3, hipEventDisableTiming |
-                                                hipEventDisableSystemFence) != hipSuccess ||
-      hipEventCreateWithFlags(&e->ev_pretok, hipEventDisableTiming |
-                                                hipEventDisableSystemFence) != hipSuccess )
+                                                hipEventDisableSystemFence) != hipSuccess)
     return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   for (auto& ev : e->ev)
     // timing-only events: no system-scope fence between the stages
@@ -1034,7 +1032,6 @@ void tk_engine_close(tk_engine* e) {
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->ev_join3) (void)hipEventDestroy(e->ev_join3);
-  if (e->ev_pretok) (void)hipEventDestroy(e->ev_pretok);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (e->stream2) (void)hipStreamDestroy(e->stream2);
   if (e->stream3) (void)hipStreamDestroy(e->stream3);
