@@ -36,6 +36,10 @@ _GPU_OUTCOMES = {"passed": 0, "failed": 0, "skipped": 0}
 # GPU tests that cover no single family
 _FAMILY_OUTCOMES: dict[str, dict[str, int]] = {}
 _SELECTION = {"deselected_gpu": 0}
+# GPU tests parked in the source with an explicit skip mark and its reason
+# (listed in the evidence by node id; any other skip blocks certification)
+_PARKED: set[str] = set()
+_PARKED_SEEN: list[str] = []
 
 
 def _family_of(nodeid: str) -> str:
@@ -51,6 +55,9 @@ def pytest_runtest_logreport(report):
     if "gpu" not in report.keywords:
         return
     if report.when == "call" or (report.when == "setup" and not report.passed):
+        if report.skipped and report.nodeid in _PARKED:
+            _PARKED_SEEN.append(report.nodeid)
+            return
         key = ("passed" if report.passed else
                "skipped" if report.skipped else "failed")
         _GPU_OUTCOMES[key] += 1
@@ -101,6 +108,7 @@ def pytest_sessionfinish(session, exitstatus):
               "build_mismatch": verify(man),
               "architecture": arch, "driver_version": driver,
               "hip_version": torch.version.hip, **_GPU_OUTCOMES,
+              "parked": sorted(_PARKED_SEEN),
               "families": _FAMILY_OUTCOMES,
               "selection": {
                   "complete": _complete_selection(session.config),
@@ -119,6 +127,11 @@ def pytest_sessionfinish(session, exitstatus):
 
 
 def pytest_collection_modifyitems(config, items):
+    for item in items:
+        if "gpu" in item.keywords and any(
+                m.name == "skip" and m.kwargs.get("reason")
+                for m in item.iter_markers("skip")):
+            _PARKED.add(item.nodeid)
     if _gpu_available():
         return
     skip = pytest.mark.skip(reason="no GPU visible")

@@ -321,6 +321,11 @@ hipError_t launch_added(const DevAdded& a, const DevWork& w,
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);
+// the document-start mask of a batch (nwords words) from its offsets
+// (n_docs + 1 of them, non-decreasing) in device memory
+hipError_t launch_doc_mask(uint64_t* mask, int64_t nwords,
+                           const uint64_t* doc_offsets, uint32_t n_docs,
+                           int64_t nb, hipStream_t s);
 
 // The allocation-free entry (tk_engine_encode_device_noalloc) carves its
 // workspace out of a static device array of SCRATCH_BYTES, one copy per

@@ -3944,24 +3944,58 @@ hipError_t launch_seed(const DevWork& w, const uint8_t* text, int64_t nb,
 }
 
 // row d starts at the number of tokens whose first byte lies before
-// doc_offsets[d]
-__global__ void k_doc_offsets(DevWork w, const uint64_t* doc_offsets,
-                              uint32_t n, uint64_t* rows) {
-  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d > n) return;
+// doc_offsets[d]: the compaction's prefix at its block plus the token slots
+// of the block before it, counted by one wave (lanes strided, then a wave
+// sum)
+__global__ __launch_bounds__(256) void k_doc_offsets(DevWork w,
+                                                     const uint64_t* doc_offsets,
+                                                     uint32_t n, uint64_t* rows) {
+  const uint32_t d = blockIdx.x * 4 + wave_id();
+  if (d > n) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
   int64_t p = (int64_t)doc_offsets[d];
   if (p > w.nb) p = w.nb;
   const int64_t blk = p / COMPACT_BLOCK;
-  uint64_t c = w.blkprefix[blk];
-  for (int64_t q = blk * COMPACT_BLOCK; q < p; ++q) c += w.tok[q] != INVALID_ID;
-  rows[d] = c;
+  uint32_t c = 0;
+  for (int64_t q = blk * COMPACT_BLOCK + lane; q < p; q += 64)
+    c += w.tok[q] != INVALID_ID;
+  for (int o = 32; o > 0; o >>= 1) c += (uint32_t)__shfl_xor((int)c, o);
+  if (lane == 0) rows[d] = (uint64_t)w.blkprefix[blk] + c;
+}
+
+// the document-start mask of a batch from its offsets: one thread per mask
+// word, the documents that start in it found by a binary search
+__global__ __launch_bounds__(256) void k_doc_mask(uint64_t* mask, int64_t nwords,
+                                                  const uint64_t* offs,
+                                                  uint32_t n_docs, int64_t nb) {
+  const int64_t wd = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (wd >= nwords) return;
+  const uint64_t lo = (uint64_t)wd * 64, hi = lo + 64;
+  uint32_t a = 0, b = n_docs;  // first document with offs[d] >= lo
+  while (a < b) {
+    const uint32_t m = (a + b) / 2;
+    if (offs[m] < lo) a = m + 1;
+    else b = m;
+  }
+  uint64_t bits = 0;
+  for (uint32_t d = a; d < n_docs && offs[d] < hi; ++d)
+    if (offs[d] < (uint64_t)nb) bits |= 1ull << (offs[d] & 63);
+  mask[wd] = bits;
+}
+
+hipError_t launch_doc_mask(uint64_t* mask, int64_t nwords,
+                           const uint64_t* doc_offsets, uint32_t n_docs,
+                           int64_t nb, hipStream_t s) {
+  hipLaunchKernelGGL(k_doc_mask, dim3((uint32_t)((nwords + 255) / 256)),
+                     dim3(256), 0, s, mask, nwords, doc_offsets, n_docs, nb);
+  return hipGetLastError();
 }
 
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s) {
-  const uint32_t n = n_docs + 1;
-  hipLaunchKernelGGL(k_doc_offsets, dim3((n + 63) / 64), dim3(64), 0, s, w,
+  const uint32_t n = n_docs + 1;  // rows, one wave each
+  hipLaunchKernelGGL(k_doc_offsets, dim3((n + 3) / 4), dim3(256), 0, s, w,
                      doc_offsets, n_docs, row_offsets);
   return hipGetLastError();
 }

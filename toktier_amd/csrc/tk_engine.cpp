@@ -1467,15 +1467,12 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
   int rc = ensure_workspace(e, nb, n_docs);
   if (rc != TK_OK) return rc;
   hipStream_t s = e->stream;
-  // forced piece starts at every document head (gpu.rs:644-652)
-  std::vector<uint64_t> mask((nb + 63) / 64 + 2, 0);
-  for (size_t d = 0; d < n_docs; ++d) {
-    const uint64_t p = doc_offsets[d];
-    if (p < nb) mask[p >> 6] |= 1ULL << (p & 63);
-  }
+  // forced piece starts at every document head (gpu.rs:644-652): the mask
+  // is built on the device from the offsets
   if ((rc = stage_in(e, e->ws.text, joined, nb, s)) != TK_OK) return rc;
-  HIP_TRY(hipMemcpyAsync(e->ws.docmask, mask.data(), mask.size() * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
+  HIP_TRY(tk::launch_doc_mask(e->ws.docmask, (int64_t)((nb + 63) / 64 + 2),
+                              e->docoffs.p, (uint32_t)n_docs, (int64_t)nb, s));
   HostOut o;
   if ((rc = host_out(e, ids, ids_cap, &o)) != TK_OK) return rc;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);

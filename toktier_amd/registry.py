@@ -232,10 +232,12 @@ def suite_judged(evidence: dict, manifest: dict) -> bool:
     """The evidence is a complete, clean run of the GPU suite on this very
     build on gfx950: the library was the manifest's build, the whole
     ``-m gpu`` selection ran (no ``-k``, nothing deselected), and no test
-    failed or was skipped."""
+    failed or was skipped (tests parked in the source by an explicit skip
+    mark with a reason are listed by node id under ``parked`` and counted
+    as collected, not as run)."""
     sel = evidence.get("selection") or {}
     ran = (evidence.get("passed", 0) + evidence.get("failed", 0)
-           + evidence.get("skipped", 0))
+           + evidence.get("skipped", 0) + len(evidence.get("parked") or []))
     return (evidence.get("build_key") == manifest["build_key"]
             and evidence.get("build_mismatch") is None
             and evidence.get("architecture") == ARCH
