@@ -208,6 +208,9 @@ __host__ __device__ __forceinline__ uint32_t added_slot(uint32_t key,
 // (blocks of four waves, 256 CUs); the eighth wave slot is left to the
 // side streams' long-piece kernels, which run beside it
 constexpr int PACK_BLOCKS = 1792;
+// k_bpe_pack merges the queued pieces of 65..128 bytes itself when at most
+// this many pieces over 64 bytes are queued; else k_bpe_rows does
+constexpr int PACK_ROWS_MAX = 8192;
 // The piece lists come in PACK_XCDS segments: segment x holds the pieces of
 // the k_pretok tiles b with b % PACK_XCDS == x (those of one XCD: workgroups
 // go to the XCDs in turn), and the k_bpe_pack blocks of the same residue

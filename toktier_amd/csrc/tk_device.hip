@@ -2411,7 +2411,9 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
 // queue with k % PACK_XCDS == x), one per unit, merged by the wave with its
 // state in registers (wave_bpe_rows): the longest chains of all. (Longer
 // ones go to the side streams: the 256-byte instance does not fit this
-// kernel's registers.)
+// kernel's registers; so do these when more than PACK_ROWS_MAX pieces are
+// queued, where they would lengthen this kernel more than the side
+// stream's join costs.)
 // The long units thus all start at once, and the SIMDs end on the short
 // ones, each SIMD busy until its share is done (with a fixed share per wave
 // a SIMD holding a few long units ran on alone, latency-bound, long after
@@ -2455,7 +2457,8 @@ void k_bpe_pack(DevTables t, DevWork w) {
     const bool ko = lane <= PACK_CLASSES;
     const int oc = lane == 0 ? PACK_CLASSES : ko ? PACK_ORDER[lane - 1] : 0;
     const uint32_t nuo = (uint32_t)__shfl((int)nu, oc);
-    const uint32_t nr = nl > (uint32_t)x ? (nl - x + PACK_XCDS - 1) / PACK_XCDS : 0u;
+    const uint32_t nr = nl <= (uint32_t)PACK_ROWS_MAX && nl > (uint32_t)x
+                            ? (nl - x + PACK_XCDS - 1) / PACK_XCDS : 0u;
     const uint32_t lk = lane == 0 ? nr : ko ? nuo : 0u;
     const uint32_t incl = wave_incl_scan(lk, lane);
     if (lane < 16) {
@@ -3338,11 +3341,15 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   const uint32_t waves = gridDim.x * 4;
   // few, latency-bound waves beside k_bpe_pack on the same SIMDs
   __builtin_amdgcn_s_setprio(3);
+  // (pieces of 65..128 bytes too when k_bpe_pack left them: more than
+  // PACK_ROWS_MAX queued)
+  const int lo = n > (uint32_t)PACK_ROWS_MAX ? 64 : 128;
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
     const int len = (int)(b - a);
-    if (len <= 128 || len > 256) continue;  // wave-uniform
-    wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
+    if (len <= lo || len > 256) continue;  // wave-uniform
+    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
+    else wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
   }
 }
 

@@ -543,13 +543,15 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
-  const bool side2 = nrows > 0 || nwide > 0 ||
+  // (pieces of 65..128 bytes are k_bpe_rows' too past PACK_ROWS_MAX)
+  const bool rows = nrows > 0 || nlong > (uint32_t)tk::PACK_ROWS_MAX;
+  const bool side2 = rows || nwide > 0 ||
                      (!e->t.cert && e->gate[tk::GATE_BIG] > 0);
   {
     // two independent jobs on two side streams: pieces of 129..WIDE_MAX
     // bytes merged whole, and the cut / segment / certify path of the
     // longer ones (they touch disjoint bytes and read the same lists)
-    if (nrows > 0) HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong));
+    if (rows) HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong));
     if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     // (a table that drops bytes merges its pieces over WIDE_MAX bytes
     // whole, a workgroup each, after the wide merges)
