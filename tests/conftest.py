@@ -21,6 +21,8 @@ FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
     config.addinivalue_line("markers", "slow: long-running CPU test")
+    config.addinivalue_line("markers", "family(name): the one family a test "
+                            "covers (counted under it in the route evidence)")
 
 
 def _gpu_available() -> bool:
@@ -40,9 +42,14 @@ _SELECTION = {"deselected_gpu": 0}
 # (listed in the evidence by node id; any other skip blocks certification)
 _PARKED: set[str] = set()
 _PARKED_SEEN: list[str] = []
+# the family a test covers when no parameter names it: its
+# ``@pytest.mark.family(name)`` mark
+_NODE_FAMILY: dict[str, str] = {}
 
 
 def _family_of(nodeid: str) -> str:
+    if nodeid in _NODE_FAMILY:
+        return _NODE_FAMILY[nodeid]
     params = nodeid.split("[", 1)[1] if "[" in nodeid else ""
     for name in FAMILY_NAMES:
         if name in params:
@@ -55,14 +62,18 @@ def pytest_runtest_logreport(report):
     if "gpu" not in report.keywords:
         return
     if report.when == "call" or (report.when == "setup" and not report.passed):
+        fam = _FAMILY_OUTCOMES.setdefault(
+            _family_of(report.nodeid),
+            {"passed": 0, "failed": 0, "skipped": 0, "parked": 0})
         if report.skipped and report.nodeid in _PARKED:
+            # counted against the family it covers (a shared one, against
+            # every family): a parked test blocks certification
             _PARKED_SEEN.append(report.nodeid)
+            fam["parked"] += 1
             return
         key = ("passed" if report.passed else
                "skipped" if report.skipped else "failed")
         _GPU_OUTCOMES[key] += 1
-        fam = _FAMILY_OUTCOMES.setdefault(
-            _family_of(report.nodeid), {"passed": 0, "failed": 0, "skipped": 0})
         fam[key] += 1
 
 
@@ -128,6 +139,9 @@ def pytest_sessionfinish(session, exitstatus):
 
 def pytest_collection_modifyitems(config, items):
     for item in items:
+        mark = item.get_closest_marker("family")
+        if mark is not None:
+            _NODE_FAMILY[item.nodeid] = mark.args[0]
         if "gpu" in item.keywords and any(
                 m.name == "skip" and m.kwargs.get("reason")
                 for m in item.iter_markers("skip")):

@@ -288,3 +288,94 @@ def test_planted_walk_mistakes_are_caught(mistake, data, cuts):
     assert planted == (True, False), mistake  # holds, with wrong ids
     ok, same = _trial("llama_3_1_8b", data, cuts, False, walk)
     assert same or not ok, mistake  # the correct walk refuses it
+
+
+# ------------------------------------------------------- the repair passes
+
+def window_cuts(family, ids, lens, off):
+    """k_long_windows on a piece whose first byte is text position `off`:
+    every 64-byte window of both grids (text positions 64v and 64v - 32),
+    clipped to the piece, merged alone; the token starts in its central 32
+    bytes become cuts (piece offsets)."""
+    rules, unsafe, _ = _model(family)
+    n = len(ids)
+    cuts = set()
+    for ws in range((off // 32) * 32 - 32, off + n, 32):
+        a, b = max(ws, off), min(ws + 64, off + n)
+        if a >= b:
+            continue
+        toks, _ = merge(rules, unsafe, ids[a - off:b - off], True)
+        pos = a
+        for t in toks:
+            if ws + 16 <= pos < ws + 48 and off < pos:
+                cuts.add(pos - off)
+            pos += lens[t]
+    return sorted(cuts)
+
+
+def repair(family, data, off, whole_from=None, limit=10_000):
+    """The certification and its repair passes on one piece: certify every
+    cut, drop the failed ones, redo the segments, until none fails (cert 1,
+    a monotone table). From pass `whole_from` on, a piece that still has a
+    failed cut drops every cut (k_fail_pieces). Returns (ids, passes)."""
+    rules, unsafe, byte_id = _model(family)
+    lens = _lengths(family)
+    ids = [byte_id[b] for b in data]
+    cuts = window_cuts(family, ids, lens, off)
+    passes = 0
+    while True:
+        bounds = [0, *cuts, len(ids)]
+        segs = [merge(rules, unsafe, ids[a:b], True) for a, b in zip(bounds, bounds[1:])]
+        failed = [c for k, c in enumerate(cuts)
+                  if not walk_events(rules, ids[c - 1], ids[c], segs[k][1], segs[k + 1][1])]
+        if not failed or passes >= limit:
+            return [t for s in segs for t in s[0]], passes
+        passes += 1
+        if whole_from is not None and passes >= whole_from:
+            cuts = []
+        else:
+            cuts = [c for c in cuts if c not in failed]
+
+
+def test_repair_passes_cascade_on_periodic_runs_and_escalation_ends_them():
+    """A run of one letter led by a character that joins its piece ("!"
+    + "QQQ...": one piece under the Qwen2 pattern) fixes the token parity
+    at its first window, while every later window pairs the letters from
+    an even text position. Removing the one cut that fails makes the next
+    one fail: one cut per pass, so the passes grow with the run. Merging a
+    piece that still fails whole from pass 3 on (the device's REPAIR_WHOLE)
+    ends them with the whole piece's ids."""
+    family = "qwen3_8b"
+    rules, unsafe, byte_id = _model(family)
+    for n in (300, 600, 1200):
+        data = b"!" + b"Q" * n
+        whole, _ = merge(rules, unsafe, [byte_id[b] for b in data], True)
+        ids, passes = repair(family, data, off=64)
+        assert ids == whole
+        assert passes >= n // 2 - 40, (n, passes)  # one cut per pass
+        ids, passes = repair(family, data, off=64, whole_from=3)
+        assert ids == whole and passes <= 3, (n, passes)
+
+
+def test_escalated_repair_keeps_the_ids_of_ordinary_pieces():
+    """Letter runs of C5's text (monotone Qwen table) at shifting text
+    offsets: the escalated repair loop gives the whole piece's ids within
+    three passes."""
+    family = "qwen3_8b"
+    rules, unsafe, byte_id = _model(family)
+    from toktier_amd import standin, workloads
+    js = standin.load_artifact_json(family)
+    text = workloads.config5(js, n_chars=40_000, n_runs=2, run_chars=3_000, sample=9)
+    letters = "".join(ch for ch in text if ch.isalpha()).encode("utf-8")
+    rng = np.random.default_rng(21)
+    for _ in range(12):
+        k = int(rng.integers(513, 1500))
+        a = int(rng.integers(0, len(letters) - k))
+        while a < len(letters) and (letters[a] & 0xC0) == 0x80:
+            a += 1
+        data = letters[a:a + k]
+        while data and (data[-1] & 0xC0) == 0x80 or (data and data[-1] >= 0xC0):
+            data = data[:-1]
+        whole, _ = merge(rules, unsafe, [byte_id[b] for b in data], True)
+        ids, passes = repair(family, data, off=int(rng.integers(0, 64)), whole_from=3)
+        assert ids == whole and passes <= 3, passes

@@ -63,6 +63,7 @@ def test_probe_tables(probe):
             full.encode(d, add_special_tokens=False).ids, d
 
 
+@pytest.mark.family("qwen3_8b")
 def test_literals_across_tile_and_block_edges():
     """A literal starting at every offset around the pretokenizer's tiles
     (PT_TILE bytes) and the literal kernels' 4096-byte blocks."""
@@ -81,6 +82,7 @@ def test_literals_across_tile_and_block_edges():
             assert np.array_equal(got, want), (edge, d)
 
 
+@pytest.mark.family("qwen3_8b")
 def test_dense_literal_streams():
     k, t = kit("qwen3_8b"), tok("qwen3_8b")
     for s in ["<|im_end|>" * 50_000, ("<|im_start|>" + "x") * 30_000,
@@ -91,6 +93,7 @@ def test_dense_literal_streams():
     assert list(t.encode("<|im_end|>" * 300).array) == [151645] * 300
 
 
+@pytest.mark.family("qwen3_8b")
 def test_full_size_chat_request_matches_oracle():
     from toktier_amd import workloads
     k, t = kit("qwen3_8b"), tok("qwen3_8b")
@@ -118,6 +121,7 @@ def test_batch_rows_with_literals():
         assert list(r.array) == k.hf_ids(d), d[:60]
 
 
+@pytest.mark.family("qwen3_8b")
 def test_nfc_fallback_splits_literals_first():
     k, t = kit("qwen3_8b"), tok("qwen3_8b")
     texts = ["<|im_end|≯ x", "e<|im_start|>́",
@@ -129,6 +133,7 @@ def test_nfc_fallback_splits_literals_first():
         assert list(r.array) == k.hf_ids(s), s
 
 
+@pytest.mark.family("qwen3_8b")
 def test_no_added_flag_and_device_entry():
     import torch
     from tokenizers import Tokenizer

@@ -49,6 +49,7 @@ def test_seed_of_mixed_text(stride):
     _check("qwen3_8b", workloads.config2(k.json, n_chars=200_000), stride)
 
 
+@pytest.mark.family("deepseek_v3")
 def test_seed_of_cjk_text_through_deepseek():
     from toktier_amd import workloads
     k = kit("deepseek_v3")

@@ -1,4 +1,4 @@
-"""CPU model of the o200k and kimi split automaton (the device's
+r"""CPU model of the o200k and kimi split automaton (the device's
 ``o2k_char`` with the state carried across lanes, words and tiles in
 ``k_pretok<4, ...>`` / ``k_pretok<5, ...>``).
 

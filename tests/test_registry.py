@@ -133,12 +133,39 @@ def test_generate_certifies_only_a_judged_build():
                 dict(families={"qwen3_8b": {"passed": 29, "failed": 1, "skipped": 0}}),
                 dict(families={"qwen3_8b": {"passed": 29, "failed": 0, "skipped": 1}}),
                 dict(families={"shared": {"passed": 40, "failed": 0, "skipped": 0}}),
-                dict(families=None)):
+                dict(families=None),
+                # a test of the family, or one shared by every family, is
+                # parked by an explicit skip mark (listed, not run)
+                dict(families={"qwen3_8b": {"passed": 30, "failed": 0, "skipped": 0,
+                                            "parked": 1}},
+                     parked=["tests/x.py::test_p"],
+                     selection={**sel, "collected_gpu": 41}),
+                dict(families={"qwen3_8b": {"passed": 30, "failed": 0, "skipped": 0},
+                               "shared": {"passed": 10, "failed": 0, "skipped": 0,
+                                          "parked": 1}},
+                     parked=["tests/x.py::test_p"],
+                     selection={**sel, "collected_gpu": 41})):
         reg = R.generate(_evidence(**bad), man, {"qwen3_8b": SHA})
         row = _status(reg)
         assert row["status"] == R.STATUS_EXPERIMENTAL, bad
         assert R.architecture_statuses(row) == {"gfx950": R.STATUS_EXPERIMENTAL}
         assert not R.admit(reg, SHA, _facts(), R.POLICY_CERTIFIED).admitted
+
+
+def test_a_parked_test_blocks_only_its_own_family():
+    man = {"build_key": KEY, "hipcc": [], "flags": []}
+    sel = _evidence()["selection"]
+    ev = _evidence(families={
+        "qwen3_8b": {"passed": 30, "failed": 0, "skipped": 0},
+        "deepseek_v3": {"passed": 9, "failed": 0, "skipped": 0, "parked": 1},
+        "shared": {"passed": 10, "failed": 0, "skipped": 0}},
+        passed=49, parked=["tests/x.py::test_p"],
+        selection={**sel, "collected_gpu": 50})
+    reg = R.generate(ev, man, {"qwen3_8b": SHA, "deepseek_v3": "c" * 64})
+    by_family = {a["family"]: a["backends"]["gpu"]["status"]
+                 for a in reg["artifacts"]}
+    assert by_family == {"qwen3_8b": R.STATUS_CERTIFIED,
+                         "deepseek_v3": R.STATUS_EXPERIMENTAL}
 
 
 def test_generate_judges_each_family_on_its_own_tests():

@@ -17,6 +17,10 @@ constexpr uint32_t ST_NFC = 2u;      // NFC quick check failed
 constexpr uint32_t ST_LONGOVF = 4u;  // long-piece list overflow (internal)
 constexpr uint32_t ST_CAPACITY = 8u;  // more ids than the output holds
 constexpr uint32_t ST_STALL = 16u;    // compaction look-back timed out (internal)
+constexpr uint32_t ST_STALL_PRETOK = 32u;  // a pretokenize tile's look-back
+                                           // (digit run, o200k state) timed out
+constexpr uint32_t ST_ROUNDS = 64u;   // a workgroup merge ran past its round
+                                      // bound (internal)
 
 // Compact pair table: 16-byte buckets of two u64 slots, two candidate
 // buckets per pair (cuckoo placement), so a lookup is two independent
@@ -132,6 +136,9 @@ struct DevWork {
   uint32_t* prepdone;    // k_bpe_pack waves done with the long pieces (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
   uint32_t seq;          // call number written to gate[GATE_SEQ]
+  // bound of every wait on another workgroup's published word, in ticks
+  // of the device's constant-rate real-time counter (wall_clock64)
+  uint64_t wait_ticks;
   // added-token literals (nullptr when the call extracts none): a literal
   // [s, e) marks s in lits and s+1..e-1 in litb, and s and e as document
   // starts; its bytes form no piece, and its id is written at tok[s]
@@ -307,7 +314,12 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s);
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop = nullptr);
-hipError_t launch_apply_fail(const DevWork& w, hipStream_t s);
+// (whole: pieces with a failed cut drop every cut, k_fail_pieces, first;
+// nlong: the queued pieces over 64 bytes)
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, bool whole,
+                             uint32_t nlong);
+// the first repair pass that merges a still-failing piece whole
+constexpr int REPAIR_WHOLE = 3;
 hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // k_added: the literal split of the request into w.docmask (read-write;

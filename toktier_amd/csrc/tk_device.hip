@@ -329,7 +329,22 @@ constexpr int LTAB_CLS = 20, LTAB_NFC = 24;
 // a tile's digit-run word (nrun): call tag << 32 | NRUN_FULL (the run
 // spans the whole tile) | N characters of the run at the tile's end
 constexpr uint64_t NRUN_FULL = 1ull << 31;
-constexpr int NRUN_SPIN = 1 << 20;
+// A wait on another workgroup's published word ends at a deadline on the
+// device's constant-rate real-time counter, DevWork::wait_ticks after the
+// waiting workgroup's first poll: far above any launch's duration, so only
+// a broken protocol reaches it, and the call then fails with the stage
+// named (ST_STALL_PRETOK, ST_STALL) instead of hanging.
+struct WaitBound {
+  uint64_t end = 0;  // 0: not started
+  __device__ __forceinline__ bool expired(uint64_t ticks) {
+    const uint64_t now = (uint64_t)wall_clock64();
+    if (end == 0) {
+      end = now + ticks;
+      return false;
+    }
+    return now > end;
+  }
+};
 __device__ __forceinline__ void nrun_store(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -633,7 +648,13 @@ __device__ __forceinline__ bool ds_lm(int k) { return k == DS_L || k == DS_M; }
 __device__ __forceinline__ bool ds_space(int k) { return k >= DS_WS; }
 
 template <class C>
-__device__ bool start_deepseek(const C& c, const Ch& ci, int dmax) {
+__device__ bool ds_run_led(const C& c, int64_t s);
+// FAST_FAR: a letter / mark after an ASCII-alpha run that reaches below the
+// LDS span; *far is the highest position of the run not yet read, and the
+// wave searches from there (ds_stop_hbm)
+constexpr int FAST_FAR = -5;
+template <class C>
+__device__ int start_deepseek(const C& c, const Ch& ci, int dmax, int64_t* far) {
   const int r0 = ds_region(ci.cl, ci.cp);
   // the character before / after p inside c0's region (-1 at its edge)
   auto prev_in = [&](int64_t p) -> int64_t {
@@ -667,11 +688,15 @@ __device__ bool start_deepseek(const C& c, const Ch& ci, int dmax) {
   if (ds_lm(ci.cl)) {
     if (ds_lm(p1.cl)) {
       if (ascii_alpha(ci.cp) || !ascii_alpha(p1.cp)) return false;
+      // down the run (one byte per letter) while it stays in the span
       for (int64_t q = q1;;) {
-        const int64_t r = prev_in(q);
-        if (r < 0) return false;
-        const Ch x = c.at(r);
-        if (!ascii_alpha(x.cp)) return ascii_punct(x.cp) && arrives(r);
+        if (c.ds(q)) return false;  // a document starts inside the run
+        const int64_t r = q - 1;
+        if (!c.in(r)) {
+          *far = r;
+          return FAST_FAR;
+        }
+        if (!ascii_alpha(c.at(r).cp)) return ds_run_led(c, r);
         q = r;
       }
     }
@@ -760,6 +785,74 @@ __device__ __forceinline__ int fast_deepseek(const Ctx5& x, int dmax) {
   if (k3 == DS_PS) return 1;
   if (k3 != DS_CR) return 0;
   return FAST_CRLF;
+}
+
+// A letter / mark right after an ASCII-alpha run (FAST_GENERAL) starts a
+// piece exactly when [ascii punct][A-Za-z]+ took the run: the run holds no
+// document start, and the character before it, whose last byte is s, is
+// ASCII punctuation that starts its own match (no P/S and no U+0020
+// before it in its region, or a document start at s). So the answer needs
+// only s, the highest position below the run that is not an ASCII letter
+// or that opens a document, however long the run is.
+template <class C>
+__device__ bool ds_run_led(const C& c, int64_t s) {
+  if (s < 0) return false;
+  const Ch x = c.at(s);  // (a non-ASCII byte at s gives a code point >= 0x80)
+  if (!ascii_punct(x.cp)) return false;
+  const int64_t q = c.prev(s);
+  if (q < 0) return true;
+  const Ch y = c.at(q);
+  return ds_region(y.cl, y.cp) != 0 || (y.cl != DS_PS && y.cp != ' ');
+}
+// The ASCII letters of four bytes, one bit each (bit 7 of every byte);
+// no byte carries into the next (every sum stays below 0x100).
+__device__ __forceinline__ uint32_t alpha_bytes(uint32_t v) {
+  const uint32_t y = (v | 0x20202020u) & 0x7F7F7F7Fu;  // lower case, 7 bits
+  const uint32_t ge = y + 0x1F1F1F1Fu;                 // >= 'a'
+  const uint32_t gt = y + 0x05050505u;                 // > 'z'
+  const uint32_t a = ge & ~gt & ~v & 0x80808080u;      // and ASCII
+  return ((a >> 7) & 1u) | ((a >> 14) & 2u) | ((a >> 21) & 4u) | ((a >> 28) & 8u);
+}
+// Wave-cooperative: the highest position <= q that is not an ASCII letter
+// or that opens a document, read from the text in HBM. Lane l takes the
+// 64-byte chunk (q >> 6) - l of each 4 KiB step, so a step is one wave of
+// coalesced loads; chunk 0 holds position 0, which opens the text, so the
+// search ends there at the latest. q >= 0; every lane calls it with the
+// same q (wave-uniform).
+__device__ int64_t ds_stop_hbm(const uint8_t* t, const uint64_t* dm, int64_t q) {
+  const int lane = (int)(threadIdx.x & 63);
+  const bool al = ((uintptr_t)t & 15) == 0;
+  for (int64_t cq = q >> 6; cq >= 0; cq -= 64) {
+    const int64_t ch = cq - lane;
+    uint64_t m = 0;
+    if (ch >= 0) {
+      const uint8_t* p = t + 64 * ch;  // the whole chunk lies at or below q | 63 < nb
+      uint64_t alpha = 0;
+      if (al) {
+        const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 x = v[j];
+          alpha |= (uint64_t)(alpha_bytes(x.x) | (alpha_bytes(x.y) << 4) |
+                              (alpha_bytes(x.z) << 8) | (alpha_bytes(x.w) << 12))
+                   << (16 * j);
+        }
+      } else {
+        for (int j = 0; j < 64; ++j) alpha |= (uint64_t)ascii_alpha(p[j]) << j;
+      }
+      m = ~alpha;
+      if (dm) m |= dm[ch];
+      if (ch == 0) m |= 1;
+      if (ch == (q >> 6)) m &= mask_le((int)(q & 63));
+    }
+    const uint64_t any = __ballot(m != 0);
+    if (any) {
+      const int l = __builtin_ctzll(any);
+      const int hb = m ? 63 - __builtin_clzll(m) : 0;
+      return 64 * (cq - l) + __builtin_amdgcn_readlane(hb, l);
+    }
+  }
+  return -1;  // (q < 0: nothing to search)
 }
 
 // ---- o200k (gpt-oss): o200k_base with contractions,
@@ -1307,15 +1400,15 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
         c0 = after_break(0);
       } else if (gNL[0] && w.nrun) {
         // the run reaches back past the halo: the tiles before it
+        WaitBound wb;
         for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0; --u) {
           uint64_t v;
-          int spin = 0;
           while ((uint32_t)((v = nrun_load(&w.nrun[u])) >> 32) != w.seq) {
-            if (++spin > NRUN_SPIN) break;
+            if (wb.expired(w.wait_ticks)) break;
             __builtin_amdgcn_s_sleep(2);
           }
           if ((uint32_t)(v >> 32) != w.seq) {
-            st |= ST_STALL;
+            st |= ST_STALL_PRETOK;
             break;
           }
           c0 += (uint32_t)(v & (NRUN_FULL - 1));
@@ -1346,6 +1439,23 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       if (!D) return L == Lz;
       const int64_t i = lo + L;
       return i == 0 || ((sdm[(i >> 6) - wlo] >> (i & 63)) & 1) != 0;
+    };
+    // (deepseek) the highest position <= from that is not an ASCII letter
+    // or that opens a document: the staged bytes 64 a step, then the text
+    // in HBM (ds_stop_hbm); position 0 opens the text, so the search ends.
+    // Wave-uniform, from >= 0.
+    auto ds_stop = [&](int64_t from) -> int64_t {
+      const int64_t st0 = base - PT_PAD;  // the position of sb[0]
+      const int64_t lo_st = st0 > 0 ? st0 : 0;
+      for (int64_t top = from; top >= lo_st; top -= 64) {
+        const int64_t p = top - lane;
+        bool stop = false;
+        if (p >= lo_st) stop = !ascii_alpha(sb[p - st0]) || ds((int)(p - lo));
+        const uint64_t m = __ballot(stop);
+        if (m) return top - __builtin_ctzll(m);
+      }
+      // (lo_st == 0: position 0 stopped the loop above; guarded all the same)
+      return lo_st > 0 ? ds_stop_hbm(w.text, c.g.dm, lo_st - 1) : (int64_t)-1;
     };
     for (int k = wv; k <= PT_TILE / 64; k += PRETOK_TPB / 64) {
       const int64_t wd = (base >> 6) + k;
@@ -1402,6 +1512,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       // (also at the span's last byte, where the fixed context stops)
       if (groups && kcl(e) == KN) r = FAST_DIGITS;
       const bool open = lead && !d0 && r < 0;
+      int64_t far = -1;  // (deepseek) FAST_FAR: where the search starts
       if (__builtin_amdgcn_ballot_w64(open)) {  // wave-uniform
         if (open) {
           const uint64_t below = (1ULL << lane) - 1;
@@ -1448,29 +1559,16 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
             }
           } else if (RS == RS_DEEPSEEK && r == FAST_GENERAL) {
             // a letter / mark after an ASCII-alpha run longer than the
-            // context: it starts a piece exactly when the run was taken by
-            // [ascii punct][A-Za-z]+, i.e. the byte before the run is ASCII
-            // punctuation that starts its own match (no P/S or U+0020
-            // before it, or a document start at it). Resolved here when
-            // the run starts inside this word.
-            const uint64_t na = ~mAL & below;
-            if (na) {
-              const int h = 63 - __builtin_clzll(na);
-              const int64_t ph = i - (lane - h);  // the byte before the run
-              if (dmw & lanes_in(h + 1, lane)) {
-                r = 0;  // a document starts inside the run
-              } else if (!((mHI >> h) & 1)) {
-                const int bh = sb[64 * k + h + PT_PAD];
-                if (!ascii_punct(bh)) {
-                  r = 0;
-                } else if (ph == 0 || ((dmw >> h) & 1)) {
-                  r = 1;
-                } else {
-                  // the byte before the punctuation (staged even for h = 0)
-                  const int bq = sb[64 * k + h - 1 + PT_PAD];
-                  if (bq < 0x80) r = !(ascii_punct(bq) || bq == ' ');
-                }
-              }
+            // context (ds_run_led): the highest byte below the lane that is
+            // not an ASCII letter or that opens a document decides; when
+            // the run reaches back past the word's first byte the wave
+            // searches for it below (FAST_FAR)
+            const uint64_t stop = (~mAL | dmw | (wd == 0 ? 1ULL : 0ULL)) & below;
+            if (stop) {
+              r = ds_run_led(c, i - (lane - (63 - __builtin_clzll(stop))));
+            } else {
+              r = FAST_FAR;
+              far = i - lane - 1;
             }
           }
           if (r == FAST_CRLF) {
@@ -1504,11 +1602,25 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
               }
             }
           }
-          if (r < 0) {
+          if (r < 0 && r != FAST_FAR) {
             const Ch ci{i, (int32_t)(e & 0x1FFFFF), (uint8_t)kcl(e)};
             r = RS == 1 ? start_r50k(c, ci)
-              : RS == RS_DEEPSEEK ? start_deepseek(c, ci, t.dmax)
+              : RS == RS_DEEPSEEK ? start_deepseek(c, ci, t.dmax, &far)
                                   : start_cl100k(c, ci, t.dmax);
+          }
+        }
+        if (RS == RS_DEEPSEEK) {
+          // the ASCII-alpha runs that reach below the word (at most one a
+          // word, the word's first run) or the span: one search each by
+          // the whole wave, with no wait on another tile
+          uint64_t farm = __ballot(open && r == FAST_FAR);
+          while (farm) {
+            const int l = __builtin_ctzll(farm);
+            farm &= farm - 1;
+            const int64_t from = ((int64_t)__builtin_amdgcn_readlane((int)(far >> 32), l) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)far, l);
+            const int64_t s = ds_stop(from);
+            if (lane == l) r = ds_run_led(c, s);
           }
         }
       }
@@ -1725,18 +1837,18 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
           // G: the function of the tiles after u up to this one
           Fn G = o2_ident<W>();
           bool done = false;
+          WaitBound wb;
           for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0 && !done; --u) {
             const uint64_t* q = w.ostate + 2 * u;
             uint64_t v1;
-            int spin = 0;
             while ((uint32_t)((v1 = __hip_atomic_load(q + 1, __ATOMIC_ACQUIRE,
                                                       __HIP_MEMORY_SCOPE_AGENT)) >> 32) !=
                    w.seq) {
-              if (++spin > NRUN_SPIN) break;
+              if (wb.expired(w.wait_ticks)) break;
               __builtin_amdgcn_s_sleep(2);
             }
             if ((uint32_t)(v1 >> 32) != w.seq) {
-              st |= ST_STALL;
+              st |= ST_STALL_PRETOK;
               done = true;
             } else if (((v1 >> 30) & 3) == O2_INCL) {
               entry = o2_at(G, (uint32_t)(v1 >> 26) & 15);
@@ -2829,7 +2941,7 @@ __device__ void block_bpe(const DevTables& t, const DevWork& w, uint32_t a,
     // every round merges at least its leftmost lowest pair, so n rounds
     // end it; past that the state is broken: report it, never spin
     if (round > n) {
-      if (tid == 0) atomicOr(w.status, ST_STALL);
+      if (tid == 0) atomicOr(w.status, ST_ROUNDS);
       break;
     }
     const uint32_t s0 = (uint32_t)m;
@@ -3590,6 +3702,43 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   }
 }
 
+// An escalated repair pass (REPAIR_WHOLE on): a piece over WIDE_MAX bytes
+// that still has a failed cut drops every cut and is merged whole, as one
+// segment (k_seg_block). Without it a pass can expose the next failing cut
+// each time: in a periodic run whose token parity its first window fixes
+// ("!" + "QQQ...": every later window pairs the letters from an even
+// offset), removing a failed cut makes the one after it fail, one cut per
+// pass, 35,000 passes for 70,000 letters. With it the passes end: a piece
+// with no cut has nothing to fail. One wave per long piece, ahead of
+// k_apply_fail (it marks the piece's words dirty for the pass).
+__global__ __launch_bounds__(256) void k_fail_pieces(DevWork w) {
+  if (!pass_live(w)) return;
+  const int lane = threadIdx.x & 63;
+  uint32_t n = *w.longcount;
+  if (n > w.long_cap) n = w.long_cap;
+  for (uint32_t k = blockIdx.x * 4 + wave_id(); k < n; k += gridDim.x * 4) {
+    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
+    if (b <= a || b - a <= (uint32_t)WIDE_MAX) continue;  // wave-uniform
+    const int64_t w0 = a >> 6, w1 = ((int64_t)b - 1) >> 6;
+    // the piece's bytes [a, b) of word q
+    auto in_piece = [&](int64_t q) {
+      uint64_t m = ~0ULL;
+      if (q == w0) m &= ~((1ULL << (a & 63)) - 1);
+      if (q == w1) m &= mask_le((int)((b - 1) & 63));
+      return m;
+    };
+    uint64_t f = 0;
+    for (int64_t q = w0 + lane; q <= w1; q += 64) f |= w.failm[q] & in_piece(q);
+    if (!__ballot(f != 0)) continue;  // wave-uniform
+    for (int64_t q = w0 + lane; q <= w1; q += 64) {
+      // (a is a piece start: its cut bit does not matter)
+      atomicAnd(reinterpret_cast<unsigned long long*>(&w.cuts[q]), ~in_piece(q));
+      atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
+               1ULL << (q & 63));
+    }
+  }
+}
+
 // Pieces of 129..256 bytes (k_bpe_rows) and of 257..WIDE_MAX bytes
 // (k_bpe_wide, state in LDS) are merged whole, one wave each, once the host
 // knows there are any (a wave per queued piece, up to 2048 blocks of four;
@@ -3652,7 +3801,12 @@ hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
   return hipGetLastError();
 }
 
-hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, bool whole,
+                             uint32_t nlong) {
+  if (whole) {
+    const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
+    hipLaunchKernelGGL(k_fail_pieces, dim3(blocks), dim3(256), 0, s, w);
+  }
   const int64_t nwords = (w.nb + 63) / 64;
   hipLaunchKernelGGL(k_apply_fail, dim3((uint32_t)((nwords + 255) / 256)),
                      dim3(256), 0, s, w, nwords);
@@ -3675,7 +3829,6 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s) {
 // published. A block waits only for blocks dispatched before it, which
 // publish their counts without waiting, and every wait is bounded.
 constexpr uint32_t CST_TOTAL = 1u << 31;
-constexpr int COMPACT_SPIN = 1 << 20;
 constexpr int COMPACT_LOOK = 1;
 
 __device__ __forceinline__ void cst_store(uint64_t* p, uint64_t v) {
@@ -3737,7 +3890,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
         // Only the words before the nearest published running total are
         // needed: wait for those (every unpublished one re-read at once,
         // one round trip per round), and never for the words behind it.
-        for (int spin = 0;; ++spin) {
+        for (WaitBound wb;;) {
           bool need = false, found = false;
 #pragma unroll
           for (int k = 0; k < COMPACT_LOOK; ++k) {
@@ -3749,7 +3902,7 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
             found = tm != 0;
           }
           if (!need) break;
-          if (spin >= COMPACT_SPIN) {  // only after the bounded wait
+          if (wb.expired(w.wait_ticks)) {  // only after the bounded wait
             ok = false;
 #pragma unroll
             for (int k = 0; k < COMPACT_LOOK; ++k)

@@ -53,6 +53,8 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr size_t PLANE = 0x110000;
+// bound of a device wait on another workgroup's published word (ms)
+constexpr int WAIT_MS = 100;
 
 bool pow2(uint64_t x) { return x && !(x & (x - 1)); }
 
@@ -281,6 +283,9 @@ struct tk_engine {
   volatile uint32_t* gate = nullptr;
   uint32_t* gate_dev = nullptr;
   uint32_t seq = 0;
+  // bound of a device wait on another workgroup (DevWork::wait_ticks):
+  // WAIT_MS in ticks of the device's real-time counter
+  uint64_t wait_ticks = 0;
   // timing
   int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
   hipEvent_t ev[8] = {};
@@ -419,6 +424,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.nrows = ctrl + tk::CTRL_ROWS;
   w.gate = e->gate_dev;
   w.seq = e->seq;
+  w.wait_ticks = e->wait_ticks;
   w.ctrl_next = ws.ctrl + (ws.slot ^ 1) * tk::CTRL_WORDS;
   w.nlit = ctrl + tk::CTRL_NLIT;
   w.nrun = ws.nrun;
@@ -447,14 +453,28 @@ tk::DevWork pass_work(const tk::DevWork& w, uint32_t* ctrl, int p) {
   return q;
 }
 
+// The internal failures a call's status word can carry, each naming the
+// stage that reported it (TK_OK when there is none).
+int internal_status(uint32_t st) {
+  if (st & tk::ST_LONGOVF) return fail(TK_E_INTERNAL, "piece queue overflow");
+  if (st & tk::ST_STALL_PRETOK)
+    return fail(TK_E_INTERNAL,
+                "pretokenize look-back timed out (a tile's digit-run count or "
+                "automaton state was not published within %d ms)", WAIT_MS);
+  if (st & tk::ST_STALL)
+    return fail(TK_E_INTERNAL,
+                "compaction look-back timed out (a block's running total was "
+                "not published within %d ms)", WAIT_MS);
+  if (st & tk::ST_ROUNDS)
+    return fail(TK_E_INTERNAL, "workgroup merge ran past its round bound");
+  return TK_OK;
+}
+
 int read_ctrl_words(const uint32_t* ctrl, hipStream_t s, uint32_t* h) {
   HIP_TRY(hipMemcpyAsync(h, ctrl, 16 * sizeof(uint32_t),
                          hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
-  if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
-    return fail(TK_E_INTERNAL, "piece queue overflow");
-  if (h[tk::CTRL_STATUS] & tk::ST_STALL)
-    return fail(TK_E_INTERNAL, "compaction look-back timed out");
+  if (int rc = internal_status(h[tk::CTRL_STATUS])) return rc;
   return TK_OK;
 }
 
@@ -565,7 +585,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
-        HIP_TRY(tk::launch_apply_fail(wp, s3));
+        HIP_TRY(tk::launch_apply_fail(wp, s3, p >= tk::REPAIR_WHOLE, nlong));
         HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s3));
         HIP_TRY(tk::launch_certify(e->t, wp, 0, s3));
       }
@@ -595,10 +615,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   uint32_t residual = e->gate[tk::GATE_FAIL];
   e->last_passes = e->gate[tk::GATE_PASS];
   e->last_literals = literals && docs->n ? e->gate[tk::GATE_NLIT] : 0;
-  if (h[tk::CTRL_STATUS] & tk::ST_LONGOVF)
-    return fail(TK_E_INTERNAL, "piece queue overflow");
-  if (h[tk::CTRL_STATUS] & tk::ST_STALL)
-    return fail(TK_E_INTERNAL, "compaction look-back timed out");
+  if (int rc = internal_status(h[tk::CTRL_STATUS])) return rc;
   int rc = TK_OK;
   if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
@@ -616,16 +633,18 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   }
   if (residual != 0) {
     // cuts still fail after the queued passes: more passes from the host,
-    // one at a time. Every pass removes at least one cut, so this ends (at
-    // worst with each long piece as one segment); the bound only guards
+    // one at a time. Not expected: a queued pass from REPAIR_WHOLE on
+    // leaves no cut in a piece that failed, so the bound only guards
     // against a defect.
     int p = DEV_REPAIRS;
     if (stages) HIP_TRY(hipEventRecord(ev[5], s));
     while (residual != 0) {
-      if (++p > (int64_t)nb + DEV_REPAIRS + 1)
+      // (from pass REPAIR_WHOLE on, a piece that fails is merged whole and
+      // then has no cut left to fail: one such pass ends the repairs)
+      if (++p > DEV_REPAIRS + 2)
         return fail(TK_E_INTERNAL, "certification did not converge");
       const tk::DevWork wp = pass_work(w, ctrl, p);
-      HIP_TRY(tk::launch_apply_fail(wp, s));
+      HIP_TRY(tk::launch_apply_fail(wp, s, p >= tk::REPAIR_WHOLE, nlong));
       HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s));
       HIP_TRY(tk::launch_certify(e->t, wp, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
@@ -885,6 +904,17 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->cfg.artifact_sha256 = e->sha.c_str();
   e->cfg.expected_architecture = nullptr;
   e->arch = arch;
+  {
+    // a wait on another workgroup's published word gives up after WAIT_MS
+    // (far above any launch: the longest measured, a guarded block merge
+    // of a 32,000-space run, takes ~32 ms); another engine's kernels on
+    // the same device can delay a predecessor's dispatch by a launch
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate,
+                              cfg->device_ordinal) != hipSuccess || khz <= 0)
+      khz = 100000;  // the 100 MHz counter of CDNA3 / CDNA4
+    e->wait_ticks = (uint64_t)khz * WAIT_MS;
+  }
   auto bail = [&](int code) {
     tk_engine_close(e);
     return code;

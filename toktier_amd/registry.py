@@ -234,7 +234,8 @@ def suite_judged(evidence: dict, manifest: dict) -> bool:
     ``-m gpu`` selection ran (no ``-k``, nothing deselected), and no test
     failed or was skipped (tests parked in the source by an explicit skip
     mark with a reason are listed by node id under ``parked`` and counted
-    as collected, not as run)."""
+    as collected, not as run; each blocks the family it covers,
+    ``family_judged``)."""
     sel = evidence.get("selection") or {}
     ran = (evidence.get("passed", 0) + evidence.get("failed", 0)
            + evidence.get("skipped", 0) + len(evidence.get("parked") or []))
@@ -250,13 +251,19 @@ def suite_judged(evidence: dict, manifest: dict) -> bool:
 
 
 def family_judged(evidence: dict, manifest: dict, family: str) -> bool:
-    """Certified for `family`: the suite as a whole is judged, and the
-    family's own parity tests ran and all passed."""
-    fam = (evidence.get("families") or {}).get(family) or {}
+    """Certified for `family`: the suite as a whole is judged, the
+    family's own parity tests ran and all passed, and none of them, nor
+    any test shared by every family, is parked (a parked test is a case
+    of the family that no run covered)."""
+    fams = evidence.get("families") or {}
+    fam = fams.get(family) or {}
+    shared = fams.get("shared") or {}
     return (suite_judged(evidence, manifest)
             and fam.get("passed", 0) > 0
             and fam.get("failed", 1) == 0
-            and fam.get("skipped", 1) == 0)
+            and fam.get("skipped", 1) == 0
+            and fam.get("parked", 0) == 0
+            and shared.get("parked", 0) == 0)
 
 
 def generate(evidence: dict, manifest: dict, artifacts: dict[str, str]) -> dict:
