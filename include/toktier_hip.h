@@ -289,6 +289,13 @@ int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
  * splitmix64 open addressing) on every path. Returns TK_OK, or
  * TK_E_INVALID_ARG for an unknown option or value. */
 #define TK_OPT_COMPACT_PAIRS 1
+/* TK_OPT_REPAIR_WHOLE: pieces over 512 bytes are cut into segments and
+ * every cut certified; a failed cut is dropped and its segments redone, one
+ * repair pass after another. From this pass on (default 3; 1..64) a piece
+ * that still has a failed cut drops every cut and is merged whole by a
+ * workgroup, so the passes end. 0: every piece over 512 bytes is merged
+ * whole from the start, with no cut (the path of tables that drop bytes). */
+#define TK_OPT_REPAIR_WHOLE 2
 int tk_engine_set_option(tk_engine* engine, int option, int64_t value);
 
 /* Test-only fault injection (no counterpart in the reference; the hook its

@@ -298,6 +298,32 @@ def test_deepseek_marks_after_long_ascii_runs():
                     (len(s), cut)
 
 
+@pytest.mark.parametrize("name", ["llama_3_1_8b", "qwen3_8b"])
+def test_whole_piece_block_merges_match_oracle(name):
+    """Every piece over 512 bytes merged whole by a workgroup
+    (TK_OPT_REPAIR_WHOLE 0: 65,536-letter Latin and CJK runs, thousands of
+    guarded rounds on the Llama table), and merged whole from the first
+    repair pass (1): each run alone in a fresh small workspace and the C5
+    request whole, against the oracle."""
+    from toktier_amd import _ffi, workloads
+    k, t = kit(name), tok(name)
+    data = workloads.config5(k.json, n_chars=1_200_000, n_runs=4, sample=2).encode()
+    starts = k.oracle.pretokenize(data)
+    big = [(a, b) for a, b in zip(starts, starts[1:]) if b - a > 512]
+    assert len(big) >= 4
+    try:
+        for opt in (0, 1):
+            t.engine.set_option(_ffi.TK_OPT_REPAIR_WHOLE, opt)
+            for a, b in big:
+                piece = data[a:b]
+                assert np.array_equal(t.encode_bytes(piece),
+                                      k.oracle.encode_bytes(piece)), (name, opt, b - a)
+            assert np.array_equal(t.encode_bytes(data), k.oracle.encode_bytes(data)), \
+                (name, opt)
+    finally:
+        t.engine.set_option(_ffi.TK_OPT_REPAIR_WHOLE, 3)
+
+
 @pytest.mark.family("deepseek_v3")
 def test_deepseek_c5_runs_glued_to_marks_are_linear():
     """C5's text at full size with each of its ten 65,536-letter runs made

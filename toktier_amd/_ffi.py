@@ -34,6 +34,7 @@ TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
 TK_NOALLOC_MAX_BYTES = 1 << 20
 TK_OPT_COMPACT_PAIRS = 1
+TK_OPT_REPAIR_WHOLE = 2
 # added-token flags (tokenizer.json "added_tokens" fields)
 TK_ADDED_SPECIAL = 1
 TK_ADDED_SINGLE_WORD = 2
@@ -320,7 +321,10 @@ class Engine:
 
     def set_option(self, option: int, value: int) -> None:
         """``TK_OPT_COMPACT_PAIRS``: 1 probe the compact pair table (the
-        default when the artifact fits it), 0 the boundary-format table."""
+        default when the artifact fits it), 0 the boundary-format table.
+        ``TK_OPT_REPAIR_WHOLE``: the first certification repair pass that
+        merges a still-failing piece over 512 bytes whole (default 3); 0
+        merges every such piece whole, with no cut."""
         check(self._L.tk_engine_set_option(self._h, int(option), int(value)),
               "tk_engine_set_option")
 

@@ -2998,9 +2998,17 @@ __device__ void block_bpe(const DevTables& t, const DevWork& w, uint32_t a,
       }
       if (lsel) L.last = pl;
     }
-    // the merges: a selected symbol takes its right neighbour
+    // the merges: a selected symbol takes its right neighbour (a symbol
+    // without one, or one already merged away, means a broken state:
+    // reported, and nothing is written through its stale links)
     auto merge = [&](uint32_t i) {
-      const int32_t p = (int32_t)(a + i), q = nx[p], nn = nx[q];
+      const int32_t p = (int32_t)(a + i), q = nx[p];
+      if (q < (int32_t)a || q >= (int32_t)b || tok[p] == INVALID_ID ||
+          tok[q] == INVALID_ID) {
+        atomicOr(w.status, ST_ROUNDS);
+        return;
+      }
+      const int32_t nn = nx[q];
       tok[p] = prod;
       tok[q] = INVALID_ID;
       nx[p] = nn;
@@ -3035,6 +3043,9 @@ __device__ void block_bpe(const DevTables& t, const DevWork& w, uint32_t a,
       const uint64_t mc = block_min64(k, L);
       if (tid == 0) cmin[c] = mc;
     }
+    // thread 0's last chunk minimum must be written before the next round
+    // reads the minima (thread c reads chunk c's before any barrier)
+    __syncthreads();
   }
   if (hist && tid == 0) w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
   __syncthreads();

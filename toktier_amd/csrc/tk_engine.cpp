@@ -286,6 +286,10 @@ struct tk_engine {
   // bound of a device wait on another workgroup (DevWork::wait_ticks):
   // WAIT_MS in ticks of the device's real-time counter
   uint64_t wait_ticks = 0;
+  // TK_OPT_REPAIR_WHOLE: the first repair pass that merges a still-failing
+  // long piece whole; 0: every piece over WIDE_MAX bytes merged whole, no
+  // cuts (the path of tables that drop bytes)
+  int repair_whole = tk::REPAIR_WHOLE;
   // timing
   int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
   hipEvent_t ev[8] = {};
@@ -560,13 +564,16 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   const uint32_t nlong = e->gate[tk::GATE_NLONG];
   const uint32_t nrows = e->gate[tk::GATE_NROWS];
   const uint32_t nwide = e->gate[tk::GATE_NWIDE];
-  const uint32_t big = e->t.cert ? e->gate[tk::GATE_BIG] : 0;
+  // (cut / segment / certify, unless the pieces over WIDE_MAX bytes are
+  // merged whole: tables that drop bytes, or TK_OPT_REPAIR_WHOLE 0)
+  const bool cut = e->t.cert && e->repair_whole > 0;
+  const uint32_t big = cut ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
   // (pieces of 65..128 bytes are k_bpe_rows' too past PACK_ROWS_MAX)
   const bool rows = nrows > 0 || nlong > (uint32_t)tk::PACK_ROWS_MAX;
   const bool side2 = rows || nwide > 0 ||
-                     (!e->t.cert && e->gate[tk::GATE_BIG] > 0);
+                     (!cut && e->gate[tk::GATE_BIG] > 0);
   {
     // two independent jobs on two side streams: pieces of 129..WIDE_MAX
     // bytes merged whole, and the cut / segment / certify path of the
@@ -575,7 +582,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     // (a table that drops bytes merges its pieces over WIDE_MAX bytes
     // whole, a workgroup each, after the wide merges)
-    if (!e->t.cert && e->gate[tk::GATE_BIG] > 0)
+    if (!cut && e->gate[tk::GATE_BIG] > 0)
       HIP_TRY(tk::launch_long_block(e->t, w, s2));
     if (big) {
       // cut / segment / certify, then the repair passes, all on their own
@@ -585,7 +592,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
-        HIP_TRY(tk::launch_apply_fail(wp, s3, p >= tk::REPAIR_WHOLE, nlong));
+        HIP_TRY(tk::launch_apply_fail(wp, s3, p >= e->repair_whole, nlong));
         HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s3));
         HIP_TRY(tk::launch_certify(e->t, wp, 0, s3));
       }
@@ -641,10 +648,10 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     while (residual != 0) {
       // (from pass REPAIR_WHOLE on, a piece that fails is merged whole and
       // then has no cut left to fail: one such pass ends the repairs)
-      if (++p > DEV_REPAIRS + 2)
+      if (++p > std::max(DEV_REPAIRS, e->repair_whole) + 2)
         return fail(TK_E_INTERNAL, "certification did not converge");
       const tk::DevWork wp = pass_work(w, ctrl, p);
-      HIP_TRY(tk::launch_apply_fail(wp, s, p >= tk::REPAIR_WHOLE, nlong));
+      HIP_TRY(tk::launch_apply_fail(wp, s, p >= e->repair_whole, nlong));
       HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s));
       HIP_TRY(tk::launch_certify(e->t, wp, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
@@ -1221,6 +1228,12 @@ int tk_engine_set_option(tk_engine* e, int option, int64_t value) {
     if (value != 0 && value != 1)
       return fail(TK_E_INVALID_ARG, "TK_OPT_COMPACT_PAIRS takes 0 or 1");
     e->t.ctab = value && e->ctab.p ? e->ctab.p : nullptr;
+    return TK_OK;
+  }
+  if (option == TK_OPT_REPAIR_WHOLE) {
+    if (value < 0 || value > 64)
+      return fail(TK_E_INVALID_ARG, "TK_OPT_REPAIR_WHOLE takes 0..64");
+    e->repair_whole = (int)value;
     return TK_OK;
   }
   return fail(TK_E_INVALID_ARG, "unknown option %d", option);
