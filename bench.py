@@ -26,18 +26,26 @@ p99 over the same distinct requests after warm-ups, with chars/s and
 tokens/s. The 3.88 ms bar (``target_ms``) is quoted on this window.
 
 Also on the JSON line:
-- ``roofline``: the dominant kernel's (k_bpe_pack, the packed merge)
-  achieved bandwidth, taken as the per-request algorithmic bytes (UTF-8
-  bytes read once + 4 bytes per id written once) over its average duration
-  in the timed region, from the pair of HIP events its own dispatch takes
-  on the engine's stream (timing mode 2: one timed dispatch per request),
-  against the 8 TB/s HBM peak. ``traffic`` is the kernel's measured HBM
-  bytes per launch from the committed rocprofv3 counter summary
-  (profiles/c<config>_traffic.json) when it was taken on the library build
-  being run, else null.
-- ``stage_us``: per-stage device times from a second, untimed pass over the
-  same requests with an event on every stage boundary (timing mode 1; those
-  events add a few microseconds each, so that pass is not the timed one).
+- ``roofline``: the dominant kernel's achieved bandwidth, taken as the
+  per-request algorithmic bytes (UTF-8 bytes read once + 4 bytes per id
+  written once) over its average duration in the timed region. The
+  dominant kernel is the one with the largest median own duration in an
+  untimed stage pass over the timed requests, with every kernel timed on
+  its own dispatch (timing mode 1); the timed loop then times that
+  kernel's dispatch alone, with
+  the pair of HIP events it takes on the stream it runs on (timing mode 2,
+  ``TK_OPT_TIMED_KERNEL``). Against the 8 TB/s HBM peak. ``traffic`` is
+  its measured HBM bytes per launch from the committed rocprofv3 counter
+  summary (profiles/c<config>_traffic.json) when that was taken on the
+  library build being run and on the same kernel, else null.
+- ``stage_us`` / ``kernels_us``: per-stage device times and every kernel's
+  own mean duration from a second, untimed pass over the same requests
+  (timing mode 1; those events add a few microseconds each, so that pass
+  is not the timed one).
+- ``other_configs`` (the default C2 run only; ``--no-legs`` skips it): C3,
+  C4 and C5 with ``--leg-steps`` distinct requests each: protocol p50 /
+  p90 / p99, the device-resident time, parity against the oracle, the
+  dominant kernel and its roofline fraction, each kernel's duration.
 - ``cpu_baseline``: the C restatement (oracle) timed on this host's cores on
   a bounded sample of the same workload, on every core the process may use
   (one request per thread); ``cpu_lanes`` adds the same on one core and
@@ -304,6 +312,293 @@ def cpu_lanes(tok, config: int, reqs, budget_s: float) -> tuple[dict, dict]:
     return base, lanes
 
 
+# ------------------------------------------------------------ measurement
+
+def kernel_names():
+    from toktier_amd._ffi import KERNELS
+    return KERNELS
+
+
+def kernel_pass(eng, run, idxs):
+    """Timing mode 1 over the requests `idxs` (untimed: every kernel's own
+    dispatch carries an event pair, which delays the next dispatch by a few
+    microseconds): per request the stage times [0..4] and each kernel's own
+    duration (0 when the call did not launch it)."""
+    names = kernel_names()
+    eng.set_timing(1)
+    st, ku = [], []
+    for i in idxs:
+        run(i)
+        t = eng.last_timing()
+        st.append(t[:5])
+        ku.append(t[8:8 + len(names)])
+    eng.set_timing(0)
+    return np.asarray(st), np.asarray(ku)
+
+
+def dominant_kernel(ku) -> int:
+    """The kernel with the largest median own duration per request."""
+    return int(np.argmax(np.median(np.asarray(ku), axis=0)))
+
+
+def launch_mean(xs) -> float:
+    """Mean duration over the requests that launched the kernel."""
+    xs = [x for x in xs if x > 0]
+    return float(np.mean(xs)) if xs else 0.0
+
+
+def roofline(kernel: str, kernel_us: float, b_alg: float, traffic) -> dict:
+    achieved = b_alg / (kernel_us * 1e-6) / 1e9 if kernel_us > 0 else 0.0
+    return {"bound": "hbm", "kernel": kernel, "kernel_us": round(kernel_us, 2),
+            "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": traffic,
+            "alg_bytes_per_launch": int(b_alg)}
+
+
+def measure_single(tok, reqs, K, W, seed=False, plain=True):
+    """Requests 0..K-1 timed, K..K+W-1 warm-ups. After the warm-ups, an
+    untimed stage pass over the timed requests with every kernel timed
+    (mode 1) names the dominant kernel (largest median own duration); the
+    timed loop (device-resident: bytes in HBM, ids compacted into a device
+    buffer) times that kernel's own dispatch only (mode 2); then the
+    protocol window (host UTF-8 in, host uint32 ids out) over the same
+    requests."""
+    import torch
+    import toktier_amd
+    from toktier_amd import _ffi
+    eng = tok.engine
+    dev = torch.device("cuda:0")
+    d_texts = [torch.frombuffer(bytearray(r), dtype=torch.uint8).to(dev)
+               for r in reqs]
+    cap = max(len(r) for r in reqs)
+    d_ids = [torch.empty(cap, dtype=torch.int32, device=dev)
+             for _ in range(K + W)]
+    stride = toktier_amd.SPAN_CHECKPOINT_STRIDE
+    n_pts = cap // stride + 1
+    d_pts = ([torch.empty(3 * n_pts, dtype=torch.int64, device=dev)
+              for _ in range(K + W)] if seed else [])
+    torch.cuda.synchronize()
+
+    def run(i):
+        d = d_texts[i]
+        if seed:
+            return eng.encode_seed(d.data_ptr(), d.numel(), d_ids[i].data_ptr(),
+                                   cap, stride, d_pts[i].data_ptr(), n_pts)[0]
+        return eng.encode_device(d.data_ptr(), d.numel(), d_ids[i].data_ptr(), cap)
+
+    for i in range(K, K + W):
+        run(i)
+    stages, ku = kernel_pass(eng, run, range(K))
+    kdom = dominant_kernel(ku)
+    eng.set_option(_ffi.TK_OPT_TIMED_KERNEL, kdom)
+    eng.set_timing(2)
+    torch.cuda.synchronize()
+    lat, kus, n_ids = [], [], []
+    t_all = time.perf_counter()
+    for i in range(K):
+        t1 = time.perf_counter()
+        n_ids.append(run(i))
+        lat.append((time.perf_counter() - t1) * 1e3)
+        kus.append(eng.last_timing()[1])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_all
+    eng.set_timing(0)
+    ids_dev = [d_ids[i][:n_ids[i]].cpu().numpy().view(np.uint32).copy()
+               for i in range(K)]
+
+    # the protocol window, into a reused numpy id buffer as a serving loop
+    # keeps one: page-locked (the compaction kernel writes the ids straight
+    # into it) and plain pageable memory (through the engine's pinned
+    # staging); the request bytes are ordinary Python bytes either way
+    out_pinned = torch.empty(cap + 1, dtype=torch.int32,
+                             pin_memory=True).numpy().view(np.uint32)
+    out_plain = np.zeros(cap + 1, dtype=np.uint32)
+
+    def protocol(out):
+        for i in range(K, K + W):
+            eng.encode(reqs[i], out=out)
+        lat_, parts_, ok_ = [], [], True
+        for i in range(K):
+            t1 = time.perf_counter()
+            got = eng.encode(reqs[i], out=out)
+            lat_.append((time.perf_counter() - t1) * 1e3)
+            parts_.append(eng.last_timing()[5:8])
+            if not np.array_equal(got, ids_dev[i]):
+                log(f"host/device id mismatch on request {i}")
+                ok_ = False
+        return lat_, parts_, ok_
+    host_lat, host_parts, ok1 = protocol(out_pinned)
+    plain_lat, plain_parts, ok2 = protocol(out_plain) if plain else ([], [], True)
+    return {"lat": lat, "wall": wall, "kernel": kdom, "kernel_us": kus,
+            "ids": ids_dev, "stages": stages, "ku": ku,
+            "host_lat": host_lat, "host_parts": host_parts,
+            "plain_lat": plain_lat, "plain_parts": plain_parts,
+            "host_ok": ok1 and ok2, "d_pts": d_pts, "stride": stride}
+
+
+def measure_batch(tok, reqs, K, W):
+    """C3: a ragged batch per step through tk_engine_encode_batch (host
+    documents in, host ids and row offsets out). An untimed stage pass
+    (mode 1) names the dominant kernel; the timed loop times its dispatch
+    (mode 2). Here k_compact writes the ids straight into page-locked host
+    memory, so its duration includes that PCIe write."""
+    from toktier_amd import _ffi
+    eng = tok.engine
+
+    def run(i):
+        return eng.encode_batch(reqs[i])
+    for i in range(K, K + W):
+        run(i)
+    stages, ku = kernel_pass(eng, run, range(K))
+    kdom = dominant_kernel(ku)
+    eng.set_option(_ffi.TK_OPT_TIMED_KERNEL, kdom)
+    eng.set_timing(2)
+    lat, rows_all, kus = [], [], []
+    t_all = time.perf_counter()
+    for i in range(K):
+        t1 = time.perf_counter()
+        ids, rows, status = run(i)
+        lat.append((time.perf_counter() - t1) * 1e3)
+        kus.append(eng.last_timing()[1])
+        rows_all.append((ids[:int(rows[-1])].copy(), rows.copy(), status.copy()))
+    wall = time.perf_counter() - t_all
+    eng.set_timing(0)
+    return {"lat": lat, "wall": wall, "kernel": kdom, "kernel_us": kus,
+            "rows": rows_all, "stages": stages, "ku": ku}
+
+
+def check_parity(tok, reqs, ids) -> int:
+    """Every request against the oracle (threads: the C calls release the
+    GIL); returns the number of mismatching requests."""
+    from concurrent.futures import ThreadPoolExecutor
+    orc = make_oracle(tok)
+
+    def one(i):
+        want = orc.encode_bytes(reqs[i])
+        return not (isinstance(want, int) or not np.array_equal(want, ids[i]))
+    n = max(1, min(MAX_WORKERS, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(n) as ex:
+        ok = list(ex.map(one, range(len(reqs))))
+    mism = len(ok) - sum(ok)
+    log(f"parity: {sum(ok)}/{len(ok)} requests bit-identical to the oracle")
+    return mism
+
+
+def check_batch_parity(tok, reqs, rows_all) -> int:
+    """Every row of every batch against the oracle's encode of that
+    document alone; returns the number of batches with a mismatching row."""
+    from concurrent.futures import ThreadPoolExecutor
+    orc = make_oracle(tok)
+
+    def one(i):
+        ids, rows, status = rows_all[i]
+        for d, doc in enumerate(reqs[i]):
+            want = orc.encode_bytes(doc)
+            got = ids[int(rows[d]):int(rows[d + 1])]
+            if status[d] != 0 or isinstance(want, int) or not np.array_equal(got, want):
+                return 1
+        return 0
+    n = max(1, min(MAX_WORKERS, len(os.sched_getaffinity(0))))
+    with ThreadPoolExecutor(n) as ex:
+        bad = list(ex.map(one, range(len(rows_all))))
+    log(f"parity: {len(bad) - sum(bad)}/{len(bad)} batches with every row "
+        f"bit-identical to the oracle")
+    return sum(bad)
+
+
+def check_seed(tok, reqs, ids_dev, d_pts, stride, K) -> int:
+    """The checkpoints of two requests against the store's restated
+    construction over the engine's ids."""
+    from oracle.oracle import span_checkpoints, token_byte_lengths
+    lens = token_byte_lengths(tok._json)
+    for t in tok.added_tokens:
+        lens[t.id] = len(t.content.encode("utf-8"))
+    mism = 0
+    for i in range(min(K, 2)):
+        m = (ids_dev[i].size + stride - 1) // stride
+        got = d_pts[i][:3 * m].cpu().numpy().view(np.uint64).reshape(m, 3)
+        want = span_checkpoints(reqs[i], ids_dev[i], lens, stride)
+        if not np.array_equal(got, want):
+            mism += 1
+            log(f"seed checkpoints differ on request {i}")
+    return mism
+
+
+STAGE_NAMES = ["pretokenize and piece lists (k_added, k_pretok)",
+               "k_bpe_pack",
+               "long pieces past k_bpe_pack (k_bpe_rows, k_bpe_wide, k_long_*, "
+               "k_certify; side streams)",
+               "compaction (k_compact)"]
+
+
+def kernel_summary(ku) -> dict:
+    """Each kernel's mean own duration (us) over the requests that
+    launched it, from the stage pass."""
+    names = kernel_names()
+    ku = np.asarray(ku)
+    return {n: round(launch_mean(ku[:, k]), 2) for k, n in enumerate(names)
+            if (ku[:, k] > 0).any()}
+
+
+LEG_WORKLOADS = {
+    3: "C3: GPT-2, a ragged batch of 256 requests of U[1,024, 32,768] chars "
+       "(host documents in, host ids and row offsets out)",
+    4: "C4: Llama-3, one 4,194,304-char code-like request",
+    5: "C5: Qwen3, one 4,194,304-char request, 50% CJK, 10% emoji, ten "
+       "65,536-char letter runs",
+}
+
+
+def leg(config: int, K: int, W: int, gen_workers: int) -> dict:
+    """A compact line for another configuration: protocol latency, the
+    device-resident time, parity against the oracle, the dominant kernel
+    and its roofline fraction."""
+    import toktier_amd
+    from toktier_amd import workloads
+    fam = workloads.CONFIGS[config][0]
+    t0 = time.perf_counter()
+    reqs = make_requests(config, fam, False, K + W, workloads.CHARS_4M,
+                         max_workers=gen_workers)
+    log(f"leg C{config}: {K + W} requests in {time.perf_counter() - t0:.1f}s")
+    import torch  # noqa: F401
+    tok = toktier_amd.load(fam)
+    names = kernel_names()
+    try:
+        if config == 3:
+            m = measure_batch(tok, reqs, K, W)
+            mism = check_batch_parity(tok, reqs[:K], m["rows"])
+            n_tok = float(np.mean([r[0].size for r in m["rows"]]))
+            n_bytes = float(np.mean([sum(len(d) for d in r) for r in reqs[:K]]))
+            host = m["lat"]
+            dev_ms = None
+        else:
+            m = measure_single(tok, reqs, K, W, plain=False)
+            mism = check_parity(tok, reqs[:K], m["ids"]) + (0 if m["host_ok"] else 1)
+            n_tok = float(np.mean([a.size for a in m["ids"]]))
+            n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
+            host = m["host_lat"]
+            dev_ms = pcts(m["lat"])
+        chars = float(np.mean([n_chars_of(r) for r in reqs[:K]]))
+        kname = names[m["kernel"]]
+        out = {
+            "workload": LEG_WORKLOADS[config],
+            "family": fam, "requests": K, "warmup": W, "chars": int(chars),
+            "bytes": int(n_bytes), "tokens": int(n_tok),
+            "protocol_latency_ms": pcts(host),
+            "protocol_mchars_per_s": round(chars / (np.mean(host) * 1e-3) / 1e6, 2),
+            "device_resident_latency_ms": dev_ms,
+            "roofline": roofline(kname, launch_mean(m["kernel_us"]),
+                                 n_bytes + 4.0 * n_tok,
+                                 measured_traffic(config, kname)),
+            "kernels_us": kernel_summary(m["ku"]),
+            "parity": {"checked": K, "mismatches": mism,
+                       "against": "CPU oracle" + (", every row" if config == 3 else "")},
+        }
+    finally:
+        tok.close()
+    return out
+
+
 # ------------------------------------------------------------ main
 
 def main() -> int:
@@ -325,6 +620,10 @@ def main() -> int:
                          "second workload line, not the contract line")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline lanes")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the C3 / C4 / C5 legs of the default run")
+    ap.add_argument("--leg-steps", type=int, default=8,
+                    help="requests per C3 / C4 / C5 leg")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="time budget of each CPU lane")
     ap.add_argument("--no-check", action="store_true",
@@ -384,118 +683,92 @@ def main() -> int:
         t.added_tokens = toktier_amd.added_tokens(t._json)
         cpu, lanes = cpu_lanes(t, args.config, reqs, args.cpu_seconds)
 
-    import torch
+    import torch  # noqa: F401  (before the engine opens: torch's HIP init first)
     tok = toktier_amd.load(fam)
-    eng = tok.engine
-    dev = torch.device("cuda:0")
-
+    names = kernel_names()
+    plain_traffic = not (args.chat or args.family or args.seed)
     if batch:
-        return bench_batch(args, tok, reqs, K, W, cpu, lanes)
-
-    d_texts = [torch.frombuffer(bytearray(r), dtype=torch.uint8).to(dev)
-               for r in reqs]
-    cap = max(len(r) for r in reqs)
-    # one id buffer per request: the ids are copied out after the timed
-    # region, so the steps run back to back
-    d_ids = [torch.empty(cap, dtype=torch.int32, device=dev)
-             for _ in range(K + W)]
-    torch.cuda.synchronize()
-    eng.set_timing(2)  # k_bpe_pack's own dispatch only
-
-    stride = toktier_amd.SPAN_CHECKPOINT_STRIDE
-    n_pts = cap // stride + 1
-    d_pts = ([torch.empty(3 * n_pts, dtype=torch.int64, device=dev)
-              for _ in range(K + W)] if args.seed else [])
-
-    def run(i):
-        d = d_texts[i]
-        if args.seed:
-            return eng.encode_seed(d.data_ptr(), d.numel(), d_ids[i].data_ptr(),
-                                   cap, stride, d_pts[i].data_ptr(), n_pts)[0]
-        return eng.encode_device(d.data_ptr(), d.numel(), d_ids[i].data_ptr(),
-                                 cap)
-
-    for i in range(W):
-        run(K + i)
-    torch.cuda.synchronize()
-    lat, pack_us, n_ids = [], [], []
-    t_all = time.perf_counter()
-    for i in range(K):
-        t1 = time.perf_counter()
-        n_ids.append(run(i))
-        lat.append((time.perf_counter() - t1) * 1e3)
-        pack_us.append(eng.last_timing()[1])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_all
-    ms_per_step = float(np.mean(lat))
-    ids_dev = [d_ids[i][:n_ids[i]].cpu().numpy().view(np.uint32).copy()
-               for i in range(K)]
-
-    # per-stage breakdown: the same requests again, events on every stage
-    eng.set_timing(1)
-    stages = []
-    for i in range(K):
-        if run(i) != ids_dev[i].size:
-            log(f"stage pass: id count differs on request {i}")
-            return 1
-        stages.append(eng.last_timing())
-    eng.set_timing(0)
-
-    # the protocol window: host bytes in -> host ids out, into a reused
-    # numpy id buffer as a serving loop keeps one: page-locked (the serving
-    # configuration: the compaction kernel writes the ids straight into
-    # it), and plain pageable memory (through the engine's pinned staging);
-    # the request bytes are ordinary Python bytes either way
-    out_pinned = torch.empty(cap + 1, dtype=torch.int32,
-                             pin_memory=True).numpy().view(np.uint32)
-    out_plain = np.zeros(cap + 1, dtype=np.uint32)  # pages touched once
-
-    def protocol(out):
-        for i in range(W):
-            eng.encode(reqs[K + i], out=out)
-        lat_, parts_, ok_ = [], [], True
-        for i in range(K):
-            t1 = time.perf_counter()
-            got = eng.encode(reqs[i], out=out)
-            lat_.append((time.perf_counter() - t1) * 1e3)
-            parts_.append(eng.last_timing()[5:8])
-            if not np.array_equal(got, ids_dev[i]):
-                log(f"host/device id mismatch on request {i}")
-                ok_ = False
-        return lat_, parts_, ok_
-    host_lat, host_parts, host_ok = protocol(out_pinned)
-    plain_lat, plain_parts, plain_ok = protocol(out_plain)
-    host_ok = host_ok and plain_ok
-
-    mism = 0 if host_ok else 1
-    if not args.no_check:
-        mism += check_parity(tok, reqs[:K], ids_dev)
-        if args.seed:
-            mism += check_seed(tok, reqs, ids_dev, d_pts, stride, K)
-
-    n_tok = float(np.mean([a.size for a in ids_dev]))
-    n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
+        m = measure_batch(tok, reqs, K, W)
+        mism = 0 if args.no_check else check_batch_parity(tok, reqs[:K], m["rows"])
+        n_tok = float(np.mean([r[0].size for r in m["rows"]]))
+        n_bytes = float(np.mean([sum(len(d) for d in r) for r in reqs[:K]]))
+        ms = float(np.mean(m["lat"]))
+        host_lat = m["lat"]
+    else:
+        m = measure_single(tok, reqs, K, W, seed=args.seed)
+        mism = 0 if m["host_ok"] else 1
+        if not args.no_check:
+            mism += check_parity(tok, reqs[:K], m["ids"])
+            if args.seed:
+                mism += check_seed(tok, reqs, m["ids"], m["d_pts"], m["stride"], K)
+        n_tok = float(np.mean([a.size for a in m["ids"]]))
+        n_bytes = float(np.mean([len(r) for r in reqs[:K]]))
+        ms = float(np.mean(m["lat"]))
+        host_lat = m["host_lat"]
     chars = float(np.mean([n_chars_of(r) for r in reqs[:K]]))
-    st = np.asarray(stages)  # [K, 5]: pretok, bpe_small, bpe_long, compact, total
-    names = ["pretokenize and piece lists (k_added, k_pretok)",
-             "k_bpe_pack",
-             "long pieces past k_bpe_pack (k_bpe_rows, k_bpe_wide, k_long_*, "
-             "k_certify; side streams)",
-             "compaction (k_compact)"]
-    avg = st[:, :4].mean(axis=0)
-    pack_avg_us = float(np.mean(pack_us))
     b_alg = n_bytes + 4.0 * n_tok
-    achieved = b_alg / (pack_avg_us * 1e-6) / 1e9
+    kname = names[m["kernel"]]
     host_ms = float(np.mean(host_lat))
-
+    st = np.asarray(m["stages"])
+    if batch:
+        workload = (f"C3: {fam}, a ragged batch of 256 requests of U[1,024, "
+                    "32,768] chars per step, host documents in, host ids and "
+                    "row offsets out (tk_engine_encode_batch; the engine takes "
+                    "batches from host memory only, so value is host-to-host)")
+    else:
+        workload = (f"C{args.config}{' chat' if args.chat else ''}"
+                    f"{' seed' if args.seed else ''}: {fam}, one fresh request "
+                    f"of {n_chars:,} chars"
+                    f"{' in chat turns (added-token literals)' if args.chat else ''}"
+                    ", bytes resident in HBM"
+                    f"{'; ids plus span checkpoints every 4096 tokens (tk_engine_encode_seed)' if args.seed else ''}")
+    protocol = {
+        "window": ("host UTF-8 buffer in -> host uint32 ids out "
+                   "(tk_engine_encode, transfers included); request bytes in "
+                   "pageable memory, ids into a reused page-locked numpy "
+                   "buffer") if not batch else
+                  ("host documents in -> host uint32 ids and row offsets out "
+                   "(tk_engine_encode_batch, transfers included)"),
+        "latency_ms": pcts(host_lat),
+        "mean_ms": round(host_ms, 4),
+        "all_ms": [round(x, 3) for x in host_lat],
+        "mchars_per_s": round(chars / (host_ms * 1e-3) / 1e6, 2),
+        "tokens_per_s": round(n_tok / (host_ms * 1e-3), 1),
+        "target_ms": TARGET_MS,
+        "meets_target_p99": bool(pct(host_lat, 99) <= TARGET_MS),
+    }
+    if not batch:
+        protocol["parts_us"] = {n: round(float(v), 1) for n, v in zip(
+            ["bytes in (copy threads into the pinned staging)",
+             "pipeline (one DMA in, the kernels, ids written into the "
+             "page-locked buffer by k_compact)",
+             "ids out (copy threads; none for a page-locked buffer)"],
+            np.mean(np.asarray(m["host_parts"]), axis=0))}
+        protocol["pageable_ids"] = {
+            "window": "the same, ids into a reused pageable numpy buffer "
+                      "(k_compact writes the engine's pinned staging, the "
+                      "copy threads fill the buffer from it)",
+            "latency_ms": pcts(m["plain_lat"]),
+            "mean_ms": round(float(np.mean(m["plain_lat"])), 4),
+            "parts_us": {n: round(float(v), 1) for n, v in zip(
+                ["bytes in", "pipeline", "ids out"],
+                np.mean(np.asarray(m["plain_parts"]), axis=0))},
+        }
+    rl = roofline(kname, launch_mean(m["kernel_us"]), b_alg,
+                  measured_traffic(args.config, kname) if plain_traffic else None)
+    rl["path_achieved"] = round(b_alg / (ms * 1e-3) / 1e9, 3)
+    rl["chosen_by"] = ("the largest median own duration per request among "
+                       f"{', '.join(names)} in the untimed stage pass over "
+                       "the timed requests (every kernel timed); then timed "
+                       "on its own dispatch in the timed region")
     line = {
         "metric": METRIC,
-        "value": round(chars / (ms_per_step * 1e-3) / 1e6, 2),
+        "value": round(chars / (ms * 1e-3) / 1e6, 2),
         "unit": "Mchars/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -504,188 +777,35 @@ def main() -> int:
                 "stand-in vocabulary of the family; every step a distinct "
                 "seeded request",
         "config": {
-            "workload": f"C{args.config}{' chat' if args.chat else ''}"
-                        f"{' seed' if args.seed else ''}: "
-                        f"{fam}, one fresh request of {n_chars:,} chars"
-                        f"{' in chat turns (added-token literals)' if args.chat else ''}"
-                        ", bytes resident in HBM"
-                        f"{'; ids plus span checkpoints every 4096 tokens (tk_engine_encode_seed)' if args.seed else ''}",
-            "family": fam, "chars": int(chars), "bytes": int(n_bytes),
-            "tokens": int(n_tok), "requests": K, "distinct_requests": True,
-            "samples": [1, K + W],
-        },
-        "latency_ms": pcts(lat),
-        "protocol": {
-            "window": "host UTF-8 buffer in -> host uint32 ids out "
-                      "(tk_engine_encode, transfers included); request bytes "
-                      "in pageable memory, ids into a reused page-locked "
-                      "numpy buffer",
-            "latency_ms": pcts(host_lat),
-            "mean_ms": round(host_ms, 4),
-            "all_ms": [round(x, 3) for x in host_lat],
-            "parts_us": {n: round(float(v), 1) for n, v in zip(
-                ["bytes in (copy threads into the pinned staging)",
-                 "pipeline (one DMA in, the kernels, ids written into the "
-                 "page-locked buffer by k_compact)",
-                 "ids out (copy threads; none for a page-locked buffer)"],
-                np.mean(np.asarray(host_parts), axis=0))},
-            "mchars_per_s": round(chars / (host_ms * 1e-3) / 1e6, 2),
-            "tokens_per_s": round(n_tok / (host_ms * 1e-3), 1),
-            "target_ms": TARGET_MS,
-            "meets_target_p99": bool(pct(host_lat, 99) <= TARGET_MS),
-            "pageable_ids": {
-                "window": "the same, ids into a reused pageable numpy buffer "
-                          "(k_compact writes the engine's pinned staging, the "
-                          "copy threads fill the buffer from it)",
-                "latency_ms": pcts(plain_lat),
-                "mean_ms": round(float(np.mean(plain_lat)), 4),
-                "parts_us": {n: round(float(v), 1) for n, v in zip(
-                    ["bytes in", "pipeline", "ids out"],
-                    np.mean(np.asarray(plain_parts), axis=0))},
-            },
-        },
-        "tokens_per_s": round(n_tok / (ms_per_step * 1e-3), 1),
-        "stage_us": {n: round(float(v), 2) for n, v in zip(names, avg)},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "k_bpe_pack",
-            "kernel_us": round(pack_avg_us, 2),
-            "achieved": round(achieved, 3),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 6),
-            "traffic": (None if args.chat or args.family or args.seed else
-                        measured_traffic(args.config, "k_bpe_pack")),
-            "alg_bytes_per_launch": int(b_alg),
-            "path_achieved": round(b_alg / (ms_per_step * 1e-3) / 1e9, 3),
-        },
-        "cpu_baseline": cpu,
-        "cpu_lanes": lanes,
-        "parity": {"checked": 0 if args.no_check else K, "mismatches": mism,
-                   "against": "CPU oracle (C restatement), every timed request"},
-        "wall_s": round(wall, 3),
-    }
-    print(json.dumps(line), flush=True)
-    tok.close()
-    return 0 if mism == 0 else 1
-
-
-def check_parity(tok, reqs, ids) -> int:
-    """Every request against the oracle (threads: the C calls release the
-    GIL); returns the number of mismatching requests."""
-    from concurrent.futures import ThreadPoolExecutor
-    orc = make_oracle(tok)
-
-    def one(i):
-        want = orc.encode_bytes(reqs[i])
-        return not (isinstance(want, int) or not np.array_equal(want, ids[i]))
-    n = max(1, min(MAX_WORKERS, len(os.sched_getaffinity(0))))
-    with ThreadPoolExecutor(n) as ex:
-        ok = list(ex.map(one, range(len(reqs))))
-    mism = len(ok) - sum(ok)
-    log(f"parity: {sum(ok)}/{len(ok)} requests bit-identical to the oracle")
-    return mism
-
-
-def check_seed(tok, reqs, ids_dev, d_pts, stride, K) -> int:
-    """The checkpoints of two requests against the store's restated
-    construction over the engine's ids."""
-    from oracle.oracle import span_checkpoints, token_byte_lengths
-    lens = token_byte_lengths(tok._json)
-    for t in tok.added_tokens:
-        lens[t.id] = len(t.content.encode("utf-8"))
-    mism = 0
-    for i in range(min(K, 2)):
-        m = (ids_dev[i].size + stride - 1) // stride
-        got = d_pts[i][:3 * m].cpu().numpy().view(np.uint64).reshape(m, 3)
-        want = span_checkpoints(reqs[i], ids_dev[i], lens, stride)
-        if not np.array_equal(got, want):
-            mism += 1
-            log(f"seed checkpoints differ on request {i}")
-    return mism
-
-
-def bench_batch(args, tok, reqs, K, W, cpu, lanes) -> int:
-    """C3: a ragged batch of 256 requests per step through
-    tk_engine_encode_batch (host documents in, host ids and row offsets
-    out); every row of every timed batch checked against the oracle's
-    encode of that document alone."""
-    eng = tok.engine
-    for i in range(W):
-        eng.encode_batch(reqs[K + i])
-    lat, rows_all = [], []
-    t_all = time.perf_counter()
-    for i in range(K):
-        t1 = time.perf_counter()
-        ids, rows, status = eng.encode_batch(reqs[i])
-        lat.append((time.perf_counter() - t1) * 1e3)
-        rows_all.append((ids[:int(rows[-1])].copy(), rows.copy(), status.copy()))
-    wall = time.perf_counter() - t_all
-    mism = 0
-    if not args.no_check:
-        from concurrent.futures import ThreadPoolExecutor
-        orc = make_oracle(tok)
-
-        def one(i):
-            ids, rows, status = rows_all[i]
-            bad = 0
-            for d, doc in enumerate(reqs[i]):
-                want = orc.encode_bytes(doc)
-                got = ids[int(rows[d]):int(rows[d + 1])]
-                if status[d] != 0 or isinstance(want, int) or \
-                        not np.array_equal(got, want):
-                    bad += 1
-            return bad
-        n = max(1, min(MAX_WORKERS, len(os.sched_getaffinity(0))))
-        with ThreadPoolExecutor(n) as ex:
-            bad_rows = list(ex.map(one, range(K)))
-        mism = sum(1 for b in bad_rows if b)
-        log(f"parity: {K - mism}/{K} batches with every row bit-identical "
-            f"to the oracle ({sum(len(r) for r in reqs[:K])} rows)")
-    ms = float(np.mean(lat))
-    chars = float(np.mean([n_chars_of(r) for r in reqs[:K]]))
-    n_bytes = float(np.mean([sum(len(d) for d in r) for r in reqs[:K]]))
-    n_tok = float(np.mean([r[0].size for r in rows_all]))
-    line = {
-        "metric": METRIC,
-        "value": round(chars / (ms * 1e-3) / 1e6, 2),
-        "unit": "Mchars/s",
-        "n_gpus": 1, "steps": K, "warmup": W,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8",
-        "data": "synthetic: seeded Zipf token-concat generator over the "
-                "stand-in vocabulary of the family; every step a distinct "
-                "seeded batch",
-        "config": {
-            "workload": f"C3: {tok.family.name}, a ragged batch of 256 "
-                        "requests of U[1,024, 32,768] chars per step, host "
-                        "documents in, host ids and row offsets out "
-                        "(tk_engine_encode_batch; the engine takes batches "
-                        "from host memory only, so value is host-to-host)",
-            "family": tok.family.name, "chars": int(chars),
+            "workload": workload, "family": fam, "chars": int(chars),
             "bytes": int(n_bytes), "tokens": int(n_tok), "requests": K,
-            "rows_per_request": len(reqs[0]), "distinct_requests": True,
-            "samples": [1, K + W],
+            "distinct_requests": True, "samples": [1, K + W],
+            **({"rows_per_request": len(reqs[0])} if batch else {}),
         },
-        "latency_ms": pcts(lat),
-        "protocol": {
-            "window": "host documents in -> host uint32 ids and row offsets "
-                      "out (tk_engine_encode_batch, transfers included)",
-            "latency_ms": pcts(lat), "mean_ms": round(ms, 4),
-            "mchars_per_s": round(chars / (ms * 1e-3) / 1e6, 2),
-            "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
-        },
+        "latency_ms": pcts(m["lat"]),
+        "protocol": protocol,
+        "host_to_host_ms": {"p50": protocol["latency_ms"]["p50"],
+                            "p99": protocol["latency_ms"]["p99"]},
         "tokens_per_s": round(n_tok / (ms * 1e-3), 1),
-        "roofline": None,
+        "stage_us": {n: round(float(v), 2) for n, v in zip(STAGE_NAMES, st[:, :4].mean(axis=0))},
+        "kernels_us": kernel_summary(m["ku"]),
+        "roofline": rl,
         "cpu_baseline": cpu,
         "cpu_lanes": lanes,
         "parity": {"checked": 0 if args.no_check else K, "mismatches": mism,
-                   "against": "CPU oracle, every row of every timed batch"},
-        "wall_s": round(wall, 3),
+                   "against": "CPU oracle (C restatement), every timed request"
+                              + (", every row" if batch else "")},
+        "wall_s": round(m["wall"], 3),
     }
-    print(json.dumps(line), flush=True)
     tok.close()
+    if (args.config == 2 and not (args.family or args.chat or args.seed
+                                  or args.no_legs)):
+        line["other_configs"] = {}
+        for c in (3, 4, 5):
+            lg = leg(c, max(1, args.leg_steps), 2, args.gen_workers)
+            line["other_configs"][f"C{c}"] = lg
+            mism += lg["parity"]["mismatches"]
+    print(json.dumps(line), flush=True)
     return 0 if mism == 0 else 1
 
 

@@ -274,12 +274,22 @@ const char* tk_engine_architecture(const tk_engine* engine); /* "gfx950" */
  * events taken by the dispatches themselves. Mode 1 (every stage): [0]
  * pretokenize and piece listing, [1] short-piece BPE, [2] the time the
  * long-piece BPE (run beside the short-piece BPE) went past it, [3]
- * compaction, [4] total. Mode 2 (least disturbance): [1] the short-piece
- * BPE kernel's own duration, the others 0. Mode 0 (default): nothing is
- * recorded. Host wall times of the last tk_engine_encode, in every mode:
- * [5] the request bytes into device memory, [6] the pipeline up to the ids
- * being final in device memory, [7] the ids into the caller's buffer.
- * Returns the number of values written (<= n). */
+ * compaction, [4] total, and [8 + k] the own duration of kernel k
+ * (TK_KERNEL_*; 0 when the call did not launch it). Mode 2 (least
+ * disturbance): [1] the own duration of the one kernel TK_OPT_TIMED_KERNEL
+ * names (default TK_KERNEL_BPE_PACK; 0 when the call did not launch it),
+ * the others 0. Mode 0 (default): nothing is recorded. Host wall times of
+ * the last tk_engine_encode, in every mode: [5] the request bytes into
+ * device memory, [6] the pipeline up to the ids being final in device
+ * memory, [7] the ids into the caller's buffer. Returns the number of
+ * values written (<= n, at most 8 + TK_KERNELS). */
+#define TK_KERNEL_PRETOK 0       /* k_pretok: pretokenize, list the pieces */
+#define TK_KERNEL_BPE_PACK 1     /* k_bpe_pack: pieces of up to 128 bytes */
+#define TK_KERNEL_COMPACT 2      /* k_compact: ids compacted */
+#define TK_KERNEL_BPE_ROWS 3     /* k_bpe_rows: pieces of 129-256 bytes */
+#define TK_KERNEL_LONG_WINDOWS 4 /* k_long_windows: cuts of pieces > 512 B */
+#define TK_KERNEL_ADDED 5        /* k_added: added-token literal split */
+#define TK_KERNELS 6
 int tk_engine_set_timing(tk_engine* engine, int mode);
 int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
 
@@ -289,13 +299,17 @@ int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
  * splitmix64 open addressing) on every path. Returns TK_OK, or
  * TK_E_INVALID_ARG for an unknown option or value. */
 #define TK_OPT_COMPACT_PAIRS 1
-/* TK_OPT_REPAIR_WHOLE: pieces over 512 bytes are cut into segments and
+/* TK_OPT_REPAIR_WIDEN: pieces over 512 bytes are cut into segments and
  * every cut certified; a failed cut is dropped and its segments redone, one
- * repair pass after another. From this pass on (default 3; 1..64) a piece
- * that still has a failed cut drops every cut and is merged whole by a
- * workgroup, so the passes end. 0: every piece over 512 bytes is merged
- * whole from the start, with no cut (the path of tables that drop bytes). */
-#define TK_OPT_REPAIR_WHOLE 2
+ * repair pass after another. From this pass on (default 4; 1..64) each
+ * failed cut also drops its 4^(p - value + 1) nearest cuts on each side
+ * inside its piece, so a cascade of failures (each drop exposing the next,
+ * as in periodic runs) ends within a few passes. 0: every piece over 512
+ * bytes is merged whole by a workgroup, with no cut (the path of tables
+ * that drop bytes). */
+#define TK_OPT_REPAIR_WIDEN 2
+/* TK_OPT_TIMED_KERNEL: the TK_KERNEL_* timing mode 2 times. */
+#define TK_OPT_TIMED_KERNEL 3
 int tk_engine_set_option(tk_engine* engine, int option, int64_t value);
 
 /* Test-only fault injection (no counterpart in the reference; the hook its

@@ -313,11 +313,12 @@ def window_cuts(family, ids, lens, off):
     return sorted(cuts)
 
 
-def repair(family, data, off, whole_from=None, limit=10_000):
+def repair(family, data, off, widen_from=None, limit=10_000):
     """The certification and its repair passes on one piece: certify every
     cut, drop the failed ones, redo the segments, until none fails (cert 1,
-    a monotone table). From pass `whole_from` on, a piece that still has a
-    failed cut drops every cut (k_fail_pieces). Returns (ids, passes)."""
+    a monotone table). From pass `widen_from` on, each failed cut also
+    drops its 4^(p - widen_from + 1) nearest cuts on each side
+    (k_fail_widen). Returns (ids, passes)."""
     rules, unsafe, byte_id = _model(family)
     lens = _lengths(family)
     ids = [byte_id[b] for b in data]
@@ -326,41 +327,44 @@ def repair(family, data, off, whole_from=None, limit=10_000):
     while True:
         bounds = [0, *cuts, len(ids)]
         segs = [merge(rules, unsafe, ids[a:b], True) for a, b in zip(bounds, bounds[1:])]
-        failed = [c for k, c in enumerate(cuts)
+        failed = [k for k, c in enumerate(cuts)
                   if not walk_events(rules, ids[c - 1], ids[c], segs[k][1], segs[k + 1][1])]
         if not failed or passes >= limit:
             return [t for s in segs for t in s[0]], passes
         passes += 1
-        if whole_from is not None and passes >= whole_from:
-            cuts = []
-        else:
-            cuts = [c for c in cuts if c not in failed]
+        width = 4 ** (passes - widen_from + 1) if widen_from and passes >= widen_from else 0
+        drop = set()
+        for k in failed:
+            drop.update(range(max(0, k - width), min(len(cuts), k + width + 1)))
+        cuts = [c for k, c in enumerate(cuts) if k not in drop]
 
 
-def test_repair_passes_cascade_on_periodic_runs_and_escalation_ends_them():
+def test_repair_passes_cascade_on_periodic_runs_and_widening_ends_them():
     """A run of one letter led by a character that joins its piece ("!"
     + "QQQ...": one piece under the Qwen2 pattern) fixes the token parity
     at its first window, while every later window pairs the letters from
     an even text position. Removing the one cut that fails makes the next
-    one fail: one cut per pass, so the passes grow with the run. Merging a
-    piece that still fails whole from pass 3 on (the device's REPAIR_WHOLE)
-    ends them with the whole piece's ids."""
+    one fail: one cut per pass, so the passes grow with the run. Dropping a
+    fourfold wider ring of cuts around each failed one from pass 4 on (the
+    device's REPAIR_WIDEN) ends them within about log4 of the run's cuts,
+    with the whole piece's ids."""
     family = "qwen3_8b"
     rules, unsafe, byte_id = _model(family)
-    for n in (300, 600, 1200):
+    for n in (300, 600, 1200, 4000):
         data = b"!" + b"Q" * n
         whole, _ = merge(rules, unsafe, [byte_id[b] for b in data], True)
-        ids, passes = repair(family, data, off=64)
-        assert ids == whole
-        assert passes >= n // 2 - 40, (n, passes)  # one cut per pass
-        ids, passes = repair(family, data, off=64, whole_from=3)
-        assert ids == whole and passes <= 3, (n, passes)
+        if n <= 1200:
+            ids, passes = repair(family, data, off=64)
+            assert ids == whole
+            assert passes >= n // 2 - 40, (n, passes)  # one cut per pass
+        ids, passes = repair(family, data, off=64, widen_from=4)
+        assert ids == whole and passes <= 3 + 8, (n, passes)
 
 
-def test_escalated_repair_keeps_the_ids_of_ordinary_pieces():
+def test_widened_repair_keeps_the_ids_of_ordinary_pieces():
     """Letter runs of C5's text (monotone Qwen table) at shifting text
-    offsets: the escalated repair loop gives the whole piece's ids within
-    three passes."""
+    offsets: the widened repair loop gives the whole piece's ids, widened
+    from the first pass too."""
     family = "qwen3_8b"
     rules, unsafe, byte_id = _model(family)
     from toktier_amd import standin, workloads
@@ -377,5 +381,7 @@ def test_escalated_repair_keeps_the_ids_of_ordinary_pieces():
         while data and (data[-1] & 0xC0) == 0x80 or (data and data[-1] >= 0xC0):
             data = data[:-1]
         whole, _ = merge(rules, unsafe, [byte_id[b] for b in data], True)
-        ids, passes = repair(family, data, off=int(rng.integers(0, 64)), whole_from=3)
-        assert ids == whole and passes <= 3, passes
+        for widen in (1, 4):
+            ids, passes = repair(family, data, off=int(rng.integers(0, 64)),
+                                 widen_from=widen)
+            assert ids == whole, (widen, passes)

@@ -34,7 +34,11 @@ TK_FLAG_NORMALIZED = 1
 TK_FLAG_NO_ADDED = 2
 TK_NOALLOC_MAX_BYTES = 1 << 20
 TK_OPT_COMPACT_PAIRS = 1
-TK_OPT_REPAIR_WHOLE = 2
+TK_OPT_REPAIR_WIDEN = 2
+TK_OPT_TIMED_KERNEL = 3
+# TK_KERNEL_* in the header's order: the kernels the timing modes time
+KERNELS = ("k_pretok", "k_bpe_pack", "k_compact", "k_bpe_rows",
+           "k_long_windows", "k_added")
 # added-token flags (tokenizer.json "added_tokens" fields)
 TK_ADDED_SPECIAL = 1
 TK_ADDED_SINGLE_WORD = 2
@@ -322,9 +326,10 @@ class Engine:
     def set_option(self, option: int, value: int) -> None:
         """``TK_OPT_COMPACT_PAIRS``: 1 probe the compact pair table (the
         default when the artifact fits it), 0 the boundary-format table.
-        ``TK_OPT_REPAIR_WHOLE``: the first certification repair pass that
-        merges a still-failing piece over 512 bytes whole (default 3); 0
-        merges every such piece whole, with no cut."""
+        ``TK_OPT_REPAIR_WIDEN``: the first certification repair pass that
+        also drops cuts around each failed one (default 4); 0 merges every
+        piece over 512 bytes whole, with no cut. ``TK_OPT_TIMED_KERNEL``:
+        the kernel timing mode 2 times (an index into ``KERNELS``)."""
         check(self._L.tk_engine_set_option(self._h, int(option), int(value)),
               "tk_engine_set_option")
 
@@ -346,14 +351,16 @@ class Engine:
         return {n: int(buf[i]) for i, n in enumerate(names[:k])}
 
     def set_timing(self, mode: int) -> None:
-        """0 off, 1 (or True) every stage, 2 the packed merge kernel only."""
+        """0 off, 1 (or True) every stage and every kernel, 2 one kernel
+        only (``TK_OPT_TIMED_KERNEL``; default the packed merge)."""
         check(self._L.tk_engine_set_timing(self._h, int(mode)),
               "tk_engine_set_timing")
 
     def last_timing(self) -> list[float]:
-        """Device stage times [0..4] (timing modes 1 / 2) and the host wall
+        """Device stage times [0..4] (timing modes 1 / 2), the host wall
         times [5..7] of the last host-to-host encode (bytes in, pipeline,
-        ids out), microseconds."""
-        buf = (C.c_double * 8)()
-        k = self._L.tk_engine_last_timing(self._h, buf, 8)
+        ids out), and (mode 1) each kernel's own duration [8 + k] for k in
+        ``KERNELS``, microseconds."""
+        buf = (C.c_double * (8 + len(KERNELS)))()
+        k = self._L.tk_engine_last_timing(self._h, buf, len(buf))
         return list(buf[:k])

@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void k_added(DevAdded a, DevWork w,
 
 hipError_t launch_added(const DevAdded& a, const DevWork& w,
                         const uint64_t* host_dm, hipStream_t s,
-                        hipEvent_t start) {
+                        hipEvent_t start, hipEvent_t stop) {
   // the words k_pretok reads; the caller's mask holds nb / 64 + 2 of them
   const int64_t nwords = (w.nb + 63) / 64 + 2;
   uint64_t* dm = const_cast<uint64_t*>(w.docmask);
@@ -359,8 +359,8 @@ hipError_t launch_added(const DevAdded& a, const DevWork& w,
   const bool lds = a.tab_size <= (uint32_t)ADDED_TAB_LDS &&
                    a.n <= (uint32_t)ADDED_LEN_LDS;
   auto k = lds ? k_added<true> : k_added<false>;
-  if (start)
-    hipExtLaunchKernelGGL(k, dim3(g), dim3(256), 0, s, start, nullptr, 0,
+  if (start || stop)
+    hipExtLaunchKernelGGL(k, dim3(g), dim3(256), 0, s, start, stop, 0,
                           a, w, host_dm, dm, nwords);
   else
     hipLaunchKernelGGL(k, dim3(g), dim3(256), 0, s, a, w, host_dm, dm, nwords);

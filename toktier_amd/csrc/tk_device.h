@@ -302,11 +302,13 @@ hipError_t launch_pretok(const DevTables& t, const DevWork& w, hipStream_t s,
 hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t start, hipEvent_t stop);
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
-                           uint32_t nlong);
+                           uint32_t nlong, hipEvent_t start = nullptr,
+                           hipEvent_t stop = nullptr);
 hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
                            hipEvent_t stop, uint32_t nlong);
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
-                               hipStream_t s);
+                               hipStream_t s, hipEvent_t start = nullptr,
+                               hipEvent_t stop = nullptr);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
                                 int all, hipStream_t s);
 // pieces over WIDE_MAX bytes merged whole, a workgroup each (tables that
@@ -314,12 +316,17 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s);
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop = nullptr);
-// (whole: pieces with a failed cut drop every cut, k_fail_pieces, first;
-// nlong: the queued pieces over 64 bytes)
-hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, bool whole,
-                             uint32_t nlong);
-// the first repair pass that merges a still-failing piece whole
-constexpr int REPAIR_WHOLE = 3;
+// (width > 0: each failed cut also drops its `width` nearest cuts on each
+// side inside its piece, k_fail_widen, first)
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, uint32_t width);
+// the first repair pass that widens the failed cuts (TK_OPT_REPAIR_WIDEN),
+// and the width of pass p >= it: 4^(p - first + 1), capped
+constexpr int REPAIR_WIDEN = 4;
+__host__ __device__ constexpr uint32_t repair_width(int p, int first) {
+  return first <= 0 || p < first ? 0u
+         : (p - first + 1) >= 15 ? (1u << 30)
+                                 : (1u << (2 * (p - first + 1)));
+}
 hipError_t launch_compact(const DevWork& w, hipStream_t s, uint32_t tag,
                           hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // k_added: the literal split of the request into w.docmask (read-write;
@@ -332,7 +339,7 @@ hipError_t launch_seed(const DevWork& w, const uint8_t* text, int64_t nb,
                        uint64_t* pts, hipStream_t s);
 hipError_t launch_added(const DevAdded& a, const DevWork& w,
                         const uint64_t* host_dm, hipStream_t s,
-                        hipEvent_t start = nullptr);
+                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 hipError_t launch_doc_offsets(const DevWork& w, const uint64_t* doc_offsets,
                               uint32_t n_docs, uint64_t* row_offsets,
                               hipStream_t s);

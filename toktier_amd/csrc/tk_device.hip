@@ -3713,40 +3713,87 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
   }
 }
 
-// An escalated repair pass (REPAIR_WHOLE on): a piece over WIDE_MAX bytes
-// that still has a failed cut drops every cut and is merged whole, as one
-// segment (k_seg_block). Without it a pass can expose the next failing cut
-// each time: in a periodic run whose token parity its first window fixes
-// ("!" + "QQQ...": every later window pairs the letters from an even
-// offset), removing a failed cut makes the one after it fail, one cut per
-// pass, 35,000 passes for 70,000 letters. With it the passes end: a piece
-// with no cut has nothing to fail. One wave per long piece, ahead of
-// k_apply_fail (it marks the piece's words dirty for the pass).
-__global__ __launch_bounds__(256) void k_fail_pieces(DevWork w) {
-  if (!pass_live(w)) return;
-  const int lane = threadIdx.x & 63;
-  uint32_t n = *w.longcount;
-  if (n > w.long_cap) n = w.long_cap;
-  for (uint32_t k = blockIdx.x * 4 + wave_id(); k < n; k += gridDim.x * 4) {
-    const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
-    if (b <= a || b - a <= (uint32_t)WIDE_MAX) continue;  // wave-uniform
-    const int64_t w0 = a >> 6, w1 = ((int64_t)b - 1) >> 6;
-    // the piece's bytes [a, b) of word q
-    auto in_piece = [&](int64_t q) {
-      uint64_t m = ~0ULL;
-      if (q == w0) m &= ~((1ULL << (a & 63)) - 1);
-      if (q == w1) m &= mask_le((int)((b - 1) & 63));
-      return m;
+// A widened repair pass (from the pass TK_OPT_REPAIR_WIDEN names on): a
+// failed cut also drops the `width` nearest cuts on each side of it inside
+// its piece. Without it a pass can expose the next failing cut each time:
+// in a periodic run whose token parity its first window fixes ("!" +
+// "QQQ...": every later window pairs the letters from an even offset),
+// removing a failed cut makes the one after it fail, one cut per pass,
+// 35,000 passes for 70,000 letters. The width grows fourfold a pass, so a
+// cascade of L cuts ends in about log4(L) passes, while the isolated
+// failures of ordinary text (all fixed by the third pass on C5) never see
+// it. One thread per failed-cut word, ahead of k_apply_fail; the words
+// from the new segment's start to its end are marked dirty for the pass.
+// Clears by other threads only shorten what a thread sees, so it drops
+// more, never less, and the union of the marked ranges covers every joined
+// segment.
+__global__ void k_fail_widen(DevWork w, int64_t nwords, uint32_t width) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (v >= nwords || !pass_live(w)) return;
+  uint64_t f = w.failm[v];
+  while (f) {
+    const int bit = __builtin_ctzll(f);
+    f &= f - 1;
+    const int64_t c = v * 64 + bit;
+    auto drop = [&](int64_t wd, int b) {
+      atomicAnd(reinterpret_cast<unsigned long long*>(&w.cuts[wd]), ~(1ULL << b));
     };
-    uint64_t f = 0;
-    for (int64_t q = w0 + lane; q <= w1; q += 64) f |= w.failm[q] & in_piece(q);
-    if (!__ballot(f != 0)) continue;  // wave-uniform
-    for (int64_t q = w0 + lane; q <= w1; q += 64) {
-      // (a is a piece start: its cut bit does not matter)
-      atomicAnd(reinterpret_cast<unsigned long long*>(&w.cuts[q]), ~in_piece(q));
+    // down: clear `width` cuts, stop at the piece start or the next cut
+    int64_t lo = c;
+    {
+      uint32_t k = 0;
+      int64_t wd = v;
+      uint64_t m = bit ? (1ULL << bit) - 1 : 0;  // bits below c in its word
+      for (;;) {
+        const uint64_t st = w.starts[wd];
+        uint64_t sb = (st | (w.cuts[wd] & w.inlong[wd])) & m;
+        bool done = false;
+        while (sb) {
+          const int b = 63 - __builtin_clzll(sb);
+          sb &= ~(1ULL << b);
+          if (((st >> b) & 1) || k == width) {
+            lo = wd * 64 + b;
+            done = true;
+            break;
+          }
+          drop(wd, b);
+          ++k;
+        }
+        if (done || wd == 0) break;
+        --wd;
+        m = ~0ULL;
+      }
+    }
+    // up: the same towards the piece end (a start bit; sentinel start bits
+    // lie past the text)
+    int64_t hi = c;
+    {
+      uint32_t k = 0;
+      int64_t wd = v;
+      uint64_t m = ~mask_le(bit);  // bits above c in its word
+      for (;;) {
+        const uint64_t st = w.starts[wd];
+        uint64_t sb = (st | (w.cuts[wd] & w.inlong[wd])) & m;
+        bool done = false;
+        while (sb) {
+          const int b = __builtin_ctzll(sb);
+          sb &= sb - 1;
+          if (((st >> b) & 1) || k == width) {
+            hi = wd * 64 + b;
+            done = true;
+            break;
+          }
+          drop(wd, b);
+          ++k;
+        }
+        if (done) break;
+        ++wd;
+        m = ~0ULL;
+      }
+    }
+    for (int64_t q = lo >> 6; q <= (hi >> 6); ++q)
       atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
                1ULL << (q & 63));
-    }
   }
 }
 
@@ -3755,11 +3802,15 @@ __global__ __launch_bounds__(256) void k_fail_pieces(DevWork w) {
 // knows there are any (a wave per queued piece, up to 2048 blocks of four;
 // those of 65..128 bytes were merged by k_bpe_pack).
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
-                           uint32_t nlong) {
+                           uint32_t nlong, hipEvent_t start, hipEvent_t stop) {
   const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
   const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
                          ? (size_t)t.unsafe_words * 4 : 0;
-  hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, t, w);
+  if (start || stop)
+    hipExtLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, start, stop,
+                          0, t, w);
+  else
+    hipLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, t, w);
   return hipGetLastError();
 }
 
@@ -3773,10 +3824,10 @@ hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
 }
 
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
-                               hipStream_t s) {
+                               hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   const int64_t nwin = (w.nb + 63) / 64;
-  hipLaunchKernelGGL(k_long_windows, dim3((uint32_t)((nwin + 4) / 4)),
-                     dim3(256), 0, s, t, w, nwin);
+  launch_ev(k_long_windows, dim3((uint32_t)((nwin + 4) / 4)), dim3(256), s, start,
+            stop, t, w, nwin);
   return hipGetLastError();
 }
 
@@ -3812,13 +3863,11 @@ hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
   return hipGetLastError();
 }
 
-hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, bool whole,
-                             uint32_t nlong) {
-  if (whole) {
-    const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
-    hipLaunchKernelGGL(k_fail_pieces, dim3(blocks), dim3(256), 0, s, w);
-  }
+hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, uint32_t width) {
   const int64_t nwords = (w.nb + 63) / 64;
+  if (width)
+    hipLaunchKernelGGL(k_fail_widen, dim3((uint32_t)((nwords + 255) / 256)),
+                       dim3(256), 0, s, w, nwords, width);
   hipLaunchKernelGGL(k_apply_fail, dim3((uint32_t)((nwords + 255) / 256)),
                      dim3(256), 0, s, w, nwords);
   return hipGetLastError();

@@ -286,13 +286,16 @@ struct tk_engine {
   // bound of a device wait on another workgroup (DevWork::wait_ticks):
   // WAIT_MS in ticks of the device's real-time counter
   uint64_t wait_ticks = 0;
-  // TK_OPT_REPAIR_WHOLE: the first repair pass that merges a still-failing
-  // long piece whole; 0: every piece over WIDE_MAX bytes merged whole, no
+  // TK_OPT_REPAIR_WIDEN: the first repair pass that widens the failed cuts
+  // (k_fail_widen); 0: every piece over WIDE_MAX bytes merged whole, no
   // cuts (the path of tables that drop bytes)
-  int repair_whole = tk::REPAIR_WHOLE;
+  int repair_widen = tk::REPAIR_WIDEN;
   // timing
-  int timing = 0;  // 0 off, 1 every stage, 2 k_bpe_pack only
+  int timing = 0;  // 0 off, 1 every kernel, 2 one kernel (timed_kernel)
+  int timed_kernel = TK_KERNEL_BPE_PACK;
   hipEvent_t ev[8] = {};
+  hipEvent_t kev[TK_KERNELS][2] = {};  // mode 1: each kernel's own dispatch
+  double last_kus[TK_KERNELS] = {};
   // side stream for the long-piece stages, and its fork / join events
   hipStream_t stream2 = nullptr;
   hipEvent_t ev_join = nullptr;  // side stream -> engine stream
@@ -530,29 +533,36 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
                                   out, out_cap, literals);
   uint32_t* ctrl = ws.ctrl + ws.slot * tk::CTRL_WORDS;
   hipEvent_t* ev = e->ev;
-  // Timing mode 1, stage boundaries taken by the dispatches themselves:
-  // ev[0] start of k_added or k_pretok; ev[1] end of k_pretok (the pieces
-  // listed); ev[2] end of k_bpe_pack; ev[3] end of the
-  // long-piece stages on the side streams (when they have work); ev[4] end
-  // of the compaction. Mode 2: ev[1] / ev[2] are the start / end of
-  // k_bpe_pack's own dispatch only. (Each timed dispatch delays the next
-  // one by a few microseconds, so the events sit on as few dispatches as
-  // they can.)
-  const bool stages = e->timing == 1, packonly = e->timing == 2;
-  auto at = [&](int k) { return stages ? ev[k] : nullptr; };
+  // Timing mode 1: every kernel of TK_KERNEL_* takes a start / stop event
+  // pair on its own dispatch (kev), and ev[3] marks the end of the side
+  // streams' work (when they have any) on the engine stream; the stage
+  // boundaries are read from those. Mode 2: ev[1] / ev[2] are the start /
+  // end of the dispatch of the kernel TK_OPT_TIMED_KERNEL names only. (Each
+  // timed dispatch delays the next one by a few microseconds, so the timed
+  // loop of a benchmark uses mode 2.)
+  const bool stages = e->timing == 1, one = e->timing == 2;
+  auto ks = [&](int k) -> hipEvent_t {
+    return stages ? e->kev[k][0] : one && e->timed_kernel == k ? ev[1] : nullptr;
+  };
+  auto ke = [&](int k) -> hipEvent_t {
+    return stages ? e->kev[k][1] : one && e->timed_kernel == k ? ev[2] : nullptr;
+  };
+  bool launched[TK_KERNELS] = {};
   if (literals) {
-    HIP_TRY(tk::launch_added(*docs, w, host_dm, s, at(0)));
-    HIP_TRY(tk::launch_pretok(e->t, w, s, nullptr, at(1)));
-  } else {
-    HIP_TRY(tk::launch_pretok(e->t, w, s, at(0), at(1)));
+    HIP_TRY(tk::launch_added(*docs, w, host_dm, s, ks(TK_KERNEL_ADDED),
+                             ke(TK_KERNEL_ADDED)));
+    launched[TK_KERNEL_ADDED] = true;
   }
+  HIP_TRY(tk::launch_pretok(e->t, w, s, ks(TK_KERNEL_PRETOK), ke(TK_KERNEL_PRETOK)));
+  launched[TK_KERNEL_PRETOK] = true;
   hipStream_t s2 = e->stream2, s3 = e->stream3;
   ws.slot ^= 1;  // this call's k_pretok clears the other slot
   // (k_bpe_pack's first waves resolve the long pieces' ends and open the
   // gate before they take their work units; its first units are the long
   // pieces of up to 128 bytes)
-  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, packonly ? ev[1] : nullptr,
-                              stages || packonly ? ev[2] : nullptr));
+  HIP_TRY(tk::launch_bpe_pack(e->t, w, s, ks(TK_KERNEL_BPE_PACK),
+                              ke(TK_KERNEL_BPE_PACK)));
+  launched[TK_KERNEL_BPE_PACK] = true;
   // The gate words tell, while the packed merge runs, how many pieces are
   // over 64 bytes, how many of them have 129..256 bytes, 257..WIDE_MAX bytes
   // and more. Only then do the stages of those pieces go on the side streams,
@@ -565,8 +575,8 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   const uint32_t nrows = e->gate[tk::GATE_NROWS];
   const uint32_t nwide = e->gate[tk::GATE_NWIDE];
   // (cut / segment / certify, unless the pieces over WIDE_MAX bytes are
-  // merged whole: tables that drop bytes, or TK_OPT_REPAIR_WHOLE 0)
-  const bool cut = e->t.cert && e->repair_whole > 0;
+  // merged whole: tables that drop bytes, or TK_OPT_REPAIR_WIDEN 0)
+  const bool cut = e->t.cert && e->repair_widen > 0;
   const uint32_t big = cut ? e->gate[tk::GATE_BIG] : 0;
   e->last_nlong = nlong;
   e->last_big = e->gate[tk::GATE_BIG];
@@ -578,7 +588,11 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     // two independent jobs on two side streams: pieces of 129..WIDE_MAX
     // bytes merged whole, and the cut / segment / certify path of the
     // longer ones (they touch disjoint bytes and read the same lists)
-    if (rows) HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong));
+    if (rows) {
+      HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong, ks(TK_KERNEL_BPE_ROWS),
+                                  ke(TK_KERNEL_BPE_ROWS)));
+      launched[TK_KERNEL_BPE_ROWS] = true;
+    }
     if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
     // (a table that drops bytes merges its pieces over WIDE_MAX bytes
     // whole, a workgroup each, after the wide merges)
@@ -587,12 +601,14 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     if (big) {
       // cut / segment / certify, then the repair passes, all on their own
       // stream beside the packed merge and the wide merges
-      HIP_TRY(tk::launch_long_windows(e->t, w, s3));
+      HIP_TRY(tk::launch_long_windows(e->t, w, s3, ks(TK_KERNEL_LONG_WINDOWS),
+                                      ke(TK_KERNEL_LONG_WINDOWS)));
+      launched[TK_KERNEL_LONG_WINDOWS] = true;
       HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
-        HIP_TRY(tk::launch_apply_fail(wp, s3, p >= e->repair_whole, nlong));
+        HIP_TRY(tk::launch_apply_fail(wp, s3, tk::repair_width(p, e->repair_widen)));
         HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s3));
         HIP_TRY(tk::launch_certify(e->t, wp, 0, s3));
       }
@@ -610,7 +626,9 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   // the compaction reports the failed cuts left after the last queued pass
   tk::DevWork wc = w;
   if (big) wc.nfail = fail_count(ctrl, DEV_REPAIRS);
-  HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag, nullptr, at(4)));
+  HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag, ks(TK_KERNEL_COMPACT),
+                             ke(TK_KERNEL_COMPACT)));
+  launched[TK_KERNEL_COMPACT] = true;
   // k_compact's last block has left the outcome in the gate words: no
   // read-back copy
   HIP_TRY(hipStreamSynchronize(s));
@@ -626,32 +644,35 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   int rc = TK_OK;
   if (stages) {
     // [2]: how far the long-piece stages ran past the packed merge
-    const double t1 = elapsed_us(ev[0], ev[1]), t2 = elapsed_us(ev[0], ev[2]);
-    const double t3 = side ? elapsed_us(ev[0], ev[3]) : 0.0;
-    const double t4 = elapsed_us(ev[0], ev[4]);
+    hipEvent_t t0ev = e->kev[literals ? TK_KERNEL_ADDED : TK_KERNEL_PRETOK][0];
+    const double t1 = elapsed_us(t0ev, e->kev[TK_KERNEL_PRETOK][1]);
+    const double t2 = elapsed_us(t0ev, e->kev[TK_KERNEL_BPE_PACK][1]);
+    const double t3 = side ? elapsed_us(t0ev, ev[3]) : 0.0;
+    const double t4 = elapsed_us(t0ev, e->kev[TK_KERNEL_COMPACT][1]);
     e->last_us[0] = t1;
     e->last_us[1] = t2 - t1;
     e->last_us[2] = t3 > t2 ? t3 - t2 : 0.0;
     e->last_us[3] = t4 - (t3 > t2 ? t3 : t2);
     e->last_us[4] = t4;
-  } else if (packonly) {
+    for (int k = 0; k < TK_KERNELS; ++k)
+      e->last_kus[k] = launched[k] ? elapsed_us(e->kev[k][0], e->kev[k][1]) : 0.0;
+  } else if (one) {
     for (double& x : e->last_us) x = 0.0;
-    e->last_us[1] = elapsed_us(ev[1], ev[2]);
+    e->last_us[1] = launched[e->timed_kernel] ? elapsed_us(ev[1], ev[2]) : 0.0;
   }
   if (residual != 0) {
     // cuts still fail after the queued passes: more passes from the host,
-    // one at a time. Not expected: a queued pass from REPAIR_WHOLE on
-    // leaves no cut in a piece that failed, so the bound only guards
-    // against a defect.
+    // one at a time. From pass REPAIR_WIDEN on each failed cut also drops
+    // 4^(p - REPAIR_WIDEN + 1) cuts on each side, so a cascade of L cuts
+    // ends within about log4(L) passes; the bound (a width past 2^30 cuts)
+    // only guards against a defect.
     int p = DEV_REPAIRS;
     if (stages) HIP_TRY(hipEventRecord(ev[5], s));
     while (residual != 0) {
-      // (from pass REPAIR_WHOLE on, a piece that fails is merged whole and
-      // then has no cut left to fail: one such pass ends the repairs)
-      if (++p > std::max(DEV_REPAIRS, e->repair_whole) + 2)
+      if (++p > std::max(DEV_REPAIRS, e->repair_widen) + 16)
         return fail(TK_E_INTERNAL, "certification did not converge");
       const tk::DevWork wp = pass_work(w, ctrl, p);
-      HIP_TRY(tk::launch_apply_fail(wp, s, p >= e->repair_whole, nlong));
+      HIP_TRY(tk::launch_apply_fail(wp, s, tk::repair_width(p, e->repair_widen)));
       HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s));
       HIP_TRY(tk::launch_certify(e->t, wp, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
@@ -665,7 +686,8 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     if (stages) {
       e->last_us[2] += elapsed_us(ev[5], ev[6]);
       e->last_us[3] = elapsed_us(ev[6], ev[7]);
-      e->last_us[4] = elapsed_us(ev[0], ev[7]);
+      e->last_us[4] = elapsed_us(e->kev[literals ? TK_KERNEL_ADDED : TK_KERNEL_PRETOK][0],
+                                 ev[7]);
     }
     e->last_passes = h[tk::CTRL_PASS];
   }
@@ -941,6 +963,10 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
     // timing-only events: no system-scope fence between the stages
     if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
       return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
+  for (auto& pair : e->kev)
+    for (auto& ev : pair)
+      if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess)
+        return bail(fail(TK_E_DEVICE, "hipEventCreateWithFlags failed"));
   // the device's copy of the static scratch array (the allocation-free
   // entry's workspace), looked up once per device with the device current
   {
@@ -1069,6 +1095,11 @@ void tk_engine_close(tk_engine* e) {
     if (ev) (void)hipEventDestroy(ev);
   if (e->stream2) (void)hipStreamSynchronize(e->stream2);
   if (e->stream3) (void)hipStreamSynchronize(e->stream3);
+  for (auto& pair : e->kev)
+    for (auto& ev : pair)
+      if (ev) (void)hipEventDestroy(ev);
+  if (e->stream2) (void)hipStreamSynchronize(e->stream2);
+  if (e->stream3) (void)hipStreamSynchronize(e->stream3);
   if (e->ev_join) (void)hipEventDestroy(e->ev_join);
   if (e->ev_join3) (void)hipEventDestroy(e->ev_join3);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1092,6 +1123,7 @@ int tk_engine_last_timing(const tk_engine* e, double* us, int n) {
   if (!e || !us) return fail(TK_E_INVALID_ARG, "null argument");
   int k = 0;
   for (; k < n && k < 8; ++k) us[k] = e->last_us[k];
+  for (; k < n && k < 8 + TK_KERNELS; ++k) us[k] = e->last_kus[k - 8];
   return k;
 }
 
@@ -1230,10 +1262,16 @@ int tk_engine_set_option(tk_engine* e, int option, int64_t value) {
     e->t.ctab = value && e->ctab.p ? e->ctab.p : nullptr;
     return TK_OK;
   }
-  if (option == TK_OPT_REPAIR_WHOLE) {
+  if (option == TK_OPT_TIMED_KERNEL) {
+    if (value < 0 || value >= TK_KERNELS)
+      return fail(TK_E_INVALID_ARG, "TK_OPT_TIMED_KERNEL takes 0..%d", TK_KERNELS - 1);
+    e->timed_kernel = (int)value;
+    return TK_OK;
+  }
+  if (option == TK_OPT_REPAIR_WIDEN) {
     if (value < 0 || value > 64)
-      return fail(TK_E_INVALID_ARG, "TK_OPT_REPAIR_WHOLE takes 0..64");
-    e->repair_whole = (int)value;
+      return fail(TK_E_INVALID_ARG, "TK_OPT_REPAIR_WIDEN takes 0..64");
+    e->repair_widen = (int)value;
     return TK_OK;
   }
   return fail(TK_E_INVALID_ARG, "unknown option %d", option);
