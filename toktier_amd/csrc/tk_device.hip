@@ -3432,9 +3432,11 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
   if (n > cap) n = cap;
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
-  // These waves are few and latency-bound (one merge round after another)
-  // while k_bpe_pack fills the same SIMDs: they get issue priority.
-  if (blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
+  // With histories these are the segments of the certified long pieces,
+  // one merge round after another on the request's critical path (the
+  // cut / segment / certify chain ends last on C5): they get issue
+  // priority over the other side work.
+  if (hist && blockIdx.x * 4 + wv < n) __builtin_amdgcn_s_setprio(3);
   for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
     const uint32_t a = list[2 * k], b = list[2 * k + 1];
     const int len = (int)(b - a);
@@ -3462,8 +3464,8 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   }
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
-  // few, latency-bound waves beside k_bpe_pack on the same SIMDs
-  __builtin_amdgcn_s_setprio(3);
+  // (no issue priority: these pieces end well before the cut / segment /
+  // certify chain of the long pieces, whose kernels take it)
   // (pieces of 65..128 bytes too when k_bpe_pack left them: more than
   // PACK_ROWS_MAX queued)
   const int lo = n > (uint32_t)PACK_ROWS_MAX ? 64 : 128;
@@ -3492,6 +3494,9 @@ __global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
   const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v > nwin) return;
+  // the long pieces' chain (windows, segments, certification, repairs)
+  // sets the end of a request that has any: issue priority
+  __builtin_amdgcn_s_setprio(2);
   auto seg = [&](int64_t wd) { return w.starts[wd]; };
   uint16_t* cut16 = reinterpret_cast<uint16_t*>(w.cuts);
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
@@ -3538,6 +3543,7 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
   const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v > nwin || !pass_live(w)) return;
+  __builtin_amdgcn_s_setprio(2);  // (the long pieces' chain: k_long_windows)
   auto seg = [&](int64_t wd) { return seg_word(w, wd); };
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
     if (!all && !word_dirty(w.dirty_cur, v) &&
@@ -3801,9 +3807,15 @@ __global__ void k_fail_widen(DevWork w, int64_t nwords, uint32_t width) {
 // (k_bpe_wide, state in LDS) are merged whole, one wave each, once the host
 // knows there are any (a wave per queued piece, up to 2048 blocks of four;
 // those of 65..128 bytes were merged by k_bpe_pack).
+// Its waves loop over the queue, so the grid is capped at half the
+// machine's wave slots: with all of them (2048 blocks) the loop held every
+// slot while the long pieces' window kernel ran, and that kernel, on C5's
+// critical path, starved (846 us; 277 us with a quarter of the slots, but
+// the row merge then took 2 ms).
+constexpr uint32_t ROWS_MAX_BLOCKS = 1024;
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
                            uint32_t nlong, hipEvent_t start, hipEvent_t stop) {
-  const uint32_t blocks = nlong / 4 + 1 < 2048 ? nlong / 4 + 1 : 2048;
+  const uint32_t blocks = nlong / 4 + 1 < ROWS_MAX_BLOCKS ? nlong / 4 + 1 : ROWS_MAX_BLOCKS;
   const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
                          ? (size_t)t.unsafe_words * 4 : 0;
   if (start || stop)

@@ -449,7 +449,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
 // any cut (its count: the other of two alternating control words). Up to
 // DEV_REPAIRS repair passes are queued on the long-piece stream without
 // the host; the host continues only if cuts still fail after them.
-constexpr int DEV_REPAIRS = 6;
+constexpr int DEV_REPAIRS = 3;
 uint32_t* fail_count(uint32_t* ctrl, int p) {
   return ctrl + ((p & 1) ? tk::CTRL_FAIL2 : tk::CTRL_FAIL);
 }
@@ -585,25 +585,23 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   const bool side2 = rows || nwide > 0 ||
                      (!cut && e->gate[tk::GATE_BIG] > 0);
   {
-    // two independent jobs on two side streams: pieces of 129..WIDE_MAX
-    // bytes merged whole, and the cut / segment / certify path of the
-    // longer ones (they touch disjoint bytes and read the same lists)
-    if (rows) {
-      HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong, ks(TK_KERNEL_BPE_ROWS),
-                                  ke(TK_KERNEL_BPE_ROWS)));
-      launched[TK_KERNEL_BPE_ROWS] = true;
-    }
-    if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
-    // (a table that drops bytes merges its pieces over WIDE_MAX bytes
-    // whole, a workgroup each, after the wide merges)
-    if (!cut && e->gate[tk::GATE_BIG] > 0)
-      HIP_TRY(tk::launch_long_block(e->t, w, s2));
+    // two independent jobs on two side streams: the cut / segment / certify
+    // path of the pieces over WIDE_MAX bytes (the request's critical path
+    // when there are any), and the pieces of 129..WIDE_MAX bytes merged
+    // whole (they touch disjoint bytes and read the same lists)
     if (big) {
       // cut / segment / certify, then the repair passes, all on their own
       // stream beside the packed merge and the wide merges
       HIP_TRY(tk::launch_long_windows(e->t, w, s3, ks(TK_KERNEL_LONG_WINDOWS),
                                       ke(TK_KERNEL_LONG_WINDOWS)));
       launched[TK_KERNEL_LONG_WINDOWS] = true;
+      // the row merges next (their launch is not held behind the chain's
+      // twenty-odd launches on the host)
+      if (rows) {
+        HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong, ks(TK_KERNEL_BPE_ROWS),
+                                    ke(TK_KERNEL_BPE_ROWS)));
+        launched[TK_KERNEL_BPE_ROWS] = true;
+      }
       HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
@@ -615,6 +613,17 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       HIP_TRY(hipEventRecord(e->ev_join3, s3));
       HIP_TRY(hipStreamWaitEvent(s, e->ev_join3, 0));
     }
+    // (after the chain's first kernel, so that one is dispatched first)
+    if (rows && !big) {
+      HIP_TRY(tk::launch_bpe_rows(e->t, w, s2, nlong, ks(TK_KERNEL_BPE_ROWS),
+                                  ke(TK_KERNEL_BPE_ROWS)));
+      launched[TK_KERNEL_BPE_ROWS] = true;
+    }
+    if (nwide > 0) HIP_TRY(tk::launch_bpe_wide(e->t, w, s2, nullptr, nlong));
+    // (a table that drops bytes merges its pieces over WIDE_MAX bytes
+    // whole, a workgroup each, after the wide merges)
+    if (!cut && e->gate[tk::GATE_BIG] > 0)
+      HIP_TRY(tk::launch_long_block(e->t, w, s2));
   }
   if (side2) {
     HIP_TRY(hipEventRecord(e->ev_join, s2));
