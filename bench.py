@@ -173,9 +173,11 @@ def n_chars_of(req) -> int:
 def make_oracle(tok):
     from oracle.oracle import Oracle
     from toktier_amd import classes
+    from toktier_amd import families
     f = tok.family
-    orc = Oracle(tok.tables, classes.table_for(f.ruleset_name),
-                 classes.nfc_qc_table(), f.ruleset, f.digits_max, f.needs_nfc)
+    orc = Oracle(tok.tables, classes.table_named(families.class_table_name(f)),
+                 classes.nfc_qc_table(), f.ruleset, f.digits_max, f.needs_nfc,
+                 contractions=f.contractions)
     orc.set_added([t.content.encode() for t in tok.added_tokens],
                   [t.id for t in tok.added_tokens])
     return orc

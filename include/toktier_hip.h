@@ -183,9 +183,11 @@ int tk_engine_encode_device(tk_engine* engine, const void* d_text,
                             size_t ids_cap, size_t* n_ids, void* stream);
 
 /* Allocation-free form of tk_engine_encode_device. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). It calls no hipMalloc / hipFree and no allocating library
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). Like every entry here it
+ * waits for *n_ids, so it cannot be recorded into a HIP graph: on a stream
+ * under capture it returns TK_E_INVALID_ARG and runs nothing. It calls no
+ * hipMalloc / hipFree and no allocating library
  * routine: the per-request workspace is carved from a static device array
  * (one copy per device, about 96 MiB, held until the process ends) instead
  * of the engine's own workspace; the tables are the ones tk_engine_open

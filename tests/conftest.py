@@ -15,7 +15,8 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 FAMILY_NAMES = ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
-                "deepseek_v3", "gpt_oss_120b", "kimi_k3")
+                "deepseek_v3", "gpt_oss_120b", "kimi_k3", "qwen3_5_08b",
+                "nemotron_3_nano_4b")
 
 
 def pytest_configure(config):
@@ -165,9 +166,11 @@ class FamilyKit:
         self.family = families.family(name)
         self.json = standin.load_artifact_json(name)
         self.tables = bpe_tables.load_tables(self.json)
-        self.oracle = Oracle(self.tables, classes.table_for(self.family.ruleset_name),
+        self.oracle = Oracle(self.tables,
+                             classes.table_named(families.class_table_name(self.family)),
                              classes.nfc_qc_table(), self.family.ruleset,
-                             self.family.digits_max, self.family.needs_nfc)
+                             self.family.digits_max, self.family.needs_nfc,
+                             contractions=self.family.contractions)
         # the artifact's added-token literals, split out as HF does
         import toktier_amd
         self.added = toktier_amd.added_tokens(self.json)

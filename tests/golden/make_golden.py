@@ -58,7 +58,7 @@ def literal_cases(name: str) -> list[str]:
         "".join(lits[:12]), " ".join(lits[-6:]),
         a + "\u0338 e\u0301 done", "café" + b + "\u0301",
     ]
-    if name == "qwen3_8b":
+    if name in ("qwen3_8b", "qwen3_5_08b"):
         texts += [
             "<|im_start|>system\nYou are helpful.<|im_end|>\n"
             "<|im_start|>user\nWhat's 2+2?<|im_end|>\n"
@@ -109,6 +109,12 @@ def literal_cases(name: str) -> list[str]:
             "<|start|>assistant<|channel|>commentary to=functions.f "
             "<|constrain|>json<|message|>{}<|call|>",
             "<|reserved_200013|>x<|endoftext|>", "<|start|", "|start|>",
+        ]
+    elif name == "nemotron_3_nano_4b":
+        texts += [
+            "<s><|im_start|>system\nBe brief.<|im_end|>\n<|im_start|>user\n"
+            "What's 2+2?<|im_end|>\n<|im_start|>assistant\n<think>\nok</think>4"
+            "<|im_end|></s>", "<unk>x<SPECIAL_10>", "<|im_start", "im_end|>",
         ]
     else:
         texts += ["doc one.<|endoftext|>doc two<|endoftext|><|endoftext|>",
@@ -165,10 +171,32 @@ KIMI_CASES = [
 ]
 
 
+#: strings where the Qwen3.5 split (combining marks inside the letter
+#: run, [\p{L}\p{M}]+) differs from Qwen3's: Devanagari and Thai syllables
+#: with vowel signs and viramas, stacked accents after letters, marks after
+#: punctuation, digits and spaces, marks before the contraction suffix
+QWEN35_CASES = [
+    "नमस्ते दुनिया", "हिन्दी", "क्षत्रिय", "ภาษาไทย", "สวัสดี", "น้ำ",
+    "e\u0301\u0301x", "q\u0323\u0331z", "!\u0301!", "1\u0301", " \u0301a",
+    "a \u0301!", "\u0301x", "x\u0301's", "ñ'S", "café\u0301'll",
+    "abc\u0301def ghi", "中\u0301文", "\u0e31\u0e31ก", "क\u094d\u094d",
+]
+
+#: strings where the Nemotron-3 split (o200k without the contraction
+#: suffix, single digits) differs from gpt-oss's: contractions in either
+#: case, digit runs, letters with marks before an apostrophe
+NEMOTRON_CASES = [
+    "it's", "don't", "I'M HERE'LL", "they'RE we'VE", "x'S", "'s", "a's'd",
+    "1234567", "12 345", "a1234b", "3.14159", "½²³⁴", "٣٤٥٦", "x=12345678;",
+    "HelloWorld's", "ÀÉÎ'll", "e\u0301's", "中文's", "OK'd 99's",
+]
+
+
 def main() -> None:
     out = {"tokenizers_version": tk_version, "families": {}}
     for name in ("qwen3_8b", "llama_3_1_8b", "gpt2", "laguna_s_2_1",
-                 "deepseek_v3", "gpt_oss_120b", "kimi_k3"):
+                 "deepseek_v3", "gpt_oss_120b", "kimi_k3", "qwen3_5_08b",
+                 "nemotron_3_nano_4b"):
         js = standin.load_artifact_json(name)
         tok = Tokenizer.from_str(js)
         rng = np.random.default_rng(99)
@@ -182,8 +210,12 @@ def main() -> None:
         texts += literal_cases(name)
         if name == "deepseek_v3":
             texts += DEEPSEEK_CASES
-        if name == "gpt_oss_120b":
+        if name in ("gpt_oss_120b", "nemotron_3_nano_4b"):
             texts += O200K_CASES
+        if name == "nemotron_3_nano_4b":
+            texts += NEMOTRON_CASES
+        if name == "qwen3_5_08b":
+            texts += QWEN35_CASES
         if name == "kimi_k3":
             texts += KIMI_CASES
         cases = [{"text": t, "ids": tok.encode(t, add_special_tokens=False).ids}

@@ -123,3 +123,39 @@ def test_null_arguments_are_refused():
     assert L.tk_engine_encode(None, b"abc", 3, 0, None, 0, C.byref(n)) == _ffi.TK_E_INVALID_ARG
     assert L.tk_engine_set_timing(None, 1) == _ffi.TK_E_INVALID_ARG
     assert L.tk_engine_delivery(None) == b""
+
+
+CRATE = HEADER.parent.parent / "crates" / "toktier-hip-driver" / "src" / "lib.rs"
+
+
+def _header_defines() -> dict[str, int]:
+    out = {}
+    for name, val in re.findall(r"#define\s+(TK_[A-Z0-9_]+)\s+\(?(-?\d+)u?\)?",
+                                HEADER.read_text()):
+        out[name] = int(val)
+    return out
+
+
+def test_rust_crate_binds_every_symbol_with_the_headers_constants():
+    """The source crate `toktier-hip-driver` (no Rust toolchain here, so it
+    is checked as text): it loads every entry point the header declares,
+    and each constant it repeats has the header's value, the ruleset codes
+    included. Its ruleset strings are the reference's (gpu.rs:40-62)."""
+    src = CRATE.read_text()
+    loaded = set(re.findall(r'symbol\(handle, "(tk_[a-z_]+)"\)', src))
+    assert loaded == declared_symbols()
+    consts = {n: int(v.replace("_", "")) for n, v in re.findall(
+        r"pub const (TK_[A-Z0-9_]+): \w+ = (-?[\d_]+);", src)}
+    defines = _header_defines()
+    assert consts, "no constants found"
+    for name, val in consts.items():
+        assert name in defines, name
+        assert defines[name] == val, name
+    for name in defines:
+        if name.startswith(("TK_RULESET_", "TK_E_", "TK_OPT_", "TK_KERNEL")):
+            assert name in consts, name
+    arms = dict(re.findall(r'"([a-z0-9]+)" => Ok\(Self::(\w+)\)', src))
+    assert set(arms) == {"cl100k", "r50k", "laguna", "deepseek", "o200k", "kimi"}
+    codes = dict(re.findall(r"Self::(\w+) => (TK_RULESET_[A-Z0-9]+),", src))
+    for s, variant in arms.items():
+        assert codes[variant] == "TK_RULESET_" + s.upper()

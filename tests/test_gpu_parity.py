@@ -74,13 +74,26 @@ def test_long_mixed_text(name):
           "kimi_k3": lambda js, n_chars: workloads.config5(
               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
           "deepseek_v3": lambda js, n_chars: workloads.config5(
-              js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
+              js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+          "nemotron_3_nano_4b": lambda js, n_chars: workloads.config5(
+              js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+          "qwen3_5_08b": _qwen35_mixed}[name]
     text = fn(k.json, n_chars=300_000)
     got = t.encode(text).array
-    want = k.oracle.encode_bytes(text.encode())
+    want = k.expected(text)
     assert not isinstance(want, int)
     assert np.array_equal(got, want)
     assert list(got[:2000]) == k.hf_ids(text[:0] + text)[:2000]
+
+
+def _qwen35_mixed(js: str, n_chars: int) -> str:
+    """Mixed text and lines dense in combining marks (Devanagari, Thai,
+    stacked accents), NFC-normal."""
+    import unicodedata
+    from toktier_amd import standin, workloads
+    marks = "\n".join(standin._mark_corpus(5, 2000))
+    return unicodedata.normalize(
+        "NFC", workloads.config2(js, n_chars=n_chars) + "\n" + marks)
 
 
 def test_batch_rows_equal_single():
@@ -556,21 +569,24 @@ def _o200k_long_runs(rng):
     return out
 
 
-@pytest.mark.family("gpt_oss_120b")
-def test_o200k_branches_match_hf():
-    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+O200K_ROWS = ["gpt_oss_120b", "nemotron_3_nano_4b"]
+
+
+@pytest.mark.parametrize("name", O200K_ROWS)
+def test_o200k_branches_match_hf(name):
+    k, t = kit(name), tok(name)
     for s in O200K_BRANCHES:
         for pre in ("", "z", " ", "中", "x" * 62):
             u = pre + s
             assert list(t.encode(u).array) == k.hf_ids(u), repr(u)
 
 
-@pytest.mark.family("gpt_oss_120b")
-def test_o200k_long_runs_match_oracle():
+@pytest.mark.parametrize("name", O200K_ROWS)
+def test_o200k_long_runs_match_oracle(name):
     """The automaton's state carried across words, the waves' blocks and
     tiles (a tile whose halo word does not fix its entry state composes
     its function and looks back over the tiles before it)."""
-    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    k, t = kit(name), tok(name)
     rng = np.random.default_rng(41)
     texts = _o200k_long_runs(rng)
     for s in texts:
@@ -581,11 +597,11 @@ def test_o200k_long_runs_match_oracle():
         assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
 
 
-@pytest.mark.family("gpt_oss_120b")
-def test_o200k_documents_cut_inside_runs():
+@pytest.mark.parametrize("name", O200K_ROWS)
+def test_o200k_documents_cut_inside_runs(name):
     """Batch rows cut anywhere in long runs: a document start resets the
     state, and each row equals the oracle's encode of that document."""
-    k, t = kit("gpt_oss_120b"), tok("gpt_oss_120b")
+    k, t = kit(name), tok(name)
     rng = np.random.default_rng(43)
     run = "".join(chr(int(c)) for c in rng.integers(0x4E00, 0x9FA5, 9000))
     base = ("a" + run + "ABC d " + "!!" + "\u0301!" * 3000 + "\n" +
@@ -618,6 +634,62 @@ def test_o200k_long_cjk_request_is_linear():
     dt = time.perf_counter() - t0
     assert np.array_equal(got, k.oracle.encode_bytes(s.encode()))
     assert dt < 0.5, dt
+
+
+def test_qwen35_marks_continue_letter_runs():
+    """The m2l class table (Qwen3.5: combining marks continue a letter run,
+    [\\p{L}\\p{M}]+): syllables with vowel signs and viramas, and stacked
+    accents, in runs that cross the 64-byte word and the pretokenizer's
+    tile and make pieces over 512 bytes (cut and certified), after letters,
+    digits, punctuation and spaces; against the oracle, and a selection
+    against HF."""
+    name = "qwen3_5_08b"
+    k, t = kit(name), tok(name)
+    texts = []
+    for unit in ("\u0915\u094d\u0937", "\u0928\u094d", "\u093f",
+                 "\u0e19\u0e49\u0e33", "q\u0301\u0331"):
+        for n in (1, 21, 22, 64, 65, TILE // 3, TILE // 3 + 1, 200, 700):
+            for lead in ("", " ", "a", "1", "!", "x" * 61):
+                texts.append(lead + unit * n + " z")
+    rng = np.random.default_rng(53)
+    from toktier_amd import standin
+    lines = standin._mark_corpus(7, 600)
+    for _ in range(10):
+        a = int(rng.integers(0, len(lines) - 60))
+        texts.append("".join(lines[a:a + 60]))  # runs joined without spaces
+    for s in texts:
+        got = t.encode(s).array
+        want = k.expected(s)
+        assert not isinstance(want, int), (len(s), s[:20])
+        assert np.array_equal(got, want), (len(s), s[:20])
+    for s in texts[::7]:
+        assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
+
+
+def test_nemotron_single_digits_and_no_contractions():
+    """The o200k row without the contraction suffix and with single digits
+    (Nemotron-3): digit runs at the word and tile edges (each digit a piece
+    of its own), apostrophes after letters of either case (the letter run
+    ends before the apostrophe); against the oracle, and a selection
+    against HF."""
+    name = "nemotron_3_nano_4b"
+    k, t = kit(name), tok(name)
+    texts = []
+    for n in (1, 2, 3, 4, 63, 64, 65, TILE - 1, TILE, TILE + 1, 5000):
+        for lead in ("", "a", " ", "x" * 61, "\u4e2d"):
+            texts.append(lead + "7" * n + "x")
+            texts.append(lead + "12" * n + "'s")
+            texts.append(lead + "\u0663" * n + " ")
+    for w in ("it's", "DON'T", "they'RE", "Mc'Donald", "'s'd"):
+        texts.append((w + " ") * 400)
+        texts.append(w * 300)
+    for s in texts:
+        got = t.encode(s).array
+        want = k.oracle.encode_bytes(s.encode())
+        assert not isinstance(want, int)
+        assert np.array_equal(got, want), (len(s), s[:20])
+    for s in texts[::5]:
+        assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
 
 
 # kimi: Han runs of every subclass, Han numbers inside and at the start of

@@ -340,6 +340,67 @@ def test_o200k_without_contractions_brute_force():
 
 # ------------------------------------------------------------ encodes
 
+#: the Qwen3.5 split's cases: letters (ASCII, Latin-1, Devanagari, Thai),
+#: marks of three kinds (a combining accent, a Devanagari vowel sign and
+#: virama, a Thai vowel mark), the contraction letters, digits,
+#: punctuation, whitespace of four kinds
+Q35_ALPHABET = ["a", "'", "s", "\u0301", "\u093f", "\u094d", "\u0e31", "क",
+                "ก", "é", "1", " ", "\n", "!", "\t", "中"]
+
+
+def _qwen35_oracle(table):
+    from oracle.oracle import Oracle
+    from toktier_amd import classes, families
+    return Oracle(kit("qwen3_8b").tables, table, classes.nfc_qc_table(),
+                  families.RULESET_CL100K, 1, False)
+
+
+def test_m2l_class_table_matches_reference_digest():
+    """The marks-as-letters table (cl100k_m2l_v3) probed here equals the
+    reference's pin; it differs from the base table exactly at the Mark
+    code points, all moved from P to L."""
+    from toktier_amd import classes, tables_gen
+    m2l, base = classes.m2l_class_table(), classes.class_table()
+    assert classes.npy_sha256(m2l) == classes.M2L_TABLE_SHA256
+    marks = tables_gen._probe_membership(r"\p{M}")
+    assert ((m2l != base) == marks).all()
+    assert (base[marks] == tables_gen.P).all() and (m2l[marks] == tables_gen.L).all()
+
+
+def test_qwen35_split_brute_force():
+    """The cl100k restatement over the marks-as-letters table splits like
+    the certified engine's Split with the Qwen3.5 pattern: every string of
+    length <= 3 over the alphabet, every length-5 string over a core, 3,000
+    fuzz strings; over the plain table (the planted mistake) some split
+    differently."""
+    from tokenizers import Regex, pre_tokenizers
+    from toktier_amd import classes, families
+    split = pre_tokenizers.Split(Regex(families.QWEN35_PATTERN), behavior="isolated")
+
+    def hf(text):
+        offs = [o for _, o in split.pre_tokenize_str(text)]
+        return (sorted({len(text[:a].encode("utf-8")) for a, _ in offs})
+                + [len(text.encode("utf-8"))])
+    o = _qwen35_oracle(classes.m2l_class_table())
+    plain = _qwen35_oracle(classes.class_table())
+    core = ["a", "\u0301", "\u093f", "!", " ", "'", "s", "1"]
+    rng = np.random.default_rng(35)
+    cases = itertools.chain(
+        ("".join(p) for n in range(1, 4) for p in itertools.product(Q35_ALPHABET, repeat=n)),
+        ("".join(p) for p in itertools.product(core, repeat=5)),
+        ("".join(Q35_ALPHABET[int(i)] for i in rng.integers(0, len(Q35_ALPHABET),
+                                                            int(rng.integers(1, 40))))
+         for _ in range(3000)))
+    bad, planted = [], 0
+    for s in cases:
+        want = hf(s)
+        if o.pretokenize(s.encode("utf-8")) != want:
+            bad.append(s)
+        planted += plain.pretokenize(s.encode("utf-8")) != want
+    assert not bad, bad[:10]
+    assert planted > 0
+
+
 def _expected(k, text: str, ids: list[int]):
     """Oracle result for text; an NFC family's failing quick check is
     answered segment by segment with the engine-normalized text, as the
@@ -371,9 +432,24 @@ def test_oracle_matches_hf_on_mixed_text(name):
            "kimi_k3": lambda js, n_chars: workloads.config5(
                js, n_chars=n_chars, n_runs=4, run_chars=20_000),
            "deepseek_v3": lambda js, n_chars: workloads.config5(
-               js, n_chars=n_chars, n_runs=4, run_chars=20_000)}[name]
+               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+           "nemotron_3_nano_4b": lambda js, n_chars: workloads.config5(
+               js, n_chars=n_chars, n_runs=4, run_chars=20_000),
+           "qwen3_5_08b": _qwen35_mixed}[name]
     text = gen(k.json, n_chars=200_000)
-    assert k.oracle.encode_bytes(text.encode()).tolist() == k.hf_ids(text)
+    got = k.expected(text)
+    assert not isinstance(got, int), got
+    assert got.tolist() == k.hf_ids(text)
+
+
+def _qwen35_mixed(js: str, n_chars: int) -> str:
+    """Mixed text and lines dense in combining marks (Devanagari, Thai,
+    stacked accents), NFC-normal as the engine receives it."""
+    import unicodedata
+    from toktier_amd import standin, workloads
+    marks = "\n".join(standin._mark_corpus(5, 400))
+    return unicodedata.normalize(
+        "NFC", workloads.config2(js, n_chars=n_chars) + "\n" + marks)
 
 
 def test_oracle_matches_hf_on_cjk_and_long_runs():

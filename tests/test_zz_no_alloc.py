@@ -98,3 +98,34 @@ def test_noalloc_shared_by_two_engines_and_limits():
     finally:
         a.close()
         b.close()
+
+
+def test_noalloc_refuses_a_capturing_stream():
+    """The entry waits for the id count, which a stream under HIP graph
+    capture cannot do: it returns TK_E_INVALID_ARG and records nothing (the
+    capture ends with an empty graph), and the engine works after it."""
+    import torch
+    import toktier_amd
+    from toktier_amd._ffi import EngineError, TK_E_INVALID_ARG
+    k = kit("qwen3_8b")
+    tok = toktier_amd.load("qwen3_8b")
+    try:
+        data = _text(k.json, 20_000, 11, False)
+        d, ids = _dev(data)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        err = None
+        with torch.cuda.graph(g, stream=s, capture_error_mode="relaxed"):
+            try:
+                tok.engine.encode_device_noalloc(d.data_ptr(), len(data),
+                                                 ids.data_ptr(), ids.numel(),
+                                                 stream=s.cuda_stream)
+            except EngineError as x:
+                err = x
+        assert err is not None and err.status == TK_E_INVALID_ARG
+        assert "captur" in err.detail
+        got = _run(tok.engine, data, True)
+        assert np.array_equal(got, k.expected(data.decode("utf-8")))
+    finally:
+        tok.close()

@@ -221,7 +221,8 @@ class Tokenizer:
         cfg = TkConfig(
             abi_version=TK_ABI_VERSION, device_ordinal=device,
             ruleset=fam.ruleset, digits_max=fam.digits_max,
-            contractions=int(fam.ruleset != families.RULESET_DEEPSEEK),
+            contractions=int(fam.ruleset != families.RULESET_DEEPSEEK
+                             and fam.contractions),
             needs_nfc=int(fam.needs_nfc),
             ignore_merges=int(self.tables.ignore_merges),
             pair_count=self.tables.pair_count,
@@ -230,7 +231,7 @@ class Tokenizer:
             expected_architecture=(expected_architecture.encode()
                                    if expected_architecture else None))
         nfc = classes.nfc_qc_table() if fam.needs_nfc else None
-        self.engine = Engine(cfg, classes.table_for(fam.ruleset_name),
+        self.engine = Engine(cfg, classes.table_named(families.class_table_name(fam)),
                              self.tables, nfc)
         self._lock = threading.Lock()
         self._counters = _Counters()

@@ -729,14 +729,25 @@ uint8_t* pinned_dev(const void* p) {
          (static_cast<const uint8_t*>(p) - static_cast<const uint8_t*>(a.hostPointer));
 }
 
-// the device's address of [p, p + bytes) when the whole range is
-// page-locked and mapped in one piece, else nullptr
+// the device's address of [p, p + bytes) when the whole range lies in one
+// page-locked allocation, else nullptr. Both ends mapping at the right
+// distance is not enough (two adjacent allocations can): the allocation
+// that holds the first byte must also hold the last one. A failed range
+// query takes the staged path.
 uint8_t* pinned_range(const void* p, size_t bytes) {
   if (bytes == 0) return nullptr;
   uint8_t* d0 = pinned_dev(p);
   if (!d0) return nullptr;
   uint8_t* d1 = pinned_dev(static_cast<const uint8_t*>(p) + bytes - 1);
-  return d1 && (size_t)(d1 - d0) == bytes - 1 ? d0 : nullptr;
+  if (!d1 || (size_t)(d1 - d0) != bytes - 1) return nullptr;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, d0) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  const uint8_t* b = static_cast<const uint8_t*>(base);
+  return d0 >= b && (size_t)(d0 - b) + bytes <= size ? d0 : nullptr;
 }
 
 // n bytes between host buffers by the copy threads and this thread
@@ -1386,6 +1397,14 @@ int tk_engine_encode_device_noalloc(tk_engine* e, const void* d_text,
   std::lock_guard<std::mutex> sk(scratch_lock(e->device));
   HIP_TRY(hipSetDevice(e->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
+  // the entry waits for *n_ids (and reads host-mapped words mid-run), which
+  // a stream under capture cannot do
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(TK_E_INVALID_ARG,
+                "the stream is being captured: the entry synchronizes and "
+                "cannot be recorded into a graph");
   // the workspace over the device's scratch array; the array keeps the last
   // call's contents, so the words that must start clear (the control slots
   // and the compaction status words) are cleared by a kernel first

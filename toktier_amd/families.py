@@ -29,9 +29,11 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-__all__ = ["Family", "FAMILIES", "family", "RULESET_CL100K", "RULESET_R50K",
+__all__ = ["Family", "FAMILIES", "family", "class_table_name",
+           "RULESET_CL100K", "RULESET_R50K",
            "RULESET_LAGUNA", "RULESET_DEEPSEEK", "RULESET_O200K",
-           "RULESET_KIMI", "DEEPSEEK_STAGES", "O200K_PATTERN", "KIMI_PATTERN"]
+           "RULESET_KIMI", "DEEPSEEK_STAGES", "O200K_PATTERN", "KIMI_PATTERN",
+           "QWEN35_PATTERN", "NEMOTRON_PATTERN"]
 
 #: Device ruleset ids (the ``ruleset`` field of the engine config).
 RULESET_CL100K = 0
@@ -105,6 +107,25 @@ O200K_PATTERN = (
     r"|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n/]*|\s*[\r\n]+|\s+(?!\S)|\s+"
 )
 
+#: Qwen3.5 (``options.rs`` Qwen35 row): the Qwen2 pattern with marks in
+#: the letter run and out of the punctuation run; the cl100k ruleset over
+#: the marks-as-letters class table (``kernel_families.v1.json`` family
+#: ``qwen3_5_08b``: class table cl100k_m2l_v3, digits_max 1).
+QWEN35_PATTERN = (
+    r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?[\p{L}\p{M}]+|\p{N}"
+    r"| ?[^\s\p{L}\p{M}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+)
+
+#: Nemotron-3 (``options.rs`` Nemotron row; ``pretokenize/fast/nemotron.rs``):
+#: o200k without the contraction suffix and with single-digit groups
+#: (``kernel_families.v1.json`` families ``nemotron_3_nano_4b`` and
+#: ``ministral_3_8b``: ruleset o200k, digits_max 1, contractions false).
+NEMOTRON_PATTERN = (
+    r"[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]*[\p{Ll}\p{Lm}\p{Lo}\p{M}]+"
+    r"|[^\r\n\p{L}\p{N}]?[\p{Lu}\p{Lt}\p{Lm}\p{Lo}\p{M}]+[\p{Ll}\p{Lm}\p{Lo}\p{M}]*"
+    r"|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n/]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+)
+
 #: The pattern HF ``ByteLevel(use_regex=True)`` applies (GPT-2).
 GPT2_PATTERN = (
     r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+"
@@ -125,6 +146,11 @@ class Family:
     vocab_size: int        # regular (model) vocabulary size of the real artifact
     hf_repo: str           # where the real artifact lives (not fetched here)
     real_sha256: str | None  # pinned sha256 of the real tokenizer.json, if any
+    # (o200k) the contraction suffix is part of the letter alternatives
+    contractions: bool = True
+    # the class table the ruleset reads (kernel_families.v1.json names);
+    # "" for the ruleset's default
+    class_table: str = ""
 
 
 FAMILIES: dict[str, Family] = {
@@ -185,6 +211,32 @@ FAMILIES: dict[str, Family] = {
         # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (9,703,692 B)
         real_sha256="773c2476259d9e092bba48d1f4840aaf584fa87cd5083a7e33b54d6d6f9feb77",
     ),
+    "qwen3_5_08b": Family(
+        name="qwen3_5_08b", ruleset=RULESET_CL100K, ruleset_name="cl100k",
+        pattern=QWEN35_PATTERN, digits_max=1, contractions_fold=True,
+        needs_nfc=True, ignore_merges=False,
+        # vocabulary size of the stand-in (the real artifact's is not
+        # recorded in the reference)
+        vocab_size=151643,
+        hf_repo="Qwen/Qwen3.5-0.8B",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (12,807,982 B)
+        real_sha256="5f9e4d4901a92b997e463c1f46055088b6cca5ca61a6522d1b9f64c4bb81cb42",
+        class_table="cl100k_m2l_v3",
+    ),
+    "nemotron_3_nano_4b": Family(
+        name="nemotron_3_nano_4b", ruleset=RULESET_O200K, ruleset_name="o200k",
+        pattern=NEMOTRON_PATTERN, digits_max=1, contractions_fold=False,
+        # tiktoken-derived vocabulary, as gpt-oss: no normalizer,
+        # whole-vocabulary pieces first
+        needs_nfc=False, ignore_merges=True,
+        # vocabulary size of the stand-in (the real artifact's is not
+        # recorded in the reference)
+        vocab_size=131072,
+        hf_repo="nvidia/NVIDIA-Nemotron-3-Nano-4B-BF16",
+        # src/toktier/artifacts/tables/artifact_manifest.v1.json pin (17,077,484 B)
+        real_sha256="623c34567aebb18582765289fbe23d901c62704d6518d71866e0e58db892b5b7",
+        contractions=False,
+    ),
     "gpt2": Family(
         name="gpt2", ruleset=RULESET_R50K, ruleset_name="r50k",
         pattern=GPT2_PATTERN, digits_max=0, contractions_fold=False,
@@ -192,6 +244,14 @@ FAMILIES: dict[str, Family] = {
         hf_repo="openai-community/gpt2", real_sha256=None,
     ),
 }
+
+
+def class_table_name(fam: Family) -> str:
+    """The reference name of the class table the family's ruleset reads."""
+    if fam.class_table:
+        return fam.class_table
+    return {"deepseek": "deepseek_v1", "o200k": "o200k_v4",
+            "kimi": "kimi_v1"}.get(fam.ruleset_name, "cl100k_v3")
 
 
 def family(name: str) -> Family:

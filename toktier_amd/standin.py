@@ -35,6 +35,12 @@ Shapes follow the real artifacts:
   ``ByteLevel(use_regex=False)``; BPE with ``ignore_merges`` true over
   199,998 regular entries, merges re-derived tiktoken-style as for
   Llama-3, and the harmony markers from id 199,998.
+- ``qwen3_5_08b``: as ``qwen3_8b`` with the Qwen3.5 split (marks in the
+  letter run), trained with text dense in combining marks; 151,643
+  entries (the stand-in's size).
+- ``nemotron_3_nano_4b``: as ``gpt_oss_120b`` with the Nemotron-3 split
+  (no contraction suffix, single digits); 131,072 entries (the
+  stand-in's size).
 
 The committed artifacts live in ``toktier_amd/data/artifacts`` (xz
 compressed); this module regenerates them (``python -m toktier_amd.standin``),
@@ -182,6 +188,43 @@ def _synthetic_corpus(seed: int, cjk_chars: int, latin1_words: int,
     return out
 
 
+def _mark_corpus(seed: int, n_lines: int) -> list[str]:
+    """Lines dense in combining marks, whose split differs between the
+    Qwen2 pattern (marks outside the letter run) and Qwen3.5's (marks in
+    it): Devanagari and Thai syllables (vowel signs, viramas, tone marks
+    that NFC keeps), and Latin letters with stacked accents."""
+    rng = np.random.default_rng(seed)
+    deva_c = [chr(c) for c in range(0x0915, 0x0939)]
+    deva_v = [chr(c) for c in (0x093E, 0x093F, 0x0940, 0x0941, 0x0942, 0x0947,
+                               0x0948, 0x094B, 0x094C, 0x0902, 0x094D)]
+    thai_c = [chr(c) for c in range(0x0E01, 0x0E2F)]
+    thai_m = [chr(c) for c in (0x0E31, 0x0E34, 0x0E35, 0x0E36, 0x0E37, 0x0E38,
+                               0x0E39, 0x0E47, 0x0E48, 0x0E49, 0x0E4A, 0x0E4B)]
+    accents = [chr(c) for c in (0x0301, 0x0300, 0x0308, 0x0323, 0x0331, 0x0330)]
+    out = []
+    for _ in range(n_lines):
+        words = []
+        for _ in range(int(rng.integers(4, 12))):
+            kind = rng.random()
+            k = int(rng.integers(1, 5))
+            if kind < 0.4:
+                w = "".join(deva_c[int(rng.integers(len(deva_c)))]
+                            + (deva_v[int(rng.integers(len(deva_v)))] if rng.random() < 0.7 else "")
+                            for _ in range(k))
+            elif kind < 0.75:
+                w = "".join(thai_c[int(rng.integers(len(thai_c)))]
+                            + (thai_m[int(rng.integers(len(thai_m)))] if rng.random() < 0.6 else "")
+                            for _ in range(k))
+            else:
+                w = "".join("qxzk"[int(rng.integers(4))]
+                            + "".join(accents[int(rng.integers(len(accents)))]
+                                      for _ in range(int(rng.integers(1, 3))))
+                            for _ in range(k))
+            words.append(w)
+        out.append(" ".join(words))
+    return out
+
+
 # -------------------------------------------------------------- training
 
 def _train(name: str) -> dict:
@@ -227,7 +270,8 @@ def _train(name: str) -> dict:
         initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
         show_progress=False,
     )
-    corpus = _code_corpus(150_000_000 if name not in ("gpt2", "laguna_s_2_1")
+    corpus = _code_corpus(150_000_000 if name not in (
+        "gpt2", "laguna_s_2_1", "qwen3_5_08b", "nemotron_3_nano_4b")
                           else 60_000_000)
     if name == "qwen3_8b":
         corpus += _synthetic_corpus(20261201, 6_000_000, 1_500_000, 40000)
@@ -239,6 +283,11 @@ def _train(name: str) -> dict:
         corpus += _synthetic_corpus(20261204, 6_000_000, 1_500_000, 40000)
     elif name == "kimi_k3":
         corpus += _synthetic_corpus(20261205, 10_000_000, 1_500_000, 40000)
+    elif name == "qwen3_5_08b":
+        corpus += _synthetic_corpus(20261206, 3_000_000, 1_000_000, 20000)
+        corpus += _mark_corpus(20261206, 300_000)
+    elif name == "nemotron_3_nano_4b":
+        corpus += _synthetic_corpus(20261207, 3_000_000, 1_000_000, 20000)
     tok.train_from_iterator(corpus, trainer)
     spec = json.loads(tok.to_str())
     model = spec["model"]
@@ -247,7 +296,7 @@ def _train(name: str) -> dict:
         raise RuntimeError(
             f"{name}: corpus too small: vocab {len(vocab)} < {n_regular}")
     model["ignore_merges"] = bool(fam.ignore_merges)
-    if name in ("llama_3_1_8b", "gpt_oss_120b"):
+    if name in ("llama_3_1_8b", "gpt_oss_120b", "nemotron_3_nano_4b"):
         model["merges"] = _tiktoken_style_merges(vocab)
     elif name == "kimi_k3":
         model["merges"] = _tiktoken_style_merges(vocab, ties="cut")
@@ -301,6 +350,16 @@ def family_added_tokens(name: str) -> list[tuple[str, int, bool]]:
                  200007: "<|end|>", 200008: "<|message|>", 200012: "<|call|>"}
         return [(named.get(i, f"<|reserved_{i}|>"), i, True)
                 for i in range(199998, 200019)]
+    if name == "qwen3_5_08b":
+        # (the real list is not recorded offline; Qwen3's markers, numbered
+        # after the stand-in's vocabulary)
+        return family_added_tokens("qwen3_8b")
+    if name == "nemotron_3_nano_4b":
+        # (the real list is not recorded offline; the common control and
+        # chat markers, numbered after the stand-in's vocabulary)
+        names = ["<unk>", "<s>", "</s>", "<|im_start|>", "<|im_end|>",
+                 "<think>", "</think>", "<SPECIAL_10>"]
+        return [(c, 131072 + k, k < 3 or k == 7) for k, c in enumerate(names)]
     if name == "laguna_s_2_1":
         # (the real list is not recorded offline; chat and FIM markers in
         # the common form)

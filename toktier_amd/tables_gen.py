@@ -76,6 +76,17 @@ def build_classes() -> np.ndarray:
     return tab
 
 
+def build_cl100k_m2l(base: np.ndarray) -> np.ndarray:
+    """The four-class table with the Mark code points moved into L: the
+    Qwen3.5 split runs letters as ``[\p{L}\p{M}]+`` and leaves marks out
+    of its punctuation run, and both differences are this one change to the
+    table (the reference's generator ``class_tables:cl100k_m2l``,
+    ``tools/generate_class_tables.py:574-597``)."""
+    tab = base.copy()
+    tab[_probe_membership(r"\p{M}")] = L
+    return tab
+
+
 #: DeepSeek seven-class encoding (the reference's
 #: pretok_classes_deepseek.v1.meta.json enum)
 DS_O, DS_L, DS_M, DS_N, DS_PS, DS_WS, DS_CRLF = range(7)
@@ -269,6 +280,9 @@ def main() -> None:
     cls = build_classes()
     np.savez_compressed(TABLE_DIR / "classes.npz", cl100k=cls)
     print("classes", np.bincount(cls, minlength=4), flush=True)
+    m2l = build_cl100k_m2l(cls)
+    np.savez_compressed(TABLE_DIR / "classes_m2l.npz", cl100k_m2l=m2l)
+    print("m2l classes", np.bincount(m2l, minlength=4), flush=True)
     ds = build_deepseek_classes()
     np.savez_compressed(TABLE_DIR / "classes_deepseek.npz", deepseek=ds)
     print("deepseek classes", np.bincount(ds, minlength=7), flush=True)
