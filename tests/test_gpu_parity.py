@@ -636,6 +636,7 @@ def test_o200k_long_cjk_request_is_linear():
     assert dt < 0.5, dt
 
 
+@pytest.mark.family("qwen3_5_08b")
 def test_qwen35_marks_continue_letter_runs():
     """The m2l class table (Qwen3.5: combining marks continue a letter run,
     [\\p{L}\\p{M}]+): syllables with vowel signs and viramas, and stacked
@@ -666,6 +667,7 @@ def test_qwen35_marks_continue_letter_runs():
         assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
 
 
+@pytest.mark.family("nemotron_3_nano_4b")
 def test_nemotron_single_digits_and_no_contractions():
     """The o200k row without the contraction suffix and with single digits
     (Nemotron-3): digit runs at the word and tile edges (each digit a piece

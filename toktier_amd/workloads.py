@@ -277,19 +277,21 @@ def chat(tokenizer_json: str, family: str, n_chars: int = CHARS_4M,
     ``<|start|>role<|message|>`` ... ``<|end|>`` turns (assistant turns on
     the final channel, some after an analysis one), Kimi
     ``<|im_role|>role<|im_middle|>`` ... ``<|im_end|>`` turns, GPT-2
-    documents joined by ``<|endoftext|>``. Turns hold U[200, 3000] chars."""
+    documents joined by ``<|endoftext|>``; Qwen3.5 as Qwen3, Nemotron-3 the
+    Qwen3 turns after ``<s>``. Turns hold U[200, 3000] chars."""
     rng = np.random.default_rng(SEED_BASE + 6 + 1000 * sample)
     body = config2(tokenizer_json, n_chars=n_chars, sample=sample)
     roles = ["system", "user", "assistant"]
     out: list[str] = (["<|begin_of_text|>"] if family == "llama_3_1_8b" else
-                      ["<｜begin▁of▁sentence｜>"] if family == "deepseek_v3" else [])
+                      ["<｜begin▁of▁sentence｜>"] if family == "deepseek_v3" else
+                      ["<s>"] if family == "nemotron_3_nano_4b" else [])
     total, at, turn = sum(map(len, out)), 0, 0
     while total < n_chars and at < len(body):
         n = int(rng.integers(200, 3001))
         content = body[at:at + n]
         at += n
         role = roles[0] if turn == 0 else roles[1 + (turn - 1) % 2]
-        if family == "qwen3_8b":
+        if family in ("qwen3_8b", "qwen3_5_08b", "nemotron_3_nano_4b"):
             if role == "assistant" and rng.random() < 0.5:
                 content = "<think>\n" + content[: n // 3] + "\n</think>\n\n" + content[n // 3:]
             piece = f"<|im_start|>{role}\n{content}<|im_end|>\n"
