@@ -234,3 +234,18 @@ def test_committed_rows_cover_the_stand_ins():
         assert row["status"] in (R.STATUS_CERTIFIED, R.STATUS_EXPERIMENTAL)
         assert "gfx950" in R.architecture_statuses(row)
         assert len(row["binary_digest"]) == 64
+
+
+def test_committed_soak_covers_every_family():
+    """The committed soak reading (tests/test_gpu_soak.py at
+    TK_SOAK_CHARS=100000000 on gfx950): at least 100 M characters per
+    family, every row equal to the oracle's."""
+    from conftest import FAMILY_NAMES
+    path = R.REGISTRY_PATH.with_name("gfx950_soak.v1.json")
+    soak = json.loads(path.read_text(encoding="utf-8"))
+    assert soak["mismatches"] == 0
+    for name in FAMILY_NAMES:
+        rec = soak["families"][name]
+        assert rec["chars"] >= 100_000_000, name
+        assert rec["mismatch"] is None, name
+        assert rec["documents"] > 10_000 and rec["long_documents"] > 1_000, name
