@@ -36,7 +36,7 @@ for p in (str(ROOT), str(HERE), str(HERE / "golden")):
 
 SOAK_SEED = 20261202
 BATCH_CHARS = 2_000_000
-MAX_DOCS = 400
+MAX_DOCS = 1000  # a batch ends at BATCH_CHARS characters, well before this
 
 _ATOMS_COMMON = [
     "a", "A", "'", "s", "S", "\u017f", "1", "2", "9", " ", "  ", "\t", "\r",
