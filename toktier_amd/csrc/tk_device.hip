@@ -322,6 +322,8 @@ struct GCtx {
 //   bit  27     the decode at p is valid UTF-8
 //   bits 28..29 class bits 2..3 (the seven DeepSeek / o200k classes, the
 //               ten kimi classes)
+//   bits 30..31 back(p - 1), so that prev(p) = p - 1 - (entry(p) >> 30)
+//               reads the entry at p only (set at every span position)
 // packed LDS table entry of k_pretok: byte id (LTAB_NOID: none), class of
 // the code point, its NFC quick-check value
 constexpr uint32_t LTAB_NOID = 0xFFFFFu;
@@ -1192,10 +1194,12 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total)
 // into the word. Positions inside the block are 32-bit offsets from lo (the
 // first entry); RS is the ruleset, DM whether document starts are marked.
 template <int RS, bool DM>
-__global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_pretok(DevTables t, DevWork w,
+__global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(7, 7))) void k_pretok(DevTables t, DevWork w,
                                                        int64_t nwords) {
   __shared__ __align__(16) uint8_t sb[PT_BYTES];
   __shared__ uint32_t se[PT_SPAN];
+  // the NFC quick-check value of each span position's code point
+  __shared__ uint8_t snfc[PT_SPAN];
   __shared__ uint64_t sdm[PT_DMW];
   __shared__ uint64_t sw[PT_TILE / 64 + 1];  // the tile's start words + next
   __shared__ uint32_t lcnt[PACK_CLASSES];
@@ -1293,11 +1297,22 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   for (int j = tid; j < PT_SPAN; j += PRETOK_TPB) {
     const int sj = j + (PT_PAD - PT_HALO);  // its byte in sb
     uint32_t e = 0;
+    uint8_t snf = 0;
+    {
+      // the step from this position to the previous character's lead
+      // (back of the byte before, with its own position clamp)
+      const int64_t pos = lo + j;
+      const bool u1 = is_cont(sb[sj - 1]) && pos > 1;
+      const bool u2 = u1 && is_cont(sb[sj - 2]) && pos > 2;
+      const bool u3 = u2 && is_cont(sb[sj - 3]) && pos > 3;
+      e = (uint32_t)(u1 + u2 + u3) << 30;
+    }
     if (j >= jlo && j < jhi) {
       const int pg = lo + j < 3 ? (int)(lo + j) : 3;  // min(position, 3)
       const uint32_t b0 = sb[sj], b1 = sb[sj + 1], b2 = sb[sj + 2], b3 = sb[sj + 3];
       const bool c0 = is_cont(b0), c1 = is_cont(b1), c2 = is_cont(b2), c3 = is_cont(b3);
       const bool m1 = is_cont(sb[sj - 1]), m2 = is_cont(sb[sj - 2]);
+      const bool m3 = is_cont(sb[sj - 3]);
       // steps back to a lead over at most three continuation bytes (never
       // below position 0); continuation bytes after this one (bytes past
       // the text are staged as 0)
@@ -1316,22 +1331,31 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
                        (n == 3 && v < 0x10000) || v > 0x10FFFF ||
                        (v >= 0xD800 && v <= 0xDFFF);
       const uint32_t cp = bad ? 0xFFFDu : v;
-      const uint32_t cl = cp < 256 ? (ltab[cp] >> LTAB_CLS) & 7 : t.cls[cp];
+      uint32_t cl, nv;
+      if (cp < 256) {
+        const uint32_t lt = ltab[cp];
+        cl = (lt >> LTAB_CLS) & 7;
+        nv = lt >> LTAB_NFC;
+      } else {
+        cl = t.cls[cp];
+        nv = w.check_nfc ? t.nfc[cp] : 0u;
+      }
+      snf = (uint8_t)nv;
       // a continuation byte is valid when the first byte back that is not
       // one (at most three back, not before position 0) is a lead that
       // announces at least that many continuation bytes
       bool ok = !bad;
       if (c0) {
-        const bool m3 = is_cont(sb[sj - 3]);
         const int d = !m1 ? 1 : !m2 ? 2 : !m3 ? 3 : 4;
         const uint32_t l = sb[sj - (d < 4 ? d : 3)];
         const int need = l >= 0xF8 ? 0 : l >= 0xF0 ? 3 : l >= 0xE0 ? 2 : l >= 0xC0 ? 1 : 0;
         ok = d <= pg && need >= d;
       }
-      e = cp | ((cl & 3) << 21) | ((cl >> 2) << 28) | ((uint32_t)back << 23) |
+      e |= cp | ((cl & 3) << 21) | ((cl >> 2) << 28) | ((uint32_t)back << 23) |
           ((uint32_t)fwd << 25) | (ok ? 1u << 27 : 0u);
     }
     se[j] = e;
+    snfc[j] = snf;
   }
   __syncthreads();
   const int lane = tid & 63, wv = wave_id();
@@ -1424,7 +1448,7 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
   // document start at local offset L: position 0, or a marked doc head
   const int Lz = lo <= 0 ? (int)(-lo) : -1;
   auto prv = [&](int L) {  // local offset of the character before L
-    return L - 1 - (int)((se[L - 1] >> 23) & 3);
+    return L - 1 - (int)(se[L] >> 30);
   };
   // the tile's words, and the first word after it (the next block writes
   // that one; it is recomputed here to size the pieces near the tile end)
@@ -1487,19 +1511,22 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       // the fixed context: every offset used lies in the LDS span (tile
       // positions are at least PT_HALO from either end, and the four
       // characters back cover at most 16 bytes); the one after is checked
+      // (each step back reads one entry: the entry holds the step to the
+      // character before it; the steps past a document start are read all
+      // the same and not used, h2 .. h4)
       Ctx5 x;
       x.c0 = e;
-      const int L1 = prv(Li);
+      const int L1 = Li - 1 - (int)(e >> 30);
       x.c1 = se[L1];
-      x.h2 = !ds(L1);
-      const int L2 = x.h2 ? prv(L1) : L1;
+      const int L2 = L1 - 1 - (int)(x.c1 >> 30);
       x.c2 = se[L2];
-      x.h3 = x.h2 && !ds(L2);
-      const int L3 = x.h3 ? prv(L2) : L2;
+      const int L3 = L2 - 1 - (int)(x.c2 >> 30);
       x.c3 = se[L3];
-      x.h4 = x.h3 && !ds(L3);
-      const int L4 = x.h4 ? prv(L3) : L3;
+      const int L4 = L3 - 1 - (int)(x.c3 >> 30);
       x.c4 = se[L4];
+      x.h2 = !ds(L1);
+      x.h3 = x.h2 && !ds(L2);
+      x.h4 = x.h3 && !ds(L3);
       const int Ln = Li + 1 + (int)((e >> 25) & 3);
       const bool nin = Ln < PT_SPAN;
       x.hn = lo + Ln < nb && !ds(Ln);
@@ -1627,14 +1654,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       // sentinel starts past the text; no start inside a character
       const bool s = !in || (lead && (d0 || r != 0));
       if (w.check_nfc && lead) {
-        const uint32_t cp = e & 0x1FFFFF;
-        const uint8_t v = cp < 256 ? ltab[cp] >> LTAB_NFC : t.nfc[cp];
-        if (v == 255) {
-          st |= ST_NFC;
-        } else if (v != 0 && !d0) {
-          const uint32_t pc = x.c1 & 0x1FFFFF;
-          if ((pc < 256 ? ltab[pc] >> LTAB_NFC : t.nfc[pc]) > v) st |= ST_NFC;
-        }
+        const uint32_t v = snfc[Li];
+        if (v == 255 || (v != 0 && !d0 && snfc[L1] > v)) st |= ST_NFC;
       }
       uint64_t m = __ballot(s);
       // no start inside an added-token literal (its first byte is a document
@@ -1782,14 +1803,8 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(8, 8
       // sentinel starts past the text; no start inside a character
       const bool s = !in || (lead && ((g >> sp) & 1));
       if (w.check_nfc && lead) {
-        const uint32_t cp = e & 0x1FFFFF;
-        const uint8_t v = cp < 256 ? ltab[cp] >> LTAB_NFC : t.nfc[cp];
-        if (v == 255) {
-          st |= ST_NFC;
-        } else if (v != 0 && !ds(Li)) {
-          const uint32_t pc = se[prv(Li)] & 0x1FFFFF;
-          if ((pc < 256 ? ltab[pc] >> LTAB_NFC : t.nfc[pc]) > v) st |= ST_NFC;
-        }
+        const uint32_t v = snfc[Li];
+        if (v == 255 || (v != 0 && !ds(Li) && snfc[prv(Li)] > v)) st |= ST_NFC;
       }
       uint64_t m = __ballot(s);
       if (DM && w.litb) m &= ~w.litb[wd];
