@@ -60,6 +60,7 @@ pub const TK_KERNELS: usize = 6;
 pub const TK_OPT_COMPACT_PAIRS: c_int = 1;
 pub const TK_OPT_REPAIR_WIDEN: c_int = 2;
 pub const TK_OPT_TIMED_KERNEL: c_int = 3;
+pub const TK_OPT_HOT_PAIRS: c_int = 4;
 
 /// The value of `tk_config.ruleset` for each ruleset.
 pub const TK_RULESET_CL100K: i32 = 0;

@@ -312,6 +312,11 @@ int tk_engine_last_timing(const tk_engine* engine, double* us, int n);
 #define TK_OPT_REPAIR_WIDEN 2
 /* TK_OPT_TIMED_KERNEL: the TK_KERNEL_* timing mode 2 times. */
 #define TK_OPT_TIMED_KERNEL 3
+/* TK_OPT_HOT_PAIRS: 1 makes the merge kernels of pieces of 65..256 bytes
+ * probe a 16 KB copy of the lowest-ranked rules in LDS before the pair
+ * table in HBM (when the engine built the compact table); 0 (default) the
+ * table only. */
+#define TK_OPT_HOT_PAIRS 4
 int tk_engine_set_option(tk_engine* engine, int option, int64_t value);
 
 /* Test-only fault injection (no counterpart in the reference; the hook its

@@ -694,6 +694,27 @@ def test_nemotron_single_digits_and_no_contractions():
         assert list(t.encode(s).array) == k.hf_ids(s), (len(s), s[:20])
 
 
+@pytest.mark.parametrize("name", ["qwen3_8b", "llama_3_1_8b"])
+def test_hot_pair_probe_matches_oracle(name):
+    """TK_OPT_HOT_PAIRS on: the merges of pieces of 65..256 bytes probe the
+    LDS copy of the lowest-ranked rules first (Llama: beside the
+    unsafe-rank bitmap in the same LDS); the ids equal the option off and
+    the oracle's."""
+    from toktier_amd import _ffi, workloads
+    k, t = kit(name), tok(name)
+    text = workloads.config5(k.json, n_chars=300_000, n_runs=1, run_chars=2_000)
+    want = k.oracle.encode_bytes(text.encode())
+    assert not isinstance(want, int)
+    try:
+        t.engine.set_option(_ffi.TK_OPT_HOT_PAIRS, 1)
+        on = t.encode(text).array
+    finally:
+        t.engine.set_option(_ffi.TK_OPT_HOT_PAIRS, 0)
+    off = t.encode(text).array
+    assert np.array_equal(on, want)
+    assert np.array_equal(off, want)
+
+
 # kimi: Han runs of every subclass, Han numbers inside and at the start of
 # digit groups, other Han in punctuation runs, the tail without '/'
 KIMI_BRANCHES = [

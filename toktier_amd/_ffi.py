@@ -36,6 +36,7 @@ TK_NOALLOC_MAX_BYTES = 1 << 20
 TK_OPT_COMPACT_PAIRS = 1
 TK_OPT_REPAIR_WIDEN = 2
 TK_OPT_TIMED_KERNEL = 3
+TK_OPT_HOT_PAIRS = 4
 # TK_KERNEL_* in the header's order: the kernels the timing modes time
 KERNELS = ("k_pretok", "k_bpe_pack", "k_compact", "k_bpe_rows",
            "k_long_windows", "k_added")

@@ -80,7 +80,19 @@ struct DevTables {
   const uint64_t* ctab;        // compact pair table or nullptr
   uint64_t cmask;              // buckets - 1
   uint32_t cbits;              // log2(buckets)
+  // hot pairs: the rules of rank < hot_k in the compact table's layout with
+  // HOT_BITS buckets (HOT_BYTES), copied into LDS by the kernels that probe
+  // it before the table in HBM; nullptr: none
+  const uint64_t* hot;
+  uint32_t hot_k;
 };
+
+// The hot-pair table: 2^HOT_BITS buckets of 16 bytes (16 KB), the compact
+// table's bijection, bucket pair and slot layout with a 26-bit tag. An
+// empty slot is all ones; its rank field (2^19 - 1) is never below hot_k,
+// which is how a probe tells it from a rule.
+constexpr uint32_t HOT_BITS = 10;
+constexpr uint32_t HOT_BYTES = 16u << HOT_BITS;
 
 // length classes of the packed short-piece BPE (see pack_slot)
 constexpr int PACK_CLASSES = 13;
@@ -117,6 +129,9 @@ struct DevWork {
   uint32_t* seglist;     // segments that fit no grid window
   uint32_t* segcount;    // ctrl[3]
   uint32_t seg_cap;
+  uint32_t* wlist;       // a repair pass's windows: v << 1 | (phase 0 too)
+  uint32_t* wcount;      // ctrl[12]
+  uint32_t wlist_cap;
   uint32_t* nfail;       // this certify pass's failed cuts (ctrl[4] / [8])
   uint32_t* nfail_prev;  // a device-side repair pass: the previous pass's
                          // count (the pass runs only when it is not 0);
@@ -171,6 +186,7 @@ constexpr uint64_t HR_FIRST = 1ull << 31, HR_LAST = 1ull << 30;
 constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PASS = 7,
               CTRL_FAIL2 = 8, CTRL_PREP = 9, CTRL_WIDE = 10, CTRL_ROWS = 11,
+              CTRL_WIN = 12,
               CTRL_PSEG = 64, CTRL_PSEG_STRIDE = 64,
               CTRL_PSEG_COUNT = 32, CTRL_WORDS = CTRL_PSEG + 8 * CTRL_PSEG_STRIDE;
 // gate words in host memory: k_bpe_pack writes GATE_NLONG / GATE_NROWS /
@@ -319,6 +335,11 @@ hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
 // (width > 0: each failed cut also drops its `width` nearest cuts on each
 // side inside its piece, k_fail_widen, first)
 hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, uint32_t width);
+// A repair pass's merges (after launch_apply_fail): the windows of the dirty
+// words and the segments that fit no window, listed by k_seg_scan and
+// merged together by k_repair_merge, then the segments over WIDE_MAX bytes
+// (k_seg_block).
+hipError_t launch_repair_segments(const DevTables& t, const DevWork& w, hipStream_t s);
 // the first repair pass that widens the failed cuts (TK_OPT_REPAIR_WIDEN),
 // and the width of pass p >= it: 4^(p - first + 1), capped
 constexpr int REPAIR_WIDEN = 4;

@@ -126,6 +126,36 @@ __device__ __forceinline__ bool ctab_find(const DevTables& t, uint32_t l,
   return (k0 | k1 | k2 | k3) != 0u;
 }
 
+// The hot-pair table's probe (ctab_find's, over HOT_BITS buckets in LDS):
+// true, with the rule, when the pair has a rule of rank < hot_k; false
+// says nothing about rules of higher rank (the caller asks the compact
+// table then).
+__device__ __forceinline__ bool hot_find(const uint4* hot, uint32_t hot_k,
+                                         uint32_t l, uint32_t r,
+                                         uint32_t* rank, uint32_t* id) {
+  const uint32_t b = (r ^ pair_round(l, 0x9E3779u)) & 0x3FFFFu;
+  const uint32_t lo = (l << 18) | b, hi = l >> 14;
+  const uint32_t b1 = lo & ((1u << HOT_BITS) - 1);
+  const uint32_t tag = __builtin_amdgcn_alignbit(hi, lo, HOT_BITS);
+  const uint32_t b2 = pair_alt(b1, tag, HOT_BITS);
+  const uint4 u = hot[b1], v = hot[b2];
+  const uint32_t w0 = tag << 1, w1 = w0 | 1u;
+  const uint32_t k0 = (u.y >> 5) == w0 ? ~0u : 0u, k1 = (u.w >> 5) == w0 ? ~0u : 0u;
+  const uint32_t k2 = (v.y >> 5) == w1 ? ~0u : 0u, k3 = (v.w >> 5) == w1 ? ~0u : 0u;
+  const uint32_t slo = (u.x & k0) | (u.z & k1) | (v.x & k2) | (v.z & k3);
+  const uint32_t shi = (u.y & k0) | (u.w & k1) | (v.y & k2) | (v.w & k3);
+  *rank = __builtin_amdgcn_alignbit(shi, slo, 18) & 0x7FFFFu;
+  *id = slo & 0x3FFFFu;
+  return (k0 | k1 | k2 | k3) != 0u && *rank < hot_k;
+}
+
+// The block's LDS copy of the hot-pair table (HOT_BYTES at `dst`), filled
+// by all threads; the caller synchronizes before the first probe.
+__device__ __forceinline__ void hot_stage(const DevTables& t, uint4* dst) {
+  const uint4* src = reinterpret_cast<const uint4*>(t.hot);
+  for (uint32_t j = threadIdx.x; j < HOT_BYTES / 16; j += blockDim.x) dst[j] = src[j];
+}
+
 // whole-piece vocabulary id (ignore_merges) or -1; a piece longer than the
 // longest vocabulary entry is none (no hash over it)
 __device__ int32_t vocab_lookup(const DevTables& t, const uint8_t* s,
@@ -2521,7 +2551,8 @@ template <int R>
 __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
                                               const DevWork& w, uint32_t a,
                                               int len, bool vocab_first,
-                                              const uint32_t* unsafe_lds);
+                                              const uint32_t* unsafe_lds,
+                                              const uint4* hot = nullptr);
 
 // Work units by class: pack_per_unit(c) pieces of class c each. Workgroups
 // go to the XCDs in turn (block b on XCD b % PACK_XCDS, up to a rotation),
@@ -3282,7 +3313,8 @@ template <int R>
 __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
                                               const DevWork& w, uint32_t a,
                                               int len, bool vocab_first,
-                                              const uint32_t* unsafe_lds) {
+                                              const uint32_t* unsafe_lds,
+                                              const uint4* hot) {
   const int lane = threadIdx.x & 63;
   if (vocab_first && t.ignore_merges) {
     int32_t hit = -1;
@@ -3370,7 +3402,8 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
             if (v != ~0ULL) { rk[r] = (uint32_t)(v >> 32); mid[r] = (uint32_t)v; }
           } else if (t.ctab) {
             uint32_t r_, m_;
-            if (ctab_find(t, sym[r] & SYM_ID, ns & SYM_ID, &r_, &m_)) {
+            if ((hot && hot_find(hot, t.hot_k, sym[r] & SYM_ID, ns & SYM_ID, &r_, &m_)) ||
+                ctab_find(t, sym[r] & SYM_ID, ns & SYM_ID, &r_, &m_)) {
               rk[r] = r_;
               mid[r] = m_;
             }
@@ -3467,16 +3500,21 @@ __global__ __launch_bounds__(256) void k_bpe_wide(DevTables t, DevWork w,
 // copy of it in LDS (one lookup per merge round).
 constexpr uint32_t ROWS_UNSAFE_LDS = 12288;
 __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
-  extern __shared__ uint32_t unsafe_lds[];
+  extern __shared__ __align__(16) uint32_t unsafe_lds[];
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
   if (blockIdx.x * 4 >= n) return;
   const bool lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS;
-  if (lds) {
+  if (lds)
     for (uint32_t j = threadIdx.x; j < t.unsafe_words; j += 256)
       unsafe_lds[j] = t.unsafe[j];
-    __syncthreads();
+  // the hot-pair table after the bitmap (16-byte aligned)
+  uint4* hot = nullptr;
+  if (t.hot) {
+    hot = reinterpret_cast<uint4*>(unsafe_lds + (lds ? (t.unsafe_words + 3) & ~3u : 0u));
+    hot_stage(t, hot);
   }
+  if (lds || hot) __syncthreads();
   const int wv = wave_id();
   const uint32_t waves = gridDim.x * 4;
   // (no issue priority: these pieces end well before the cut / segment /
@@ -3488,8 +3526,8 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
     const int len = (int)(b - a);
     if (len <= lo || len > 256) continue;  // wave-uniform
-    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
-    else wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr);
+    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
+    else wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
   }
 }
 
@@ -3549,43 +3587,127 @@ __device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
   return wd >= 0 && ((d[wd >> 6] >> (wd & 63)) & 1);
 }
 
+// Segment work of one grid window (phase 0: aligned [64v, 64v+64), phase 1:
+// shifted [64v-32, 64v+32)): the BPE of the long-piece segments the window
+// holds whole, with histories. With `push`, phase 0 also lists the segment
+// that starts in the window and fits no grid window (seglist). Wave-uniform.
+__device__ __forceinline__ void segment_window(const DevTables& t, const DevWork& w,
+                                               int64_t v, int phase, bool push) {
+  const int lane = threadIdx.x & 63;
+  auto seg = [&](int64_t wd) { return seg_word(w, wd); };
+  const uint64_t L = inlong_window(w, v, phase);
+  if (L == 0) return;
+  const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
+  uint64_t S;
+  bool E;
+  window_bits(v, phase, seg, &S, &E);
+  const int64_t pos = base + lane;
+  const bool inl = (L >> lane) & 1;
+  const uint64_t le = S & mask_le(lane);
+  const int ps = le ? 63 - __builtin_clzll(le) : -1;
+  const uint64_t gt = S & ~mask_le(lane);
+  const int pe = gt ? __builtin_ctzll(gt) : 64;
+  const bool contained = ps >= 0 && (pe < 64 || E);
+  bool elig = inl && contained;
+  if (phase == 1 && elig && ((base + ps) >> 6) == ((base + pe - 1) >> 6))
+    elig = false;
+  if (push && phase == 0 && inl && ps == lane && !contained) {
+    const int64_t b = seg_end_after(v + 1, seg);
+    if (!fits_a_grid(pos, b))
+      push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
+  }
+  wave_bpe<false, true, true>(t, w, base, base + lane, lane, elig, ps, pe);
+}
+
 // Segment pass over the long-piece bytes (64-byte grid windows, aligned and
 // shifted by 32, with histories). Segments that fit no grid window go to
-// seglist. With
-// all == 0 (a repair pass) only windows touching a dirty word are redone.
+// seglist. With all == 0 only windows touching a dirty word are redone.
 __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
                                                        int64_t nwin, int all) {
-  const int lane = threadIdx.x & 63;
   const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
   if (v > nwin || !pass_live(w)) return;
   __builtin_amdgcn_s_setprio(2);  // (the long pieces' chain: k_long_windows)
-  auto seg = [&](int64_t wd) { return seg_word(w, wd); };
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
     if (!all && !word_dirty(w.dirty_cur, v) &&
         !(phase == 1 && word_dirty(w.dirty_cur, v - 1)))
       continue;
-    const uint64_t L = inlong_window(w, v, phase);
-    if (L == 0) continue;
-    const int64_t base = phase == 0 ? v * 64 : v * 64 - 32;
-    uint64_t S;
-    bool E;
-    window_bits(v, phase, seg, &S, &E);
-    const int64_t pos = base + lane;
-    const bool inl = (L >> lane) & 1;
-    const uint64_t le = S & mask_le(lane);
-    const int ps = le ? 63 - __builtin_clzll(le) : -1;
-    const uint64_t gt = S & ~mask_le(lane);
-    const int pe = gt ? __builtin_ctzll(gt) : 64;
-    const bool contained = ps >= 0 && (pe < 64 || E);
-    bool elig = inl && contained;
-    if (phase == 1 && elig && ((base + ps) >> 6) == ((base + pe - 1) >> 6))
-      elig = false;
-    if (phase == 0 && inl && ps == lane && !contained) {
-      const int64_t b = seg_end_after(v + 1, seg);
-      if (!fits_a_grid(pos, b))
-        push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
+    segment_window(t, w, v, phase, true);
+  }
+}
+
+// A repair pass's work list, one thread per word of the dirty bitmap (64
+// text words): every window k_long_segments would redo (v dirty: both
+// phases; v - 1 dirty alone: phase 1), as v << 1 | (phase 0 too), and every
+// segment it would list (the segment that starts in a dirty word at its
+// last start, runs past the word and fits no grid window). Run after
+// k_apply_fail, so the cuts are final for the pass.
+__global__ void k_seg_scan(DevWork w, int64_t nwin) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q > nwin / 64 || !pass_live(w)) return;
+  uint64_t D = w.dirty_cur[q];
+  if (!D) return;
+  auto seg = [&](int64_t wd) { return seg_word(w, wd); };
+  const uint64_t Dn = w.dirty_cur[q + 1];
+  while (D) {
+    const int j = __builtin_ctzll(D);
+    D &= D - 1;
+    const int64_t d = 64 * q + j;
+    if (d > nwin) break;
+    auto put = [&](uint32_t item) {
+      const uint32_t k = atomicAdd(w.wcount, 1u);
+      if (k < w.wlist_cap) w.wlist[k] = item;
+      else atomicOr(w.status, ST_LONGOVF);
+    };
+    put(((uint32_t)d << 1) | (d < nwin ? 1u : 0u));
+    const bool next_dirty = j < 63 ? ((D >> (j + 1)) & 1) != 0 : (Dn & 1) != 0;
+    if (d + 1 <= nwin && !next_dirty) put((uint32_t)(d + 1) << 1);
+    if (d < nwin) {
+      const uint64_t S = seg(d);
+      if (S) {
+        const int st = 63 - __builtin_clzll(S);  // the word's last start
+        if (((w.inlong[d] >> st) & 1) && !(seg(d + 1) & 1)) {
+          const int64_t a = 64 * d + st;
+          const int64_t b = seg_end_after(d + 1, seg);
+          if (!fits_a_grid(a, b))
+            push_pair(w.seglist, w.segcount, w.seg_cap, w.status, a, b);
+        }
+      }
     }
-    wave_bpe<false, true, true>(t, w, base, base + lane, lane, elig, ps, pe);
+  }
+}
+
+// A repair pass's merges in one launch: the listed segments of up to
+// WIDE_MAX bytes (first: the longest chains) and the listed windows, one
+// wave per entry, all at once (in separate launches they ran one after the
+// other, each as long as its slowest wave).
+__global__ __launch_bounds__(256) void k_repair_merge(DevTables t, DevWork w,
+                                                      int64_t nwin) {
+  __shared__ WideLds lds[4];
+  if (!pass_live(w)) return;
+  uint32_t ns = *w.segcount;
+  if (ns > w.seg_cap) ns = w.seg_cap;
+  uint32_t nw = *w.wcount;
+  if (nw > w.wlist_cap) nw = w.wlist_cap;
+  const int lane = threadIdx.x & 63;
+  const int wv = wave_id();
+  const uint32_t waves = gridDim.x * 4;
+  // (the long pieces' chain, as k_bpe_wide's segments with histories)
+  if (blockIdx.x * 4 + wv < ns + nw) __builtin_amdgcn_s_setprio(3);
+  for (uint32_t k = blockIdx.x * 4 + wv; k < ns + nw; k += waves) {
+    if (k < ns) {
+      const uint32_t a = w.seglist[2 * k], b = w.seglist[2 * k + 1];
+      const int len = (int)(b - a);
+      if (len <= 64)
+        wave_bpe<false, true, true>(t, w, (int64_t)a, (int64_t)a + lane, lane,
+                                    lane < len, 0, len);
+      else if (len <= WIDE_MAX)
+        wave_bpe_wide(t, w, a, len, false, true, lds[wv]);
+    } else {
+      const uint32_t it = w.wlist[k - ns];
+      const int64_t v = (int64_t)(it >> 1);
+      if (it & 1) segment_window(t, w, v, 0, false);
+      segment_window(t, w, v, 1, false);
+    }
   }
 }
 
@@ -3719,6 +3841,7 @@ __global__ void k_apply_fail(DevWork w, int64_t nwords) {
     *w.nfail = 0;
     if (live) {
       *w.segcount = 0;
+      *w.wcount = 0;
       if (w.npass) *w.npass += 1;
     }
   }
@@ -3831,8 +3954,9 @@ constexpr uint32_t ROWS_MAX_BLOCKS = 1024;
 hipError_t launch_bpe_rows(const DevTables& t, const DevWork& w, hipStream_t s,
                            uint32_t nlong, hipEvent_t start, hipEvent_t stop) {
   const uint32_t blocks = nlong / 4 + 1 < ROWS_MAX_BLOCKS ? nlong / 4 + 1 : ROWS_MAX_BLOCKS;
-  const size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
-                         ? (size_t)t.unsafe_words * 4 : 0;
+  size_t lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS
+                   ? (size_t)((t.unsafe_words + 3) & ~3u) * 4 : 0;
+  if (t.hot) lds += HOT_BYTES;
   if (start || stop)
     hipExtLaunchKernelGGL(k_bpe_rows, dim3(blocks), dim3(256), lds, s, start, stop,
                           0, t, w);
@@ -3869,6 +3993,18 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
   hipLaunchKernelGGL(k_bpe_wide, dim3(512), dim3(256), 0, s, t, w,
                      (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
                      w.seg_cap, 1);
+  hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
+                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
+                     w.seg_cap, 0);
+  return hipGetLastError();
+}
+
+constexpr uint32_t REPAIR_BLOCKS = 512;
+hipError_t launch_repair_segments(const DevTables& t, const DevWork& w, hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_seg_scan, dim3((uint32_t)((nwin / 64 + 1 + 255) / 256)), dim3(256),
+                     0, s, w, nwin);
+  hipLaunchKernelGGL(k_repair_merge, dim3(REPAIR_BLOCKS), dim3(256), 0, s, t, w, nwin);
   hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
                      (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
                      w.seg_cap, 0);

@@ -104,10 +104,17 @@ uint64_t host_pair_lookup(const uint64_t* keys, const uint64_t* vals,
 // placement walk runs too long. Returns false when the artifact does not fit
 // the packing (ids >= 2^18, ranks >= 2^19 - 1); the engine then probes the
 // interleaved boundary table instead.
+using PairEntries = std::vector<std::pair<uint64_t, uint64_t>>;  // (key36, rank<<18|id)
+
+// Cuckoo placement of the first n entries into 2^bits two-slot buckets
+// (the compact table's layout); false when one does not fit.
+bool place_pairs(const PairEntries& ent, size_t n, uint32_t bits,
+                 std::vector<uint64_t>& out);
+
 bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
                          uint64_t count, std::vector<uint64_t>& out,
-                         uint32_t& bits) {
-  std::vector<std::pair<uint64_t, uint64_t>> ent;  // (key36, rank<<18|id)
+                         uint32_t& bits, PairEntries* entries) {
+  PairEntries ent;
   for (uint64_t i = 0; i < count; ++i) {
     if (keys[i] == ~0ULL) continue;
     const uint64_t l = keys[i] >> 32, r = keys[i] & 0xFFFFFFFFULL;
@@ -120,11 +127,42 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
   bits = tk::CTAB_MIN_BITS;
   while ((2ULL << bits) * 6 < ent.size() * 10) ++bits;
   for (; bits <= tk::CTAB_MAX_BITS; ++bits) {
+    if (place_pairs(ent, ent.size(), bits, out)) {
+      if (entries) *entries = std::move(ent);
+      return true;
+    }
+  }
+  return false;
+}
+
+// The hot-pair table: the rules of the lowest ranks, as many as the
+// HOT_BITS buckets take; hot_k is one past the highest rank placed, so
+// every rule of a rank below hot_k is in it (each rule has its own rank).
+// False when not even the first rule fits.
+bool build_hot_pairs(PairEntries ent, std::vector<uint64_t>& out, uint32_t& hot_k) {
+  std::sort(ent.begin(), ent.end(),
+            [](const auto& a, const auto& b) { return a.second < b.second; });
+  size_t lo = 0, hi = std::min<size_t>(ent.size(), (size_t)2 << tk::HOT_BITS);
+  while (lo < hi) {  // the largest count that fits
+    const size_t mid = (lo + hi + 1) / 2;
+    std::vector<uint64_t> t;
+    if (place_pairs(ent, mid, tk::HOT_BITS, t)) lo = mid;
+    else hi = mid - 1;
+  }
+  if (lo == 0 || !place_pairs(ent, lo, tk::HOT_BITS, out)) return false;
+  hot_k = (uint32_t)(ent[lo - 1].second >> 18) + 1;
+  return true;
+}
+
+bool place_pairs(const PairEntries& ent, size_t n, uint32_t bits,
+                 std::vector<uint64_t>& out) {
+  {
     const uint64_t nbk = 1ULL << bits;
     out.assign(nbk * 2, ~0ULL);
     uint64_t rng = 0x2545F4914F6CDD1DULL;
     bool ok = true;
-    for (const auto& e : ent) {
+    for (size_t ei = 0; ei < n; ++ei) {
+      const auto& e = ent[ei];
       const uint64_t x = tk::pair_perm((uint32_t)(e.first >> 18),
                                        (uint32_t)(e.first & 0x3FFFF));
       // the entry being placed: tag, first bucket, rank<<18 | id, and the
@@ -162,9 +200,8 @@ bool build_compact_pairs(const uint64_t* keys, const uint64_t* vals,
       }
       if (!placed) { ok = false; break; }
     }
-    if (ok) return true;
+    return ok;
   }
-  return false;
 }
 
 // One request's device workspace: every per-call buffer, carved out of one
@@ -187,6 +224,7 @@ struct Workspace {
   uint32_t *tok = nullptr, *longlist = nullptr, *ctrl = nullptr;
   uint32_t *blkcount = nullptr, *blkprefix = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
+  uint32_t* wlist = nullptr;  // a repair pass's windows
   int32_t *nx = nullptr, *pv = nullptr;
   size_t long_pairs = 0, seg_pairs = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
@@ -225,6 +263,7 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.hlast, cap);
   take(w.hmeta, cap);
   take(w.seglist, 2 * seg_cap);
+  take(w.wlist, words);
   take(w.dirty_cur, words / 64 + 2);
   take(w.dirty_next, words / 64 + 2);
   take(w.blkcount, nblk);
@@ -254,7 +293,8 @@ struct tk_engine {
   // tables
   DevBuf<uint8_t> cls, nfc, blob;
   DevBuf<ulonglong2> pairs, vocab;
-  DevBuf<uint64_t> bytepair, ctab;
+  DevBuf<uint64_t> bytepair, ctab, hot;
+  uint32_t hot_k = 0;  // rules of rank below it are in `hot`
   DevBuf<int32_t> byte_id;
   std::vector<uint8_t> host_nfc;
   tk::DevTables t{};
@@ -418,6 +458,9 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.seglist = ws.seglist;
   w.segcount = ctrl + tk::CTRL_SEG;
   w.seg_cap = (uint32_t)ws.seg_pairs;
+  w.wlist = ws.wlist;
+  w.wcount = ctrl + tk::CTRL_WIN;
+  w.wlist_cap = (uint32_t)(ws.cap / 64 + 8);
   w.nfail = ctrl + tk::CTRL_FAIL;
   w.nfail_prev = nullptr;
   w.npass = ctrl + tk::CTRL_PASS;
@@ -607,7 +650,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
         HIP_TRY(tk::launch_apply_fail(wp, s3, tk::repair_width(p, e->repair_widen)));
-        HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s3));
+        HIP_TRY(tk::launch_repair_segments(e->t, wp, s3));
         HIP_TRY(tk::launch_certify(e->t, wp, 0, s3));
       }
       HIP_TRY(hipEventRecord(e->ev_join3, s3));
@@ -682,7 +725,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
         return fail(TK_E_INTERNAL, "certification did not converge");
       const tk::DevWork wp = pass_work(w, ctrl, p);
       HIP_TRY(tk::launch_apply_fail(wp, s, tk::repair_width(p, e->repair_widen)));
-      HIP_TRY(tk::launch_long_segments(e->t, wp, 0, s));
+      HIP_TRY(tk::launch_repair_segments(e->t, wp, s));
       HIP_TRY(tk::launch_certify(e->t, wp, 0, s));
       if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
       residual = h[(p & 1) ? tk::CTRL_FAIL2 : tk::CTRL_FAIL];
@@ -1080,6 +1123,8 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
   e->t.cert = !all_bytes ? 0 : monotone ? 1 : 2;
   e->t.all_bytes = all_bytes ? 1 : 0;
   e->t.ctab = nullptr;
+  e->t.hot = nullptr;
+  e->t.hot_k = 0;
   {
     // with the compact table every symbol the packed merge looks up (a
     // byte's id or a rule's product) is below 2^18
@@ -1087,11 +1132,19 @@ int tk_engine_open(const tk_config* cfg, const uint8_t* class_table,
     for (int b = 0; b < 256; ++b) small_ids = small_ids && byte_id[b] < (1 << 18);
     std::vector<uint64_t> ct;
     uint32_t bits = 0;
-    if (small_ids && build_compact_pairs(pair_keys, pair_vals, n_pairs, ct, bits)) {
+    PairEntries ent;
+    if (small_ids && build_compact_pairs(pair_keys, pair_vals, n_pairs, ct, bits, &ent)) {
       if ((rc = up(e->ctab, ct.data(), ct.size())) != TK_OK) return bail(rc);
       e->t.ctab = e->ctab.p;
       e->t.cmask = (1ULL << bits) - 1;
       e->t.cbits = bits;
+      // the hot pairs (probed only with TK_OPT_HOT_PAIRS)
+      std::vector<uint64_t> ht;
+      uint32_t hk = 0;
+      if (build_hot_pairs(std::move(ent), ht, hk)) {
+        if ((rc = up(e->hot, ht.data(), ht.size())) != TK_OK) return bail(rc);
+        e->hot_k = hk;
+      }
     }
   }
   e->t.unsafe = nullptr;
@@ -1280,6 +1333,13 @@ int tk_engine_set_option(tk_engine* e, int option, int64_t value) {
     if (value != 0 && value != 1)
       return fail(TK_E_INVALID_ARG, "TK_OPT_COMPACT_PAIRS takes 0 or 1");
     e->t.ctab = value && e->ctab.p ? e->ctab.p : nullptr;
+    return TK_OK;
+  }
+  if (option == TK_OPT_HOT_PAIRS) {
+    if (value != 0 && value != 1)
+      return fail(TK_E_INVALID_ARG, "TK_OPT_HOT_PAIRS takes 0 or 1");
+    e->t.hot = value && e->hot.p ? e->hot.p : nullptr;
+    e->t.hot_k = e->hot_k;
     return TK_OK;
   }
   if (option == TK_OPT_TIMED_KERNEL) {
