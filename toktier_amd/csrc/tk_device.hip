@@ -3503,7 +3503,6 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
   extern __shared__ __align__(16) uint32_t unsafe_lds[];
   uint32_t n = *w.longcount;
   if (n > w.long_cap) n = w.long_cap;
-  if (blockIdx.x * 4 >= n) return;
   const bool lds = t.unsafe && t.unsafe_words <= ROWS_UNSAFE_LDS;
   if (lds)
     for (uint32_t j = threadIdx.x; j < t.unsafe_words; j += 256)
@@ -3515,19 +3514,37 @@ __global__ __launch_bounds__(256) void k_bpe_rows(DevTables t, DevWork w) {
     hot_stage(t, hot);
   }
   if (lds || hot) __syncthreads();
-  const int wv = wave_id();
-  const uint32_t waves = gridDim.x * 4;
-  // (no issue priority: these pieces end well before the cut / segment /
-  // certify chain of the long pieces, whose kernels take it)
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  // (no issue priority: the cut / segment / certify chain of the long
+  // pieces takes it)
   // (pieces of 65..128 bytes too when k_bpe_pack left them: more than
   // PACK_ROWS_MAX queued)
   const int lo = n > (uint32_t)PACK_ROWS_MAX ? 64 : 128;
-  for (uint32_t k = blockIdx.x * 4 + wv; k < n; k += waves) {
+  // The queue in X contiguous shares (X = PACK_XCDS, or the blocks when
+  // fewer), share x to the blocks of residue x (the blocks go to the XCDs
+  // in turn). Wave g of a share's G waves takes entry g first, every later
+  // one from the share's counter (G plus the count so far; the counters
+  // start at 0 in each call's control slot), one at a time as waves finish
+  // theirs: the waves end together instead of each on a fixed share whose
+  // pieces' lengths it happened to draw.
+  const uint32_t X = gridDim.x < (uint32_t)PACK_XCDS ? gridDim.x : (uint32_t)PACK_XCDS;
+  const uint32_t x = blockIdx.x % X;
+  const uint32_t k0 = (uint32_t)((uint64_t)n * x / X);
+  const uint32_t k1 = (uint32_t)((uint64_t)n * (x + 1) / X);
+  const uint32_t G = (gridDim.x - x + X - 1) / X * 4;
+  uint32_t k = k0 + blockIdx.x / X * 4 + wv;
+  while (k < k1) {
     const uint32_t a = w.longlist[2 * k], b = w.longlist[2 * k + 1];
     const int len = (int)(b - a);
-    if (len <= lo || len > 256) continue;  // wave-uniform
-    if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
-    else wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
+    if (len > lo && len <= 256) {  // wave-uniform
+      if (len <= 128) wave_bpe_rows<2>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
+      else wave_bpe_rows<4>(t, w, a, len, true, lds ? unsafe_lds : nullptr, hot);
+    }
+    uint32_t got = 0;
+    if (lane == 0)
+      got = __hip_atomic_fetch_add(w.rowq + x, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    k = k0 + G + (uint32_t)__builtin_amdgcn_readfirstlane((int)got);
   }
 }
 

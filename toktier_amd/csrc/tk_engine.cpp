@@ -472,6 +472,7 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.prepdone = ctrl + tk::CTRL_PREP;
   w.nwide = ctrl + tk::CTRL_WIDE;
   w.nrows = ctrl + tk::CTRL_ROWS;
+  w.rowq = ctrl + tk::CTRL_ROWQ;
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.wait_ticks = e->wait_ticks;
