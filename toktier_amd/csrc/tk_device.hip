@@ -4056,7 +4056,7 @@ hipError_t launch_apply_fail(const DevWork& w, hipStream_t s, uint32_t width) {
 // ------------------------------------------------------ 4. compaction
 
 // One pass over the token slots: every block counts the ids in its
-// COMPACT_BLOCK slots (COMPACT_PER_THREAD consecutive slots per thread) and
+// COMPACT_BLOCK slots (a wave per quarter, 64 consecutive slots a step) and
 // stages them in LDS, publishes the count, takes its offset from its
 // predecessors' words (decoupled look-back: the nearest predecessor that has
 // published a running total, plus the counts in between, 64 * COMPACT_LOOK
@@ -4081,34 +4081,45 @@ __device__ __forceinline__ uint64_t cst_load(const uint64_t* p) {
 __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk,
                                                          uint32_t tag) {
   __shared__ uint32_t sbase;
-  __shared__ uint32_t sout[COMPACT_BLOCK];  // the block's ids, in order
+  // the block's ids: wave g's, in position order, from sout[g * CW]
+  constexpr int CW = COMPACT_BLOCK / (COMPACT_TPB / 64);
+  __shared__ uint32_t sout[COMPACT_BLOCK];
+  __shared__ uint32_t wcnt[COMPACT_TPB / 64];
   const int tid = threadIdx.x, lane = tid & 63, wv = wave_id();
   const int64_t b = blockIdx.x;
-  const int64_t p0 = b * COMPACT_BLOCK + (int64_t)tid * COMPACT_PER_THREAD;
-  uint32_t v[COMPACT_PER_THREAD];
-  if (p0 + COMPACT_PER_THREAD <= w.nb) {
-    const uint4* src = reinterpret_cast<const uint4*>(w.tok + p0);
+  // Wave g compacts the block's g-th CW positions, 64 a step (lane l reads
+  // position 64k + l): the step's ids go to the next consecutive LDS words
+  // at the ballot's prefix (neighbouring lanes, neighbouring banks).
+  {
+    const int64_t p0 = b * COMPACT_BLOCK + (int64_t)wv * CW + lane;
+    const uint64_t below = (1ULL << lane) - 1;
+    // every load first (one memory round trip), then the ballots
+    uint32_t v[CW / 64];
+    if (p0 - lane + CW <= w.nb) {  // wave-uniform: the whole quarter is text
 #pragma unroll
-    for (int q = 0; q < COMPACT_PER_THREAD / 4; ++q) {
-      const uint4 x = src[q];
-      v[4 * q] = x.x;
-      v[4 * q + 1] = x.y;
-      v[4 * q + 2] = x.z;
-      v[4 * q + 3] = x.w;
+      for (int k = 0; k < CW / 64; ++k) v[k] = w.tok[p0 + 64 * k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < CW / 64; ++k)
+        v[k] = p0 + 64 * k < w.nb ? w.tok[p0 + 64 * k] : INVALID_ID;
     }
-  } else {
+    uint32_t run = 0;
 #pragma unroll
-    for (int k = 0; k < COMPACT_PER_THREAD; ++k)
-      v[k] = p0 + k < w.nb ? w.tok[p0 + k] : INVALID_ID;
+    for (int k = 0; k < CW / 64; ++k) {
+      const uint64_t m = __ballot(v[k] != INVALID_ID);
+      if (v[k] != INVALID_ID) sout[wv * CW + run + (uint32_t)__popcll(m & below)] = v[k];
+      run += (uint32_t)__popcll(m);
+    }
+    if (lane == 0) wcnt[wv] = run;
   }
-  uint32_t c = 0;
+  __syncthreads();
+  uint32_t pre[COMPACT_TPB / 64];  // the ids of the waves before each wave
+  uint32_t tot = 0;
 #pragma unroll
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k) c += v[k] != INVALID_ID;
-  uint32_t tot;
-  uint32_t off = block_excl_scan(c, &tot);
-#pragma unroll
-  for (int k = 0; k < COMPACT_PER_THREAD; ++k)
-    if (v[k] != INVALID_ID) sout[off++] = v[k];
+  for (int g = 0; g < COMPACT_TPB / 64; ++g) {
+    pre[g] = tot;
+    tot += wcnt[g];
+  }
   if (wv == 0) {
     const uint64_t hi = (uint64_t)tag << 32;
     uint32_t base = 0;
@@ -4176,10 +4187,15 @@ __global__ __launch_bounds__(COMPACT_TPB) void k_compact(DevWork w, int64_t nblk
     }
   }
   __syncthreads();
-  // contiguous stores of the staged ids
+  // contiguous stores of the staged ids (id j of the block is wave g's
+  // j - pre[g]-th, g the last wave with pre[g] <= j)
   const uint32_t base = sbase;
-  for (uint32_t j = tid; j < tot; j += COMPACT_TPB)
-    if (base + j < w.out_cap) w.out[base + j] = sout[j];
+  for (uint32_t j = tid; j < tot; j += COMPACT_TPB) {
+    int g = 0;
+#pragma unroll
+    for (int q = 1; q < COMPACT_TPB / 64; ++q) g += j >= pre[q];
+    if (base + j < w.out_cap) w.out[base + j] = sout[g * CW + (j - pre[g])];
+  }
   if (b == nblk - 1 && tid == 0) {
     const uint32_t total = base + tot;
     w.blkprefix[nblk] = total;
