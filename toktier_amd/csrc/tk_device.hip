@@ -3652,42 +3652,34 @@ __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
   }
 }
 
-// A repair pass's work list, one thread per word of the dirty bitmap (64
-// text words): every window k_long_segments would redo (v dirty: both
-// phases; v - 1 dirty alone: phase 1), as v << 1 | (phase 0 too), and every
-// segment it would list (the segment that starts in a dirty word at its
-// last start, runs past the word and fits no grid window). Run after
-// k_apply_fail, so the cuts are final for the pass.
+// A repair pass's work list, one thread per text word d: when d is dirty,
+// every window k_long_segments would redo for it (v = d: both phases; v =
+// d + 1 when that word is not dirty itself: phase 1), as v << 1 | (phase 0
+// too), and the segment it would list (the segment that starts at d's last
+// start, runs past d and fits no grid window). Run after k_apply_fail, so
+// the cuts are final for the pass. (One thread per 64 words walked a
+// pass's thousands of dirty words 64 at a time: 34 us on C5's first pass.)
 __global__ void k_seg_scan(DevWork w, int64_t nwin) {
-  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (q > nwin / 64 || !pass_live(w)) return;
-  uint64_t D = w.dirty_cur[q];
-  if (!D) return;
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d > nwin || !pass_live(w)) return;
+  if (!word_dirty(w.dirty_cur, d)) return;
   auto seg = [&](int64_t wd) { return seg_word(w, wd); };
-  const uint64_t Dn = w.dirty_cur[q + 1];
-  while (D) {
-    const int j = __builtin_ctzll(D);
-    D &= D - 1;
-    const int64_t d = 64 * q + j;
-    if (d > nwin) break;
-    auto put = [&](uint32_t item) {
-      const uint32_t k = atomicAdd(w.wcount, 1u);
-      if (k < w.wlist_cap) w.wlist[k] = item;
-      else atomicOr(w.status, ST_LONGOVF);
-    };
-    put(((uint32_t)d << 1) | (d < nwin ? 1u : 0u));
-    const bool next_dirty = j < 63 ? ((D >> (j + 1)) & 1) != 0 : (Dn & 1) != 0;
-    if (d + 1 <= nwin && !next_dirty) put((uint32_t)(d + 1) << 1);
-    if (d < nwin) {
-      const uint64_t S = seg(d);
-      if (S) {
-        const int st = 63 - __builtin_clzll(S);  // the word's last start
-        if (((w.inlong[d] >> st) & 1) && !(seg(d + 1) & 1)) {
-          const int64_t a = 64 * d + st;
-          const int64_t b = seg_end_after(d + 1, seg);
-          if (!fits_a_grid(a, b))
-            push_pair(w.seglist, w.segcount, w.seg_cap, w.status, a, b);
-        }
+  auto put = [&](uint32_t item) {
+    const uint32_t k = atomicAdd(w.wcount, 1u);
+    if (k < w.wlist_cap) w.wlist[k] = item;
+    else atomicOr(w.status, ST_LONGOVF);
+  };
+  put(((uint32_t)d << 1) | (d < nwin ? 1u : 0u));
+  if (d + 1 <= nwin && !word_dirty(w.dirty_cur, d + 1)) put((uint32_t)(d + 1) << 1);
+  if (d < nwin) {
+    const uint64_t S = seg(d);
+    if (S) {
+      const int st = 63 - __builtin_clzll(S);  // the word's last start
+      if (((w.inlong[d] >> st) & 1) && !(seg(d + 1) & 1)) {
+        const int64_t a = 64 * d + st;
+        const int64_t b = seg_end_after(d + 1, seg);
+        if (!fits_a_grid(a, b))
+          push_pair(w.seglist, w.segcount, w.seg_cap, w.status, a, b);
       }
     }
   }
@@ -4019,7 +4011,7 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
 constexpr uint32_t REPAIR_BLOCKS = 512;
 hipError_t launch_repair_segments(const DevTables& t, const DevWork& w, hipStream_t s) {
   const int64_t nwin = (w.nb + 63) / 64;
-  hipLaunchKernelGGL(k_seg_scan, dim3((uint32_t)((nwin / 64 + 1 + 255) / 256)), dim3(256),
+  hipLaunchKernelGGL(k_seg_scan, dim3((uint32_t)((nwin + 1 + 255) / 256)), dim3(256),
                      0, s, w, nwin);
   hipLaunchKernelGGL(k_repair_merge, dim3(REPAIR_BLOCKS), dim3(256), 0, s, t, w, nwin);
   hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
