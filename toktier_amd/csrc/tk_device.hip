@@ -1427,50 +1427,61 @@ __global__ __launch_bounds__(PRETOK_TPB) __attribute__((amdgpu_waves_per_eu(7, 7
       }
     }
     __syncthreads();
-    if (tid == 0) {
-      // N characters after the last break of word k (a document start that
-      // is an N character opens the run and counts)
-      auto after_break = [&](int k) {
-        const uint64_t b = gBR[k], n = gNL[k];
-        const int h = 63 - __builtin_clzll(b);
-        return (uint32_t)__popcll(n & ~mask_le(h)) + (uint32_t)((n >> h) & 1);
-      };
-      uint32_t run = 0;
-      int fb = PT_TILE / 64;  // the tile's first word with a break
-      for (int k = 1; k <= PT_TILE / 64; ++k) {
-        if (gBR[k]) {
-          run = after_break(k);
-          if (fb == PT_TILE / 64) fb = k - 1;
-        } else {
-          run += (uint32_t)__popcll(gNL[k]);
-        }
-        gC[k] = run;
+    if (wv == 0) {
+      // Wave 0, lane k for tile word k (1 .. TW): the N characters of the
+      // run at the word's end, as a segmented prefix sum (a word with a
+      // break restarts the run at its last break; a document start that is
+      // an N character opens the run and counts).
+      constexpr int TW = PT_TILE / 64;
+      static_assert(TW < 64, "a lane per tile word");
+      const bool act = lane >= 1 && lane <= TW;
+      const uint64_t bw = act ? gBR[lane] : 0, nw = act ? gNL[lane] : 0;
+      uint32_t ab = 0;  // N characters after the word's last break
+      if (bw) {
+        const int h = 63 - __builtin_clzll(bw);
+        ab = (uint32_t)__popcll(nw & ~mask_le(h)) + (uint32_t)((nw >> h) & 1);
       }
-      if (w.nrun)
-        nrun_store(&w.nrun[blockIdx.x], ((uint64_t)w.seq << 32) |
-                                            (fb == PT_TILE / 64 ? NRUN_FULL : 0) | run);
+      const uint32_t P = wave_incl_scan((uint32_t)__popcll(nw), lane);
+      const uint64_t bm = __ballot(bw != 0);
+      const uint64_t le = bm & mask_le(lane);
+      const int lb = le ? 63 - __builtin_clzll(le) : 0;  // the last word with a break
+      const uint32_t abl = (uint32_t)__shfl((int)ab, lb);
+      const uint32_t Pl = (uint32_t)__shfl((int)P, lb);
+      const uint32_t run = le ? abl + (P - Pl) : P;
+      if (act) gC[lane] = run;
+      // the tile's first word with a break, less one (TW: none)
+      const int fb = bm ? __builtin_ctzll(bm) - 1 : TW;
+      const uint32_t run_end = (uint32_t)__builtin_amdgcn_readlane((int)run, TW);
       uint32_t c0 = 0;
-      if (gBR[0]) {
-        c0 = after_break(0);
-      } else if (gNL[0] && w.nrun) {
-        // the run reaches back past the halo: the tiles before it
-        WaitBound wb;
-        for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0; --u) {
-          uint64_t v;
-          while ((uint32_t)((v = nrun_load(&w.nrun[u])) >> 32) != w.seq) {
-            if (wb.expired(w.wait_ticks)) break;
-            __builtin_amdgcn_s_sleep(2);
+      if (lane == 0) {
+        if (w.nrun)
+          nrun_store(&w.nrun[blockIdx.x], ((uint64_t)w.seq << 32) |
+                                              (fb == TW ? NRUN_FULL : 0) | run_end);
+        if (gBR[0]) {
+          const uint64_t b0 = gBR[0], n0 = gNL[0];
+          const int h = 63 - __builtin_clzll(b0);
+          c0 = (uint32_t)__popcll(n0 & ~mask_le(h)) + (uint32_t)((n0 >> h) & 1);
+        } else if (gNL[0] && w.nrun) {
+          // the run reaches back past the halo: the tiles before it
+          WaitBound wb;
+          for (int64_t u = (int64_t)blockIdx.x - 1; u >= 0; --u) {
+            uint64_t v;
+            while ((uint32_t)((v = nrun_load(&w.nrun[u])) >> 32) != w.seq) {
+              if (wb.expired(w.wait_ticks)) break;
+              __builtin_amdgcn_s_sleep(2);
+            }
+            if ((uint32_t)(v >> 32) != w.seq) {
+              st |= ST_STALL_PRETOK;
+              break;
+            }
+            c0 += (uint32_t)(v & (NRUN_FULL - 1));
+            if (!(v & NRUN_FULL)) break;
           }
-          if ((uint32_t)(v >> 32) != w.seq) {
-            st |= ST_STALL_PRETOK;
-            break;
-          }
-          c0 += (uint32_t)(v & (NRUN_FULL - 1));
-          if (!(v & NRUN_FULL)) break;
         }
+        gC[0] = c0;
       }
-      gC[0] = c0;
-      for (int k = 1; k <= fb; ++k) gC[k] += c0;
+      c0 = (uint32_t)__shfl((int)c0, 0);
+      if (act && lane <= fb) gC[lane] = run + c0;
     }
     __syncthreads();
   }
