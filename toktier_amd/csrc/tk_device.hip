@@ -3312,6 +3312,43 @@ __device__ __forceinline__ uint32_t wave_min_dpp(uint32_t v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
+// 64R-bit masks over a piece's positions, word r holding positions 64r ..
+// 64r + 63 (wave-uniform, on the scalar unit). next_live_mask: for each
+// bit q of `from`, the first live position after q, found as wave_bpe does
+// on one word: a carry entered above q runs over the dead positions and
+// stops on the first live one, (~live + (from << 1)) & live, with the
+// carry passed from word to word. prev_live_mask: the last live position
+// before each, the same on the bit-reversed masks.
+template <int R>
+__device__ __forceinline__ void next_live_mask(const uint64_t* live,
+                                               const uint64_t* from,
+                                               uint64_t* out) {
+  unsigned long long c = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint64_t sh = (from[r] << 1) | (r ? from[r - 1] >> 63 : 0);
+    unsigned long long co;
+    const uint64_t s = __builtin_addcll(~live[r], sh, c, &co);
+    out[r] = s & live[r];
+    c = co;
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void prev_live_mask(const uint64_t* live,
+                                               const uint64_t* from,
+                                               uint64_t* out) {
+  uint64_t rl[R], rf[R], ro[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rl[r] = __brevll(live[R - 1 - r]);
+    rf[r] = __brevll(from[R - 1 - r]);
+  }
+  next_live_mask<R>(rl, rf, ro);
+#pragma unroll
+  for (int r = 0; r < R; ++r) out[r] = __brevll(ro[R - 1 - r]);
+}
+
 // One piece of 65..64R bytes merged by one wave with its state in registers:
 // position p = 64r + lane sits in row r (symbol, pair rank and product per
 // row and lane; live masks per row). Same order as wave_bpe_wide: each round
@@ -3354,7 +3391,7 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
     mid[r] = 0;
   }
   const uint64_t above = ~mask_le(lane);
-  // next / previous live position of position q (scalar), -1 when none
+  // next live position after position q (scalar), -1 when none
   auto next_live = [&](int q) {
     int res = -1;
 #pragma unroll
@@ -3363,17 +3400,6 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
       if (r == (q >> 6)) m &= ~mask_le(q & 63);
       else if (r < (q >> 6)) m = 0;
       if (m) res = 64 * r + __builtin_ctzll(m);
-    }
-    return res;
-  };
-  auto prev_live = [&](int q) {
-    int res = -1;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      uint64_t m = live[r];
-      if (r == (q >> 6)) m &= (1ULL << (q & 63)) - 1;
-      else if (r > (q >> 6)) m = 0;
-      if (m) res = 64 * r + 63 - __builtin_clzll(m);
     }
     return res;
   };
@@ -3433,44 +3459,60 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
     const uint32_t best = wave_min_dpp(m);
     if (best == RANK_INF) break;
     const uint32_t rank = best >> 9;
-    // the merges of this round, as bits r of the lane holding position
-    // 64r + lane: winners, the positions they absorb, the positions whose
-    // pair changes
-    uint32_t wbit = 0, gbit = 0, dbit = 0;
-    auto set = [&](uint32_t& bits, int q) {
-      if (q >= 0 && lane == (q & 63)) bits |= 1u << (q >> 6);
-    };
-    auto take = [&](int q) {
-      const int g = next_live(q);
-      set(wbit, q);
-      set(gbit, g);
-      set(dbit, q);
-      set(dbit, prev_live(q));
-      return g;
-    };
     const bool unsafe =
         unsafe_lds ? ((rank >> 5) < t.unsafe_words &&
                       ((unsafe_lds[rank >> 5] >> (rank & 31)) & 1))
                    : rank_unsafe(t, rank);
+    // The round's merges as 64R-bit masks over the positions (word r: row
+    // r): the pairs of this rank (occ), the winners (win), the positions
+    // they absorb (gone: each winner's next live position) and the live
+    // positions before them (prev), whose right neighbour changes.
+    uint64_t occ[R], win[R], gone[R], prev[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      occ[r] = __builtin_amdgcn_ballot_w64(lane_bit(live[r]) && rk[r] == rank);
     if (unsafe) {
-      take((int)(best & 511));
-    } else {
-      int blocked = -1;
+      // an unsafe rank merges its leftmost pair alone
+      bool found = false;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        uint64_t o = __builtin_amdgcn_ballot_w64(lane_bit(live[r]) && rk[r] == rank);
-        while (o) {  // wave-uniform, positions in order
-          const int q = 64 * r + __builtin_ctzll(o);
-          o &= o - 1;
-          if (q != blocked) blocked = take(q);
+        win[r] = found ? 0 : occ[r] & (~occ[r] + 1);
+        found = found || occ[r];
+      }
+    } else {
+      // every pair of the rank, unless one's right symbol is the next
+      // one's left: then leftmost first, each blocking the next
+      next_live_mask<R>(live, occ, gone);
+      uint64_t clash = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) clash |= gone[r] & occ[r];
+      if (!clash) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) win[r] = occ[r];
+      } else {
+        int blocked = -1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          win[r] = 0;
+          uint64_t o = occ[r];
+          while (o) {  // wave-uniform, positions in order
+            const int q = 64 * r + __builtin_ctzll(o);
+            o &= o - 1;
+            if (q != blocked) {
+              win[r] |= 1ULL << (q & 63);
+              blocked = next_live(q);
+            }
+          }
         }
       }
     }
+    next_live_mask<R>(live, win, gone);
+    prev_live_mask<R>(live, win, prev);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if ((wbit >> r) & 1) sym[r] = mid[r];
-      live[r] &= ~__builtin_amdgcn_ballot_w64((gbit >> r) & 1);
-      dirty[r] = __builtin_amdgcn_ballot_w64((dbit >> r) & 1) & live[r];
+      if (lane_bit(win[r])) sym[r] = mid[r];
+      live[r] &= ~gone[r];
+      dirty[r] = (win[r] | prev[r]) & live[r];
     }
   }
 #pragma unroll
