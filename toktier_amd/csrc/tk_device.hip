@@ -981,7 +981,7 @@ __device__ __forceinline__ O2Fn<W> o2_then(const O2Fn<W>& a, const O2Fn<W>& b) {
 template <int RS>
 __device__ __forceinline__ bool o2_const(const O2Fn<o2_words<RS>()>& f) {
   const uint32_t r = (f.d[0] & 0xFFu) * 0x01010101u;
-  if (RS == RS_KIMI)
+  if constexpr (RS == RS_KIMI)
     return f.d[0] == r && f.d[1] == r && ((f.d[2] ^ r) & 0x00FFFFFFu) == 0;
   return f.d[0] == r && f.d[1] == r;
 }
