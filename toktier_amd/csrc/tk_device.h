@@ -148,6 +148,8 @@ struct DevWork {
   uint32_t* nbig;        // queued pieces over WIDE_MAX bytes (ctrl)
   uint32_t* nrows;       // queued pieces of 129..256 bytes (ctrl)
   uint32_t* rowq;        // k_bpe_rows' piece counters, one per XCD (ctrl)
+  uint32_t* vlist;       // the grid windows with long-piece bytes (k_win_list)
+  uint32_t* vcount;      // their number (ctrl)
   uint32_t* nwide;       // queued pieces of 257..WIDE_MAX bytes (ctrl)
   uint32_t* prepdone;    // k_bpe_pack waves done with the long pieces (ctrl)
   uint32_t* gate;        // GATE_WORDS in host memory, or nullptr
@@ -188,6 +190,7 @@ constexpr int CTRL_STATUS = 0, CTRL_TOTAL = 1, CTRL_LONG = 2, CTRL_SEG = 3,
               CTRL_FAIL = 4, CTRL_BIG = 5, CTRL_NLIT = 6, CTRL_PASS = 7,
               CTRL_FAIL2 = 8, CTRL_PREP = 9, CTRL_WIDE = 10, CTRL_ROWS = 11,
               CTRL_WIN = 12, CTRL_ROWQ = 16,  // (ROWQ: PACK_XCDS words)
+              CTRL_VLIST = 24,
               CTRL_PSEG = 64, CTRL_PSEG_STRIDE = 64,
               CTRL_PSEG_COUNT = 32, CTRL_WORDS = CTRL_PSEG + 8 * CTRL_PSEG_STRIDE;
 // gate words in host memory: k_bpe_pack writes GATE_NLONG / GATE_NROWS /
@@ -242,7 +245,8 @@ constexpr int PACK_ROWS_MAX = 8192;
 constexpr int PACK_XCDS = 8;
 static_assert(CTRL_WORDS == CTRL_PSEG + PACK_XCDS * CTRL_PSEG_STRIDE,
               "one control line per segment");
-static_assert(CTRL_ROWQ + PACK_XCDS <= CTRL_PSEG, "row counters before the segment lines");
+static_assert(CTRL_ROWQ + PACK_XCDS <= CTRL_VLIST, "row counters before the window list's");
+static_assert(CTRL_VLIST < CTRL_PSEG, "the window count before the segment lines");
 // slots (lanes per piece) of the length classes, and the shortest piece of
 // each class: class c holds pieces of pack_lmin(c)..pack_slot(c) bytes
 __host__ __device__ constexpr int pack_slot(int c) {
@@ -327,8 +331,7 @@ hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s, hipEvent_t start = nullptr,
                                hipEvent_t stop = nullptr);
-hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
-                                int all, hipStream_t s);
+hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_t s);
 // pieces over WIDE_MAX bytes merged whole, a workgroup each (tables that
 // drop bytes: no cut certification)
 hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s);

@@ -3608,18 +3608,33 @@ __device__ __forceinline__ uint64_t inlong_window(const DevWork& w, int64_t v,
   return (lo >> 32) | (w.inlong[v] << 32);
 }
 
-// Cut selection: BPE of the long-piece bytes of every window, window edges
-// taken as cuts; the token starts in the window's central 32 bytes become
-// candidate cuts. Aligned window v owns bits 16..47 of word v, shifted
-// window v owns bits 48..63 of word v-1 and 0..15 of word v.
-__global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
-                                                      int64_t nwin) {
+// The grid windows that hold long-piece bytes (v in 0..nwin with a phase
+// whose inlong_window is not empty), listed once each in vlist (vcount of
+// them), in no particular order. The window, segment and certify kernels
+// keep a wave per window of the text, but wave i takes listed window i:
+// the waves with work are the grid's first (on C5 ten runs fill ~20,000 of
+// ~150,000 windows, spread through the text, and the waves for them came
+// between the empty ones), and the rest end at once. (A fixed grid of
+// 1024 or 2048 blocks walking the list from a counter was slower: C5
+// 1.92 / 2.01 ms against 1.82; this order: 1.73.)
+__global__ void k_win_list(DevWork w, int64_t nwin) {
+  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  bool need = false;
+  if (v <= nwin)
+    for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase)
+      need = need || inlong_window(w, v, phase) != 0;
+  const uint64_t m = __ballot(need);
+  if (!m) return;
   const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
-  if (v > nwin) return;
-  // the long pieces' chain (windows, segments, certification, repairs)
-  // sets the end of a request that has any: issue priority
-  __builtin_amdgcn_s_setprio(2);
+  uint32_t base = 0;
+  if (lane == 0) base = atomicAdd(w.vcount, (uint32_t)__popcll(m));
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+  if (need) w.vlist[base + (uint32_t)__popcll(m & ((1ULL << lane) - 1))] = (uint32_t)v;
+}
+
+__device__ __forceinline__ void long_window(const DevTables& t, const DevWork& w,
+                                            int64_t v, int64_t nwin) {
+  const int lane = threadIdx.x & 63;
   auto seg = [&](int64_t wd) { return w.starts[wd]; };
   uint16_t* cut16 = reinterpret_cast<uint16_t*>(w.cuts);
   for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
@@ -3647,6 +3662,21 @@ __global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
       }
     }
   }
+}
+
+// Cut selection: BPE of the long-piece bytes of every window, window edges
+// taken as cuts; the token starts in the window's central 32 bytes become
+// candidate cuts. Aligned window v owns bits 16..47 of word v, shifted
+// window v owns bits 48..63 of word v-1 and 0..15 of word v. Wave i takes
+// listed window i.
+__global__ __launch_bounds__(256) void k_long_windows(DevTables t, DevWork w,
+                                                      int64_t nwin) {
+  const uint32_t i = blockIdx.x * 4 + wave_id();
+  if (i >= *w.vcount) return;
+  // the long pieces' chain (windows, segments, certification, repairs)
+  // sets the end of a request that has any: issue priority
+  __builtin_amdgcn_s_setprio(2);
+  long_window(t, w, w.vlist[i], nwin);
 }
 
 __device__ __forceinline__ uint64_t seg_word(const DevWork& w, int64_t wd) {
@@ -3690,19 +3720,18 @@ __device__ __forceinline__ void segment_window(const DevTables& t, const DevWork
 }
 
 // Segment pass over the long-piece bytes (64-byte grid windows, aligned and
-// shifted by 32, with histories). Segments that fit no grid window go to
-// seglist. With all == 0 only windows touching a dirty word are redone.
+// shifted by 32, with histories), wave i over listed window i. Segments
+// that fit no grid window go to seglist. (The
+// repair passes redo only the windows of dirty words: k_seg_scan,
+// k_repair_merge.)
 __global__ __launch_bounds__(256) void k_long_segments(DevTables t, DevWork w,
-                                                       int64_t nwin, int all) {
-  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
-  if (v > nwin || !pass_live(w)) return;
+                                                       int64_t nwin) {
+  const uint32_t i = blockIdx.x * 4 + wave_id();
+  if (i >= *w.vcount || !pass_live(w)) return;
   __builtin_amdgcn_s_setprio(2);  // (the long pieces' chain: k_long_windows)
-  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase) {
-    if (!all && !word_dirty(w.dirty_cur, v) &&
-        !(phase == 1 && word_dirty(w.dirty_cur, v - 1)))
-      continue;
+  const int64_t v = w.vlist[i];
+  for (int phase = (v == nwin ? 1 : 0); phase < 2; ++phase)
     segment_window(t, w, v, phase, true);
-  }
 }
 
 // A repair pass's work list, one thread per text word d: when d is dirty,
@@ -3812,15 +3841,8 @@ __device__ __forceinline__ uint32_t pair_rank(const DevTables& t, uint32_t l,
   return pair_find(t, l, r, &rank, &id) ? rank : RANK_INF;
 }
 
-__global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
-                                                 int64_t nwords, int all) {
-  const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + wave_id();
-  if (v >= nwords || !pass_live(w)) return;
-  if (!all && !word_dirty(w.dirty_cur, v)) return;  // wave-uniform
-  const uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
-  if (!((cuts >> lane) & 1)) return;
-  const int bit = lane;
+// One cut c = 64v + bit (the calling lane's).
+__device__ void certify_cut(const DevTables& t, const DevWork& w, int64_t v, int bit) {
   const int64_t c = v * 64 + bit;
   // start of the segment that ends at c
   int64_t wd = v;
@@ -3889,6 +3911,22 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
       atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
                1ULL << (q & 63));
   }
+}
+
+// Certify the cuts of the listed windows' words (a word holds cuts only
+// where it holds long-piece bytes, so every such word is listed): wave i
+// over listed word i (in a repair pass only the dirty words).
+__global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
+                                                 int64_t nwords, int all) {
+  const int lane = threadIdx.x & 63;
+  if (!pass_live(w)) return;
+  const uint32_t i = blockIdx.x * 4 + wave_id();
+  if (i >= *w.vcount) return;
+  const int64_t v = w.vlist[i];
+  if (v >= nwords) return;
+  if (!all && !word_dirty(w.dirty_cur, v)) return;  // wave-uniform
+  const uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
+  if ((cuts >> lane) & 1) certify_cut(t, w, v, lane);
 }
 
 // Between passes: drop the failed cuts, and make the words marked by the
@@ -4039,16 +4077,17 @@ hipError_t launch_bpe_wide(const DevTables& t, const DevWork& w, hipStream_t s,
 hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   const int64_t nwin = (w.nb + 63) / 64;
-  launch_ev(k_long_windows, dim3((uint32_t)((nwin + 4) / 4)), dim3(256), s, start,
+  launch_ev(k_win_list, dim3((uint32_t)((nwin + 1 + 255) / 256)), dim3(256), s,
+            start, nullptr, w, nwin);
+  launch_ev(k_long_windows, dim3((uint32_t)((nwin + 4) / 4)), dim3(256), s, nullptr,
             stop, t, w, nwin);
   return hipGetLastError();
 }
 
-hipError_t launch_long_segments(const DevTables& t, const DevWork& w,
-                                int all, hipStream_t s) {
+hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_t s) {
   const int64_t nwin = (w.nb + 63) / 64;
-  hipLaunchKernelGGL(k_long_segments, dim3((uint32_t)((nwin + 4) / 4)),
-                     dim3(256), 0, s, t, w, nwin, all);
+  hipLaunchKernelGGL(k_long_segments, dim3((uint32_t)((nwin + 4) / 4)), dim3(256), 0,
+                     s, t, w, nwin);
   hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
                      (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
                      w.seg_cap, 1);
@@ -4083,8 +4122,8 @@ hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s
 hipError_t launch_certify(const DevTables& t, const DevWork& w, int all,
                           hipStream_t s, hipEvent_t stop) {
   const int64_t nwords = (w.nb + 63) / 64;
-  launch_ev(k_certify, dim3((uint32_t)((nwords + 3) / 4)), dim3(256), s,
-            nullptr, stop, t, w, nwords, all);
+  launch_ev(k_certify, dim3((uint32_t)((nwords + 4) / 4)), dim3(256), s, nullptr,
+            stop, t, w, nwords, all);
   return hipGetLastError();
 }
 

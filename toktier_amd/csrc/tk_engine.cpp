@@ -225,6 +225,7 @@ struct Workspace {
   uint32_t *blkcount = nullptr, *blkprefix = nullptr;
   uint32_t *hmeta = nullptr, *seglist = nullptr, *plist = nullptr;
   uint32_t* wlist = nullptr;  // a repair pass's windows
+  uint32_t* vlist = nullptr;  // the grid windows with long-piece bytes
   int32_t *nx = nullptr, *pv = nullptr;
   size_t long_pairs = 0, seg_pairs = 0, nblk = 0, tiles = 0;
   uint32_t slot = 0;
@@ -264,6 +265,7 @@ size_t carve(Workspace& w, uint8_t* base, size_t cap) {
   take(w.hmeta, cap);
   take(w.seglist, 2 * seg_cap);
   take(w.wlist, words);
+  take(w.vlist, words);
   take(w.dirty_cur, words / 64 + 2);
   take(w.dirty_next, words / 64 + 2);
   take(w.blkcount, nblk);
@@ -473,6 +475,8 @@ tk::DevWork make_work(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   w.nwide = ctrl + tk::CTRL_WIDE;
   w.nrows = ctrl + tk::CTRL_ROWS;
   w.rowq = ctrl + tk::CTRL_ROWQ;
+  w.vlist = ws.vlist;
+  w.vcount = ctrl + tk::CTRL_VLIST;
   w.gate = e->gate_dev;
   w.seq = e->seq;
   w.wait_ticks = e->wait_ticks;
@@ -646,7 +650,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
                                     ke(TK_KERNEL_BPE_ROWS)));
         launched[TK_KERNEL_BPE_ROWS] = true;
       }
-      HIP_TRY(tk::launch_long_segments(e->t, w, 1, s3));
+      HIP_TRY(tk::launch_long_segments(e->t, w, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
