@@ -332,6 +332,8 @@ hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s, hipEvent_t start = nullptr,
                                hipEvent_t stop = nullptr);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_t s);
+// the first pass's listed segments (at most WIDE_MAX bytes each)
+hipError_t launch_seg_lists(const DevTables& t, const DevWork& w, hipStream_t s);
 // pieces over WIDE_MAX bytes merged whole, a workgroup each (tables that
 // drop bytes: no cut certification)
 hipError_t launch_long_block(const DevTables& t, const DevWork& w, hipStream_t s);

@@ -2789,26 +2789,6 @@ hipError_t launch_bpe_pack(const DevTables& t, const DevWork& w, hipStream_t s,
   return hipGetLastError();
 }
 
-// Entries of at most 64 bytes from a (start, end) list: one wave each,
-// lane = byte offset. Longer entries are left to the other stages.
-__global__ __launch_bounds__(256) void k_bpe_list(DevTables t, DevWork w,
-                                                  const uint32_t* list,
-                                                  const uint32_t* count,
-                                                  uint32_t cap, int hist) {
-  const int lane = threadIdx.x & 63;
-  if (!pass_live(w)) return;
-  uint32_t n = *count;
-  if (n > cap) n = cap;
-  const uint32_t waves = gridDim.x * 4;
-  for (uint32_t k = blockIdx.x * 4 + wave_id(); k < n; k += waves) {
-    const uint32_t a = list[2 * k], b = list[2 * k + 1];
-    const int len = (int)(b - a);
-    if (len > 64) continue;  // wave-uniform
-    if (hist) wave_bpe<false, true, true>(t, w, (int64_t)a, (int64_t)a + lane, lane, lane < len, 0, len);
-    else wave_bpe<true, false, true>(t, w, (int64_t)a, (int64_t)a + lane, lane, lane < len, 0, len);
-  }
-}
-
 // ------------------------------------------------- 3. long-piece BPE
 //
 // A piece longer than 64 bytes is cut into short segments at positions that
@@ -3687,6 +3667,48 @@ __device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
   return wd >= 0 && ((d[wd >> 6] >> (wd & 63)) & 1);
 }
 
+// A first-pass segment [a, b) over WIDE_MAX bytes (a stretch with no cut
+// candidate): instead of a workgroup merge of it on this pass (whose
+// 1024-thread blocks find no room beside the row merges until those end:
+// 200-330 us of C5's critical path), its bounding cuts are failed as
+// certification fails a cut, so the first repair pass joins it to its
+// neighbours and merges the joined segment (k_seg_scan lists it from its
+// dirty words, k_seg_block merges it). Dropping a cut is always safe: the
+// cuts that remain are certified. One lane.
+__device__ void fail_segment_cuts(const DevWork& w, int64_t a, int64_t b) {
+  auto is_cut = [&](int64_t c) {
+    const int64_t wd = c >> 6;
+    return ((w.cuts[wd] & w.inlong[wd] & ~w.starts[wd]) >> (c & 63)) & 1;
+  };
+  auto fail = [&](int64_t c) {
+    atomicOr(reinterpret_cast<unsigned long long*>(&w.failm[c >> 6]), 1ULL << (c & 63));
+    atomicAdd(w.nfail, 1u);
+  };
+  int64_t lo = a, hi = b;
+  // (a segment bounded by piece starts alone still counts one failure, so
+  // that the repair pass runs and lists it)
+  if (!is_cut(a) && !is_cut(b)) atomicAdd(w.nfail, 1u);
+  if (is_cut(a)) {
+    fail(a);
+    // start of the segment that ends at a
+    int64_t wd = a >> 6;
+    uint64_t word = seg_word(w, wd) & ((1ULL << (a & 63)) - 1);
+    while (word == 0) word = seg_word(w, --wd);
+    lo = wd * 64 + (63 - __builtin_clzll(word));
+  }
+  if (is_cut(b)) {
+    fail(b);
+    // end of the segment that starts at b
+    int64_t we = b >> 6;
+    uint64_t up = seg_word(w, we) & ~mask_le((int)(b & 63));
+    while (up == 0) up = seg_word(w, ++we);
+    hi = we * 64 + __builtin_ctzll(up);
+  }
+  for (int64_t q = lo >> 6; q <= (hi >> 6); ++q)
+    atomicOr(reinterpret_cast<unsigned long long*>(&w.dirty_next[q >> 6]),
+             1ULL << (q & 63));
+}
+
 // Segment work of one grid window (phase 0: aligned [64v, 64v+64), phase 1:
 // shifted [64v-32, 64v+32)): the BPE of the long-piece segments the window
 // holds whole, with histories. With `push`, phase 0 also lists the segment
@@ -3713,8 +3735,10 @@ __device__ __forceinline__ void segment_window(const DevTables& t, const DevWork
     elig = false;
   if (push && phase == 0 && inl && ps == lane && !contained) {
     const int64_t b = seg_end_after(v + 1, seg);
-    if (!fits_a_grid(pos, b))
-      push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
+    if (!fits_a_grid(pos, b)) {
+      if (b - pos > WIDE_MAX) fail_segment_cuts(w, pos, b);
+      else push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
+    }
   }
   wave_bpe<false, true, true>(t, w, base, base + lane, lane, elig, ps, pe);
 }
@@ -4088,19 +4112,21 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_
   const int64_t nwin = (w.nb + 63) / 64;
   hipLaunchKernelGGL(k_long_segments, dim3((uint32_t)((nwin + 4) / 4)), dim3(256), 0,
                      s, t, w, nwin);
-  hipLaunchKernelGGL(k_bpe_list, dim3(512), dim3(256), 0, s, t, w,
-                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
-                     w.seg_cap, 1);
-  hipLaunchKernelGGL(k_bpe_wide, dim3(512), dim3(256), 0, s, t, w,
-                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
-                     w.seg_cap, 1);
-  hipLaunchKernelGGL(k_seg_block, dim3(SEGB_GRID), dim3(SEGB_TPB), 0, s, t, w,
-                     (const uint32_t*)w.seglist, (const uint32_t*)w.segcount,
-                     w.seg_cap, 0);
   return hipGetLastError();
 }
 
+// The first pass's listed segments (all of at most WIDE_MAX bytes: the
+// longer ones had their cuts failed, fail_segment_cuts), both classes in
+// one launch of k_repair_merge (no windows are listed before the first
+// repair pass); one after the other, the two classes each took as long as
+// its slowest merge (on C5 up to 355 and 110 us).
 constexpr uint32_t REPAIR_BLOCKS = 512;
+hipError_t launch_seg_lists(const DevTables& t, const DevWork& w, hipStream_t s) {
+  const int64_t nwin = (w.nb + 63) / 64;
+  hipLaunchKernelGGL(k_repair_merge, dim3(REPAIR_BLOCKS), dim3(256), 0, s, t, w, nwin);
+  return hipGetLastError();
+}
+
 hipError_t launch_repair_segments(const DevTables& t, const DevWork& w, hipStream_t s) {
   const int64_t nwin = (w.nb + 63) / 64;
   hipLaunchKernelGGL(k_seg_scan, dim3((uint32_t)((nwin + 1 + 255) / 256)), dim3(256),

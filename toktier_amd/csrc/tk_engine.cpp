@@ -651,6 +651,7 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
         launched[TK_KERNEL_BPE_ROWS] = true;
       }
       HIP_TRY(tk::launch_long_segments(e->t, w, s3));
+      HIP_TRY(tk::launch_seg_lists(e->t, w, s3));
       HIP_TRY(tk::launch_certify(e->t, w, 1, s3));
       for (int p = 1; p <= DEV_REPAIRS; ++p) {
         const tk::DevWork wp = pass_work(w, ctrl, p);
