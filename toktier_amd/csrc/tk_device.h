@@ -332,7 +332,7 @@ hipError_t launch_long_windows(const DevTables& t, const DevWork& w,
                                hipStream_t s, hipEvent_t start = nullptr,
                                hipEvent_t stop = nullptr);
 hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_t s);
-// the first pass's listed segments (at most WIDE_MAX bytes each)
+// the first pass's listed segments (at most 64 bytes each)
 hipError_t launch_seg_lists(const DevTables& t, const DevWork& w, hipStream_t s);
 // pieces over WIDE_MAX bytes merged whole, a workgroup each (tables that
 // drop bytes: no cut certification)

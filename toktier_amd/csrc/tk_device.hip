@@ -3667,14 +3667,15 @@ __device__ __forceinline__ bool word_dirty(const uint64_t* d, int64_t wd) {
   return wd >= 0 && ((d[wd >> 6] >> (wd & 63)) & 1);
 }
 
-// A first-pass segment [a, b) over WIDE_MAX bytes (a stretch with no cut
-// candidate): instead of a workgroup merge of it on this pass (whose
-// 1024-thread blocks find no room beside the row merges until those end:
-// 200-330 us of C5's critical path), its bounding cuts are failed as
-// certification fails a cut, so the first repair pass joins it to its
-// neighbours and merges the joined segment (k_seg_scan lists it from its
-// dirty words, k_seg_block merges it). Dropping a cut is always safe: the
-// cuts that remain are certified. One lane.
+// A first-pass segment [a, b) over 64 bytes (a stretch with few cut
+// candidates): instead of merging it on this pass, beside the row merges,
+// with a kernel that needs LDS or 1024-thread blocks (no room for either
+// until the row merges end: 200-400 us of C5's critical path), its
+// bounding cuts are failed as certification fails a cut, so the first
+// repair pass joins it to its neighbours and merges the joined segment
+// (k_seg_scan lists it from its dirty words; k_repair_merge, k_seg_block).
+// Dropping a cut is always safe: the cuts that remain are certified. One
+// lane.
 __device__ void fail_segment_cuts(const DevWork& w, int64_t a, int64_t b) {
   auto is_cut = [&](int64_t c) {
     const int64_t wd = c >> 6;
@@ -3736,7 +3737,7 @@ __device__ __forceinline__ void segment_window(const DevTables& t, const DevWork
   if (push && phase == 0 && inl && ps == lane && !contained) {
     const int64_t b = seg_end_after(v + 1, seg);
     if (!fits_a_grid(pos, b)) {
-      if (b - pos > WIDE_MAX) fail_segment_cuts(w, pos, b);
+      if (b - pos > 64) fail_segment_cuts(w, pos, b);
       else push_pair(w.seglist, w.segcount, w.seg_cap, w.status, pos, b);
     }
   }
@@ -3788,6 +3789,30 @@ __global__ void k_seg_scan(DevWork w, int64_t nwin) {
           push_pair(w.seglist, w.segcount, w.seg_cap, w.status, a, b);
       }
     }
+  }
+}
+
+// The first pass's listed segments (each at most 64 bytes: the longer ones
+// had their cuts failed), one wave each, with histories. No LDS and few
+// registers, so its waves find room beside the row merges (whose LDS holds
+// the unsafe-rank bitmap on tables that have one).
+__global__ __launch_bounds__(256) void k_seg_short(DevTables t, DevWork w) {
+  const int lane = threadIdx.x & 63;
+  if (!pass_live(w)) return;
+  uint32_t n = *w.segcount;
+  if (n > w.seg_cap) n = w.seg_cap;
+  const uint32_t waves = gridDim.x * 4;
+  const uint32_t k0 = blockIdx.x * 4 + wave_id();
+  // (the long pieces' chain, as k_repair_merge)
+  if (k0 < n) __builtin_amdgcn_s_setprio(3);
+  for (uint32_t k = k0; k < n; k += waves) {
+    const uint32_t a = w.seglist[2 * k], b = w.seglist[2 * k + 1];
+    const int len = (int)(b - a);
+    if (len > 64) {  // (not listed on this pass; an internal error if seen)
+      if (lane == 0) atomicOr(w.status, ST_ROUNDS);
+      continue;
+    }
+    wave_bpe<false, true, true>(t, w, (int64_t)a, (int64_t)a + lane, lane, lane < len, 0, len);
   }
 }
 
@@ -4115,15 +4140,11 @@ hipError_t launch_long_segments(const DevTables& t, const DevWork& w, hipStream_
   return hipGetLastError();
 }
 
-// The first pass's listed segments (all of at most WIDE_MAX bytes: the
-// longer ones had their cuts failed, fail_segment_cuts), both classes in
-// one launch of k_repair_merge (no windows are listed before the first
-// repair pass); one after the other, the two classes each took as long as
-// its slowest merge (on C5 up to 355 and 110 us).
+// The first pass's listed segments (each at most 64 bytes: the longer ones
+// had their cuts failed, fail_segment_cuts), one wave each (k_seg_short).
 constexpr uint32_t REPAIR_BLOCKS = 512;
 hipError_t launch_seg_lists(const DevTables& t, const DevWork& w, hipStream_t s) {
-  const int64_t nwin = (w.nb + 63) / 64;
-  hipLaunchKernelGGL(k_repair_merge, dim3(REPAIR_BLOCKS), dim3(256), 0, s, t, w, nwin);
+  hipLaunchKernelGGL(k_seg_short, dim3(1024), dim3(256), 0, s, t, w);
   return hipGetLastError();
 }
 
