@@ -3975,6 +3975,9 @@ __global__ __launch_bounds__(256) void k_certify(DevTables t, DevWork w,
   if (v >= nwords) return;
   if (!all && !word_dirty(w.dirty_cur, v)) return;  // wave-uniform
   const uint64_t cuts = w.cuts[v] & w.inlong[v] & ~w.starts[v];
+  if (!cuts) return;
+  // (the long pieces' chain: the first pass runs beside the row merges)
+  __builtin_amdgcn_s_setprio(2);
   if ((cuts >> lane) & 1) certify_cut(t, w, v, lane);
 }
 
