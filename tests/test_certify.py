@@ -313,12 +313,17 @@ def window_cuts(family, ids, lens, off):
     return sorted(cuts)
 
 
-def repair(family, data, off, widen_from=None, limit=10_000):
+def repair(family, data, off, widen_from=None, limit=10_000, first_max=None,
+           stats=None):
     """The certification and its repair passes on one piece: certify every
     cut, drop the failed ones, redo the segments, until none fails (cert 1,
     a monotone table). From pass `widen_from` on, each failed cut also
     drops its 4^(p - widen_from + 1) nearest cuts on each side
-    (k_fail_widen). Returns (ids, passes)."""
+    (k_fail_widen). With `first_max`, the first pass fails both cuts around
+    every segment longer than that instead of merging it (the device's
+    first segment pass: fail_segment_cuts past 64 bytes), and a segment
+    with no cut to fail still makes the repair pass run. Returns (ids,
+    passes)."""
     rules, unsafe, byte_id = _model(family)
     lens = _lengths(family)
     ids = [byte_id[b] for b in data]
@@ -326,10 +331,24 @@ def repair(family, data, off, widen_from=None, limit=10_000):
     passes = 0
     while True:
         bounds = [0, *cuts, len(ids)]
-        segs = [merge(rules, unsafe, ids[a:b], True) for a, b in zip(bounds, bounds[1:])]
+        # (the first pass leaves a segment over first_max unmerged: its
+        # bytes, no events)
+        segs = [(list(ids[a:b]), []) if first_max and passes == 0 and b - a > first_max
+                else merge(rules, unsafe, ids[a:b], True)
+                for a, b in zip(bounds, bounds[1:])]
         failed = [k for k, c in enumerate(cuts)
                   if not walk_events(rules, ids[c - 1], ids[c], segs[k][1], segs[k + 1][1])]
-        if not failed or passes >= limit:
+        forced = False
+        if first_max and passes == 0:
+            extra = set()
+            for k, (a, b) in enumerate(zip(bounds, bounds[1:])):
+                if b - a > first_max:
+                    forced = True
+                    extra.update(j for j in (k - 1, k) if 0 <= j < len(cuts))
+            failed = sorted(set(failed) | extra)
+            if stats is not None:
+                stats["long_first"] = stats.get("long_first", 0) + int(forced)
+        if (not failed and not forced) or passes >= limit:
             return [t for s in segs for t in s[0]], passes
         passes += 1
         width = 4 ** (passes - widen_from + 1) if widen_from and passes >= widen_from else 0
@@ -385,3 +404,30 @@ def test_widened_repair_keeps_the_ids_of_ordinary_pieces():
             ids, passes = repair(family, data, off=int(rng.integers(0, 64)),
                                  widen_from=widen)
             assert ids == whole, (widen, passes)
+
+
+def test_first_pass_long_segments_left_to_the_repair_passes():
+    """The device's first segment pass fails the cuts around a segment over
+    64 bytes instead of merging it there (k_long_segments:
+    fail_segment_cuts), and the repair passes join and merge it. The ids
+    stay the whole piece's: space runs and periodic runs, where the windows
+    find few cuts and segments run past 64 bytes, C5 letter runs, and the
+    cascading "!" + "QQQ..." run."""
+    family = "qwen3_8b"
+    rules, unsafe, byte_id = _model(family)
+    from toktier_amd import standin, workloads
+    js = standin.load_artifact_json(family)
+    text = workloads.config5(js, n_chars=40_000, n_runs=2, run_chars=3_000, sample=5)
+    letters = "".join(ch for ch in text if ch.isalpha()).encode("utf-8")
+    cases = [b" " * 1500, b"ab" * 700, b"\t\n " * 400, b"!" + b"Q" * 900,
+             letters[:1200], letters[3000:4100]]
+    stats = {}
+    for data in cases:
+        while data and (data[-1] & 0xC0) == 0x80 or (data and data[-1] >= 0xC0):
+            data = data[:-1]
+        whole, _ = merge(rules, unsafe, [byte_id[b] for b in data], True)
+        for off in (0, 37):
+            ids, passes = repair(family, data, off=off, widen_from=4, first_max=64,
+                                 stats=stats)
+            assert ids == whole, (data[:8], off, passes)
+    assert stats.get("long_first", 0) > 0  # the path ran
