@@ -2558,7 +2558,7 @@ __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
 }
 
 // (defined with the long-piece merges below)
-template <int R>
+template <int R, bool H = false>
 __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
                                               const DevWork& w, uint32_t a,
                                               int len, bool vocab_first,
@@ -3336,8 +3336,10 @@ __device__ __forceinline__ void prev_live_mask(const uint64_t* live,
 // non-overlapping occurrences at once, an unsafe one its leftmost alone.
 // Per round: one wave minimum, the selection on the scalar unit, and pair
 // lookups for the positions whose pair changed (the winners and the live
-// positions before them).
-template <int R>
+// positions before them). H: the piece is a segment of a certified long
+// piece, and its merge rounds go to the histories as wave_bpe_wide writes
+// them (the repair passes' segments of 65..64R bytes).
+template <int R, bool H>
 __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
                                               const DevWork& w, uint32_t a,
                                               int len, bool vocab_first,
@@ -3359,6 +3361,7 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
   }
   uint32_t sym[R], rk[R], mid[R];
   uint64_t live[R], dirty[R];
+  uint32_t nfirst = 0, nlast = 0;  // (H) history entries written
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int p = 64 * r + lane;
@@ -3486,6 +3489,57 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
         }
       }
     }
+    if constexpr (H) {
+      // the first live position f, the last one l and the live position
+      // pl before it (the left symbol of the segment's last pair), all
+      // wave-uniform; the round takes the first / last token when it
+      // merges at f / pl
+      int f = -1, l = -1, pl = -1;
+#pragma unroll
+      for (int r = R - 1; r >= 0; --r)
+        if (live[r]) f = 64 * r + __builtin_ctzll(live[r]);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (live[r]) l = 64 * r + 63 - __builtin_clzll(live[r]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        uint64_t m = live[r];
+        if (r == (l >> 6)) m &= (1ULL << (l & 63)) - 1;
+        else if (r > (l >> 6)) m = 0;
+        if (m) pl = 64 * r + 63 - __builtin_clzll(m);
+      }
+      auto won = [&](int q) {
+        bool b = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (r == (q >> 6)) b = (win[r] >> (q & 63)) & 1;
+        return b;
+      };
+      auto product = [&](int q) {  // the pair product at position q
+        uint32_t v = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (r == (q >> 6)) v = (uint32_t)__builtin_amdgcn_readlane((int)mid[r], q & 63);
+        return v;
+      };
+      const bool fsel = won(f);
+      const bool lsel = pl >= 0 && won(pl);
+      if (t.cert == 2) {
+        if (lane == 0)
+          w.hfirst[a + nfirst] = ((uint64_t)rank << 32) | (fsel ? HR_FIRST : 0) |
+                                 (lsel ? HR_LAST : 0) | product((int)(best & 511));
+        ++nfirst;
+      } else {
+        if (fsel) {
+          if (lane == 0) w.hfirst[a + nfirst] = ((uint64_t)rank << 32) | product(f);
+          ++nfirst;
+        }
+        if (lsel) {
+          if (lane == 0) w.hlast[a + nlast] = ((uint64_t)rank << 32) | product(pl);
+          ++nlast;
+        }
+      }
+    }
     next_live_mask<R>(live, win, gone);
     prev_live_mask<R>(live, win, prev);
 #pragma unroll
@@ -3500,6 +3554,7 @@ __device__ __forceinline__ void wave_bpe_rows(const DevTables& t,
     const int p = 64 * r + lane;
     if (p < len) w.tok[a + p] = lane_bit(live[r]) ? (sym[r] & SYM_ID) : INVALID_ID;
   }
+  if (H && lane == 0) w.hmeta[a] = t.cert == 2 ? nfirst : nfirst | (nlast << 16);
 }
 
 // Entries of 65..WIDE_MAX bytes from a (start, end) list, one wave each.
@@ -3840,6 +3895,11 @@ __global__ __launch_bounds__(256) void k_repair_merge(DevTables t, DevWork w,
       if (len <= 64)
         wave_bpe<false, true, true>(t, w, (int64_t)a, (int64_t)a + lane, lane,
                                     lane < len, 0, len);
+      else if (len <= 128)  // (state in registers: about half the LDS
+        // merge's time per round)
+        wave_bpe_rows<2, true>(t, w, a, len, false, nullptr);
+      else if (len <= 256)
+        wave_bpe_rows<4, true>(t, w, a, len, false, nullptr);
       else if (len <= WIDE_MAX)
         wave_bpe_wide(t, w, a, len, false, true, lds[wv]);
     } else {
@@ -3890,6 +3950,40 @@ __device__ __forceinline__ uint32_t pair_rank(const DevTables& t, uint32_t l,
   return pair_find(t, l, r, &rank, &id) ? rank : RANK_INF;
 }
 
+// A segment's history entries read in order, four loads ahead of the one
+// in use: the walk below takes one entry per step, and each step's pair
+// lookup no longer waits behind the load of the entry it needs.
+struct EvStream {
+  const uint64_t* e;
+  uint32_t n, i;
+  uint64_t q0, q1, q2, q3;
+  __device__ __forceinline__ uint64_t at(uint32_t k) const {
+    return k < n ? e[k] : ~0ULL;
+  }
+  __device__ __forceinline__ void init(const uint64_t* p, uint32_t cnt) {
+    e = p;
+    n = cnt;
+    i = 0;
+    q0 = at(0);
+    q1 = at(1);
+    q2 = at(2);
+    q3 = at(3);
+  }
+  // the next entry's rank, RANK_INF past the last one
+  __device__ __forceinline__ uint32_t rank() const {
+    return i < n ? (uint32_t)(q0 >> 32) : RANK_INF;
+  }
+  __device__ __forceinline__ uint64_t take() {
+    const uint64_t v = q0;
+    q0 = q1;
+    q1 = q2;
+    q2 = q3;
+    q3 = at(i + 4);
+    ++i;
+    return v;
+  }
+};
+
 // One cut c = 64v + bit (the calling lane's).
 __device__ void certify_cut(const DevTables& t, const DevWork& w, int64_t v, int bit) {
   const int64_t c = v * 64 + bit;
@@ -3900,9 +3994,9 @@ __device__ void certify_cut(const DevTables& t, const DevWork& w, int64_t v, int
   const int64_t a = wd * 64 + (63 - __builtin_clzll(word));
   uint32_t L = (uint32_t)t.byte_id[w.text[c - 1]];
   uint32_t R = (uint32_t)t.byte_id[w.text[c]];
-  uint32_t i = 0, j = 0;
   bool ok = true;
   uint32_t rho = pair_rank(t, L, R);
+  EvStream A, B;
   if (t.cert == 2) {
     // Any table: the two segments' merge rounds in the order the whole
     // piece would run them (the left segment's next round first when its
@@ -3912,22 +4006,20 @@ __device__ void certify_cut(const DevTables& t, const DevWork& w, int64_t v, int
     // product of, so the pair it leaves across c while it goes on ranks
     // above it and cannot merge then: the states between rounds are the
     // ones to check.
-    const uint32_t na = w.hmeta[a], nbv = w.hmeta[c];
-    const uint64_t* ea = w.hfirst + a;
-    const uint64_t* eb = w.hfirst + c;
+    A.init(w.hfirst + a, w.hmeta[a]);
+    B.init(w.hfirst + c, w.hmeta[c]);
     for (;;) {
-      const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
-      const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
+      const uint32_t ra = A.rank(), rb = B.rank();
       if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
       if (ra == RANK_INF && rb == RANK_INF) break;
       if (ra <= rb) {
-        const uint64_t e = ea[i++];
+        const uint64_t e = A.take();
         if (e & HR_LAST) {
           L = (uint32_t)e & SYM_ID;
           rho = pair_rank(t, L, R);
         }
       } else {
-        const uint64_t e = eb[j++];
+        const uint64_t e = B.take();
         if (e & HR_FIRST) {
           R = (uint32_t)e & SYM_ID;
           rho = pair_rank(t, L, R);
@@ -3935,16 +4027,14 @@ __device__ void certify_cut(const DevTables& t, const DevWork& w, int64_t v, int
       }
     }
   } else {
-    const uint32_t na = w.hmeta[a] >> 16, nbv = w.hmeta[c] & 0xFFFF;
-    const uint64_t* ea = w.hlast + a;
-    const uint64_t* eb = w.hfirst + c;
+    A.init(w.hlast + a, w.hmeta[a] >> 16);
+    B.init(w.hfirst + c, w.hmeta[c] & 0xFFFF);
     for (;;) {
-      const uint32_t ra = i < na ? (uint32_t)(ea[i] >> 32) : RANK_INF;
-      const uint32_t rb = j < nbv ? (uint32_t)(eb[j] >> 32) : RANK_INF;
+      const uint32_t ra = A.rank(), rb = B.rank();
       if (rho < ra && rho <= rb) { ok = false; break; }  // merges across c
       if (ra == RANK_INF && rb == RANK_INF) break;
-      if (ra <= rb) { L = (uint32_t)ea[i]; ++i; }
-      if (rb <= ra) { R = (uint32_t)eb[j]; ++j; }
+      if (ra <= rb) L = (uint32_t)A.take();
+      if (rb <= ra) R = (uint32_t)B.take();
       rho = pair_rank(t, L, R);
     }
   }
