@@ -2502,15 +2502,42 @@ __device__ __forceinline__ uint32_t long_prep_step(const DevTables& t,
     else if (nx) b = (uint32_t)((wd + 1) * 64 + __builtin_ctzll(nx));
     else far = true;
   }
-  // longer pieces: the wave reads 64 words at a time (the words pretok
-  // wrote end at nwords, and the word holding byte nb has a start bit at
-  // or after nb, so the search ends before them)
+  // longer pieces (the words pretok wrote end at nwords, and the word
+  // holding byte nb has a start bit at or after nb, so every search ends
+  // before them). Eight at a time first: lane group g (lanes 8g..8g+7)
+  // reads words 2..9 of the g-th pending piece, one load a lane, which
+  // ends every piece of up to ~576 bytes (one dependent load for eight
+  // pieces instead of one each: a wave of C5's 129-256-byte pieces has
+  // fifty of them, and the gate opens after its slowest wave).
   const int64_t nwords = (w.nb + 63) / 64 + 2;
-  for (uint64_t pend = __ballot(far); pend; pend &= pend - 1) {
+  uint64_t rest = 0;
+  for (uint64_t pend = __ballot(far); pend;) {
+    const int g = lane >> 3, sub = lane & 7;
+    uint64_t p = pend;
+    for (int q = 0; q < g && p; ++q) p &= p - 1;
+    const int j = p ? __builtin_ctzll(p) : 0;
+    const uint32_t pa = __shfl(a, j);
+    const int64_t wq = (int64_t)(pa >> 6) + 2 + sub;
+    const uint64_t word = !p ? 0ULL : wq < nwords ? w.starts[wq] : ~0ULL;
+    const uint32_t gm = (uint32_t)(__ballot(word != 0) >> (8 * g)) & 0xFFu;
+    const int l = gm ? __builtin_ctz(gm) : 0;
+    const uint64_t wl = __shfl(word, 8 * g + l);
+    const uint32_t ge = (uint32_t)(((pa >> 6) + 2 + l) * 64 + __builtin_ctzll(wl | (1ULL << 63)));
+    // each pending lane among the first eight takes its group's result
+    const uint32_t r = (uint32_t)__popcll(pend & ((1ULL << lane) - 1));
+    const bool mine = ((pend >> lane) & 1) && r < 8;
+    const uint32_t e8 = (uint32_t)__shfl((int)ge, 8 * (int)(r & 7));
+    const bool ok8 = __shfl((int)gm, 8 * (int)(r & 7)) != 0;
+    if (mine && ok8) b = e8;
+    rest |= __ballot(mine && !ok8);
+    for (int q = 0; q < 8 && pend; ++q) pend &= pend - 1;
+  }
+  // the rest, one after another: the wave reads 64 words at a time
+  for (uint64_t pend = rest; pend; pend &= pend - 1) {
     const int j = __builtin_ctzll(pend);
     const uint32_t pa = __shfl(a, j);
     uint32_t end = 0;
-    for (int64_t wd = (pa >> 6) + 2;; wd += 64) {
+    for (int64_t wd = (pa >> 6) + 10;; wd += 64) {
       const uint64_t word = wd + lane < nwords ? w.starts[wd + lane] : ~0ULL;
       const uint64_t nz = __ballot(word != 0);
       if (nz) {
