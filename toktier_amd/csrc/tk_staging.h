@@ -8,7 +8,8 @@
 // into the staging is spread over several threads and followed by ONE
 // transfer: on MI355X a DMA split into chunks runs at half the rate of a
 // single one (each transfer command carries a fixed cost of about 10 us),
-// while eight threads fill 4 MiB of staging in under 20 us. Ids come back
+// while the copy threads fill the 4.28 MB of a C2 request at about 130
+// GB/s, a third of the transfer's time. Ids come back
 // without a transfer command: the compaction kernel writes them straight
 // into page-locked host memory (the caller's buffer or the out staging).
 #pragma once
