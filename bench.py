@@ -17,8 +17,9 @@ ids are checked bit for bit against the CPU oracle after the timed region.
 second) and mean latency with the UTF-8 bytes already resident in HBM
 (``tk_engine_encode_device``: every kernel and the count read-back, until
 the ids are final in device memory). For C3, which the engine takes only
-from host memory (``tk_engine_encode_batch``), they are the host-to-host
-batch figures.
+from host memory (``tk_engine_encode_batch_docs``: each document in its own
+buffer, as the reference's ``texts: &[&str]``), they are the host-to-host
+batch figures, ids into a reused page-locked buffer.
 
 ``protocol``: the reference's timing window (host UTF-8 buffer in, host
 ``uint32`` ids out, transfers included; ``tk_engine_encode``), p50 / p90 /
@@ -439,16 +440,20 @@ def measure_single(tok, reqs, K, W, seed=False, plain=True):
 
 
 def measure_batch(tok, reqs, K, W):
-    """C3: a ragged batch per step through tk_engine_encode_batch (host
-    documents in, host ids and row offsets out). An untimed stage pass
+    """C3: a ragged batch per step through tk_engine_encode_batch_docs (host
+    documents in, each in its own buffer; host ids, into a reused
+    page-locked buffer as a serving loop keeps one, and row offsets out). An untimed stage pass
     (mode 1) names the dominant kernel; the timed loop times its dispatch
     (mode 2). Here k_compact writes the ids straight into page-locked host
     memory, so its duration includes that PCIe write."""
+    import torch
     from toktier_amd import _ffi
     eng = tok.engine
+    cap = max(sum(len(d) for d in r) for r in reqs) + 1
+    out = torch.empty(cap, dtype=torch.int32, pin_memory=True).numpy().view(np.uint32)
 
     def run(i):
-        return eng.encode_batch(reqs[i])
+        return eng.encode_batch(reqs[i], out=out)
     for i in range(K, K + W):
         run(i)
     stages, ku = kernel_pass(eng, run, range(K))
@@ -715,8 +720,9 @@ def main() -> int:
     if batch:
         workload = (f"C3: {fam}, a ragged batch of 256 requests of U[1,024, "
                     "32,768] chars per step, host documents in, host ids and "
-                    "row offsets out (tk_engine_encode_batch; the engine takes "
-                    "batches from host memory only, so value is host-to-host)")
+                    "row offsets out (tk_engine_encode_batch_docs; the engine "
+                    "takes batches from host memory only, so value is "
+                    "host-to-host)")
     else:
         workload = (f"C{args.config}{' chat' if args.chat else ''}"
                     f"{' seed' if args.seed else ''}: {fam}, one fresh request "
@@ -729,8 +735,10 @@ def main() -> int:
                    "(tk_engine_encode, transfers included); request bytes in "
                    "pageable memory, ids into a reused page-locked numpy "
                    "buffer") if not batch else
-                  ("host documents in -> host uint32 ids and row offsets out "
-                   "(tk_engine_encode_batch, transfers included)"),
+                  ("host documents in, each in its own pageable buffer -> "
+                   "host uint32 ids, into a reused page-locked numpy buffer, "
+                   "and row offsets out (tk_engine_encode_batch_docs, "
+                   "transfers included)"),
         "latency_ms": pcts(host_lat),
         "mean_ms": round(host_ms, 4),
         "all_ms": [round(x, 3) for x in host_lat],

@@ -248,6 +248,10 @@ type Encode =
 type EncodeBatch = unsafe extern "C" fn(
     *mut TkEngine, *const u8, *const u64, usize, u32, *mut u32, usize, *mut u64, *mut i32,
 ) -> c_int;
+type EncodeBatchDocs = unsafe extern "C" fn(
+    *mut TkEngine, *const *const u8, *const usize, usize, u32, *mut u32, usize, *mut u64,
+    *mut i32,
+) -> c_int;
 type EncodeDevice = unsafe extern "C" fn(
     *mut TkEngine, *const c_void, usize, u32, *mut c_void, usize, *mut usize, *mut c_void,
 ) -> c_int;
@@ -279,6 +283,7 @@ struct Api {
     close: Close,
     encode: Encode,
     encode_batch: EncodeBatch,
+    encode_batch_docs: EncodeBatchDocs,
     encode_device: EncodeDevice,
     encode_device_noalloc: EncodeDevice,
     encode_seed: EncodeSeed,
@@ -356,6 +361,7 @@ impl Library {
                     close: symbol(handle, "tk_engine_close")?,
                     encode: symbol(handle, "tk_engine_encode")?,
                     encode_batch: symbol(handle, "tk_engine_encode_batch")?,
+                    encode_batch_docs: symbol(handle, "tk_engine_encode_batch_docs")?,
                     encode_device: symbol(handle, "tk_engine_encode_device")?,
                     encode_device_noalloc: symbol(handle, "tk_engine_encode_device_noalloc")?,
                     encode_seed: symbol(handle, "tk_engine_encode_seed")?,
@@ -532,30 +538,29 @@ impl HipEngine {
 
     /// A batch in one device pass (`NativeGpuEngine::encode_batch_ids`);
     /// each row equals [`encode`](Self::encode) of that document alone. A
-    /// failure of the whole call is every row's error.
+    /// failure of the whole call is every row's error. The documents stay
+    /// where they are: the engine's copy threads gather them into its
+    /// pinned staging (`tk_engine_encode_batch_docs`).
     pub fn encode_batch(&self, docs: &[&[u8]], flags: u32) -> BatchRows {
-        let mut joined = Vec::new();
-        let mut offs = Vec::with_capacity(docs.len() + 1);
-        offs.push(0u64);
-        for d in docs {
-            joined.extend_from_slice(d);
-            offs.push(joined.len() as u64);
-        }
-        let mut ids = vec![0u32; joined.len().max(1)];
+        let ptrs: Vec<*const u8> = docs.iter().map(|d| d.as_ptr()).collect();
+        let lens: Vec<usize> = docs.iter().map(|d| d.len()).collect();
+        let total: usize = lens.iter().sum();
+        let mut ids = vec![0u32; total.max(1)];
         let mut rows = vec![0u64; docs.len() + 1];
         let mut status = vec![0i32; docs.len().max(1)];
         let st = unsafe {
-            (self.lib.api.encode_batch)(self.raw, joined.as_ptr(), offs.as_ptr(), docs.len(),
-                                        flags, ids.as_mut_ptr(), ids.len(), rows.as_mut_ptr(),
-                                        status.as_mut_ptr())
+            (self.lib.api.encode_batch_docs)(self.raw, ptrs.as_ptr(), lens.as_ptr(), docs.len(),
+                                             flags, ids.as_mut_ptr(), ids.len(),
+                                             rows.as_mut_ptr(), status.as_mut_ptr())
         };
-        if let Err(e) = self.check("tk_engine_encode_batch", st) {
+        if let Err(e) = self.check("tk_engine_encode_batch_docs", st) {
             return docs.iter().map(|_| Err(e.clone())).collect();
         }
         (0..docs.len())
             .map(|d| match status[d] {
                 TK_OK => Ok(ids[rows[d] as usize..rows[d + 1] as usize].to_vec()),
-                s => Err(HipError::new("tk_engine_encode_batch row", s, format!("document {d}"))),
+                s => Err(HipError::new("tk_engine_encode_batch_docs row", s,
+                                       format!("document {d}"))),
             })
             .collect()
     }

@@ -15,6 +15,9 @@
  *                           (runtime.rs:76-82; gpu.rs:1446-1461, :500-600)
  *   tk_engine_encode_batch <- NativeGpuEngine::encode_batch_ids
  *                           (gpu.rs:1463-1546, Executor::encode_batch :605-750)
+ *   tk_engine_encode_batch_docs <- the same, with the documents as the
+ *                           reference passes them (texts: &[&str],
+ *                           gpu.rs:1463): separate buffers
  *   tk_engine_set_added  <- AddedTokenFrontend construction and the
  *                           router's added-token check ahead of the GPU
  *                           (src/toktier/frontend/added.py:316-375, scan
@@ -172,6 +175,15 @@ int tk_engine_encode_batch(tk_engine* engine, const uint8_t* joined,
                            const uint64_t* doc_offsets, size_t n_docs,
                            uint32_t flags, uint32_t* ids, size_t ids_cap,
                            uint64_t* row_offsets, int32_t* row_status);
+
+/* The same batch with document d in its own buffer docs[d] of doc_lens[d]
+ * bytes (a null pointer only where the length is 0): the engine's copy
+ * threads gather the documents into its pinned staging, so the caller
+ * joins nothing. Rows, status and errors as tk_engine_encode_batch. */
+int tk_engine_encode_batch_docs(tk_engine* engine, const uint8_t* const* docs,
+                                const size_t* doc_lens, size_t n_docs,
+                                uint32_t flags, uint32_t* ids, size_t ids_cap,
+                                uint64_t* row_offsets, int32_t* row_status);
 
 /* Device-resident form (no host copies): d_text and d_ids are device
  * pointers on the engine's device; `stream` is a hipStream_t or NULL for

@@ -140,3 +140,39 @@ def test_batch_into_pinned_ids_with_a_failed_row(qwen):
             continue
         assert status[d] == 0
         assert np.array_equal(ids[rows[d]:rows[d + 1]], k.oracle.encode_bytes(doc)), d
+
+
+def test_batch_of_separate_documents_equals_the_joined_batch(qwen):
+    """tk_engine_encode_batch_docs (each document in its own buffer, gathered
+    into the pinned staging by the engine) against tk_engine_encode_batch on
+    the same documents joined: empty documents at the start, inside and at
+    the end, a document that is not UTF-8, a batch the calling thread
+    gathers alone (under 256 KiB) and one spread over the copy threads
+    (ragged documents across many 64 KiB claims), ids into a fresh buffer
+    and into a reused page-locked one; every good row against the oracle."""
+    import torch
+    k, t = qwen
+    E = t.engine
+    base = _texts(k)[2]
+    small = [b"", base[:300].encode(), b"", base[300:2900].encode(), b""]
+    big = [base[7000 * i:7000 * (i + 1) + 13 * (i % 5)].encode() for i in range(60)]
+    big[3] = b""
+    big[11] = big[11][:50] + b"\xff" + big[11][50:]  # not UTF-8
+    big.append(b"")
+    pinned = _pinned(sum(map(len, big)) + 1, torch.int32).numpy().view(np.uint32)
+    for docs in (small, big):
+        offs = np.zeros(len(docs) + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum([len(d) for d in docs])
+        want_ids, want_rows, want_status = E.encode_batch_joined(b"".join(docs), offs)
+        for out in (None, pinned):
+            ids, rows, status = E.encode_batch(docs, out=out)
+            assert np.array_equal(rows, want_rows)
+            assert np.array_equal(status, want_status)
+            assert np.array_equal(ids[:int(rows[-1])], want_ids[:int(want_rows[-1])])
+        for d, doc in enumerate(docs):
+            if docs is big and d == 11:
+                assert status[d] == _ffi.TK_E_UTF8 and rows[d] == rows[d + 1]
+                continue
+            assert status[d] == 0
+            assert np.array_equal(ids[int(rows[d]):int(rows[d + 1])],
+                                  k.oracle.encode_bytes(doc)), d

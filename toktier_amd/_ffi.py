@@ -58,7 +58,8 @@ STATUS_NAMES = {
 #: every entry point include/toktier_hip.h declares
 SYMBOLS = (
     "tk_engine_preflight", "tk_engine_open", "tk_engine_close",
-    "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_device",
+    "tk_engine_encode", "tk_engine_encode_batch", "tk_engine_encode_batch_docs",
+    "tk_engine_encode_device",
     "tk_engine_encode_device_noalloc", "tk_engine_encode_seed",
     "tk_engine_encode_seed_host",
     "tk_engine_delivery", "tk_engine_architecture", "tk_engine_set_timing",
@@ -121,6 +122,9 @@ def lib(path: Path | None = None) -> C.CDLL:
     L.tk_engine_encode_batch.restype = C.c_int
     L.tk_engine_encode_batch.argtypes = [vp, vp, vp, sz, C.c_uint32, vp, sz,
                                          vp, vp]
+    L.tk_engine_encode_batch_docs.restype = C.c_int
+    L.tk_engine_encode_batch_docs.argtypes = [vp, vp, vp, sz, C.c_uint32, vp,
+                                              sz, vp, vp]
     L.tk_engine_encode_device.restype = C.c_int
     L.tk_engine_encode_device.argtypes = [vp, vp, sz, C.c_uint32, vp, sz,
                                           C.POINTER(sz), vp]
@@ -226,20 +230,42 @@ class Engine:
         check(st, "tk_engine_encode")
         return out[: n.value]
 
-    def encode_batch(self, docs: list[bytes], flags: int = 0
+    def encode_batch(self, docs: list[bytes], flags: int = 0,
+                     out: np.ndarray | None = None
                      ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-        offs = np.zeros(len(docs) + 1, dtype=np.uint64)
-        if docs:
-            offs[1:] = np.cumsum([len(d) for d in docs], dtype=np.uint64)
-        joined = b"".join(docs)
-        ids = np.empty(max(1, len(joined)), dtype=np.uint32)
+        """Documents in their own buffers (tk_engine_encode_batch_docs: the
+        engine gathers them); returns (ids, row offsets, row status).
+        ``out``: a reusable uint32 buffer of at least the documents' total
+        bytes (``ids`` is then a view of it)."""
+        lens = np.fromiter((len(d) for d in docs), dtype=np.uint64, count=len(docs))
+        ptrs = (C.c_char_p * max(1, len(docs)))(*docs)
+        nb = int(lens.sum())
+        if (out is None or out.dtype != np.uint32 or out.ndim != 1
+                or not out.flags.c_contiguous or out.size < max(1, nb)):
+            out = np.empty(max(1, nb), dtype=np.uint32)
         rows = np.zeros(len(docs) + 1, dtype=np.uint64)
         status = np.zeros(max(1, len(docs)), dtype=np.int32)
+        st = self._L.tk_engine_encode_batch_docs(
+            self._h, ptrs, lens.ctypes.data, len(docs), flags,
+            out.ctypes.data, out.size, rows.ctypes.data, status.ctypes.data)
+        check(st, "tk_engine_encode_batch_docs")
+        return out, rows, status[: len(docs)]
+
+    def encode_batch_joined(self, joined: bytes, doc_offsets: np.ndarray,
+                            flags: int = 0
+                            ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """The same batch as one buffer of concatenated documents and their
+        offsets (tk_engine_encode_batch)."""
+        offs = np.ascontiguousarray(doc_offsets, dtype=np.uint64)
+        n = offs.size - 1
+        ids = np.empty(max(1, len(joined)), dtype=np.uint32)
+        rows = np.zeros(n + 1, dtype=np.uint64)
+        status = np.zeros(max(1, n), dtype=np.int32)
         st = self._L.tk_engine_encode_batch(
-            self._h, joined, offs.ctypes.data, len(docs), flags,
+            self._h, joined, offs.ctypes.data, n, flags,
             ids.ctypes.data, ids.size, rows.ctypes.data, status.ctypes.data)
         check(st, "tk_engine_encode_batch")
-        return ids, rows, status[: len(docs)]
+        return ids, rows, status[:n]
 
     def encode_device(self, d_text: int, nbytes: int, d_ids: int,
                       ids_cap: int, flags: int = 0, stream: int | None = None

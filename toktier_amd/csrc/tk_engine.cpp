@@ -1392,7 +1392,7 @@ namespace {
 
 // tk_engine_encode_device with the engine's lock held, the device current
 // and a workspace that holds nbytes
-int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
+static int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
                   size_t nbytes, uint32_t flags, void* d_ids, size_t ids_cap,
                   size_t* n_ids, void* stream) {
   *n_ids = 0;
@@ -1414,7 +1414,7 @@ int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
 }
 
 // the engine's own workspace, grown to hold nbytes
-int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
+static int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
                uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
                void* stream) {
   *n_ids = 0;
@@ -1428,7 +1428,7 @@ int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
 
 // One lock per device for the static scratch array: every engine on a
 // device shares that device's copy of the array.
-std::mutex& scratch_lock(int device) {
+static std::mutex& scratch_lock(int device) {
   static std::mutex locks[64];
   return locks[device & 63];
 }
@@ -1517,7 +1517,7 @@ int tk_engine_encode_seed(tk_engine* e, const void* d_text, size_t nbytes,
 
 namespace {
 // the injected fault of a host-buffer call (tk_engine_set_fault_marker)
-bool injected_fault(const tk_engine* e, const uint8_t* data, size_t n) {
+static bool injected_fault(const tk_engine* e, const uint8_t* data, size_t n) {
   const std::string& m = e->fault_marker;
   if (m.empty() || n < m.size()) return false;
   const uint8_t* end = data + n;
@@ -1623,13 +1623,42 @@ int tk_engine_encode(tk_engine* e, const uint8_t* text, size_t nbytes,
   return TK_OK;
 }
 
-int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
-                           const uint64_t* doc_offsets, size_t n_docs,
-                           uint32_t flags, uint32_t* ids, size_t ids_cap,
-                           uint64_t* row_offsets, int32_t* row_status) {
-  if (!e || !doc_offsets || !row_offsets || !row_status)
-    return fail(TK_E_INVALID_ARG, "null argument");
-  std::lock_guard<std::mutex> lk(e->mu);
+namespace {
+
+// The documents end to end into dst, by the copy threads in claims of
+// STAGE_CHUNK bytes of the joined range (a claim copies the parts of the
+// documents it covers); offs: the documents' offsets, offs.back() bytes.
+static void gather_docs(tk_engine* e, uint8_t* dst, const uint8_t* const* docs,
+                 const std::vector<uint64_t>& offs) {
+  const size_t nb = offs.back();
+  auto part = [&](size_t lo, size_t hi) {
+    // the document holding byte lo (past any empty ones)
+    size_t d = (size_t)(std::upper_bound(offs.begin(), offs.end(), (uint64_t)lo) -
+                        offs.begin()) - 1;
+    while (lo < hi) {
+      const size_t end = std::min<size_t>(hi, offs[d + 1]);
+      if (end > lo) std::memcpy(dst + lo, docs[d] + (lo - offs[d]), end - lo);
+      lo = std::max(lo, end);
+      ++d;
+    }
+  };
+  if (nb <= STAGE_SMALL) {
+    part(0, nb);
+    return;
+  }
+  copy_pool(e)->run((nb + STAGE_CHUNK - 1) / STAGE_CHUNK, [&](size_t k) {
+    const size_t lo = k * STAGE_CHUNK;
+    part(lo, std::min(nb, lo + STAGE_CHUNK));
+  });
+}
+
+// The batch entries' body, under the engine's lock: `joined` holds the
+// documents' bytes in host memory (the caller's buffer, or the pinned
+// staging that gather_docs filled).
+static int encode_batch_locked(tk_engine* e, const uint8_t* joined,
+                        const uint64_t* doc_offsets, size_t n_docs,
+                        uint32_t flags, uint32_t* ids, size_t ids_cap,
+                        uint64_t* row_offsets, int32_t* row_status) {
   const size_t nb = n_docs ? doc_offsets[n_docs] : 0;
   for (size_t d = 0; d < n_docs; ++d) {
     if (doc_offsets[d] > doc_offsets[d + 1])
@@ -1695,6 +1724,45 @@ int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
     std::memcpy(ids, keep.data(), keep.size() * 4);
   }
   return TK_OK;
+}
+
+}  // namespace
+
+int tk_engine_encode_batch(tk_engine* e, const uint8_t* joined,
+                           const uint64_t* doc_offsets, size_t n_docs,
+                           uint32_t flags, uint32_t* ids, size_t ids_cap,
+                           uint64_t* row_offsets, int32_t* row_status) {
+  if (!e || !doc_offsets || !row_offsets || !row_status)
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  return encode_batch_locked(e, joined, doc_offsets, n_docs, flags, ids, ids_cap,
+                             row_offsets, row_status);
+}
+
+int tk_engine_encode_batch_docs(tk_engine* e, const uint8_t* const* docs,
+                                const size_t* doc_lens, size_t n_docs,
+                                uint32_t flags, uint32_t* ids, size_t ids_cap,
+                                uint64_t* row_offsets, int32_t* row_status) {
+  if (!e || !row_offsets || !row_status || (n_docs && (!docs || !doc_lens)))
+    return fail(TK_E_INVALID_ARG, "null argument");
+  std::lock_guard<std::mutex> lk(e->mu);
+  std::vector<uint64_t> offs(n_docs + 1, 0);
+  for (size_t d = 0; d < n_docs; ++d) {
+    if (doc_lens[d] && !docs[d]) return fail(TK_E_INVALID_ARG, "document %zu is null", d);
+    offs[d + 1] = offs[d] + doc_lens[d];
+  }
+  const uint8_t* joined = nullptr;
+  if (offs[n_docs]) {
+    // (the pinned staging, already the size stage_in would make it; its
+    // bytes then go to the device in one transfer, as a page-locked
+    // request does)
+    HIP_TRY(hipSetDevice(e->device));
+    HIP_TRY(e->pin_in.ensure(std::max((size_t)offs[n_docs], e->ws.cap) + 64));
+    gather_docs(e, e->pin_in.p, docs, offs);
+    joined = e->pin_in.p;
+  }
+  return encode_batch_locked(e, joined, offs.data(), n_docs, flags, ids, ids_cap,
+                             row_offsets, row_status);
 }
 
 }  // extern "C"
