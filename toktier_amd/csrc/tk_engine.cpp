@@ -303,7 +303,10 @@ struct tk_engine {
   // workspace (carved from one allocation) and the batch / seed buffers
   DevBuf<uint8_t> wsmem;
   Workspace ws;
-  DevBuf<uint64_t> docoffs, rows;
+  DevBuf<uint64_t> docoffs;
+  // a batch's document offsets on their way in, and its row offsets, which
+  // k_doc_offsets writes here over PCIe right after the compaction
+  tk::PinnedBuf offs_pin, rows_pin;
   DevBuf<uint32_t> seedc;  // per-block character counts (session seed)
   DevBuf<uint64_t> seedp;  // span checkpoints of the host-buffer seed
   // test-only: a host-buffer call whose input holds these bytes fails as a
@@ -422,7 +425,8 @@ int ensure_workspace(tk_engine* e, size_t nb, size_t n_docs) {
   }
   if (n_docs + 1 > e->docs_cap) {
     HIP_TRY(e->docoffs.alloc(n_docs + 1));
-    HIP_TRY(e->rows.alloc(n_docs + 1));
+    HIP_TRY(e->offs_pin.ensure((n_docs + 1) * sizeof(uint64_t)));
+    HIP_TRY(e->rows_pin.ensure((n_docs + 1) * sizeof(uint64_t)));
     e->docs_cap = n_docs + 1;
   }
   return TK_OK;
@@ -568,11 +572,21 @@ float elapsed_us(hipEvent_t a, hipEvent_t b) {
 // first; the split marks document starts, so k_pretok runs its
 // document-mask instance, on a mask k_added writes whole (ws.docmask_lit:
 // the caller's document starts, if any, are read from d_docmask and kept).
+// A batch's row offsets, counted right after the compaction, before the
+// call's one stream sync (offs: the document offsets on the device; rows:
+// n + 1 entries, e.g. host-mapped).
+struct RowsOut {
+  const uint64_t* offs;
+  uint32_t n;
+  uint64_t* rows;
+};
+
 int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
                  size_t nb, const uint64_t* d_docmask, bool check_nfc,
                  hipStream_t s, uint32_t* out, size_t out_cap,
                  uint32_t* status, uint32_t* total,
-                 const tk::DevAdded* docs = nullptr) {
+                 const tk::DevAdded* docs = nullptr,
+                 const RowsOut* rows_out = nullptr) {
   ++e->seq;
   const bool literals = docs != nullptr;
   const uint64_t* host_dm = d_docmask;
@@ -687,6 +701,8 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
   HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag, ks(TK_KERNEL_COMPACT),
                              ke(TK_KERNEL_COMPACT)));
   launched[TK_KERNEL_COMPACT] = true;
+  if (rows_out)
+    HIP_TRY(tk::launch_doc_offsets(w, rows_out->offs, rows_out->n, rows_out->rows, s));
   // k_compact's last block has left the outcome in the gate words: no
   // read-back copy
   HIP_TRY(hipStreamSynchronize(s));
@@ -1676,7 +1692,9 @@ static int encode_batch_locked(tk_engine* e, const uint8_t* joined,
   // forced piece starts at every document head (gpu.rs:644-652): the mask
   // is built on the device from the offsets
   if ((rc = stage_in(e, e->ws.text, joined, nb, s)) != TK_OK) return rc;
-  HIP_TRY(hipMemcpyAsync(e->docoffs.p, doc_offsets, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
+  // (the offsets cross from page-locked memory: one plain DMA)
+  std::memcpy(e->offs_pin.p, doc_offsets, (n_docs + 1) * 8);
+  HIP_TRY(hipMemcpyAsync(e->docoffs.p, e->offs_pin.p, (n_docs + 1) * 8, hipMemcpyHostToDevice, s));
   HIP_TRY(tk::launch_doc_mask(e->ws.docmask, (int64_t)((nb + 63) / 64 + 2),
                               e->docoffs.p, (uint32_t)n_docs, (int64_t)nb, s));
   HostOut o;
@@ -1684,12 +1702,11 @@ static int encode_batch_locked(tk_engine* e, const uint8_t* joined,
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
   uint32_t st, total;
   tk::DevAdded docs;
+  const RowsOut ro{e->docoffs.p, (uint32_t)n_docs,
+                   reinterpret_cast<uint64_t*>(e->rows_pin.dev)};
   rc = run_pipeline(e, e->ws, e->ws.text, nb, e->ws.docmask, check, s,
-                    o.dev, o.cap, &st, &total, doc_pass(e, flags, &docs));
+                    o.dev, o.cap, &st, &total, doc_pass(e, flags, &docs), &ro);
   if (rc != TK_OK) return rc;
-  const tk::DevWork w = make_work(e, e->ws, e->ws.text, nb, e->ws.docmask,
-                                  check, o.dev, o.cap, false);
-  HIP_TRY(tk::launch_doc_offsets(w, e->docoffs.p, (uint32_t)n_docs, e->rows.p, s));
   if (total > ids_cap) return fail(TK_E_CAPACITY, "%u ids exceed the %zu-id buffer", total, ids_cap);
   // a batch holding a poisoned document fails as a whole, as a device
   // guard trip would
@@ -1698,9 +1715,9 @@ static int encode_batch_locked(tk_engine* e, const uint8_t* joined,
       HIP_TRY(hipStreamSynchronize(s));
       return fail(TK_E_INTERNAL, "injected fault (document %zu)", d);
     }
-  HIP_TRY(hipMemcpyAsync(row_offsets, e->rows.p, (n_docs + 1) * 8, hipMemcpyDeviceToHost, s));
+  // (the pipeline's sync has made the row offsets visible here)
+  std::memcpy(row_offsets, e->rows_pin.p, (n_docs + 1) * 8);
   ids_from_staging(e, o, ids, total);
-  HIP_TRY(hipStreamSynchronize(s));
   if (st & (tk::ST_UTF8 | tk::ST_NFC)) {
     // find the rows that failed; their ids are dropped, the others stand
     std::vector<uint32_t> keep;
