@@ -756,6 +756,9 @@ int run_pipeline(tk_engine* e, Workspace& ws, const uint8_t* d_text,
     wc.nfail = fail_count(ctrl, p);
     HIP_TRY(tk::launch_compact(wc, s, ++ws.ctag));
     if (stages) HIP_TRY(hipEventRecord(ev[7], s));
+    // (the row offsets again, over the final compaction)
+    if (rows_out)
+      HIP_TRY(tk::launch_doc_offsets(w, rows_out->offs, rows_out->n, rows_out->rows, s));
     if ((rc = read_ctrl_words(ctrl, s, h)) != TK_OK) return rc;
     if (stages) {
       e->last_us[2] += elapsed_us(ev[5], ev[6]);
