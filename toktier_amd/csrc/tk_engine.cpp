@@ -1412,8 +1412,8 @@ namespace {
 // tk_engine_encode_device with the engine's lock held, the device current
 // and a workspace that holds nbytes
 static int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
-                  size_t nbytes, uint32_t flags, void* d_ids, size_t ids_cap,
-                  size_t* n_ids, void* stream) {
+                         size_t nbytes, uint32_t flags, void* d_ids, size_t ids_cap,
+                         size_t* n_ids, void* stream) {
   *n_ids = 0;
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : e->stream;
   const bool check = e->t.needs_nfc && !(flags & TK_FLAG_NORMALIZED);
@@ -1434,8 +1434,8 @@ static int device_encode(tk_engine* e, Workspace& ws, const void* d_text,
 
 // the engine's own workspace, grown to hold nbytes
 static int own_encode(tk_engine* e, const void* d_text, size_t nbytes,
-               uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
-               void* stream) {
+                      uint32_t flags, void* d_ids, size_t ids_cap, size_t* n_ids,
+                      void* stream) {
   *n_ids = 0;
   if (nbytes == 0) return TK_OK;
   HIP_TRY(hipSetDevice(e->device));
@@ -1648,7 +1648,7 @@ namespace {
 // STAGE_CHUNK bytes of the joined range (a claim copies the parts of the
 // documents it covers); offs: the documents' offsets, offs.back() bytes.
 static void gather_docs(tk_engine* e, uint8_t* dst, const uint8_t* const* docs,
-                 const std::vector<uint64_t>& offs) {
+                        const std::vector<uint64_t>& offs) {
   const size_t nb = offs.back();
   auto part = [&](size_t lo, size_t hi) {
     // the document holding byte lo (past any empty ones)
@@ -1675,9 +1675,9 @@ static void gather_docs(tk_engine* e, uint8_t* dst, const uint8_t* const* docs,
 // documents' bytes in host memory (the caller's buffer, or the pinned
 // staging that gather_docs filled).
 static int encode_batch_locked(tk_engine* e, const uint8_t* joined,
-                        const uint64_t* doc_offsets, size_t n_docs,
-                        uint32_t flags, uint32_t* ids, size_t ids_cap,
-                        uint64_t* row_offsets, int32_t* row_status) {
+                               const uint64_t* doc_offsets, size_t n_docs,
+                               uint32_t flags, uint32_t* ids, size_t ids_cap,
+                               uint64_t* row_offsets, int32_t* row_status) {
   const size_t nb = n_docs ? doc_offsets[n_docs] : 0;
   for (size_t d = 0; d < n_docs; ++d) {
     if (doc_offsets[d] > doc_offsets[d + 1])
